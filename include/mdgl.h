@@ -1,0 +1,157 @@
+/* libmdgl.so -- MI355X (gfx950) message-passing kernel layer, C ABI.
+ *
+ * Drop-in for the reference's Mojo C ABI (src/capi.mojo), which the Python
+ * host layer binds through ctypes (python/mojodgl/_lib.py:51-63). Every
+ * entry point keeps the reference's symbol name and its leading arguments in
+ * the reference's order and meaning, then adds what a GPU needs:
+ *   - device pointers (every array argument is device memory unless stated);
+ *   - int32 graph indices (CSR row pointers, neighbour ids, edge ids, COO
+ *     endpoints, segment offsets); the host converts the reference's int64
+ *     ids once per graph and refuses 2**31 or more nodes or edges;
+ *   - a dtype code (MDGL_FLOAT32 / MDGL_FLOAT64) instead of float64 only;
+ *   - NumPy broadcasting by operand feature shapes instead of materialised
+ *     width-1 operands (python/mojodgl/ops/sddmm.py:62-68);
+ *   - optional arg outputs for max/min, a heavy-row schedule, a caller-owned
+ *     workspace, and a HIP stream (hipStream_t passed as void*; NULL is the
+ *     default stream).
+ *
+ * Conventions (as the reference, capi.mojo:1-17): the caller owns all
+ * memory, nothing here allocates or frees, and launches are asynchronous on
+ * `stream`. Unlike the reference every call returns a status: 0 on success,
+ * a negative MDGL_E* code for an invalid argument (detected before anything
+ * is launched; mdgl_last_error() names it), or a positive hipError_t from
+ * the launch.
+ *
+ * Codes (src/ported.mojo:44-65, python/mojodgl/_lib.py:65-73):
+ *   targets  u = 0, v = 1, e = 2
+ *   ops      add, sub, mul, div, dot = 0..4, copy_lhs = 5, copy_rhs = 6
+ *   reducers sum, max, min, mean = 0..3
+ */
+#ifndef MDGL_H
+#define MDGL_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MDGL_OK 0
+#define MDGL_EINVAL (-1)     /* invalid argument */
+#define MDGL_EWORKSPACE (-2) /* workspace missing or too small */
+#define MDGL_ENOTSUP (-3)    /* valid but unsupported shape (e.g. > 6 broadcast dims) */
+
+#define MDGL_FLOAT32 0
+#define MDGL_FLOAT64 1
+
+/* flags of mdgl_gspmm / mdgl_segment_reduce */
+#define MDGL_REPLACE_INF 1 /* +-inf results become 0 (heterograph.py:232-239) */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* mdgl_last_error(void);
+
+/* Replaces capi.mojo:48-50 (`mdgl_workers`). The reference returns its CPU
+ * worker count; here it is the number of compute units the launches are
+ * shaped for (256 on MI355X), always > 1. */
+int64_t mdgl_workers(void);
+
+/* Replaces capi.mojo:54-56. Inclusive int64 prefix sum, dst[i] = src[0..i]. */
+int mdgl_cumsum(const int64_t* src, int64_t* dst, int64_t n, void* stream);
+
+/* Replaces capi.mojo:59-61. dst[i] = 0 where src[i] is +-inf, else src[i]. */
+int mdgl_replace_inf_with_zero(const void* src, void* dst, int64_t n, int dtype, void* stream);
+
+/* Replaces capi.mojo:64-66. dst[i] = min(max(src[i], lo), hi). */
+int mdgl_clamp_i64(const int64_t* src, int64_t* dst, int64_t n, int64_t lo, int64_t hi,
+                   void* stream);
+
+/* Replaces capi.mojo:70-91 (`mdgl_gsddmm`): in edge-id order,
+ *   dst[e] = op(lhs[t_l(e)], rhs[t_r(e)]), t = u: uids[e], v: vids[e], e: e.
+ * dl / dr / dout are the operand and output row widths. `nd`, `lhs_shape`,
+ * `rhs_shape` (host arrays) are the two operands' feature shapes padded to
+ * the same rank (sddmm.py:24-47); nd = 0 means no broadcasting
+ * (dl == dr == dout). For dot the last axis is contracted: it must be equal,
+ * and dout counts the broadcast leading positions (1 for 2-D operands).
+ * Copy ops read one operand and ignore the shapes. */
+int mdgl_gsddmm(const int32_t* uids, const int32_t* vids, const void* lhs, const void* rhs,
+                void* dst, int64_t num_edges, int lhs_target, int rhs_target, int op, int64_t dl,
+                int64_t dr, int64_t dout, int nd, const int64_t* lhs_shape,
+                const int64_t* rhs_shape, int dtype, void* stream);
+
+/* Replaces capi.mojo:95-115 (`mdgl_gspmm`): over the in-edge CSR
+ * (indptr, indices = source node, eid = edge id of each slot),
+ *   dst[v] = reduce over slots i of row v of op(lhs[indices[i]], rhs[eid[i]]),
+ * folded in CSR order; mean divides the sum by max(deg[v], 1) (deg may be
+ * NULL: the row length); a row with no in-edges gets the reduce identity
+ * (0, -inf, +inf) unless MDGL_REPLACE_INF is set.
+ * Extensions: broadcasting as in mdgl_gsddmm; arg_u / arg_e (nullable, max
+ * and min only) receive the source node and edge id of the selected message
+ * (the first in CSR order among ties, 0 for an empty row); rows longer than
+ * chunk_len are split into the num_chunks chunks (chunk_row[c],
+ * chunk_start[c]: each covers up to chunk_len slots) whose partials are
+ * reduced in order per heavy row (heavy_rows[h], chunks
+ * heavy_ptr[h]..heavy_ptr[h+1]) -- the chunks of every row of length
+ * > chunk_len, in CSR order, and nothing else; num_chunks = 0 disables the
+ * split. The partials live in `workspace` (mdgl_gspmm_workspace_bytes). */
+int mdgl_gspmm(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
+               const void* lhs, const void* rhs, void* dst, int64_t num_dst, int op, int64_t dl,
+               int64_t dr, int64_t dout, int reduce_op, const int32_t* deg, int nd,
+               const int64_t* lhs_shape, const int64_t* rhs_shape, int32_t* arg_u,
+               int32_t* arg_e, const int32_t* chunk_row, const int32_t* chunk_start,
+               int64_t num_chunks, int32_t chunk_len, const int32_t* heavy_rows,
+               const int32_t* heavy_ptr, int64_t num_heavy, void* workspace,
+               int64_t workspace_bytes, int flags, int dtype, void* stream);
+
+/* Workspace mdgl_gspmm needs for `num_chunks` chunk partials. */
+int64_t mdgl_gspmm_workspace_bytes(int64_t num_chunks, int64_t dout, int reduce_op, int dtype);
+
+/* Replaces capi.mojo:119-129 (`mdgl_segment_reduce`): dst[s] = reduce of
+ * value rows offsets[s]..offsets[s+1], in row order; mean divides by
+ * max(length, 1) (= the reference's clamp(seglen, 1, n) divide,
+ * segment.py:99-105). offsets has num_seg + 1 entries, non-decreasing, from
+ * 0 to n. */
+int mdgl_segment_reduce(const int32_t* offsets, const void* value, void* dst, int64_t num_seg,
+                        int64_t d, int reduce_op, int64_t n, int flags, int dtype, void* stream);
+
+/* Replaces capi.mojo:132-138 (`mdgl_segment_softmax`): per segment and
+ * column, softmax over the segment's rows; rows of empty segments are not
+ * written. `scratch` is accepted for signature compatibility and unused. */
+int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, void* scratch,
+                         int64_t num_seg, int64_t d, int64_t n, int dtype, void* stream);
+
+/* Replaces capi.mojo:149-165 (`mdgl_edge_softmax_`): per CSR row, per
+ * column, softmax of logits[eid[i]] over the row's slots whose edge is
+ * selected (all_ones = 1, or mask[e] == 1); dst rows of the selected edges
+ * are written. `indices` and `scratch` are accepted for signature
+ * compatibility and unused. Rows longer than heavy_deg are listed in
+ * heavy_rows (num_heavy of them) and get a whole workgroup each; num_heavy
+ * = 0 disables that. */
+int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
+                       const int8_t* mask, const void* logits, void* dst, void* scratch,
+                       int64_t num_nodes, int all_ones, int64_t d, const int32_t* heavy_rows,
+                       int64_t num_heavy, int32_t heavy_deg, int dtype, void* stream);
+
+/* Replaces capi.mojo:141-145 (`mdgl_segment_mm`): out rows of segment r are
+ * a[rows] @ b[r]; seglen_a (device, int64, r entries) sums to at most n and
+ * rows past the sum are left as they are. Needs `workspace`
+ * (mdgl_segment_mm_workspace_bytes). */
+int mdgl_segment_mm(const void* a, const void* b, void* dst, const int64_t* seglen_a, int64_t n,
+                    int64_t d1, int64_t r, int64_t d2, void* workspace, int64_t workspace_bytes,
+                    int dtype, void* stream);
+int64_t mdgl_segment_mm_workspace_bytes(int64_t n, int64_t d1, int64_t d2, int64_t r, int dtype);
+
+/* Replaces capi.mojo:169-173 (`mdgl_gather_mm`): dst[i] = a[i] @ b[idx_b[i]]
+ * with idx_b (device, int64) in [0, r) (rows with other values are left
+ * unwritten). `r` (the number of b blocks, at most 2048) is an added
+ * argument; rows are bucketed by idx_b in `workspace`
+ * (mdgl_gather_mm_workspace_bytes) and multiplied block by block. */
+int mdgl_gather_mm(const void* a, const void* b, const int64_t* idx_b, void* dst, int64_t n,
+                   int64_t d1, int64_t d2, int64_t r, void* workspace, int64_t workspace_bytes,
+                   int dtype, void* stream);
+int64_t mdgl_gather_mm_workspace_bytes(int64_t n, int64_t d1, int64_t d2, int64_t r, int dtype);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MDGL_H */

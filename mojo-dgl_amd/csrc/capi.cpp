@@ -1,0 +1,553 @@
+// C ABI of libmdgl.so (declared in include/mdgl.h).
+//
+// This file validates arguments (before anything is launched), turns operand
+// feature shapes into the collapsed broadcast descriptor, chooses per
+// operand how a lane loads its columns (16-byte vector, one splatted scalar,
+// or a scalar gather), and dispatches to the kernel launchers.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/mdgl.h"
+#include "mdgl_kernels.h"
+
+using namespace mdgl;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return MDGL_OK;
+  return fail((int)e, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool dtype_ok(int dtype) { return dtype == MDGL_FLOAT32 || dtype == MDGL_FLOAT64; }
+int64_t dsize(int dtype) { return dtype == MDGL_FLOAT32 ? 4 : 8; }
+int vec_width(int dtype) { return dtype == MDGL_FLOAT32 ? 4 : 2; }
+
+bool aligned(const void* p, int64_t bytes) {
+  return (reinterpret_cast<uintptr_t>(p) % (uintptr_t)bytes) == 0;
+}
+
+// Builds the broadcast descriptor of two operands whose feature shapes are
+// padded to the same rank `nd`. For dot the last axis is contracted and
+// `red` receives its length. Returns 0 or a negative MDGL code.
+int make_bcast(int nd, const int64_t* ls, const int64_t* rs, bool dot, Bcast* bc, int64_t* red,
+               int64_t* lwidth, int64_t* rwidth, int64_t* owidth) {
+  std::vector<int64_t> lsh(ls, ls + nd), rsh(rs, rs + nd);
+  *red = 1;
+  if (dot) {
+    if (nd < 1) return fail(MDGL_EINVAL, "dot needs at least one feature axis");
+    if (lsh[nd - 1] != rsh[nd - 1])
+      return fail(MDGL_EINVAL, "dot needs matching last axes, got %lld and %lld",
+                  (long long)lsh[nd - 1], (long long)rsh[nd - 1]);
+    *red = lsh[nd - 1];
+    lsh.pop_back();
+    rsh.pop_back();
+  }
+  const int n = (int)lsh.size();
+  std::vector<int64_t> out(n), lst(n), rst(n);
+  int64_t lw = 1, rw = 1, ow = 1;
+  for (int d = n - 1; d >= 0; --d) {
+    if (lsh[d] < 0 || rsh[d] < 0) return fail(MDGL_EINVAL, "negative feature dimension");
+    if (lsh[d] != rsh[d] && lsh[d] != 1 && rsh[d] != 1)
+      return fail(MDGL_EINVAL, "feature shapes are not broadcastable at axis %d: %lld vs %lld",
+                  d + 1, (long long)lsh[d], (long long)rsh[d]);
+    out[d] = lsh[d] == 1 ? rsh[d] : lsh[d];
+    lst[d] = (lsh[d] == 1 && out[d] != 1) ? 0 : lw;
+    rst[d] = (rsh[d] == 1 && out[d] != 1) ? 0 : rw;
+    lw *= lsh[d];
+    rw *= rsh[d];
+    ow *= out[d];
+  }
+  *lwidth = lw * *red;
+  *rwidth = rw * *red;
+  *owidth = ow;
+  // collapse: drop size-1 axes, merge neighbours that stay contiguous in both
+  std::vector<int64_t> cs, cl, cr;
+  for (int d = 0; d < n; ++d) {
+    if (out[d] == 1) continue;
+    if (!cs.empty() && cl.back() == lst[d] * out[d] && cr.back() == rst[d] * out[d]) {
+      cs.back() *= out[d];
+      cl.back() = lst[d];
+      cr.back() = rst[d];
+    } else {
+      cs.push_back(out[d]);
+      cl.push_back(lst[d]);
+      cr.push_back(rst[d]);
+    }
+  }
+  if (cs.empty()) {
+    cs.push_back(1);
+    cl.push_back(0);
+    cr.push_back(0);
+  }
+  if ((int)cs.size() > MAX_DIMS)
+    return fail(MDGL_ENOTSUP, "broadcast needs %d axes after collapsing, at most %d supported",
+                (int)cs.size(), MAX_DIMS);
+  bc->nd = (int)cs.size();
+  int64_t div = 1;
+  for (int d = bc->nd - 1; d >= 0; --d) {
+    bc->shape[d] = cs[d];
+    bc->div[d] = div;
+    bc->lstride[d] = cl[d];
+    bc->rstride[d] = cr[d];
+    div *= cs[d];
+  }
+  return 0;
+}
+
+void identity_bcast(int64_t width, Bcast* bc) {
+  bc->nd = 1;
+  bc->shape[0] = width > 0 ? width : 1;
+  bc->div[0] = 1;
+  bc->lstride[0] = 1;
+  bc->rstride[0] = 1;
+}
+
+// Load mode of one operand for lanes owning `vec` consecutive output
+// columns. Contiguous 16-byte loads need aligned rows and groups.
+int pick_mode(const Bcast& bc, bool lhs, int64_t dout, int vec, int64_t width, const void* base,
+              int64_t esize) {
+  if (vec == 1) return M_CONTIG;  // VEC = 1 kernels load one element whatever the mode
+  bool contig = dout % vec == 0 && width % vec == 0 && aligned(base, vec * esize);
+  bool splat = true;
+  for (int64_t g = 0; g < dout && (contig || splat); g += vec) {
+    const int64_t o0 = bcast_off(bc, g, lhs);
+    if (o0 % vec != 0) contig = false;
+    for (int j = 1; j < vec && g + j < dout; ++j) {
+      const int64_t o = bcast_off(bc, g + j, lhs);
+      if (o != o0 + j) contig = false;
+      if (o != o0) splat = false;
+    }
+  }
+  if (contig) return M_CONTIG;
+  if (splat) return M_SPLAT;
+  return M_GATHER;
+}
+
+bool row_widths_fit(int64_t w, int64_t esize) { return w >= 0 && w * esize < (int64_t(1) << 31); }
+
+}  // namespace
+
+extern "C" {
+
+const char* mdgl_last_error(void) { return g_last_error.c_str(); }
+
+int64_t mdgl_workers(void) { return 256; }
+
+int mdgl_cumsum(const int64_t* src, int64_t* dst, int64_t n, void* stream) {
+  if (n < 0) return fail(MDGL_EINVAL, "cumsum: n must be >= 0");
+  if (n > 0 && (!src || !dst)) return fail(MDGL_EINVAL, "cumsum: null buffer");
+  return hip_status(launch_cumsum_i64(src, dst, n, (hipStream_t)stream), "cumsum");
+}
+
+int mdgl_replace_inf_with_zero(const void* src, void* dst, int64_t n, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "replace_inf_with_zero: bad dtype %d", dtype);
+  if (n < 0) return fail(MDGL_EINVAL, "replace_inf_with_zero: n must be >= 0");
+  if (n > 0 && (!src || !dst)) return fail(MDGL_EINVAL, "replace_inf_with_zero: null buffer");
+  return hip_status(launch_replace_inf(src, dst, n, dtype, (hipStream_t)stream),
+                    "replace_inf_with_zero");
+}
+
+int mdgl_clamp_i64(const int64_t* src, int64_t* dst, int64_t n, int64_t lo, int64_t hi,
+                   void* stream) {
+  if (n < 0) return fail(MDGL_EINVAL, "clamp_i64: n must be >= 0");
+  if (n > 0 && (!src || !dst)) return fail(MDGL_EINVAL, "clamp_i64: null buffer");
+  return hip_status(launch_clamp_i64(src, dst, n, lo, hi, (hipStream_t)stream), "clamp_i64");
+}
+
+int mdgl_gsddmm(const int32_t* uids, const int32_t* vids, const void* lhs, const void* rhs,
+                void* dst, int64_t num_edges, int lhs_target, int rhs_target, int op, int64_t dl,
+                int64_t dr, int64_t dout, int nd, const int64_t* lhs_shape,
+                const int64_t* rhs_shape, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "gsddmm: bad dtype %d", dtype);
+  if (op < OP_ADD || op > OP_COPY_RHS) return fail(MDGL_EINVAL, "gsddmm: bad op %d", op);
+  if (lhs_target < 0 || lhs_target > 2 || rhs_target < 0 || rhs_target > 2)
+    return fail(MDGL_EINVAL, "gsddmm: targets must be 0 (u), 1 (v) or 2 (e)");
+  if (num_edges < 0 || dl < 0 || dr < 0 || dout < 0)
+    return fail(MDGL_EINVAL, "gsddmm: negative size");
+  if (num_edges >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "gsddmm: 2**31 or more edges");
+  const int64_t es = dsize(dtype);
+  if (!row_widths_fit(dl, es) || !row_widths_fit(dr, es) || !row_widths_fit(dout, es))
+    return fail(MDGL_EINVAL, "gsddmm: feature rows of 2 GiB or more");
+  GsddmmParams p{};
+  p.uids = uids;
+  p.vids = vids;
+  p.lhs = lhs;
+  p.rhs = rhs;
+  p.out = dst;
+  p.num_edges = num_edges;
+  p.dl = dl;
+  p.dr = dr;
+  p.dout = dout;
+  p.lt = lhs_target;
+  p.rt = rhs_target;
+  p.op = op;
+  p.stream = (hipStream_t)stream;
+  const bool dot = op == OP_DOT;
+  const bool copy = op == OP_COPY_LHS || op == OP_COPY_RHS;
+  if (copy) {
+    const int64_t w = op == OP_COPY_LHS ? dl : dr;
+    if (dout != w) return fail(MDGL_EINVAL, "gsddmm: copy output width %lld != operand width %lld",
+                               (long long)dout, (long long)w);
+    identity_bcast(dout, &p.bc);
+    p.red = 1;
+  } else if (nd > 0) {
+    if (!lhs_shape || !rhs_shape) return fail(MDGL_EINVAL, "gsddmm: null shape");
+    int64_t lw, rw, ow;
+    int rc = make_bcast(nd, lhs_shape, rhs_shape, dot, &p.bc, &p.red, &lw, &rw, &ow);
+    if (rc) return rc;
+    if (lw != dl || rw != dr || ow != dout)
+      return fail(MDGL_EINVAL, "gsddmm: widths (%lld, %lld, %lld) do not match the shapes "
+                  "(%lld, %lld, %lld)", (long long)dl, (long long)dr, (long long)dout,
+                  (long long)lw, (long long)rw, (long long)ow);
+  } else {
+    if (dot) {
+      if (dl != dr || dout != 1) return fail(MDGL_EINVAL, "gsddmm: dot needs dl == dr, dout == 1");
+      identity_bcast(1, &p.bc);
+      p.bc.lstride[0] = p.bc.rstride[0] = 0;
+      p.red = dl;
+    } else {
+      if (dl != dr || dl != dout)
+        return fail(MDGL_EINVAL, "gsddmm: without shapes dl, dr and dout must be equal");
+      identity_bcast(dout, &p.bc);
+      p.red = 1;
+    }
+  }
+  const bool need_u = (op != OP_COPY_RHS && lhs_target == TGT_U) ||
+                      (op != OP_COPY_LHS && rhs_target == TGT_U);
+  const bool need_v = (op != OP_COPY_RHS && lhs_target == TGT_V) ||
+                      (op != OP_COPY_LHS && rhs_target == TGT_V);
+  if (num_edges > 0 && dout > 0) {
+    if (!dst) return fail(MDGL_EINVAL, "gsddmm: null output");
+    if ((need_u && !uids) || (need_v && !vids)) return fail(MDGL_EINVAL, "gsddmm: null ids");
+    if ((op != OP_COPY_RHS && !lhs) || (op != OP_COPY_LHS && !rhs))
+      return fail(MDGL_EINVAL, "gsddmm: null operand");
+  } else {
+    return MDGL_OK;
+  }
+  const int vw = vec_width(dtype);
+  if (dot) {
+    p.vec = (p.red % vw == 0 && dl % vw == 0 && dr % vw == 0 && aligned(lhs, vw * es) &&
+             aligned(rhs, vw * es)) ? vw : 1;
+    p.lmode = p.rmode = M_CONTIG;
+    p.out_vec = 0;
+  } else {
+    p.vec = dout % vw == 0 ? vw : 1;
+    p.lmode = op == OP_COPY_RHS ? M_CONTIG : pick_mode(p.bc, true, dout, p.vec, dl, lhs, es);
+    p.rmode = op == OP_COPY_LHS ? M_CONTIG : pick_mode(p.bc, false, dout, p.vec, dr, rhs, es);
+    p.out_vec = p.vec > 1 && aligned(dst, p.vec * es);
+  }
+  hipError_t e = dtype == MDGL_FLOAT32 ? launch_gsddmm<float>(p) : launch_gsddmm<double>(p);
+  return hip_status(e, "gsddmm");
+}
+
+int64_t mdgl_gspmm_workspace_bytes(int64_t num_chunks, int64_t dout, int reduce_op, int dtype) {
+  if (num_chunks <= 0) return 0;
+  const int64_t n = num_chunks * dout;
+  int64_t bytes = ((n * dsize(dtype) + 255) / 256) * 256;
+  if (reduce_op == RED_MAX || reduce_op == RED_MIN) bytes += 2 * (((n * 4) + 255) / 256) * 256;
+  return bytes;
+}
+
+}  // extern "C"
+
+namespace {
+
+// gspmm proper; `ident` makes the edge id of CSR slot i be i (segment
+// reduce, where the slots are the value rows).
+int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
+                 const void* lhs, const void* rhs, void* dst, int64_t num_dst, int op, int64_t dl,
+                 int64_t dr, int64_t dout, int reduce_op, const int32_t* deg, int nd,
+                 const int64_t* lhs_shape, const int64_t* rhs_shape, int32_t* arg_u,
+                 int32_t* arg_e, const int32_t* chunk_row, const int32_t* chunk_start,
+                 int64_t num_chunks, int32_t chunk_len, const int32_t* heavy_rows,
+                 const int32_t* heavy_ptr, int64_t num_heavy, void* workspace,
+                 int64_t workspace_bytes, int flags, int dtype, void* stream, bool ident) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "gspmm: bad dtype %d", dtype);
+  if (op < OP_ADD || op > OP_COPY_RHS || op == OP_DOT)
+    return fail(MDGL_EINVAL, "gspmm: bad op %d (dot is a gsddmm operator)", op);
+  if (reduce_op < RED_SUM || reduce_op > RED_MEAN)
+    return fail(MDGL_EINVAL, "gspmm: bad reduce_op %d", reduce_op);
+  if (num_dst < 0 || dl < 0 || dr < 0 || dout < 0) return fail(MDGL_EINVAL, "gspmm: negative size");
+  if (num_dst >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "gspmm: 2**31 or more rows");
+  const int64_t es = dsize(dtype);
+  if (!row_widths_fit(dl, es) || !row_widths_fit(dr, es) || !row_widths_fit(dout, es))
+    return fail(MDGL_EINVAL, "gspmm: feature rows of 2 GiB or more");
+  if (num_chunks < 0 || num_heavy < 0) return fail(MDGL_EINVAL, "gspmm: negative chunk counts");
+  if (num_chunks > 0 && (chunk_len <= 0 || !chunk_row || !chunk_start || num_heavy <= 0 ||
+                         !heavy_rows || !heavy_ptr))
+    return fail(MDGL_EINVAL, "gspmm: incomplete heavy-row schedule");
+  if (num_chunks == 0 && num_heavy != 0)
+    return fail(MDGL_EINVAL, "gspmm: heavy rows without chunks");
+  GspmmParams p{};
+  p.indptr = indptr;
+  p.indices = indices;
+  p.eid = eid;
+  p.deg = deg;
+  p.lhs = lhs;
+  p.rhs = rhs;
+  p.out = dst;
+  p.num_rows = num_dst;
+  p.dl = dl;
+  p.dr = dr;
+  p.dout = dout;
+  p.op = op;
+  p.red = reduce_op == RED_MEAN ? RED_SUM : reduce_op;
+  p.flags = (reduce_op == RED_MEAN ? F_MEAN : 0) | ((flags & MDGL_REPLACE_INF) ? F_REPLACE_INF : 0);
+  const bool arg = reduce_op == RED_MAX || reduce_op == RED_MIN;
+  p.arg_u = arg ? arg_u : nullptr;
+  p.arg_e = arg ? arg_e : nullptr;
+  p.stream = (hipStream_t)stream;
+  const bool copy = op == OP_COPY_LHS || op == OP_COPY_RHS;
+  if (copy) {
+    const int64_t w = op == OP_COPY_LHS ? dl : dr;
+    if (dout != w) return fail(MDGL_EINVAL, "gspmm: copy output width %lld != operand width %lld",
+                               (long long)dout, (long long)w);
+    identity_bcast(dout, &p.bc);
+  } else if (nd > 0) {
+    if (!lhs_shape || !rhs_shape) return fail(MDGL_EINVAL, "gspmm: null shape");
+    int64_t red, lw, rw, ow;
+    int rc = make_bcast(nd, lhs_shape, rhs_shape, false, &p.bc, &red, &lw, &rw, &ow);
+    if (rc) return rc;
+    if (lw != dl || rw != dr || ow != dout)
+      return fail(MDGL_EINVAL, "gspmm: widths (%lld, %lld, %lld) do not match the shapes "
+                  "(%lld, %lld, %lld)", (long long)dl, (long long)dr, (long long)dout,
+                  (long long)lw, (long long)rw, (long long)ow);
+  } else {
+    if (dl != dr || dl != dout)
+      return fail(MDGL_EINVAL, "gspmm: without shapes dl, dr and dout must be equal");
+    identity_bcast(dout, &p.bc);
+  }
+  if (num_dst == 0 || dout == 0) return MDGL_OK;
+  if (!indptr || !dst) return fail(MDGL_EINVAL, "gspmm: null indptr or output");
+  if (op != OP_COPY_LHS && !eid && !ident) return fail(MDGL_EINVAL, "gspmm: null eid");
+  if (op != OP_COPY_RHS && !indices) return fail(MDGL_EINVAL, "gspmm: null indices");
+  if ((op != OP_COPY_RHS && !lhs) || (op != OP_COPY_LHS && !rhs))
+    return fail(MDGL_EINVAL, "gspmm: null operand");
+  if (arg && p.arg_e && !eid && !ident) return fail(MDGL_EINVAL, "gspmm: arg_e needs eid");
+  if (arg && p.arg_u && !indices) return fail(MDGL_EINVAL, "gspmm: arg_u needs indices");
+  // copy_lhs without edge ids never reads edge data: slot ids stand in
+  if (ident || (op == OP_COPY_LHS && !eid)) p.flags |= F_EID_IDENTITY;
+  if (op == OP_COPY_RHS && !p.arg_u) p.indices = nullptr;
+  p.num_chunks = num_chunks;
+  p.chunk_row = chunk_row;
+  p.chunk_start = chunk_start;
+  p.chunk_len = chunk_len;
+  p.num_heavy = num_heavy;
+  p.heavy_rows = heavy_rows;
+  p.heavy_ptr = heavy_ptr;
+  if (num_chunks > 0) {
+    const int64_t need = mdgl_gspmm_workspace_bytes(num_chunks, dout, reduce_op, dtype);
+    if (!workspace || workspace_bytes < need)
+      return fail(MDGL_EWORKSPACE, "gspmm: workspace of %lld bytes needed, %lld given",
+                  (long long)need, (long long)workspace_bytes);
+    char* w = static_cast<char*>(workspace);
+    const int64_t n = num_chunks * dout;
+    p.part_val = w;
+    w += ((n * es + 255) / 256) * 256;
+    if (arg) {
+      p.part_u = reinterpret_cast<int32_t*>(w);
+      w += ((n * 4 + 255) / 256) * 256;
+      p.part_e = reinterpret_cast<int32_t*>(w);
+    }
+  }
+  const int vw = vec_width(dtype);
+  p.vec = dout % vw == 0 ? vw : 1;
+  p.lmode = op == OP_COPY_RHS ? M_CONTIG : pick_mode(p.bc, true, dout, p.vec, dl, lhs, es);
+  p.rmode = op == OP_COPY_LHS ? M_CONTIG : pick_mode(p.bc, false, dout, p.vec, dr, rhs, es);
+  if (p.vec > 1 && aligned(dst, p.vec * es)) p.flags |= F_OUT_VEC;
+  hipError_t e;
+  if (dtype == MDGL_FLOAT32) {
+    e = p.red == RED_MAX ? launch_gspmm_red<float, RED_MAX>(p)
+        : p.red == RED_MIN ? launch_gspmm_red<float, RED_MIN>(p)
+                           : launch_gspmm_red<float, RED_SUM>(p);
+  } else {
+    e = p.red == RED_MAX ? launch_gspmm_red<double, RED_MAX>(p)
+        : p.red == RED_MIN ? launch_gspmm_red<double, RED_MIN>(p)
+                           : launch_gspmm_red<double, RED_SUM>(p);
+  }
+  return hip_status(e, "gspmm");
+}
+
+}  // namespace
+
+extern "C" {
+
+int mdgl_gspmm(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
+               const void* lhs, const void* rhs, void* dst, int64_t num_dst, int op, int64_t dl,
+               int64_t dr, int64_t dout, int reduce_op, const int32_t* deg, int nd,
+               const int64_t* lhs_shape, const int64_t* rhs_shape, int32_t* arg_u,
+               int32_t* arg_e, const int32_t* chunk_row, const int32_t* chunk_start,
+               int64_t num_chunks, int32_t chunk_len, const int32_t* heavy_rows,
+               const int32_t* heavy_ptr, int64_t num_heavy, void* workspace,
+               int64_t workspace_bytes, int flags, int dtype, void* stream) {
+  return gspmm_common(indptr, indices, eid, lhs, rhs, dst, num_dst, op, dl, dr, dout, reduce_op,
+                      deg, nd, lhs_shape, rhs_shape, arg_u, arg_e, chunk_row, chunk_start,
+                      num_chunks, chunk_len, heavy_rows, heavy_ptr, num_heavy, workspace,
+                      workspace_bytes, flags, dtype, stream, false);
+}
+
+int mdgl_segment_reduce(const int32_t* offsets, const void* value, void* dst, int64_t num_seg,
+                        int64_t d, int reduce_op, int64_t n, int flags, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "segment_reduce: bad dtype %d", dtype);
+  if (reduce_op < RED_SUM || reduce_op > RED_MEAN)
+    return fail(MDGL_EINVAL, "segment_reduce: bad reduce_op %d", reduce_op);
+  if (num_seg < 0 || d < 0 || n < 0) return fail(MDGL_EINVAL, "segment_reduce: negative size");
+  if (num_seg >= (int64_t(1) << 31) || n >= (int64_t(1) << 31))
+    return fail(MDGL_EINVAL, "segment_reduce: 2**31 or more segments or rows");
+  if (!row_widths_fit(d, dsize(dtype))) return fail(MDGL_EINVAL, "segment_reduce: rows too wide");
+  if (num_seg == 0 || d == 0) return MDGL_OK;
+  if (!offsets || !dst || (n > 0 && !value)) return fail(MDGL_EINVAL, "segment_reduce: null buffer");
+  // a segment is a CSR row whose slots are the value rows themselves
+  return gspmm_common(offsets, nullptr, nullptr, value, value, dst, num_seg, OP_COPY_RHS, d, d, d,
+                      reduce_op, nullptr, 0, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                      0, 0, nullptr, nullptr, 0, nullptr, 0, flags, dtype, stream, true);
+}
+
+int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, void* scratch,
+                         int64_t num_seg, int64_t d, int64_t n, int dtype, void* stream) {
+  (void)scratch;
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "segment_softmax: bad dtype %d", dtype);
+  if (num_seg < 0 || d < 0 || n < 0) return fail(MDGL_EINVAL, "segment_softmax: negative size");
+  if (num_seg >= (int64_t(1) << 31) || n >= (int64_t(1) << 31))
+    return fail(MDGL_EINVAL, "segment_softmax: 2**31 or more segments or rows");
+  if (num_seg == 0 || d == 0 || n == 0) return MDGL_OK;
+  if (!offsets || !value || !dst) return fail(MDGL_EINVAL, "segment_softmax: null buffer");
+  SoftmaxParams p{};
+  p.indptr = offsets;
+  p.eid = nullptr;
+  p.mask = nullptr;
+  p.logits = value;
+  p.out = dst;
+  p.num_rows = num_seg;
+  p.d = d;
+  const int vw = vec_width(dtype);
+  const int64_t es = dsize(dtype);
+  p.vec = (d % vw == 0 && aligned(value, vw * es) && aligned(dst, vw * es)) ? vw : 1;
+  p.stream = (hipStream_t)stream;
+  hipError_t e = dtype == MDGL_FLOAT32 ? launch_softmax<float>(p) : launch_softmax<double>(p);
+  return hip_status(e, "segment_softmax");
+}
+
+int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
+                       const int8_t* mask, const void* logits, void* dst, void* scratch,
+                       int64_t num_nodes, int all_ones, int64_t d, const int32_t* heavy_rows,
+                       int64_t num_heavy, int32_t heavy_deg, int dtype, void* stream) {
+  (void)indices;
+  (void)scratch;
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "edge_softmax: bad dtype %d", dtype);
+  if (num_nodes < 0 || d < 0) return fail(MDGL_EINVAL, "edge_softmax: negative size");
+  if (num_nodes >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "edge_softmax: 2**31 or more rows");
+  if (num_heavy < 0 || (num_heavy > 0 && (!heavy_rows || heavy_deg < 0)))
+    return fail(MDGL_EINVAL, "edge_softmax: bad heavy-row list");
+  if (num_nodes == 0 || d == 0) return MDGL_OK;
+  if (!indptr || !eid || !logits || !dst) return fail(MDGL_EINVAL, "edge_softmax: null buffer");
+  if (all_ones != 1 && !mask) return fail(MDGL_EINVAL, "edge_softmax: null mask");
+  SoftmaxParams p{};
+  p.indptr = indptr;
+  p.eid = eid;
+  p.mask = all_ones == 1 ? nullptr : mask;
+  p.logits = logits;
+  p.out = dst;
+  p.num_rows = num_nodes;
+  p.d = d;
+  const int vw = vec_width(dtype);
+  const int64_t es = dsize(dtype);
+  p.vec = (d % vw == 0 && aligned(logits, vw * es) && aligned(dst, vw * es)) ? vw : 1;
+  p.num_heavy = num_heavy;
+  p.heavy_rows = heavy_rows;
+  p.heavy_deg = heavy_deg;
+  p.stream = (hipStream_t)stream;
+  hipError_t e = dtype == MDGL_FLOAT32 ? launch_softmax<float>(p) : launch_softmax<double>(p);
+  return hip_status(e, "edge_softmax");
+}
+
+int64_t mdgl_segment_mm_workspace_bytes(int64_t n, int64_t d1, int64_t d2, int64_t r, int dtype) {
+  if (n < 0 || d1 < 0 || d2 < 0 || r < 0 || !dtype_ok(dtype)) return -1;
+  return dtype == MDGL_FLOAT32 ? grouped_workspace_bytes<float>(n, d1, d2, r, false)
+                               : grouped_workspace_bytes<double>(n, d1, d2, r, false);
+}
+
+int64_t mdgl_gather_mm_workspace_bytes(int64_t n, int64_t d1, int64_t d2, int64_t r, int dtype) {
+  if (n < 0 || d1 < 0 || d2 < 0 || r < 0 || !dtype_ok(dtype)) return -1;
+  return dtype == MDGL_FLOAT32 ? grouped_workspace_bytes<float>(n, d1, d2, r, true)
+                               : grouped_workspace_bytes<double>(n, d1, d2, r, true);
+}
+
+}  // extern "C"
+
+namespace {
+
+constexpr int64_t MAX_GATHER_BLOCKS = 2048;  // bucketing keeps 5 * r ints in LDS
+
+int grouped_common(const void* a, const void* b, void* dst, const int64_t* idx_b,
+                   const int64_t* seglen, int64_t n, int64_t d1, int64_t d2, int64_t r,
+                   void* workspace, int64_t workspace_bytes, int dtype, void* stream,
+                   bool gather) {
+  const char* what = gather ? "gather_mm" : "segment_mm";
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "%s: bad dtype %d", what, dtype);
+  if (n < 0 || d1 < 0 || d2 < 0 || r < 0) return fail(MDGL_EINVAL, "%s: negative size", what);
+  if (n >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "%s: 2**31 or more rows", what);
+  if (gather && r > MAX_GATHER_BLOCKS)
+    return fail(MDGL_ENOTSUP, "%s: at most %lld b blocks supported, got %lld", what,
+                (long long)MAX_GATHER_BLOCKS, (long long)r);
+  if (n == 0 || d2 == 0) return MDGL_OK;
+  if (r == 0) return fail(MDGL_EINVAL, "%s: rows but no b blocks", what);
+  if (!a || !b || !dst || (gather ? !idx_b : !seglen))
+    return fail(MDGL_EINVAL, "%s: null buffer", what);
+  const int64_t need = gather ? mdgl_gather_mm_workspace_bytes(n, d1, d2, r, dtype)
+                              : mdgl_segment_mm_workspace_bytes(n, d1, d2, r, dtype);
+  if (!workspace || workspace_bytes < need)
+    return fail(MDGL_EWORKSPACE, "%s: workspace of %lld bytes needed, %lld given", what,
+                (long long)need, (long long)workspace_bytes);
+  GemmLaunch L{};
+  L.a = a;
+  L.b = b;
+  L.out = dst;
+  L.idx_b = idx_b;
+  L.seglen = seglen;
+  L.n = n;
+  L.K = d1;
+  L.N = d2;
+  L.R = r;
+  L.workspace = workspace;
+  L.stream = (hipStream_t)stream;
+  hipError_t e = dtype == MDGL_FLOAT32 ? launch_grouped<float>(L, gather)
+                                       : launch_grouped<double>(L, gather);
+  return hip_status(e, what);
+}
+
+}  // namespace
+
+extern "C" {
+
+int mdgl_segment_mm(const void* a, const void* b, void* dst, const int64_t* seglen_a, int64_t n,
+                    int64_t d1, int64_t r, int64_t d2, void* workspace, int64_t workspace_bytes,
+                    int dtype, void* stream) {
+  return grouped_common(a, b, dst, nullptr, seglen_a, n, d1, d2, r, workspace, workspace_bytes,
+                        dtype, stream, false);
+}
+
+int mdgl_gather_mm(const void* a, const void* b, const int64_t* idx_b, void* dst, int64_t n,
+                   int64_t d1, int64_t d2, int64_t r, void* workspace, int64_t workspace_bytes,
+                   int dtype, void* stream) {
+  return grouped_common(a, b, dst, idx_b, nullptr, n, d1, d2, r, workspace, workspace_bytes,
+                        dtype, stream, true);
+}
+
+}  // extern "C"

@@ -1,0 +1,439 @@
+// Grouped GEMM on the matrix cores behind segment_mm and gather_mm
+// (included once per dtype).
+//
+//   out[row] = a[row] @ b[g]   for every row of group g.
+//
+// segment_mm's groups are consecutive row ranges (offsets from seglen);
+// gather_mm's are the rows with idx_b == g, found by a stable counting sort
+// on the GPU (count per block, scan, ballot-ranked scatter) into `perm`.
+//
+// Tiles. A workgroup (4 wavefronts, 2 x 2) computes a 128 x 128 output tile
+// of one group: 128 rows of the group x 128 columns. Wavefront (wm, wn) owns
+// 64 x 64 of it as 4 x 4 blocks of v_mfma_{f32,f64}_16x16x4. The K axis is
+// walked in BK-deep stages staged through LDS, double buffered: the next
+// stage's global loads are in registers while the current stage multiplies.
+// b is first transposed into the workspace (bt[g][n][k], k padded to a
+// multiple of BK) so both LDS tiles are k-contiguous and every MFMA operand
+// fragment is one 16-byte LDS read: lane l reads 4 consecutive k values
+// (k = 4 * (l / 16) + s, s = 0..3) and feeds them to 4 successive MFMAs.
+// Rows are padded in LDS so those reads are bank-conflict free.
+//
+// Arithmetic. Each output element is the sum over k of a * b in the MFMA
+// units' order, in the input precision (float32 or float64); the reference
+// sums in k order (src/ported.mojo:786-790, 1115-1119), so the two agree to
+// rounding.
+#pragma once
+
+#include "mdgl_kernels.h"
+
+namespace mdgl {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+template <class T> struct Mfma;
+template <> struct Mfma<float> {
+  using acc_t = f32x4;
+  static constexpr int BK = 32;
+  static constexpr int PAD = 4;
+  __device__ static acc_t step(float a, float b, acc_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<double> {
+  using acc_t = f64x4;
+  static constexpr int BK = 16;
+  static constexpr int PAD = 2;
+  __device__ static acc_t step(double a, double b, acc_t c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+  }
+};
+
+constexpr int GBM = 128, GBN = 128;
+
+template <class T>
+struct GemmArgs {
+  const T* a;
+  const T* bt;  // [R][N][Kp]
+  T* out;
+  const int32_t* perm;       // null: group rows are contiguous
+  const int32_t* group_off;  // R + 1
+  const int32_t* tile_ptr;   // R + 1, M tiles per group (prefix)
+  int64_t R, K, Kp, N;
+  int a_vec;  // rows of a allow 16-byte loads
+};
+
+// bt[g][n][k] = b[g][k][n], zero for k in [K, Kp).
+template <class T>
+__global__ __launch_bounds__(BLOCK) void transpose_b_kernel(const T* __restrict__ b,
+                                                            T* __restrict__ bt, int64_t R,
+                                                            int64_t K, int64_t Kp, int64_t N) {
+  const int64_t total = R * N * Kp;
+  for (int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * BLOCK) {
+    const int64_t k = i % Kp, n = (i / Kp) % N, g = i / (Kp * N);
+    bt[i] = k < K ? b[(g * K + k) * N + n] : T(0);
+  }
+}
+
+template <class T>
+__global__ __launch_bounds__(BLOCK) void grouped_gemm_kernel(GemmArgs<T> p) {
+  using M = Mfma<T>;
+  using acc_t = typename M::acc_t;
+  constexpr int BK = M::BK, LD = BK + M::PAD;
+  constexpr int EV = 16 / sizeof(T);          // elements per 16-byte load
+  constexpr int CPR = BK / EV;                // 16-byte chunks per tile row per stage
+  constexpr int RPP = BLOCK / CPR;            // tile rows covered per pass of the block
+  constexpr int PASSES = GBM / RPP;           // passes to cover 128 rows
+  __shared__ __align__(16) T As[2][GBM][LD];
+  __shared__ __align__(16) T Bs[2][GBN][LD];
+  __shared__ int rowid_s[GBM];
+
+  const int64_t tile = blockIdx.x;
+  const int64_t total = p.tile_ptr[p.R];
+  if (tile >= total) return;  // uniform per workgroup
+  // group of this tile: last g with tile_ptr[g] <= tile
+  int64_t lo = 0, hi = p.R - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) / 2;
+    if (p.tile_ptr[mid] <= tile) lo = mid; else hi = mid - 1;
+  }
+  const int64_t g = lo;
+  const int64_t m0 = p.group_off[g] + (tile - p.tile_ptr[g]) * GBM;
+  const int64_t m_end = p.group_off[g + 1];
+  const int64_t n0 = (int64_t)blockIdx.y * GBN;
+  const int t = threadIdx.x;
+  if (t < GBM) {
+    const int64_t pos = m0 + t;
+    rowid_s[t] = pos < m_end ? (p.perm ? p.perm[pos] : (int32_t)pos) : -1;
+  }
+  __syncthreads();
+
+  const int lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1;
+  const int li = lane & 15, h = lane >> 4;
+  const T* bt_g = p.bt + g * p.N * p.Kp;
+
+  // global -> register staging of one stage
+  T ra[PASSES][EV], rb[PASSES][EV];
+  auto load_stage = [&](int64_t k0) {
+#pragma unroll
+    for (int q = 0; q < PASSES; ++q) {
+      const int r = q * RPP + t / CPR;
+      const int64_t kk = k0 + (t % CPR) * EV;
+      const int rid = rowid_s[r];
+      if (rid >= 0 && p.a_vec && kk + EV <= p.K) {
+        load_vec<T>(p.a + (int64_t)rid * p.K + kk, ra[q]);
+      } else {
+#pragma unroll
+        for (int v = 0; v < EV; ++v)
+          ra[q][v] = (rid >= 0 && kk + v < p.K) ? p.a[(int64_t)rid * p.K + kk + v] : T(0);
+      }
+      const int64_t n = n0 + r;
+      if (n < p.N) {
+        load_vec<T>(bt_g + n * p.Kp + kk, rb[q]);  // Kp is a multiple of BK: in bounds
+      } else {
+#pragma unroll
+        for (int v = 0; v < EV; ++v) rb[q][v] = T(0);
+      }
+    }
+  };
+  auto store_stage = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < PASSES; ++q) {
+      const int r = q * RPP + t / CPR;
+      const int c = (t % CPR) * EV;
+      store_vec<T>(&As[buf][r][c], ra[q]);
+      store_vec<T>(&Bs[buf][r][c], rb[q]);
+    }
+  };
+
+  acc_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = T(0);
+
+  const int64_t nstages = p.Kp / BK;
+  load_stage(0);
+  store_stage(0);
+  __syncthreads();
+  for (int64_t s = 0; s < nstages; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < nstages) load_stage((s + 1) * BK);
+#pragma unroll
+    for (int kc = 0; kc < BK; kc += 16) {
+      T af[4][4], bf[4][4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const T* pa = &As[buf][wm * 64 + i * 16 + li][kc + 4 * h];
+        const T* pb = &Bs[buf][wn * 64 + i * 16 + li][kc + 4 * h];
+#pragma unroll
+        for (int v = 0; v < 4; v += EV) {
+          T tmp[EV];
+          load_vec<T>(pa + v, tmp);
+#pragma unroll
+          for (int e = 0; e < EV; ++e) af[i][v + e] = tmp[e];
+          load_vec<T>(pb + v, tmp);
+#pragma unroll
+          for (int e = 0; e < EV; ++e) bf[i][v + e] = tmp[e];
+        }
+      }
+#pragma unroll
+      for (int sstep = 0; sstep < 4; ++sstep)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = M::step(af[i][sstep], bf[j][sstep], acc[i][j]);
+    }
+    if (s + 1 < nstages) {
+      store_stage(buf ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // C layout of a 16x16 block: lane l holds column l % 16, rows 4 * (l / 16) + r
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int rl = wm * 64 + i * 16 + 4 * h + r;
+      const int rid = rowid_s[rl];
+      if (rid < 0) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t n = n0 + wn * 64 + j * 16 + li;
+        if (n < p.N) p.out[(int64_t)rid * p.N + n] = acc[i][j][r];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- grouping
+// offsets[g] = exclusive prefix of seglen; tile_ptr[g] = exclusive prefix of
+// ceil(len / 128). One workgroup; R is small (number of b blocks).
+static __global__ __launch_bounds__(1024) void seg_plan_kernel(const int64_t* __restrict__ seglen,
+                                                        int32_t* __restrict__ group_off,
+                                                        int32_t* __restrict__ tile_ptr, int64_t R) {
+  if (threadIdx.x != 0) return;
+  int64_t off = 0, tiles = 0;
+  for (int64_t g = 0; g < R; ++g) {
+    group_off[g] = (int32_t)off;
+    tile_ptr[g] = (int32_t)tiles;
+    const int64_t len = seglen[g];
+    off += len;
+    tiles += (len + GBM - 1) / GBM;
+  }
+  group_off[R] = (int32_t)off;
+  tile_ptr[R] = (int32_t)tiles;
+}
+
+constexpr int SORT_CHUNK = 4096;  // rows per counting-sort workgroup
+
+// counts[b * R + g] = rows of chunk b with idx == g
+static __global__ __launch_bounds__(BLOCK) void bucket_count_kernel(const int64_t* __restrict__ idx,
+                                                             int32_t* __restrict__ counts,
+                                                             int64_t n, int64_t R) {
+  extern __shared__ int32_t hist[];
+  for (int64_t g = threadIdx.x; g < R; g += BLOCK) hist[g] = 0;
+  __syncthreads();
+  const int64_t lo = (int64_t)blockIdx.x * SORT_CHUNK;
+  const int64_t hi = lo + SORT_CHUNK < n ? lo + SORT_CHUNK : n;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += BLOCK) {
+    const int64_t key = idx[i];
+    if (key >= 0 && key < R) atomicAdd(&hist[key], 1);  // the host rejects other keys
+  }
+  __syncthreads();
+  for (int64_t g = threadIdx.x; g < R; g += BLOCK) counts[blockIdx.x * R + g] = hist[g];
+}
+
+// In place: counts[b * R + g] -> position of chunk b's first row of group g
+// in the sorted order; also group_off / tile_ptr. One workgroup, groups in
+// passes of 1024 (one thread each).
+static __global__ __launch_bounds__(1024) void bucket_scan_kernel(int32_t* __restrict__ counts,
+                                                           int32_t* __restrict__ group_off,
+                                                           int32_t* __restrict__ tile_ptr,
+                                                           int64_t nblocks, int64_t R) {
+  __shared__ int64_t tot[1024];
+  __shared__ int64_t goff[1024];
+  __shared__ int64_t run_off, run_tiles;
+  if (threadIdx.x == 0) {
+    run_off = 0;
+    run_tiles = 0;
+  }
+  __syncthreads();
+  for (int64_t g0 = 0; g0 < R; g0 += 1024) {
+    const int64_t g = g0 + threadIdx.x;
+    int64_t s = 0;
+    if (g < R)
+      for (int64_t b = 0; b < nblocks; ++b) s += counts[b * R + g];
+    tot[threadIdx.x] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int64_t off = run_off, tiles = run_tiles;
+      for (int64_t q = 0; q < 1024 && g0 + q < R; ++q) {
+        goff[q] = off;
+        group_off[g0 + q] = (int32_t)off;
+        tile_ptr[g0 + q] = (int32_t)tiles;
+        off += tot[q];
+        tiles += (tot[q] + GBM - 1) / GBM;
+      }
+      run_off = off;
+      run_tiles = tiles;
+      if (g0 + 1024 >= R) {
+        group_off[R] = (int32_t)off;
+        tile_ptr[R] = (int32_t)tiles;
+      }
+    }
+    __syncthreads();
+    if (g < R) {
+      int64_t run = goff[threadIdx.x];
+      for (int64_t b = 0; b < nblocks; ++b) {
+        const int32_t c = counts[b * R + g];
+        counts[b * R + g] = (int32_t)run;
+        run += c;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// perm[sorted position] = row, stable: rows of a group keep their order.
+// Each workgroup walks its chunk 256 rows at a time; inside a wavefront a
+// row's rank among equal keys comes from ballots over the key bits, and the
+// four wavefronts are ordered through per-wavefront counts in LDS.
+static __global__ __launch_bounds__(BLOCK) void bucket_scatter_kernel(const int64_t* __restrict__ idx,
+                                                               const int32_t* __restrict__ starts,
+                                                               int32_t* __restrict__ perm,
+                                                               int64_t n, int64_t R, int bits) {
+  extern __shared__ int32_t sm[];
+  int32_t* cursor = sm;          // R: next position per group
+  int32_t* wcount = sm + R;      // 4 x R: rows per group in each wavefront of this pass
+  for (int64_t g = threadIdx.x; g < R; g += BLOCK) cursor[g] = starts[blockIdx.x * R + g];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t lo = (int64_t)blockIdx.x * SORT_CHUNK;
+  const int64_t hi = lo + SORT_CHUNK < n ? lo + SORT_CHUNK : n;
+  __syncthreads();
+  for (int64_t base = lo; base < hi; base += BLOCK) {
+    for (int64_t g = threadIdx.x; g < 4 * R; g += BLOCK) wcount[g] = 0;
+    __syncthreads();
+    const int64_t i = base + threadIdx.x;
+    int64_t key = i < hi ? idx[i] : -1;
+    const bool ok = key >= 0 && key < R;
+    if (!ok) key = 0;
+    uint64_t same = __ballot(ok);
+    for (int bit = 0; bit < bits; ++bit) {
+      const uint64_t ones = __ballot(ok && ((key >> bit) & 1));
+      same &= ((key >> bit) & 1) ? ones : ~ones;  // lanes whose key agrees on this bit
+    }
+    const uint64_t below = lane ? (~uint64_t(0) >> (64 - lane)) : 0;
+    const int rank = __popcll(same & below);
+    const int cnt = __popcll(same);
+    if (ok && rank == 0) wcount[w * R + key] = cnt;
+    __syncthreads();
+    if (ok) {
+      int32_t pos = cursor[key] + rank;
+      for (int q = 0; q < w; ++q) pos += wcount[q * R + key];
+      perm[pos] = (int32_t)i;
+    }
+    __syncthreads();
+    for (int64_t g = threadIdx.x; g < R; g += BLOCK)
+      cursor[g] += wcount[g] + wcount[R + g] + wcount[2 * R + g] + wcount[3 * R + g];
+    __syncthreads();
+  }
+}
+
+}  // namespace mdgl
+
+
+namespace mdgl {
+
+inline int64_t ws_align(int64_t b) { return ((b + 255) / 256) * 256; }
+
+template <class T>
+inline int64_t gemm_kp(int64_t K) {
+  const int64_t bk = Mfma<T>::BK;
+  const int64_t kp = ((K + bk - 1) / bk) * bk;
+  return kp < bk ? bk : kp;
+}
+
+// Workspace of one grouped GEMM: bt, group_off, tile_ptr and, to gather,
+// the per-chunk counts and the row permutation.
+template <class T>
+int64_t grouped_workspace_bytes(int64_t n, int64_t K, int64_t N, int64_t R, bool gather) {
+  int64_t b = ws_align(R * N * gemm_kp<T>(K) * (int64_t)sizeof(T));
+  b += 2 * ws_align((R + 1) * 4);
+  if (gather) {
+    const int64_t nb = (n + SORT_CHUNK - 1) / SORT_CHUNK;
+    b += ws_align(nb * R * 4) + ws_align(n * 4);
+  }
+  return b;
+}
+
+template <class T>
+hipError_t launch_grouped(const GemmLaunch& L, bool gather) {
+  if (L.n <= 0 || L.N <= 0 || L.R <= 0) return hipSuccess;
+  const int64_t Kp = gemm_kp<T>(L.K);
+  char* w = static_cast<char*>(L.workspace);
+  T* bt = reinterpret_cast<T*>(w);
+  w += ws_align(L.R * L.N * Kp * (int64_t)sizeof(T));
+  int32_t* group_off = reinterpret_cast<int32_t*>(w);
+  w += ws_align((L.R + 1) * 4);
+  int32_t* tile_ptr = reinterpret_cast<int32_t*>(w);
+  w += ws_align((L.R + 1) * 4);
+  int32_t* perm = nullptr;
+
+  const int64_t tot = L.R * L.N * Kp;
+  int64_t tb = (tot + BLOCK - 1) / BLOCK;
+  if (tb > 65536) tb = 65536;
+  hipLaunchKernelGGL((transpose_b_kernel<T>), dim3((unsigned)tb), dim3(BLOCK), 0, L.stream,
+                     static_cast<const T*>(L.b), bt, L.R, L.K, Kp, L.N);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+
+  if (gather) {
+    const int64_t nb = (L.n + SORT_CHUNK - 1) / SORT_CHUNK;
+    int32_t* counts = reinterpret_cast<int32_t*>(w);
+    w += ws_align(nb * L.R * 4);
+    perm = reinterpret_cast<int32_t*>(w);
+    int bits = 0;
+    while ((int64_t(1) << bits) < L.R) ++bits;
+    hipLaunchKernelGGL(bucket_count_kernel, dim3((unsigned)nb), dim3(BLOCK),
+                       (size_t)(L.R * 4), L.stream, L.idx_b, counts, L.n, L.R);
+    hipLaunchKernelGGL(bucket_scan_kernel, dim3(1), dim3(1024), 0, L.stream, counts, group_off,
+                       tile_ptr, nb, L.R);
+    hipLaunchKernelGGL(bucket_scatter_kernel, dim3((unsigned)nb), dim3(BLOCK),
+                       (size_t)(5 * L.R * 4), L.stream, L.idx_b, counts, perm, L.n, L.R, bits);
+  } else {
+    hipLaunchKernelGGL(seg_plan_kernel, dim3(1), dim3(64), 0, L.stream, L.seglen, group_off,
+                       tile_ptr, L.R);
+  }
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+
+  GemmArgs<T> a;
+  a.a = static_cast<const T*>(L.a);
+  a.bt = bt;
+  a.out = static_cast<T*>(L.out);
+  a.perm = perm;
+  a.group_off = group_off;
+  a.tile_ptr = tile_ptr;
+  a.R = L.R;
+  a.K = L.K;
+  a.Kp = Kp;
+  a.N = L.N;
+  constexpr int EV = 16 / sizeof(T);
+  a.a_vec = (L.K % EV == 0) && (reinterpret_cast<uintptr_t>(L.a) % 16 == 0);
+  const int64_t mt = (L.n + GBM - 1) / GBM + L.R;
+  const int64_t nt = (L.N + GBN - 1) / GBN;
+  hipLaunchKernelGGL((grouped_gemm_kernel<T>), dim3((unsigned)mt, (unsigned)nt), dim3(BLOCK), 0,
+                     L.stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace mdgl
+
+#define MDGL_INSTANTIATE_GEMM(T)                                                               \
+  template int64_t mdgl::grouped_workspace_bytes<T>(int64_t, int64_t, int64_t, int64_t, bool); \
+  template hipError_t mdgl::launch_grouped<T>(const mdgl::GemmLaunch&, bool);

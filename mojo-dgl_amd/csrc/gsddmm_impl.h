@@ -1,0 +1,197 @@
+// Edge-parallel kernel behind gsddmm (included once per dtype).
+//
+// Elementwise ops: G consecutive lanes (power of two covering the output
+// row's vectors, at most 64) own one edge, so a wavefront writes 64 / G
+// consecutive output rows with coalesced stores; each lane gathers its VEC
+// columns from the two operand rows selected by the targets (u[e], v[e] or
+// e itself). One IEEE operation per element, so the result is bit-identical
+// to the reference's (src/ported.mojo:295-328).
+//
+// dot: G lanes own one (edge, output column) pair and split the contracted
+// axis `red` between them (VEC consecutive elements per lane per step), then
+// add the G lane partials with a butterfly of __shfl_xor. The reference keeps
+// W lane partials and reduces them once (ported.mojo:273-293), so the two
+// agree to rounding, not bit for bit.
+#pragma once
+
+#include "mdgl_kernels.h"
+
+namespace mdgl {
+
+template <class T>
+struct GsddmmArgs {
+  const int32_t* uids;
+  const int32_t* vids;
+  const T* lhs;
+  const T* rhs;
+  T* out;
+  int64_t num_edges, dl, dr, dout, red;
+  Bcast bc;
+  int lt, rt, lmode, rmode, out_vec, G, S;
+  int64_t num_tasks, num_waves, num_blocks;
+};
+
+__device__ __forceinline__ int64_t target_row(int t, const int32_t* u, const int32_t* v, int64_t e) {
+  return t == TGT_U ? (int64_t)u[e] : (t == TGT_V ? (int64_t)v[e] : e);
+}
+
+template <class T, int VEC>
+__device__ __forceinline__ void fetch_rt(const T* __restrict__ row, int mode, const int (&off)[VEC],
+                                         T (&x)[VEC]) {
+  if (VEC > 1 && mode == M_CONTIG) {
+    if constexpr (VEC == VecOf<T>::n) load_vec<T>(row + off[0], x);
+  } else if (mode == M_SPLAT) {
+    const T s = row[off[0]];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) x[v] = s;
+  } else {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) x[v] = row[off[v]];
+  }
+}
+
+template <class T, int OP, int VEC>
+__global__ __launch_bounds__(BLOCK) void gsddmm_kernel(GsddmmArgs<T> a) {
+  const int64_t blk = xcd_remap(blockIdx.x, a.num_blocks);
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int64_t wave = blk * WAVES_PER_BLOCK + (threadIdx.x >> 6);
+  if (wave >= a.num_waves) return;
+  const int G = a.G;
+  const int grp = lane / G, gl = lane % G;
+  const int64_t slab = wave % a.S;
+  const int64_t e = (wave / a.S) * (WAVE / G) + grp;
+  const int64_t k0 = (slab * G + gl) * VEC;
+  if (e >= a.num_edges || k0 >= a.dout) return;
+
+  int loff[VEC], roff[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    const int64_t k = k0 + v < a.dout ? k0 + v : k0;
+    loff[v] = (int)bcast_off(a.bc, k, true);
+    roff[v] = (int)bcast_off(a.bc, k, false);
+  }
+  T x[VEC], y[VEC], o[VEC];
+  if constexpr (OP != OP_COPY_RHS)
+    fetch_rt<T, VEC>(a.lhs + target_row(a.lt, a.uids, a.vids, e) * a.dl, a.lmode, loff, x);
+  if constexpr (OP != OP_COPY_LHS)
+    fetch_rt<T, VEC>(a.rhs + target_row(a.rt, a.uids, a.vids, e) * a.dr, a.rmode, roff, y);
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    T xv = T(0), yv = T(0);
+    if constexpr (OP != OP_COPY_RHS) xv = x[v];
+    if constexpr (OP != OP_COPY_LHS) yv = y[v];
+    o[v] = message<OP>(xv, yv);
+  }
+  const int64_t base = e * a.dout + k0;
+  if (VEC > 1 && a.out_vec) {
+    if constexpr (VEC == VecOf<T>::n) store_vec<T>(a.out + base, o);
+  } else {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+      if (k0 + v < a.dout) a.out[base + v] = o[v];
+  }
+}
+
+// dot: tasks are (edge, output column) pairs, G lanes per task.
+template <class T, int VEC>
+__global__ __launch_bounds__(BLOCK) void gsddmm_dot_kernel(GsddmmArgs<T> a) {
+  const int64_t blk = xcd_remap(blockIdx.x, a.num_blocks);
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int64_t wave = blk * WAVES_PER_BLOCK + (threadIdx.x >> 6);
+  if (wave >= a.num_waves) return;  // uniform per wavefront
+  const int G = a.G;
+  const int grp = lane / G, gl = lane % G;
+  const int64_t task = wave * (WAVE / G) + grp;
+  const bool ok = task < a.num_tasks;
+  T part = T(0);
+  int64_t e = 0, col = 0;
+  if (ok) {
+    e = task / a.dout;
+    col = task % a.dout;
+    const T* l = a.lhs + target_row(a.lt, a.uids, a.vids, e) * a.dl +
+                 bcast_off(a.bc, col, true) * a.red;
+    const T* r = a.rhs + target_row(a.rt, a.uids, a.vids, e) * a.dr +
+                 bcast_off(a.bc, col, false) * a.red;
+    for (int64_t k = (int64_t)gl * VEC; k < a.red; k += (int64_t)G * VEC) {
+      if constexpr (VEC > 1) {
+        T xv[VEC], yv[VEC];
+        load_vec<T>(l + k, xv);
+        load_vec<T>(r + k, yv);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) part = part + xv[v] * yv[v];
+      } else {
+        part = part + l[k] * r[k];
+      }
+    }
+  }
+  // butterfly inside the lane group; every lane of the wavefront runs it
+  for (int off = G >> 1; off >= 1; off >>= 1) part = part + __shfl_xor(part, off);
+  if (ok && gl == 0) a.out[e * a.dout + col] = part;
+}
+
+template <class T, int VEC>
+hipError_t launch_gsddmm_vec(const GsddmmParams& p) {
+  GsddmmArgs<T> a;
+  a.uids = p.uids;
+  a.vids = p.vids;
+  a.lhs = static_cast<const T*>(p.lhs);
+  a.rhs = static_cast<const T*>(p.rhs);
+  a.out = static_cast<T*>(p.out);
+  a.num_edges = p.num_edges;
+  a.dl = p.dl;
+  a.dr = p.dr;
+  a.dout = p.dout;
+  a.red = p.red;
+  a.bc = p.bc;
+  a.lt = p.lt;
+  a.rt = p.rt;
+  a.lmode = p.lmode;
+  a.rmode = p.rmode;
+  a.out_vec = p.out_vec;
+  if (p.op == OP_DOT) {
+    const int64_t nvec = (p.red + VEC - 1) / VEC;
+    int G = 1;
+    while (G < nvec && G < WAVE) G <<= 1;
+    a.G = G;
+    a.S = 1;
+    a.num_tasks = p.num_edges * p.dout;
+    a.num_waves = (a.num_tasks + (WAVE / G) - 1) / (WAVE / G);
+  } else {
+    const int64_t nvec = (p.dout + VEC - 1) / VEC;
+    int G = 1;
+    while (G < nvec && G < WAVE) G <<= 1;
+    a.G = G;
+    a.S = (int)((nvec + G - 1) / G);
+    a.num_tasks = p.num_edges;
+    a.num_waves = ((p.num_edges + (WAVE / G) - 1) / (WAVE / G)) * a.S;
+  }
+  a.num_blocks = (a.num_waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
+  if (a.num_blocks == 0) return hipSuccess;
+  const dim3 grid((unsigned)a.num_blocks), block(BLOCK);
+  switch (p.op) {
+    case OP_ADD: hipLaunchKernelGGL((gsddmm_kernel<T, OP_ADD, VEC>), grid, block, 0, p.stream, a); break;
+    case OP_SUB: hipLaunchKernelGGL((gsddmm_kernel<T, OP_SUB, VEC>), grid, block, 0, p.stream, a); break;
+    case OP_MUL: hipLaunchKernelGGL((gsddmm_kernel<T, OP_MUL, VEC>), grid, block, 0, p.stream, a); break;
+    case OP_DIV: hipLaunchKernelGGL((gsddmm_kernel<T, OP_DIV, VEC>), grid, block, 0, p.stream, a); break;
+    case OP_COPY_LHS:
+      hipLaunchKernelGGL((gsddmm_kernel<T, OP_COPY_LHS, VEC>), grid, block, 0, p.stream, a);
+      break;
+    case OP_COPY_RHS:
+      hipLaunchKernelGGL((gsddmm_kernel<T, OP_COPY_RHS, VEC>), grid, block, 0, p.stream, a);
+      break;
+    case OP_DOT: hipLaunchKernelGGL((gsddmm_dot_kernel<T, VEC>), grid, block, 0, p.stream, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <class T>
+hipError_t launch_gsddmm(const GsddmmParams& p) {
+  if (p.vec == VecOf<T>::n) return launch_gsddmm_vec<T, VecOf<T>::n>(p);
+  return launch_gsddmm_vec<T, 1>(p);
+}
+
+}  // namespace mdgl
+
+#define MDGL_INSTANTIATE_GSDDMM(T) \
+  template hipError_t mdgl::launch_gsddmm<T>(const mdgl::GsddmmParams&);

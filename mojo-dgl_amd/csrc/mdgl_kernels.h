@@ -1,0 +1,115 @@
+// Launch interfaces between the C ABI (capi.cpp) and the kernel translation
+// units. Every launcher is asynchronous on `stream` and returns the launch
+// status; nothing here allocates.
+#pragma once
+
+#include "mdgl_common.h"
+
+namespace mdgl {
+
+// Flags of the CSR-reduce kernel.
+enum {
+  F_MEAN = 1,          // divide the sum by max(degree, 1)
+  F_REPLACE_INF = 2,   // +-inf -> 0 on the final value (update_all max/min)
+  F_OUT_VEC = 4,       // output rows allow 16-byte stores
+  F_EID_IDENTITY = 8,  // edge id of CSR slot i is i (segment reduce)
+};
+
+// gspmm / segment_reduce: out[row, k] = red over CSR slots of row of
+// op(lhs[indices[i]], rhs[eid[i]]). Rows of degree > chunk_len are split
+// into chunks (chunk_row / chunk_start, num_chunks of them) whose partials
+// are reduced in CSR order by a second kernel over heavy_rows / heavy_ptr.
+struct GspmmParams {
+  const int32_t* indptr;
+  const int32_t* indices;  // may be null when op does not read lhs and no arg_u
+  const int32_t* eid;      // ignored with F_EID_IDENTITY
+  const int32_t* deg;      // mean divisor; null -> row length
+  const void* lhs;
+  const void* rhs;
+  void* out;
+  int32_t* arg_u;  // optional, max/min only
+  int32_t* arg_e;
+  int64_t num_rows, dl, dr, dout;
+  Bcast bc;
+  int lmode, rmode;
+  int op, red;  // red in {SUM, MAX, MIN}; mean is F_MEAN
+  int flags;
+  int vec;      // elements per lane (1 or 16 / sizeof(T))
+  int64_t num_chunks;
+  const int32_t* chunk_row;
+  const int32_t* chunk_start;
+  int32_t chunk_len;
+  int64_t num_heavy;
+  const int32_t* heavy_rows;
+  const int32_t* heavy_ptr;
+  void* part_val;
+  int32_t* part_u;
+  int32_t* part_e;
+  hipStream_t stream;
+};
+
+template <class T, int RED>
+hipError_t launch_gspmm_red(const GspmmParams& p);
+
+// gsddmm: out[e, o] = op(lhs[t_l(e)], rhs[t_r(e)]) (or the dot over `red`).
+struct GsddmmParams {
+  const int32_t* uids;
+  const int32_t* vids;
+  const void* lhs;
+  const void* rhs;
+  void* out;
+  int64_t num_edges, dl, dr, dout, red;
+  Bcast bc;
+  int lt, rt, op;
+  int lmode, rmode;
+  int out_vec;
+  int vec;
+  hipStream_t stream;
+};
+
+template <class T>
+hipError_t launch_gsddmm(const GsddmmParams& p);
+
+// CSR softmax (edge_softmax over in/out CSR, segment_softmax over offsets):
+// per row and column, max, then exp(x - max) summed, then divided.
+struct SoftmaxParams {
+  const int32_t* indptr;
+  const int32_t* eid;  // null -> identity (segment softmax)
+  const int8_t* mask;  // null -> all selected
+  const void* logits;
+  void* out;
+  int64_t num_rows, d;
+  int vec;  // elements per lane
+  int64_t num_heavy;
+  const int32_t* heavy_rows;
+  int32_t heavy_deg;  // rows above this degree are in heavy_rows
+  hipStream_t stream;
+};
+
+template <class T>
+hipError_t launch_softmax(const SoftmaxParams& p);
+
+// Grouped GEMM behind segment_mm (groups = consecutive rows, seglen) and
+// gather_mm (groups = rows with equal idx_b, bucketed on the GPU).
+struct GemmLaunch {
+  const void* a;
+  const void* b;
+  void* out;
+  const int64_t* idx_b;   // gather_mm: block of each row
+  const int64_t* seglen;  // segment_mm: rows per block
+  int64_t n, K, N, R;
+  void* workspace;
+  hipStream_t stream;
+};
+template <class T>
+int64_t grouped_workspace_bytes(int64_t n, int64_t K, int64_t N, int64_t R, bool gather);
+template <class T>
+hipError_t launch_grouped(const GemmLaunch& L, bool gather);
+
+// Elementwise helpers.
+hipError_t launch_replace_inf(const void* src, void* dst, int64_t n, int dtype, hipStream_t s);
+hipError_t launch_clamp_i64(const int64_t* src, int64_t* dst, int64_t n, int64_t lo, int64_t hi,
+                            hipStream_t s);
+hipError_t launch_cumsum_i64(const int64_t* src, int64_t* dst, int64_t n, hipStream_t s);
+
+}  // namespace mdgl

@@ -1,0 +1,275 @@
+"""Loads libmdgl.so (the gfx950 kernels) and moves data to and from the GPU.
+
+Replaces the reference's loader (python/mojodgl/_lib.py): the same code
+tables and lazy `lib()`, a ctypes signature table for the C ABI declared in
+include/mdgl.h, and the value / id ingest rules of its `f64` / `i64`
+(_lib.py:127-180), changed in one way: features keep float32 or float64
+instead of becoming float64 (every other dtype still becomes float64, with
+the reference's rejections of complex values and of integers float64 cannot
+hold).
+
+Data movement. numpy arrays (and CPU tensors) are copied to the GPU for the
+call and results come back as numpy arrays (CPU tensors); torch tensors on
+the GPU are used in place and results stay on the GPU. torch is used only for
+device memory, copies and the current stream; every kernel is libmdgl.so's.
+There is no CPU fallback: without a visible GPU a call that would launch a
+kernel raises RuntimeError.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+import torch  # loads the HIP runtime libmdgl.so then binds to
+
+from .base import DGLError
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(ROOT, "csrc")
+LIB = os.environ.get("MOJODGL_LIB") or os.path.join(ROOT, "lib", "libmdgl.so")
+
+
+class BuildError(RuntimeError):
+    pass
+
+
+# codes of src/ported.mojo:44-65 (the same values cross the C ABI)
+SRC_CODE, DST_CODE, EDGE_CODE = 0, 1, 2
+OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_DOT = 0, 1, 2, 3, 4
+OP_COPY_LHS, OP_COPY_RHS = 5, 6
+REDUCE_SUM, REDUCE_MAX, REDUCE_MIN, REDUCE_MEAN = 0, 1, 2, 3
+
+BINARY_OPS = {"add": OP_ADD, "sub": OP_SUB, "mul": OP_MUL, "div": OP_DIV, "dot": OP_DOT}
+REDUCERS = {"sum": REDUCE_SUM, "max": REDUCE_MAX, "min": REDUCE_MIN, "mean": REDUCE_MEAN}
+TARGETS = {"u": SRC_CODE, "v": DST_CODE, "e": EDGE_CODE}
+
+FLOAT32, FLOAT64 = 0, 1
+REPLACE_INF = 1
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_C = ctypes.c_int
+
+# name -> (argtypes, restype), as declared in include/mdgl.h
+_SIGNATURES = {
+    "mdgl_last_error": ([], ctypes.c_char_p),
+    "mdgl_workers": ([], _I64),
+    "mdgl_cumsum": ([_P, _P, _I64, _P], _C),
+    "mdgl_replace_inf_with_zero": ([_P, _P, _I64, _C, _P], _C),
+    "mdgl_clamp_i64": ([_P, _P, _I64, _I64, _I64, _P], _C),
+    "mdgl_gsddmm": ([_P, _P, _P, _P, _P, _I64, _C, _C, _C, _I64, _I64, _I64, _C, _P, _P, _C, _P],
+                    _C),
+    "mdgl_gspmm": ([_P, _P, _P, _P, _P, _P, _I64, _C, _I64, _I64, _I64, _C, _P, _C, _P, _P, _P,
+                    _P, _P, _P, _I64, _I32, _P, _P, _I64, _P, _I64, _C, _C, _P], _C),
+    "mdgl_gspmm_workspace_bytes": ([_I64, _I64, _C, _C], _I64),
+    "mdgl_segment_reduce": ([_P, _P, _P, _I64, _I64, _C, _I64, _C, _C, _P], _C),
+    "mdgl_segment_softmax": ([_P, _P, _P, _P, _I64, _I64, _I64, _C, _P], _C),
+    "mdgl_edge_softmax_": ([_P, _P, _P, _P, _P, _P, _P, _I64, _C, _I64, _P, _I64, _I32, _C, _P],
+                           _C),
+    "mdgl_segment_mm": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _C, _P], _C),
+    "mdgl_segment_mm_workspace_bytes": ([_I64, _I64, _I64, _I64, _C], _I64),
+    "mdgl_gather_mm": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _C, _P], _C),
+    "mdgl_gather_mm_workspace_bytes": ([_I64, _I64, _I64, _I64, _C], _I64),
+}
+
+
+def build(force: bool = False) -> str:
+    """Compile csrc/ into lib/libmdgl.so with hipcc (make decides what is stale)."""
+    cmd = ["make", "-C", CSRC, "-j8"]
+    if force:
+        subprocess.run(["make", "-C", CSRC, "clean"], check=False, capture_output=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True, timeout=1800)
+    if proc.returncode != 0 or not os.path.exists(LIB):
+        raise BuildError((proc.stderr or proc.stdout).strip()[-4000:])
+    return LIB
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded libmdgl.so. It is never built implicitly: run `build()`."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            raise BuildError(
+                "{} is missing; build it with mojodgl.build() or `make -C {}`".format(LIB, CSRC))
+        handle = ctypes.CDLL(LIB)
+        for name, (argtypes, restype) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = argtypes
+            fn.restype = restype
+        _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raise for a non-zero status of a libmdgl call."""
+    if rc == 0:
+        return
+    msg = lib().mdgl_last_error().decode(errors="replace")
+    if rc < 0:
+        raise DGLError("{}: {}".format(what, msg))
+    raise RuntimeError("{} failed on the GPU: {}".format(what, msg))
+
+
+# ------------------------------------------------------------------ device
+def device() -> torch.device:
+    if not torch.cuda.is_available():
+        raise RuntimeError(
+            "mojodgl runs its kernels on an AMD GPU through libmdgl.so and no GPU is visible")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+# ------------------------------------------------------------------ values
+_TORCH_TO_NP = {torch.float32: np.float32, torch.float64: np.float64}
+
+
+class Feat:
+    """A validated feature operand: a float32/float64 numpy array or tensor."""
+
+    __slots__ = ("data", "is_torch", "device")
+
+    def __init__(self, data, is_torch, dev):
+        self.data = data
+        self.is_torch = is_torch
+        self.device = dev
+
+    @property
+    def shape(self):
+        return tuple(self.data.shape)
+
+    @property
+    def dtype(self):
+        if self.is_torch:
+            return np.dtype(_TORCH_TO_NP[self.data.dtype])
+        return self.data.dtype
+
+    @property
+    def ndim(self):
+        return len(self.data.shape)
+
+
+def _check_int_exact(a: np.ndarray) -> None:
+    # every integer dtype but int64 must survive float64 exactly (_lib.py:144-161)
+    if np.issubdtype(a.dtype, np.integer) and a.dtype != np.int64 and a.size:
+        with np.errstate(invalid="ignore"):
+            back = a.astype(np.float64).astype(a.dtype)
+        if not bool(np.array_equal(back, a)):
+            raise DGLError("{} values do not survive the conversion to float64 exactly".format(
+                a.dtype))
+
+
+def feature(a) -> Feat:
+    """Validate a feature operand without touching the GPU."""
+    if isinstance(a, Feat):
+        return a
+    if isinstance(a, torch.Tensor):
+        if a.is_complex():
+            raise DGLError("complex features are not supported")
+        if a.dtype in (torch.float32, torch.float64):
+            t = a
+        elif a.dtype in (torch.float16, torch.bfloat16):
+            t = a.to(torch.float32)
+        else:
+            if a.dtype != torch.bool and a.dtype != torch.int64:
+                _check_int_exact(a.detach().cpu().numpy())
+            t = a.to(torch.float64)
+        return Feat(t, True, a.device)
+    arr = np.asanyarray(a)
+    if np.iscomplexobj(arr):
+        raise DGLError("complex features are not supported")
+    if arr.dtype == np.float32 or arr.dtype == np.float64:
+        out = np.ascontiguousarray(arr)
+    elif arr.dtype == np.float16:
+        out = np.ascontiguousarray(arr, dtype=np.float32)
+    else:
+        _check_int_exact(arr)
+        out = np.ascontiguousarray(arr, dtype=np.float64)
+    return Feat(out, False, None)
+
+
+def common_dtype(*feats) -> np.dtype:
+    kinds = [f.dtype for f in feats if f is not None]
+    if kinds and all(k == np.float32 for k in kinds):
+        return np.dtype(np.float32)
+    return np.dtype(np.float64)
+
+
+def dtype_code(dtype) -> int:
+    return FLOAT32 if np.dtype(dtype) == np.float32 else FLOAT64
+
+
+def torch_dtype(dtype) -> torch.dtype:
+    return torch.float32 if np.dtype(dtype) == np.float32 else torch.float64
+
+
+def on_device(f: Feat, dtype) -> torch.Tensor:
+    """The operand as a contiguous GPU tensor of `dtype` (copied if needed)."""
+    dev = device()
+    tdt = torch_dtype(dtype)
+    if f.is_torch:
+        t = f.data
+    else:
+        t = torch.from_numpy(f.data)
+    return t.to(device=dev, dtype=tdt).contiguous()
+
+
+def wants_torch(*feats) -> bool:
+    return any(f is not None and f.is_torch for f in feats)
+
+
+def out_device(*feats):
+    for f in feats:
+        if f is not None and f.is_torch:
+            return f.device
+    return None
+
+
+def give_back(t: torch.Tensor, as_torch: bool, dev):
+    """A result tensor in the caller's container: numpy, or a tensor on `dev`."""
+    if as_torch:
+        return t if dev is None or t.device == dev else t.to(dev)
+    return t.cpu().numpy()
+
+
+# ------------------------------------------------------------------ ids
+def i64(a) -> np.ndarray:
+    """Node ids / lengths as C-contiguous int64 numpy (reference _lib.py:166-180)."""
+    if isinstance(a, torch.Tensor):
+        a = a.detach().cpu().numpy()
+    a = np.asanyarray(a)
+    if np.issubdtype(a.dtype, np.floating) and a.size:
+        if not bool(np.all(a == np.floor(a))):
+            raise DGLError("node ids and segment lengths must be whole numbers, got {}".format(
+                a.dtype))
+    return np.ascontiguousarray(a, dtype=np.int64)
+
+
+def i32_device(a: np.ndarray) -> torch.Tensor:
+    """An int64 host index array as an int32 GPU tensor (values checked < 2**31)."""
+    if a.size and (int(a.max()) >= 2 ** 31 or int(a.min()) < -2 ** 31):
+        raise DGLError("index values must fit in int32 on the GPU")
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(device())
+
+
+def main() -> int:
+    print(build(force=False))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,381 @@
+"""Homogeneous graph and the message-passing dispatcher (reference
+python/mojodgl/heterograph.py).
+
+Edges keep the order they were given. The two CSR views (by destination for
+gspmm / edge_softmax(dst), by source for edge_softmax(src)) are built the
+reference's way -- bincount, cumsum, stable argsort by endpoint
+(heterograph.py:69-86), so inside a row the slots are in edge-id order, which
+fixes the fold order and the max/min tie order -- once per graph and only
+when first needed. Their GPU copies (int32) are cached with two schedules:
+
+* gspmm: rows longer than CHUNK_LEN are split into CHUNK_LEN-slot chunks
+  whose partials are folded in order, so a power-law hub is spread over
+  many wavefronts without atomics;
+* softmax: rows longer than SOFTMAX_HEAVY_DEG get a whole workgroup.
+
+`update_all` / `pull` route builtins exactly as the reference does
+(heterograph.py:206-290): copy_u, copy_e and u_{add,sub,mul,div}_e with a
+builtin reducer run as one fused gspmm; every other message is computed by
+gsddmm and reduced by gspmm(copy_rhs); max/min results get +-inf -> 0
+(done in the gspmm epilogue here, a separate pass in the reference).
+"""
+
+from __future__ import annotations
+
+from collections import namedtuple
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import i64
+from .base import DGLError, is_all
+from .function.base import TargetCode
+from .function.message import BinaryMessageFunction, CopyMessageFunction, MessageFunction
+from .function.reducer import ReduceFunction
+from .ops import spmm as _spmm
+from .ops.sddmm import gsddmm
+from .udf import EdgeBatch, FeatureDict, NodeBatch
+
+__all__ = ["DGLGraph"]
+
+_EdgeTuple = namedtuple("EdgeTuple", "u v eid")
+_Code2Str = TargetCode.CODE2STR
+
+# rows of more in-edges than this are split into chunks of this many for gspmm
+CHUNK_LEN = 512
+# rows of more edges than this get a whole workgroup in edge_softmax
+SOFTMAX_HEAVY_DEG = 1024
+
+
+def chunk_plan(indptr: np.ndarray, chunk_len: int):
+    """gspmm heavy-row schedule of a CSR, on the host.
+
+    Returns (heavy_rows, heavy_ptr, chunk_row, chunk_start): the rows with
+    more than `chunk_len` slots, and their chunks of `chunk_len` slots (the
+    last one shorter) in CSR order; chunks heavy_ptr[h]..heavy_ptr[h+1] are
+    row heavy_rows[h]'s.
+    """
+    deg = np.diff(indptr)
+    heavy = np.nonzero(deg > chunk_len)[0].astype(np.int64)
+    per = (deg[heavy] + chunk_len - 1) // chunk_len
+    ptr = np.zeros(heavy.size + 1, dtype=np.int64)
+    np.cumsum(per, out=ptr[1:])
+    row = np.repeat(heavy, per)
+    local = np.arange(int(ptr[-1]), dtype=np.int64) - np.repeat(ptr[:-1], per)
+    start = indptr[row] + local * chunk_len
+    return heavy, ptr, row, start
+
+
+class _Chunks:
+    """gspmm heavy-row schedule of one CSR, on the GPU."""
+
+    def __init__(self, indptr: np.ndarray, chunk_len: int):
+        heavy, ptr, row, start = chunk_plan(indptr, chunk_len)
+        self.chunk_len = int(chunk_len)
+        self.num_heavy = int(heavy.size)
+        self.num_chunks = int(row.size)
+        if heavy.size == 0:
+            self.chunk_row = self.chunk_start = self.heavy_rows = self.heavy_ptr = None
+            return
+        self.chunk_row = _lib.i32_device(row)
+        self.chunk_start = _lib.i32_device(start)
+        self.heavy_rows = _lib.i32_device(heavy)
+        self.heavy_ptr = _lib.i32_device(ptr)
+
+
+class _DeviceCSR:
+    """A CSR view on the GPU (int32) with its gspmm and softmax schedules."""
+
+    def __init__(self, indptr, indices, order, chunk_len, heavy_deg):
+        self.indptr = _lib.i32_device(indptr)
+        self.indices = _lib.i32_device(indices)
+        self.eid = _lib.i32_device(order)
+        self.chunks = _Chunks(indptr, chunk_len)
+        deg = np.diff(indptr)
+        hv = np.nonzero(deg > heavy_deg)[0]
+        self.num_soft_heavy = int(hv.size)
+        self.soft_heavy = _lib.i32_device(hv) if hv.size else None
+        self.soft_heavy_deg = int(heavy_deg)
+        self.params = (int(chunk_len), int(heavy_deg))
+
+
+class DGLGraph(object):
+    """A homogeneous graph whose message passing runs on the GPU."""
+
+    def __init__(self, u, v, num_nodes=None, idtype=np.int64):
+        u = i64(u)
+        v = i64(v)
+        if u.shape != v.shape:
+            raise DGLError("u and v must have the same length")
+        if num_nodes is None:
+            num_nodes = 0 if u.size == 0 else int(max(u.max(), v.max())) + 1
+        num_nodes = int(num_nodes)
+        if num_nodes < 0:
+            raise DGLError("num_nodes must be non-negative, got {}".format(num_nodes))
+        if u.size and (int(u.max()) >= num_nodes or int(v.max()) >= num_nodes
+                       or int(u.min()) < 0 or int(v.min()) < 0):
+            raise DGLError("node ids must be in [0, {}), got [{}, {}]".format(
+                num_nodes, int(min(u.min(), v.min())), int(max(u.max(), v.max()))))
+        self._u = u
+        self._v = v
+        self._num_nodes = num_nodes
+        self.idtype = idtype
+        self._nstore = {}
+        self._estore = {}
+        self.ndata = FeatureDict(self._nstore, self._num_nodes, "ndata")
+        self.edata = FeatureDict(self._estore, len(u), "edata")
+        self._csr = {}
+        self._dcsr = {}
+        self._dcoo = None
+
+    # ------------------------------------------------------------------ csr
+    def _build(self, kind):
+        key, other = (self._v, self._u) if kind == "in" else (self._u, self._v)
+        deg = np.bincount(key, minlength=self._num_nodes).astype(np.int64)
+        indptr = np.zeros(self._num_nodes + 1, dtype=np.int64)
+        np.cumsum(deg, out=indptr[1:])
+        order = np.argsort(key, kind="stable").astype(np.int64)
+        self._csr[kind] = (indptr, np.ascontiguousarray(other[order]), order, deg)
+
+    def _host_csr(self, kind):
+        if kind not in self._csr:
+            self._build(kind)
+        return self._csr[kind]
+
+    def _edge_arrays(self):
+        return self._u, self._v
+
+    def _in_csr(self):
+        return self._host_csr("in")[:3]
+
+    def _out_csr(self):
+        return self._host_csr("out")[:3]
+
+    def _check_int32(self):
+        if self._u.size >= 2 ** 31 or self._num_nodes >= 2 ** 31:
+            raise DGLError("graphs with 2**31 or more nodes or edges are not supported on the GPU")
+
+    def _device_csr(self, kind):
+        """The GPU copy of the in ("in") or out ("out") CSR, built once."""
+        self._check_int32()
+        params = (int(CHUNK_LEN), int(SOFTMAX_HEAVY_DEG))
+        cached = self._dcsr.get(kind)
+        if cached is None or cached.params != params:
+            indptr, indices, order, _ = self._host_csr(kind)
+            cached = _DeviceCSR(indptr, indices, order, *params)
+            self._dcsr[kind] = cached
+        return cached
+
+    def _device_coo(self):
+        """int32 GPU copies of the edge endpoints, in edge-id order."""
+        self._check_int32()
+        if self._dcoo is None:
+            self._dcoo = (_lib.i32_device(self._u), _lib.i32_device(self._v))
+        return self._dcoo
+
+    def _softmax_heavy_deg(self):
+        return int(SOFTMAX_HEAVY_DEG)
+
+    # -------------------------------------------------------------- queries
+    def number_of_nodes(self, ntype=None):
+        return self._num_nodes
+
+    def number_of_src_nodes(self, ntype=None):
+        return self._num_nodes
+
+    def number_of_dst_nodes(self, ntype=None):
+        return self._num_nodes
+
+    @property
+    def canonical_etypes(self):
+        return (("_N", "_E", "_N"),)
+
+    def number_of_edges(self, etype=None):
+        return int(self._u.size)
+
+    def num_nodes(self):
+        return self._num_nodes
+
+    def num_edges(self):
+        return int(self._u.size)
+
+    def num_src_nodes(self):
+        return self._num_nodes
+
+    def num_dst_nodes(self):
+        return self._num_nodes
+
+    def __len__(self):
+        return self._num_nodes
+
+    def __repr__(self):
+        return "Graph(num_nodes={}, num_edges={},)".format(self._num_nodes, self.num_edges())
+
+    def __str__(self):
+        return self.__repr__()
+
+    def edges(self, form="uv", order="eid", etype=None):
+        """All edges as a named tuple of (u, v, eid), in edge-id order."""
+        if form not in ("uv", "all"):
+            raise DGLError("form must be 'uv' or 'all'")
+        if order != "eid":
+            raise DGLError("only order='eid' is supported")
+        return _EdgeTuple(self._u, self._v, np.arange(self._u.size, dtype=np.int64))
+
+    def _select(self, ids, order, on_src):
+        if is_all(ids):
+            sel = np.arange(self._u.size)
+        else:
+            key = self._u if on_src else self._v
+            sel = np.nonzero(np.isin(key, i64(ids)))[0]
+        if order == "srcid":
+            sel = sel[np.argsort(self._u[sel], kind="stable")]
+        elif order == "dstid":
+            sel = sel[np.argsort(self._v[sel], kind="stable")]
+        sel = sel.astype(np.int64)
+        return _EdgeTuple(self._u[sel], self._v[sel], sel)
+
+    def in_edges(self, v, form="uv", order="eid", etype=None):
+        """All in-edges of `v` (every node when `v` is ALL), in edge-id order."""
+        return self._select(v, order, False)
+
+    def out_edges(self, u, form="uv", order="eid", etype=None):
+        """All out-edges of `u` (every node when `u` is ALL), in edge-id order."""
+        return self._select(u, order, True)
+
+    def in_degrees(self, v=None):
+        deg = self._host_csr("in")[3]
+        return deg if v is None else deg[i64(v)]
+
+    def out_degrees(self, u=None):
+        deg = self._host_csr("out")[3]
+        return deg if u is None else deg[i64(u)]
+
+    # ------------------------------------------------------- message passing
+    def _builtin_message(self, message_func):
+        """Per-edge messages of a builtin message function (gsddmm)."""
+        if isinstance(message_func, CopyMessageFunction):
+            target = _Code2Str[message_func.target]
+            if target == "e":
+                return self.edata[message_func.in_field]
+            return gsddmm(self, "copy_lhs", self.ndata[message_func.in_field], None,
+                          lhs_target=target)
+        if not isinstance(message_func, BinaryMessageFunction):
+            raise DGLError("unrecognised message function {}".format(message_func))
+        lhs = _Code2Str[message_func.lhs]
+        rhs = _Code2Str[message_func.rhs]
+        lhs_data = self.edata[message_func.lhs_field] if lhs == "e" \
+            else self.ndata[message_func.lhs_field]
+        rhs_data = self.edata[message_func.rhs_field] if rhs == "e" \
+            else self.ndata[message_func.rhs_field]
+        return gsddmm(self, message_func.binary_op, lhs_data, rhs_data, lhs_target=lhs,
+                      rhs_target=rhs)
+
+    def _fusable(self, message_func):
+        """(op, lhs field, rhs field) when gspmm computes message and reduce at once."""
+        if isinstance(message_func, CopyMessageFunction):
+            target = _Code2Str[message_func.target]
+            if target == "u":
+                return "copy_lhs", message_func.in_field, None
+            if target == "e":
+                return "copy_rhs", None, message_func.in_field
+            return None
+        if not isinstance(message_func, BinaryMessageFunction):
+            return None
+        if message_func.binary_op == "dot":
+            return None
+        if _Code2Str[message_func.lhs] != "u" or _Code2Str[message_func.rhs] != "e":
+            return None
+        return message_func.binary_op, message_func.lhs_field, message_func.rhs_field
+
+    def _reduce(self, op, reduce_op, lhs, rhs):
+        """gspmm whose max/min results get +-inf -> 0, as message passing wants."""
+        out, _, _, as_torch, dev = _spmm._run(self, op, reduce_op, lhs, rhs,
+                                              replace_inf=reduce_op in ("max", "min"))
+        return _lib.give_back(out, as_torch, dev)
+
+    def _pass(self, message_func, reduce_func, apply_node_func, write=True):
+        """One message-passing round; returns the new node features.
+
+        `write=False` leaves the feature store untouched (for `pull`).
+        """
+        num_nodes = self._num_nodes
+        fused = self._fusable(message_func) if isinstance(message_func, MessageFunction) \
+            else None
+        if fused is not None and isinstance(reduce_func, ReduceFunction):
+            op, lhs_field, rhs_field = fused
+            lhs_data = self.ndata[lhs_field] if lhs_field is not None else None
+            rhs_data = self.edata[rhs_field] if rhs_field is not None else None
+            result = {reduce_func.out_field: self._reduce(op, reduce_func.name, lhs_data,
+                                                          rhs_data)}
+        else:
+            if isinstance(message_func, MessageFunction):
+                messages = {message_func.out_field: self._builtin_message(message_func)}
+            else:
+                edges = EdgeBatch(self, np.arange(self._u.size, dtype=np.int64))
+                messages = dict(message_func(edges))
+            if isinstance(reduce_func, ReduceFunction):
+                key = next(iter(messages))
+                result = {reduce_func.out_field: self._reduce("copy_rhs", reduce_func.name, None,
+                                                              messages[key])}
+            else:
+                # the reduce UDF sees each message field pre-summed over in-edges
+                mailbox = {k: self._reduce("copy_rhs", "sum", None, m)
+                           for k, m in messages.items()}
+                nodes = NodeBatch(data=self._nstore, mailbox=mailbox, num_nodes=num_nodes)
+                result = dict(reduce_func(nodes))
+        if apply_node_func is not None:
+            nodes = NodeBatch(data=result, mailbox=None, num_nodes=num_nodes)
+            result = dict(apply_node_func(nodes))
+        if write:
+            for key, value in result.items():
+                self.ndata[key] = value
+        return result
+
+    def update_all(self, message_func, reduce_func, apply_node_func=None, etype=None):
+        """Send messages along all the edges and update all the nodes.
+
+        Parameters
+        ----------
+        message_func : builtin message function or callable(EdgeBatch) -> dict
+        reduce_func : builtin reduce function or callable(NodeBatch) -> dict
+        apply_node_func : callable(NodeBatch) -> dict, optional
+        etype : str or (str, str, str), optional
+
+        Nodes without in-edges get zero from every builtin reducer.
+        """
+        if etype is not None and etype not in self.canonical_etypes:
+            raise DGLError("etype {} not in {}".format(etype, self.canonical_etypes))
+        self._pass(message_func, reduce_func, apply_node_func)
+
+    def pull(self, v, message_func, reduce_func, apply_node_func=None, etype=None):
+        """Pull messages from the in-edges of nodes `v` and update only those rows.
+
+        The written feature is zero outside `v` (reference heterograph.py:318-347).
+        """
+        if etype is not None and etype not in self.canonical_etypes:
+            raise DGLError("etype {} not in {}".format(etype, self.canonical_etypes))
+        v = np.unique(i64(v))
+        if v.size == 0:
+            return
+        mask = np.isin(self._v, v)
+        sub = DGLGraph(self._u[mask], self._v[mask], num_nodes=self._num_nodes)
+        for key, value in self._nstore.items():
+            sub.ndata[key] = value
+        for key, value in self._estore.items():
+            if isinstance(value, torch.Tensor):
+                sub.edata[key] = value[torch.as_tensor(mask, device=value.device)]
+            else:
+                sub.edata[key] = value[mask]
+        result = sub._pass(message_func, reduce_func, apply_node_func, write=False)
+        for key, value in result.items():
+            if isinstance(value, torch.Tensor):
+                rows = torch.zeros_like(value)
+                idx = torch.as_tensor(v, device=value.device)
+                rows[idx] = value[idx]
+            else:
+                value = np.asarray(value)
+                rows = np.zeros_like(value)
+                rows[v] = value[v]
+            self.ndata[key] = rows

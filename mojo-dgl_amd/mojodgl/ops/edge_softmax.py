@@ -1,0 +1,113 @@
+"""edge_softmax (reference python/mojodgl/ops/edge_softmax.py).
+
+Same arguments, shapes and errors as the reference, including its positional
+`eids` rule (edge_softmax.py:119-158): with a subset `eids`, the positions of
+`eids` are grouped by endpoint (groups in ascending endpoint id, positions in
+the order they appear), position i reads `logits[i]`, and the result is as
+long as `logits` with rows past len(eids) zero. The grouping is one stable
+argsort here instead of a Python loop; logits keep float32/float64.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from .. import _lib
+from ..base import ALL, DGLError, is_all
+
+__all__ = ["edge_softmax"]
+
+
+def edge_softmax(graph, logits, eids=ALL, norm_by="dst"):
+    r"""Compute softmax over weights of incoming edges for every node.
+
+    For a node :math:`i`, edge softmax is an operation that computes
+
+    .. math::
+      a_{ij} = \frac{\exp(z_{ij})}{\sum_{j\in\mathcal{N}(i)}\exp(z_{ij})}
+
+    where :math:`z_{ij}` is the signal (logit) of edge :math:`j\rightarrow i`.
+    ``norm_by='dst'`` normalizes over each node's incoming edges (GAT,
+    Transformer); ``norm_by='src'`` over its outgoing edges.
+
+    Parameters
+    ----------
+    graph : DGLGraph
+    logits : array or tensor of shape ``(E,)``, ``(E, 1)`` or ``(E, *, 1)``;
+        every trailing column is an independent softmax.
+    eids : array of edge ids or ALL
+    norm_by : 'src' or 'dst'
+
+    Returns
+    -------
+    Softmax values, of the same shape as ``logits``.
+
+    Examples
+    --------
+    >>> g = mojodgl.graph(([0, 0, 0, 1, 1, 2], [0, 1, 2, 1, 2, 2]))
+    >>> edge_softmax(g, np.ones((6, 1)))
+    array([[1.        ],
+           [0.5       ],
+           [0.33333333],
+           [0.5       ],
+           [0.33333333],
+           [0.33333333]])
+    """
+    num_edges = graph.number_of_edges()
+    X = _lib.feature(logits)
+    shape = X.shape
+    if len(shape) == 1:
+        d = 1
+    elif len(shape) >= 2 and shape[-1] == 1:
+        d = int(np.prod(shape[1:], dtype=np.int64))
+    else:
+        raise DGLError("logits must be (E,), (E, 1) or (E, *, 1); got shape {}".format(shape))
+    if norm_by not in ("dst", "src"):
+        raise DGLError("norm_by must be 'src' or 'dst'")
+    num_nodes = graph.number_of_nodes()
+    if is_all(eids):
+        order = None
+    else:
+        order = _lib.i64(eids)
+        if order.size and (int(order.min()) < 0 or int(order.max()) >= num_edges):
+            raise DGLError("edge ids must be in [0, {}), got [{}, {})".format(
+                num_edges, int(order.min()), int(order.max()) + 1))
+    out_len = shape[0]
+    if order is None and out_len != num_edges:
+        raise DGLError("logits has {} rows but the graph has {} edges".format(out_len, num_edges))
+    if order is not None and order.size > out_len:
+        raise DGLError("{} edge ids selected but logits has only {} rows".format(
+            order.size, out_len))
+
+    dtype = X.dtype
+    gdev = _lib.device()
+    out = torch.zeros((out_len, d), dtype=_lib.torch_dtype(dtype), device=gdev)
+    if out_len and d:
+        lg = _lib.on_device(X, dtype).reshape(out_len, d)
+        if order is None:
+            csr = graph._device_csr("in" if norm_by == "dst" else "out")
+            indptr, eid, rows = csr.indptr, csr.eid, num_nodes
+            heavy, num_heavy, heavy_deg = csr.soft_heavy, csr.num_soft_heavy, csr.soft_heavy_deg
+        else:
+            u, v = graph._edge_arrays()
+            key = (v if norm_by == "dst" else u)[order]
+            pos = np.argsort(key, kind="stable")  # positions by (endpoint, appearance)
+            counts = np.bincount(key, minlength=num_nodes)
+            counts = counts[counts > 0]
+            ptr = np.zeros(counts.size + 1, dtype=np.int64)
+            np.cumsum(counts, out=ptr[1:])
+            rows = int(counts.size)
+            indptr, eid = _lib.i32_device(ptr), _lib.i32_device(pos)
+            heavy_deg = graph._softmax_heavy_deg()
+            hv = np.nonzero(counts > heavy_deg)[0]
+            num_heavy = int(hv.size)
+            heavy = _lib.i32_device(hv) if num_heavy else None
+            lg = lg[: order.size].contiguous()
+        if rows:
+            rc = _lib.lib().mdgl_edge_softmax_(
+                indptr.data_ptr(), None, eid.data_ptr(), None, lg.data_ptr(), out.data_ptr(), None,
+                rows, 1, d, _lib.ptr(heavy), num_heavy, heavy_deg, _lib.dtype_code(dtype),
+                _lib.stream())
+            _lib.check(rc, "edge_softmax")
+    return _lib.give_back(out.reshape(shape), X.is_torch, X.device)

@@ -1,0 +1,74 @@
+"""gather_mm (reference python/mojodgl/ops/gather_mm.py).
+
+Same arguments and validation. Both of the reference's routes are kept and
+give the same numbers: above `_SEGMENT_BLOCK` (D1 * D2) the rows are sorted
+by `idx_b` on the host side of the call and multiplied with segment_mm, as
+the reference does; otherwise one mdgl_gather_mm call buckets the rows on the
+GPU and multiplies them block by block on the matrix cores.
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import torch
+
+from .. import _lib
+from ..base import DGLError
+from .segment import _grouped_mm
+
+__all__ = ["gather_mm"]
+
+# D1 * D2 above which the sorted segment_mm route is taken (the reference's
+# switch, overridable by the same environment variable).
+_SEGMENT_BLOCK = int(os.environ.get("MOJODGL_GATHER_MM_SEGMENT_BLOCK", 16384))
+
+
+def gather_mm(a, b, *, idx_b):
+    r"""Gather data according to the given indices and perform matrix multiplication.
+
+    Let the result tensor be ``c``, the operator conducts the following computation:
+
+      c[i] = a[i] @ b[idx_b[i]]
+      , where len(c) == len(idx_b)
+
+    Parameters
+    ----------
+    a : (N, D1) array or tensor
+    b : (R, D1, D2) array or tensor
+    idx_b : (N,) integer indices into the first axis of b
+
+    Returns
+    -------
+    The (N, D2) product.
+    """
+    A = _lib.feature(a)
+    B = _lib.feature(b)
+    if A.ndim != 2 or B.ndim != 3:
+        raise DGLError("gather_mm wants a 2-D and a 3-D operand")
+    N, D1 = A.shape
+    R, b_d1, D2 = B.shape
+    if b_d1 != D1:
+        raise DGLError("inner dimensions do not match: a is {} wide, b blocks are {}".format(
+            D1, b_d1))
+    idx = _lib.i64(idx_b)
+    if idx.ndim != 1 or idx.size != N:
+        raise DGLError("idx_b must be 1-D with one index per row of a: got shape {} for "
+                       "N={}".format(idx.shape, N))
+    if idx.size and (int(idx.min()) < 0 or int(idx.max()) >= R):
+        raise DGLError("idx_b must be in [0, {}), got [{}, {})".format(
+            R, int(idx.min()), int(idx.max()) + 1))
+    as_torch, dev = _lib.wants_torch(A, B), _lib.out_device(A, B)
+    if D1 * D2 > _SEGMENT_BLOCK:
+        perm = np.argsort(idx, kind="stable")
+        seglen = np.bincount(idx, minlength=R).astype(np.int64)
+        gdev = _lib.device()
+        p = torch.from_numpy(perm).to(gdev)
+        a_sorted = _lib.on_device(A, _lib.common_dtype(A, B)).index_select(0, p)
+        out_sorted = _grouped_mm(_lib.Feat(a_sorted, True, gdev), B, None, seglen, gather=False)
+        out = torch.empty_like(out_sorted)
+        out.index_copy_(0, p, out_sorted)
+    else:
+        out = _grouped_mm(A, B, idx, None, gather=True)
+    return _lib.give_back(out, as_torch, dev)

@@ -1,0 +1,205 @@
+"""Segment operators (reference python/mojodgl/ops/segment.py).
+
+segment_reduce, segment_softmax and segment_mm with the reference's
+arguments, validation and empty-segment conventions; values keep their
+float32/float64 dtype. The offsets ([0] + cumsum(seglen)) are formed on the
+host, where they are validated anyway, and uploaded as int32.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from .. import _lib
+from .._lib import REDUCERS
+from ..base import DGLError
+
+__all__ = ["segment_reduce", "segment_softmax", "segment_mm"]
+
+
+def _offsets(seglen: np.ndarray) -> np.ndarray:
+    out = np.zeros(seglen.size + 1, dtype=np.int64)
+    np.cumsum(seglen, out=out[1:])
+    return out
+
+
+def _check_offsets(offsets, n):
+    if offsets.size and (int(offsets[-1]) != n or bool(np.any(np.diff(offsets) < 0))):
+        raise DGLError(
+            "segment lengths must be non-negative and sum to {}, got offsets ending at {} for "
+            "{} rows".format(n, int(offsets[-1]) if offsets.size else 0, n))
+
+
+def _flat_width(shape):
+    return 1 if len(shape) < 2 else int(np.prod(shape[1:], dtype=np.int64))
+
+
+def segment_reduce(seglen, value, reducer="sum"):
+    """Segment reduction operator.
+
+    It aggregates the value tensor along the first dimension by segments.
+    The first argument ``seglen`` stores the length of each segment. Its
+    summation must be equal to the first dimension of the ``value`` tensor.
+    Zero-length segments are allowed.
+
+    Parameters
+    ----------
+    seglen : array or tensor of segment lengths
+    value : array or tensor to aggregate
+    reducer : 'sum', 'max', 'min' or 'mean'
+
+    Returns
+    -------
+    Aggregated values of shape ``(len(seglen), value.shape[1:])`` (a 1-D value
+    gives ``(len(seglen), 1)``). Empty segments give 0 for every reducer.
+
+    Examples
+    --------
+    >>> val = np.ones((10, 3))
+    >>> seg = np.array([1, 0, 5, 4])
+    >>> segment_reduce(seg, val)
+    array([[1., 1., 1.],
+           [0., 0., 0.],
+           [5., 5., 5.],
+           [4., 4., 4.]])
+    """
+    seglen = _lib.i64(seglen)
+    offsets = _offsets(seglen)
+    V = _lib.feature(value)
+    if reducer not in ("sum", "max", "min", "mean"):
+        raise DGLError("reducer {} not recognized.".format(reducer))
+    n = V.shape[0] if V.ndim else 0
+    _check_offsets(offsets, n)
+    d = _flat_width(V.shape)
+    fshape = tuple(V.shape[1:]) if V.ndim > 1 else (1,)
+    num_seg = seglen.size
+    dtype = V.dtype
+    gdev = _lib.device()
+    out = torch.empty((num_seg, d), dtype=_lib.torch_dtype(dtype), device=gdev)
+    if num_seg and d:
+        val = _lib.on_device(V, dtype)
+        off = _lib.i32_device(offsets)
+        flags = _lib.REPLACE_INF if reducer in ("max", "min") else 0
+        rc = _lib.lib().mdgl_segment_reduce(off.data_ptr(), val.data_ptr(), out.data_ptr(),
+                                            num_seg, d, REDUCERS[reducer], n, flags,
+                                            _lib.dtype_code(dtype), _lib.stream())
+        _lib.check(rc, "segment_reduce")
+    return _lib.give_back(out.reshape((num_seg,) + fshape), V.is_torch, V.device)
+
+
+def segment_softmax(seglen, value):
+    """Softmax over the rows of each segment, per column.
+
+    The first argument ``seglen`` stores the length of each segment. Its
+    summation must be equal to the first dimension of the ``value`` tensor.
+    Zero-length segments are allowed.
+
+    Returns
+    -------
+    Result of the same shape as ``value``.
+    """
+    seglen = _lib.i64(seglen)
+    V = _lib.feature(value)
+    shape = V.shape
+    n = shape[0] if len(shape) else 0
+    d = _flat_width(shape)
+    offsets = _offsets(seglen)
+    _check_offsets(offsets, n)
+    num_seg = seglen.size
+    dtype = V.dtype
+    gdev = _lib.device()
+    out = torch.zeros((n, d), dtype=_lib.torch_dtype(dtype), device=gdev)
+    if num_seg and n and d:
+        val = _lib.on_device(V, dtype)
+        off = _lib.i32_device(offsets)
+        rc = _lib.lib().mdgl_segment_softmax(off.data_ptr(), val.data_ptr(), out.data_ptr(), None,
+                                             num_seg, d, n, _lib.dtype_code(dtype), _lib.stream())
+        _lib.check(rc, "segment_softmax")
+    return _lib.give_back(out.reshape(shape), V.is_torch, V.device)
+
+
+def _grouped_mm(a, b, idx_b, seglen, gather):
+    """Launch the grouped GEMM; returns the (n, d2) GPU tensor."""
+    n, d1 = a.shape
+    r, _, d2 = b.shape
+    dtype = _lib.common_dtype(a, b)
+    gdev = _lib.device()
+    tdt = _lib.torch_dtype(dtype)
+    out = torch.zeros((n, d2), dtype=tdt, device=gdev)
+    if n == 0 or d2 == 0:
+        return out
+    A = _lib.on_device(a, dtype)
+    B = _lib.on_device(b, dtype)
+    code = _lib.dtype_code(dtype)
+    L = _lib.lib()
+    if gather:
+        nbytes = L.mdgl_gather_mm_workspace_bytes(n, d1, d2, r, code)
+    else:
+        nbytes = L.mdgl_segment_mm_workspace_bytes(n, d1, d2, r, code)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=gdev)
+    if gather:
+        idx = torch.as_tensor(idx_b, dtype=torch.int64).to(gdev).contiguous()
+        rc = L.mdgl_gather_mm(A.data_ptr(), B.data_ptr(), idx.data_ptr(), out.data_ptr(), n, d1,
+                              d2, r, ws.data_ptr(), nbytes, code, _lib.stream())
+        _lib.check(rc, "gather_mm")
+    else:
+        sl = torch.as_tensor(seglen, dtype=torch.int64).to(gdev).contiguous()
+        rc = L.mdgl_segment_mm(A.data_ptr(), B.data_ptr(), out.data_ptr(), sl.data_ptr(), n, d1, r,
+                               d2, ws.data_ptr(), nbytes, code, _lib.stream())
+        _lib.check(rc, "segment_mm")
+    return out
+
+
+def segment_mm(a, b, seglen_a):
+    r"""Performs matrix multiplication according to segments.
+
+    Suppose ``seglen_a == [10, 5, 0, 3]``, the operator will perform
+    four matrix multiplications::
+
+        a[0:10] @ b[0], a[10:15] @ b[1],
+        a[15:15] @ b[2], a[15:18] @ b[3]
+
+    Parameters
+    ----------
+    a : (N, D1) array or tensor
+    b : (R, D1, D2) array or tensor
+    seglen_a : (R,) integer lengths, non-negative, summing to at most N
+
+    Returns
+    -------
+    The (N, D2) product; rows past ``sum(seglen_a)`` are zero.
+    """
+    A = _lib.feature(a)
+    B = _lib.feature(b)
+    if A.ndim != 2 or B.ndim != 3:
+        raise DGLError("segment_mm wants a 2-D left operand and a 3-D right operand")
+    n, d1 = A.shape
+    r, b_d1, d2 = B.shape
+    if b_d1 != d1:
+        raise DGLError("inner dimensions do not match: {} vs {}".format(d1, b_d1))
+    seglen_a = _lib.i64(seglen_a)
+    if seglen_a.size != r:
+        raise DGLError("seglen_a must have one entry per b block: {} != {}".format(
+            seglen_a.size, r))
+    if seglen_a.size:
+        lo = int(seglen_a.min())
+        total = int(seglen_a.sum())
+        if lo < 0 or total > n:
+            raise DGLError(
+                "segment lengths must be non-negative and sum to {}, got a minimum of {} and a "
+                "sum of {}".format(n, lo, total))
+    out = _grouped_mm(A, B, None, seglen_a, gather=False)
+    return _lib.give_back(out, _lib.wants_torch(A, B), _lib.out_device(A, B))
+
+
+def _replace_inf_with_zero(x):
+    """+-inf -> 0, elementwise (reference segment.py:55-59), through the GPU kernel."""
+    X = _lib.feature(x)
+    dtype = X.dtype
+    t = _lib.on_device(X, dtype)
+    out = torch.empty_like(t)
+    rc = _lib.lib().mdgl_replace_inf_with_zero(t.data_ptr(), out.data_ptr(), t.numel(),
+                                               _lib.dtype_code(dtype), _lib.stream())
+    _lib.check(rc, "replace_inf_with_zero")
+    return _lib.give_back(out, X.is_torch, X.device)

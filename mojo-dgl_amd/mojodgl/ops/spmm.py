@@ -1,0 +1,193 @@
+"""gspmm and its generated variants (reference python/mojodgl/ops/spmm.py).
+
+Same entry points, argument meaning and errors as the reference; operands
+broadcast with NumPy's rules and keep their float32/float64 dtype. `_gspmm`
+additionally returns the arg indices of max/min, which the reference does
+not produce (its kernel writes values only, src/ported.mojo:352-423).
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import torch
+
+from .. import _lib
+from .._lib import BINARY_OPS, OP_COPY_LHS, OP_COPY_RHS, REDUCERS
+from ..base import DGLError
+from .sddmm import _check_rows, feat_shape, out_feat_shape, reshape_lhs_rhs, shape_args, width
+
+__all__ = ["gspmm"]
+
+
+def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False,
+         arg_dtype=torch.int64):
+    """Validate, launch, and return device tensors (out, arg_u, arg_e) plus
+    the caller-container info."""
+    if reduce_op not in REDUCERS:
+        raise DGLError("reduce_op {} not recognized".format(reduce_op))
+    if op not in list(BINARY_OPS) + ["copy_lhs", "copy_rhs"]:
+        raise DGLError("op {} not recognized".format(op))
+    if op == "dot":
+        raise DGLError("dot is not a gspmm operator; use gsddmm")
+    num_dst = g.number_of_nodes()
+    num_edges = g.number_of_edges()
+    L = R = None
+    if op == "copy_lhs":
+        L = _lib.feature(lhs_data)
+        fshape = feat_shape(L.shape)
+        code = OP_COPY_LHS
+        _check_rows(L, num_dst, "node")
+    elif op == "copy_rhs":
+        R = _lib.feature(rhs_data)
+        fshape = feat_shape(R.shape)
+        code = OP_COPY_RHS
+        _check_rows(R, num_edges, "edge")
+    else:
+        L, R = reshape_lhs_rhs(_lib.feature(lhs_data), _lib.feature(rhs_data))
+        fshape = out_feat_shape(L.shape, R.shape)
+        code = BINARY_OPS[op]
+        _check_rows(L, num_dst, "node")
+        _check_rows(R, num_edges, "edge")
+    dtype = _lib.common_dtype(L, R)
+    as_torch = _lib.wants_torch(L, R)
+    dev = _lib.out_device(L, R)
+    dout = int(np.prod(fshape, dtype=np.int64))
+    shape = (num_dst,) + tuple(fshape)
+    tdt = _lib.torch_dtype(dtype)
+    gdev = _lib.device()
+    out = torch.empty((num_dst, dout), dtype=tdt, device=gdev)
+    arg = want_arg and reduce_op in ("max", "min")
+    arg_u = torch.empty((num_dst, dout), dtype=torch.int32, device=gdev) if arg else None
+    arg_e = torch.empty((num_dst, dout), dtype=torch.int32, device=gdev) if arg else None
+    if num_dst and dout:
+        lt = L if L is not None else R
+        rt = R if R is not None else L
+        dl, dr = width(lt.shape), width(rt.shape)
+        if code in (OP_COPY_LHS, OP_COPY_RHS):
+            nd, ls, rs = 0, None, None
+        else:
+            nd, ls, rs = shape_args(L.shape, R.shape)
+        lhs = _lib.on_device(L, dtype) if L is not None else None
+        rhs = _lib.on_device(R, dtype) if R is not None else None
+        csr = g._device_csr("in")
+        sched = csr.chunks
+        ws = None
+        nbytes = _lib.lib().mdgl_gspmm_workspace_bytes(sched.num_chunks, dout,
+                                                         REDUCERS[reduce_op],
+                                                         _lib.dtype_code(dtype))
+        if nbytes:
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=gdev)
+        rc = _lib.lib().mdgl_gspmm(
+            csr.indptr.data_ptr(), csr.indices.data_ptr(), csr.eid.data_ptr(), _lib.ptr(lhs),
+            _lib.ptr(rhs), out.data_ptr(), num_dst, code, dl, dr, dout, REDUCERS[reduce_op], None,
+            nd, None if ls is None else ls.ctypes.data, None if rs is None else rs.ctypes.data,
+            _lib.ptr(arg_u), _lib.ptr(arg_e), _lib.ptr(sched.chunk_row),
+            _lib.ptr(sched.chunk_start), sched.num_chunks, sched.chunk_len,
+            _lib.ptr(sched.heavy_rows), _lib.ptr(sched.heavy_ptr), sched.num_heavy, _lib.ptr(ws),
+            nbytes, _lib.REPLACE_INF if replace_inf else 0, _lib.dtype_code(dtype),
+            _lib.stream())
+        _lib.check(rc, "gspmm")
+    out = out.reshape(shape)
+    if arg:
+        arg_u = arg_u.reshape(shape).to(arg_dtype)
+        arg_e = arg_e.reshape(shape).to(arg_dtype)
+    return out, arg_u, arg_e, as_torch, dev
+
+
+def gspmm(g, op, reduce_op, lhs_data, rhs_data):
+    r"""Generalized Sparse Matrix Multiplication interface.
+    It fuses two steps into one kernel.
+
+    1. Computes messages by :attr:`op` source node and edge features.
+    2. Aggregate the messages by :attr:`reduce_op` as the features on destination nodes.
+
+    .. math::
+        x_v = \psi_{(u, v, e) \in \mathcal{G}}(\rho(x_u, x_e))
+
+    Parameters
+    ----------
+    g : DGLGraph
+    op : str
+        ``add``, ``sub``, ``mul``, ``div``, ``copy_lhs`` or ``copy_rhs``.
+    reduce_op : str
+        ``sum``, ``max``, ``min`` or ``mean``.
+    lhs_data, rhs_data : numpy array, torch tensor or None
+        Source-node and edge operands (None when the op does not read it).
+
+    Returns
+    -------
+    Node features of shape ``(N,) + broadcast feature shape``. A node with no
+    in-edges gets 0 (sum, mean), -inf (max) or +inf (min).
+    """
+    out, _, _, as_torch, dev = _run(g, op, reduce_op, lhs_data, rhs_data)
+    return _lib.give_back(out, as_torch, dev)
+
+
+def _gspmm(g, op, reduce_op, lhs_data, rhs_data):
+    """gspmm that also returns ``(arg_u, arg_e)`` for max/min (else ``(None, None)``).
+
+    arg_u / arg_e hold, per output element, the source node and the edge id
+    of the message selected by max/min: the first in CSR order (smallest edge
+    id) among equal values, 0 for a node with no in-edges.
+    """
+    out, au, ae, as_torch, dev = _run(g, op, reduce_op, lhs_data, rhs_data, want_arg=True)
+    res = _lib.give_back(out, as_torch, dev)
+    if au is None:
+        return res, (None, None)
+    return res, (_lib.give_back(au, as_torch, dev), _lib.give_back(ae, as_torch, dev))
+
+
+def _gen_spmm_func(binary_op, reduce_op):
+    name = "u_{}_e_{}".format(binary_op, reduce_op)
+
+    def func(g, x, y):
+        return gspmm(g, binary_op, reduce_op, x, y)
+
+    func.__name__ = name
+    func.__qualname__ = name
+    func.__doc__ = (
+        "Generalized SpMM function: messages {op} of source node features `x` and edge "
+        "features `y`, aggregated by {red} on destination nodes. Feature shapes broadcast "
+        "with NumPy's rules.{zero}\n").format(op=binary_op, red=reduce_op, zero=_zero_note(
+            reduce_op))
+    return func
+
+
+def _gen_copy_reduce_func(binary_op, reduce_op):
+    name = "{}_{}".format(binary_op, reduce_op)
+
+    def func(g, x):
+        if binary_op == "copy_u":
+            return gspmm(g, "copy_lhs", reduce_op, x, None)
+        return gspmm(g, "copy_rhs", reduce_op, None, x)
+
+    what = "source node" if binary_op == "copy_u" else "edge"
+    func.__name__ = name
+    func.__qualname__ = name
+    func.__doc__ = ("Generalized SpMM function: {w} features `x` as messages, aggregated by "
+                    "{red} on destination nodes.{zero}\n").format(w=what, red=reduce_op,
+                                                                  zero=_zero_note(reduce_op))
+    return func
+
+
+def _zero_note(reduce_op):
+    if reduce_op in ("max", "min"):
+        return (" A node with no in-edges gets {}inf here; update_all replaces it with "
+                "zero.".format("-" if reduce_op == "max" else "+"))
+    return " A node with no in-edges gets zero."
+
+
+def _register_spmm_func():
+    for binary_op in ("add", "sub", "mul", "div", "copy_u", "copy_e"):
+        for reduce_op in ("sum", "max", "min", "mean"):
+            if binary_op.startswith("copy"):
+                func = _gen_copy_reduce_func(binary_op, reduce_op)
+            else:
+                func = _gen_spmm_func(binary_op, reduce_op)
+            setattr(sys.modules[__name__], func.__name__, func)
+            __all__.append(func.__name__)
+
+
+_register_spmm_func()

@@ -1,0 +1,96 @@
+"""The C ABI of libmdgl.so without a GPU: it loads, exports every entry point
+include/mdgl.h declares, and rejects invalid arguments before launching."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mdgl.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mdgl_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from mojodgl import _lib
+
+    return _lib.lib()
+
+
+def test_header_declares_the_reference_entry_points():
+    names = declared()
+    # the 11 symbols of the reference's capi.mojo keep their names
+    for ref in ("mdgl_workers", "mdgl_cumsum", "mdgl_replace_inf_with_zero", "mdgl_clamp_i64",
+                "mdgl_gsddmm", "mdgl_gspmm", "mdgl_segment_reduce", "mdgl_segment_softmax",
+                "mdgl_segment_mm", "mdgl_edge_softmax_", "mdgl_gather_mm"):
+        assert ref in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in declared():
+        assert hasattr(lib, name), name
+
+
+def test_workers_is_parallel(lib):
+    assert lib.mdgl_workers() > 1
+
+
+def err(lib):
+    return lib.mdgl_last_error().decode()
+
+
+def test_invalid_arguments_are_rejected_without_launching(lib):
+    # bad op / reducer / dtype / target codes: negative status, named in the message
+    rc = lib.mdgl_gspmm(None, None, None, None, None, None, 10, 4, 1, 1, 1, 0, None, 0, None,
+                        None, None, None, None, None, 0, 0, None, None, 0, None, 0, 0, 0, None)
+    assert rc == -1 and "dot" in err(lib)
+    rc = lib.mdgl_gspmm(None, None, None, None, None, None, 10, 2, 1, 1, 1, 9, None, 0, None,
+                        None, None, None, None, None, 0, 0, None, None, 0, None, 0, 0, 0, None)
+    assert rc == -1 and "reduce_op" in err(lib)
+    rc = lib.mdgl_gsddmm(None, None, None, None, None, 5, 0, 3, 0, 1, 1, 1, 0, None, None, 0, None)
+    assert rc == -1 and "target" in err(lib)
+    rc = lib.mdgl_segment_reduce(None, None, None, 4, 2, 0, 8, 0, 7, None)
+    assert rc == -1 and "dtype" in err(lib)
+    # null buffers for a non-empty problem
+    rc = lib.mdgl_gspmm(None, None, None, None, None, None, 10, 2, 4, 4, 4, 0, None, 0, None,
+                        None, None, None, None, None, 0, 0, None, None, 0, None, 0, 0, 0, None)
+    assert rc == -1 and "null" in err(lib)
+    # widths that do not match the broadcast shapes
+    import numpy as np
+
+    ls = np.array([8, 32], dtype=np.int64)
+    rs = np.array([8, 2], dtype=np.int64)
+    rc = lib.mdgl_gspmm(None, None, None, None, None, None, 10, 2, 256, 16, 256, 0, None, 2,
+                        ls.ctypes.data, rs.ctypes.data, None, None, None, None, 0, 0, None, None,
+                        0, None, 0, 0, 0, None)
+    assert rc == -1 and "broadcastable" in err(lib)
+    # a chunk schedule without its workspace
+    rc = lib.mdgl_gspmm(1, 1, 1, 1, 1, 1, 10, 2, 4, 4, 4, 0, None, 0, None, None, None, None, 1,
+                        1, 3, 8, 1, 1, 1, None, 0, 0, 0, None)
+    assert rc == -2 and "workspace" in err(lib)
+    # too many b blocks for the GPU bucketing
+    rc = lib.mdgl_gather_mm(1, 1, 1, 1, 100, 4, 4, 100000, 1, 1 << 40, 0, None)
+    assert rc == -3
+
+
+def test_empty_problems_are_no_ops(lib):
+    assert lib.mdgl_gspmm(None, None, None, None, None, None, 0, 2, 4, 4, 4, 0, None, 0, None,
+                          None, None, None, None, None, 0, 0, None, None, 0, None, 0, 0, 0,
+                          None) == 0
+    assert lib.mdgl_segment_mm(None, None, None, None, 0, 4, 2, 3, None, 0, 0, None) == 0
+    assert lib.mdgl_cumsum(None, None, 0, None) == 0
+
+
+def test_workspace_sizes(lib):
+    assert lib.mdgl_gspmm_workspace_bytes(0, 64, 0, 0) == 0
+    assert lib.mdgl_gspmm_workspace_bytes(10, 64, 0, 0) >= 10 * 64 * 4
+    assert lib.mdgl_gspmm_workspace_bytes(10, 64, 1, 1) >= 10 * 64 * (8 + 4 + 4)
+    assert lib.mdgl_gather_mm_workspace_bytes(1000, 128, 128, 64, 0) >= 64 * 128 * 128 * 4 + 4000
+    assert lib.mdgl_segment_mm_workspace_bytes(1000, 5, 3, 7, 1) > 0

@@ -1,0 +1,437 @@
+"""HIP kernels (through the mojodgl API and libmdgl.so) against the CPU oracle.
+
+Tolerance rule for sums and softmaxes, stated once: with ref the float64
+oracle on the same inputs and T the oracle's result on |inputs| (the sum of
+absolute terms), |gpu - ref| <= tol * max(|ref|, T), tol = 1e-5 for float32
+and 1e-12 for float64. Where the GPU folds in the reference's order (gspmm /
+segment_reduce rows that are not split) it is also checked bit for bit
+against the oracle run in the same precision. max/min values, their arg
+indices and every integer output are bit-exact.
+"""
+
+import importlib
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+import mojodgl as dgl
+import mojodgl.function as fn
+import mojodgl.heterograph as hg
+import mojodgl.ops as ops
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = {np.float32: 1e-5, np.float64: 1e-12}
+
+
+def rand_graph(n, e, seed):
+    rng = np.random.default_rng(seed)
+    return rng.integers(0, n, e), rng.integers(0, n, e)
+
+
+def close(got, ref, bound, dtype, what=""):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    bound = np.maximum(np.abs(ref), np.abs(np.asarray(bound, dtype=np.float64)))
+    assert got.shape == ref.shape, (what, got.shape, ref.shape)
+    err = np.abs(got - ref)
+    ok = err <= TOL[dtype] * bound + 1e-300
+    if not ok.all():
+        i = np.unravel_index(np.argmax(err - TOL[dtype] * bound), err.shape)
+        raise AssertionError("{}: {} of {} outside tolerance; worst at {}: got {} ref {} bound "
+                             "{}".format(what, int((~ok).sum()), ok.size, i, got[i], ref[i],
+                                         bound[i]))
+
+
+ABS_OP = {"add": "add", "sub": "add", "mul": "mul", "div": "div"}
+
+
+@pytest.fixture(params=[None, 4], ids=["whole-rows", "split-rows"])
+def chunk_len(request, monkeypatch):
+    """Run each gspmm test with the hub split off and forced on (chunks of 4)."""
+    if request.param is not None:
+        monkeypatch.setattr(hg, "CHUNK_LEN", request.param)
+    return request.param
+
+
+# ------------------------------------------------------------------ gspmm
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div", "copy_u", "copy_e"])
+@pytest.mark.parametrize("reduce_op", ["sum", "max", "min", "mean"])
+def test_gspmm_all_families(dtype, op, reduce_op, chunk_len):
+    n, e = 300, 4000
+    u, v = rand_graph(n, e, 1)
+    u[:300] = 7  # one hub source, plus a hub destination below
+    v[:600] = 11
+    rng = np.random.default_rng(2)
+    d = 13
+    x = rng.normal(size=(n, d)).astype(dtype)
+    w = (rng.random((e, d)) + 0.25).astype(dtype)
+    if op == "copy_u":
+        oop, L, R = "copy_lhs", x, None
+    elif op == "copy_e":
+        oop, L, R = "copy_rhs", None, w
+    else:
+        oop, L, R = op, x, w
+    g = dgl.graph((u, v), num_nodes=n)
+    got, (au, ae) = ops.spmm._gspmm(g, oop, reduce_op, L, R)
+    assert got.dtype == dtype
+    ref64 = oracle.gspmm(u, v, n, oop, reduce_op, L, R, np.float64)
+    if reduce_op in ("max", "min"):
+        same, ru, re_ = oracle.gspmm(u, v, n, oop, reduce_op, L, R, dtype, with_arg=True)
+        np.testing.assert_array_equal(got, same)
+        np.testing.assert_array_equal(au, ru)
+        np.testing.assert_array_equal(ae, re_)
+        return
+    if chunk_len is None:
+        np.testing.assert_array_equal(got, oracle.gspmm(u, v, n, oop, reduce_op, L, R, dtype))
+    absop = "copy_lhs" if oop == "copy_lhs" else "copy_rhs" if oop == "copy_rhs" else ABS_OP[op]
+    bound = oracle.gspmm(u, v, n, absop, reduce_op, None if L is None else np.abs(L),
+                         None if R is None else np.abs(R), np.float64)
+    close(got, ref64, bound, dtype, "{} {}".format(op, reduce_op))
+
+
+@pytest.mark.parametrize("d", [1, 2, 3, 5, 7, 8, 16, 33, 64, 130, 602])
+def test_gspmm_feature_widths(d):
+    n, e = 200, 3000
+    u, v = rand_graph(n, e, 3)
+    rng = np.random.default_rng(4)
+    x = rng.normal(size=(n, d)).astype(np.float32)
+    w = rng.normal(size=(e, d)).astype(np.float32)
+    g = dgl.graph((u, v), num_nodes=n)
+    for name, oop, L, R in (("u_mul_e_sum", "mul", x, w), ("u_div_e_min", "div", x, w),
+                            ("copy_u_max", "copy_lhs", x, None), ("copy_e_mean", "copy_rhs",
+                                                                  None, w)):
+        got = getattr(ops, name)(g, *[a for a in (L, R) if a is not None])
+        red = name.rsplit("_", 1)[1]
+        np.testing.assert_array_equal(got, oracle.gspmm(u, v, n, oop, red, L, R, np.float32),
+                                      err_msg="{} d={}".format(name, d))
+
+
+@pytest.mark.parametrize("lshape,rshape", [((8, 32), (8, 1)), ((602,), (1,)), ((4, 3), (4, 1)),
+                                           ((1,), (6,)), ((2, 3, 4), (2, 1, 4)),
+                                           ((3, 1), (1, 5))])
+def test_gspmm_broadcast(lshape, rshape, chunk_len):
+    n, e = 150, 2500
+    u, v = rand_graph(n, e, 5)
+    rng = np.random.default_rng(6)
+    x = rng.normal(size=(n,) + lshape).astype(np.float32)
+    w = rng.normal(size=(e,) + rshape).astype(np.float32)
+    g = dgl.graph((u, v), num_nodes=n)
+    got = ops.u_mul_e_sum(g, x, w)
+    ref = oracle.gspmm(u, v, n, "mul", "sum", x, w, np.float64)
+    assert got.shape == ref.shape
+    bound = oracle.gspmm(u, v, n, "mul", "sum", np.abs(x), np.abs(w), np.float64)
+    close(got, ref, bound, np.float32, "bcast {} {}".format(lshape, rshape))
+    if chunk_len is None:
+        np.testing.assert_array_equal(got, oracle.gspmm(u, v, n, "mul", "sum", x, w, np.float32))
+    gmax, (au, ae) = ops.spmm._gspmm(g, "mul", "max", x, w)
+    rmax, ru, re_ = oracle.gspmm(u, v, n, "mul", "max", x, w, np.float32, with_arg=True)
+    np.testing.assert_array_equal(gmax, rmax)
+    np.testing.assert_array_equal(au, ru)
+    np.testing.assert_array_equal(ae, re_)
+
+
+def test_gspmm_power_law_hubs_against_oracle():
+    """Degrees spanning 0 .. 5000 with the default split threshold."""
+    rng = np.random.default_rng(7)
+    n = 3000
+    z = np.minimum(rng.zipf(2.1, n), 5000)
+    deg = rng.multinomial(60000, z / z.sum())
+    v = rng.permutation(np.repeat(np.arange(n), deg))
+    u = rng.integers(0, n, v.size)
+    x = rng.normal(size=(n, 8, 32)).astype(np.float32)
+    a = rng.normal(size=(v.size, 8, 1)).astype(np.float32)
+    g = dgl.graph((u, v), num_nodes=n)
+    got = ops.u_mul_e_sum(g, x, a)
+    ref = oracle.gspmm(u, v, n, "mul", "sum", x, a, np.float64)
+    bound = oracle.gspmm(u, v, n, "mul", "sum", np.abs(x), np.abs(a), np.float64)
+    close(got, ref, bound, np.float32, "power law")
+    gm, (au, ae) = ops.spmm._gspmm(g, "copy_lhs", "max", x, None)
+    rm, ru, re_ = oracle.gspmm(u, v, n, "copy_lhs", "max", x, None, np.float32, with_arg=True)
+    np.testing.assert_array_equal(gm, rm)
+    np.testing.assert_array_equal(au, ru)
+    np.testing.assert_array_equal(ae, re_)
+
+
+def test_gspmm_zero_degree_and_empty_graph():
+    u, v = np.array([0, 1]), np.array([1, 2])
+    g = dgl.graph((u, v), num_nodes=5)
+    x = np.random.default_rng(8).normal(size=(5, 4))
+    e = np.ones((2, 4))
+    assert np.all(ops.copy_u_max(g, x)[[0, 3, 4]] == -np.inf)
+    assert np.all(ops.copy_e_min(g, e)[[0, 3, 4]] == np.inf)
+    assert np.all(ops.u_mul_e_mean(g, x, e)[[0, 3, 4]] == 0)
+    empty = dgl.graph((np.array([], dtype=np.int64), np.array([], dtype=np.int64)))
+    assert ops.u_mul_e_sum(empty, np.zeros((0, 4)), np.zeros((0, 4))).shape == (0, 4)
+
+
+# ------------------------------------------------------------------ gsddmm
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("lt,rt", list(itertools.permutations("uve", 2)))
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div", "dot"])
+def test_gsddmm_all_families(dtype, lt, rt, op):
+    n, e = 200, 3000
+    u, v = rand_graph(n, e, 9)
+    rng = np.random.default_rng(10)
+    d = 12
+    data = {"u": rng.normal(size=(n, d)), "v": rng.normal(size=(n, d)) + 3,
+            "e": rng.normal(size=(e, d)) + 3}
+    data = {k: a.astype(dtype) for k, a in data.items()}
+    g = dgl.graph((u, v), num_nodes=n)
+    got = getattr(ops, "{}_{}_{}".format(lt, op, rt))(g, data[lt], data[rt])
+    if op != "dot":
+        np.testing.assert_array_equal(got, oracle.gsddmm(u, v, n, op, data[lt], data[rt], lt, rt,
+                                                         dtype))
+    else:
+        ref = oracle.gsddmm(u, v, n, op, data[lt], data[rt], lt, rt, np.float64)
+        bound = oracle.gsddmm(u, v, n, op, np.abs(data[lt]), np.abs(data[rt]), lt, rt,
+                              np.float64)
+        close(got, ref, bound, dtype, "dot")
+
+
+@pytest.mark.parametrize("d", [1, 3, 4, 8, 33, 128])
+def test_gsddmm_widths_and_dot(d):
+    n, e = 300, 5000
+    u, v = rand_graph(n, e, 11)
+    rng = np.random.default_rng(12)
+    x = rng.normal(size=(n, d)).astype(np.float32)
+    y = rng.normal(size=(e, d)).astype(np.float32)
+    g = dgl.graph((u, v), num_nodes=n)
+    np.testing.assert_array_equal(ops.u_mul_v(g, x, x), oracle.gsddmm(u, v, n, "mul", x, x, "u",
+                                                                       "v", np.float32))
+    np.testing.assert_array_equal(ops.u_add_e(g, x, y), oracle.gsddmm(u, v, n, "add", x, y, "u",
+                                                                       "e", np.float32))
+    got = ops.u_dot_v(g, x, x)
+    ref = oracle.gsddmm(u, v, n, "dot", x, x, "u", "v", np.float64)
+    bound = oracle.gsddmm(u, v, n, "dot", np.abs(x), np.abs(x), "u", "v", np.float64)
+    close(got, ref, bound, np.float32, "dot d={}".format(d))
+
+
+def test_gsddmm_broadcast_copy_and_multihead_dot():
+    n, e = 100, 1500
+    u, v = rand_graph(n, e, 13)
+    rng = np.random.default_rng(14)
+    el = rng.normal(size=(n, 8, 1)).astype(np.float32)
+    er = rng.normal(size=(n, 8, 1)).astype(np.float32)
+    h = rng.normal(size=(n, 8, 32)).astype(np.float32)
+    g = dgl.graph((u, v), num_nodes=n)
+    np.testing.assert_array_equal(ops.u_add_v(g, el, er), el[u] + er[v])
+    np.testing.assert_array_equal(ops.u_mul_v(g, h, er), h[u] * er[v])
+    np.testing.assert_array_equal(ops.copy_u(g, h), h[u])
+    np.testing.assert_array_equal(ops.copy_v(g, h), h[v])
+    got = ops.u_dot_v(g, h, h)
+    assert got.shape == (e, 8, 1)
+    ref = oracle.gsddmm(u, v, n, "dot", h, h, "u", "v", np.float64)
+    bound = oracle.gsddmm(u, v, n, "dot", np.abs(h), np.abs(h), "u", "v", np.float64)
+    close(got, ref, bound, np.float32, "multi-head dot")
+
+
+# ------------------------------------------------------------------ edge_softmax
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("norm_by", ["dst", "src"])
+@pytest.mark.parametrize("shape", [(), (1,), (3, 1), (8, 1), (2, 4, 1), (40, 1)])
+def test_edge_softmax(dtype, norm_by, shape, monkeypatch):
+    monkeypatch.setattr(hg, "SOFTMAX_HEAVY_DEG", 64)
+    n, e = 400, 6000
+    u, v = rand_graph(n, e, 15)
+    v[:500] = 3  # a hub above the workgroup threshold
+    u[:300] = 5
+    rng = np.random.default_rng(16)
+    logits = (rng.normal(size=(e,) + shape) * 3).astype(dtype)
+    g = dgl.graph((u, v), num_nodes=n)
+    got = ops.edge_softmax(g, logits, norm_by=norm_by)
+    assert got.shape == logits.shape and got.dtype == dtype
+    ref = oracle.edge_softmax(u, v, n, logits, norm_by=norm_by, dtype=np.float64)
+    close(got, ref, ref, dtype, "edge_softmax")
+    key = v if norm_by == "dst" else u
+    flat = np.asarray(got, dtype=np.float64).reshape(e, -1)
+    sums = np.zeros((n, flat.shape[1]))
+    np.add.at(sums, key, flat)
+    np.testing.assert_allclose(sums[np.bincount(key, minlength=n) > 0], 1.0,
+                               atol=1e-4 if dtype == np.float32 else 1e-12)
+
+
+@pytest.mark.parametrize("norm_by", ["dst", "src"])
+def test_edge_softmax_positional_eids(norm_by):
+    rng = np.random.default_rng(17)
+    for case in range(20):
+        n = int(rng.integers(2, 30))
+        e = int(rng.integers(1, 200))
+        u, v = rng.integers(0, n, e), rng.integers(0, n, e)
+        logits = rng.normal(size=(e, 2, 1))
+        eids = rng.choice(e, size=int(rng.integers(1, e + 1)), replace=bool(case % 2))
+        g = dgl.graph((u, v), num_nodes=n)
+        got = ops.edge_softmax(g, logits, eids=eids, norm_by=norm_by)
+        ref = oracle.edge_softmax(u, v, n, logits, eids=eids, norm_by=norm_by)
+        close(got, ref, ref, np.float64, "eids case {}".format(case))
+
+
+# ------------------------------------------------------------------ segments
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("reducer", ["sum", "max", "min", "mean"])
+@pytest.mark.parametrize("d", [1, 3, 16, 33])
+def test_segment_reduce(dtype, reducer, d):
+    rng = np.random.default_rng(18)
+    seglen = rng.poisson(20, 3000)
+    seglen[::13] = 0
+    value = rng.normal(size=(int(seglen.sum()), d)).astype(dtype)
+    got = ops.segment_reduce(seglen, value, reducer)
+    np.testing.assert_array_equal(got, oracle.segment_reduce(seglen, value, reducer, dtype))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("d", [1, 4, 16, 33])
+def test_segment_softmax(dtype, d):
+    rng = np.random.default_rng(19)
+    seglen = rng.poisson(20, 2000)
+    seglen[::11] = 0
+    seglen[5] = 3000  # one segment above the workgroup threshold is not special here
+    value = (rng.normal(size=(int(seglen.sum()), d)) * 2).astype(dtype)
+    got = ops.segment_softmax(seglen, value)
+    ref = oracle.segment_softmax(seglen, value, np.float64)
+    close(got, ref, ref, dtype, "segment_softmax")
+
+
+# ------------------------------------------------------------------ dense
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("d1,d2,r", [(128, 128, 64), (5, 3, 7), (16, 16, 4), (33, 130, 3),
+                                     (1, 1, 2)])
+def test_gather_mm(dtype, d1, d2, r):
+    rng = np.random.default_rng(20)
+    n = 1500
+    a = rng.normal(size=(n, d1)).astype(dtype)
+    b = (rng.normal(size=(r, d1, d2)) / np.sqrt(d1)).astype(dtype)
+    idx = rng.integers(0, r, n)
+    got = ops.gather_mm(a, b, idx_b=idx)
+    ref = oracle.gather_mm(a, b, idx, np.float64)
+    bound = oracle.gather_mm(np.abs(a), np.abs(b), idx, np.float64)
+    close(got, ref, bound, dtype, "gather_mm")
+
+
+def test_gather_mm_routes_agree(monkeypatch):
+    rng = np.random.default_rng(21)
+    a = rng.normal(size=(900, 9)).astype(np.float32)
+    b = rng.normal(size=(6, 9, 7)).astype(np.float32)
+    idx = rng.integers(0, 6, 900)
+    fused = ops.gather_mm(a, b, idx_b=idx)
+    monkeypatch.setattr(importlib.import_module("mojodgl.ops.gather_mm"), "_SEGMENT_BLOCK", 0)
+    np.testing.assert_array_equal(ops.gather_mm(a, b, idx_b=idx), fused)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_segment_mm(dtype):
+    rng = np.random.default_rng(22)
+    seglen = rng.multinomial(5000, rng.dirichlet(0.5 * np.ones(16)))
+    n = 5100  # 100 trailing rows outside every segment stay zero
+    a = rng.normal(size=(n, 64)).astype(dtype)
+    b = (rng.normal(size=(16, 64, 48)) / 8).astype(dtype)
+    got = ops.segment_mm(a, b, seglen)
+    ref = oracle.segment_mm(a, b, seglen, np.float64)
+    bound = oracle.segment_mm(np.abs(a), np.abs(b), seglen, np.float64)
+    close(got, ref, bound, dtype, "segment_mm")
+    assert np.all(np.asarray(got)[5000:] == 0)
+
+
+# ------------------------------------------------------------------ dispatcher
+@pytest.mark.parametrize("lhs,rhs", list(itertools.permutations("uve", 2)))
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div", "dot"])
+def test_update_all_binary_builtins(lhs, rhs, op):
+    n, e = 48, 400
+    u, v = rand_graph(n, e, 23)
+    rng = np.random.default_rng(24)
+    x = rng.normal(size=(n, 6))
+    w = rng.normal(size=(e, 6)) + 3
+    g = dgl.graph((u, v), num_nodes=n)
+    g.ndata["x"] = x
+    g.edata["e"] = w
+    field = {"u": "x", "v": "x", "e": "e"}
+    g.update_all(getattr(fn, "{}_{}_{}".format(lhs, op, rhs))(field[lhs], field[rhs], "m"),
+                 fn.sum("m", "h"))
+    data = {"u": x, "v": x, "e": w}
+    msg = oracle.gsddmm(u, v, n, op, data[lhs], data[rhs], lhs, rhs)
+    ref = oracle.gspmm(u, v, n, "copy_rhs", "sum", None, msg)
+    close(g.ndata["h"], ref, oracle.gspmm(u, v, n, "copy_rhs", "sum", None, np.abs(msg)),
+          np.float64, "update_all " + op)
+
+
+def test_update_all_fused_max_min_zero_fill_and_udfs():
+    u, v = np.array([0, 0, 1]), np.array([1, 1, 2])
+    g = dgl.graph((u, v))
+    g.ndata["h"] = np.array([[1.0], [2.0], [3.0]])
+    want = [[[0.0], [1.0], [2.0]], [[0.0], [0.0], [1.0]], [[0.0], [0.0], [0.0]],
+            [[0.0], [0.0], [0.0]]]
+    for red, w in zip(("max", "min", "mean", "sum"), want):
+        g.update_all(fn.copy_u("h", "m"), getattr(fn, red)("m", "h"))
+        np.testing.assert_array_equal(g.ndata["h"], np.array(w))
+    n, e = 48, 400
+    u, v = rand_graph(n, e, 25)
+    rng = np.random.default_rng(26)
+    x, w = rng.normal(size=(n, 6)), rng.normal(size=(e, 6))
+    g = dgl.graph((u, v), num_nodes=n)
+    g.ndata["x"] = x
+    g.edata["e"] = w
+    g.update_all(lambda edges: {"m": edges.src["x"] * edges.data["e"] + 1.0}, fn.mean("m", "h"))
+    ref = oracle.gspmm(u, v, n, "copy_rhs", "mean", None, x[u] * w + 1.0)
+    close(g.ndata["h"], ref, oracle.gspmm(u, v, n, "copy_rhs", "mean", None,
+                                          np.abs(x[u] * w) + 1.0), np.float64, "udf")
+    g.update_all(fn.u_mul_e("x", "e", "m"), lambda nodes: {"s": nodes.mailbox["m"] * 2.0})
+    ref = oracle.gspmm(u, v, n, "mul", "sum", x, w) * 2.0
+    close(g.ndata["s"], ref, oracle.gspmm(u, v, n, "mul", "sum", np.abs(x), np.abs(w)) * 2.0,
+          np.float64, "pre-summed mailbox")
+
+
+def test_pull_and_readme_vector():
+    g = dgl.graph((np.array([0, 1, 2, 0, 1]), np.array([1, 2, 0, 2, 2])))
+    g.ndata["h"] = np.array([[1.0, 0.0], [0.0, 1.0], [2.0, 2.0]])
+    g.edata["e"] = np.array([[0.5, 0.5], [1.0, 0.0], [0.0, 1.0], [2.0, 1.0], [1.0, 1.0]])
+    g.update_all(fn.u_mul_e("h", "e", "m"), fn.mean("m", "z"))
+    np.testing.assert_allclose(g.ndata["z"], [[0.0, 2.0], [0.5, 0.0], [2 / 3, 1 / 3]], rtol=1e-15)
+    n, e = 48, 400
+    u, v = rand_graph(n, e, 27)
+    rng = np.random.default_rng(28)
+    x, w = rng.normal(size=(n, 6)), rng.normal(size=(e, 6))
+    g = dgl.graph((u, v), num_nodes=n)
+    g.ndata["x"] = x
+    g.edata["e"] = w
+    targets = np.array([1, 5, 9, 40])
+    g.pull(targets, fn.u_mul_e("x", "e", "m"), fn.sum("m", "h"))
+    full = oracle.gspmm(u, v, n, "mul", "sum", x, w)
+    want = np.zeros_like(full)
+    want[targets] = full[targets]
+    close(g.ndata["h"], want, oracle.gspmm(u, v, n, "mul", "sum", np.abs(x), np.abs(w)),
+          np.float64, "pull")
+
+
+def test_torch_tensors_stay_on_the_gpu():
+    n, e = 500, 8000
+    u, v = rand_graph(n, e, 29)
+    g = dgl.graph((torch.as_tensor(u), torch.as_tensor(v)), num_nodes=n)
+    x = torch.randn(n, 8, 32, device="cuda")
+    a = torch.rand(e, 8, 1, device="cuda")
+    out = ops.u_mul_e_sum(g, x, a)
+    assert isinstance(out, torch.Tensor) and out.is_cuda and out.dtype == torch.float32
+    ref = oracle.gspmm(u, v, n, "mul", "sum", x.cpu().numpy(), a.cpu().numpy(), np.float64)
+    bound = oracle.gspmm(u, v, n, "mul", "sum", np.abs(x.cpu().numpy()), a.cpu().numpy(),
+                         np.float64)
+    close(out.cpu().numpy(), ref, bound, np.float32, "torch")
+
+
+def test_repeat_runs_are_bit_identical():
+    """No atomics in the reductions: two runs give the same bits."""
+    rng = np.random.default_rng(30)
+    n = 2000
+    v = rng.permutation(np.repeat(np.arange(n), np.minimum(rng.zipf(2.0, n), 3000)))
+    u = rng.integers(0, n, v.size)
+    g = dgl.graph((u, v), num_nodes=n)
+    x = torch.randn(n, 64, device="cuda")
+    w = torch.randn(v.size, 64, device="cuda")
+    a = ops.u_mul_e_sum(g, x, w)
+    b = ops.u_mul_e_sum(g, x, w)
+    assert torch.equal(a, b)
+    s1 = ops.edge_softmax(g, w[:, :1])
+    s2 = ops.edge_softmax(g, w[:, :1])
+    assert torch.equal(s1, s2)

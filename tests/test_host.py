@@ -1,0 +1,170 @@
+"""Host-side logic of mojodgl that needs no GPU: the API surface, graph
+construction and queries, argument validation (which runs before anything is
+copied to the GPU), the gspmm heavy-row schedule, and the refusal to run
+without a GPU."""
+
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+import mojodgl as dgl
+import mojodgl.function as fn
+import mojodgl.heterograph as hg
+import mojodgl.ops as ops
+import mojodgl.ops.sddmm as sddmm_mod
+
+U = np.array([2, 0, 1, 0])
+V = np.array([1, 2, 0, 1])
+
+
+def test_api_surface_matches_the_reference():
+    # 64 names in ops: 34 from sddmm, 25 from spmm, 5 others (reference README.md:51-52)
+    assert len(ops.__all__) == 64
+    expected = {"{}_{}_{}".format(a, op, b) for a, b in itertools.permutations("uve", 2)
+                for op in ("add", "sub", "mul", "div", "dot")}
+    assert expected <= set(dir(fn)) and expected <= set(dir(ops))
+    for b in ("add", "sub", "mul", "div"):
+        for r in ("sum", "max", "min", "mean"):
+            assert callable(getattr(ops, "u_{}_e_{}".format(b, r)))
+    for r in ("sum", "max", "min", "mean"):
+        assert callable(getattr(ops, "copy_u_" + r)) and callable(getattr(ops, "copy_e_" + r))
+    for name in ("gspmm", "gsddmm", "segment_reduce", "segment_softmax", "segment_mm",
+                 "gather_mm", "edge_softmax", "copy_u", "copy_v", "copy_e"):
+        assert callable(getattr(ops, name))
+    import mojodgl.nn.functional as nnf
+
+    assert nnf.edge_softmax is ops.edge_softmax
+    for name in expected:
+        assert getattr(ops, name).__doc__
+
+
+def test_builtin_descriptors():
+    for name in ("u_add_v", "u_mul_e", "v_div_u", "e_dot_v", "u_sub_e"):
+        msg = getattr(fn, name)("a", "b", "m")
+        assert msg.name == name
+        assert (msg.lhs_field, msg.rhs_field, msg.out_field) == ("a", "b", "m")
+    assert fn.copy_u("a", "m").name == "copy_u" and fn.copy_e("a", "m").name == "copy_e"
+    for name in ("sum", "max", "min", "mean"):
+        red = getattr(fn, name)("m", "h")
+        assert red.name == name and red.msg_field == "m" and red.out_field == "h"
+
+
+def test_graph_queries():
+    g = dgl.graph((U, V))
+    assert g.num_nodes() == 3 and g.num_edges() == 4
+    np.testing.assert_array_equal(g.edges().u, U)
+    np.testing.assert_array_equal(g.edges().eid, np.arange(4))
+    np.testing.assert_array_equal(g.in_degrees(), [1, 2, 1])
+    np.testing.assert_array_equal(g.out_degrees(), [2, 1, 1])
+    np.testing.assert_array_equal(g.in_degrees([0, 2]), [1, 1])
+    e = g.in_edges(1)
+    assert e.u.tolist() == [2, 0] and e.eid.tolist() == [0, 3]
+    assert dgl.graph((U, V), num_nodes=10).number_of_nodes() == 10
+    assert list(g.canonical_etypes) == [("_N", "_E", "_N")]
+    empty = dgl.graph((np.array([], dtype=np.int64), np.array([], dtype=np.int64)))
+    assert empty.num_nodes() == 0 and empty.num_edges() == 0
+    import scipy.sparse as sp
+
+    m = sp.csr_matrix(np.array([[0, 1, 0], [0, 0, 1], [1, 0, 0]], dtype=np.float64))
+    gs = dgl.graph(m)
+    assert sorted(zip(gs.edges().u.tolist(), gs.edges().v.tolist())) == [(0, 1), (1, 2), (2, 0)]
+    gt = dgl.graph((torch.tensor([0, 1]), torch.tensor([1, 2])))
+    assert gt.num_nodes() == 3
+
+
+def test_graph_validation():
+    with pytest.raises(dgl.DGLError):
+        dgl.graph(([0, 1], [1, 5]), num_nodes=3)
+    with pytest.raises(dgl.DGLError):
+        dgl.graph(([-1, 1], [1, 2]))
+    with pytest.raises(dgl.DGLError):
+        dgl.graph((np.array([0.5]), np.array([1.0])))
+    g = dgl.graph((U, V))
+    with pytest.raises(ValueError):
+        g.ndata["h"] = np.ones((2, 3))
+    with pytest.raises(KeyError):
+        g.ndata["missing"]
+
+
+def test_feature_store_keeps_dtypes():
+    g = dgl.graph((U, V))
+    g.ndata["a"] = np.ones((3, 2), dtype=np.float32)
+    g.ndata["b"] = np.ones((3, 2), dtype=np.int32)
+    g.ndata["c"] = torch.ones(3, 2, dtype=torch.float32)
+    assert g.ndata["a"].dtype == np.float32
+    assert g.ndata["b"].dtype == np.float64
+    assert isinstance(g.ndata["c"], torch.Tensor)
+
+
+def test_reshape_lhs_rhs():
+    a, b = sddmm_mod.reshape_lhs_rhs(np.zeros((4, 3, 1)), np.zeros((5, 3, 3, 4)))
+    assert a.shape == (4, 1, 3, 1) and b.shape == (5, 3, 3, 4)
+    assert sddmm_mod.out_feat_shape((4, 1, 3, 1), (5, 3, 3, 4)) == (3, 3, 4)
+    assert sddmm_mod.out_feat_shape((4, 8, 32), (5, 8, 32), dot=True) == (8, 1)
+
+
+def test_validation_errors_come_before_the_gpu():
+    g = dgl.graph((U, V))
+    x = np.ones((3, 4))
+    e = np.ones((4, 4))
+    for call in (lambda: ops.u_add_e_sum(g, np.ones((2, 4)), e),
+                 lambda: ops.copy_e_sum(g, e[:-1]),
+                 lambda: ops.u_add_v(g, np.ones((2, 4)), x),
+                 lambda: ops.gspmm(g, "dot", "sum", x, e),
+                 lambda: ops.gspmm(g, "mul", "median", x, e),
+                 lambda: ops.gsddmm(g, "add", x, x, lhs_target="w"),
+                 lambda: ops.u_dot_v(g, np.ones((3, 4)), np.ones((3, 5))),
+                 lambda: ops.u_add_v(g, np.ones((3, 4)), np.ones((3, 5))),
+                 lambda: ops.u_mul_e_sum(g, np.ones((3, 2), dtype=np.complex128),
+                                         np.ones((4, 2))),
+                 lambda: ops.segment_reduce(np.array([3, 3]), np.ones((4, 2))),
+                 lambda: ops.segment_reduce(np.array([6, -2]), np.ones((4, 2))),
+                 lambda: ops.segment_reduce(np.array([4]), np.ones((4, 1)), "median"),
+                 lambda: ops.segment_softmax(np.array([3]), np.ones((4, 1))),
+                 lambda: ops.segment_mm(np.ones((6, 3)), np.ones((4, 3, 2)), np.array([2, 2, 2])),
+                 lambda: ops.segment_mm(np.ones((6, 3)), np.ones((4, 3, 2)),
+                                        np.array([-3, 3, 3, 3])),
+                 lambda: ops.segment_mm(np.ones((6, 3)), np.ones((4, 3, 2)),
+                                        np.array([10, 0, 0, 0])),
+                 lambda: ops.gather_mm(np.ones((4, 3)), np.ones((2, 3, 5)),
+                                       idx_b=np.array([0, 1, 2, 5])),
+                 lambda: ops.gather_mm(np.ones((4, 3)), np.ones((2, 3, 5)),
+                                       idx_b=np.array([0, 1, 2, -1])),
+                 lambda: ops.gather_mm(np.ones((5, 9)), np.ones((2, 2, 3)),
+                                       idx_b=np.array([0, 1, 0, 1, 0])),
+                 lambda: ops.gather_mm(np.ones((4, 3)), np.ones((2, 3, 5)),
+                                       idx_b=np.array([0, 1, 2])),
+                 lambda: ops.gather_mm(np.full((4, 2), 2 ** 53 + 1, dtype=np.uint64),
+                                       np.ones((2, 2, 3)), idx_b=np.zeros(4, dtype=np.int64)),
+                 lambda: ops.edge_softmax(g, np.ones((4, 3))),
+                 lambda: ops.edge_softmax(g, np.ones(4), norm_by="edge"),
+                 lambda: ops.edge_softmax(g, np.ones(4), eids=np.array([0, 4])),
+                 lambda: ops.edge_softmax(g, np.ones(3)),
+                 lambda: ops.edge_softmax(g, np.ones(4, dtype=np.complex128))):
+        with pytest.raises(dgl.DGLError):
+            call()
+
+
+def test_no_gpu_means_a_loud_error():
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    g = dgl.graph((U, V))
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.u_mul_e_sum(g, np.ones((3, 2)), np.ones((4, 2)))
+
+
+def test_chunk_plan():
+    rng = np.random.default_rng(0)
+    deg = rng.integers(0, 40, 200)
+    deg[7] = 1000
+    indptr = np.concatenate([[0], np.cumsum(deg)])
+    heavy, ptr, row, start = hg.chunk_plan(indptr, 16)
+    np.testing.assert_array_equal(heavy, np.nonzero(deg > 16)[0])
+    # the chunks of each heavy row tile its slots exactly, in order
+    for h, r in enumerate(heavy):
+        starts = start[ptr[h]:ptr[h + 1]]
+        assert np.all(row[ptr[h]:ptr[h + 1]] == r)
+        np.testing.assert_array_equal(starts, np.arange(indptr[r], indptr[r + 1], 16))
+    assert row.size == sum((d + 15) // 16 for d in deg if d > 16)
