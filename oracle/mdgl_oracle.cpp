@@ -85,6 +85,17 @@ inline T message(int op, T x, T y) {  // ported.mojo:92-105
   }
 }
 
+// The message of one (lhs element, rhs element) pair, reading only the
+// operand(s) the op uses. A copy op's missing operand aliases the present one
+// (spmm.py:64-69, sddmm.py:354-361), whose row count need not fit the other
+// role's index (node rows indexed by edge id), so it must not be read.
+template <class T>
+inline T message_at(int op, const T* lhs, int64_t li, const T* rhs, int64_t ri) {
+  if (op == OP_COPY_LHS) return lhs[li];
+  if (op == OP_COPY_RHS) return rhs[ri];
+  return message<T>(op, lhs[li], rhs[ri]);
+}
+
 // ---------------------------------------------------------------- array ops
 void cumsum(const int64_t* src, int64_t* dst, int64_t n) {  // ported.mojo:145-151
   int64_t acc = 0;
@@ -143,7 +154,7 @@ void gsddmm(const int64_t* uids, const int64_t* vids, const T* lhs, const T* rhs
           for (; k < red; ++k) acc = acc + lhs[lo + k] * rhs[ro + k];
           dst[e * dout + o] = acc;
         } else {
-          dst[e * dout + o] = message<T>(op, lhs[lo], rhs[ro]);
+          dst[e * dout + o] = message_at<T>(op, lhs, lo, rhs, ro);
         }
       }
     }
@@ -175,7 +186,7 @@ void gspmm(const int64_t* indptr, const int64_t* indices, const int64_t* eid, co
         T acc = seed<T>(red);
         int64_t au = 0, ae = 0;
         for (int64_t i = start; i < stop; ++i) {
-          T m = message<T>(op, lhs[indices[i] * dl + lo], rhs[eid[i] * dr + ro]);
+          T m = message_at<T>(op, lhs, indices[i] * dl + lo, rhs, eid[i] * dr + ro);
           if (red == RED_MAX) {
             if (m > acc) { acc = m; au = indices[i]; ae = eid[i]; }
           } else if (red == RED_MIN) {

@@ -51,9 +51,8 @@ ABS_OP = {"add": "add", "sub": "add", "mul": "mul", "div": "div"}
 
 @pytest.fixture(params=[None, 4], ids=["whole-rows", "split-rows"])
 def chunk_len(request, monkeypatch):
-    """Run each gspmm test with the hub split off and forced on (chunks of 4)."""
-    if request.param is not None:
-        monkeypatch.setattr(hg, "CHUNK_LEN", request.param)
+    """Run each gspmm test with row splitting off and forced on (chunks of 4)."""
+    monkeypatch.setattr(hg, "CHUNK_LEN", request.param if request.param else 2 ** 30)
     return request.param
 
 

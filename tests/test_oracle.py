@@ -406,3 +406,40 @@ def test_reference_vectors(vec):
         assert sorted(oeid[outptr[0]:outptr[1]].tolist()) == vec["out_edges_0"]["eid"]
     else:
         raise AssertionError(op)
+
+
+# --------------------------------------------------------------- memory safety
+def _guarded(n_elems, dtype):
+    """A numpy array whose last element ends right before an unreadable page."""
+    import ctypes
+    import mmap
+
+    page = mmap.PAGESIZE
+    nbytes = n_elems * np.dtype(dtype).itemsize
+    body = -(-nbytes // page) * page
+    buf = mmap.mmap(-1, body + page)
+    base = ctypes.addressof(ctypes.c_char.from_buffer(buf))
+    libc = ctypes.CDLL(None)
+    assert libc.mprotect(ctypes.c_void_p(base + body), page, 0) == 0  # PROT_NONE
+    arr = np.frombuffer(buf, dtype=dtype, count=n_elems, offset=body - nbytes)
+    return arr, buf
+
+
+def test_copy_ops_read_only_their_operand():
+    """copy_lhs aliases rhs to the node data; reading it at edge ids would run
+    past the node rows. With the rows placed right before an unreadable page,
+    any such read faults."""
+    n, e, d = 20, 500, 3
+    u, v = rand_graph(n, e, 31)
+    x, keep = _guarded(n * d, np.float64)
+    x[:] = np.arange(n * d, dtype=np.float64)
+    x = x.reshape(n, d)
+    want = np.full((n, d), -np.inf)
+    np.maximum.at(want, v, x[u])
+    np.testing.assert_array_equal(oracle.gspmm(u, v, n, "copy_lhs", "max", x, None), want)
+    # edge data read through copy_rhs by an 'e' target while lhs targets 'u'
+    w, keep2 = _guarded(e * d, np.float64)
+    w[:] = 1.0
+    got = oracle.gsddmm(u, v, n, "copy_rhs", None, w.reshape(e, d), "u", "e")
+    np.testing.assert_array_equal(got, np.ones((e, d)))
+    del keep, keep2
