@@ -32,6 +32,11 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
 template <class T> struct Mfma;
+// Both instructions take A[i][k] from lane i + 16k and B[k][j] from lane
+// j + 16k. They differ in where output row i lands: the f32 form keeps it in
+// lane group i / 4 (register i % 4), the f64 form in lane group i % 4
+// (register i / 4). `row(g, r)` is the block row held by lane group g (lanes
+// 16g..16g+15) in accumulator register r; the column is the lane mod 16.
 template <> struct Mfma<float> {
   using acc_t = f32x4;
   static constexpr int BK = 32;
@@ -39,6 +44,7 @@ template <> struct Mfma<float> {
   __device__ static acc_t step(float a, float b, acc_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
   }
+  __device__ static int row(int g, int r) { return 4 * g + r; }
 };
 template <> struct Mfma<double> {
   using acc_t = f64x4;
@@ -47,6 +53,7 @@ template <> struct Mfma<double> {
   __device__ static acc_t step(double a, double b, acc_t c) {
     return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
   }
+  __device__ static int row(int g, int r) { return g + 4 * r; }
 };
 
 constexpr int GBM = 128, GBN = 128;
@@ -193,12 +200,11 @@ __global__ __launch_bounds__(BLOCK) void grouped_gemm_kernel(GemmArgs<T> p) {
     }
   }
 
-  // C layout of a 16x16 block: lane l holds column l % 16, rows 4 * (l / 16) + r
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int rl = wm * 64 + i * 16 + 4 * h + r;
+      const int rl = wm * 64 + i * 16 + M::row(h, r);
       const int rid = rowid_s[rl];
       if (rid < 0) continue;
 #pragma unroll
