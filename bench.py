@@ -37,6 +37,9 @@ for _p in (ROOT, os.path.join(ROOT, "mojo-dgl_amd")):
 import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the gspmm kernel on the default workload, from
+# rocprofv3 FETCH_SIZE / WRITE_SIZE scaled by a 1 GiB copy (profiles/gat_c2_kernels.md)
+GSPMM_TRAFFIC_BYTES = 72.28e9
 MFMA_F32_PEAK_TFLOPS = 157.3
 
 
@@ -427,7 +430,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="finish with a 1 GiB device-to-device copy (counter calibration)")
-    ap.add_argument("--traffic", type=float, default=None,
+    ap.add_argument("--traffic", type=float, default=GSPMM_TRAFFIC_BYTES,
                     help="HBM bytes per gspmm launch measured by rocprofv3 (reported as is)")
     args = ap.parse_args()
     if args.gpus != 1:

@@ -82,7 +82,10 @@ def edge_softmax(graph, logits, eids=ALL, norm_by="dst"):
 
     dtype = X.dtype
     gdev = _lib.device()
-    out = torch.zeros((out_len, d), dtype=_lib.torch_dtype(dtype), device=gdev)
+    # on the ALL path every edge is in exactly one CSR row, so every output
+    # row is written; a subset leaves the rows past len(eids) at zero
+    alloc = torch.empty if order is None else torch.zeros
+    out = alloc((out_len, d), dtype=_lib.torch_dtype(dtype), device=gdev)
     if out_len and d:
         lg = _lib.on_device(X, dtype).reshape(out_len, d)
         if order is None:
