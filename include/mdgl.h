@@ -113,23 +113,49 @@ int64_t mdgl_gspmm_workspace_bytes(int64_t num_chunks, int64_t dout, int reduce_
 int mdgl_segment_reduce(const int32_t* offsets, const void* value, void* dst, int64_t num_seg,
                         int64_t d, int reduce_op, int64_t n, int flags, int dtype, void* stream);
 
+/* Softmax planning. A softmax call serves rows by degree, with a lane layout
+ * that depends on d, the dtype and the 16-byte alignment of the two buffers:
+ * `slots` edge slots per wavefront. Rows of up to `chunk_len` (= 8 * slots)
+ * edges are served whole; longer rows must be passed as chunks of chunk_len
+ * edges. Call this with the buffers of the call to plan. No counterpart in the
+ * reference (its split is a fixed 32-way CPU split, ported.mojo:34-42). */
+int mdgl_softmax_geometry(int64_t d, int dtype, const void* logits, const void* out,
+                          int64_t* slots, int64_t* chunk_len);
+/* Workspace of a softmax call with `num_chunks` chunks (their partials). */
+int64_t mdgl_softmax_workspace_bytes(int64_t num_chunks, int64_t d, int dtype);
+
 /* Replaces capi.mojo:132-138 (`mdgl_segment_softmax`): per segment and
  * column, softmax over the segment's rows; rows of empty segments are not
- * written. `scratch` is accepted for signature compatibility and unused. */
+ * written. Segments are served in their own order; segments longer than
+ * chunk_len come as chunks: chunk c covers rows chunk_start[c] ..
+ * min(chunk_start[c] + chunk_len, offsets[chunk_row[c] + 1]) of segment
+ * chunk_row[c], a segment's chunks are consecutive and chunk_first[c] is the
+ * first of them. `slots` is the value mdgl_softmax_geometry returned.
+ * `scratch` is accepted for signature compatibility and unused. */
 int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, void* scratch,
-                         int64_t num_seg, int64_t d, int64_t n, int dtype, void* stream);
+                         int64_t num_seg, int64_t d, int64_t n, const int32_t* chunk_row,
+                         const int32_t* chunk_start, const int32_t* chunk_first,
+                         int64_t num_chunks, int64_t slots, void* workspace,
+                         int64_t workspace_bytes, int dtype, void* stream);
 
 /* Replaces capi.mojo:149-165 (`mdgl_edge_softmax_`): per CSR row, per
  * column, softmax of logits[eid[i]] over the row's slots whose edge is
  * selected (all_ones = 1, or mask[e] == 1); dst rows of the selected edges
- * are written. `indices` and `scratch` are accepted for signature
- * compatibility and unused. Rows longer than heavy_deg are listed in
- * heavy_rows (num_heavy of them) and get a whole workgroup each; num_heavy
- * = 0 disables that. */
+ * are written. Plan: `order` (device) lists the rows of degree 1 .. chunk_len
+ * sorted by degree, with host `bounds` (nbins + 2 entries, nbins =
+ * log2(slots) + 1): bin k = order[bounds[k] .. bounds[k+1]) holds the rows of
+ * degree <= 2^k (and > 2^(k-1)), order[bounds[nbins] .. bounds[nbins+1])
+ * the rows of degree slots+1 .. chunk_len; or `order` = NULL: every row of
+ * degree <= chunk_len in natural order. Longer rows come as chunks, as in
+ * mdgl_segment_softmax. `indices` and `scratch` are accepted for signature
+ * compatibility and unused. */
 int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
                        const int8_t* mask, const void* logits, void* dst, void* scratch,
-                       int64_t num_nodes, int all_ones, int64_t d, const int32_t* heavy_rows,
-                       int64_t num_heavy, int32_t heavy_deg, int dtype, void* stream);
+                       int64_t num_nodes, int all_ones, int64_t d, const int32_t* order,
+                       const int64_t* bounds, int nbins, const int32_t* chunk_row,
+                       const int32_t* chunk_start, const int32_t* chunk_first,
+                       int64_t num_chunks, int64_t slots, void* workspace,
+                       int64_t workspace_bytes, int dtype, void* stream);
 
 /* Replaces capi.mojo:141-145 (`mdgl_segment_mm`): out rows of segment r are
  * a[rows] @ b[r]; seglen_a (device, int64, r entries) sums to at most n and

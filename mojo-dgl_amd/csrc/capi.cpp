@@ -419,74 +419,127 @@ int mdgl_segment_reduce(const int32_t* offsets, const void* value, void* dst, in
                       0, 0, nullptr, nullptr, 0, nullptr, 0, flags, dtype, stream, true);
 }
 
-int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, void* scratch,
-                         int64_t num_seg, int64_t d, int64_t n, int dtype, void* stream) {
-  (void)scratch;
-  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "segment_softmax: bad dtype %d", dtype);
-  if (num_seg < 0 || d < 0 || n < 0) return fail(MDGL_EINVAL, "segment_softmax: negative size");
-  if (num_seg >= (int64_t(1) << 31) || n >= (int64_t(1) << 31))
-    return fail(MDGL_EINVAL, "segment_softmax: 2**31 or more segments or rows");
-  if (num_seg == 0 || d == 0 || n == 0) return MDGL_OK;
-  if (!offsets || !value || !dst) return fail(MDGL_EINVAL, "segment_softmax: null buffer");
-  SoftmaxParams p{};
-  p.indptr = offsets;
-  p.eid = nullptr;
-  p.mask = nullptr;
-  p.logits = value;
-  p.out = dst;
-  p.num_rows = num_seg;
-  p.d = d;
+// Softmax geometry for (d, dtype) and the two buffers: the vector width
+// follows d and the buffers' alignment, the lane layout follows the width.
+static void softmax_geom(int64_t d, int dtype, const void* logits, const void* out, int* vec,
+                         int64_t* slots, int64_t* chunk_len) {
   const int vw = vec_width(dtype);
   const int64_t es = dsize(dtype);
-  p.vec = (d % vw == 0 && aligned(value, vw * es) && aligned(dst, vw * es)) ? vw : 1;
+  *vec = (d % vw == 0 && aligned(logits, vw * es) && aligned(out, vw * es)) ? vw : 1;
+  const int64_t nvec = (d + *vec - 1) / *vec;
+  int64_t L = 1;
+  while (L < nvec && L < WAVE) L <<= 1;
+  *slots = WAVE / L;
+  *chunk_len = SOFT_CPL * *slots;
+}
+
+int mdgl_softmax_geometry(int64_t d, int dtype, const void* logits, const void* out,
+                          int64_t* slots, int64_t* chunk_len) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "softmax_geometry: bad dtype %d", dtype);
+  if (d <= 0 || !slots || !chunk_len) return fail(MDGL_EINVAL, "softmax_geometry: bad arguments");
+  int vec;
+  softmax_geom(d, dtype, logits, out, &vec, slots, chunk_len);
+  return MDGL_OK;
+}
+
+int64_t mdgl_softmax_workspace_bytes(int64_t num_chunks, int64_t d, int dtype) {
+  if (num_chunks <= 0) return 0;
+  return 2 * num_chunks * d * dsize(dtype);
+}
+
+}  // extern "C"
+
+namespace {
+
+int softmax_common(const char* what, const int32_t* indptr, const int32_t* eid,
+                   const int8_t* mask, const void* logits, void* dst, int64_t num_rows, int64_t d,
+                   const int32_t* order, const int64_t* bounds, int nbins,
+                   const int32_t* chunk_row, const int32_t* chunk_start,
+                   const int32_t* chunk_first, int64_t num_chunks, int64_t slots,
+                   void* workspace, int64_t workspace_bytes, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "%s: bad dtype %d", what, dtype);
+  if (num_rows < 0 || d < 0 || num_chunks < 0) return fail(MDGL_EINVAL, "%s: negative size", what);
+  if (num_rows >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "%s: 2**31 or more rows", what);
+  if (num_rows == 0 || d == 0) return MDGL_OK;
+  if (!indptr || !logits || !dst) return fail(MDGL_EINVAL, "%s: null buffer", what);
+  SoftmaxParams p{};
+  int64_t want_slots, chunk_len;
+  softmax_geom(d, dtype, logits, dst, &p.vec, &want_slots, &chunk_len);
+  if (slots != want_slots)
+    return fail(MDGL_EINVAL, "%s: plan made for %lld slots per wavefront, this call needs %lld "
+                "(ask mdgl_softmax_geometry with the same buffers)", what, (long long)slots,
+                (long long)want_slots);
+  int want_bins = 0;
+  while ((int64_t(1) << want_bins) < slots) ++want_bins;
+  ++want_bins;
+  if (order) {
+    if (!bounds || nbins != want_bins)
+      return fail(MDGL_EINVAL, "%s: a row order needs %d degree bins and their bounds", what,
+                  want_bins);
+    for (int k = 0; k <= nbins; ++k)
+      if (bounds[k] > bounds[k + 1] || bounds[k] < 0)
+        return fail(MDGL_EINVAL, "%s: bin bounds must be non-decreasing", what);
+  }
+  if (num_chunks > 0) {
+    if (!chunk_row || !chunk_start || !chunk_first)
+      return fail(MDGL_EINVAL, "%s: incomplete chunk list", what);
+    const int64_t need = mdgl_softmax_workspace_bytes(num_chunks, d, dtype);
+    if (!workspace || workspace_bytes < need)
+      return fail(MDGL_EWORKSPACE, "%s: workspace of %lld bytes needed, %lld given", what,
+                  (long long)need, (long long)workspace_bytes);
+  }
+  p.indptr = indptr;
+  p.eid = eid;
+  p.mask = mask;
+  p.logits = logits;
+  p.out = dst;
+  p.num_rows = num_rows;
+  p.d = d;
+  p.order = order;
+  p.bounds = bounds;
+  p.nbins = nbins;
+  p.num_chunks = num_chunks;
+  p.chunk_row = chunk_row;
+  p.chunk_start = chunk_start;
+  p.chunk_first = chunk_first;
+  p.part = workspace;
   p.stream = (hipStream_t)stream;
   hipError_t e = dtype == MDGL_FLOAT32 ? launch_softmax<float>(p) : launch_softmax<double>(p);
-  return hip_status(e, "segment_softmax");
+  return hip_status(e, what);
+}
+
+}  // namespace
+
+extern "C" {
+
+int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, void* scratch,
+                         int64_t num_seg, int64_t d, int64_t n, const int32_t* chunk_row,
+                         const int32_t* chunk_start, const int32_t* chunk_first,
+                         int64_t num_chunks, int64_t slots, void* workspace,
+                         int64_t workspace_bytes, int dtype, void* stream) {
+  (void)scratch;
+  if (n < 0) return fail(MDGL_EINVAL, "segment_softmax: negative size");
+  if (n >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "segment_softmax: 2**31 or more rows");
+  if (n == 0) return MDGL_OK;
+  return softmax_common("segment_softmax", offsets, nullptr, nullptr, value, dst, num_seg, d,
+                        nullptr, nullptr, 0, chunk_row, chunk_start, chunk_first, num_chunks,
+                        slots, workspace, workspace_bytes, dtype, stream);
 }
 
 int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
                        const int8_t* mask, const void* logits, void* dst, void* scratch,
-                       int64_t num_nodes, int all_ones, int64_t d, const int32_t* heavy_rows,
-                       int64_t num_heavy, int32_t heavy_deg, int dtype, void* stream) {
+                       int64_t num_nodes, int all_ones, int64_t d, const int32_t* order,
+                       const int64_t* bounds, int nbins, const int32_t* chunk_row,
+                       const int32_t* chunk_start, const int32_t* chunk_first,
+                       int64_t num_chunks, int64_t slots, void* workspace,
+                       int64_t workspace_bytes, int dtype, void* stream) {
   (void)indices;
   (void)scratch;
-  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "edge_softmax: bad dtype %d", dtype);
-  if (num_nodes < 0 || d < 0) return fail(MDGL_EINVAL, "edge_softmax: negative size");
-  if (num_nodes >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "edge_softmax: 2**31 or more rows");
-  if (num_heavy < 0 || (num_heavy > 0 && (!heavy_rows || heavy_deg < 0)))
-    return fail(MDGL_EINVAL, "edge_softmax: bad heavy-row list");
-  if (num_nodes == 0 || d == 0) return MDGL_OK;
-  if (!indptr || !eid || !logits || !dst) return fail(MDGL_EINVAL, "edge_softmax: null buffer");
+  if (num_nodes > 0 && d > 0 && !eid) return fail(MDGL_EINVAL, "edge_softmax: null eid");
   if (all_ones != 1 && !mask) return fail(MDGL_EINVAL, "edge_softmax: null mask");
-  SoftmaxParams p{};
-  p.indptr = indptr;
-  p.eid = eid;
-  p.mask = all_ones == 1 ? nullptr : mask;
-  p.logits = logits;
-  p.out = dst;
-  p.num_rows = num_nodes;
-  p.d = d;
-  const int vw = vec_width(dtype);
-  const int64_t es = dsize(dtype);
-  p.vec = (d % vw == 0 && aligned(logits, vw * es) && aligned(dst, vw * es)) ? vw : 1;
-  p.num_heavy = num_heavy;
-  p.heavy_rows = heavy_rows;
-  p.heavy_deg = heavy_deg;
-  p.stream = (hipStream_t)stream;
-  hipError_t e = dtype == MDGL_FLOAT32 ? launch_softmax<float>(p) : launch_softmax<double>(p);
-  return hip_status(e, "edge_softmax");
-}
-
-int64_t mdgl_segment_mm_workspace_bytes(int64_t n, int64_t d1, int64_t d2, int64_t r, int dtype) {
-  if (n < 0 || d1 < 0 || d2 < 0 || r < 0 || !dtype_ok(dtype)) return -1;
-  return dtype == MDGL_FLOAT32 ? grouped_workspace_bytes<float>(n, d1, d2, r, false)
-                               : grouped_workspace_bytes<double>(n, d1, d2, r, false);
-}
-
-int64_t mdgl_gather_mm_workspace_bytes(int64_t n, int64_t d1, int64_t d2, int64_t r, int dtype) {
-  if (n < 0 || d1 < 0 || d2 < 0 || r < 0 || !dtype_ok(dtype)) return -1;
-  return dtype == MDGL_FLOAT32 ? grouped_workspace_bytes<float>(n, d1, d2, r, true)
-                               : grouped_workspace_bytes<double>(n, d1, d2, r, true);
+  return softmax_common("edge_softmax", indptr, eid, all_ones == 1 ? nullptr : mask, logits, dst,
+                        num_nodes, d, order, bounds, nbins, chunk_row, chunk_start, chunk_first,
+                        num_chunks, slots, workspace, workspace_bytes, dtype, stream);
 }
 
 }  // extern "C"

@@ -71,7 +71,14 @@ template <class T>
 hipError_t launch_gsddmm(const GsddmmParams& p);
 
 // CSR softmax (edge_softmax over in/out CSR, segment_softmax over offsets):
-// per row and column, max, then exp(x - max) summed, then divided.
+// per row and column, max, then exp(x - max) summed, then divided. Rows are
+// served through a plan (see softmax_impl.h): `order` lists the rows sorted
+// by degree with `bounds` (host) delimiting the packed degree bins and the
+// wavefront rows, or is null for all rows in natural order; rows longer than
+// the chunk length come as chunks (chunk_row / chunk_start / chunk_first)
+// whose partials live in `part` (2 * num_chunks * d values).
+constexpr int SOFT_CPL = 8;  // logits cached per lane in a wavefront row of the softmax
+
 struct SoftmaxParams {
   const int32_t* indptr;
   const int32_t* eid;  // null -> identity (segment softmax)
@@ -80,9 +87,14 @@ struct SoftmaxParams {
   void* out;
   int64_t num_rows, d;
   int vec;  // elements per lane
-  int64_t num_heavy;
-  const int32_t* heavy_rows;
-  int32_t heavy_deg;  // rows above this degree are in heavy_rows
+  const int32_t* order;
+  const int64_t* bounds;  // host: nbins + 2 entries
+  int nbins;
+  int64_t num_chunks;
+  const int32_t* chunk_row;
+  const int32_t* chunk_start;
+  const int32_t* chunk_first;
+  void* part;
   hipStream_t stream;
 };
 

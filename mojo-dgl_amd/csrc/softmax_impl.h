@@ -3,23 +3,30 @@
 // the segment offsets with the identity edge id.
 //
 // For each row and each of the d columns: m = max over the row's selected
-// edges, s = sum of exp(x - m), out = exp(x - m) / s, which is the
-// reference's three passes (src/ported.mojo:918-987, 679-768). Only the
-// order of the max and the sum differs: lanes take strided edges and the
-// lane results are combined by a butterfly (and, for heavy rows, across the
-// four wavefronts of a workgroup through LDS). A row with no selected edge
-// writes nothing.
+// edges, s = sum of exp(x - m), out = exp(x - m) / s -- the reference's three
+// passes (src/ported.mojo:918-987, 679-768) -- but every logit is read from
+// memory once: a row's values stay in registers from the max to the write.
+// Only the order of the max and of the sum differs from the reference (lanes
+// combine by __shfl_xor butterflies), so results agree to rounding.
 //
-// Lane layout: L lanes cover the row's d columns (VEC per lane, L a power of
-// two, at most 64) and a wavefront holds P = 64 / L edge slots. Rows wider
-// than 64 * VEC are cut into slabs. Light rows: one wavefront per
-// (row, slab), four per workgroup. Rows above heavy_deg: one workgroup each,
-// in the first num_heavy workgroups.
+// Lane layout. L lanes (a power of two, at most 64) cover the d columns, VEC
+// per lane; a wavefront holds Pw = 64 / L edge slots; rows wider than 64 * VEC
+// are cut into slabs, one wavefront per slab. Rows are served by degree:
+//   * packed: rows sorted by degree; a row of at most 2^k edges gets 2^k slots
+//     (one edge each), so a wavefront takes Pw / 2^k rows of one degree bin;
+//   * wavefront rows: up to CPL * Pw edges, CPL per slot;
+//   * chunked rows (longer): chunks of CPL * Pw edges; launch 1 writes each
+//     chunk's (max, sum of exp(x - max)) per column, launch 2 merges a row's
+//     chunks in chunk order (M = max m_c, S = sum s_c * exp(m_c - M)) and writes
+//     exp(x - M) / S over the chunk.
+// Chunk workgroups come first in launch 1 so the long rows start early.
 #pragma once
 
 #include "mdgl_kernels.h"
 
 namespace mdgl {
+
+enum { SM_FULL = 0, SM_STATS = 1, SM_WRITE = 2 };
 
 template <class T>
 struct SoftmaxArgs {
@@ -29,11 +36,20 @@ struct SoftmaxArgs {
   const T* logits;
   T* out;
   int64_t num_rows, d;
-  int L, S, vec_io;
-  int64_t num_heavy;
-  const int32_t* heavy_rows;
-  int heavy_deg;
-  int64_t light_waves, light_blocks;
+  int L, Pw, S, vec_io, nbins;
+  const int32_t* order;          // rows sorted by degree, or null (natural order)
+  int64_t bin_start[8];          // packed bin k (2^k slots): order[bin_start[k] .. bin_start[k+1])
+  int64_t bin_wave[9];           // wavefronts before bin k (slabs included)
+  int64_t mid_start, mid_end;    // wavefront rows: order[mid_start .. mid_end) or all rows
+  int64_t num_chunks;
+  const int32_t* chunk_row;
+  const int32_t* chunk_start;
+  const int32_t* chunk_first;    // first chunk of the same row
+  int chunk_len;
+  T* pm;  // [num_chunks][d] chunk maxima
+  T* ps;  // [num_chunks][d] chunk sums of exp(x - max)
+  int64_t chunk_waves, chunk_blocks, light_waves, light_blocks;
+  int mode2;  // launch 2: the chunk write pass
 };
 
 __device__ __forceinline__ float exp_t(float x) { return expf(x); }
@@ -62,135 +78,173 @@ __device__ __forceinline__ void store_cols(T* __restrict__ p, int64_t k0, int64_
   }
 }
 
-// One (row, slab) by `nw` cooperating wavefronts (1 for light rows, 4 for
-// heavy ones). `w` is this wavefront's index among them, `red` the LDS area
-// for the cross-wavefront step (heavy only).
-template <class T, int VEC>
-__device__ __forceinline__ void softmax_row(const SoftmaxArgs<T>& a, int64_t row, int64_t slab,
-                                            int w, int nw, int lane, T* red) {
-  const int L = a.L, P = WAVE / L;
-  const int slot = lane / L, cl = lane % L;
-  const int64_t k0 = (slab * L + cl) * VEC;
+// One row (or one chunk of a row) served by a group of Pr slots x L lanes.
+// Every lane of the wavefront calls this with the same Pr, so the slot
+// butterflies below always run on a full wavefront.
+template <class T, int VEC, int NQ>
+__device__ __forceinline__ void soft_group(const SoftmaxArgs<T>& a, int mode, bool row_ok,
+                                           int start, int stop, int Pr, int64_t slab, int lane,
+                                           int64_t chunk) {
+  const int L = a.L;
+  const int s = (lane / L) % Pr, c = lane % L;
+  const int64_t k0 = (slab * L + c) * VEC;
   const bool feat_ok = k0 < a.d;
   const bool vec_io = a.vec_io;
-  const int start = a.indptr[row], stop = a.indptr[row + 1];
-  const int step = P * nw;
-  const int first = start + w * P + slot;
 
-  // pass 1: max
-  T m[VEC];
-  int any = 0;
+  int64_t e[NQ];
+  bool ok[NQ];
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) m[v] = T(-__builtin_huge_val());
-  for (int j = first; j < stop; j += step) {
-    const int64_t e = a.eid ? a.eid[j] : j;
-    if (a.mask && a.mask[e] != 1) continue;
-    any = 1;
-    if (feat_ok) {
-      T x[VEC];
-      load_cols<T, VEC>(a.logits + e * a.d, k0, a.d, vec_io, x);
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) m[v] = x[v] > m[v] ? x[v] : m[v];
-    }
+  for (int q = 0; q < NQ; ++q) {
+    const int j = start + q * Pr + s;
+    ok[q] = row_ok && j < stop;
+    e[q] = 0;
+    if (ok[q]) e[q] = a.eid ? (int64_t)a.eid[j] : (int64_t)j;
   }
-  for (int off = L; off < WAVE; off <<= 1) {
-    any |= __shfl_xor(any, off);
+  if (a.mask) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+      if (ok[q]) ok[q] = a.mask[e[q]] == 1;
+  }
+  T x[NQ][VEC];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q)
+    if (ok[q] && feat_ok) load_cols<T, VEC>(a.logits + e[q] * a.d, k0, a.d, vec_io, x[q]);
+
+  T m[VEC], sum[VEC];
+  const T ninf = T(-__builtin_huge_val());
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) m[v] = ninf;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q)
+    if (ok[q] && feat_ok) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) m[v] = x[q][v] > m[v] ? x[q][v] : m[v];
+    }
+  const int span = L * Pr;
+  for (int off = L; off < span; off <<= 1) {
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
       const T o = __shfl_xor(m[v], off);
       m[v] = o > m[v] ? o : m[v];
     }
   }
-  if (nw > 1) {
-    // lanes of slot 0 publish, then everyone folds the wavefronts in order
-    if (slot == 0) {
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) red[(w * WAVE + cl) * VEC + v] = m[v];
-      red[4 * WAVE * VEC + w] = T(any);
-    }
-    __syncthreads();
-    any = 0;
-    for (int q = 0; q < nw; ++q) {
-      any |= red[4 * WAVE * VEC + q] != T(0);
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        const T o = red[(q * WAVE + cl) * VEC + v];
-        m[v] = (q == 0 || o > m[v]) ? o : m[v];
-      }
-    }
-    __syncthreads();
-  }
-  if (!any) return;  // uniform across the row's wavefronts
 
-  // pass 2: sum of exponentials
-  T s[VEC];
-#pragma unroll
-  for (int v = 0; v < VEC; ++v) s[v] = T(0);
-  for (int j = first; j < stop; j += step) {
-    const int64_t e = a.eid ? a.eid[j] : j;
-    if (a.mask && a.mask[e] != 1) continue;
-    if (feat_ok) {
-      T x[VEC];
-      load_cols<T, VEC>(a.logits + e * a.d, k0, a.d, vec_io, x);
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) s[v] = s[v] + exp_t(x[v] - m[v]);
-    }
-  }
-  for (int off = L; off < WAVE; off <<= 1) {
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) s[v] = s[v] + __shfl_xor(s[v], off);
-  }
-  if (nw > 1) {
-    if (slot == 0) {
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) red[(w * WAVE + cl) * VEC + v] = s[v];
-    }
-    __syncthreads();
+  if (mode == SM_WRITE) {
+    // merge this row's chunk partials in chunk order
+    const int64_t c0 = a.chunk_first[chunk];
+    const int64_t row = a.chunk_row[chunk];
+    const int64_t nch = (a.indptr[row + 1] - a.indptr[row] + a.chunk_len - 1) / a.chunk_len;
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
-      T t = T(0);
-      for (int q = 0; q < nw; ++q) t = t + red[(q * WAVE + cl) * VEC + v];
-      s[v] = t;
+      m[v] = ninf;
+      sum[v] = T(0);
     }
-    __syncthreads();
+    if (feat_ok) {
+      for (int64_t q = c0; q < c0 + nch; ++q)
+#pragma unroll
+        for (int v = 0; v < VEC; ++v)
+          if (k0 + v < a.d) {
+            const T t = a.pm[q * a.d + k0 + v];
+            m[v] = t > m[v] ? t : m[v];
+          }
+      for (int64_t q = c0; q < c0 + nch; ++q)
+#pragma unroll
+        for (int v = 0; v < VEC; ++v)
+          if (k0 + v < a.d) {
+            const T t = a.pm[q * a.d + k0 + v];
+            if (t != ninf) sum[v] = sum[v] + a.ps[q * a.d + k0 + v] * exp_t(t - m[v]);
+          }
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) sum[v] = T(0);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+      if (ok[q] && feat_ok) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) sum[v] = sum[v] + exp_t(x[q][v] - m[v]);
+      }
+    for (int off = L; off < span; off <<= 1) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) sum[v] = sum[v] + __shfl_xor(sum[v], off);
+    }
   }
 
-  // pass 3: write
-  if (!feat_ok) return;
-  for (int j = first; j < stop; j += step) {
-    const int64_t e = a.eid ? a.eid[j] : j;
-    if (a.mask && a.mask[e] != 1) continue;
-    T x[VEC];
-    load_cols<T, VEC>(a.logits + e * a.d, k0, a.d, vec_io, x);
+  if (mode == SM_STATS) {
+    if (row_ok && s == 0 && feat_ok) {
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) x[v] = exp_t(x[v] - m[v]) / s[v];
-    store_cols<T, VEC>(a.out + e * a.d, k0, a.d, vec_io, x);
+      for (int v = 0; v < VEC; ++v)
+        if (k0 + v < a.d) {
+          a.pm[chunk * a.d + k0 + v] = m[v];
+          a.ps[chunk * a.d + k0 + v] = sum[v];
+        }
+    }
+    return;
+  }
+  if (!feat_ok) return;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    if (!ok[q]) continue;
+    T y[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) y[v] = exp_t(x[q][v] - m[v]) / sum[v];
+    store_cols<T, VEC>(a.out + e[q] * a.d, k0, a.d, vec_io, y);
   }
 }
 
 template <class T, int VEC>
 __global__ __launch_bounds__(BLOCK) void softmax_kernel(SoftmaxArgs<T> a) {
-  __shared__ T red[4 * WAVE * VEC + 4];
   const int lane = threadIdx.x & (WAVE - 1);
-  const int w = threadIdx.x >> 6;
   const int64_t b = blockIdx.x;
-  if (b < a.num_heavy) {
-    const int64_t row = a.heavy_rows[b];
-    for (int64_t slab = 0; slab < a.S; ++slab)
-      softmax_row<T, VEC>(a, row, slab, w, WAVES_PER_BLOCK, lane, red);
+  const int Pw = a.Pw;
+  if (b < a.chunk_blocks) {
+    // chunks of the long rows (statistics in launch 1, the write in launch 2)
+    const int64_t w = b * WAVES_PER_BLOCK + (threadIdx.x >> 6);
+    if (w >= a.chunk_waves) return;
+    const int64_t chunk = w / a.S, slab = w % a.S;
+    const int64_t row = a.chunk_row[chunk];
+    const int start = a.chunk_start[chunk];
+    const int end = a.indptr[row + 1];
+    const int stop = end - start > a.chunk_len ? start + a.chunk_len : end;
+    soft_group<T, VEC, SOFT_CPL>(a, a.mode2 ? SM_WRITE : SM_STATS, true, start, stop, Pw, slab,
+                                 lane, chunk);
     return;
   }
-  const int64_t lb = xcd_remap(b - a.num_heavy, a.light_blocks);
-  const int64_t wave = lb * WAVES_PER_BLOCK + w;
-  if (wave >= a.light_waves) return;
-  const int64_t row = wave / a.S, slab = wave % a.S;
-  if (a.num_heavy > 0 && a.indptr[row + 1] - a.indptr[row] > a.heavy_deg) return;
-  softmax_row<T, VEC>(a, row, slab, 0, 1, lane, red);
+  const int64_t lb = xcd_remap(b - a.chunk_blocks, a.light_blocks);
+  const int64_t w = lb * WAVES_PER_BLOCK + (threadIdx.x >> 6);
+  if (w >= a.light_waves) return;
+  const int64_t nmid = (a.mid_end - a.mid_start) * a.S;
+  if (w < nmid) {
+    // one wavefront per row
+    const int64_t i = a.mid_start + w / a.S, slab = w % a.S;
+    const int64_t row = a.order ? (int64_t)a.order[i] : i;
+    const int start = a.indptr[row], stop = a.indptr[row + 1];
+    const bool ok = stop > start && stop - start <= a.chunk_len;
+    soft_group<T, VEC, SOFT_CPL>(a, SM_FULL, ok, start, stop, Pw, slab, lane, 0);
+    return;
+  }
+  // packed rows: find the degree bin of this wavefront
+  const int64_t pw = w - nmid;
+  int k = 0;
+  while (k + 1 < a.nbins && a.bin_wave[k + 1] <= pw) ++k;
+  const int Pr = 1 << k;
+  const int per = Pw / Pr;  // rows per wavefront
+  const int64_t local = pw - a.bin_wave[k];
+  const int64_t slab = local % a.S;
+  const int64_t i = a.bin_start[k] + (local / a.S) * per + lane / (Pr * a.L);
+  const bool ok = i < a.bin_start[k + 1];
+  int start = 0, stop = 0;
+  if (ok) {
+    const int64_t row = a.order[i];
+    start = a.indptr[row];
+    stop = a.indptr[row + 1];
+  }
+  soft_group<T, VEC, 1>(a, SM_FULL, ok, start, stop, Pr, slab, lane, 0);
 }
 
 template <class T, int VEC>
 hipError_t launch_softmax_vec(const SoftmaxParams& p) {
-  SoftmaxArgs<T> a;
+  SoftmaxArgs<T> a{};
   a.indptr = p.indptr;
   a.eid = p.eid;
   a.mask = p.mask;
@@ -202,17 +256,55 @@ hipError_t launch_softmax_vec(const SoftmaxParams& p) {
   int L = 1;
   while (L < nvec && L < WAVE) L <<= 1;
   a.L = L;
+  a.Pw = WAVE / L;
   a.S = (int)((nvec + L - 1) / L);
   a.vec_io = (VEC > 1) && (p.d % VEC == 0);
-  a.num_heavy = p.num_heavy;
-  a.heavy_rows = p.heavy_rows;
-  a.heavy_deg = p.heavy_deg;
-  a.light_waves = p.num_rows * a.S;
+  a.chunk_len = SOFT_CPL * a.Pw;
+  a.order = p.order;
+  a.nbins = 0;
+  int64_t waves = 0;
+  if (p.order) {
+    a.nbins = p.nbins;
+    for (int k = 0; k <= p.nbins; ++k) a.bin_start[k] = p.bounds[k];
+    for (int k = 0; k < p.nbins; ++k) {
+      const int64_t per = a.Pw >> k;
+      a.bin_wave[k] = waves;
+      waves += ((a.bin_start[k + 1] - a.bin_start[k] + per - 1) / per) * a.S;
+    }
+    a.bin_wave[p.nbins] = waves;
+    a.mid_start = p.bounds[p.nbins];
+    a.mid_end = p.bounds[p.nbins + 1];
+  } else {
+    a.mid_start = 0;
+    a.mid_end = p.num_rows;
+  }
+  a.light_waves = (a.mid_end - a.mid_start) * a.S + waves;
   a.light_blocks = (a.light_waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
-  const int64_t blocks = a.num_heavy + a.light_blocks;
-  if (blocks == 0) return hipSuccess;
-  hipLaunchKernelGGL((softmax_kernel<T, VEC>), dim3((unsigned)blocks), dim3(BLOCK), 0, p.stream, a);
-  return hipGetLastError();
+  a.num_chunks = p.num_chunks;
+  a.chunk_row = p.chunk_row;
+  a.chunk_start = p.chunk_start;
+  a.chunk_first = p.chunk_first;
+  a.pm = static_cast<T*>(p.part);
+  a.ps = a.pm ? a.pm + p.num_chunks * p.d : nullptr;
+  a.chunk_waves = p.num_chunks * a.S;
+  a.chunk_blocks = (a.chunk_waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
+  a.mode2 = 0;
+  const int64_t blocks = a.chunk_blocks + a.light_blocks;
+  if (blocks > 0) {
+    hipLaunchKernelGGL((softmax_kernel<T, VEC>), dim3((unsigned)blocks), dim3(BLOCK), 0, p.stream,
+                       a);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  if (a.chunk_blocks > 0) {
+    a.mode2 = 1;
+    a.light_waves = 0;
+    a.light_blocks = 0;
+    hipLaunchKernelGGL((softmax_kernel<T, VEC>), dim3((unsigned)a.chunk_blocks), dim3(BLOCK), 0,
+                       p.stream, a);
+    return hipGetLastError();
+  }
+  return hipSuccess;
 }
 
 template <class T>

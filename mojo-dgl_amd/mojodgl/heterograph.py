@@ -11,7 +11,8 @@ when first needed. Their GPU copies (int32) are cached with two schedules:
 * gspmm: rows longer than CHUNK_LEN are split into CHUNK_LEN-slot chunks
   whose partials are folded in order, so a power-law hub is spread over
   many wavefronts without atomics;
-* softmax: rows longer than SOFTMAX_HEAVY_DEG get a whole workgroup.
+* softmax: rows sorted by degree (packed several to a wavefront when short,
+  one wavefront each when longer, chunks when longer still), per lane layout.
 
 `update_all` / `pull` route builtins exactly as the reference does
 (heterograph.py:206-290): copy_u, copy_e and u_{add,sub,mul,div}_e with a
@@ -34,6 +35,7 @@ from .function.base import TargetCode
 from .function.message import BinaryMessageFunction, CopyMessageFunction, MessageFunction
 from .function.reducer import ReduceFunction
 from .ops import spmm as _spmm
+from .ops._plan import SoftmaxPlan
 from .ops.sddmm import gsddmm
 from .udf import EdgeBatch, FeatureDict, NodeBatch
 
@@ -44,8 +46,6 @@ _Code2Str = TargetCode.CODE2STR
 
 # rows of more in-edges than this are split into chunks of this many for gspmm
 CHUNK_LEN = 512
-# rows of more edges than this get a whole workgroup in edge_softmax
-SOFTMAX_HEAVY_DEG = 1024
 
 
 def chunk_plan(indptr: np.ndarray, chunk_len: int):
@@ -87,17 +87,21 @@ class _Chunks:
 class _DeviceCSR:
     """A CSR view on the GPU (int32) with its gspmm and softmax schedules."""
 
-    def __init__(self, indptr, indices, order, chunk_len, heavy_deg):
+    def __init__(self, indptr, indices, order, chunk_len):
+        self.host_indptr = indptr
         self.indptr = _lib.i32_device(indptr)
         self.indices = _lib.i32_device(indices)
         self.eid = _lib.i32_device(order)
         self.chunks = _Chunks(indptr, chunk_len)
-        deg = np.diff(indptr)
-        hv = np.nonzero(deg > heavy_deg)[0]
-        self.num_soft_heavy = int(hv.size)
-        self.soft_heavy = _lib.i32_device(hv) if hv.size else None
-        self.soft_heavy_deg = int(heavy_deg)
-        self.params = (int(chunk_len), int(heavy_deg))
+        self.params = int(chunk_len)
+        self._softmax = {}
+
+    def softmax_plan(self, slots, chunk_len):
+        """Degree-sorted row order and chunks for a softmax lane layout (cached)."""
+        key = (int(slots), int(chunk_len))
+        if key not in self._softmax:
+            self._softmax[key] = SoftmaxPlan(self.host_indptr, slots, chunk_len, ordered=True)
+        return self._softmax[key]
 
 
 class DGLGraph(object):
@@ -159,11 +163,11 @@ class DGLGraph(object):
     def _device_csr(self, kind):
         """The GPU copy of the in ("in") or out ("out") CSR, built once."""
         self._check_int32()
-        params = (int(CHUNK_LEN), int(SOFTMAX_HEAVY_DEG))
+        params = int(CHUNK_LEN)
         cached = self._dcsr.get(kind)
         if cached is None or cached.params != params:
             indptr, indices, order, _ = self._host_csr(kind)
-            cached = _DeviceCSR(indptr, indices, order, *params)
+            cached = _DeviceCSR(indptr, indices, order, params)
             self._dcsr[kind] = cached
         return cached
 
@@ -173,9 +177,6 @@ class DGLGraph(object):
         if self._dcoo is None:
             self._dcoo = (_lib.i32_device(self._u), _lib.i32_device(self._v))
         return self._dcoo
-
-    def _softmax_heavy_deg(self):
-        return int(SOFTMAX_HEAVY_DEG)
 
     # -------------------------------------------------------------- queries
     def number_of_nodes(self, ntype=None):

@@ -1,0 +1,74 @@
+"""Host-side work plans for the softmax kernels (rows served by degree).
+
+A softmax call on the GPU serves rows in three ways (csrc/softmax_impl.h):
+rows of degree <= `slots` packed several to a wavefront by degree bin, rows of
+degree <= `chunk_len` one wavefront each, longer rows as chunks of
+`chunk_len` edges. `slots` and `chunk_len` come from mdgl_softmax_geometry
+for the buffers of the call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from .. import _lib
+
+
+class SoftmaxPlan:
+    """Plan arrays on the GPU (order / chunks) and the host bin bounds."""
+
+    def __init__(self, indptr: np.ndarray, slots: int, chunk_len: int, ordered: bool):
+        deg = np.diff(indptr)
+        self.slots = int(slots)
+        self.chunk_len = int(chunk_len)
+        self.nbins = int(np.log2(slots)) + 1
+        heavy = np.nonzero(deg > chunk_len)[0]
+        per = (deg[heavy] + chunk_len - 1) // chunk_len
+        first = np.zeros(heavy.size + 1, dtype=np.int64)
+        np.cumsum(per, out=first[1:])
+        row = np.repeat(heavy, per)
+        cfirst = np.repeat(first[:-1], per)
+        local = np.arange(row.size, dtype=np.int64) - cfirst
+        start = indptr[row] + local * chunk_len
+        self.num_chunks = int(row.size)
+        if self.num_chunks:
+            self.chunk_row = _lib.i32_device(row)
+            self.chunk_start = _lib.i32_device(start)
+            self.chunk_first = _lib.i32_device(cfirst)
+        else:
+            self.chunk_row = self.chunk_start = self.chunk_first = None
+        self.order = None
+        self.bounds = None
+        if ordered:
+            rows = np.nonzero((deg > 0) & (deg <= chunk_len))[0]
+            d = deg[rows]
+            key = np.where(d <= slots, np.ceil(np.log2(np.maximum(d, 1))), self.nbins)
+            key = key.astype(np.uint8)
+            perm = np.argsort(key, kind="stable")
+            self.order = _lib.i32_device(rows[perm])
+            counts = np.bincount(key, minlength=self.nbins + 1)
+            self.bounds = np.zeros(self.nbins + 2, dtype=np.int64)
+            np.cumsum(counts, out=self.bounds[1:])
+
+    def bounds_ptr(self):
+        return None if self.bounds is None else self.bounds.ctypes.data
+
+
+def geometry(d, dtype, logits: torch.Tensor, out: torch.Tensor):
+    slots = ctypes.c_int64()
+    chunk = ctypes.c_int64()
+    rc = _lib.lib().mdgl_softmax_geometry(d, _lib.dtype_code(dtype), logits.data_ptr(),
+                                          out.data_ptr(), ctypes.byref(slots),
+                                          ctypes.byref(chunk))
+    _lib.check(rc, "softmax_geometry")
+    return slots.value, chunk.value
+
+
+def workspace(plan: SoftmaxPlan, d, dtype):
+    n = _lib.lib().mdgl_softmax_workspace_bytes(plan.num_chunks, d, _lib.dtype_code(dtype))
+    if not n:
+        return None, 0
+    return torch.empty(n, dtype=torch.uint8, device=_lib.device()), n

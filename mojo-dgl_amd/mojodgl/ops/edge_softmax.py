@@ -15,6 +15,7 @@ import torch
 
 from .. import _lib
 from ..base import ALL, DGLError, is_all
+from . import _plan
 
 __all__ = ["edge_softmax"]
 
@@ -88,10 +89,13 @@ def edge_softmax(graph, logits, eids=ALL, norm_by="dst"):
     out = alloc((out_len, d), dtype=_lib.torch_dtype(dtype), device=gdev)
     if out_len and d:
         lg = _lib.on_device(X, dtype).reshape(out_len, d)
+        if order is not None:
+            lg = lg[: order.size].contiguous()
+        slots, chunk_len = _plan.geometry(d, dtype, lg, out)
         if order is None:
             csr = graph._device_csr("in" if norm_by == "dst" else "out")
             indptr, eid, rows = csr.indptr, csr.eid, num_nodes
-            heavy, num_heavy, heavy_deg = csr.soft_heavy, csr.num_soft_heavy, csr.soft_heavy_deg
+            plan = csr.softmax_plan(slots, chunk_len)
         else:
             u, v = graph._edge_arrays()
             key = (v if norm_by == "dst" else u)[order]
@@ -102,15 +106,14 @@ def edge_softmax(graph, logits, eids=ALL, norm_by="dst"):
             np.cumsum(counts, out=ptr[1:])
             rows = int(counts.size)
             indptr, eid = _lib.i32_device(ptr), _lib.i32_device(pos)
-            heavy_deg = graph._softmax_heavy_deg()
-            hv = np.nonzero(counts > heavy_deg)[0]
-            num_heavy = int(hv.size)
-            heavy = _lib.i32_device(hv) if num_heavy else None
-            lg = lg[: order.size].contiguous()
+            plan = _plan.SoftmaxPlan(ptr, slots, chunk_len, ordered=True)
         if rows:
+            ws, nbytes = _plan.workspace(plan, d, dtype)
             rc = _lib.lib().mdgl_edge_softmax_(
                 indptr.data_ptr(), None, eid.data_ptr(), None, lg.data_ptr(), out.data_ptr(), None,
-                rows, 1, d, _lib.ptr(heavy), num_heavy, heavy_deg, _lib.dtype_code(dtype),
+                rows, 1, d, _lib.ptr(plan.order), plan.bounds_ptr(), plan.nbins,
+                _lib.ptr(plan.chunk_row), _lib.ptr(plan.chunk_start), _lib.ptr(plan.chunk_first),
+                plan.num_chunks, plan.slots, _lib.ptr(ws), nbytes, _lib.dtype_code(dtype),
                 _lib.stream())
             _lib.check(rc, "edge_softmax")
     return _lib.give_back(out.reshape(shape), X.is_torch, X.device)

@@ -14,6 +14,7 @@ import torch
 from .. import _lib
 from .._lib import REDUCERS
 from ..base import DGLError
+from . import _plan
 
 __all__ = ["segment_reduce", "segment_softmax", "segment_mm"]
 
@@ -111,10 +112,16 @@ def segment_softmax(seglen, value):
     gdev = _lib.device()
     out = torch.zeros((n, d), dtype=_lib.torch_dtype(dtype), device=gdev)
     if num_seg and n and d:
-        val = _lib.on_device(V, dtype)
+        val = _lib.on_device(V, dtype).reshape(n, d)
         off = _lib.i32_device(offsets)
-        rc = _lib.lib().mdgl_segment_softmax(off.data_ptr(), val.data_ptr(), out.data_ptr(), None,
-                                             num_seg, d, n, _lib.dtype_code(dtype), _lib.stream())
+        slots, chunk_len = _plan.geometry(d, dtype, val, out)
+        plan = _plan.SoftmaxPlan(offsets, slots, chunk_len, ordered=False)
+        ws, nbytes = _plan.workspace(plan, d, dtype)
+        rc = _lib.lib().mdgl_segment_softmax(
+            off.data_ptr(), val.data_ptr(), out.data_ptr(), None, num_seg, d, n,
+            _lib.ptr(plan.chunk_row), _lib.ptr(plan.chunk_start), _lib.ptr(plan.chunk_first),
+            plan.num_chunks, plan.slots, _lib.ptr(ws), nbytes, _lib.dtype_code(dtype),
+            _lib.stream())
         _lib.check(rc, "segment_softmax")
     return _lib.give_back(out.reshape(shape), V.is_torch, V.device)
 

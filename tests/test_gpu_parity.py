@@ -233,8 +233,8 @@ def test_gsddmm_broadcast_copy_and_multihead_dot():
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("norm_by", ["dst", "src"])
 @pytest.mark.parametrize("shape", [(), (1,), (3, 1), (8, 1), (2, 4, 1), (40, 1)])
-def test_edge_softmax(dtype, norm_by, shape, monkeypatch):
-    monkeypatch.setattr(hg, "SOFTMAX_HEAVY_DEG", 64)
+def test_edge_softmax(dtype, norm_by, shape):
+    # degrees 0 .. ~520: every row class (packed bins, wavefront rows, chunked hubs)
     n, e = 400, 6000
     u, v = rand_graph(n, e, 15)
     v[:500] = 3  # a hub above the workgroup threshold
@@ -434,3 +434,49 @@ def test_repeat_runs_are_bit_identical():
     s1 = ops.edge_softmax(g, w[:, :1])
     s2 = ops.edge_softmax(g, w[:, :1])
     assert torch.equal(s1, s2)
+
+
+def test_edge_softmax_power_law_and_mask_through_the_abi():
+    """Hubs of thousands of edges (many chunks), then the C ABI's mask path
+    (all_ones = 0), which the Python API never takes, against the oracle."""
+    import ctypes
+
+    from mojodgl import _lib
+    from mojodgl.ops import _plan
+
+    rng = np.random.default_rng(31)
+    n = 4000
+    deg = np.minimum(rng.zipf(1.8, n), 6000)
+    v = rng.permutation(np.repeat(np.arange(n), deg))
+    u = rng.integers(0, n, v.size)
+    e = v.size
+    logits = (rng.normal(size=(e, 8, 1)) * 3).astype(np.float32)
+    g = dgl.graph((u, v), num_nodes=n)
+    got = ops.edge_softmax(g, logits)
+    ref = oracle.edge_softmax(u, v, n, logits)
+    close(got, ref, ref, np.float32, "power-law edge_softmax")
+
+    mask = (rng.random(e) < 0.6).astype(np.int8)
+    csr = g._device_csr("in")
+    lg = torch.from_numpy(logits.reshape(e, 8)).cuda()
+    out = torch.full((e, 8), -7.0, device="cuda")
+    slots, chunk_len = _plan.geometry(8, np.float32, lg, out)
+    plan = csr.softmax_plan(slots, chunk_len)
+    ws, nbytes = _plan.workspace(plan, 8, np.float32)
+    m = torch.from_numpy(mask).cuda()
+    rc = _lib.lib().mdgl_edge_softmax_(
+        csr.indptr.data_ptr(), None, csr.eid.data_ptr(), m.data_ptr(), lg.data_ptr(),
+        out.data_ptr(), None, n, 0, 8, _lib.ptr(plan.order), plan.bounds_ptr(), plan.nbins,
+        _lib.ptr(plan.chunk_row), _lib.ptr(plan.chunk_start), _lib.ptr(plan.chunk_first),
+        plan.num_chunks, plan.slots, _lib.ptr(ws), nbytes, 0, _lib.stream())
+    assert rc == 0
+    got = out.cpu().numpy()
+    indptr, _, eid = oracle.csr(u, v, n, "dst")
+    want = np.full((e, 8), -7.0)
+    oracle.lib().oracle_edge_softmax(indptr.ctypes.data, eid.ctypes.data, mask.ctypes.data,
+                                     np.ascontiguousarray(logits.reshape(e, 8),
+                                                          dtype=np.float64).ctypes.data,
+                                     want.ctypes.data, n, 0, 8, 1)
+    sel = mask == 1
+    np.testing.assert_array_equal(got[~sel], -7.0)  # unselected rows untouched
+    close(got[sel], want[sel], want[sel], np.float32, "masked")
