@@ -447,6 +447,18 @@ int64_t mdgl_softmax_workspace_bytes(int64_t num_chunks, int64_t d, int dtype) {
   return 2 * num_chunks * d * dsize(dtype);
 }
 
+int64_t mdgl_segment_mm_workspace_bytes(int64_t n, int64_t d1, int64_t d2, int64_t r, int dtype) {
+  if (n < 0 || d1 < 0 || d2 < 0 || r < 0 || !dtype_ok(dtype)) return -1;
+  return dtype == MDGL_FLOAT32 ? grouped_workspace_bytes<float>(n, d1, d2, r, false)
+                               : grouped_workspace_bytes<double>(n, d1, d2, r, false);
+}
+
+int64_t mdgl_gather_mm_workspace_bytes(int64_t n, int64_t d1, int64_t d2, int64_t r, int dtype) {
+  if (n < 0 || d1 < 0 || d2 < 0 || r < 0 || !dtype_ok(dtype)) return -1;
+  return dtype == MDGL_FLOAT32 ? grouped_workspace_bytes<float>(n, d1, d2, r, true)
+                               : grouped_workspace_bytes<double>(n, d1, d2, r, true);
+}
+
 }  // extern "C"
 
 namespace {
