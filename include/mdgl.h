@@ -121,8 +121,10 @@ int mdgl_segment_reduce(const int32_t* offsets, const void* value, void* dst, in
  * reference (its split is a fixed 32-way CPU split, ported.mojo:34-42). */
 int mdgl_softmax_geometry(int64_t d, int dtype, const void* logits, const void* out,
                           int64_t* slots, int64_t* chunk_len);
-/* Workspace of a softmax call with `num_chunks` chunks (their partials). */
-int64_t mdgl_softmax_workspace_bytes(int64_t num_chunks, int64_t d, int dtype);
+/* Workspace of a softmax call: partials of `num_chunks` chunks, plus a
+ * (max, sum) table of `table_rows` rows for the two-pass edge_softmax. */
+int64_t mdgl_softmax_workspace_bytes(int64_t num_chunks, int64_t table_rows, int64_t d,
+                                     int dtype);
 
 /* Replaces capi.mojo:132-138 (`mdgl_segment_softmax`): per segment and
  * column, softmax over the segment's rows; rows of empty segments are not
@@ -147,15 +149,20 @@ int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, v
  * degree <= 2^k (and > 2^(k-1)), order[bounds[nbins] .. bounds[nbins+1])
  * the rows of degree slots+1 .. chunk_len; or `order` = NULL: every row of
  * degree <= chunk_len in natural order. Longer rows come as chunks, as in
- * mdgl_segment_softmax. `indices` and `scratch` are accepted for signature
- * compatibility and unused. */
+ * mdgl_segment_softmax. With `row_of_edge` (device, num_edges entries: the
+ * CSR row of every edge id, i.e. the destination -- or source -- node) the
+ * output is written by a second, edge-parallel pass in edge-id order
+ * (coalesced stores) from a per-row (max, sum) table in the workspace;
+ * without it every row writes its own edges. `indices` and `scratch` are
+ * accepted for signature compatibility and unused. */
 int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
                        const int8_t* mask, const void* logits, void* dst, void* scratch,
                        int64_t num_nodes, int all_ones, int64_t d, const int32_t* order,
                        const int64_t* bounds, int nbins, const int32_t* chunk_row,
                        const int32_t* chunk_start, const int32_t* chunk_first,
-                       int64_t num_chunks, int64_t slots, void* workspace,
-                       int64_t workspace_bytes, int dtype, void* stream);
+                       int64_t num_chunks, int64_t slots, const int32_t* row_of_edge,
+                       int64_t num_edges, void* workspace, int64_t workspace_bytes, int dtype,
+                       void* stream);
 
 /* Replaces capi.mojo:141-145 (`mdgl_segment_mm`): out rows of segment r are
  * a[rows] @ b[r]; seglen_a (device, int64, r entries) sums to at most n and

@@ -442,9 +442,11 @@ int mdgl_softmax_geometry(int64_t d, int dtype, const void* logits, const void* 
   return MDGL_OK;
 }
 
-int64_t mdgl_softmax_workspace_bytes(int64_t num_chunks, int64_t d, int dtype) {
-  if (num_chunks <= 0) return 0;
-  return 2 * num_chunks * d * dsize(dtype);
+int64_t mdgl_softmax_workspace_bytes(int64_t num_chunks, int64_t table_rows, int64_t d,
+                                     int dtype) {
+  if (num_chunks < 0 || table_rows < 0 || d < 0 || !dtype_ok(dtype)) return -1;
+  const int64_t part = ((2 * num_chunks * d * dsize(dtype) + 255) / 256) * 256;
+  return part + 2 * table_rows * d * dsize(dtype);
 }
 
 int64_t mdgl_segment_mm_workspace_bytes(int64_t n, int64_t d1, int64_t d2, int64_t r, int dtype) {
@@ -468,7 +470,8 @@ int softmax_common(const char* what, const int32_t* indptr, const int32_t* eid,
                    const int32_t* order, const int64_t* bounds, int nbins,
                    const int32_t* chunk_row, const int32_t* chunk_start,
                    const int32_t* chunk_first, int64_t num_chunks, int64_t slots,
-                   void* workspace, int64_t workspace_bytes, int dtype, void* stream) {
+                   const int32_t* row_of, int64_t num_edges, void* workspace,
+                   int64_t workspace_bytes, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "%s: bad dtype %d", what, dtype);
   if (num_rows < 0 || d < 0 || num_chunks < 0) return fail(MDGL_EINVAL, "%s: negative size", what);
   if (num_rows >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "%s: 2**31 or more rows", what);
@@ -492,14 +495,13 @@ int softmax_common(const char* what, const int32_t* indptr, const int32_t* eid,
       if (bounds[k] > bounds[k + 1] || bounds[k] < 0)
         return fail(MDGL_EINVAL, "%s: bin bounds must be non-decreasing", what);
   }
-  if (num_chunks > 0) {
-    if (!chunk_row || !chunk_start || !chunk_first)
-      return fail(MDGL_EINVAL, "%s: incomplete chunk list", what);
-    const int64_t need = mdgl_softmax_workspace_bytes(num_chunks, d, dtype);
-    if (!workspace || workspace_bytes < need)
-      return fail(MDGL_EWORKSPACE, "%s: workspace of %lld bytes needed, %lld given", what,
-                  (long long)need, (long long)workspace_bytes);
-  }
+  if (num_chunks > 0 && (!chunk_row || !chunk_start || !chunk_first))
+    return fail(MDGL_EINVAL, "%s: incomplete chunk list", what);
+  if (row_of && num_edges < 0) return fail(MDGL_EINVAL, "%s: negative edge count", what);
+  const int64_t need = mdgl_softmax_workspace_bytes(num_chunks, row_of ? num_rows : 0, d, dtype);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(MDGL_EWORKSPACE, "%s: workspace of %lld bytes needed, %lld given", what,
+                (long long)need, (long long)workspace_bytes);
   p.indptr = indptr;
   p.eid = eid;
   p.mask = mask;
@@ -514,7 +516,12 @@ int softmax_common(const char* what, const int32_t* indptr, const int32_t* eid,
   p.chunk_row = chunk_row;
   p.chunk_start = chunk_start;
   p.chunk_first = chunk_first;
-  p.part = workspace;
+  p.part = num_chunks > 0 ? workspace : nullptr;
+  if (row_of) {
+    p.row_of = row_of;
+    p.num_edges = num_edges;
+    p.table = static_cast<char*>(workspace) + ((2 * num_chunks * d * dsize(dtype) + 255) / 256) * 256;
+  }
   p.stream = (hipStream_t)stream;
   hipError_t e = dtype == MDGL_FLOAT32 ? launch_softmax<float>(p) : launch_softmax<double>(p);
   return hip_status(e, what);
@@ -535,7 +542,7 @@ int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, v
   if (n == 0) return MDGL_OK;
   return softmax_common("segment_softmax", offsets, nullptr, nullptr, value, dst, num_seg, d,
                         nullptr, nullptr, 0, chunk_row, chunk_start, chunk_first, num_chunks,
-                        slots, workspace, workspace_bytes, dtype, stream);
+                        slots, nullptr, 0, workspace, workspace_bytes, dtype, stream);
 }
 
 int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
@@ -543,15 +550,17 @@ int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int3
                        int64_t num_nodes, int all_ones, int64_t d, const int32_t* order,
                        const int64_t* bounds, int nbins, const int32_t* chunk_row,
                        const int32_t* chunk_start, const int32_t* chunk_first,
-                       int64_t num_chunks, int64_t slots, void* workspace,
-                       int64_t workspace_bytes, int dtype, void* stream) {
+                       int64_t num_chunks, int64_t slots, const int32_t* row_of_edge,
+                       int64_t num_edges, void* workspace, int64_t workspace_bytes, int dtype,
+                       void* stream) {
   (void)indices;
   (void)scratch;
   if (num_nodes > 0 && d > 0 && !eid) return fail(MDGL_EINVAL, "edge_softmax: null eid");
   if (all_ones != 1 && !mask) return fail(MDGL_EINVAL, "edge_softmax: null mask");
   return softmax_common("edge_softmax", indptr, eid, all_ones == 1 ? nullptr : mask, logits, dst,
                         num_nodes, d, order, bounds, nbins, chunk_row, chunk_start, chunk_first,
-                        num_chunks, slots, workspace, workspace_bytes, dtype, stream);
+                        num_chunks, slots, row_of_edge, num_edges, workspace, workspace_bytes,
+                        dtype, stream);
 }
 
 }  // extern "C"

@@ -95,6 +95,10 @@ struct SoftmaxParams {
   const int32_t* chunk_start;
   const int32_t* chunk_first;
   void* part;
+  // two-pass form: the row of every edge id and a [num_rows][2][d] table
+  const int32_t* row_of;
+  int64_t num_edges;
+  void* table;
   hipStream_t stream;
 };
 

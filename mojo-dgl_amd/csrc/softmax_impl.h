@@ -20,6 +20,13 @@
 //     chunks in chunk order (M = max m_c, S = sum s_c * exp(m_c - M)) and writes
 //     exp(x - M) / S over the chunk.
 // Chunk workgroups come first in launch 1 so the long rows start early.
+//
+// Two-pass form (edge_softmax with a row-of-edge array): a random 32-byte
+// write per edge costs more than the rest of the op, so the row pass then
+// only writes each row's (max, sum) to a node table tab[row][2][d], and an
+// edge-parallel pass in edge-id order writes out[e] = exp(x - max) / sum with
+// coalesced loads and stores, reading the table row of the edge's row. The
+// values are the ones the one-pass form writes.
 #pragma once
 
 #include "mdgl_kernels.h"
@@ -50,6 +57,7 @@ struct SoftmaxArgs {
   T* ps;  // [num_chunks][d] chunk sums of exp(x - max)
   int64_t chunk_waves, chunk_blocks, light_waves, light_blocks;
   int mode2;  // launch 2: the chunk write pass
+  T* tab;     // two-pass form: [num_rows][2][d] (max, sum), else null
 };
 
 __device__ __forceinline__ float exp_t(float x) { return expf(x); }
@@ -83,20 +91,22 @@ __device__ __forceinline__ void store_cols(T* __restrict__ p, int64_t k0, int64_
 // butterflies below always run on a full wavefront.
 template <class T, int VEC, int NQ>
 __device__ __forceinline__ void soft_group(const SoftmaxArgs<T>& a, int mode, bool row_ok,
-                                           int start, int stop, int Pr, int64_t slab, int lane,
-                                           int64_t chunk) {
+                                           int64_t row_id, int start, int stop, int Pr,
+                                           int64_t slab, int lane, int64_t chunk) {
   const int L = a.L;
   const int s = (lane / L) % Pr, c = lane % L;
   const int64_t k0 = (slab * L + c) * VEC;
   const bool feat_ok = k0 < a.d;
   const bool vec_io = a.vec_io;
 
+  // the two-pass chunk merge needs the partials only, not the logits
+  const bool load = !(mode == SM_WRITE && a.tab);
   int64_t e[NQ];
   bool ok[NQ];
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     const int j = start + q * Pr + s;
-    ok[q] = row_ok && j < stop;
+    ok[q] = load && row_ok && j < stop;
     e[q] = 0;
     if (ok[q]) e[q] = a.eid ? (int64_t)a.eid[j] : (int64_t)j;
   }
@@ -182,6 +192,21 @@ __device__ __forceinline__ void soft_group(const SoftmaxArgs<T>& a, int mode, bo
     return;
   }
   if (!feat_ok) return;
+  if (a.tab) {
+    // two-pass form: the row's (max, sum) go to the node table
+    const bool writer = mode == SM_WRITE ? (s == 0 && a.chunk_first[chunk] == chunk)
+                                         : (row_ok && s == 0);
+    if (writer) {
+      T* t = a.tab + row_id * 2 * a.d;
+#pragma unroll
+      for (int v = 0; v < VEC; ++v)
+        if (k0 + v < a.d) {
+          t[k0 + v] = m[v];
+          t[a.d + k0 + v] = sum[v];
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     if (!ok[q]) continue;
@@ -202,12 +227,14 @@ __global__ __launch_bounds__(BLOCK) void softmax_kernel(SoftmaxArgs<T> a) {
     const int64_t w = b * WAVES_PER_BLOCK + (threadIdx.x >> 6);
     if (w >= a.chunk_waves) return;
     const int64_t chunk = w / a.S, slab = w % a.S;
+    // two-pass merge: the first chunk of each row writes the row's table entry
+    if (a.mode2 && a.tab && a.chunk_first[chunk] != chunk) return;
     const int64_t row = a.chunk_row[chunk];
     const int start = a.chunk_start[chunk];
     const int end = a.indptr[row + 1];
     const int stop = end - start > a.chunk_len ? start + a.chunk_len : end;
-    soft_group<T, VEC, SOFT_CPL>(a, a.mode2 ? SM_WRITE : SM_STATS, true, start, stop, Pw, slab,
-                                 lane, chunk);
+    soft_group<T, VEC, SOFT_CPL>(a, a.mode2 ? SM_WRITE : SM_STATS, true, row, start, stop, Pw,
+                                 slab, lane, chunk);
     return;
   }
   const int64_t lb = xcd_remap(b - a.chunk_blocks, a.light_blocks);
@@ -220,7 +247,7 @@ __global__ __launch_bounds__(BLOCK) void softmax_kernel(SoftmaxArgs<T> a) {
     const int64_t row = a.order ? (int64_t)a.order[i] : i;
     const int start = a.indptr[row], stop = a.indptr[row + 1];
     const bool ok = stop > start && stop - start <= a.chunk_len;
-    soft_group<T, VEC, SOFT_CPL>(a, SM_FULL, ok, start, stop, Pw, slab, lane, 0);
+    soft_group<T, VEC, SOFT_CPL>(a, SM_FULL, ok, row, start, stop, Pw, slab, lane, 0);
     return;
   }
   // packed rows: find the degree bin of this wavefront
@@ -234,12 +261,41 @@ __global__ __launch_bounds__(BLOCK) void softmax_kernel(SoftmaxArgs<T> a) {
   const int64_t i = a.bin_start[k] + (local / a.S) * per + lane / (Pr * a.L);
   const bool ok = i < a.bin_start[k + 1];
   int start = 0, stop = 0;
+  int64_t row = 0;
   if (ok) {
-    const int64_t row = a.order[i];
+    row = a.order[i];
     start = a.indptr[row];
     stop = a.indptr[row + 1];
   }
-  soft_group<T, VEC, 1>(a, SM_FULL, ok, start, stop, Pr, slab, lane, 0);
+  soft_group<T, VEC, 1>(a, SM_FULL, ok, row, start, stop, Pr, slab, lane, 0);
+}
+
+// Edge-parallel write of the two-pass form: L lanes per edge, 64 / L edges
+// per wavefront, edges in id order.
+template <class T, int VEC>
+__global__ __launch_bounds__(BLOCK) void softmax_edge_kernel(const T* __restrict__ logits,
+                                                             T* __restrict__ out,
+                                                             const T* __restrict__ tab,
+                                                             const int32_t* __restrict__ row_of,
+                                                             const int8_t* __restrict__ mask,
+                                                             int64_t num_edges, int64_t d, int L,
+                                                             int S, int vec_io, int64_t nblocks) {
+  const int64_t blk = xcd_remap(blockIdx.x, nblocks);
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int64_t w = blk * WAVES_PER_BLOCK + (threadIdx.x >> 6);
+  const int64_t slab = w % S;
+  const int64_t e = (w / S) * (WAVE / L) + lane / L;
+  const int64_t k0 = (slab * L + lane % L) * VEC;
+  if (e >= num_edges || k0 >= d) return;
+  if (mask && mask[e] != 1) return;
+  const int64_t r = row_of[e];
+  T x[VEC], m[VEC], s[VEC];
+  load_cols<T, VEC>(logits + e * d, k0, d, vec_io, x);
+  load_cols<T, VEC>(tab + r * 2 * d, k0, d, vec_io, m);
+  load_cols<T, VEC>(tab + r * 2 * d + d, k0, d, vec_io, s);
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) x[v] = exp_t(x[v] - m[v]) / s[v];
+  store_cols<T, VEC>(out + e * d, k0, d, vec_io, x);
 }
 
 template <class T, int VEC>
@@ -289,6 +345,7 @@ hipError_t launch_softmax_vec(const SoftmaxParams& p) {
   a.chunk_waves = p.num_chunks * a.S;
   a.chunk_blocks = (a.chunk_waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
   a.mode2 = 0;
+  a.tab = static_cast<T*>(p.table);
   const int64_t blocks = a.chunk_blocks + a.light_blocks;
   if (blocks > 0) {
     hipLaunchKernelGGL((softmax_kernel<T, VEC>), dim3((unsigned)blocks), dim3(BLOCK), 0, p.stream,
@@ -302,6 +359,15 @@ hipError_t launch_softmax_vec(const SoftmaxParams& p) {
     a.light_blocks = 0;
     hipLaunchKernelGGL((softmax_kernel<T, VEC>), dim3((unsigned)a.chunk_blocks), dim3(BLOCK), 0,
                        p.stream, a);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  if (a.tab && p.num_edges > 0) {
+    const int64_t waves = ((p.num_edges + (WAVE / L) - 1) / (WAVE / L)) * a.S;
+    const int64_t nb = (waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
+    hipLaunchKernelGGL((softmax_edge_kernel<T, VEC>), dim3((unsigned)nb), dim3(BLOCK), 0,
+                       p.stream, a.logits, a.out, a.tab, p.row_of, a.mask, p.num_edges, p.d, L,
+                       a.S, a.vec_io, nb);
     return hipGetLastError();
   }
   return hipSuccess;

@@ -67,8 +67,9 @@ def geometry(d, dtype, logits: torch.Tensor, out: torch.Tensor):
     return slots.value, chunk.value
 
 
-def workspace(plan: SoftmaxPlan, d, dtype):
-    n = _lib.lib().mdgl_softmax_workspace_bytes(plan.num_chunks, d, _lib.dtype_code(dtype))
+def workspace(plan: SoftmaxPlan, d, dtype, table_rows=0):
+    n = _lib.lib().mdgl_softmax_workspace_bytes(plan.num_chunks, table_rows, d,
+                                                _lib.dtype_code(dtype))
     if not n:
         return None, 0
     return torch.empty(n, dtype=torch.uint8, device=_lib.device()), n

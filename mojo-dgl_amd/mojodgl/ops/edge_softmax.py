@@ -96,6 +96,10 @@ def edge_softmax(graph, logits, eids=ALL, norm_by="dst"):
             csr = graph._device_csr("in" if norm_by == "dst" else "out")
             indptr, eid, rows = csr.indptr, csr.eid, num_nodes
             plan = csr.softmax_plan(slots, chunk_len)
+            # the row of an edge is its destination (source) node: the second,
+            # edge-parallel pass writes the output in edge-id order
+            uids, vids = graph._device_coo()
+            row_of = vids if norm_by == "dst" else uids
         else:
             u, v = graph._edge_arrays()
             key = (v if norm_by == "dst" else u)[order]
@@ -107,13 +111,15 @@ def edge_softmax(graph, logits, eids=ALL, norm_by="dst"):
             rows = int(counts.size)
             indptr, eid = _lib.i32_device(ptr), _lib.i32_device(pos)
             plan = _plan.SoftmaxPlan(ptr, slots, chunk_len, ordered=True)
+            row_of = None
         if rows:
-            ws, nbytes = _plan.workspace(plan, d, dtype)
+            n_edges = lg.shape[0]
+            ws, nbytes = _plan.workspace(plan, d, dtype, rows if row_of is not None else 0)
             rc = _lib.lib().mdgl_edge_softmax_(
                 indptr.data_ptr(), None, eid.data_ptr(), None, lg.data_ptr(), out.data_ptr(), None,
                 rows, 1, d, _lib.ptr(plan.order), plan.bounds_ptr(), plan.nbins,
                 _lib.ptr(plan.chunk_row), _lib.ptr(plan.chunk_start), _lib.ptr(plan.chunk_first),
-                plan.num_chunks, plan.slots, _lib.ptr(ws), nbytes, _lib.dtype_code(dtype),
-                _lib.stream())
+                plan.num_chunks, plan.slots, _lib.ptr(row_of), n_edges, _lib.ptr(ws), nbytes,
+                _lib.dtype_code(dtype), _lib.stream())
             _lib.check(rc, "edge_softmax")
     return _lib.give_back(out.reshape(shape), X.is_torch, X.device)

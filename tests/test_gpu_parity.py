@@ -462,15 +462,7 @@ def test_edge_softmax_power_law_and_mask_through_the_abi():
     out = torch.full((e, 8), -7.0, device="cuda")
     slots, chunk_len = _plan.geometry(8, np.float32, lg, out)
     plan = csr.softmax_plan(slots, chunk_len)
-    ws, nbytes = _plan.workspace(plan, 8, np.float32)
     m = torch.from_numpy(mask).cuda()
-    rc = _lib.lib().mdgl_edge_softmax_(
-        csr.indptr.data_ptr(), None, csr.eid.data_ptr(), m.data_ptr(), lg.data_ptr(),
-        out.data_ptr(), None, n, 0, 8, _lib.ptr(plan.order), plan.bounds_ptr(), plan.nbins,
-        _lib.ptr(plan.chunk_row), _lib.ptr(plan.chunk_start), _lib.ptr(plan.chunk_first),
-        plan.num_chunks, plan.slots, _lib.ptr(ws), nbytes, 0, _lib.stream())
-    assert rc == 0
-    got = out.cpu().numpy()
     indptr, _, eid = oracle.csr(u, v, n, "dst")
     want = np.full((e, 8), -7.0)
     oracle.lib().oracle_edge_softmax(indptr.ctypes.data, eid.ctypes.data, mask.ctypes.data,
@@ -478,5 +470,17 @@ def test_edge_softmax_power_law_and_mask_through_the_abi():
                                                           dtype=np.float64).ctypes.data,
                                      want.ctypes.data, n, 0, 8, 1)
     sel = mask == 1
-    np.testing.assert_array_equal(got[~sel], -7.0)  # unselected rows untouched
-    close(got[sel], want[sel], want[sel], np.float32, "masked")
+    _, vids = g._device_coo()
+    for row_of in (None, vids):  # one-pass and two-pass forms
+        out.fill_(-7.0)
+        ws, nbytes = _plan.workspace(plan, 8, np.float32, n if row_of is not None else 0)
+        rc = _lib.lib().mdgl_edge_softmax_(
+            csr.indptr.data_ptr(), None, csr.eid.data_ptr(), m.data_ptr(), lg.data_ptr(),
+            out.data_ptr(), None, n, 0, 8, _lib.ptr(plan.order), plan.bounds_ptr(), plan.nbins,
+            _lib.ptr(plan.chunk_row), _lib.ptr(plan.chunk_start), _lib.ptr(plan.chunk_first),
+            plan.num_chunks, plan.slots, _lib.ptr(row_of), e, _lib.ptr(ws), nbytes, 0,
+            _lib.stream())
+        assert rc == 0
+        got = out.cpu().numpy()
+        np.testing.assert_array_equal(got[~sel], -7.0)  # unselected rows untouched
+        close(got[sel], want[sel], want[sel], np.float32, "masked")
