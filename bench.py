@@ -351,13 +351,14 @@ def workload_c4(args):
     seglen = rng.poisson(20, 1_000_000)
     R = int(seglen.sum())
     val = torch.randn(R, 16, device="cuda", generator=gen)
+    seglen_d = torch.from_numpy(seglen).cuda()  # lengths resident on the GPU like the values
 
     def step(t):
         run = t if t is not None else (lambda name, fn_: fn_())
         run("u_dot_v", lambda: ops.u_dot_v(g, h, h))
-        run("segment_sum", lambda: ops.segment_reduce(seglen, val, "sum"))
-        run("segment_max", lambda: ops.segment_reduce(seglen, val, "max"))
-        run("segment_softmax", lambda: ops.segment_softmax(seglen, val))
+        run("segment_sum", lambda: ops.segment_reduce(seglen_d, val, "sum"))
+        run("segment_max", lambda: ops.segment_reduce(seglen_d, val, "max"))
+        run("segment_softmax", lambda: ops.segment_softmax(seglen_d, val))
 
     timer = OpTimer()
     ms = run_steps(step, args.steps, args.warmup, timer)

@@ -235,7 +235,7 @@ static __global__ __launch_bounds__(1024) void seg_plan_kernel(const int64_t* __
   tile_ptr[R] = (int32_t)tiles;
 }
 
-constexpr int SORT_CHUNK = 4096;  // rows per counting-sort workgroup
+constexpr int SORT_CHUNK = 8192;  // rows per counting-sort workgroup
 
 // counts[b * R + g] = rows of chunk b with idx == g
 static __global__ __launch_bounds__(BLOCK) void bucket_count_kernel(const int64_t* __restrict__ idx,
@@ -254,55 +254,54 @@ static __global__ __launch_bounds__(BLOCK) void bucket_count_kernel(const int64_
   for (int64_t g = threadIdx.x; g < R; g += BLOCK) counts[blockIdx.x * R + g] = hist[g];
 }
 
-// In place: counts[b * R + g] -> position of chunk b's first row of group g
-// in the sorted order; also group_off / tile_ptr. One workgroup, groups in
-// passes of 1024 (one thread each).
-static __global__ __launch_bounds__(1024) void bucket_scan_kernel(int32_t* __restrict__ counts,
-                                                           int32_t* __restrict__ group_off,
-                                                           int32_t* __restrict__ tile_ptr,
-                                                           int64_t nblocks, int64_t R) {
-  __shared__ int64_t tot[1024];
-  __shared__ int64_t goff[1024];
-  __shared__ int64_t run_off, run_tiles;
-  if (threadIdx.x == 0) {
-    run_off = 0;
-    run_tiles = 0;
-  }
+// Per group g (one workgroup each): counts[b * R + g] over the chunks b
+// becomes the exclusive prefix (the group-local position of chunk b's first
+// row of group g); the group's total goes to totals[g]. 256 threads take
+// contiguous spans of chunks, their span sums are scanned in LDS.
+static __global__ __launch_bounds__(BLOCK) void bucket_colscan_kernel(int32_t* __restrict__ counts,
+                                                               int64_t* __restrict__ totals,
+                                                               int64_t nblocks, int64_t R) {
+  __shared__ int64_t part[BLOCK];
+  const int64_t g = blockIdx.x;
+  const int t = threadIdx.x;
+  const int64_t span = (nblocks + BLOCK - 1) / BLOCK;
+  const int64_t lo = t * span < nblocks ? t * span : nblocks;
+  const int64_t hi = lo + span < nblocks ? lo + span : nblocks;
+  int64_t s = 0;
+  for (int64_t b = lo; b < hi; ++b) s += counts[b * R + g];
+  part[t] = s;
   __syncthreads();
-  for (int64_t g0 = 0; g0 < R; g0 += 1024) {
-    const int64_t g = g0 + threadIdx.x;
-    int64_t s = 0;
-    if (g < R)
-      for (int64_t b = 0; b < nblocks; ++b) s += counts[b * R + g];
-    tot[threadIdx.x] = s;
+  for (int off = 1; off < BLOCK; off <<= 1) {
+    const int64_t add = t >= off ? part[t - off] : 0;
     __syncthreads();
-    if (threadIdx.x == 0) {
-      int64_t off = run_off, tiles = run_tiles;
-      for (int64_t q = 0; q < 1024 && g0 + q < R; ++q) {
-        goff[q] = off;
-        group_off[g0 + q] = (int32_t)off;
-        tile_ptr[g0 + q] = (int32_t)tiles;
-        off += tot[q];
-        tiles += (tot[q] + GBM - 1) / GBM;
-      }
-      run_off = off;
-      run_tiles = tiles;
-      if (g0 + 1024 >= R) {
-        group_off[R] = (int32_t)off;
-        tile_ptr[R] = (int32_t)tiles;
-      }
-    }
-    __syncthreads();
-    if (g < R) {
-      int64_t run = goff[threadIdx.x];
-      for (int64_t b = 0; b < nblocks; ++b) {
-        const int32_t c = counts[b * R + g];
-        counts[b * R + g] = (int32_t)run;
-        run += c;
-      }
-    }
+    part[t] += add;
     __syncthreads();
   }
+  int64_t run = t > 0 ? part[t - 1] : 0;
+  for (int64_t b = lo; b < hi; ++b) {
+    const int32_t c = counts[b * R + g];
+    counts[b * R + g] = (int32_t)run;
+    run += c;
+  }
+  if (t == BLOCK - 1) totals[g] = part[BLOCK - 1];
+}
+
+// group_off / tile_ptr from the group totals (one thread; R is small), and
+// the totals turned into each group's first sorted position.
+static __global__ void bucket_plan_kernel(int64_t* __restrict__ totals, int32_t* __restrict__ group_off,
+                                   int32_t* __restrict__ tile_ptr, int64_t R) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  int64_t off = 0, tiles = 0;
+  for (int64_t g = 0; g < R; ++g) {
+    const int64_t c = totals[g];
+    group_off[g] = (int32_t)off;
+    tile_ptr[g] = (int32_t)tiles;
+    totals[g] = off;
+    off += c;
+    tiles += (c + GBM - 1) / GBM;
+  }
+  group_off[R] = (int32_t)off;
+  tile_ptr[R] = (int32_t)tiles;
 }
 
 // perm[sorted position] = row, stable: rows of a group keep their order.
@@ -311,12 +310,14 @@ static __global__ __launch_bounds__(1024) void bucket_scan_kernel(int32_t* __res
 // four wavefronts are ordered through per-wavefront counts in LDS.
 static __global__ __launch_bounds__(BLOCK) void bucket_scatter_kernel(const int64_t* __restrict__ idx,
                                                                const int32_t* __restrict__ starts,
+                                                               const int64_t* __restrict__ gstart,
                                                                int32_t* __restrict__ perm,
                                                                int64_t n, int64_t R, int bits) {
   extern __shared__ int32_t sm[];
   int32_t* cursor = sm;          // R: next position per group
   int32_t* wcount = sm + R;      // 4 x R: rows per group in each wavefront of this pass
-  for (int64_t g = threadIdx.x; g < R; g += BLOCK) cursor[g] = starts[blockIdx.x * R + g];
+  for (int64_t g = threadIdx.x; g < R; g += BLOCK)
+    cursor[g] = (int32_t)(gstart[g] + starts[blockIdx.x * R + g]);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t lo = (int64_t)blockIdx.x * SORT_CHUNK;
   const int64_t hi = lo + SORT_CHUNK < n ? lo + SORT_CHUNK : n;
@@ -372,7 +373,7 @@ int64_t grouped_workspace_bytes(int64_t n, int64_t K, int64_t N, int64_t R, bool
   b += 2 * ws_align((R + 1) * 4);
   if (gather) {
     const int64_t nb = (n + SORT_CHUNK - 1) / SORT_CHUNK;
-    b += ws_align(nb * R * 4) + ws_align(n * 4);
+    b += ws_align(nb * R * 4) + ws_align(n * 4) + ws_align(R * 8);
   }
   return b;
 }
@@ -403,14 +404,19 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather) {
     int32_t* counts = reinterpret_cast<int32_t*>(w);
     w += ws_align(nb * L.R * 4);
     perm = reinterpret_cast<int32_t*>(w);
+    w += ws_align(L.n * 4);
+    int64_t* totals = reinterpret_cast<int64_t*>(w);
     int bits = 0;
     while ((int64_t(1) << bits) < L.R) ++bits;
     hipLaunchKernelGGL(bucket_count_kernel, dim3((unsigned)nb), dim3(BLOCK),
                        (size_t)(L.R * 4), L.stream, L.idx_b, counts, L.n, L.R);
-    hipLaunchKernelGGL(bucket_scan_kernel, dim3(1), dim3(1024), 0, L.stream, counts, group_off,
-                       tile_ptr, nb, L.R);
+    hipLaunchKernelGGL(bucket_colscan_kernel, dim3((unsigned)L.R), dim3(BLOCK), 0, L.stream,
+                       counts, totals, nb, L.R);
+    hipLaunchKernelGGL(bucket_plan_kernel, dim3(1), dim3(64), 0, L.stream, totals, group_off,
+                       tile_ptr, L.R);
     hipLaunchKernelGGL(bucket_scatter_kernel, dim3((unsigned)nb), dim3(BLOCK),
-                       (size_t)(5 * L.R * 4), L.stream, L.idx_b, counts, perm, L.n, L.R, bits);
+                       (size_t)(5 * L.R * 4), L.stream, L.idx_b, counts, totals, perm, L.n, L.R,
+                       bits);
   } else {
     hipLaunchKernelGGL(seg_plan_kernel, dim3(1), dim3(64), 0, L.stream, L.seglen, group_off,
                        tile_ptr, L.R);

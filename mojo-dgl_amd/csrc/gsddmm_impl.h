@@ -9,7 +9,8 @@
 //
 // dot: G lanes own one (edge, output column) pair and split the contracted
 // axis `red` between them (VEC consecutive elements per lane per step), then
-// add the G lane partials with a butterfly of __shfl_xor. The reference keeps
+// add the G lane partials with a butterfly of __shfl_xor; each wavefront
+// serves DOT_U rounds of pairs with their loads issued together. The reference keeps
 // W lane partials and reduces them once (ported.mojo:273-293), so the two
 // agree to rounding, not bit for bit.
 #pragma once
@@ -92,7 +93,30 @@ __global__ __launch_bounds__(BLOCK) void gsddmm_kernel(GsddmmArgs<T> a) {
   }
 }
 
-// dot: tasks are (edge, output column) pairs, G lanes per task.
+// dot: tasks are (edge, output column) pairs, G lanes per task. A wavefront
+// takes DOT_U rounds of 64 / G tasks; when the contracted axis fits in one
+// vector per lane (red <= G * VEC) the loads of all rounds are issued before
+// the first product, so each lane has 2 * DOT_U row loads in flight.
+constexpr int DOT_U = 4;
+
+template <class T, int VEC>
+__device__ __forceinline__ T dot_part(const T* __restrict__ l, const T* __restrict__ r,
+                                      int64_t k0, int64_t red, int64_t step) {
+  T part = T(0);
+  for (int64_t k = k0; k < red; k += step) {
+    if constexpr (VEC > 1) {
+      T xv[VEC], yv[VEC];
+      load_vec<T>(l + k, xv);
+      load_vec<T>(r + k, yv);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) part = part + xv[v] * yv[v];
+    } else {
+      part = part + l[k] * r[k];
+    }
+  }
+  return part;
+}
+
 template <class T, int VEC>
 __global__ __launch_bounds__(BLOCK) void gsddmm_dot_kernel(GsddmmArgs<T> a) {
   const int64_t blk = xcd_remap(blockIdx.x, a.num_blocks);
@@ -101,32 +125,58 @@ __global__ __launch_bounds__(BLOCK) void gsddmm_dot_kernel(GsddmmArgs<T> a) {
   if (wave >= a.num_waves) return;  // uniform per wavefront
   const int G = a.G;
   const int grp = lane / G, gl = lane % G;
-  const int64_t task = wave * (WAVE / G) + grp;
-  const bool ok = task < a.num_tasks;
-  T part = T(0);
-  int64_t e = 0, col = 0;
-  if (ok) {
-    e = task / a.dout;
-    col = task % a.dout;
-    const T* l = a.lhs + target_row(a.lt, a.uids, a.vids, e) * a.dl +
-                 bcast_off(a.bc, col, true) * a.red;
-    const T* r = a.rhs + target_row(a.rt, a.uids, a.vids, e) * a.dr +
-                 bcast_off(a.bc, col, false) * a.red;
-    for (int64_t k = (int64_t)gl * VEC; k < a.red; k += (int64_t)G * VEC) {
-      if constexpr (VEC > 1) {
-        T xv[VEC], yv[VEC];
-        load_vec<T>(l + k, xv);
-        load_vec<T>(r + k, yv);
+  const int64_t per_round = WAVE / G;
+  const int64_t k0 = (int64_t)gl * VEC;
+  int64_t task[DOT_U];
+  const T* lp[DOT_U];
+  const T* rp[DOT_U];
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) part = part + xv[v] * yv[v];
-      } else {
-        part = part + l[k] * r[k];
-      }
+  for (int u = 0; u < DOT_U; ++u) {
+    task[u] = (wave * DOT_U + u) * per_round + grp;
+    lp[u] = rp[u] = nullptr;
+    if (task[u] < a.num_tasks) {
+      const int64_t e = task[u] / a.dout, col = task[u] % a.dout;
+      lp[u] = a.lhs + target_row(a.lt, a.uids, a.vids, e) * a.dl + bcast_off(a.bc, col, true) * a.red;
+      rp[u] = a.rhs + target_row(a.rt, a.uids, a.vids, e) * a.dr + bcast_off(a.bc, col, false) * a.red;
     }
   }
+  T part[DOT_U];
+  if (a.red <= (int64_t)G * VEC) {
+    T xv[DOT_U][VEC], yv[DOT_U][VEC];
+#pragma unroll
+    for (int u = 0; u < DOT_U; ++u) {
+      if (lp[u] && k0 < a.red) {
+        if constexpr (VEC > 1) {
+          load_vec<T>(lp[u] + k0, xv[u]);
+          load_vec<T>(rp[u] + k0, yv[u]);
+        } else {
+          xv[u][0] = lp[u][k0];
+          yv[u][0] = rp[u][k0];
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) xv[u][v] = yv[u][v] = T(0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < DOT_U; ++u) {
+      T pu = T(0);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) pu = pu + xv[u][v] * yv[u][v];
+      part[u] = pu;
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < DOT_U; ++u)
+      part[u] = lp[u] ? dot_part<T, VEC>(lp[u], rp[u], k0, a.red, (int64_t)G * VEC) : T(0);
+  }
   // butterfly inside the lane group; every lane of the wavefront runs it
-  for (int off = G >> 1; off >= 1; off >>= 1) part = part + __shfl_xor(part, off);
-  if (ok && gl == 0) a.out[e * a.dout + col] = part;
+#pragma unroll
+  for (int u = 0; u < DOT_U; ++u) {
+    T pu = part[u];
+    for (int off = G >> 1; off >= 1; off >>= 1) pu = pu + __shfl_xor(pu, off);
+    if (lp[u] && gl == 0) a.out[task[u]] = pu;
+  }
 }
 
 template <class T, int VEC>
@@ -155,7 +205,8 @@ hipError_t launch_gsddmm_vec(const GsddmmParams& p) {
     a.G = G;
     a.S = 1;
     a.num_tasks = p.num_edges * p.dout;
-    a.num_waves = (a.num_tasks + (WAVE / G) - 1) / (WAVE / G);
+    const int64_t per_wave = (WAVE / G) * DOT_U;
+    a.num_waves = (a.num_tasks + per_wave - 1) / per_wave;
   } else {
     const int64_t nvec = (p.dout + VEC - 1) / VEC;
     int G = 1;

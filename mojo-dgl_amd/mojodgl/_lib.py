@@ -262,6 +262,21 @@ def i64(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.int64)
 
 
+def i64_device(a) -> torch.Tensor:
+    """Ids / lengths as a contiguous int64 GPU tensor. A GPU tensor is
+    converted where it lies (no host round trip); anything else goes through
+    `i64` and is uploaded."""
+    if isinstance(a, torch.Tensor) and a.device.type == "cuda":
+        if a.is_complex():
+            raise DGLError("node ids and segment lengths must be whole numbers, got {}".format(
+                a.dtype))
+        if a.is_floating_point() and a.numel() and bool((a != torch.floor(a)).any()):
+            raise DGLError("node ids and segment lengths must be whole numbers, got {}".format(
+                a.dtype))
+        return a.detach().to(device=device(), dtype=torch.int64).contiguous()
+    return torch.from_numpy(i64(a)).to(device())
+
+
 def i32_device(a: np.ndarray) -> torch.Tensor:
     """An int64 host index array as an int32 GPU tensor (values checked < 2**31)."""
     if a.size and (int(a.max()) >= 2 ** 31 or int(a.min()) < -2 ** 31):

@@ -53,6 +53,33 @@ class SoftmaxPlan:
             self.bounds = np.zeros(self.nbins + 2, dtype=np.int64)
             np.cumsum(counts, out=self.bounds[1:])
 
+    @classmethod
+    def natural_device(cls, indptr: torch.Tensor, num_chunks: int, slots: int, chunk_len: int):
+        """The natural-order plan from int64 GPU offsets, built on the GPU;
+        `num_chunks` (the chunks the long rows split into) is known to the
+        caller from its validation read back."""
+        self = cls.__new__(cls)
+        self.slots = int(slots)
+        self.chunk_len = int(chunk_len)
+        self.nbins = int(np.log2(slots)) + 1
+        self.num_chunks = int(num_chunks)
+        self.order = None
+        self.bounds = None
+        self.chunk_row = self.chunk_start = self.chunk_first = None
+        if self.num_chunks:
+            deg = indptr[1:] - indptr[:-1]
+            heavy = torch.nonzero(deg > chunk_len).squeeze(1)
+            per = (deg[heavy] + chunk_len - 1) // chunk_len
+            first = torch.cumsum(per, 0) - per
+            row = torch.repeat_interleave(heavy, per, output_size=self.num_chunks)
+            cfirst = torch.repeat_interleave(first, per, output_size=self.num_chunks)
+            local = torch.arange(self.num_chunks, dtype=torch.int64, device=indptr.device) - cfirst
+            start = indptr[row] + local * chunk_len
+            self.chunk_row = row.to(torch.int32)
+            self.chunk_start = start.to(torch.int32)
+            self.chunk_first = cfirst.to(torch.int32)
+        return self
+
     def bounds_ptr(self):
         return None if self.bounds is None else self.bounds.ctypes.data
 

@@ -2,8 +2,8 @@
 
 Same arguments and validation. Both of the reference's routes are kept and
 give the same numbers: above `_SEGMENT_BLOCK` (D1 * D2) the rows are sorted
-by `idx_b` on the host side of the call and multiplied with segment_mm, as
-the reference does; otherwise one mdgl_gather_mm call buckets the rows on the
+by `idx_b` (a stable sort, on the GPU) and multiplied with segment_mm, as the
+reference does; otherwise one mdgl_gather_mm call buckets the rows on the
 GPU and multiplies them block by block on the matrix cores.
 """
 
@@ -11,7 +11,6 @@ from __future__ import annotations
 
 import os
 
-import numpy as np
 import torch
 
 from .. import _lib
@@ -52,23 +51,34 @@ def gather_mm(a, b, *, idx_b):
     if b_d1 != D1:
         raise DGLError("inner dimensions do not match: a is {} wide, b blocks are {}".format(
             D1, b_d1))
-    idx = _lib.i64(idx_b)
-    if idx.ndim != 1 or idx.size != N:
+    # GPU indices are checked on the GPU (one small read back); host indices
+    # on the host, before any GPU work
+    on_gpu = isinstance(idx_b, torch.Tensor) and idx_b.device.type == "cuda"
+    idx = _lib.i64_device(idx_b) if on_gpu else _lib.i64(idx_b)
+    if idx.ndim != 1 or idx.shape[0] != N:
         raise DGLError("idx_b must be 1-D with one index per row of a: got shape {} for "
-                       "N={}".format(idx.shape, N))
-    if idx.size and (int(idx.min()) < 0 or int(idx.max()) >= R):
-        raise DGLError("idx_b must be in [0, {}), got [{}, {})".format(
-            R, int(idx.min()), int(idx.max()) + 1))
+                       "N={}".format(tuple(idx.shape), N))
+    if N:
+        if on_gpu:
+            lo, hi = torch.stack((idx.min(), idx.max())).tolist()
+        else:
+            lo, hi = int(idx.min()), int(idx.max())
+        if lo < 0 or hi >= R:
+            raise DGLError("idx_b must be in [0, {}), got [{}, {})".format(R, lo, hi + 1))
+    if not on_gpu:
+        idx = torch.from_numpy(idx).to(_lib.device())
     as_torch, dev = _lib.wants_torch(A, B), _lib.out_device(A, B)
     if D1 * D2 > _SEGMENT_BLOCK:
-        perm = np.argsort(idx, kind="stable")
-        seglen = np.bincount(idx, minlength=R).astype(np.int64)
+        # stable sort on the GPU: the same permutation as the reference's
+        # stable host argsort
+        perm = torch.sort(idx, stable=True).indices
+        seglen = torch.bincount(idx, minlength=R)
         gdev = _lib.device()
-        p = torch.from_numpy(perm).to(gdev)
-        a_sorted = _lib.on_device(A, _lib.common_dtype(A, B)).index_select(0, p)
-        out_sorted = _grouped_mm(_lib.Feat(a_sorted, True, gdev), B, None, seglen, gather=False)
+        a_sorted = _lib.on_device(A, _lib.common_dtype(A, B)).index_select(0, perm)
+        out_sorted = _grouped_mm(_lib.Feat(a_sorted, True, gdev), B, None, seglen, gather=False,
+                                 covered=N)
         out = torch.empty_like(out_sorted)
-        out.index_copy_(0, p, out_sorted)
+        out.index_copy_(0, perm, out_sorted)
     else:
-        out = _grouped_mm(A, B, idx, None, gather=True)
+        out = _grouped_mm(A, B, idx, None, gather=True, covered=N)
     return _lib.give_back(out, as_torch, dev)

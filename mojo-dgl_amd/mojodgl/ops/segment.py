@@ -2,8 +2,10 @@
 
 segment_reduce, segment_softmax and segment_mm with the reference's
 arguments, validation and empty-segment conventions; values keep their
-float32/float64 dtype. The offsets ([0] + cumsum(seglen)) are formed on the
-host, where they are validated anyway, and uploaded as int32.
+float32/float64 dtype. The offsets ([0] + cumsum(seglen)) are formed where
+the lengths live: host lengths are validated and summed on the host and
+uploaded as int32; GPU lengths stay on the GPU and are validated there with
+one small read back.
 """
 
 from __future__ import annotations
@@ -30,6 +32,51 @@ def _check_offsets(offsets, n):
         raise DGLError(
             "segment lengths must be non-negative and sum to {}, got offsets ending at {} for "
             "{} rows".format(n, int(offsets[-1]) if offsets.size else 0, n))
+
+
+class _Segments:
+    """Validated segments: `off` is the int32 GPU offsets tensor, `host` the
+    int64 host offsets when the lengths came from the host (None when they
+    were a GPU tensor, whose offsets are formed and checked on the GPU with
+    one small read back), `heavy` the number of chunks of `chunk_len` rows
+    the segments longer than `chunk_len` split into (GPU lengths only)."""
+
+    def __init__(self, seglen, n, chunk_len=None):
+        if isinstance(seglen, torch.Tensor) and seglen.device.type == "cuda":
+            sl = _lib.i64_device(seglen).reshape(-1)
+            self.num = sl.numel()
+            self.host = None
+            self.heavy = 0
+            if n >= 2 ** 31:
+                raise DGLError("segment operators take fewer than 2**31 rows, got {}".format(n))
+            if self.num:
+                stats = [sl.min(), sl.sum()]
+                if chunk_len is not None:
+                    stats.append(torch.where(sl > chunk_len, (sl + chunk_len - 1) // chunk_len,
+                                             0).sum())
+                got = torch.stack(stats).tolist()
+                if got[0] < 0 or got[1] != n:
+                    raise DGLError(
+                        "segment lengths must be non-negative and sum to {}, got offsets ending "
+                        "at {} for {} rows".format(n, got[1], n))
+                if chunk_len is not None:
+                    self.heavy = got[2]
+            off = torch.zeros(self.num + 1, dtype=torch.int64, device=sl.device)
+            torch.cumsum(sl, 0, out=off[1:])
+            self.off64 = off
+            self.off = off.to(torch.int32)
+        else:
+            sl = _lib.i64(seglen)
+            self.num = sl.size
+            self.host = _offsets(sl)
+            _check_offsets(self.host, n)
+            self.off64 = None
+            self.off = None
+
+    def device(self):
+        if self.off is None:
+            self.off = _lib.i32_device(self.host)
+        return self.off
 
 
 def _flat_width(shape):
@@ -65,22 +112,20 @@ def segment_reduce(seglen, value, reducer="sum"):
            [5., 5., 5.],
            [4., 4., 4.]])
     """
-    seglen = _lib.i64(seglen)
-    offsets = _offsets(seglen)
     V = _lib.feature(value)
     if reducer not in ("sum", "max", "min", "mean"):
         raise DGLError("reducer {} not recognized.".format(reducer))
     n = V.shape[0] if V.ndim else 0
-    _check_offsets(offsets, n)
+    seg = _Segments(seglen, n)
     d = _flat_width(V.shape)
     fshape = tuple(V.shape[1:]) if V.ndim > 1 else (1,)
-    num_seg = seglen.size
+    num_seg = seg.num
     dtype = V.dtype
     gdev = _lib.device()
     out = torch.empty((num_seg, d), dtype=_lib.torch_dtype(dtype), device=gdev)
     if num_seg and d:
         val = _lib.on_device(V, dtype)
-        off = _lib.i32_device(offsets)
+        off = seg.device()
         flags = _lib.REPLACE_INF if reducer in ("max", "min") else 0
         rc = _lib.lib().mdgl_segment_reduce(off.data_ptr(), val.data_ptr(), out.data_ptr(),
                                             num_seg, d, REDUCERS[reducer], n, flags,
@@ -100,22 +145,30 @@ def segment_softmax(seglen, value):
     -------
     Result of the same shape as ``value``.
     """
-    seglen = _lib.i64(seglen)
     V = _lib.feature(value)
     shape = V.shape
     n = shape[0] if len(shape) else 0
     d = _flat_width(shape)
-    offsets = _offsets(seglen)
-    _check_offsets(offsets, n)
-    num_seg = seglen.size
     dtype = V.dtype
+    on_gpu = isinstance(seglen, torch.Tensor) and seglen.device.type == "cuda"
+    if not on_gpu:
+        seg = _Segments(seglen, n)  # host lengths: checked before any GPU work
     gdev = _lib.device()
-    out = torch.zeros((n, d), dtype=_lib.torch_dtype(dtype), device=gdev)
-    if num_seg and n and d:
-        val = _lib.on_device(V, dtype).reshape(n, d)
-        off = _lib.i32_device(offsets)
+    # every row lies in one segment, so the kernel writes all of `out`
+    out = torch.empty((n, d), dtype=_lib.torch_dtype(dtype), device=gdev)
+    val = _lib.on_device(V, dtype).reshape(n, d) if n and d else None
+    slots = chunk_len = None
+    if val is not None:
         slots, chunk_len = _plan.geometry(d, dtype, val, out)
-        plan = _plan.SoftmaxPlan(offsets, slots, chunk_len, ordered=False)
+    if on_gpu:
+        seg = _Segments(seglen, n, chunk_len)
+    num_seg = seg.num
+    if num_seg and n and d:
+        off = seg.device()
+        if seg.host is not None:
+            plan = _plan.SoftmaxPlan(seg.host, slots, chunk_len, ordered=False)
+        else:
+            plan = _plan.SoftmaxPlan.natural_device(seg.off64, seg.heavy, slots, chunk_len)
         ws, nbytes = _plan.workspace(plan, d, dtype)
         rc = _lib.lib().mdgl_segment_softmax(
             off.data_ptr(), val.data_ptr(), out.data_ptr(), None, num_seg, d, n,
@@ -126,15 +179,19 @@ def segment_softmax(seglen, value):
     return _lib.give_back(out.reshape(shape), V.is_torch, V.device)
 
 
-def _grouped_mm(a, b, idx_b, seglen, gather):
-    """Launch the grouped GEMM; returns the (n, d2) GPU tensor."""
+def _grouped_mm(a, b, idx_b, seglen, gather, covered):
+    """Launch the grouped GEMM; returns the (n, d2) GPU tensor. The kernel
+    writes the first `covered` rows (every row of a group); the rest are
+    zeroed here."""
     n, d1 = a.shape
     r, _, d2 = b.shape
     dtype = _lib.common_dtype(a, b)
     gdev = _lib.device()
     tdt = _lib.torch_dtype(dtype)
-    out = torch.zeros((n, d2), dtype=tdt, device=gdev)
-    if n == 0 or d2 == 0:
+    out = torch.empty((n, d2), dtype=tdt, device=gdev)
+    if covered < n:
+        out[covered:].zero_()
+    if covered == 0 or d2 == 0:
         return out
     A = _lib.on_device(a, dtype)
     B = _lib.on_device(b, dtype)
@@ -146,7 +203,7 @@ def _grouped_mm(a, b, idx_b, seglen, gather):
         nbytes = L.mdgl_segment_mm_workspace_bytes(n, d1, d2, r, code)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=gdev)
     if gather:
-        idx = torch.as_tensor(idx_b, dtype=torch.int64).to(gdev).contiguous()
+        idx = idx_b
         rc = L.mdgl_gather_mm(A.data_ptr(), B.data_ptr(), idx.data_ptr(), out.data_ptr(), n, d1,
                               d2, r, ws.data_ptr(), nbytes, code, _lib.stream())
         _lib.check(rc, "gather_mm")
@@ -196,7 +253,7 @@ def segment_mm(a, b, seglen_a):
             raise DGLError(
                 "segment lengths must be non-negative and sum to {}, got a minimum of {} and a "
                 "sum of {}".format(n, lo, total))
-    out = _grouped_mm(A, B, None, seglen_a, gather=False)
+    out = _grouped_mm(A, B, None, seglen_a, gather=False, covered=total if r else 0)
     return _lib.give_back(out, _lib.wants_torch(A, B), _lib.out_device(A, B))
 
 

@@ -295,6 +295,45 @@ def test_segment_softmax(dtype, d):
     close(got, ref, ref, dtype, "segment_softmax")
 
 
+@pytest.mark.parametrize("reducer", ["sum", "max", "mean"])
+def test_segment_reduce_gpu_lengths(reducer):
+    """Lengths given as a GPU tensor: offsets formed and checked on the GPU."""
+    rng = np.random.default_rng(40)
+    seglen = rng.poisson(9, 700)
+    seglen[::7] = 0
+    value = rng.normal(size=(int(seglen.sum()), 5)).astype(np.float32)
+    got = ops.segment_reduce(torch.from_numpy(seglen).cuda(), torch.from_numpy(value).cuda(),
+                             reducer)
+    assert isinstance(got, torch.Tensor) and got.is_cuda
+    np.testing.assert_array_equal(got.cpu().numpy(),
+                                  oracle.segment_reduce(seglen, value, reducer, np.float32))
+
+
+@pytest.mark.parametrize("d", [1, 16])
+def test_segment_softmax_gpu_lengths_with_long_segments(d):
+    """GPU lengths, with segments long enough to be split into chunks."""
+    rng = np.random.default_rng(41)
+    seglen = rng.poisson(12, 900)
+    seglen[::17] = 0
+    seglen[[3, 400, 899]] = [5000, 1300, 2049]
+    value = (rng.normal(size=(int(seglen.sum()), d)) * 2).astype(np.float32)
+    got = ops.segment_softmax(torch.from_numpy(seglen).cuda(), torch.from_numpy(value).cuda())
+    ref = oracle.segment_softmax(seglen, value, np.float64)
+    close(got.cpu().numpy(), ref, ref, np.float32, "segment_softmax gpu lengths")
+    host = ops.segment_softmax(seglen, value)
+    np.testing.assert_array_equal(got.cpu().numpy(), host)
+
+
+def test_segment_gpu_lengths_are_validated():
+    value = torch.ones(10, 2, device="cuda")
+    for bad in ([3, 3, 3], [12, -2], [4.5, 5.5]):
+        t = torch.tensor(bad, device="cuda")
+        with pytest.raises(dgl.DGLError):
+            ops.segment_reduce(t, value, "sum")
+        with pytest.raises(dgl.DGLError):
+            ops.segment_softmax(t, value)
+
+
 # ------------------------------------------------------------------ dense
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("d1,d2,r", [(128, 128, 64), (5, 3, 7), (16, 16, 4), (33, 130, 3),
@@ -319,6 +358,45 @@ def test_gather_mm_routes_agree(monkeypatch):
     fused = ops.gather_mm(a, b, idx_b=idx)
     monkeypatch.setattr(importlib.import_module("mojodgl.ops.gather_mm"), "_SEGMENT_BLOCK", 0)
     np.testing.assert_array_equal(ops.gather_mm(a, b, idx_b=idx), fused)
+
+
+@pytest.mark.parametrize("block", [None, 0], ids=["bucketed", "sorted"])
+def test_gather_mm_gpu_indices(block, monkeypatch):
+    """idx_b as a GPU tensor (checked on the GPU) on both routes."""
+    if block is not None:
+        monkeypatch.setattr(importlib.import_module("mojodgl.ops.gather_mm"), "_SEGMENT_BLOCK",
+                            block)
+    rng = np.random.default_rng(42)
+    a = rng.normal(size=(20000, 32)).astype(np.float32)
+    b = (rng.normal(size=(300, 32, 24)) / 6).astype(np.float32)
+    idx = rng.integers(0, 300, 20000)
+    got = ops.gather_mm(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda(),
+                        idx_b=torch.from_numpy(idx).cuda())
+    ref = oracle.gather_mm(a, b, idx, np.float64)
+    bound = oracle.gather_mm(np.abs(a), np.abs(b), idx, np.float64)
+    close(got.cpu().numpy(), ref, bound, np.float32, "gather_mm gpu idx")
+    np.testing.assert_array_equal(got.cpu().numpy(), ops.gather_mm(a, b, idx_b=idx))
+    bad = torch.from_numpy(idx).cuda()
+    bad[7] = 300
+    with pytest.raises(dgl.DGLError):
+        ops.gather_mm(a, b, idx_b=bad)
+    with pytest.raises(dgl.DGLError):
+        ops.gather_mm(a, b, idx_b=bad[:-1])
+
+
+def test_gather_mm_many_sort_chunks():
+    """More row chunks than the bucketing scan has threads (several per thread)."""
+    rng = np.random.default_rng(43)
+    n = 2_600_000
+    a = rng.normal(size=(n, 4)).astype(np.float32)
+    b = rng.normal(size=(37, 4, 3)).astype(np.float32)
+    idx = rng.integers(0, 37, n)
+    idx[: n // 2] = np.sort(idx[: n // 2])  # long runs of one block as well as mixed rows
+    got = ops.gather_mm(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda(),
+                        idx_b=torch.from_numpy(idx).cuda()).cpu().numpy()
+    ref = oracle.gather_mm(a, b, idx, np.float64)
+    bound = oracle.gather_mm(np.abs(a), np.abs(b), idx, np.float64)
+    close(got, ref, bound, np.float32, "gather_mm many chunks")
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
