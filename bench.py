@@ -202,9 +202,38 @@ def workload_gat(args):
         "breakdown_ms": breakdown,
         "kernels": kernels,
     }
+    result["graph_build"] = time_graph_build(g, u, v, N, args)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_gat(g, el, er, h, args)
     return result
+
+
+def time_graph_build(g, u, v, N, args):
+    """The in-CSR build (not part of a step): on the GPU from the resident
+    int32 endpoints (mdgl_build_csr, HIP events, average of 3), and the
+    reference's host method (numpy bincount / cumsum / stable argsort, once)."""
+    import torch
+
+    from mojodgl.heterograph import build_device_csr
+
+    ud, vd = g._device_coo()
+    build_device_csr(vd, ud, N)
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    t = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(3):
+        build_device_csr(vd, ud, N)
+    t.record()
+    torch.cuda.synchronize()
+    out = {"gpu_ms": round(s.elapsed_time(t) / 3, 3)}
+    if not args.no_cpu_baseline:
+        import oracle
+
+        t0 = time.perf_counter()
+        oracle.csr(u, v, N, "dst")
+        out["host_numpy_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
+    return out
 
 
 def cpu_baseline_gat(g, el, er, h, args):

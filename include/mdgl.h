@@ -183,6 +183,20 @@ int mdgl_gather_mm(const void* a, const void* b, const int64_t* idx_b, void* dst
                    int dtype, void* stream);
 int64_t mdgl_gather_mm_workspace_bytes(int64_t n, int64_t d1, int64_t d2, int64_t r, int dtype);
 
+/* Graph build: replaces DGLGraph._build_csr (python/mojodgl/heterograph.py:69-86),
+ * which the reference runs in numpy on the host. Groups the edges 0..num_edges-1
+ * (COO in edge-id order, int32 on the GPU) by `key` (v for the in-CSR, u for
+ * the out-CSR; values in [0, num_rows), not checked here):
+ *   indptr  (num_rows + 1) = [0] + cumsum(bincount(key)),
+ *   eid     (num_edges)    = argsort(key, stable): inside a row, increasing edge id,
+ *   indices (num_edges)    = other[eid].
+ * Bit-identical to the numpy build. Workspace: mdgl_build_csr_workspace_bytes
+ * (0 when num_rows <= 1 or there are no edges; null is then accepted). */
+int mdgl_build_csr(const int32_t* key, const int32_t* other, int64_t num_edges, int64_t num_rows,
+                   int32_t* indptr, int32_t* indices, int32_t* eid, void* workspace,
+                   int64_t workspace_bytes, void* stream);
+int64_t mdgl_build_csr_workspace_bytes(int64_t num_edges, int64_t num_rows);
+
 #ifdef __cplusplus
 }
 #endif

@@ -155,6 +155,30 @@ int mdgl_cumsum(const int64_t* src, int64_t* dst, int64_t n, void* stream) {
   return hip_status(launch_cumsum_i64(src, dst, n, (hipStream_t)stream), "cumsum");
 }
 
+int64_t mdgl_build_csr_workspace_bytes(int64_t num_edges, int64_t num_rows) {
+  if (num_edges < 0 || num_rows < 0) return -1;
+  return csr_workspace_bytes(num_edges, num_rows);
+}
+
+int mdgl_build_csr(const int32_t* key, const int32_t* other, int64_t num_edges, int64_t num_rows,
+                   int32_t* indptr, int32_t* indices, int32_t* eid, void* workspace,
+                   int64_t workspace_bytes, void* stream) {
+  if (num_edges < 0 || num_rows < 0) return fail(MDGL_EINVAL, "build_csr: negative size");
+  if (num_edges >= (int64_t(1) << 31) || num_rows >= (int64_t(1) << 31))
+    return fail(MDGL_EINVAL, "build_csr: 2**31 or more edges or rows");
+  if (num_edges > 0 && num_rows == 0)
+    return fail(MDGL_EINVAL, "build_csr: edges but no rows");
+  if (!indptr || (num_edges > 0 && (!key || !other || !indices || !eid)))
+    return fail(MDGL_EINVAL, "build_csr: null buffer");
+  const int64_t need = csr_workspace_bytes(num_edges, num_rows);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(MDGL_EWORKSPACE, "build_csr: workspace of %lld bytes needed, %lld given",
+                (long long)need, (long long)workspace_bytes);
+  return hip_status(launch_build_csr(key, other, num_edges, num_rows, indptr, indices, eid,
+                                     workspace, (hipStream_t)stream),
+                    "build_csr");
+}
+
 int mdgl_replace_inf_with_zero(const void* src, void* dst, int64_t n, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "replace_inf_with_zero: bad dtype %d", dtype);
   if (n < 0) return fail(MDGL_EINVAL, "replace_inf_with_zero: n must be >= 0");

@@ -1,0 +1,241 @@
+// Graph build on the GPU: COO (edge-id order) -> CSR grouped by one endpoint,
+// the reference's DGLGraph._build_csr (python/mojodgl/heterograph.py:69-86):
+// indptr = [0] + cumsum(bincount(key)), order = argsort(key, stable),
+// indices = other[order].
+//
+// The stable argsort is an LSD radix sort of (key, edge id) pairs, 8-bit
+// digits, as many passes as the node count needs (3 up to 16M nodes). Each
+// pass is three kernels: per-chunk digit counts (LDS histogram), a column
+// scan per digit over the chunks, and a scatter in which each workgroup walks
+// its chunk in order and ranks equal digits inside a wavefront with ballots,
+// so equal keys keep their input order. Every step is integer counting, so
+// the result is the numpy stable argsort bit for bit. indptr then comes from
+// the sorted keys (row r starts at the first slot whose key is >= r) and the
+// indices from one gather.
+#include "mdgl_kernels.h"
+
+namespace mdgl {
+
+namespace {
+
+constexpr int RADIX = 256;          // digit values; one thread each in a workgroup
+constexpr int RADIX_CHUNK = 4096;   // keys per workgroup per pass
+static_assert(RADIX == BLOCK, "one thread per digit value");
+
+__device__ __forceinline__ int digit_of(int32_t key, int shift) {
+  return (int)(((uint32_t)key >> shift) & (RADIX - 1));
+}
+
+// counts[b * RADIX + d] = keys of chunk b whose digit is d
+__global__ __launch_bounds__(BLOCK) void radix_count_kernel(const int32_t* __restrict__ keys,
+                                                            int64_t n, int shift,
+                                                            int32_t* __restrict__ counts) {
+  __shared__ int32_t hist[RADIX];
+  hist[threadIdx.x] = 0;
+  __syncthreads();
+  const int64_t lo = (int64_t)blockIdx.x * RADIX_CHUNK;
+  const int64_t hi = lo + RADIX_CHUNK < n ? lo + RADIX_CHUNK : n;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += BLOCK)
+    atomicAdd(&hist[digit_of(keys[i], shift)], 1);
+  __syncthreads();
+  counts[blockIdx.x * RADIX + threadIdx.x] = hist[threadIdx.x];
+}
+
+// One workgroup per digit d: counts[b * RADIX + d] becomes the exclusive
+// prefix over chunks b (the digit-local position of chunk b's first key of
+// digit d) and totals[d] the digit's count. Threads take contiguous spans of
+// chunks; span sums are scanned in LDS.
+__global__ __launch_bounds__(BLOCK) void radix_colscan_kernel(int32_t* __restrict__ counts,
+                                                              int32_t* __restrict__ totals,
+                                                              int64_t nchunks) {
+  __shared__ int32_t part[BLOCK];
+  const int64_t d = blockIdx.x;
+  const int t = threadIdx.x;
+  const int64_t span = (nchunks + BLOCK - 1) / BLOCK;
+  const int64_t lo = t * span < nchunks ? t * span : nchunks;
+  const int64_t hi = lo + span < nchunks ? lo + span : nchunks;
+  int32_t s = 0;
+  for (int64_t b = lo; b < hi; ++b) s += counts[b * RADIX + d];
+  part[t] = s;
+  __syncthreads();
+  for (int off = 1; off < BLOCK; off <<= 1) {
+    const int32_t add = t >= off ? part[t - off] : 0;
+    __syncthreads();
+    part[t] += add;
+    __syncthreads();
+  }
+  int32_t run = t > 0 ? part[t - 1] : 0;
+  for (int64_t b = lo; b < hi; ++b) {
+    const int32_t c = counts[b * RADIX + d];
+    counts[b * RADIX + d] = run;
+    run += c;
+  }
+  if (t == BLOCK - 1) totals[d] = part[BLOCK - 1];
+}
+
+// Stable scatter of chunk b: key i goes to digit_start[d] + counts[b][d] +
+// (keys of digit d before it in the chunk). vals_in null means the edge ids
+// 0..n-1 (the first pass).
+__global__ __launch_bounds__(BLOCK) void radix_scatter_kernel(
+    const int32_t* __restrict__ keys_in, const int32_t* __restrict__ vals_in,
+    int32_t* __restrict__ keys_out, int32_t* __restrict__ vals_out,
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ totals, int64_t n,
+    int shift) {
+  __shared__ int32_t cursor[RADIX];
+  __shared__ int32_t wcount[WAVES_PER_BLOCK][RADIX];
+  __shared__ int32_t scan[RADIX];
+  const int t = threadIdx.x;
+  // digit starts: exclusive scan of the totals
+  scan[t] = totals[t];
+  __syncthreads();
+  for (int off = 1; off < RADIX; off <<= 1) {
+    const int32_t add = t >= off ? scan[t - off] : 0;
+    __syncthreads();
+    scan[t] += add;
+    __syncthreads();
+  }
+  cursor[t] = scan[t] - totals[t] + counts[blockIdx.x * RADIX + t];
+  const int lane = t & (WAVE - 1), w = t >> 6;
+  const uint64_t below = lane ? (~uint64_t(0) >> (64 - lane)) : 0;
+  const int64_t lo = (int64_t)blockIdx.x * RADIX_CHUNK;
+  const int64_t hi = lo + RADIX_CHUNK < n ? lo + RADIX_CHUNK : n;
+  __syncthreads();
+  for (int64_t base = lo; base < hi; base += BLOCK) {
+#pragma unroll
+    for (int q = 0; q < WAVES_PER_BLOCK; ++q) wcount[q][t] = 0;
+    __syncthreads();
+    const int64_t i = base + t;
+    const bool ok = i < hi;
+    int32_t key = 0, val = 0;
+    if (ok) {
+      key = keys_in[i];
+      val = vals_in ? vals_in[i] : (int32_t)i;
+    }
+    const int dg = digit_of(key, shift);
+    uint64_t same = __ballot(ok);
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+      const uint64_t ones = __ballot(ok && ((dg >> bit) & 1));
+      same &= ((dg >> bit) & 1) ? ones : ~ones;  // lanes whose digit agrees on this bit
+    }
+    const int rank = __popcll(same & below);
+    if (ok && rank == 0) wcount[w][dg] = __popcll(same);
+    __syncthreads();
+    if (ok) {
+      int32_t pos = cursor[dg] + rank;
+      for (int q = 0; q < w; ++q) pos += wcount[q][dg];
+      keys_out[pos] = key;
+      vals_out[pos] = val;
+    }
+    __syncthreads();
+    int32_t add = 0;
+#pragma unroll
+    for (int q = 0; q < WAVES_PER_BLOCK; ++q) add += wcount[q][t];
+    cursor[t] += add;
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(BLOCK) void iota_kernel(int32_t* __restrict__ out, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * BLOCK)
+    out[i] = (int32_t)i;
+}
+
+// indptr[r] = first slot whose key is >= r, for r in [0, num_rows]: slot i
+// writes the rows in (key[i-1], key[i]]; the thread for i == n closes the
+// rows after the last key.
+__global__ __launch_bounds__(BLOCK) void indptr_kernel(const int32_t* __restrict__ skeys,
+                                                       int64_t n, int64_t num_rows,
+                                                       int32_t* __restrict__ indptr) {
+  const int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
+  if (i > n) return;
+  int64_t k = i < n ? (int64_t)skeys[i] : num_rows;
+  int64_t prev = i > 0 ? (int64_t)skeys[i - 1] : -1;
+  if (k > num_rows) k = num_rows;
+  if (prev > num_rows) prev = num_rows;
+  for (int64_t r = prev + 1; r <= k; ++r) indptr[r] = (int32_t)i;
+}
+
+__global__ __launch_bounds__(BLOCK) void gather_i32_kernel(const int32_t* __restrict__ src,
+                                                           const int32_t* __restrict__ idx,
+                                                           int32_t* __restrict__ out, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * BLOCK)
+    out[i] = src[idx[i]];
+}
+
+unsigned grid_of(int64_t n) {
+  int64_t b = (n + BLOCK - 1) / BLOCK;
+  if (b > 65536) b = 65536;
+  return (unsigned)(b < 1 ? 1 : b);
+}
+
+int radix_passes(int64_t num_rows) {
+  int bits = 0;
+  while ((int64_t(1) << bits) < num_rows) ++bits;
+  return (bits + 7) / 8;
+}
+
+int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
+
+}  // namespace
+
+int64_t csr_workspace_bytes(int64_t num_edges, int64_t num_rows) {
+  if (radix_passes(num_rows) == 0 || num_edges == 0) return 0;
+  const int64_t nchunks = (num_edges + RADIX_CHUNK - 1) / RADIX_CHUNK;
+  return align256(nchunks * RADIX * 4) + align256(RADIX * 4) + 3 * align256(num_edges * 4);
+}
+
+hipError_t launch_build_csr(const int32_t* key, const int32_t* other, int64_t num_edges,
+                            int64_t num_rows, int32_t* indptr, int32_t* indices, int32_t* eid,
+                            void* workspace, hipStream_t stream) {
+  const int passes = num_edges ? radix_passes(num_rows) : 0;
+  const int32_t* sorted_keys = key;
+  if (passes == 0) {
+    // at most one row: every key is 0, the order is the identity
+    if (num_edges)
+      hipLaunchKernelGGL(iota_kernel, dim3(grid_of(num_edges)), dim3(BLOCK), 0, stream, eid,
+                         num_edges);
+  } else {
+    const int64_t nchunks = (num_edges + RADIX_CHUNK - 1) / RADIX_CHUNK;
+    char* w = static_cast<char*>(workspace);
+    int32_t* counts = reinterpret_cast<int32_t*>(w);
+    w += align256(nchunks * RADIX * 4);
+    int32_t* totals = reinterpret_cast<int32_t*>(w);
+    w += align256(RADIX * 4);
+    int32_t* keys_buf[2];
+    keys_buf[0] = reinterpret_cast<int32_t*>(w);
+    w += align256(num_edges * 4);
+    keys_buf[1] = reinterpret_cast<int32_t*>(w);
+    w += align256(num_edges * 4);
+    int32_t* vals_tmp = reinterpret_cast<int32_t*>(w);
+    const int32_t* kin = key;
+    const int32_t* vin = nullptr;
+    for (int p = 0; p < passes; ++p) {
+      const int shift = 8 * p;
+      int32_t* kout = keys_buf[p & 1];
+      // the last pass lands in eid
+      int32_t* vout = ((passes - 1 - p) % 2 == 0) ? eid : vals_tmp;
+      hipLaunchKernelGGL(radix_count_kernel, dim3((unsigned)nchunks), dim3(BLOCK), 0, stream,
+                         kin, num_edges, shift, counts);
+      hipLaunchKernelGGL(radix_colscan_kernel, dim3(RADIX), dim3(BLOCK), 0, stream, counts,
+                         totals, nchunks);
+      hipLaunchKernelGGL(radix_scatter_kernel, dim3((unsigned)nchunks), dim3(BLOCK), 0, stream,
+                         kin, vin, kout, vout, counts, totals, num_edges, shift);
+      kin = kout;
+      vin = vout;
+    }
+    sorted_keys = kin;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(indptr_kernel, dim3((unsigned)((num_edges + 1 + BLOCK - 1) / BLOCK)),
+                     dim3(BLOCK), 0, stream, sorted_keys, num_edges, num_rows, indptr);
+  if (num_edges)
+    hipLaunchKernelGGL(gather_i32_kernel, dim3(grid_of(num_edges)), dim3(BLOCK), 0, stream,
+                       other, eid, indices, num_edges);
+  return hipGetLastError();
+}
+
+}  // namespace mdgl

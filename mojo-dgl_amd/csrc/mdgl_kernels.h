@@ -126,6 +126,11 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather);
 hipError_t launch_replace_inf(const void* src, void* dst, int64_t n, int dtype, hipStream_t s);
 hipError_t launch_clamp_i64(const int64_t* src, int64_t* dst, int64_t n, int64_t lo, int64_t hi,
                             hipStream_t s);
+// COO -> CSR by `key` (csr.hip).
+int64_t csr_workspace_bytes(int64_t num_edges, int64_t num_rows);
+hipError_t launch_build_csr(const int32_t* key, const int32_t* other, int64_t num_edges,
+                            int64_t num_rows, int32_t* indptr, int32_t* indices, int32_t* eid,
+                            void* workspace, hipStream_t stream);
 hipError_t launch_cumsum_i64(const int64_t* src, int64_t* dst, int64_t n, hipStream_t s);
 
 }  // namespace mdgl

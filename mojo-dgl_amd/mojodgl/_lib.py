@@ -78,6 +78,8 @@ _SIGNATURES = {
     "mdgl_segment_mm_workspace_bytes": ([_I64, _I64, _I64, _I64, _C], _I64),
     "mdgl_gather_mm": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _C, _P], _C),
     "mdgl_gather_mm_workspace_bytes": ([_I64, _I64, _I64, _I64, _C], _I64),
+    "mdgl_build_csr": ([_P, _P, _I64, _I64, _P, _P, _P, _P, _I64, _P], _C),
+    "mdgl_build_csr_workspace_bytes": ([_I64, _I64], _I64),
 }
 
 

@@ -2,11 +2,14 @@
 python/mojodgl/heterograph.py).
 
 Edges keep the order they were given. The two CSR views (by destination for
-gspmm / edge_softmax(dst), by source for edge_softmax(src)) are built the
-reference's way -- bincount, cumsum, stable argsort by endpoint
+gspmm / edge_softmax(dst), by source for edge_softmax(src)) are the
+reference's -- bincount, cumsum, stable argsort by endpoint
 (heterograph.py:69-86), so inside a row the slots are in edge-id order, which
-fixes the fold order and the max/min tie order -- once per graph and only
-when first needed. Their GPU copies (int32) are cached with two schedules:
+fixes the fold order and the max/min tie order -- built once per graph and
+only when first needed, on the GPU (mdgl_build_csr, a stable radix sort) from
+the int32 edge endpoints. Host queries read that build back; with no GPU
+build yet they sort on the host the reference's way. The GPU CSRs are cached
+with two schedules:
 
 * gspmm: rows longer than CHUNK_LEN are split into CHUNK_LEN-slot chunks
   whose partials are folded in order, so a power-law hub is spread over
@@ -84,15 +87,32 @@ class _Chunks:
         self.heavy_ptr = _lib.i32_device(ptr)
 
 
-class _DeviceCSR:
-    """A CSR view on the GPU (int32) with its gspmm and softmax schedules."""
+def build_device_csr(key: torch.Tensor, other: torch.Tensor, num_rows: int):
+    """COO -> CSR grouped by `key` on the GPU (int32 tensors in edge-id order):
+    (indptr, indices, eid) int32 GPU tensors, the reference's bincount /
+    cumsum / stable argsort (heterograph.py:69-86) bit for bit."""
+    dev = _lib.device()
+    E = int(key.numel())
+    L = _lib.lib()
+    indptr = torch.empty(num_rows + 1, dtype=torch.int32, device=dev)
+    indices = torch.empty(E, dtype=torch.int32, device=dev)
+    eid = torch.empty(E, dtype=torch.int32, device=dev)
+    nbytes = L.mdgl_build_csr_workspace_bytes(E, num_rows)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes > 0 else None
+    rc = L.mdgl_build_csr(key.data_ptr(), other.data_ptr(), E, num_rows, indptr.data_ptr(),
+                          indices.data_ptr(), eid.data_ptr(), _lib.ptr(ws), max(nbytes, 0),
+                          _lib.stream())
+    _lib.check(rc, "build_csr")
+    return indptr, indices, eid
 
-    def __init__(self, indptr, indices, order, chunk_len):
-        self.host_indptr = indptr
-        self.indptr = _lib.i32_device(indptr)
-        self.indices = _lib.i32_device(indices)
-        self.eid = _lib.i32_device(order)
-        self.chunks = _Chunks(indptr, chunk_len)
+
+class _DeviceCSR:
+    """A CSR view on the GPU (int32) with its gspmm and softmax schedules;
+    the host keeps indptr (int64) for the schedules."""
+
+    def __init__(self, arrays, chunk_len):
+        self.host_indptr, self.indptr, self.indices, self.eid = arrays
+        self.chunks = _Chunks(self.host_indptr, chunk_len)
         self.params = int(chunk_len)
         self._softmax = {}
 
@@ -130,6 +150,7 @@ class DGLGraph(object):
         self.ndata = FeatureDict(self._nstore, self._num_nodes, "ndata")
         self.edata = FeatureDict(self._estore, len(u), "edata")
         self._csr = {}
+        self._draw = {}
         self._dcsr = {}
         self._dcoo = None
 
@@ -144,7 +165,14 @@ class DGLGraph(object):
 
     def _host_csr(self, kind):
         if kind not in self._csr:
-            self._build(kind)
+            raw = self._draw.get(kind)
+            if raw is not None:
+                # read back the GPU build rather than sorting again on the host
+                indptr, indices, eid = raw[0], raw[2].cpu().numpy(), raw[3].cpu().numpy()
+                self._csr[kind] = (indptr, indices.astype(np.int64), eid.astype(np.int64),
+                                   np.diff(indptr))
+            else:
+                self._build(kind)
         return self._csr[kind]
 
     def _edge_arrays(self):
@@ -160,14 +188,25 @@ class DGLGraph(object):
         if self._u.size >= 2 ** 31 or self._num_nodes >= 2 ** 31:
             raise DGLError("graphs with 2**31 or more nodes or edges are not supported on the GPU")
 
+    def _device_raw(self, kind):
+        """(host int64 indptr, GPU indptr, indices, eid) of the in ("in") or
+        out ("out") CSR, built once on the GPU from the edge endpoints."""
+        raw = self._draw.get(kind)
+        if raw is None:
+            u, v = self._device_coo()
+            key, other = (v, u) if kind == "in" else (u, v)
+            indptr, indices, eid = build_device_csr(key, other, self._num_nodes)
+            host = indptr.cpu().numpy().astype(np.int64)
+            raw = (host, indptr, indices, eid)
+            self._draw[kind] = raw
+        return raw
+
     def _device_csr(self, kind):
-        """The GPU copy of the in ("in") or out ("out") CSR, built once."""
-        self._check_int32()
+        """The GPU CSR of `kind` with the schedules for the current CHUNK_LEN."""
         params = int(CHUNK_LEN)
         cached = self._dcsr.get(kind)
         if cached is None or cached.params != params:
-            indptr, indices, order, _ = self._host_csr(kind)
-            cached = _DeviceCSR(indptr, indices, order, params)
+            cached = _DeviceCSR(self._device_raw(kind), params)
             self._dcsr[kind] = cached
         return cached
 

@@ -88,6 +88,22 @@ def test_empty_problems_are_no_ops(lib):
     assert lib.mdgl_cumsum(None, None, 0, None) == 0
 
 
+def test_build_csr_arguments(lib):
+    assert lib.mdgl_build_csr(None, None, -1, 4, None, None, None, None, 0, None) == -1
+    assert lib.mdgl_build_csr(None, None, 2 ** 31, 4, None, None, None, None, 0, None) == -1
+    rc = lib.mdgl_build_csr(None, None, 5, 0, None, None, None, None, 0, None)
+    assert rc == -1 and "no rows" in err(lib)
+    rc = lib.mdgl_build_csr(None, None, 5, 300, None, None, None, None, 0, None)
+    assert rc == -1 and "null" in err(lib)
+    rc = lib.mdgl_build_csr(8, 8, 5, 300, 8, 8, 8, None, 0, None)
+    assert rc == -2 and "workspace" in err(lib)
+    # one row or no edges: no workspace and no sort
+    assert lib.mdgl_build_csr_workspace_bytes(1000, 1) == 0
+    assert lib.mdgl_build_csr_workspace_bytes(0, 1000) == 0
+    assert lib.mdgl_build_csr_workspace_bytes(1000, 300) >= 3 * 1000 * 4
+    assert lib.mdgl_build_csr_workspace_bytes(-1, 3) == -1
+
+
 def test_workspace_sizes(lib):
     assert lib.mdgl_gspmm_workspace_bytes(0, 64, 0, 0) == 0
     assert lib.mdgl_gspmm_workspace_bytes(10, 64, 0, 0) >= 10 * 64 * 4

@@ -413,6 +413,54 @@ def test_segment_mm(dtype):
     assert np.all(np.asarray(got)[5000:] == 0)
 
 
+# ------------------------------------------------------------------ graph build
+def _csr_cases():
+    rng = np.random.default_rng(44)
+    hub = np.concatenate([np.zeros(30000, dtype=np.int64), rng.integers(0, 70000, 40000)])
+    rng.shuffle(hub)
+    return [
+        ("empty", 0, np.zeros(0, np.int64), np.zeros(0, np.int64)),
+        ("no edges", 7, np.zeros(0, np.int64), np.zeros(0, np.int64)),
+        ("one node", 1, np.zeros(50, np.int64), np.zeros(50, np.int64)),
+        ("256 nodes", 256, rng.integers(0, 256, 10000), rng.integers(0, 256, 10000)),
+        ("257 nodes", 257, rng.integers(0, 257, 10000), rng.integers(0, 257, 10000)),
+        ("65536 nodes", 65536, rng.integers(0, 65536, 300000), rng.integers(0, 65536, 300000)),
+        ("65537 nodes", 65537, rng.integers(0, 65537, 300000), rng.integers(0, 65537, 300000)),
+        ("hub", 70000, rng.integers(0, 70000, hub.size), hub),
+        ("descending", 5000, np.arange(20000) % 5000, (19999 - np.arange(20000)) // 4),
+        ("ends only", 1 << 20, rng.integers(0, 1 << 20, 9000),
+         np.where(rng.random(9000) < 0.5, 0, (1 << 20) - 1)),
+        ("17M nodes", (1 << 24) + 5, rng.integers(0, (1 << 24) + 5, 200000),
+         rng.integers(0, (1 << 24) + 5, 200000)),
+    ]
+
+
+@pytest.mark.parametrize("case", _csr_cases(), ids=lambda c: c[0])
+def test_device_csr_build_matches_the_host_sort(case):
+    """The GPU radix build equals bincount / cumsum / stable argsort bit for bit."""
+    _, n, u, v = case
+    ud = torch.from_numpy(u.astype(np.int32)).cuda()
+    vd = torch.from_numpy(v.astype(np.int32)).cuda()
+    for key, other, by in ((vd, ud, "dst"), (ud, vd, "src")):
+        indptr, indices, eid = hg.build_device_csr(key, other, n)
+        ref = oracle.csr(u, v, n, by)
+        np.testing.assert_array_equal(indptr.cpu().numpy(), ref[0])
+        np.testing.assert_array_equal(indices.cpu().numpy(), ref[1])
+        np.testing.assert_array_equal(eid.cpu().numpy(), ref[2])
+
+
+def test_graph_queries_read_the_device_build():
+    u, v = rand_graph(3000, 40000, 45)
+    g = dgl.graph((u, v), num_nodes=3000)
+    g._device_csr("in")
+    g._device_csr("out")
+    for got, by in ((g._in_csr(), "dst"), (g._out_csr(), "src")):
+        for a, b in zip(got, oracle.csr(u, v, 3000, by)):
+            np.testing.assert_array_equal(a, b)
+    np.testing.assert_array_equal(g.in_degrees(), np.bincount(v, minlength=3000))
+    np.testing.assert_array_equal(g.out_degrees(), np.bincount(u, minlength=3000))
+
+
 # ------------------------------------------------------------------ dispatcher
 @pytest.mark.parametrize("lhs,rhs", list(itertools.permutations("uve", 2)))
 @pytest.mark.parametrize("op", ["add", "sub", "mul", "div", "dot"])
