@@ -190,8 +190,9 @@ int64_t mdgl_gather_mm_workspace_bytes(int64_t n, int64_t d1, int64_t d2, int64_
  *   indptr  (num_rows + 1) = [0] + cumsum(bincount(key)),
  *   eid     (num_edges)    = argsort(key, stable): inside a row, increasing edge id,
  *   indices (num_edges)    = other[eid].
- * Bit-identical to the numpy build. Workspace: mdgl_build_csr_workspace_bytes
- * (0 when num_rows <= 1 or there are no edges; null is then accepted). */
+ * Bit-identical to the numpy build. `other` and `indices` may both be null
+ * (grouping only). Workspace: mdgl_build_csr_workspace_bytes (0 when
+ * num_rows <= 1 or there are no edges; null is then accepted). */
 int mdgl_build_csr(const int32_t* key, const int32_t* other, int64_t num_edges, int64_t num_rows,
                    int32_t* indptr, int32_t* indices, int32_t* eid, void* workspace,
                    int64_t workspace_bytes, void* stream);

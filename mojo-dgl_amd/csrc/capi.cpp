@@ -168,8 +168,10 @@ int mdgl_build_csr(const int32_t* key, const int32_t* other, int64_t num_edges, 
     return fail(MDGL_EINVAL, "build_csr: 2**31 or more edges or rows");
   if (num_edges > 0 && num_rows == 0)
     return fail(MDGL_EINVAL, "build_csr: edges but no rows");
-  if (!indptr || (num_edges > 0 && (!key || !other || !indices || !eid)))
+  if (!indptr || (num_edges > 0 && (!key || !eid)))
     return fail(MDGL_EINVAL, "build_csr: null buffer");
+  if (num_edges > 0 && !other != !indices)
+    return fail(MDGL_EINVAL, "build_csr: `other` and `indices` come together or not at all");
   const int64_t need = csr_workspace_bytes(num_edges, num_rows);
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(MDGL_EWORKSPACE, "build_csr: workspace of %lld bytes needed, %lld given",

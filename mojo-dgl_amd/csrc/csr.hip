@@ -232,7 +232,7 @@ hipError_t launch_build_csr(const int32_t* key, const int32_t* other, int64_t nu
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(indptr_kernel, dim3((unsigned)((num_edges + 1 + BLOCK - 1) / BLOCK)),
                      dim3(BLOCK), 0, stream, sorted_keys, num_edges, num_rows, indptr);
-  if (num_edges)
+  if (num_edges && other)
     hipLaunchKernelGGL(gather_i32_kernel, dim3(grid_of(num_edges)), dim3(BLOCK), 0, stream,
                        other, eid, indices, num_edges);
   return hipGetLastError();

@@ -87,20 +87,22 @@ class _Chunks:
         self.heavy_ptr = _lib.i32_device(ptr)
 
 
-def build_device_csr(key: torch.Tensor, other: torch.Tensor, num_rows: int):
+def build_device_csr(key: torch.Tensor, other, num_rows: int):
     """COO -> CSR grouped by `key` on the GPU (int32 tensors in edge-id order):
     (indptr, indices, eid) int32 GPU tensors, the reference's bincount /
-    cumsum / stable argsort (heterograph.py:69-86) bit for bit."""
+    cumsum / stable argsort (heterograph.py:69-86) bit for bit. With `other`
+    None only the grouping is made (indices is None)."""
     dev = _lib.device()
+    key = key.contiguous()
     E = int(key.numel())
     L = _lib.lib()
     indptr = torch.empty(num_rows + 1, dtype=torch.int32, device=dev)
-    indices = torch.empty(E, dtype=torch.int32, device=dev)
+    indices = torch.empty(E, dtype=torch.int32, device=dev) if other is not None else None
     eid = torch.empty(E, dtype=torch.int32, device=dev)
     nbytes = L.mdgl_build_csr_workspace_bytes(E, num_rows)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes > 0 else None
-    rc = L.mdgl_build_csr(key.data_ptr(), other.data_ptr(), E, num_rows, indptr.data_ptr(),
-                          indices.data_ptr(), eid.data_ptr(), _lib.ptr(ws), max(nbytes, 0),
+    rc = L.mdgl_build_csr(key.data_ptr(), _lib.ptr(other), E, num_rows, indptr.data_ptr(),
+                          _lib.ptr(indices), eid.data_ptr(), _lib.ptr(ws), max(nbytes, 0),
                           _lib.stream())
     _lib.check(rc, "build_csr")
     return indptr, indices, eid
@@ -120,7 +122,8 @@ class _DeviceCSR:
         """Degree-sorted row order and chunks for a softmax lane layout (cached)."""
         key = (int(slots), int(chunk_len))
         if key not in self._softmax:
-            self._softmax[key] = SoftmaxPlan(self.host_indptr, slots, chunk_len, ordered=True)
+            self._softmax[key] = SoftmaxPlan.from_device(self.indptr, slots, chunk_len,
+                                                         ordered=True)
         return self._softmax[key]
 
 
@@ -174,9 +177,6 @@ class DGLGraph(object):
             else:
                 self._build(kind)
         return self._csr[kind]
-
-    def _edge_arrays(self):
-        return self._u, self._v
 
     def _in_csr(self):
         return self._host_csr("in")[:3]

@@ -54,30 +54,50 @@ class SoftmaxPlan:
             np.cumsum(counts, out=self.bounds[1:])
 
     @classmethod
-    def natural_device(cls, indptr: torch.Tensor, num_chunks: int, slots: int, chunk_len: int):
-        """The natural-order plan from int64 GPU offsets, built on the GPU;
-        `num_chunks` (the chunks the long rows split into) is known to the
-        caller from its validation read back."""
+    def from_device(cls, indptr: torch.Tensor, slots: int, chunk_len: int, ordered: bool,
+                    num_chunks: int | None = None):
+        """The same plan built on the GPU from GPU offsets (int32 or int64):
+        chunks of the long rows, and with `ordered` the rows with
+        0 < degree <= chunk_len grouped by degree bin, stably (ascending row
+        id inside a bin), through the radix grouping of mdgl_build_csr.
+        `num_chunks`, when the caller knows it, saves a read back."""
+        from ..heterograph import build_device_csr
+
         self = cls.__new__(cls)
         self.slots = int(slots)
         self.chunk_len = int(chunk_len)
         self.nbins = int(np.log2(slots)) + 1
+        ip = indptr.to(torch.int64)
+        deg = ip[1:] - ip[:-1]
+        cl = self.chunk_len
+        if num_chunks is None:
+            num_chunks = int(torch.where(deg > cl, (deg + cl - 1) // cl, 0).sum().item())
         self.num_chunks = int(num_chunks)
-        self.order = None
-        self.bounds = None
         self.chunk_row = self.chunk_start = self.chunk_first = None
         if self.num_chunks:
-            deg = indptr[1:] - indptr[:-1]
-            heavy = torch.nonzero(deg > chunk_len).squeeze(1)
-            per = (deg[heavy] + chunk_len - 1) // chunk_len
+            heavy = torch.nonzero(deg > cl).squeeze(1)
+            per = (deg[heavy] + cl - 1) // cl
             first = torch.cumsum(per, 0) - per
             row = torch.repeat_interleave(heavy, per, output_size=self.num_chunks)
             cfirst = torch.repeat_interleave(first, per, output_size=self.num_chunks)
-            local = torch.arange(self.num_chunks, dtype=torch.int64, device=indptr.device) - cfirst
-            start = indptr[row] + local * chunk_len
+            local = torch.arange(self.num_chunks, dtype=torch.int64, device=ip.device) - cfirst
             self.chunk_row = row.to(torch.int32)
-            self.chunk_start = start.to(torch.int32)
+            self.chunk_start = (ip[row] + local * cl).to(torch.int32)
             self.chunk_first = cfirst.to(torch.int32)
+        self.order = None
+        self.bounds = None
+        if ordered:
+            nb = self.nbins
+            # bin k (ceil(log2(degree))) for degree <= slots, bin nb for the
+            # wavefront rows, nb + 1 (past the bounds) for empty and long rows
+            bits = torch.zeros_like(deg)
+            for j in range(nb - 1):
+                bits += (deg > (1 << j)).to(torch.int64)
+            key = torch.where(deg <= slots, bits, torch.full_like(deg, nb))
+            key = torch.where((deg == 0) | (deg > cl), torch.full_like(deg, nb + 1), key)
+            ptr, _, order = build_device_csr(key.to(torch.int32), None, nb + 2)
+            self.order = order
+            self.bounds = ptr[: nb + 2].cpu().numpy().astype(np.int64)
         return self
 
     def bounds_ptr(self):

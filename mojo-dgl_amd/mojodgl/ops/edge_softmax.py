@@ -5,7 +5,8 @@ Same arguments, shapes and errors as the reference, including its positional
 `eids` are grouped by endpoint (groups in ascending endpoint id, positions in
 the order they appear), position i reads `logits[i]`, and the result is as
 long as `logits` with rows past len(eids) zero. The grouping is one stable
-argsort here instead of a Python loop; logits keep float32/float64.
+radix grouping on the GPU (mdgl_build_csr) instead of a Python loop; logits
+keep float32/float64.
 """
 
 from __future__ import annotations
@@ -13,7 +14,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from .. import _lib
+from .. import _lib, heterograph
 from ..base import ALL, DGLError, is_all
 from . import _plan
 
@@ -70,16 +71,24 @@ def edge_softmax(graph, logits, eids=ALL, norm_by="dst"):
     if is_all(eids):
         order = None
     else:
-        order = _lib.i64(eids)
-        if order.size and (int(order.min()) < 0 or int(order.max()) >= num_edges):
-            raise DGLError("edge ids must be in [0, {}), got [{}, {})".format(
-                num_edges, int(order.min()), int(order.max()) + 1))
+        # GPU ids are checked on the GPU (one small read back), host ids on
+        # the host before any GPU work
+        on_gpu = isinstance(eids, torch.Tensor) and eids.device.type == "cuda"
+        order = _lib.i64_device(eids).reshape(-1) if on_gpu else _lib.i64(eids).reshape(-1)
+        if order.shape[0]:
+            if on_gpu:
+                lo, hi = torch.stack((order.min(), order.max())).tolist()
+            else:
+                lo, hi = int(order.min()), int(order.max())
+            if lo < 0 or hi >= num_edges:
+                raise DGLError("edge ids must be in [0, {}), got [{}, {})".format(
+                    num_edges, lo, hi + 1))
     out_len = shape[0]
     if order is None and out_len != num_edges:
         raise DGLError("logits has {} rows but the graph has {} edges".format(out_len, num_edges))
-    if order is not None and order.size > out_len:
+    if order is not None and order.shape[0] > out_len:
         raise DGLError("{} edge ids selected but logits has only {} rows".format(
-            order.size, out_len))
+            order.shape[0], out_len))
 
     dtype = X.dtype
     gdev = _lib.device()
@@ -90,7 +99,7 @@ def edge_softmax(graph, logits, eids=ALL, norm_by="dst"):
     if out_len and d:
         lg = _lib.on_device(X, dtype).reshape(out_len, d)
         if order is not None:
-            lg = lg[: order.size].contiguous()
+            lg = lg[: order.shape[0]].contiguous()
         slots, chunk_len = _plan.geometry(d, dtype, lg, out)
         if order is None:
             csr = graph._device_csr("in" if norm_by == "dst" else "out")
@@ -101,17 +110,15 @@ def edge_softmax(graph, logits, eids=ALL, norm_by="dst"):
             uids, vids = graph._device_coo()
             row_of = vids if norm_by == "dst" else uids
         else:
-            u, v = graph._edge_arrays()
-            key = (v if norm_by == "dst" else u)[order]
-            pos = np.argsort(key, kind="stable")  # positions by (endpoint, appearance)
-            counts = np.bincount(key, minlength=num_nodes)
-            counts = counts[counts > 0]
-            ptr = np.zeros(counts.size + 1, dtype=np.int64)
-            np.cumsum(counts, out=ptr[1:])
-            rows = int(counts.size)
-            indptr, eid = _lib.i32_device(ptr), _lib.i32_device(pos)
-            plan = _plan.SoftmaxPlan(ptr, slots, chunk_len, ordered=True)
-            row_of = None
+            # positions grouped by (endpoint, appearance): the stable grouping
+            # of the selected edges' endpoints, on the GPU; rows are all nodes
+            # (the ones no selected edge reaches are empty and skipped)
+            uids, vids = graph._device_coo()
+            idx = order if isinstance(order, torch.Tensor) else torch.from_numpy(order).to(gdev)
+            row_of = (vids if norm_by == "dst" else uids)[idx]
+            indptr, _, eid = heterograph.build_device_csr(row_of, None, num_nodes)
+            rows = num_nodes if idx.shape[0] else 0
+            plan = _plan.SoftmaxPlan.from_device(indptr, slots, chunk_len, ordered=True)
         if rows:
             n_edges = lg.shape[0]
             ws, nbytes = _plan.workspace(plan, d, dtype, rows if row_of is not None else 0)

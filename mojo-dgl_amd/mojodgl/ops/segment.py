@@ -168,7 +168,8 @@ def segment_softmax(seglen, value):
         if seg.host is not None:
             plan = _plan.SoftmaxPlan(seg.host, slots, chunk_len, ordered=False)
         else:
-            plan = _plan.SoftmaxPlan.natural_device(seg.off64, seg.heavy, slots, chunk_len)
+            plan = _plan.SoftmaxPlan.from_device(seg.off64, slots, chunk_len, ordered=False,
+                                                 num_chunks=seg.heavy)
         ws, nbytes = _plan.workspace(plan, d, dtype)
         rc = _lib.lib().mdgl_segment_softmax(
             off.data_ptr(), val.data_ptr(), out.data_ptr(), None, num_seg, d, n,

@@ -269,6 +269,48 @@ def test_edge_softmax_positional_eids(norm_by):
         close(got, ref, ref, np.float64, "eids case {}".format(case))
 
 
+@pytest.mark.parametrize("norm_by", ["dst", "src"])
+def test_edge_softmax_positional_eids_large_and_on_the_gpu(norm_by):
+    """A subset with repeats, hubs split into chunks, ids given as a GPU tensor."""
+    rng = np.random.default_rng(46)
+    n, e = 2000, 60000
+    u, v = rand_graph(n, e, 47)
+    v[:5000] = 7
+    u[:3000] = 11
+    logits = (rng.normal(size=(e, 4, 1)) * 2).astype(np.float32)
+    eids = rng.choice(e, size=45000, replace=True)
+    g = dgl.graph((u, v), num_nodes=n)
+    ref = oracle.edge_softmax(u, v, n, logits, eids=eids, norm_by=norm_by)
+    got = ops.edge_softmax(g, torch.from_numpy(logits).cuda(),
+                           eids=torch.from_numpy(eids).cuda(), norm_by=norm_by)
+    close(got.cpu().numpy(), ref, ref, np.float32, "gpu eids")
+    host = ops.edge_softmax(g, logits, eids=eids, norm_by=norm_by)
+    np.testing.assert_array_equal(got.cpu().numpy(), host)
+    with pytest.raises(dgl.DGLError):
+        ops.edge_softmax(g, logits, eids=torch.tensor([0, e], device="cuda"), norm_by=norm_by)
+
+
+@pytest.mark.parametrize("slots,chunk_len", [(16, 128), (64, 512), (1, 8)])
+def test_softmax_plan_built_on_the_gpu_equals_the_host_plan(slots, chunk_len):
+    from mojodgl.ops import _plan
+
+    rng = np.random.default_rng(48)
+    deg = np.concatenate([rng.integers(0, 3 * slots, 3000), rng.integers(0, 3 * chunk_len, 50),
+                          [0, chunk_len, chunk_len + 1, slots, slots + 1, 1]])
+    rng.shuffle(deg)
+    indptr = np.concatenate([[0], np.cumsum(deg)])
+    host = _plan.SoftmaxPlan(indptr, slots, chunk_len, ordered=True)
+    dev = _plan.SoftmaxPlan.from_device(torch.from_numpy(indptr).cuda(), slots, chunk_len,
+                                        ordered=True)
+    assert dev.num_chunks == host.num_chunks and dev.nbins == host.nbins
+    np.testing.assert_array_equal(dev.bounds, host.bounds)
+    n = int(host.bounds[-1])
+    np.testing.assert_array_equal(dev.order[:n].cpu().numpy(), host.order.cpu().numpy())
+    for name in ("chunk_row", "chunk_start", "chunk_first"):
+        np.testing.assert_array_equal(getattr(dev, name).cpu().numpy(),
+                                      getattr(host, name).cpu().numpy())
+
+
 # ------------------------------------------------------------------ segments
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("reducer", ["sum", "max", "min", "mean"])
