@@ -393,7 +393,9 @@ int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* e
     }
   }
   const int vw = vec_width(dtype);
-  p.vec = dout % vw == 0 ? vw : 1;
+  // 16-byte lanes when the width allows, else 8-byte lanes for even float32
+  // widths, else one element per lane
+  p.vec = dout % vw == 0 ? vw : (dtype == MDGL_FLOAT32 && dout % 2 == 0 ? 2 : 1);
   p.lmode = op == OP_COPY_RHS ? M_CONTIG : pick_mode(p.bc, true, dout, p.vec, dl, lhs, es);
   p.rmode = op == OP_COPY_LHS ? M_CONTIG : pick_mode(p.bc, false, dout, p.vec, dr, rhs, es);
   if (p.vec > 1 && aligned(dst, p.vec * es)) p.flags |= F_OUT_VEC;

@@ -23,8 +23,9 @@
 // neighbour ids and one of the edge ids; the ids are then broadcast with
 // v_readlane (whole-wavefront units, scalar registers, so the row address is
 // formed on the scalar unit) or ds_bpermute (packed units). Each edge costs
-// one 16-byte gather per lane of the source row and one of the edge row, with
-// U edges in flight per lane.
+// one 16-byte (float32 rows of odd multiples of 2 columns: 8-byte) gather per
+// lane of the source row and one of the edge row, with U edges in flight per
+// lane.
 #pragma once
 
 #include "mdgl_kernels.h"
@@ -62,7 +63,7 @@ __device__ __forceinline__ void fetch(const T* __restrict__ row, int mode_rt, co
                                       T (&x)[VEC]) {
   const int m = (M == M_DYN) ? mode_rt : M;
   if (VEC > 1 && m == M_CONTIG) {
-    if constexpr (VEC == VecOf<T>::n) load_vec<T>(row + off[0], x);
+    if constexpr (VEC > 1) load_n<T, VEC>(row + off[0], x);
   } else if (m == M_SPLAT) {
     const T s = row[off[0]];
 #pragma unroll
@@ -206,7 +207,7 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
   }
   const int64_t o = row * a.dout + k0;
   if (VEC > 1 && (a.flags & F_OUT_VEC)) {
-    if constexpr (VEC == VecOf<T>::n) store_vec<T>(a.out + o, acc);
+    if constexpr (VEC > 1) store_n<T, VEC>(a.out + o, acc);
   } else {
 #pragma unroll
     for (int v = 0; v < VEC; ++v)
@@ -223,7 +224,13 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
   }
 }
 
-template <class T, int OP, int RED, int VEC>
+// Kernel variants, one body each so that every launch only carries the
+// registers of its own path: whole-wavefront units (G = 64) with both
+// operands contiguous, with a splatted edge operand, or any modes; packed
+// units with contiguous operands, or any modes.
+enum { P_WIDE_CC = 0, P_WIDE_CS = 1, P_WIDE_DYN = 2, P_PACK_CC = 3, P_PACK_DYN = 4 };
+
+template <class T, int OP, int RED, int VEC, int PATH>
 __global__ __launch_bounds__(BLOCK) void gspmm_kernel(GspmmArgs<T> a) {
   const int64_t b = blockIdx.x;
   const bool chunk = b < a.chunk_blocks;
@@ -234,22 +241,16 @@ __global__ __launch_bounds__(BLOCK) void gspmm_kernel(GspmmArgs<T> a) {
   // readlanes always see a full wavefront
   const int64_t wave = blk * WAVES_PER_BLOCK + (threadIdx.x >> 6);
   if (wave >= (chunk ? a.chunk_waves : a.row_waves)) return;
-  const bool copy_l = OP == OP_COPY_LHS, copy_r = OP == OP_COPY_RHS;
-  const int lm = copy_r ? a.rmode : a.lmode;
-  const int rm = copy_l ? a.lmode : a.rmode;
-  if (a.G == WAVE) {
-    if (lm == M_CONTIG && rm == M_CONTIG)
-      gspmm_body<T, OP, RED, VEC, M_CONTIG, M_CONTIG, true>(a, chunk, wave, lane);
-    else if (lm == M_CONTIG && rm == M_SPLAT)
-      gspmm_body<T, OP, RED, VEC, M_CONTIG, M_SPLAT, true>(a, chunk, wave, lane);
-    else
-      gspmm_body<T, OP, RED, VEC, M_DYN, M_DYN, true>(a, chunk, wave, lane);
-  } else {
-    if (lm == M_CONTIG && rm == M_CONTIG)
-      gspmm_body<T, OP, RED, VEC, M_CONTIG, M_CONTIG, false>(a, chunk, wave, lane);
-    else
-      gspmm_body<T, OP, RED, VEC, M_DYN, M_DYN, false>(a, chunk, wave, lane);
-  }
+  if constexpr (PATH == P_WIDE_CC)
+    gspmm_body<T, OP, RED, VEC, M_CONTIG, M_CONTIG, true>(a, chunk, wave, lane);
+  else if constexpr (PATH == P_WIDE_CS)
+    gspmm_body<T, OP, RED, VEC, M_CONTIG, M_SPLAT, true>(a, chunk, wave, lane);
+  else if constexpr (PATH == P_WIDE_DYN)
+    gspmm_body<T, OP, RED, VEC, M_DYN, M_DYN, true>(a, chunk, wave, lane);
+  else if constexpr (PATH == P_PACK_CC)
+    gspmm_body<T, OP, RED, VEC, M_CONTIG, M_CONTIG, false>(a, chunk, wave, lane);
+  else
+    gspmm_body<T, OP, RED, VEC, M_DYN, M_DYN, false>(a, chunk, wave, lane);
 }
 
 // Folds the chunk partials of each heavy row in chunk (= CSR) order.
@@ -328,8 +329,23 @@ hipError_t launch_gspmm_op(const GspmmParams& p) {
   a.chunk_blocks = (a.chunk_waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
   a.num_blocks = a.chunk_blocks + (a.row_waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
   if (a.num_blocks > 0) {
-    hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC>), dim3((unsigned)a.num_blocks), dim3(BLOCK),
-                       0, p.stream, a);
+    const bool copy_l = OP == OP_COPY_LHS, copy_r = OP == OP_COPY_RHS;
+    const int lm = copy_r ? a.rmode : a.lmode;
+    const int rm = copy_l ? a.lmode : a.rmode;
+    const dim3 grid((unsigned)a.num_blocks), block(BLOCK);
+    if (G == WAVE) {
+      if (lm == M_CONTIG && rm == M_CONTIG)
+        hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_WIDE_CC>), grid, block, 0, p.stream, a);
+      else if (lm == M_CONTIG && rm == M_SPLAT)
+        hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_WIDE_CS>), grid, block, 0, p.stream, a);
+      else
+        hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_WIDE_DYN>), grid, block, 0, p.stream, a);
+    } else {
+      if (lm == M_CONTIG && rm == M_CONTIG)
+        hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_PACK_CC>), grid, block, 0, p.stream, a);
+      else
+        hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_PACK_DYN>), grid, block, 0, p.stream, a);
+    }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
@@ -360,6 +376,9 @@ hipError_t launch_gspmm_vec(const GspmmParams& p) {
 template <class T, int RED>
 hipError_t launch_gspmm_red(const GspmmParams& p) {
   if (p.vec == VecOf<T>::n) return launch_gspmm_vec<T, RED, VecOf<T>::n>(p);
+  if constexpr (VecOf<T>::n == 4) {
+    if (p.vec == 2) return launch_gspmm_vec<T, RED, 2>(p);  // 8-byte lanes (even widths)
+  }
   return launch_gspmm_vec<T, RED, 1>(p);
 }
 

@@ -86,6 +86,25 @@ __device__ __forceinline__ void store_vec(T* p, const T (&in)[VecOf<T>::n]) {
   *reinterpret_cast<V*>(p) = v;
 }
 
+// N consecutive elements (N * sizeof(T) = 8 or 16 bytes) in one load / store;
+// the host guarantees the alignment before selecting a mode that uses them.
+template <class T, int N>
+__device__ __forceinline__ void load_n(const T* p, T (&out)[N]) {
+  typedef T V __attribute__((ext_vector_type(N)));
+  const V v = *reinterpret_cast<const V*>(p);
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = v[i];
+}
+
+template <class T, int N>
+__device__ __forceinline__ void store_n(T* p, const T (&in)[N]) {
+  typedef T V __attribute__((ext_vector_type(N)));
+  V v;
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = in[i];
+  *reinterpret_cast<V*>(p) = v;
+}
+
 template <class T>
 __device__ __forceinline__ T seed(int red) {
   if (red == RED_MAX) return -__builtin_huge_val();
