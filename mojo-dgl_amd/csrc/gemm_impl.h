@@ -67,7 +67,8 @@ struct GemmArgs {
   const int32_t* group_off;  // R + 1
   const int32_t* tile_ptr;   // R + 1, M tiles per group (prefix)
   int64_t R, K, Kp, N;
-  int a_vec;  // rows of a allow 16-byte loads
+  int a_vec;    // rows of a allow 16-byte loads
+  int out_vec;  // rows of out allow 16-byte stores
 };
 
 // bt[g][n][k] = b[g][k][n], zero for k in [K, Kp).
@@ -216,12 +217,202 @@ __global__ __launch_bounds__(BLOCK) void grouped_gemm_kernel(GemmArgs<T> p) {
   }
 }
 
+// ---------------------------------------------------------------- b resident
+// float32, K a multiple of 32 up to 128, rows of a 16-byte aligned (the host
+// checks; other shapes take grouped_gemm_kernel): the group's whole b block
+// (128 columns x K) sits in
+// LDS, loaded once per group a workgroup meets, and the a fragments go from
+// global memory straight into registers, up to four 16-k chunks ahead of the
+// MFMAs (across tile boundaries: the next tile's first chunks are requested
+// while this tile's last ones multiply), so the K loop has no barrier and no
+// LDS traffic for a. A workgroup (8 wavefronts, 4 x 2, each 64 x 64 of the
+// output) walks a contiguous range of 256-row tiles; ranges follow the group
+// order, so b changes rarely.
+constexpr int RB_TM = 256;      // rows per tile
+constexpr int RB_KMAX = 128;    // largest padded K held in LDS
+constexpr int RB_THREADS = 512;
+constexpr int RB_LD = RB_KMAX + 4;
+
+// Within each quad of lanes (s = lane % 4), x[r] = M[r][s] becomes
+// x[c] = M[s][c]: two butterfly stages (partner lane s ^ 1, then s ^ 2), each
+// moving the elements whose position bit and lane bit differ.
+__device__ __forceinline__ int dpp_quad_xor1(int v) {
+  return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+}
+__device__ __forceinline__ int dpp_quad_xor2(int v) {
+  return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+}
+__device__ __forceinline__ void quad_transpose(float (&x)[4], int s) {
+  float t[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    t[r] = __int_as_float(dpp_quad_xor1(__float_as_int(x[r ^ 1])));
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    if ((r & 1) != (s & 1)) x[r] = t[r];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    t[r] = __int_as_float(dpp_quad_xor2(__float_as_int(x[r ^ 2])));
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    if ((r & 2) != (s & 2)) x[r] = t[r];
+}
+
+template <class T, int NCH>
+__global__ __launch_bounds__(RB_THREADS) void grouped_gemm_resident_kernel(GemmArgs<T> p,
+                                                                           int64_t tiles_per_wg) {
+  using M = Mfma<T>;
+  using acc_t = typename M::acc_t;
+  // a ring of DEPTH chunks (NCH a multiple of DEPTH, so the next tile's
+  // chunk k lands in ring slot k % DEPTH too)
+  constexpr int DEPTH = NCH == 6 ? 3 : (NCH < 4 ? NCH : 4);
+  static_assert(NCH % DEPTH == 0, "ring depth");
+  __shared__ __align__(16) T Bs[GBN][RB_LD];
+  const int t = threadIdx.x;
+  const int lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1;
+  const int li = lane & 15, h = lane >> 4;
+  const int64_t total = p.tile_ptr[p.R];
+  const int64_t first = (int64_t)blockIdx.x * tiles_per_wg;
+  const int64_t last = first + tiles_per_wg < total ? first + tiles_per_wg : total;
+  if (first >= last) return;  // uniform per workgroup
+  const int64_t n0 = (int64_t)blockIdx.y * GBN;
+
+  // rows of a tile for this lane: rid[i] = row of tile row wm*64 + 16i + li
+  // (-1 past the group); base[i] = where its a fragments start (row 0 for
+  // -1: read, never stored)
+  auto setup = [&](int64_t tl, int64_t gg, int64_t& m0, int64_t& m_end, int32_t (&rid)[4],
+                   const T* (&base)[4]) {
+    m0 = p.group_off[gg] + (tl - p.tile_ptr[gg]) * RB_TM;
+    m_end = p.group_off[gg + 1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t pos = m0 + wm * 64 + i * 16 + li;
+      rid[i] = pos < m_end ? (p.perm ? p.perm[pos] : (int32_t)pos) : -1;
+      base[i] = p.a + (int64_t)(rid[i] >= 0 ? rid[i] : 0) * p.K + 4 * h;
+    }
+  };
+
+  int64_t tile = first;
+  // group of the first tile: last g with tile_ptr[g] <= tile (uniform)
+  int64_t g = 0;
+  {
+    int64_t lo = 0, hi = p.R - 1;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi + 1) / 2;
+      if (p.tile_ptr[mid] <= tile) lo = mid; else hi = mid - 1;
+    }
+    g = lo;
+  }
+  int64_t m0, m_end;
+  int32_t rid[4];
+  const T* base[4];
+  setup(tile, g, m0, m_end, rid, base);
+  // lane (li, h) holds a[row i][16c + 4h .. +3] of chunk c in ring slot c % DEPTH
+  T af[DEPTH][4][4];
+#pragma unroll
+  for (int c = 0; c < DEPTH; ++c)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) load_global_n<T, 4>(base[i] + c * 16, af[c][i]);
+
+  int64_t cur_g = -1;
+  while (true) {
+    if (g != cur_g) {
+      __syncthreads();  // every wavefront is done with the previous block
+      const T* bt_g = p.bt + g * p.N * p.Kp;
+      constexpr int CPR = NCH * 4;  // 16-byte chunks per row of the block
+      for (int c = t; c < GBN * CPR; c += RB_THREADS) {
+        const int r = c / CPR, k = (c % CPR) * 4;
+        T v[4] = {T(0), T(0), T(0), T(0)};
+        if (n0 + r < p.N) load_global_n<T, 4>(bt_g + (n0 + r) * p.Kp + k, v);
+        store_n<T, 4>(&Bs[r][k], v);
+      }
+      __syncthreads();
+      cur_g = g;
+    }
+    // the next tile's rows are looked up now; its first chunks are requested
+    // while this tile's last chunks multiply
+    const bool has_next = tile + 1 < last;
+    int64_t g_n = g, m0_n = 0, m_end_n = 0;
+    int32_t rid_n[4] = {-1, -1, -1, -1};
+    const T* base_n[4] = {base[0], base[1], base[2], base[3]};
+    if (has_next) {
+      while (p.tile_ptr[g_n + 1] <= tile + 1) ++g_n;
+      setup(tile + 1, g_n, m0_n, m_end_n, rid_n, base_n);
+    }
+    acc_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][j][r] = T(0);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      T bf[4][4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        load_n<T, 4>(&Bs[wn * 64 + j * 16 + li][c * 16 + 4 * h], bf[j]);
+#pragma unroll
+      for (int sstep = 0; sstep < 4; ++sstep)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = M::step(af[c % DEPTH][i][sstep], bf[j][sstep], acc[i][j]);
+      if (c + DEPTH < NCH) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          load_global_n<T, 4>(base[i] + (c + DEPTH) * 16, af[c % DEPTH][i]);
+      } else if (has_next) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          load_global_n<T, 4>(base_n[i] + (c + DEPTH - NCH) * 16, af[c % DEPTH][i]);
+      }
+    }
+    // Output. Lane (li, h) holds column li of block rows 4h + r (r = 0..3).
+    // A 4 x 4 transpose inside each DPP quad (lanes 4q..4q+3) gives lane
+    // 4q + s row 4h + s at columns 4q..4q+3, stored as one 16-byte write.
+    const int s4 = li & 3, q4 = li >> 2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int orow = __shfl(rid[i], 4 * h + s4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        T x[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+        quad_transpose(x, s4);
+        const int64_t n = n0 + wn * 64 + j * 16 + 4 * q4;
+        if (orow >= 0 && n < p.N) {
+          if (p.out_vec && n + 4 <= p.N) {
+            store_n<T, 4>(p.out + (int64_t)orow * p.N + n, x);
+          } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              if (n + v < p.N) p.out[(int64_t)orow * p.N + n + v] = x[v];
+          }
+        }
+      }
+    }
+    if (!has_next) break;
+    ++tile;
+    g = g_n;
+    m0 = m0_n;
+    m_end = m_end_n;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      rid[i] = rid_n[i];
+      base[i] = base_n[i];
+    }
+  }
+}
+
 // ---------------------------------------------------------------- grouping
 // offsets[g] = exclusive prefix of seglen; tile_ptr[g] = exclusive prefix of
-// ceil(len / 128). One workgroup; R is small (number of b blocks).
+// ceil(len / tm), tm the kernel's tile height. One thread; R is small (number
+// of b blocks).
 static __global__ __launch_bounds__(1024) void seg_plan_kernel(const int64_t* __restrict__ seglen,
                                                         int32_t* __restrict__ group_off,
-                                                        int32_t* __restrict__ tile_ptr, int64_t R) {
+                                                        int32_t* __restrict__ tile_ptr, int64_t R,
+                                                        int tm) {
   if (threadIdx.x != 0) return;
   int64_t off = 0, tiles = 0;
   for (int64_t g = 0; g < R; ++g) {
@@ -229,7 +420,7 @@ static __global__ __launch_bounds__(1024) void seg_plan_kernel(const int64_t* __
     tile_ptr[g] = (int32_t)tiles;
     const int64_t len = seglen[g];
     off += len;
-    tiles += (len + GBM - 1) / GBM;
+    tiles += (len + tm - 1) / tm;
   }
   group_off[R] = (int32_t)off;
   tile_ptr[R] = (int32_t)tiles;
@@ -289,7 +480,7 @@ static __global__ __launch_bounds__(BLOCK) void bucket_colscan_kernel(int32_t* _
 // group_off / tile_ptr from the group totals (one thread; R is small), and
 // the totals turned into each group's first sorted position.
 static __global__ void bucket_plan_kernel(int64_t* __restrict__ totals, int32_t* __restrict__ group_off,
-                                   int32_t* __restrict__ tile_ptr, int64_t R) {
+                                   int32_t* __restrict__ tile_ptr, int64_t R, int tm) {
   if (threadIdx.x != 0 || blockIdx.x != 0) return;
   int64_t off = 0, tiles = 0;
   for (int64_t g = 0; g < R; ++g) {
@@ -298,7 +489,7 @@ static __global__ void bucket_plan_kernel(int64_t* __restrict__ totals, int32_t*
     tile_ptr[g] = (int32_t)tiles;
     totals[g] = off;
     off += c;
-    tiles += (c + GBM - 1) / GBM;
+    tiles += (c + tm - 1) / tm;
   }
   group_off[R] = (int32_t)off;
   tile_ptr[R] = (int32_t)tiles;
@@ -382,6 +573,10 @@ template <class T>
 hipError_t launch_grouped(const GemmLaunch& L, bool gather) {
   if (L.n <= 0 || L.N <= 0 || L.R <= 0) return hipSuccess;
   const int64_t Kp = gemm_kp<T>(L.K);
+  constexpr int EVH = 16 / sizeof(T);
+  const bool resident = sizeof(T) == 4 && Kp <= RB_KMAX && Kp == L.K &&
+                        reinterpret_cast<uintptr_t>(L.a) % 16 == 0 && L.K % EVH == 0;
+  const int tm = resident ? RB_TM : GBM;
   char* w = static_cast<char*>(L.workspace);
   T* bt = reinterpret_cast<T*>(w);
   w += ws_align(L.R * L.N * Kp * (int64_t)sizeof(T));
@@ -413,13 +608,13 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather) {
     hipLaunchKernelGGL(bucket_colscan_kernel, dim3((unsigned)L.R), dim3(BLOCK), 0, L.stream,
                        counts, totals, nb, L.R);
     hipLaunchKernelGGL(bucket_plan_kernel, dim3(1), dim3(64), 0, L.stream, totals, group_off,
-                       tile_ptr, L.R);
+                       tile_ptr, L.R, tm);
     hipLaunchKernelGGL(bucket_scatter_kernel, dim3((unsigned)nb), dim3(BLOCK),
                        (size_t)(5 * L.R * 4), L.stream, L.idx_b, counts, totals, perm, L.n, L.R,
                        bits);
   } else {
     hipLaunchKernelGGL(seg_plan_kernel, dim3(1), dim3(64), 0, L.stream, L.seglen, group_off,
-                       tile_ptr, L.R);
+                       tile_ptr, L.R, tm);
   }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -437,8 +632,28 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather) {
   a.N = L.N;
   constexpr int EV = 16 / sizeof(T);
   a.a_vec = (L.K % EV == 0) && (reinterpret_cast<uintptr_t>(L.a) % 16 == 0);
-  const int64_t mt = (L.n + GBM - 1) / GBM + L.R;
+  a.out_vec = (L.N % EV == 0) && (reinterpret_cast<uintptr_t>(L.out) % 16 == 0);
   const int64_t nt = (L.N + GBN - 1) / GBN;
+  if constexpr (sizeof(T) == 4) {
+    if (resident) {
+      // upper bound of the tile count; one resident workgroup per CU (its
+      // registers), each a contiguous range of tiles
+      const int64_t mt = (L.n + RB_TM - 1) / RB_TM + L.R;
+      int64_t wgs = 256 / nt;
+      if (wgs < 1) wgs = 1;
+      if (wgs > mt) wgs = mt;
+      const int64_t per = (mt + wgs - 1) / wgs;
+      const dim3 grid((unsigned)wgs, (unsigned)nt), block(RB_THREADS);
+      switch (Kp / 16) {
+        case 2: hipLaunchKernelGGL((grouped_gemm_resident_kernel<T, 2>), grid, block, 0, L.stream, a, per); break;
+        case 4: hipLaunchKernelGGL((grouped_gemm_resident_kernel<T, 4>), grid, block, 0, L.stream, a, per); break;
+        case 6: hipLaunchKernelGGL((grouped_gemm_resident_kernel<T, 6>), grid, block, 0, L.stream, a, per); break;
+        default: hipLaunchKernelGGL((grouped_gemm_resident_kernel<T, 8>), grid, block, 0, L.stream, a, per); break;
+      }
+      return hipGetLastError();
+    }
+  }
+  const int64_t mt = (L.n + GBM - 1) / GBM + L.R;
   hipLaunchKernelGGL((grouped_gemm_kernel<T>), dim3((unsigned)mt, (unsigned)nt), dim3(BLOCK), 0,
                      L.stream, a);
   return hipGetLastError();

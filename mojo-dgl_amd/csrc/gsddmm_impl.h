@@ -106,12 +106,12 @@ __device__ __forceinline__ T dot_part(const T* __restrict__ l, const T* __restri
   for (int64_t k = k0; k < red; k += step) {
     if constexpr (VEC > 1) {
       T xv[VEC], yv[VEC];
-      load_vec<T>(l + k, xv);
-      load_vec<T>(r + k, yv);
+      load_global_n<T, VEC>(l + k, xv);
+      load_global_n<T, VEC>(r + k, yv);
 #pragma unroll
       for (int v = 0; v < VEC; ++v) part = part + xv[v] * yv[v];
     } else {
-      part = part + l[k] * r[k];
+      part = part + load_global(l + k) * load_global(r + k);
     }
   }
   return part;
@@ -147,11 +147,11 @@ __global__ __launch_bounds__(BLOCK) void gsddmm_dot_kernel(GsddmmArgs<T> a) {
     for (int u = 0; u < DOT_U; ++u) {
       if (lp[u] && k0 < a.red) {
         if constexpr (VEC > 1) {
-          load_vec<T>(lp[u] + k0, xv[u]);
-          load_vec<T>(rp[u] + k0, yv[u]);
+          load_global_n<T, VEC>(lp[u] + k0, xv[u]);
+          load_global_n<T, VEC>(rp[u] + k0, yv[u]);
         } else {
-          xv[u][0] = lp[u][k0];
-          yv[u][0] = rp[u][k0];
+          xv[u][0] = load_global(lp[u] + k0);
+          yv[u][0] = load_global(rp[u] + k0);
         }
       } else {
 #pragma unroll

@@ -96,6 +96,24 @@ __device__ __forceinline__ void load_n(const T* p, T (&out)[N]) {
   for (int i = 0; i < N; ++i) out[i] = v[i];
 }
 
+// The same load from memory known to be global: pointers kept in arrays or
+// captured by lambdas lose their address space, and a FLAT load would also
+// hold up the LDS wait counter.
+template <class T, int N>
+__device__ __forceinline__ void load_global_n(const T* p, T (&out)[N]) {
+  typedef T V __attribute__((ext_vector_type(N)));
+  typedef const __attribute__((address_space(1))) V GV;
+  const V v = *(GV*)p;
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = v[i];
+}
+
+template <class T>
+__device__ __forceinline__ T load_global(const T* p) {
+  typedef const __attribute__((address_space(1))) T GT;
+  return *(GT*)p;
+}
+
 template <class T, int N>
 __device__ __forceinline__ void store_n(T* p, const T (&in)[N]) {
   typedef T V __attribute__((ext_vector_type(N)));
