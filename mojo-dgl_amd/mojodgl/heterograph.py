@@ -127,35 +127,106 @@ class _DeviceCSR:
         return self._softmax[key]
 
 
+_IDTYPES = {None: np.int64, np.int64: np.int64, np.int32: np.int32, "int64": np.int64,
+            "int32": np.int32, torch.int64: np.int64, torch.int32: np.int32}
+
+
+def _idtype(idtype):
+    try:
+        return _IDTYPES[idtype]
+    except (KeyError, TypeError):
+        pass
+    try:
+        return _IDTYPES[np.dtype(idtype).type]
+    except (KeyError, TypeError):
+        raise DGLError("idtype must be int32 or int64, got {}".format(idtype)) from None
+
+
+def _on_gpu(a):
+    return isinstance(a, torch.Tensor) and a.device.type == "cuda"
+
+
 class DGLGraph(object):
-    """A homogeneous graph whose message passing runs on the GPU."""
+    """A homogeneous graph whose message passing runs on the GPU.
+
+    Node ids given as GPU tensors stay on the GPU: they are checked there
+    (one small read back), converted to int32 in place of an upload, and the
+    host copy used by host-side queries is read back only when one asks.
+    `idtype` (int32 or int64) is the dtype of the ids the queries return.
+    """
 
     def __init__(self, u, v, num_nodes=None, idtype=np.int64):
-        u = i64(u)
-        v = i64(v)
-        if u.shape != v.shape:
-            raise DGLError("u and v must have the same length")
-        if num_nodes is None:
-            num_nodes = 0 if u.size == 0 else int(max(u.max(), v.max())) + 1
-        num_nodes = int(num_nodes)
-        if num_nodes < 0:
-            raise DGLError("num_nodes must be non-negative, got {}".format(num_nodes))
-        if u.size and (int(u.max()) >= num_nodes or int(v.max()) >= num_nodes
-                       or int(u.min()) < 0 or int(v.min()) < 0):
-            raise DGLError("node ids must be in [0, {}), got [{}, {}]".format(
-                num_nodes, int(min(u.min(), v.min())), int(max(u.max(), v.max()))))
-        self._u = u
-        self._v = v
-        self._num_nodes = num_nodes
-        self.idtype = idtype
+        self.idtype = _idtype(idtype)
+        self._hu = self._hv = None
+        self._dcoo = None
+        if _on_gpu(u) and _on_gpu(v):
+            if u.is_floating_point() or v.is_floating_point() or u.is_complex() or v.is_complex():
+                raise DGLError("node ids must be integers")
+            u = u.detach().reshape(-1)
+            v = v.detach().reshape(-1)
+            if u.shape != v.shape:
+                raise DGLError("u and v must have the same length")
+            E = int(u.numel())
+            lo = hi = 0
+            if E:
+                lo, hi = torch.stack((torch.minimum(u.min(), v.min()),
+                                      torch.maximum(u.max(), v.max()))).tolist()
+            if num_nodes is None:
+                num_nodes = 0 if E == 0 else hi + 1
+            num_nodes = int(num_nodes)
+            if num_nodes < 0:
+                raise DGLError("num_nodes must be non-negative, got {}".format(num_nodes))
+            if E and (hi >= num_nodes or lo < 0):
+                raise DGLError("node ids must be in [0, {}), got [{}, {}]".format(
+                    num_nodes, lo, hi))
+            self._E = E
+            self._num_nodes = num_nodes
+            self._check_int32()
+            dev = _lib.device()
+            self._dcoo = (u.to(device=dev, dtype=torch.int32).contiguous(),
+                          v.to(device=dev, dtype=torch.int32).contiguous())
+        else:
+            u = i64(u)
+            v = i64(v)
+            if u.shape != v.shape:
+                raise DGLError("u and v must have the same length")
+            if num_nodes is None:
+                num_nodes = 0 if u.size == 0 else int(max(u.max(), v.max())) + 1
+            num_nodes = int(num_nodes)
+            if num_nodes < 0:
+                raise DGLError("num_nodes must be non-negative, got {}".format(num_nodes))
+            if u.size and (int(u.max()) >= num_nodes or int(v.max()) >= num_nodes
+                           or int(u.min()) < 0 or int(v.min()) < 0):
+                raise DGLError("node ids must be in [0, {}), got [{}, {}]".format(
+                    num_nodes, int(min(u.min(), v.min())), int(max(u.max(), v.max()))))
+            self._hu = u.reshape(-1)
+            self._hv = v.reshape(-1)
+            self._E = int(self._hu.size)
+            self._num_nodes = num_nodes
         self._nstore = {}
         self._estore = {}
         self.ndata = FeatureDict(self._nstore, self._num_nodes, "ndata")
-        self.edata = FeatureDict(self._estore, len(u), "edata")
+        self.edata = FeatureDict(self._estore, self._E, "edata")
         self._csr = {}
         self._draw = {}
         self._dcsr = {}
-        self._dcoo = None
+
+    @property
+    def _u(self):
+        """Host int64 source ids (read back once from a GPU-built graph)."""
+        if self._hu is None:
+            self._hu = self._dcoo[0].cpu().numpy().astype(np.int64)
+        return self._hu
+
+    @property
+    def _v(self):
+        """Host int64 destination ids (read back once from a GPU-built graph)."""
+        if self._hv is None:
+            self._hv = self._dcoo[1].cpu().numpy().astype(np.int64)
+        return self._hv
+
+    def _ids(self, a):
+        return np.ascontiguousarray(a, dtype=self.idtype)
 
     # ------------------------------------------------------------------ csr
     def _build(self, kind):
@@ -185,7 +256,7 @@ class DGLGraph(object):
         return self._host_csr("out")[:3]
 
     def _check_int32(self):
-        if self._u.size >= 2 ** 31 or self._num_nodes >= 2 ** 31:
+        if self._E >= 2 ** 31 or self._num_nodes >= 2 ** 31:
             raise DGLError("graphs with 2**31 or more nodes or edges are not supported on the GPU")
 
     def _device_raw(self, kind):
@@ -232,13 +303,13 @@ class DGLGraph(object):
         return (("_N", "_E", "_N"),)
 
     def number_of_edges(self, etype=None):
-        return int(self._u.size)
+        return self._E
 
     def num_nodes(self):
         return self._num_nodes
 
     def num_edges(self):
-        return int(self._u.size)
+        return self._E
 
     def num_src_nodes(self):
         return self._num_nodes
@@ -261,7 +332,8 @@ class DGLGraph(object):
             raise DGLError("form must be 'uv' or 'all'")
         if order != "eid":
             raise DGLError("only order='eid' is supported")
-        return _EdgeTuple(self._u, self._v, np.arange(self._u.size, dtype=np.int64))
+        return _EdgeTuple(self._ids(self._u), self._ids(self._v),
+                          np.arange(self._E, dtype=self.idtype))
 
     def _select(self, ids, order, on_src):
         if is_all(ids):
@@ -274,7 +346,7 @@ class DGLGraph(object):
         elif order == "dstid":
             sel = sel[np.argsort(self._v[sel], kind="stable")]
         sel = sel.astype(np.int64)
-        return _EdgeTuple(self._u[sel], self._v[sel], sel)
+        return _EdgeTuple(self._ids(self._u[sel]), self._ids(self._v[sel]), self._ids(sel))
 
     def in_edges(self, v, form="uv", order="eid", etype=None):
         """All in-edges of `v` (every node when `v` is ALL), in edge-id order."""
@@ -286,11 +358,11 @@ class DGLGraph(object):
 
     def in_degrees(self, v=None):
         deg = self._host_csr("in")[3]
-        return deg if v is None else deg[i64(v)]
+        return self._ids(deg if v is None else deg[i64(v)])
 
     def out_degrees(self, u=None):
         deg = self._host_csr("out")[3]
-        return deg if u is None else deg[i64(u)]
+        return self._ids(deg if u is None else deg[i64(u)])
 
     # ------------------------------------------------------- message passing
     def _builtin_message(self, message_func):
@@ -353,7 +425,7 @@ class DGLGraph(object):
             if isinstance(message_func, MessageFunction):
                 messages = {message_func.out_field: self._builtin_message(message_func)}
             else:
-                edges = EdgeBatch(self, np.arange(self._u.size, dtype=np.int64))
+                edges = EdgeBatch(self, np.arange(self._E, dtype=np.int64))
                 messages = dict(message_func(edges))
             if isinstance(reduce_func, ReduceFunction):
                 key = next(iter(messages))
@@ -399,15 +471,23 @@ class DGLGraph(object):
         v = np.unique(i64(v))
         if v.size == 0:
             return
-        mask = np.isin(self._v, v)
-        sub = DGLGraph(self._u[mask], self._v[mask], num_nodes=self._num_nodes)
+        if int(v[0]) < 0 or int(v[-1]) >= self._num_nodes:
+            raise DGLError("node ids must be in [0, {}), got [{}, {}]".format(
+                self._num_nodes, int(v[0]), int(v[-1])))
+        # the in-edges of `v`, selected on the GPU from the resident endpoints
+        # (edge-id order kept); the subgraph is built from them there
+        du, dv = self._device_coo()
+        flag = torch.zeros(self._num_nodes, dtype=torch.bool, device=du.device)
+        flag[torch.from_numpy(v).to(du.device)] = True
+        sel = torch.nonzero(flag[dv.long()]).squeeze(1)
+        sub = DGLGraph(du[sel], dv[sel], num_nodes=self._num_nodes)
         for key, value in self._nstore.items():
             sub.ndata[key] = value
         for key, value in self._estore.items():
             if isinstance(value, torch.Tensor):
-                sub.edata[key] = value[torch.as_tensor(mask, device=value.device)]
+                sub.edata[key] = value[sel.to(value.device)]
             else:
-                sub.edata[key] = value[mask]
+                sub.edata[key] = value[sel.cpu().numpy()]
         result = sub._pass(message_func, reduce_func, apply_node_func, write=False)
         for key, value in result.items():
             if isinstance(value, torch.Tensor):

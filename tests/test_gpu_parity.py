@@ -573,6 +573,39 @@ def test_pull_and_readme_vector():
           np.float64, "pull")
 
 
+def test_graph_from_gpu_ids_is_built_on_the_gpu():
+    """GPU endpoint tensors: checked on the GPU, no host copy until a host query."""
+    n, e = 700, 9000
+    u, v = rand_graph(n, e, 49)
+    ud, vd = torch.from_numpy(u).cuda(), torch.from_numpy(v.astype(np.int32)).cuda()
+    g = dgl.graph((ud, vd))
+    assert g.num_nodes() == int(max(u.max(), v.max())) + 1 and g.num_edges() == e
+    assert g._hu is None and g._hv is None  # nothing read back yet
+    h = torch.randn(g.num_nodes(), 24, device="cuda")
+    w = torch.randn(e, 24, device="cuda")
+    got = ops.u_mul_e_max(g, h, w)
+    assert g._hu is None and g._hv is None
+    ref = ops.u_mul_e_max(dgl.graph((u, v), num_nodes=g.num_nodes()), h, w)
+    assert torch.equal(got, ref)
+    np.testing.assert_array_equal(g.edges().u, u)
+    np.testing.assert_array_equal(g.in_degrees(), np.bincount(v, minlength=g.num_nodes()))
+    with pytest.raises(dgl.DGLError):
+        dgl.graph((ud, vd), num_nodes=10)
+    with pytest.raises(dgl.DGLError):
+        dgl.graph((ud - 1, vd))
+    with pytest.raises(dgl.DGLError):
+        dgl.graph((ud.double(), vd))
+    # pull selects the subgraph on the GPU
+    g.ndata["x"] = h
+    g.edata["w"] = w
+    targets = np.array([3, 17, 400])
+    g.pull(targets, fn.u_mul_e("x", "w", "m"), fn.sum("m", "z"))
+    full = ops.u_mul_e_sum(g, h, w)
+    want = torch.zeros_like(full)
+    want[targets] = full[targets]
+    assert torch.equal(g.ndata["z"], want)
+
+
 def test_torch_tensors_stay_on_the_gpu():
     n, e = 500, 8000
     u, v = rand_graph(n, e, 29)

@@ -74,6 +74,22 @@ def test_graph_queries():
     assert gt.num_nodes() == 3
 
 
+def test_idtype_sets_the_dtype_of_returned_ids():
+    g32 = dgl.graph((U, V), idtype=np.int32)
+    g64 = dgl.graph((U, V))
+    assert g64.idtype is np.int64 and g32.idtype is np.int32
+    for g, dt in ((g32, np.int32), (g64, np.int64)):
+        e = g.edges()
+        assert e.u.dtype == dt and e.v.dtype == dt and e.eid.dtype == dt
+        assert g.in_degrees().dtype == dt and g.out_degrees([0]).dtype == dt
+        assert g.in_edges(1).eid.dtype == dt
+    np.testing.assert_array_equal(g32.edges().u, U)
+    assert dgl.graph((U, V), idtype=torch.int32).idtype is np.int32
+    assert dgl.graph((U, V), idtype="int64").idtype is np.int64
+    with pytest.raises(dgl.DGLError):
+        dgl.graph((U, V), idtype=np.float32)
+
+
 def test_graph_validation():
     with pytest.raises(dgl.DGLError):
         dgl.graph(([0, 1], [1, 5]), num_nodes=3)
