@@ -198,6 +198,27 @@ int mdgl_build_csr(const int32_t* key, const int32_t* other, int64_t num_edges, 
                    int64_t workspace_bytes, void* stream);
 int64_t mdgl_build_csr_workspace_bytes(int64_t num_edges, int64_t num_rows);
 
+/* Backward helpers. The reference has no backward pass (README.md:110-114); these
+ * are the elementwise steps of the gradients of gspmm / gsddmm / edge_softmax
+ * whose reductions run through the forward entry points above.
+ *
+ * mdgl_gspmm_edge_grad: the gradient reaching each edge's message from
+ *   grad_out (num_rows x d, rows indexed by vids[e], the destination):
+ *   dst[e, k] = alpha * grad_out[v, k] / (mean ? max(indptr[v+1] - indptr[v], 1) : 1)
+ *               * (arg_e ? (arg_e[v, k] == e) : 1)
+ *   arg_e (num_rows x d int32, from a max / min mdgl_gspmm) may be null. */
+int mdgl_gspmm_edge_grad(const int32_t* vids, const int32_t* indptr, const void* grad_out,
+                         const int32_t* arg_e, void* dst, int64_t num_edges, int64_t d, int mean,
+                         double alpha, int dtype, void* stream);
+
+/* dst[r, k] = src[r, k] / max(indptr[r+1] - indptr[r], 1): the mean's divisor on a
+ * node-shaped gradient. */
+int mdgl_rows_by_degree(const int32_t* indptr, const void* src, void* dst, int64_t rows,
+                        int64_t d, int dtype, void* stream);
+
+/* dst[i] = alpha * src[i]. */
+int mdgl_scale(const void* src, void* dst, int64_t n, double alpha, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

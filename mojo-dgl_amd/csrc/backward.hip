@@ -1,0 +1,113 @@
+// Elementwise pieces of the backward passes of gspmm / gsddmm /
+// edge_softmax. The reductions of those passes run through the forward
+// kernels (gspmm over the in- or out-CSR, gsddmm over the edges); what they
+// cannot express lives here:
+//
+//   edge_grad:   m[e, k] = alpha * g[v(e), k] / (mean ? max(deg v(e), 1) : 1)
+//                          * (arg_e ? [arg_e[v(e), k] == e] : 1)
+//                the message gradient of a max / min (only the arg edge of an
+//                output element receives it) or mean reduction, per edge;
+//   rows_by_degree: y[r, k] = x[r, k] / max(indptr[r + 1] - indptr[r], 1)
+//                (the mean's divisor applied to a node-shaped gradient);
+//   scale:       y = alpha * x (alpha = -1 for the sub / div gradients).
+//
+// One multiply, divide or select per element, so the results are exact
+// functions of the inputs (no order-dependent sums).
+#include "mdgl_kernels.h"
+
+namespace mdgl {
+
+namespace {
+
+unsigned grid_n(int64_t n) {
+  int64_t b = (n + BLOCK - 1) / BLOCK;
+  if (b > 65536) b = 65536;
+  return (unsigned)(b < 1 ? 1 : b);
+}
+
+template <class T>
+__global__ __launch_bounds__(BLOCK) void edge_grad_kernel(
+    const int32_t* __restrict__ vids, const int32_t* __restrict__ indptr,
+    const T* __restrict__ g, const int32_t* __restrict__ arg_e, T* __restrict__ m,
+    int64_t num_edges, int64_t d, T alpha, int mean) {
+  const int64_t total = num_edges * d;
+  for (int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * BLOCK) {
+    const int64_t e = i / d, k = i % d;
+    const int64_t v = vids[e];
+    T x = g[v * d + k];
+    if (mean) {
+      const int32_t deg = indptr[v + 1] - indptr[v];
+      x = x / T(deg > 1 ? deg : 1);
+    }
+    if (arg_e && arg_e[v * d + k] != (int32_t)e) x = T(0);
+    m[i] = alpha * x;
+  }
+}
+
+template <class T>
+__global__ __launch_bounds__(BLOCK) void rows_by_degree_kernel(const int32_t* __restrict__ indptr,
+                                                               const T* __restrict__ x,
+                                                               T* __restrict__ y, int64_t rows,
+                                                               int64_t d) {
+  const int64_t total = rows * d;
+  for (int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * BLOCK) {
+    const int64_t r = i / d;
+    const int32_t deg = indptr[r + 1] - indptr[r];
+    y[i] = x[i] / T(deg > 1 ? deg : 1);
+  }
+}
+
+template <class T>
+__global__ __launch_bounds__(BLOCK) void scale_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                      int64_t n, T alpha) {
+  for (int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * BLOCK)
+    y[i] = alpha * x[i];
+}
+
+}  // namespace
+
+hipError_t launch_edge_grad(const int32_t* vids, const int32_t* indptr, const void* g,
+                            const int32_t* arg_e, void* m, int64_t num_edges, int64_t d,
+                            double alpha, int mean, int dtype, hipStream_t s) {
+  const int64_t n = num_edges * d;
+  if (n <= 0) return hipSuccess;
+  if (dtype == 0)
+    hipLaunchKernelGGL(edge_grad_kernel<float>, dim3(grid_n(n)), dim3(BLOCK), 0, s, vids, indptr,
+                       static_cast<const float*>(g), arg_e, static_cast<float*>(m), num_edges, d,
+                       (float)alpha, mean);
+  else
+    hipLaunchKernelGGL(edge_grad_kernel<double>, dim3(grid_n(n)), dim3(BLOCK), 0, s, vids,
+                       indptr, static_cast<const double*>(g), arg_e, static_cast<double*>(m),
+                       num_edges, d, alpha, mean);
+  return hipGetLastError();
+}
+
+hipError_t launch_rows_by_degree(const int32_t* indptr, const void* x, void* y, int64_t rows,
+                                 int64_t d, int dtype, hipStream_t s) {
+  const int64_t n = rows * d;
+  if (n <= 0) return hipSuccess;
+  if (dtype == 0)
+    hipLaunchKernelGGL(rows_by_degree_kernel<float>, dim3(grid_n(n)), dim3(BLOCK), 0, s, indptr,
+                       static_cast<const float*>(x), static_cast<float*>(y), rows, d);
+  else
+    hipLaunchKernelGGL(rows_by_degree_kernel<double>, dim3(grid_n(n)), dim3(BLOCK), 0, s, indptr,
+                       static_cast<const double*>(x), static_cast<double*>(y), rows, d);
+  return hipGetLastError();
+}
+
+hipError_t launch_scale(const void* x, void* y, int64_t n, double alpha, int dtype,
+                        hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  if (dtype == 0)
+    hipLaunchKernelGGL(scale_kernel<float>, dim3(grid_n(n)), dim3(BLOCK), 0, s,
+                       static_cast<const float*>(x), static_cast<float*>(y), n, (float)alpha);
+  else
+    hipLaunchKernelGGL(scale_kernel<double>, dim3(grid_n(n)), dim3(BLOCK), 0, s,
+                       static_cast<const double*>(x), static_cast<double*>(y), n, alpha);
+  return hipGetLastError();
+}
+
+}  // namespace mdgl

@@ -181,6 +181,37 @@ int mdgl_build_csr(const int32_t* key, const int32_t* other, int64_t num_edges, 
                     "build_csr");
 }
 
+int mdgl_gspmm_edge_grad(const int32_t* vids, const int32_t* indptr, const void* grad_out,
+                         const int32_t* arg_e, void* dst, int64_t num_edges, int64_t d, int mean,
+                         double alpha, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "gspmm_edge_grad: bad dtype %d", dtype);
+  if (num_edges < 0 || d < 0) return fail(MDGL_EINVAL, "gspmm_edge_grad: negative size");
+  if (num_edges >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "gspmm_edge_grad: 2**31 or more edges");
+  if (num_edges == 0 || d == 0) return MDGL_OK;
+  if (!vids || !grad_out || !dst || (mean && !indptr))
+    return fail(MDGL_EINVAL, "gspmm_edge_grad: null buffer");
+  return hip_status(launch_edge_grad(vids, indptr, grad_out, arg_e, dst, num_edges, d, alpha,
+                                     mean, dtype, (hipStream_t)stream),
+                    "gspmm_edge_grad");
+}
+
+int mdgl_rows_by_degree(const int32_t* indptr, const void* src, void* dst, int64_t rows,
+                        int64_t d, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "rows_by_degree: bad dtype %d", dtype);
+  if (rows < 0 || d < 0) return fail(MDGL_EINVAL, "rows_by_degree: negative size");
+  if (rows == 0 || d == 0) return MDGL_OK;
+  if (!indptr || !src || !dst) return fail(MDGL_EINVAL, "rows_by_degree: null buffer");
+  return hip_status(launch_rows_by_degree(indptr, src, dst, rows, d, dtype, (hipStream_t)stream),
+                    "rows_by_degree");
+}
+
+int mdgl_scale(const void* src, void* dst, int64_t n, double alpha, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "scale: bad dtype %d", dtype);
+  if (n < 0) return fail(MDGL_EINVAL, "scale: n must be >= 0");
+  if (n > 0 && (!src || !dst)) return fail(MDGL_EINVAL, "scale: null buffer");
+  return hip_status(launch_scale(src, dst, n, alpha, dtype, (hipStream_t)stream), "scale");
+}
+
 int mdgl_replace_inf_with_zero(const void* src, void* dst, int64_t n, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "replace_inf_with_zero: bad dtype %d", dtype);
   if (n < 0) return fail(MDGL_EINVAL, "replace_inf_with_zero: n must be >= 0");

@@ -126,6 +126,14 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather);
 hipError_t launch_replace_inf(const void* src, void* dst, int64_t n, int dtype, hipStream_t s);
 hipError_t launch_clamp_i64(const int64_t* src, int64_t* dst, int64_t n, int64_t lo, int64_t hi,
                             hipStream_t s);
+// Backward helpers (backward.hip).
+hipError_t launch_edge_grad(const int32_t* vids, const int32_t* indptr, const void* g,
+                            const int32_t* arg_e, void* m, int64_t num_edges, int64_t d,
+                            double alpha, int mean, int dtype, hipStream_t s);
+hipError_t launch_rows_by_degree(const int32_t* indptr, const void* x, void* y, int64_t rows,
+                                 int64_t d, int dtype, hipStream_t s);
+hipError_t launch_scale(const void* x, void* y, int64_t n, double alpha, int dtype,
+                        hipStream_t s);
 // COO -> CSR by `key` (csr.hip).
 int64_t csr_workspace_bytes(int64_t num_edges, int64_t num_rows);
 hipError_t launch_build_csr(const int32_t* key, const int32_t* other, int64_t num_edges,

@@ -80,6 +80,9 @@ _SIGNATURES = {
     "mdgl_gather_mm_workspace_bytes": ([_I64, _I64, _I64, _I64, _C], _I64),
     "mdgl_build_csr": ([_P, _P, _I64, _I64, _P, _P, _P, _P, _I64, _P], _C),
     "mdgl_build_csr_workspace_bytes": ([_I64, _I64], _I64),
+    "mdgl_gspmm_edge_grad": ([_P, _P, _P, _P, _P, _I64, _I64, _C, ctypes.c_double, _C, _P], _C),
+    "mdgl_rows_by_degree": ([_P, _P, _P, _I64, _I64, _C, _P], _C),
+    "mdgl_scale": ([_P, _P, _I64, ctypes.c_double, _C, _P], _C),
 }
 
 

@@ -37,6 +37,7 @@ from .base import DGLError, is_all
 from .function.base import TargetCode
 from .function.message import BinaryMessageFunction, CopyMessageFunction, MessageFunction
 from .function.reducer import ReduceFunction
+from .ops import _autograd
 from .ops import spmm as _spmm
 from .ops._plan import SoftmaxPlan
 from .ops.sddmm import gsddmm
@@ -403,8 +404,11 @@ class DGLGraph(object):
 
     def _reduce(self, op, reduce_op, lhs, rhs):
         """gspmm whose max/min results get +-inf -> 0, as message passing wants."""
+        replace_inf = reduce_op in ("max", "min")
+        if _autograd.needs_grad(lhs, rhs):
+            return _autograd.GSpMM.apply(self, op, reduce_op, lhs, rhs, replace_inf)
         out, _, _, as_torch, dev = _spmm._run(self, op, reduce_op, lhs, rhs,
-                                              replace_inf=reduce_op in ("max", "min"))
+                                              replace_inf=replace_inf)
         return _lib.give_back(out, as_torch, dev)
 
     def _pass(self, message_func, reduce_func, apply_node_func, write=True):

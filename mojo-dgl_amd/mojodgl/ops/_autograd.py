@@ -1,0 +1,298 @@
+"""Backward passes of gspmm, gsddmm and edge_softmax for torch autograd.
+
+The reference has no backward pass (its README.md:110-114 leaves autograd out);
+these follow the calculus of the forward ops and run on the same kernels:
+
+* gspmm(op, reduce) with node operand X, edge operand Y, output gradient G:
+  - sum / mean: the gradient reaching edge e = (u, v) is G[v] (divided by
+    max(deg v, 1) for mean: ``mdgl_rows_by_degree`` on G first);
+    dX[u] = sum over u's out-edges of that gradient times d msg / dX, a
+    gspmm over the out-CSR (copy for copy_lhs / add / sub, mul / div by Y for
+    mul / div); dY[e] = gradient times d msg / dY, a gsddmm (copy of G[v],
+    its negation for sub, X[u] * G[v] for mul -- a per-head dot when Y
+    broadcasts over X's trailing axes --, -X[u] G[v] / Y[e]^2 for div);
+  - max / min: only the arg edge of an output element receives its
+    gradient: ``mdgl_gspmm_edge_grad`` writes the masked per-edge gradient M,
+    then dX is a gspmm over the out-CSR of M (times d msg / dX) and dY is M
+    times d msg / dY, per edge;
+* gsddmm(op, X at target tx, Y at target ty): the per-edge gradient times
+  d op / dX (dY) is reduced over the edges of each node of the operand's
+  target by a gspmm copy_rhs sum (in-CSR for v, out-CSR for u; nothing for e);
+* edge_softmax: dX = a * (G - s[row]) with s[row] = sum over the row of G * a:
+  gsddmm e_mul_e, gspmm copy_rhs sum over the CSR of norm_by, gsddmm e_sub_v
+  (e_sub_u for norm_by='src'), gsddmm e_mul_e.
+
+Gradients come back in the operand's shape: an operand broadcast along its
+trailing feature axes gets its gradient summed over them (a segmented sum,
+``segment_reduce``); other broadcast layouts raise DGLError in backward.
+Only torch tensors take part (numpy operands have no autograd).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from .. import _lib
+from ..base import DGLError
+
+__all__ = ["needs_grad", "GSpMM", "GSDDMM", "EdgeSoftmax"]
+
+
+def needs_grad(*xs) -> bool:
+    return torch.is_grad_enabled() and any(
+        isinstance(x, torch.Tensor) and x.requires_grad for x in xs)
+
+
+def _code(t):
+    return 0 if t.dtype == torch.float32 else 1
+
+
+def _scale(t, alpha):
+    t = t.contiguous()
+    out = torch.empty_like(t)
+    _lib.check(_lib.lib().mdgl_scale(t.data_ptr(), out.data_ptr(), t.numel(), float(alpha),
+                                     _code(t), _lib.stream()), "scale")
+    return out
+
+
+def _rows_by_degree(csr, x):
+    x = x.contiguous()
+    out = torch.empty_like(x)
+    rows = x.shape[0]
+    d = x.numel() // max(rows, 1)
+    _lib.check(_lib.lib().mdgl_rows_by_degree(csr.indptr.data_ptr(), x.data_ptr(),
+                                              out.data_ptr(), rows, d, _code(x), _lib.stream()),
+               "rows_by_degree")
+    return out
+
+
+def _edge_grad(g, grad, arg_e, mean, alpha):
+    """Per-edge gradient of a max / min / mean gspmm (see the module doc)."""
+    grad = grad.contiguous()
+    E = g.number_of_edges()
+    d = grad.numel() // max(grad.shape[0], 1)
+    out = torch.empty((E,) + tuple(grad.shape[1:]), dtype=grad.dtype, device=grad.device)
+    _, vids = g._device_coo()
+    csr = g._device_csr("in")
+    ae = None if arg_e is None else arg_e.to(torch.int32).contiguous()
+    _lib.check(_lib.lib().mdgl_gspmm_edge_grad(
+        vids.data_ptr(), csr.indptr.data_ptr(), grad.data_ptr(), _lib.ptr(ae), out.data_ptr(), E,
+        d, 1 if mean else 0, float(alpha), _code(grad), _lib.stream()), "gspmm_edge_grad")
+    return out
+
+
+def _gspmm(g, op, red, x, y, kind="in"):
+    from .spmm import _run
+
+    out, _, _, _, _ = _run(g, op, red, x, y, kind=kind)
+    return out
+
+
+def _gsddmm(g, op, x, y, tx, ty):
+    from .sddmm import gsddmm
+
+    return gsddmm(g, op, x, y, lhs_target=tx, rhs_target=ty)
+
+
+def _node_reduce(g, p, target):
+    """Sum a per-edge tensor over the edges of each node of `target`."""
+    if target == "e":
+        return p
+    return _gspmm(g, "copy_rhs", "sum", None, p, kind="in" if target == "v" else "out")
+
+
+def _reduce_to(t, shape):
+    """Sum `t` (rows, *full) down to `shape` (rows, *part): `part` must equal
+    `full` up to trailing axes of size one (after left padding with ones)."""
+    shape = tuple(shape)
+    if tuple(t.shape) == shape:
+        return t
+    rows = t.shape[0]
+    full = tuple(t.shape[1:])
+    part = shape[1:] if len(shape) > 1 else (1,)
+    pad = (1,) * (len(full) - len(part)) + tuple(part)
+    keep = len(pad)
+    while keep > 0 and pad[keep - 1] == 1 and full[keep - 1] != 1:
+        keep -= 1
+    if pad[:keep] != full[:keep] or any(p != 1 for p in pad[keep:]):
+        raise DGLError("backward of an operand broadcast along {} -> {} is not supported "
+                       "(only trailing broadcast axes)".format(part, full))
+    inner = int(np.prod(full[keep:], dtype=np.int64))
+    from .segment import segment_reduce
+
+    flat = t.contiguous().reshape(-1, 1)
+    seg = torch.full((flat.shape[0] // inner,), inner, dtype=torch.int64, device=t.device)
+    out = segment_reduce(seg, flat, "sum")
+    return out.reshape((rows,) + tuple(shape[1:]))
+
+
+def _fix_shape(grad, like):
+    return grad.reshape(like.shape)
+
+
+class GSpMM(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, g, op, red, x, y, replace_inf):
+        from .spmm import _run
+
+        out, _, arg_e, _, _ = _run(g, op, red, x, y, replace_inf=replace_inf,
+                                   want_arg=red in ("max", "min"), arg_dtype=torch.int32)
+        ctx.g, ctx.op, ctx.red = g, op, red
+        ctx.save_for_backward(x if isinstance(x, torch.Tensor) else None,
+                              y if isinstance(y, torch.Tensor) else None, arg_e)
+        ctx.out_shape = out.shape
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        g, op, red = ctx.g, ctx.op, ctx.red
+        x, y, arg_e = ctx.saved_tensors
+        G = grad_out.contiguous()
+        need_x = ctx.needs_input_grad[3] and x is not None
+        need_y = ctx.needs_input_grad[4] and y is not None
+        dx = dy = None
+        if red in ("sum", "mean"):
+            if red == "mean":
+                G = _rows_by_degree(g._device_csr("in"), G)
+            if need_x:
+                if op in ("copy_lhs", "add", "sub"):
+                    dx = _gspmm(g, "copy_lhs", "sum", G, None, kind="out")
+                else:
+                    dx = _gspmm(g, op, "sum", G, y, kind="out")
+                dx = _reduce_to(dx, _padded(x.shape, dx.shape))
+            if need_y:
+                if op in ("copy_rhs", "add"):
+                    dy = _gsddmm(g, "copy_lhs", G, None, "v", "v")
+                elif op == "sub":
+                    dy = _scale(_gsddmm(g, "copy_lhs", G, None, "v", "v"), -1.0)
+                elif op == "mul":
+                    dy = _mul_grad(g, x, G, y.shape)
+                else:  # div: -x[u] g[v] / y^2
+                    t = _gsddmm(g, "mul", x, G, "u", "v")
+                    t = _gsddmm(g, "div", t, y, "e", "e")
+                    dy = _scale(_gsddmm(g, "div", t, y, "e", "e"), -1.0)
+                dy = _reduce_to(dy, _padded(y.shape, dy.shape))
+        else:
+            M = _edge_grad(g, G, arg_e, False, 1.0)
+            if need_x:
+                if op in ("copy_lhs", "add", "sub"):
+                    p = M
+                else:
+                    p = _gsddmm(g, op, M, y, "e", "e")
+                dx = _reduce_to(_node_reduce(g, p, "u"), _padded(x.shape, M.shape))
+            if need_y:
+                if op in ("copy_rhs", "add"):
+                    dy = M
+                elif op == "sub":
+                    dy = _scale(M, -1.0)
+                elif op == "mul":
+                    dy = _gsddmm(g, "mul", x, M, "u", "e")
+                else:
+                    t = _gsddmm(g, "mul", x, M, "u", "e")
+                    t = _gsddmm(g, "div", t, y, "e", "e")
+                    dy = _scale(_gsddmm(g, "div", t, y, "e", "e"), -1.0)
+                dy = _reduce_to(dy, _padded(y.shape, dy.shape))
+        if dx is not None:
+            dx = dx.reshape(x.shape)
+        if dy is not None:
+            dy = dy.reshape(y.shape)
+        return None, None, None, dx, dy, None
+
+
+def _padded(shape, full):
+    """`shape` with ones inserted after the first axis to the rank of `full`."""
+    shape = tuple(shape)
+    if len(shape) == 1:
+        shape = shape + (1,)
+    nd = len(full)
+    if len(shape) < nd:
+        shape = (shape[0],) + (1,) * (nd - len(shape)) + shape[1:]
+    return shape
+
+
+def _mul_grad(g, x, G, yshape):
+    """dY of a u_mul_e gspmm: x[u] * G[v] per edge, summed over the axes where
+    Y broadcasts; when those are X's trailing axes, a per-edge dot."""
+    full = G.shape[1:]
+    ypad = _padded(yshape, G.shape)[1:]
+    keep = len(ypad)
+    while keep > 0 and ypad[keep - 1] == 1 and full[keep - 1] != 1:
+        keep -= 1
+    if keep < len(ypad) and tuple(ypad[:keep]) == tuple(full[:keep]) \
+            and tuple(x.shape[1:]) == tuple(full):
+        inner = int(np.prod(full[keep:], dtype=np.int64))
+        lead = tuple(full[:keep])
+        xs = x.reshape((x.shape[0],) + lead + (inner,))
+        gs = G.reshape((G.shape[0],) + lead + (inner,))
+        return _gsddmm(g, "dot", xs, gs, "u", "v")
+    return _gsddmm(g, "mul", x, G, "u", "v")
+
+
+class GSDDMM(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, g, op, x, y, tx, ty):
+        from .sddmm import gsddmm
+
+        out = gsddmm(g, op, x, y, lhs_target=tx, rhs_target=ty)
+        ctx.g, ctx.op, ctx.tx, ctx.ty = g, op, tx, ty
+        ctx.save_for_backward(x if isinstance(x, torch.Tensor) else None,
+                              y if isinstance(y, torch.Tensor) else None)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        g, op, tx, ty = ctx.g, ctx.op, ctx.tx, ctx.ty
+        x, y = ctx.saved_tensors
+        G = grad_out.contiguous()
+        need_x = ctx.needs_input_grad[2] and x is not None
+        need_y = ctx.needs_input_grad[3] and y is not None
+        dx = dy = None
+        if need_x:
+            if op in ("copy_lhs", "add", "sub"):
+                p = G
+            elif op in ("mul", "dot"):
+                p = _gsddmm(g, "mul", G, y, "e", ty)
+            else:
+                p = _gsddmm(g, "div", G, y, "e", ty)
+            p = _node_reduce(g, p, tx)
+            dx = _reduce_to(p, _padded(x.shape, p.shape)).reshape(x.shape)
+        if need_y:
+            if op in ("copy_rhs", "add"):
+                p = G
+            elif op == "sub":
+                p = _scale(G, -1.0)
+            elif op in ("mul", "dot"):
+                p = _gsddmm(g, "mul", G, x, "e", tx)
+            else:  # div: -G x / y^2
+                t = _gsddmm(g, "mul", G, x, "e", tx)
+                t = _gsddmm(g, "div", t, y, "e", ty)
+                p = _scale(_gsddmm(g, "div", t, y, "e", ty), -1.0)
+            p = _node_reduce(g, p, ty)
+            dy = _reduce_to(p, _padded(y.shape, p.shape)).reshape(y.shape)
+        return None, None, dx, dy, None, None
+
+
+class EdgeSoftmax(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, g, logits, norm_by):
+        from .edge_softmax import _edge_softmax
+
+        out = _edge_softmax(g, logits, None, norm_by)
+        ctx.g, ctx.norm_by = g, norm_by
+        ctx.save_for_backward(out)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        g, norm_by = ctx.g, ctx.norm_by
+        (a,) = ctx.saved_tensors
+        E = a.shape[0]
+        a2 = a.reshape(E, -1)
+        G = grad_out.contiguous().reshape(E, -1)
+        p = _gsddmm(g, "mul", G, a2, "e", "e")
+        row = "v" if norm_by == "dst" else "u"
+        s = _node_reduce(g, p, row)
+        dlt = _gsddmm(g, "sub", G, s, "e", row)
+        dx = _gsddmm(g, "mul", dlt, a2, "e", "e")
+        return None, dx.reshape(a.shape), None

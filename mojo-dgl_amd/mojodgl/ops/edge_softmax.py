@@ -16,7 +16,7 @@ import torch
 
 from .. import _lib, heterograph
 from ..base import ALL, DGLError, is_all
-from . import _plan
+from . import _autograd, _plan
 
 __all__ = ["edge_softmax"]
 
@@ -43,7 +43,8 @@ def edge_softmax(graph, logits, eids=ALL, norm_by="dst"):
 
     Returns
     -------
-    Softmax values, of the same shape as ``logits``.
+    Softmax values, of the same shape as ``logits``. With a torch tensor that
+    requires grad (and eids=ALL) the result takes part in autograd.
 
     Examples
     --------
@@ -56,6 +57,20 @@ def edge_softmax(graph, logits, eids=ALL, norm_by="dst"):
            [0.33333333],
            [0.33333333]])
     """
+    if _autograd.needs_grad(logits):
+        if not is_all(eids):
+            raise DGLError("backward through edge_softmax over a subset of eids is not "
+                           "supported; pass eids=ALL")
+        if norm_by not in ("dst", "src"):
+            raise DGLError("norm_by must be 'src' or 'dst'")
+        return _autograd.EdgeSoftmax.apply(graph, logits, norm_by)
+    return _edge_softmax(graph, logits, eids, norm_by)
+
+
+def _edge_softmax(graph, logits, eids, norm_by):
+    """edge_softmax without autograd (`eids` None or ALL means every edge)."""
+    if eids is None:
+        eids = ALL
     num_edges = graph.number_of_edges()
     X = _lib.feature(logits)
     shape = X.shape

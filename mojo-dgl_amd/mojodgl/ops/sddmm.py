@@ -17,6 +17,7 @@ import torch
 from .. import _lib
 from .._lib import BINARY_OPS, OP_COPY_LHS, OP_COPY_RHS, TARGETS
 from ..base import DGLError
+from . import _autograd
 
 __all__ = ["gsddmm", "copy_u", "copy_v", "copy_e"]
 
@@ -115,12 +116,15 @@ def gsddmm(g, op, lhs_data, rhs_data, lhs_target="u", rhs_target="v"):
     Returns
     -------
     Edge features of shape ``(E,) + broadcast feature shape`` (``(E, ..., 1)``
-    for dot), a numpy array or, when an operand is a tensor, a tensor.
+    for dot), a numpy array or, when an operand is a tensor, a tensor (which
+    takes part in autograd when an operand requires grad).
     """
     num_edges = g.number_of_edges()
     num_nodes = g.number_of_nodes()
     if lhs_target not in TARGETS or rhs_target not in TARGETS:
         raise DGLError("lhs_target/rhs_target must be one of 'u', 'v', 'e'")
+    if _autograd.needs_grad(lhs_data, rhs_data):
+        return _autograd.GSDDMM.apply(g, op, lhs_data, rhs_data, lhs_target, rhs_target)
     L = R = None
     if op == "copy_lhs":
         L = _lib.feature(lhs_data)

@@ -15,6 +15,7 @@ import torch
 
 from .. import _lib
 from .._lib import BINARY_OPS, OP_COPY_LHS, OP_COPY_RHS, REDUCERS
+from . import _autograd
 from ..base import DGLError
 from .sddmm import _check_rows, feat_shape, out_feat_shape, reshape_lhs_rhs, shape_args, width
 
@@ -22,9 +23,11 @@ __all__ = ["gspmm"]
 
 
 def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False,
-         arg_dtype=torch.int64):
+         arg_dtype=torch.int64, kind="in"):
     """Validate, launch, and return device tensors (out, arg_u, arg_e) plus
-    the caller-container info."""
+    the caller-container info. `kind` "out" reduces over the out-CSR instead
+    (the reversed graph: rows are sources, the node operand is read at the
+    destinations), which the backward passes use."""
     if reduce_op not in REDUCERS:
         raise DGLError("reduce_op {} not recognized".format(reduce_op))
     if op not in list(BINARY_OPS) + ["copy_lhs", "copy_rhs"]:
@@ -71,7 +74,7 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
             nd, ls, rs = shape_args(L.shape, R.shape)
         lhs = _lib.on_device(L, dtype) if L is not None else None
         rhs = _lib.on_device(R, dtype) if R is not None else None
-        csr = g._device_csr("in")
+        csr = g._device_csr(kind)
         sched = csr.chunks
         ws = None
         nbytes = _lib.lib().mdgl_gspmm_workspace_bytes(sched.num_chunks, dout,
@@ -119,8 +122,11 @@ def gspmm(g, op, reduce_op, lhs_data, rhs_data):
     Returns
     -------
     Node features of shape ``(N,) + broadcast feature shape``. A node with no
-    in-edges gets 0 (sum, mean), -inf (max) or +inf (min).
+    in-edges gets 0 (sum, mean), -inf (max) or +inf (min). With torch tensors
+    that require grad the result takes part in autograd.
     """
+    if _autograd.needs_grad(lhs_data, rhs_data):
+        return _autograd.GSpMM.apply(g, op, reduce_op, lhs_data, rhs_data, False)
     out, _, _, as_torch, dev = _run(g, op, reduce_op, lhs_data, rhs_data)
     return _lib.give_back(out, as_torch, dev)
 

@@ -104,6 +104,19 @@ def test_build_csr_arguments(lib):
     assert lib.mdgl_build_csr_workspace_bytes(-1, 3) == -1
 
 
+def test_backward_helper_arguments(lib):
+    assert lib.mdgl_gspmm_edge_grad(None, None, None, None, None, 5, 3, 0, 1.0, 9, None) == -1
+    assert lib.mdgl_gspmm_edge_grad(None, None, None, None, None, -1, 3, 0, 1.0, 0, None) == -1
+    rc = lib.mdgl_gspmm_edge_grad(None, None, None, None, None, 5, 3, 1, 1.0, 0, None)
+    assert rc == -1 and "null" in err(lib)
+    assert lib.mdgl_gspmm_edge_grad(None, None, None, None, None, 0, 3, 1, 1.0, 0, None) == 0
+    assert lib.mdgl_rows_by_degree(None, None, None, 4, 2, 0, None) == -1
+    assert lib.mdgl_rows_by_degree(None, None, None, 0, 2, 0, None) == 0
+    assert lib.mdgl_scale(None, None, 4, -1.0, 0, None) == -1
+    assert lib.mdgl_scale(None, None, 0, -1.0, 0, None) == 0
+    assert lib.mdgl_scale(None, None, 4, -1.0, 5, None) == -1
+
+
 def test_workspace_sizes(lib):
     assert lib.mdgl_gspmm_workspace_bytes(0, 64, 0, 0) == 0
     assert lib.mdgl_gspmm_workspace_bytes(10, 64, 0, 0) >= 10 * 64 * 4

@@ -1,0 +1,225 @@
+"""Backward passes of gspmm / gsddmm / edge_softmax on the GPU.
+
+The reference has no backward (README.md:110-114), so there is no oracle
+vector to match; the gradients are pinned by the mathematics instead:
+- against torch's autograd through a float64 restatement of each forward op
+  written with plain tensor indexing (index_add_, scatter_reduce), on graphs
+  where every node has in- and out-edges and values have no ties;
+- against finite differences (torch.autograd.gradcheck, float64).
+Tolerance: float64 gradients agree to rtol 1e-9 / atol 1e-12 (sums are
+formed in a different order); the float32 GAT chain to rtol 1e-4 / atol 1e-5
+of the float64 chain.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import mojodgl as dgl
+import mojodgl.function as fn
+import mojodgl.ops as ops
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def graph_with_loops(n, e, seed):
+    """Random edges plus a self loop on every node (no empty rows)."""
+    rng = np.random.default_rng(seed)
+    u = np.concatenate([rng.integers(0, n, e), np.arange(n)])
+    v = np.concatenate([rng.integers(0, n, e), np.arange(n)])
+    perm = rng.permutation(u.size)
+    return u[perm], v[perm]
+
+
+def leaf(shape, seed, positive=False, dtype=torch.float64):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    t = torch.randn(shape, generator=g, device=DEV, dtype=dtype)
+    if positive:
+        t = t.abs() + 0.5
+    return t.requires_grad_(True)
+
+
+def pad(x, nd):
+    return x.reshape((x.shape[0],) + (1,) * (nd - x.dim()) + tuple(x.shape[1:]))
+
+
+def ref_message(op, xu, ye):
+    if op == "copy_lhs":
+        return xu
+    if op == "copy_rhs":
+        return ye
+    nd = max(xu.dim(), ye.dim())
+    xu, ye = pad(xu, nd), pad(ye, nd)
+    return {"add": xu + ye, "sub": xu - ye, "mul": xu * ye, "div": xu / ye}[op]
+
+
+def ref_spmm(u, v, n, op, red, x, y):
+    ud = torch.from_numpy(u).to(DEV)
+    vd = torch.from_numpy(v).to(DEV)
+    m = ref_message(op, x[ud] if x is not None else None, y)
+    out = torch.zeros((n,) + tuple(m.shape[1:]), dtype=m.dtype, device=DEV)
+    idx = vd.reshape((-1,) + (1,) * (m.dim() - 1)).expand_as(m)
+    if red in ("sum", "mean"):
+        out = out.index_add(0, vd, m)
+        if red == "mean":
+            deg = torch.bincount(vd, minlength=n).clamp(min=1).to(m.dtype)
+            out = out / deg.reshape((-1,) + (1,) * (m.dim() - 1))
+        return out
+    return out.scatter_reduce(0, idx, m, "amax" if red == "max" else "amin", include_self=False)
+
+
+def grads(out, inputs, seed):
+    # the weights are drawn in float64 whatever the output dtype, so float32
+    # and float64 chains are weighted alike
+    w = torch.randn(out.shape, generator=torch.Generator(device=DEV).manual_seed(seed),
+                    device=DEV, dtype=torch.float64).to(out.dtype)
+    live = [t for t in inputs if t is not None]
+    return torch.autograd.grad((out * w).sum(), live)
+
+
+def assert_grads(got, ref, rtol=1e-9, atol=1e-12):
+    assert len(got) == len(ref)
+    for a, b in zip(got, ref):
+        torch.testing.assert_close(a, b, rtol=rtol, atol=atol)
+
+
+# ------------------------------------------------------------------ gspmm
+@pytest.mark.parametrize("op", ["copy_lhs", "copy_rhs", "add", "sub", "mul", "div"])
+@pytest.mark.parametrize("red", ["sum", "mean", "max", "min"])
+@pytest.mark.parametrize("yshape", [(3, 4), (3, 1)], ids=["full", "trailing-broadcast"])
+def test_gspmm_backward(op, red, yshape):
+    if op == "copy_rhs" and yshape != (3, 4):
+        pytest.skip("copy_rhs has no broadcast")
+    n, e = 60, 700
+    u, v = graph_with_loops(n, e, 50)
+    E = u.size
+    g = dgl.graph((u, v), num_nodes=n)
+    x = leaf((n, 3, 4), 1) if op != "copy_rhs" else None
+    y = leaf((E,) + yshape, 2, positive=(op == "div")) if op != "copy_lhs" else None
+    out = ops.gspmm(g, op, red, x, y)
+    ref = ref_spmm(u, v, n, op, red, x, y)
+    torch.testing.assert_close(out, ref, rtol=1e-12, atol=1e-12)
+    assert_grads(grads(out, [x, y], 3), grads(ref, [x, y], 3))
+
+
+def test_gspmm_gradcheck():
+    n, e = 12, 40
+    u, v = graph_with_loops(n, e, 51)
+    g = dgl.graph((u, v), num_nodes=n)
+    x = leaf((n, 5), 4)
+    y = leaf((u.size, 5), 5)
+    assert torch.autograd.gradcheck(lambda a, b: ops.u_mul_e_sum(g, a, b), (x, y))
+    assert torch.autograd.gradcheck(lambda a, b: ops.u_add_e_mean(g, a, b), (x, y))
+    assert torch.autograd.gradcheck(lambda a, b: ops.u_mul_e_max(g, a, b), (x, y))
+
+
+# ------------------------------------------------------------------ gsddmm
+def ref_sddmm(u, v, op, x, y, tx, ty):
+    sel = {"u": torch.from_numpy(u).to(DEV), "v": torch.from_numpy(v).to(DEV)}
+    xa = x[sel[tx]] if tx != "e" else x
+    ya = y[sel[ty]] if ty != "e" else y
+    if op == "dot":
+        return (xa * ya).sum(-1, keepdim=True)
+    return ref_message(op, xa, ya)
+
+
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div", "dot"])
+@pytest.mark.parametrize("tx,ty", [("u", "v"), ("u", "e"), ("e", "v"), ("v", "u"), ("e", "e")])
+def test_gsddmm_backward(op, tx, ty):
+    n, e = 50, 600
+    u, v = graph_with_loops(n, e, 52)
+    E = u.size
+    g = dgl.graph((u, v), num_nodes=n)
+    x = leaf((E if tx == "e" else n, 2, 6), 6)
+    y = leaf((E if ty == "e" else n, 2, 6), 7, positive=(op == "div"))
+    out = ops.gsddmm(g, op, x, y, lhs_target=tx, rhs_target=ty)
+    ref = ref_sddmm(u, v, op, x, y, tx, ty)
+    torch.testing.assert_close(out, ref, rtol=1e-12, atol=1e-12)
+    assert_grads(grads(out, [x, y], 8), grads(ref, [x, y], 8))
+
+
+def test_gsddmm_copy_and_broadcast_backward():
+    n, e = 40, 300
+    u, v = graph_with_loops(n, e, 53)
+    g = dgl.graph((u, v), num_nodes=n)
+    x = leaf((n, 4, 3), 9)
+    out = ops.copy_u(g, x)
+    assert_grads(grads(out, [x], 10), grads(x[torch.from_numpy(u).to(DEV)], [x], 10))
+    el = leaf((n, 4, 1), 11)
+    er = leaf((n, 4, 1), 12)
+    out = ops.u_add_v(g, el, er)
+    ref = ref_sddmm(u, v, "add", el, er, "u", "v")
+    assert_grads(grads(out, [el, er], 13), grads(ref, [el, er], 13))
+
+
+# ------------------------------------------------------------------ edge_softmax
+def ref_edge_softmax(u, v, n, logits, norm_by):
+    key = torch.from_numpy(v if norm_by == "dst" else u).to(DEV)
+    flat = logits.reshape(logits.shape[0], -1)
+    idx = key[:, None].expand_as(flat)
+    mx = torch.full((n, flat.shape[1]), -float("inf"), dtype=flat.dtype, device=DEV)
+    mx = mx.scatter_reduce(0, idx, flat, "amax", include_self=True)
+    ex = torch.exp(flat - mx[key])
+    s = torch.zeros((n, flat.shape[1]), dtype=flat.dtype, device=DEV).index_add(0, key, ex)
+    return (ex / s[key]).reshape(logits.shape)
+
+
+@pytest.mark.parametrize("norm_by", ["dst", "src"])
+@pytest.mark.parametrize("shape", [(), (1,), (4, 1)])
+def test_edge_softmax_backward(norm_by, shape):
+    n, e = 70, 900
+    u, v = graph_with_loops(n, e, 54)
+    g = dgl.graph((u, v), num_nodes=n)
+    logits = leaf((u.size,) + shape, 14)
+    out = ops.edge_softmax(g, logits, norm_by=norm_by)
+    ref = ref_edge_softmax(u, v, n, logits, norm_by)
+    torch.testing.assert_close(out, ref, rtol=1e-12, atol=1e-14)
+    assert_grads(grads(out, [logits], 15), grads(ref, [logits], 15))
+    small_u, small_v = graph_with_loops(10, 30, 55)
+    gs = dgl.graph((small_u, small_v), num_nodes=10)
+    z = leaf((small_u.size, 2, 1), 16)
+    assert torch.autograd.gradcheck(lambda t: ops.edge_softmax(gs, t, norm_by=norm_by), (z,))
+
+
+def test_edge_softmax_subset_backward_is_refused():
+    u, v = graph_with_loops(10, 30, 56)
+    g = dgl.graph((u, v), num_nodes=10)
+    z = leaf((u.size, 1), 17)
+    with pytest.raises(dgl.DGLError):
+        ops.edge_softmax(g, z, eids=np.arange(5))
+
+
+# ------------------------------------------------------------------ a GAT layer, float32
+def test_gat_layer_backward_float32():
+    """gsddmm u_add_v -> leaky_relu -> edge_softmax -> gspmm u_mul_e_sum, and
+    update_all with a max reducer, against the float64 torch chain."""
+    n, e, H, D = 400, 6000, 4, 8
+    u, v = graph_with_loops(n, e, 57)
+    g = dgl.graph((u, v), num_nodes=n)
+
+    def chain(el, er, h, mine):
+        if mine:
+            a = ops.edge_softmax(g, torch.nn.functional.leaky_relu(ops.u_add_v(g, el, er), 0.2))
+            return ops.u_mul_e_sum(g, h, a)
+        ev = ref_sddmm(u, v, "add", el, er, "u", "v")
+        a = ref_edge_softmax(u, v, n, torch.nn.functional.leaky_relu(ev, 0.2), "dst")
+        return ref_spmm(u, v, n, "mul", "sum", h, a)
+
+    el, er, h = leaf((n, H, 1), 18, dtype=torch.float32), leaf((n, H, 1), 19,
+                                                             dtype=torch.float32), \
+        leaf((n, H, D), 20, dtype=torch.float32)
+    got = grads(chain(el, er, h, True), [el, er, h], 21)
+    el64, er64, h64 = (t.detach().double().requires_grad_(True) for t in (el, er, h))
+    ref = grads(chain(el64, er64, h64, False), [el64, er64, h64], 21)
+    for a, b in zip(got, ref):
+        torch.testing.assert_close(a.double(), b, rtol=1e-4, atol=1e-5)
+
+    x = leaf((n, 6), 22)
+    g.ndata["x"] = x
+    g.edata["w"] = leaf((u.size, 6), 23)
+    g.update_all(fn.u_mul_e("x", "w", "m"), fn.max("m", "z"))
+    z = g.ndata["z"]
+    ref = ref_spmm(u, v, n, "mul", "max", x, g.edata["w"])
+    assert_grads(grads(z, [x, g.edata["w"]], 24), grads(ref, [x, g.edata["w"]], 24))
