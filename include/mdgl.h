@@ -128,14 +128,17 @@ int64_t mdgl_softmax_workspace_bytes(int64_t num_chunks, int64_t table_rows, int
 
 /* Replaces capi.mojo:132-138 (`mdgl_segment_softmax`): per segment and
  * column, softmax over the segment's rows; rows of empty segments are not
- * written. Segments are served in their own order; segments longer than
+ * written. Segments are served through the plan of mdgl_edge_softmax_
+ * (`order` / `bounds` / `nbins` by degree bin, or order null for every
+ * segment in its own order, one wavefront each); segments longer than
  * chunk_len come as chunks: chunk c covers rows chunk_start[c] ..
  * min(chunk_start[c] + chunk_len, offsets[chunk_row[c] + 1]) of segment
  * chunk_row[c], a segment's chunks are consecutive and chunk_first[c] is the
  * first of them. `slots` is the value mdgl_softmax_geometry returned.
  * `scratch` is accepted for signature compatibility and unused. */
 int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, void* scratch,
-                         int64_t num_seg, int64_t d, int64_t n, const int32_t* chunk_row,
+                         int64_t num_seg, int64_t d, int64_t n, const int32_t* order,
+                         const int64_t* bounds, int nbins, const int32_t* chunk_row,
                          const int32_t* chunk_start, const int32_t* chunk_first,
                          int64_t num_chunks, int64_t slots, void* workspace,
                          int64_t workspace_bytes, int dtype, void* stream);

@@ -591,7 +591,8 @@ int softmax_common(const char* what, const int32_t* indptr, const int32_t* eid,
 extern "C" {
 
 int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, void* scratch,
-                         int64_t num_seg, int64_t d, int64_t n, const int32_t* chunk_row,
+                         int64_t num_seg, int64_t d, int64_t n, const int32_t* order,
+                         const int64_t* bounds, int nbins, const int32_t* chunk_row,
                          const int32_t* chunk_start, const int32_t* chunk_first,
                          int64_t num_chunks, int64_t slots, void* workspace,
                          int64_t workspace_bytes, int dtype, void* stream) {
@@ -600,7 +601,7 @@ int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, v
   if (n >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "segment_softmax: 2**31 or more rows");
   if (n == 0) return MDGL_OK;
   return softmax_common("segment_softmax", offsets, nullptr, nullptr, value, dst, num_seg, d,
-                        nullptr, nullptr, 0, chunk_row, chunk_start, chunk_first, num_chunks,
+                        order, bounds, nbins, chunk_row, chunk_start, chunk_first, num_chunks,
                         slots, nullptr, 0, workspace, workspace_bytes, dtype, stream);
 }
 

@@ -51,6 +51,11 @@ __device__ __forceinline__ void fetch_rt(const T* __restrict__ row, int mode, co
   }
 }
 
+// A wavefront takes EW_U rounds of 64 / G edges (one slab of columns) and
+// requests every round's operand rows before it computes, so each lane has
+// 2 * EW_U row loads in flight.
+constexpr int EW_U = 4;
+
 template <class T, int OP, int VEC>
 __global__ __launch_bounds__(BLOCK) void gsddmm_kernel(GsddmmArgs<T> a) {
   const int64_t blk = xcd_remap(blockIdx.x, a.num_blocks);
@@ -60,9 +65,10 @@ __global__ __launch_bounds__(BLOCK) void gsddmm_kernel(GsddmmArgs<T> a) {
   const int G = a.G;
   const int grp = lane / G, gl = lane % G;
   const int64_t slab = wave % a.S;
-  const int64_t e = (wave / a.S) * (WAVE / G) + grp;
+  const int64_t per_round = WAVE / G;
+  const int64_t e0 = (wave / a.S) * EW_U * per_round + grp;
   const int64_t k0 = (slab * G + gl) * VEC;
-  if (e >= a.num_edges || k0 >= a.dout) return;
+  if (k0 >= a.dout) return;
 
   int loff[VEC], roff[VEC];
 #pragma unroll
@@ -71,25 +77,37 @@ __global__ __launch_bounds__(BLOCK) void gsddmm_kernel(GsddmmArgs<T> a) {
     loff[v] = (int)bcast_off(a.bc, k, true);
     roff[v] = (int)bcast_off(a.bc, k, false);
   }
-  T x[VEC], y[VEC], o[VEC];
-  if constexpr (OP != OP_COPY_RHS)
-    fetch_rt<T, VEC>(a.lhs + target_row(a.lt, a.uids, a.vids, e) * a.dl, a.lmode, loff, x);
-  if constexpr (OP != OP_COPY_LHS)
-    fetch_rt<T, VEC>(a.rhs + target_row(a.rt, a.uids, a.vids, e) * a.dr, a.rmode, roff, y);
+  T x[EW_U][VEC], y[EW_U][VEC];
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) {
-    T xv = T(0), yv = T(0);
-    if constexpr (OP != OP_COPY_RHS) xv = x[v];
-    if constexpr (OP != OP_COPY_LHS) yv = y[v];
-    o[v] = message<OP>(xv, yv);
+  for (int r = 0; r < EW_U; ++r) {
+    const int64_t e = e0 + r * per_round;
+    if (e < a.num_edges) {
+      if constexpr (OP != OP_COPY_RHS)
+        fetch_rt<T, VEC>(a.lhs + target_row(a.lt, a.uids, a.vids, e) * a.dl, a.lmode, loff, x[r]);
+      if constexpr (OP != OP_COPY_LHS)
+        fetch_rt<T, VEC>(a.rhs + target_row(a.rt, a.uids, a.vids, e) * a.dr, a.rmode, roff, y[r]);
+    }
   }
-  const int64_t base = e * a.dout + k0;
-  if (VEC > 1 && a.out_vec) {
-    if constexpr (VEC == VecOf<T>::n) store_vec<T>(a.out + base, o);
-  } else {
 #pragma unroll
-    for (int v = 0; v < VEC; ++v)
-      if (k0 + v < a.dout) a.out[base + v] = o[v];
+  for (int r = 0; r < EW_U; ++r) {
+    const int64_t e = e0 + r * per_round;
+    if (e >= a.num_edges) break;
+    T o[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      T xv = T(0), yv = T(0);
+      if constexpr (OP != OP_COPY_RHS) xv = x[r][v];
+      if constexpr (OP != OP_COPY_LHS) yv = y[r][v];
+      o[v] = message<OP>(xv, yv);
+    }
+    const int64_t base = e * a.dout + k0;
+    if (VEC > 1 && a.out_vec) {
+      if constexpr (VEC == VecOf<T>::n) store_vec<T>(a.out + base, o);
+    } else {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v)
+        if (k0 + v < a.dout) a.out[base + v] = o[v];
+    }
   }
 }
 
@@ -214,7 +232,8 @@ hipError_t launch_gsddmm_vec(const GsddmmParams& p) {
     a.G = G;
     a.S = (int)((nvec + G - 1) / G);
     a.num_tasks = p.num_edges;
-    a.num_waves = ((p.num_edges + (WAVE / G) - 1) / (WAVE / G)) * a.S;
+    const int64_t per_wave = (WAVE / G) * EW_U;
+    a.num_waves = ((p.num_edges + per_wave - 1) / per_wave) * a.S;
   }
   a.num_blocks = (a.num_waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
   if (a.num_blocks == 0) return hipSuccess;

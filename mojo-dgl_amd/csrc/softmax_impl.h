@@ -217,11 +217,30 @@ __device__ __forceinline__ void soft_group(const SoftmaxArgs<T>& a, int mode, bo
   }
 }
 
+// Launch parts: everything in one grid, or the chunks and wavefront rows in
+// one launch and the packed rows (fewer registers) in another.
+enum { PART_ALL = 0, PART_WIDE = 1, PART_PACKED = 2 };
+
+constexpr int PK_U = 4;  // packed wavefronts per wavefront of the packed launch
+
 template <class T, int VEC>
+__device__ __forceinline__ void softmax_packed(const SoftmaxArgs<T>& a, int64_t pw, int lane);
+template <class T, int VEC>
+__device__ __forceinline__ void softmax_packed_u(const SoftmaxArgs<T>& a, int64_t w, int lane);
+
+template <class T, int VEC, int PART>
 __global__ __launch_bounds__(BLOCK) void softmax_kernel(SoftmaxArgs<T> a) {
   const int lane = threadIdx.x & (WAVE - 1);
   const int64_t b = blockIdx.x;
   const int Pw = a.Pw;
+  if constexpr (PART == PART_PACKED) {
+    // packed rows only (their own launch: one slot per edge, few registers)
+    const int64_t lb = xcd_remap(b, a.light_blocks);
+    const int64_t w = lb * WAVES_PER_BLOCK + (threadIdx.x >> 6);
+    if (w * PK_U >= a.light_waves) return;  // uniform per wavefront
+    softmax_packed_u<T, VEC>(a, w, lane);
+    return;
+  }
   if (b < a.chunk_blocks) {
     // chunks of the long rows (statistics in launch 1, the write in launch 2)
     const int64_t w = b * WAVES_PER_BLOCK + (threadIdx.x >> 6);
@@ -250,8 +269,13 @@ __global__ __launch_bounds__(BLOCK) void softmax_kernel(SoftmaxArgs<T> a) {
     soft_group<T, VEC, SOFT_CPL>(a, SM_FULL, ok, row, start, stop, Pw, slab, lane, 0);
     return;
   }
-  // packed rows: find the degree bin of this wavefront
-  const int64_t pw = w - nmid;
+  if constexpr (PART == PART_ALL) softmax_packed<T, VEC>(a, w - nmid, lane);
+}
+
+// Packed wavefront pw: rows of one degree bin k, 2^k slots each.
+template <class T, int VEC>
+__device__ __forceinline__ void softmax_packed(const SoftmaxArgs<T>& a, int64_t pw, int lane) {
+  const int Pw = a.Pw;
   int k = 0;
   while (k + 1 < a.nbins && a.bin_wave[k + 1] <= pw) ++k;
   const int Pr = 1 << k;
@@ -268,6 +292,103 @@ __global__ __launch_bounds__(BLOCK) void softmax_kernel(SoftmaxArgs<T> a) {
     stop = a.indptr[row + 1];
   }
   soft_group<T, VEC, 1>(a, SM_FULL, ok, row, start, stop, Pr, slab, lane, 0);
+}
+
+// The packed launch: each wavefront serves PK_U consecutive packed
+// wavefronts' rows, walking the chain order -> indptr -> eid -> logits for
+// all of them at once, so every dependent load has PK_U requests per lane in
+// flight instead of one.
+template <class T, int VEC>
+__device__ __forceinline__ void softmax_packed_u(const SoftmaxArgs<T>& a, int64_t w, int lane) {
+  const int L = a.L, Pw = a.Pw;
+  const int c = lane % L;
+  // every bin's wavefront count is a multiple of PK_U, so all rounds of
+  // this wavefront lie in one bin k (found once, uniform)
+  const int64_t pw0 = w * PK_U;
+  int k = 0;
+  while (k + 1 < a.nbins && a.bin_wave[k + 1] <= pw0) ++k;
+  const int Pr = 1 << k;
+  const int per = Pw / Pr;
+  const int span = L * Pr;
+  const int sl = (lane / L) % Pr;
+  const int64_t b0 = a.bin_start[k], b1 = a.bin_start[k + 1];
+  // indices are clamped into the bin (and rows have >= 1 edge), so every
+  // load below is unconditional and in bounds; rok / ok mask the results
+  int64_t slab[PK_U], row[PK_U];
+  bool rok[PK_U];
+#pragma unroll
+  for (int r = 0; r < PK_U; ++r) {
+    const int64_t local = pw0 + r - a.bin_wave[k];
+    slab[r] = local % a.S;
+    const int64_t i = b0 + (local / a.S) * per + lane / (Pr * L);
+    rok[r] = i < b1;
+    row[r] = a.order[rok[r] ? i : b0];
+  }
+  int start[PK_U], stop[PK_U];
+#pragma unroll
+  for (int r = 0; r < PK_U; ++r) {
+    start[r] = a.indptr[row[r]];
+    stop[r] = a.indptr[row[r] + 1];
+  }
+  int64_t e[PK_U];
+  bool ok[PK_U];
+#pragma unroll
+  for (int r = 0; r < PK_U; ++r) {
+    const int j = start[r] + sl;
+    ok[r] = rok[r] && j < stop[r];
+    const int jc = ok[r] ? j : start[r];
+    e[r] = a.eid ? (int64_t)a.eid[jc] : (int64_t)jc;
+  }
+  if (a.mask) {
+#pragma unroll
+    for (int r = 0; r < PK_U; ++r) ok[r] = ok[r] && a.mask[e[r]] == 1;
+  }
+  T x[PK_U][VEC];
+#pragma unroll
+  for (int r = 0; r < PK_U; ++r) {
+    const int64_t k0 = (slab[r] * L + c) * VEC;
+    const int64_t kc = k0 < a.d ? k0 : 0;
+    load_cols<T, VEC>(a.logits + e[r] * a.d, kc, a.d, a.vec_io, x[r]);
+  }
+  const T ninf = T(-__builtin_huge_val());
+#pragma unroll
+  for (int r = 0; r < PK_U; ++r) {
+    const int64_t k0 = (slab[r] * L + c) * VEC;
+    const bool feat_ok = k0 < a.d;
+    T m[VEC], sum[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) m[v] = (ok[r] && feat_ok) ? x[r][v] : ninf;
+    for (int off = L; off < span; off <<= 1) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const T o = __shfl_xor(m[v], off);
+        m[v] = o > m[v] ? o : m[v];
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) sum[v] = (ok[r] && feat_ok) ? exp_t(x[r][v] - m[v]) : T(0);
+    for (int off = L; off < span; off <<= 1) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) sum[v] = sum[v] + __shfl_xor(sum[v], off);
+    }
+    if (!feat_ok) continue;
+    if (a.tab) {
+      if (rok[r] && sl == 0) {
+        T* t = a.tab + row[r] * 2 * a.d;
+#pragma unroll
+        for (int v = 0; v < VEC; ++v)
+          if (k0 + v < a.d) {
+            t[k0 + v] = m[v];
+            t[a.d + k0 + v] = sum[v];
+          }
+      }
+    } else if (ok[r]) {
+      T y[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) y[v] = exp_t(x[r][v] - m[v]) / sum[v];
+      store_cols<T, VEC>(a.out + e[r] * a.d, k0, a.d, a.vec_io, y);
+    }
+  }
 }
 
 // Edge-parallel write of the two-pass form: L lanes per edge, 64 / L edges
@@ -323,9 +444,12 @@ hipError_t launch_softmax_vec(const SoftmaxParams& p) {
     a.nbins = p.nbins;
     for (int k = 0; k <= p.nbins; ++k) a.bin_start[k] = p.bounds[k];
     for (int k = 0; k < p.nbins; ++k) {
+      // padded to a multiple of PK_U: a wavefront of the packed launch
+      // never straddles two bins
       const int64_t per = a.Pw >> k;
       a.bin_wave[k] = waves;
-      waves += ((a.bin_start[k + 1] - a.bin_start[k] + per - 1) / per) * a.S;
+      const int64_t wk = ((a.bin_start[k + 1] - a.bin_start[k] + per - 1) / per) * a.S;
+      waves += (wk + PK_U - 1) / PK_U * PK_U;
     }
     a.bin_wave[p.nbins] = waves;
     a.mid_start = p.bounds[p.nbins];
@@ -334,7 +458,8 @@ hipError_t launch_softmax_vec(const SoftmaxParams& p) {
     a.mid_start = 0;
     a.mid_end = p.num_rows;
   }
-  a.light_waves = (a.mid_end - a.mid_start) * a.S + waves;
+  const int64_t packed_waves = waves;
+  a.light_waves = (a.mid_end - a.mid_start) * a.S;
   a.light_blocks = (a.light_waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
   a.num_chunks = p.num_chunks;
   a.chunk_row = p.chunk_row;
@@ -346,10 +471,21 @@ hipError_t launch_softmax_vec(const SoftmaxParams& p) {
   a.chunk_blocks = (a.chunk_waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
   a.mode2 = 0;
   a.tab = static_cast<T*>(p.table);
+  // chunks and wavefront rows, then the packed rows in a launch of their own
   const int64_t blocks = a.chunk_blocks + a.light_blocks;
   if (blocks > 0) {
-    hipLaunchKernelGGL((softmax_kernel<T, VEC>), dim3((unsigned)blocks), dim3(BLOCK), 0, p.stream,
-                       a);
+    hipLaunchKernelGGL((softmax_kernel<T, VEC, PART_WIDE>), dim3((unsigned)blocks), dim3(BLOCK), 0,
+                       p.stream, a);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  if (packed_waves > 0) {
+    SoftmaxArgs<T> b = a;
+    b.light_waves = packed_waves;
+    const int64_t pk_waves = (packed_waves + PK_U - 1) / PK_U;
+    b.light_blocks = (pk_waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
+    hipLaunchKernelGGL((softmax_kernel<T, VEC, PART_PACKED>), dim3((unsigned)b.light_blocks),
+                       dim3(BLOCK), 0, p.stream, b);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
@@ -357,8 +493,8 @@ hipError_t launch_softmax_vec(const SoftmaxParams& p) {
     a.mode2 = 1;
     a.light_waves = 0;
     a.light_blocks = 0;
-    hipLaunchKernelGGL((softmax_kernel<T, VEC>), dim3((unsigned)a.chunk_blocks), dim3(BLOCK), 0,
-                       p.stream, a);
+    hipLaunchKernelGGL((softmax_kernel<T, VEC, PART_WIDE>), dim3((unsigned)a.chunk_blocks),
+                       dim3(BLOCK), 0, p.stream, a);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }

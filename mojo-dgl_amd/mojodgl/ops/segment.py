@@ -165,6 +165,8 @@ def segment_softmax(seglen, value):
     num_seg = seg.num
     if num_seg and n and d:
         off = seg.device()
+        # segments in their own order, one wavefront each (a degree-sorted
+        # plan costs more to build per call than it saves here)
         if seg.host is not None:
             plan = _plan.SoftmaxPlan(seg.host, slots, chunk_len, ordered=False)
         else:
@@ -173,6 +175,7 @@ def segment_softmax(seglen, value):
         ws, nbytes = _plan.workspace(plan, d, dtype)
         rc = _lib.lib().mdgl_segment_softmax(
             off.data_ptr(), val.data_ptr(), out.data_ptr(), None, num_seg, d, n,
+            _lib.ptr(plan.order), plan.bounds_ptr(), plan.nbins,
             _lib.ptr(plan.chunk_row), _lib.ptr(plan.chunk_start), _lib.ptr(plan.chunk_first),
             plan.num_chunks, plan.slots, _lib.ptr(ws), nbytes, _lib.dtype_code(dtype),
             _lib.stream())

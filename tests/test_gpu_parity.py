@@ -366,6 +366,34 @@ def test_segment_softmax_gpu_lengths_with_long_segments(d):
     np.testing.assert_array_equal(got.cpu().numpy(), host)
 
 
+def test_segment_softmax_degree_plan_through_the_abi():
+    """mdgl_segment_softmax served by a degree-binned plan (packed short
+    segments, wavefront segments, chunked long ones)."""
+    from mojodgl import _lib
+    from mojodgl.ops import _plan
+
+    rng = np.random.default_rng(58)
+    seglen = np.concatenate([rng.poisson(6, 3000), [0, 0, 700, 3000, 129, 128, 1]])
+    rng.shuffle(seglen)
+    d = 16
+    value = (rng.normal(size=(int(seglen.sum()), d)) * 2).astype(np.float32)
+    val = torch.from_numpy(value).cuda()
+    out = torch.zeros_like(val)
+    off = torch.from_numpy(np.concatenate([[0], np.cumsum(seglen)]).astype(np.int32)).cuda()
+    slots, chunk_len = _plan.geometry(d, np.float32, val, out)
+    plan = _plan.SoftmaxPlan.from_device(off, slots, chunk_len, ordered=True)
+    ws, nbytes = _plan.workspace(plan, d, np.float32)
+    rc = _lib.lib().mdgl_segment_softmax(
+        off.data_ptr(), val.data_ptr(), out.data_ptr(), None, seglen.size, d, value.shape[0],
+        _lib.ptr(plan.order), plan.bounds_ptr(), plan.nbins, _lib.ptr(plan.chunk_row),
+        _lib.ptr(plan.chunk_start), _lib.ptr(plan.chunk_first), plan.num_chunks, plan.slots,
+        _lib.ptr(ws), nbytes, 0, _lib.stream())
+    _lib.check(rc, "segment_softmax")
+    ref = oracle.segment_softmax(seglen, value, np.float64)
+    close(out.cpu().numpy(), ref, ref, np.float32, "segment_softmax degree plan")
+    np.testing.assert_array_equal(out.cpu().numpy(), ops.segment_softmax(seglen, value))
+
+
 def test_segment_gpu_lengths_are_validated():
     value = torch.ones(10, 2, device="cuda")
     for bad in ([3, 3, 3], [12, -2], [4.5, 5.5]):
