@@ -46,6 +46,7 @@ extern "C" {
 
 /* flags of mdgl_gspmm / mdgl_segment_reduce */
 #define MDGL_REPLACE_INF 1 /* +-inf results become 0 (heterograph.py:232-239) */
+#define MDGL_RHS_CSR_ORDER 2 /* mdgl_gspmm: rhs row i belongs to CSR slot i (not edge eid[i]) */
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* mdgl_last_error(void);
@@ -92,7 +93,11 @@ int mdgl_gsddmm(const int32_t* uids, const int32_t* vids, const void* lhs, const
  * reduced in order per heavy row (heavy_rows[h], chunks
  * heavy_ptr[h]..heavy_ptr[h+1]) -- the chunks of every row of length
  * > chunk_len, in CSR order, and nothing else; num_chunks = 0 disables the
- * split. The partials live in `workspace` (mdgl_gspmm_workspace_bytes). */
+ * split. The partials live in `workspace` (mdgl_gspmm_workspace_bytes).
+ * flags: MDGL_REPLACE_INF; MDGL_RHS_CSR_ORDER when the edge operand has been
+ * put in CSR slot order (mdgl_gather_rows with eid), which turns its random
+ * reads into streaming ones -- worth it for a narrow edge operand read by
+ * several column slabs; arg_e still reports edge ids. */
 int mdgl_gspmm(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
                const void* lhs, const void* rhs, void* dst, int64_t num_dst, int op, int64_t dl,
                int64_t dr, int64_t dout, int reduce_op, const int32_t* deg, int nd,
@@ -218,6 +223,11 @@ int mdgl_gspmm_edge_grad(const int32_t* vids, const int32_t* indptr, const void*
  * node-shaped gradient. */
 int mdgl_rows_by_degree(const int32_t* indptr, const void* src, void* dst, int64_t rows,
                         int64_t d, int dtype, void* stream);
+
+/* dst[i, :] = src[idx[i], :] for rows of `width` elements (the edge operand of a
+ * gspmm put in CSR slot order with idx = eid). No counterpart in the reference. */
+int mdgl_gather_rows(const void* src, const int32_t* idx, void* dst, int64_t n, int64_t width,
+                     int dtype, void* stream);
 
 /* dst[i] = alpha * src[i]. */
 int mdgl_scale(const void* src, void* dst, int64_t n, double alpha, int dtype, void* stream);

@@ -52,6 +52,19 @@ __global__ __launch_bounds__(1024) void cumsum_kernel(const int64_t* __restrict_
   }
 }
 
+template <class T>
+__global__ __launch_bounds__(BLOCK) void gather_rows_kernel(const T* __restrict__ src,
+                                                            const int32_t* __restrict__ idx,
+                                                            T* __restrict__ dst, int64_t n,
+                                                            int64_t width) {
+  const int64_t total = n * width;
+  for (int64_t t = (int64_t)blockIdx.x * BLOCK + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * BLOCK) {
+    const int64_t i = t / width, k = t % width;
+    dst[t] = src[(int64_t)idx[i] * width + k];
+  }
+}
+
 static unsigned grid_for(int64_t n) {
   int64_t b = (n + BLOCK - 1) / BLOCK;
   if (b > 65536) b = 65536;
@@ -73,6 +86,19 @@ hipError_t launch_clamp_i64(const int64_t* src, int64_t* dst, int64_t n, int64_t
                             hipStream_t s) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(clamp_kernel, dim3(grid_for(n)), dim3(BLOCK), 0, s, src, dst, n, lo, hi);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(const void* src, const int32_t* idx, void* dst, int64_t n,
+                              int64_t width, int dtype, hipStream_t s) {
+  if (n <= 0 || width <= 0) return hipSuccess;
+  const int64_t total = n * width;
+  if (dtype == 0)
+    hipLaunchKernelGGL(gather_rows_kernel<float>, dim3(grid_for(total)), dim3(BLOCK), 0, s,
+                       static_cast<const float*>(src), idx, static_cast<float*>(dst), n, width);
+  else
+    hipLaunchKernelGGL(gather_rows_kernel<double>, dim3(grid_for(total)), dim3(BLOCK), 0, s,
+                       static_cast<const double*>(src), idx, static_cast<double*>(dst), n, width);
   return hipGetLastError();
 }
 

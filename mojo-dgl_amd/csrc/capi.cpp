@@ -205,6 +205,16 @@ int mdgl_rows_by_degree(const int32_t* indptr, const void* src, void* dst, int64
                     "rows_by_degree");
 }
 
+int mdgl_gather_rows(const void* src, const int32_t* idx, void* dst, int64_t n, int64_t width,
+                     int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "gather_rows: bad dtype %d", dtype);
+  if (n < 0 || width < 0) return fail(MDGL_EINVAL, "gather_rows: negative size");
+  if (n == 0 || width == 0) return MDGL_OK;
+  if (!src || !idx || !dst) return fail(MDGL_EINVAL, "gather_rows: null buffer");
+  return hip_status(launch_gather_rows(src, idx, dst, n, width, dtype, (hipStream_t)stream),
+                    "gather_rows");
+}
+
 int mdgl_scale(const void* src, void* dst, int64_t n, double alpha, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "scale: bad dtype %d", dtype);
   if (n < 0) return fail(MDGL_EINVAL, "scale: n must be >= 0");
@@ -365,7 +375,8 @@ int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* e
   p.dout = dout;
   p.op = op;
   p.red = reduce_op == RED_MEAN ? RED_SUM : reduce_op;
-  p.flags = (reduce_op == RED_MEAN ? F_MEAN : 0) | ((flags & MDGL_REPLACE_INF) ? F_REPLACE_INF : 0);
+  p.flags = (reduce_op == RED_MEAN ? F_MEAN : 0) | ((flags & MDGL_REPLACE_INF) ? F_REPLACE_INF : 0) |
+            ((flags & MDGL_RHS_CSR_ORDER) ? F_RHS_CSR : 0);
   const bool arg = reduce_op == RED_MAX || reduce_op == RED_MIN;
   p.arg_u = arg ? arg_u : nullptr;
   p.arg_e = arg ? arg_e : nullptr;

@@ -56,6 +56,10 @@ struct GspmmArgs {
   int32_t* part_u;
   int32_t* part_e;
   int64_t chunk_waves, row_waves, chunk_blocks, num_blocks;
+  // waves per slab (slab-major order: every unit's slab s before slab s + 1,
+  // so the rows of neighbouring units share cache lines across wavefronts)
+  int64_t chunk_uwaves, row_uwaves;
+  int slab_major;
 };
 
 template <class T, int VEC, int M>
@@ -80,8 +84,9 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
   constexpr int U = 4;
   const int G = WIDE ? WAVE : a.G;
   const int grp = lane / G, gl = lane % G, gbase = grp * G;
-  const int64_t slab = wave % a.S;
-  const int64_t unit = (wave / a.S) * (WAVE / G) + grp;
+  const int64_t uw = chunk ? a.chunk_uwaves : a.row_uwaves;
+  const int64_t slab = a.slab_major ? wave / uw : wave % a.S;
+  const int64_t unit = (a.slab_major ? wave % uw : wave / a.S) * (WAVE / G) + grp;
 
   // ---- resolve the unit to a CSR slot range
   bool ok = unit < (chunk ? a.num_chunks : a.num_rows);
@@ -124,12 +129,20 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
   const bool ident = a.flags & F_EID_IDENTITY;
   const int n = ok ? stop - start : 0;
   const int nmax = WIDE ? n : wave_max_int(n);
+  // a scalar edge operand (one value per edge, splatted over the columns) is
+  // loaded with the ids, one edge per lane, and broadcast like them
+  constexpr bool SCALAR_E = WIDE && RM == M_SPLAT && OP != OP_COPY_LHS;
+  const bool scalar_e = SCALAR_E && a.dr == 1;
+  // the edge operand may come in CSR slot order (row i of rhs for slot i)
+  const bool rhs_csr = a.flags & F_RHS_CSR;
   for (int base = 0; base < nmax; base += G) {
     int my_s = 0, my_e = 0;
+    T my_w = T(0);
     if (base + gl < n) {
       const int i = start + base + gl;
       if (a.indices) my_s = a.indices[i];
       my_e = ident ? i : a.eid[i];
+      if (SCALAR_E && scalar_e) my_w = a.rhs[rhs_csr ? (int64_t)i : (int64_t)my_e];
     }
     const int cnt = n - base < G ? n - base : G;  // may be <= 0 on finished groups
     const int jmax = WIDE ? cnt : (nmax - base < G ? nmax - base : G);
@@ -149,11 +162,22 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
         }
         su[u] = s;
         se[u] = e;
+        if constexpr (SCALAR_E) {
+          if (scalar_e) {
+            const T w = readlane_val(my_w, jj);
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) y[u][v] = w;
+          }
+        }
         if (j + u < cnt && feat_ok) {
           if constexpr (OP != OP_COPY_RHS)
             fetch<T, VEC, LM>(a.lhs + (int64_t)s * a.dl, a.lmode, loff, x[u]);
-          if constexpr (OP != OP_COPY_LHS)
-            fetch<T, VEC, RM>(a.rhs + (int64_t)e * a.dr, a.rmode, roff, y[u]);
+          if constexpr (OP != OP_COPY_LHS) {
+            if (!(SCALAR_E && scalar_e)) {
+              const int64_t rrow = rhs_csr ? (int64_t)(start + base + j + u) : (int64_t)e;
+              fetch<T, VEC, RM>(a.rhs + rrow * a.dr, a.rmode, roff, y[u]);
+            }
+          }
         }
       }
 #pragma unroll
@@ -249,6 +273,7 @@ __global__ __launch_bounds__(BLOCK) void gspmm_kernel(GspmmArgs<T> a) {
     gspmm_body<T, OP, RED, VEC, M_DYN, M_DYN, true>(a, chunk, wave, lane);
   else if constexpr (PATH == P_PACK_CC)
     gspmm_body<T, OP, RED, VEC, M_CONTIG, M_CONTIG, false>(a, chunk, wave, lane);
+
   else
     gspmm_body<T, OP, RED, VEC, M_DYN, M_DYN, false>(a, chunk, wave, lane);
 }
@@ -324,8 +349,11 @@ hipError_t launch_gspmm_op(const GspmmParams& p) {
   a.part_u = p.part_u;
   a.part_e = p.part_e;
   const int64_t per_wave = WAVE / G;
-  a.chunk_waves = ((p.num_chunks + per_wave - 1) / per_wave) * a.S;
-  a.row_waves = ((p.num_rows + per_wave - 1) / per_wave) * a.S;
+  a.chunk_uwaves = (p.num_chunks + per_wave - 1) / per_wave;
+  a.row_uwaves = (p.num_rows + per_wave - 1) / per_wave;
+  a.chunk_waves = a.chunk_uwaves * a.S;
+  a.row_waves = a.row_uwaves * a.S;
+  a.slab_major = a.S > 1;
   a.chunk_blocks = (a.chunk_waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
   a.num_blocks = a.chunk_blocks + (a.row_waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
   if (a.num_blocks > 0) {

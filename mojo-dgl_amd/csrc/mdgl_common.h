@@ -169,4 +169,15 @@ __device__ __forceinline__ int readlane_int(int v, int lane) {
   return __builtin_amdgcn_readlane(v, lane);
 }
 
+__device__ __forceinline__ float readlane_val(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+__device__ __forceinline__ double readlane_val(double v, int lane) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffLL), lane);
+  const int hi = __builtin_amdgcn_readlane((int)(b >> 32), lane);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
 }  // namespace mdgl

@@ -13,6 +13,7 @@ enum {
   F_REPLACE_INF = 2,   // +-inf -> 0 on the final value (update_all max/min)
   F_OUT_VEC = 4,       // output rows allow 16-byte stores
   F_EID_IDENTITY = 8,  // edge id of CSR slot i is i (segment reduce)
+  F_RHS_CSR = 16,      // the edge operand is in CSR slot order (rhs row i for slot i)
 };
 
 // gspmm / segment_reduce: out[row, k] = red over CSR slots of row of
@@ -126,6 +127,9 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather);
 hipError_t launch_replace_inf(const void* src, void* dst, int64_t n, int dtype, hipStream_t s);
 hipError_t launch_clamp_i64(const int64_t* src, int64_t* dst, int64_t n, int64_t lo, int64_t hi,
                             hipStream_t s);
+// dst[i, :] = src[idx[i], :] (rows of `width` elements; array.hip).
+hipError_t launch_gather_rows(const void* src, const int32_t* idx, void* dst, int64_t n,
+                              int64_t width, int dtype, hipStream_t s);
 // Backward helpers (backward.hip).
 hipError_t launch_edge_grad(const int32_t* vids, const int32_t* indptr, const void* g,
                             const int32_t* arg_e, void* m, int64_t num_edges, int64_t d,

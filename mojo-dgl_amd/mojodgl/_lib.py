@@ -49,6 +49,7 @@ TARGETS = {"u": SRC_CODE, "v": DST_CODE, "e": EDGE_CODE}
 
 FLOAT32, FLOAT64 = 0, 1
 REPLACE_INF = 1
+RHS_CSR_ORDER = 2
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -83,6 +84,7 @@ _SIGNATURES = {
     "mdgl_gspmm_edge_grad": ([_P, _P, _P, _P, _P, _I64, _I64, _C, ctypes.c_double, _C, _P], _C),
     "mdgl_rows_by_degree": ([_P, _P, _P, _I64, _I64, _C, _P], _C),
     "mdgl_scale": ([_P, _P, _I64, ctypes.c_double, _C, _P], _C),
+    "mdgl_gather_rows": ([_P, _P, _P, _I64, _I64, _C, _P], _C),
 }
 
 

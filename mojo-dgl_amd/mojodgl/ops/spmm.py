@@ -22,6 +22,15 @@ from .sddmm import _check_rows, feat_shape, out_feat_shape, reshape_lhs_rhs, sha
 __all__ = ["gspmm"]
 
 
+def _slabs(dout, dtype):
+    """Column slabs of 64 lanes the kernel cuts an output row into (the lane
+    width rule of mdgl_gspmm: 16-byte lanes, else 8-byte for even float32
+    widths, else one element)."""
+    vw = 4 if dtype == np.float32 else 2
+    vec = vw if dout % vw == 0 else (2 if dtype == np.float32 and dout % 2 == 0 else 1)
+    return -(-(-(-dout // vec)) // 64)
+
+
 def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False,
          arg_dtype=torch.int64, kind="in"):
     """Validate, launch, and return device tensors (out, arg_u, arg_e) plus
@@ -76,6 +85,18 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
         rhs = _lib.on_device(R, dtype) if R is not None else None
         csr = g._device_csr(kind)
         sched = csr.chunks
+        flags = _lib.REPLACE_INF if replace_inf else 0
+        if rhs is not None and code not in (OP_COPY_LHS, OP_COPY_RHS) and dr == 1 \
+                and num_edges and _slabs(dout, dtype) > 1:
+            # a scalar edge operand read by several column slabs: put it in
+            # CSR slot order once, so every slab streams it
+            perm = torch.empty(num_edges, dtype=tdt, device=gdev)
+            _lib.check(_lib.lib().mdgl_gather_rows(rhs.data_ptr(), csr.eid.data_ptr(),
+                                                   perm.data_ptr(), num_edges, 1,
+                                                   _lib.dtype_code(dtype), _lib.stream()),
+                       "gather_rows")
+            rhs = perm
+            flags |= _lib.RHS_CSR_ORDER
         ws = None
         nbytes = _lib.lib().mdgl_gspmm_workspace_bytes(sched.num_chunks, dout,
                                                          REDUCERS[reduce_op],
@@ -89,8 +110,7 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
             _lib.ptr(arg_u), _lib.ptr(arg_e), _lib.ptr(sched.chunk_row),
             _lib.ptr(sched.chunk_start), sched.num_chunks, sched.chunk_len,
             _lib.ptr(sched.heavy_rows), _lib.ptr(sched.heavy_ptr), sched.num_heavy, _lib.ptr(ws),
-            nbytes, _lib.REPLACE_INF if replace_inf else 0, _lib.dtype_code(dtype),
-            _lib.stream())
+            nbytes, flags, _lib.dtype_code(dtype), _lib.stream())
         _lib.check(rc, "gspmm")
     out = out.reshape(shape)
     if arg:
