@@ -19,7 +19,10 @@
 //     chunk's (max, sum of exp(x - max)) per column, launch 2 merges a row's
 //     chunks in chunk order (M = max m_c, S = sum s_c * exp(m_c - M)) and writes
 //     exp(x - M) / S over the chunk.
-// Chunk workgroups come first in launch 1 so the long rows start early.
+// Launch 1 takes the chunks (their workgroups first, so the long rows start
+// early) and the wavefront rows; the packed rows run in a launch of their
+// own, whose kernel needs far fewer registers, each wavefront serving
+// PK_U packed wavefronts' rows with its dependent loads interleaved.
 //
 // Two-pass form (edge_softmax with a row-of-edge array): a random 32-byte
 // write per edge costs more than the rest of the op, so the row pass then
@@ -217,14 +220,12 @@ __device__ __forceinline__ void soft_group(const SoftmaxArgs<T>& a, int mode, bo
   }
 }
 
-// Launch parts: everything in one grid, or the chunks and wavefront rows in
-// one launch and the packed rows (fewer registers) in another.
-enum { PART_ALL = 0, PART_WIDE = 1, PART_PACKED = 2 };
+// Launch parts: the chunks and wavefront rows in one launch, the packed rows
+// (one slot per edge, fewer registers) in another.
+enum { PART_WIDE = 1, PART_PACKED = 2 };
 
 constexpr int PK_U = 4;  // packed wavefronts per wavefront of the packed launch
 
-template <class T, int VEC>
-__device__ __forceinline__ void softmax_packed(const SoftmaxArgs<T>& a, int64_t pw, int lane);
 template <class T, int VEC>
 __device__ __forceinline__ void softmax_packed_u(const SoftmaxArgs<T>& a, int64_t w, int lane);
 
@@ -269,29 +270,6 @@ __global__ __launch_bounds__(BLOCK) void softmax_kernel(SoftmaxArgs<T> a) {
     soft_group<T, VEC, SOFT_CPL>(a, SM_FULL, ok, row, start, stop, Pw, slab, lane, 0);
     return;
   }
-  if constexpr (PART == PART_ALL) softmax_packed<T, VEC>(a, w - nmid, lane);
-}
-
-// Packed wavefront pw: rows of one degree bin k, 2^k slots each.
-template <class T, int VEC>
-__device__ __forceinline__ void softmax_packed(const SoftmaxArgs<T>& a, int64_t pw, int lane) {
-  const int Pw = a.Pw;
-  int k = 0;
-  while (k + 1 < a.nbins && a.bin_wave[k + 1] <= pw) ++k;
-  const int Pr = 1 << k;
-  const int per = Pw / Pr;  // rows per wavefront
-  const int64_t local = pw - a.bin_wave[k];
-  const int64_t slab = local % a.S;
-  const int64_t i = a.bin_start[k] + (local / a.S) * per + lane / (Pr * a.L);
-  const bool ok = i < a.bin_start[k + 1];
-  int start = 0, stop = 0;
-  int64_t row = 0;
-  if (ok) {
-    row = a.order[i];
-    start = a.indptr[row];
-    stop = a.indptr[row + 1];
-  }
-  soft_group<T, VEC, 1>(a, SM_FULL, ok, row, start, stop, Pr, slab, lane, 0);
 }
 
 // The packed launch: each wavefront serves PK_U consecutive packed
