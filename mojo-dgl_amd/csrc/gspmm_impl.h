@@ -127,6 +127,7 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
   }
 
   const bool ident = a.flags & F_EID_IDENTITY;
+  constexpr bool ARG_OUT = (RED == RED_MAX || RED == RED_MIN);
   const int n = ok ? stop - start : 0;
   const int nmax = WIDE ? n : wave_max_int(n);
   // a scalar edge operand (one value per edge, splatted over the columns) is
@@ -152,13 +153,20 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int jj = (j + u < G) ? j + u : G - 1;
-        int s, e;
-        if constexpr (WIDE) {
-          s = readlane_int(my_s, jj);
+        // copy_rhs over identity edge ids (segment_reduce) needs no ids from
+        // other lanes: the slot is the edge, and the source only for an arg
+        constexpr bool NEED_S = OP != OP_COPY_RHS || ARG_OUT;
+        int s = 0, e;
+        if (OP == OP_COPY_RHS && ident) {
+          e = start + base + jj;
+        } else if constexpr (WIDE) {
           e = readlane_int(my_e, jj);
         } else {
-          s = __shfl(my_s, gbase + jj);
           e = __shfl(my_e, gbase + jj);
+        }
+        if constexpr (NEED_S) {
+          if constexpr (WIDE) s = readlane_int(my_s, jj);
+          else s = __shfl(my_s, gbase + jj);
         }
         su[u] = s;
         se[u] = e;
