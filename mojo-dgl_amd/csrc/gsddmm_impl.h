@@ -102,7 +102,7 @@ __global__ __launch_bounds__(BLOCK) void gsddmm_kernel(GsddmmArgs<T> a) {
     }
     const int64_t base = e * a.dout + k0;
     if (VEC > 1 && a.out_vec) {
-      if constexpr (VEC == VecOf<T>::n) store_vec<T>(a.out + base, o);
+      if constexpr (VEC == VecOf<T>::n) store_n_stream<T, VEC>(a.out + base, o);
     } else {
 #pragma unroll
       for (int v = 0; v < VEC; ++v)

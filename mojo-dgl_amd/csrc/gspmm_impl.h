@@ -78,7 +78,25 @@ __device__ __forceinline__ void fetch(const T* __restrict__ row, int mode_rt, co
   }
 }
 
-template <class T, int OP, int RED, int VEC, int LM, int RM, bool WIDE>
+// The same for the edge operand, read once per edge: non-temporal, so it
+// does not displace source rows that other edges will gather.
+template <class T, int VEC, int M>
+__device__ __forceinline__ void fetch_stream(const T* __restrict__ row, int mode_rt,
+                                             const int (&off)[VEC], T (&x)[VEC]) {
+  const int m = (M == M_DYN) ? mode_rt : M;
+  if (VEC > 1 && m == M_CONTIG) {
+    if constexpr (VEC > 1) load_n_stream<T, VEC>(row + off[0], x);
+  } else if (m == M_SPLAT) {
+    const T s = __builtin_nontemporal_load(row + off[0]);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) x[v] = s;
+  } else {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) x[v] = __builtin_nontemporal_load(row + off[v]);
+  }
+}
+
+template <class T, int OP, int RED, int VEC, int LM, int RM, bool WIDE, bool NT>
 __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, int64_t wave,
                                            int lane) {
   constexpr int U = 4;
@@ -141,8 +159,8 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
     T my_w = T(0);
     if (base + gl < n) {
       const int i = start + base + gl;
-      if (a.indices) my_s = a.indices[i];
-      my_e = ident ? i : a.eid[i];
+      if (a.indices) my_s = __builtin_nontemporal_load(a.indices + i);
+      my_e = ident ? i : __builtin_nontemporal_load(a.eid + i);
       if (SCALAR_E && scalar_e) my_w = a.rhs[rhs_csr ? (int64_t)i : (int64_t)my_e];
     }
     const int cnt = n - base < G ? n - base : G;  // may be <= 0 on finished groups
@@ -183,7 +201,12 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
           if constexpr (OP != OP_COPY_LHS) {
             if (!(SCALAR_E && scalar_e)) {
               const int64_t rrow = rhs_csr ? (int64_t)(start + base + j + u) : (int64_t)e;
-              fetch<T, VEC, RM>(a.rhs + rrow * a.dr, a.rmode, roff, y[u]);
+              // a row gathered by a random edge id is read once: stream it
+              // (NT); consecutive rows (identity ids) share lines: cache them
+              if constexpr (NT)
+                fetch_stream<T, VEC, RM>(a.rhs + rrow * a.dr, a.rmode, roff, y[u]);
+              else
+                fetch<T, VEC, RM>(a.rhs + rrow * a.dr, a.rmode, roff, y[u]);
             }
           }
         }
@@ -239,7 +262,7 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
   }
   const int64_t o = row * a.dout + k0;
   if (VEC > 1 && (a.flags & F_OUT_VEC)) {
-    if constexpr (VEC > 1) store_n<T, VEC>(a.out + o, acc);
+    if constexpr (VEC > 1) store_n_stream<T, VEC>(a.out + o, acc);
   } else {
 #pragma unroll
     for (int v = 0; v < VEC; ++v)
@@ -262,7 +285,7 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
 // units with contiguous operands, or any modes.
 enum { P_WIDE_CC = 0, P_WIDE_CS = 1, P_WIDE_DYN = 2, P_PACK_CC = 3, P_PACK_DYN = 4 };
 
-template <class T, int OP, int RED, int VEC, int PATH>
+template <class T, int OP, int RED, int VEC, int PATH, bool NT>
 __global__ __launch_bounds__(BLOCK) void gspmm_kernel(GspmmArgs<T> a) {
   const int64_t b = blockIdx.x;
   const bool chunk = b < a.chunk_blocks;
@@ -274,16 +297,16 @@ __global__ __launch_bounds__(BLOCK) void gspmm_kernel(GspmmArgs<T> a) {
   const int64_t wave = blk * WAVES_PER_BLOCK + (threadIdx.x >> 6);
   if (wave >= (chunk ? a.chunk_waves : a.row_waves)) return;
   if constexpr (PATH == P_WIDE_CC)
-    gspmm_body<T, OP, RED, VEC, M_CONTIG, M_CONTIG, true>(a, chunk, wave, lane);
+    gspmm_body<T, OP, RED, VEC, M_CONTIG, M_CONTIG, true, NT>(a, chunk, wave, lane);
   else if constexpr (PATH == P_WIDE_CS)
-    gspmm_body<T, OP, RED, VEC, M_CONTIG, M_SPLAT, true>(a, chunk, wave, lane);
+    gspmm_body<T, OP, RED, VEC, M_CONTIG, M_SPLAT, true, NT>(a, chunk, wave, lane);
   else if constexpr (PATH == P_WIDE_DYN)
-    gspmm_body<T, OP, RED, VEC, M_DYN, M_DYN, true>(a, chunk, wave, lane);
+    gspmm_body<T, OP, RED, VEC, M_DYN, M_DYN, true, NT>(a, chunk, wave, lane);
   else if constexpr (PATH == P_PACK_CC)
-    gspmm_body<T, OP, RED, VEC, M_CONTIG, M_CONTIG, false>(a, chunk, wave, lane);
+    gspmm_body<T, OP, RED, VEC, M_CONTIG, M_CONTIG, false, NT>(a, chunk, wave, lane);
 
   else
-    gspmm_body<T, OP, RED, VEC, M_DYN, M_DYN, false>(a, chunk, wave, lane);
+    gspmm_body<T, OP, RED, VEC, M_DYN, M_DYN, false, NT>(a, chunk, wave, lane);
 }
 
 // Folds the chunk partials of each heavy row in chunk (= CSR) order.
@@ -320,6 +343,23 @@ __global__ __launch_bounds__(BLOCK) void gspmm_combine_kernel(
   if constexpr (RED == RED_MAX || RED == RED_MIN) {
     if (arg_u) arg_u[row * dout + k] = au;
     if (arg_e) arg_e[row * dout + k] = ae;
+  }
+}
+
+template <class T, int OP, int RED, int VEC, bool NT>
+void launch_path(const GspmmArgs<T>& a, dim3 grid, dim3 block, int lm, int rm, hipStream_t st) {
+  if (a.G == WAVE) {
+    if (lm == M_CONTIG && rm == M_CONTIG)
+      hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_WIDE_CC, NT>), grid, block, 0, st, a);
+    else if (lm == M_CONTIG && rm == M_SPLAT)
+      hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_WIDE_CS, NT>), grid, block, 0, st, a);
+    else
+      hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_WIDE_DYN, NT>), grid, block, 0, st, a);
+  } else {
+    if (lm == M_CONTIG && rm == M_CONTIG)
+      hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_PACK_CC, NT>), grid, block, 0, st, a);
+    else
+      hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_PACK_DYN, NT>), grid, block, 0, st, a);
   }
 }
 
@@ -369,18 +409,15 @@ hipError_t launch_gspmm_op(const GspmmParams& p) {
     const int lm = copy_r ? a.rmode : a.lmode;
     const int rm = copy_l ? a.lmode : a.rmode;
     const dim3 grid((unsigned)a.num_blocks), block(BLOCK);
-    if (G == WAVE) {
-      if (lm == M_CONTIG && rm == M_CONTIG)
-        hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_WIDE_CC>), grid, block, 0, p.stream, a);
-      else if (lm == M_CONTIG && rm == M_SPLAT)
-        hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_WIDE_CS>), grid, block, 0, p.stream, a);
+    // edge rows are streamed unless they are consecutive (identity ids:
+    // segment_reduce, which is copy_rhs)
+    if constexpr (OP == OP_COPY_RHS) {
+      if (a.flags & F_EID_IDENTITY)
+        launch_path<T, OP, RED, VEC, false>(a, grid, block, lm, rm, p.stream);
       else
-        hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_WIDE_DYN>), grid, block, 0, p.stream, a);
+        launch_path<T, OP, RED, VEC, true>(a, grid, block, lm, rm, p.stream);
     } else {
-      if (lm == M_CONTIG && rm == M_CONTIG)
-        hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_PACK_CC>), grid, block, 0, p.stream, a);
-      else
-        hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_PACK_DYN>), grid, block, 0, p.stream, a);
+      launch_path<T, OP, RED, VEC, true>(a, grid, block, lm, rm, p.stream);
     }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;

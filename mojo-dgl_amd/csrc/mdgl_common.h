@@ -123,6 +123,26 @@ __device__ __forceinline__ void store_n(T* p, const T (&in)[N]) {
   *reinterpret_cast<V*>(p) = v;
 }
 
+// Streaming (non-temporal) 16-byte store / load: data written or read once,
+// kept from displacing reused lines (gathered rows, node tables) in the
+// caches.
+template <class T, int N>
+__device__ __forceinline__ void store_n_stream(T* p, const T (&in)[N]) {
+  typedef T V __attribute__((ext_vector_type(N)));
+  V v;
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = in[i];
+  __builtin_nontemporal_store(v, reinterpret_cast<V*>(p));
+}
+
+template <class T, int N>
+__device__ __forceinline__ void load_n_stream(const T* p, T (&out)[N]) {
+  typedef T V __attribute__((ext_vector_type(N)));
+  const V v = __builtin_nontemporal_load(reinterpret_cast<const V*>(p));
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = v[i];
+}
+
 template <class T>
 __device__ __forceinline__ T seed(int red) {
   if (red == RED_MAX) return -__builtin_huge_val();

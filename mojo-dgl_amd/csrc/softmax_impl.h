@@ -389,12 +389,20 @@ __global__ __launch_bounds__(BLOCK) void softmax_edge_kernel(const T* __restrict
   if (mask && mask[e] != 1) return;
   const int64_t r = row_of[e];
   T x[VEC], m[VEC], s[VEC];
-  load_cols<T, VEC>(logits + e * d, k0, d, vec_io, x);
+  if (VEC > 1 && vec_io) {
+    if constexpr (VEC > 1) load_n_stream<T, VEC>(logits + e * d + k0, x);
+  } else {
+    load_cols<T, VEC>(logits + e * d, k0, d, vec_io, x);
+  }
   load_cols<T, VEC>(tab + r * 2 * d, k0, d, vec_io, m);
   load_cols<T, VEC>(tab + r * 2 * d + d, k0, d, vec_io, s);
 #pragma unroll
   for (int v = 0; v < VEC; ++v) x[v] = exp_t(x[v] - m[v]) / s[v];
-  store_cols<T, VEC>(out + e * d, k0, d, vec_io, x);
+  if (VEC > 1 && vec_io) {
+    if constexpr (VEC > 1) store_n_stream<T, VEC>(out + e * d + k0, x);
+  } else {
+    store_cols<T, VEC>(out + e * d, k0, d, vec_io, x);
+  }
 }
 
 template <class T, int VEC>
