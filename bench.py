@@ -39,7 +39,7 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the gspmm kernel on the default workload, from
 # rocprofv3 FETCH_SIZE / WRITE_SIZE scaled by a 1 GiB copy (profiles/gat_power_law_kernels.md)
-GSPMM_TRAFFIC_BYTES = 72.28e9
+GSPMM_TRAFFIC_BYTES = 72.35e9
 MFMA_F32_PEAK_TFLOPS = 157.3
 
 
