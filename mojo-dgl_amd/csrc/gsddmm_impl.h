@@ -193,7 +193,7 @@ __global__ __launch_bounds__(BLOCK) void gsddmm_dot_kernel(GsddmmArgs<T> a) {
   for (int u = 0; u < DOT_U; ++u) {
     T pu = part[u];
     for (int off = G >> 1; off >= 1; off >>= 1) pu = pu + __shfl_xor(pu, off);
-    if (lp[u] && gl == 0) a.out[task[u]] = pu;
+    if (lp[u] && gl == 0) __builtin_nontemporal_store(pu, a.out + task[u]);
   }
 }
 
