@@ -129,14 +129,28 @@ def check(rc: int, what: str) -> None:
 
 
 # ------------------------------------------------------------------ device
+_GPU_SEEN = False
+_CUDA = torch.device("cuda")  # the current device, resolved at each use
+
+
 def device() -> torch.device:
-    if not torch.cuda.is_available():
-        raise RuntimeError(
-            "mojodgl runs its kernels on an AMD GPU through libmdgl.so and no GPU is visible")
-    return torch.device("cuda", torch.cuda.current_device())
+    """The current GPU (loud error when there is none; checked until one is seen)."""
+    global _GPU_SEEN
+    if not _GPU_SEEN:
+        if not torch.cuda.is_available():
+            raise RuntimeError(
+                "mojodgl runs its kernels on an AMD GPU through libmdgl.so and no GPU is visible")
+        _GPU_SEEN = True
+    return _CUDA
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def stream() -> int:
+    """torch's current stream on the current device, as a raw hipStream_t."""
+    if _raw_stream is not None:
+        return _raw_stream(torch.cuda.current_device())
     return torch.cuda.current_stream().cuda_stream
 
 
@@ -233,6 +247,8 @@ def on_device(f: Feat, dtype) -> torch.Tensor:
     tdt = torch_dtype(dtype)
     if f.is_torch:
         t = f.data
+        if t.is_cuda and t.dtype == tdt and t.is_contiguous():
+            return t
     else:
         t = torch.from_numpy(f.data)
     return t.to(device=dev, dtype=tdt).contiguous()

@@ -62,7 +62,10 @@ def feat_shape(shape):
 
 
 def width(shape) -> int:
-    return int(np.prod(feat_shape(shape), dtype=np.int64))
+    w = 1
+    for x in feat_shape(shape):
+        w *= int(x)
+    return w
 
 
 def out_feat_shape(lshape, rshape, dot=False):

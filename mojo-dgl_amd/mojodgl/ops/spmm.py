@@ -65,7 +65,9 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
     dtype = _lib.common_dtype(L, R)
     as_torch = _lib.wants_torch(L, R)
     dev = _lib.out_device(L, R)
-    dout = int(np.prod(fshape, dtype=np.int64))
+    dout = 1
+    for s_ in fshape:
+        dout *= int(s_)
     shape = (num_dst,) + tuple(fshape)
     tdt = _lib.torch_dtype(dtype)
     gdev = _lib.device()

@@ -634,6 +634,21 @@ def test_graph_from_gpu_ids_is_built_on_the_gpu():
     assert torch.equal(g.ndata["z"], want)
 
 
+def test_launches_go_to_torchs_current_stream():
+    from mojodgl import _lib
+
+    assert _lib.stream() == torch.cuda.current_stream().cuda_stream
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        assert _lib.stream() == side.cuda_stream
+        g = dgl.graph(rand_graph(100, 1000, 60), num_nodes=100)
+        x = torch.randn(100, 8, device="cuda")
+        w = torch.randn(1000, 8, device="cuda")
+        out = ops.u_mul_e_sum(g, x, w)
+    side.synchronize()
+    assert torch.equal(out, ops.u_mul_e_sum(g, x, w))
+
+
 def test_update_all_replays_from_a_captured_graph():
     """update_all on GPU tensors launches without host syncs, so it can be
     captured in a HIP graph (torch.cuda.CUDAGraph) and replayed; every
