@@ -135,7 +135,8 @@ int64_t mdgl_softmax_workspace_bytes(int64_t num_chunks, int64_t table_rows, int
  * column, softmax over the segment's rows; rows of empty segments are not
  * written. Segments are served through the plan of mdgl_edge_softmax_
  * (`order` / `bounds` / `nbins` by degree bin, or order null for every
- * segment in its own order, one wavefront each); segments longer than
+ * segment in its own order, one wavefront each; `packed_eid` as there, with
+ * the row index itself as the edge id); segments longer than
  * chunk_len come as chunks: chunk c covers rows chunk_start[c] ..
  * min(chunk_start[c] + chunk_len, offsets[chunk_row[c] + 1]) of segment
  * chunk_row[c], a segment's chunks are consecutive and chunk_first[c] is the
@@ -143,10 +144,10 @@ int64_t mdgl_softmax_workspace_bytes(int64_t num_chunks, int64_t table_rows, int
  * `scratch` is accepted for signature compatibility and unused. */
 int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, void* scratch,
                          int64_t num_seg, int64_t d, int64_t n, const int32_t* order,
-                         const int64_t* bounds, int nbins, const int32_t* chunk_row,
-                         const int32_t* chunk_start, const int32_t* chunk_first,
-                         int64_t num_chunks, int64_t slots, void* workspace,
-                         int64_t workspace_bytes, int dtype, void* stream);
+                         const int64_t* bounds, int nbins, const int32_t* packed_eid,
+                         const int32_t* chunk_row, const int32_t* chunk_start,
+                         const int32_t* chunk_first, int64_t num_chunks, int64_t slots,
+                         void* workspace, int64_t workspace_bytes, int dtype, void* stream);
 
 /* Replaces capi.mojo:149-165 (`mdgl_edge_softmax_`): per CSR row, per
  * column, softmax of logits[eid[i]] over the row's slots whose edge is
@@ -156,8 +157,12 @@ int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, v
  * log2(slots) + 1): bin k = order[bounds[k] .. bounds[k+1]) holds the rows of
  * degree <= 2^k (and > 2^(k-1)), order[bounds[nbins] .. bounds[nbins+1])
  * the rows of degree slots+1 .. chunk_len; or `order` = NULL: every row of
- * degree <= chunk_len in natural order. Longer rows come as chunks, as in
- * mdgl_segment_softmax. With `row_of_edge` (device, num_edges entries: the
+ * degree <= chunk_len in natural order. `packed_eid` (device, optional,
+ * needs `order`): for the rows of bins 0 .. nbins-1 in order, 2^k entries per
+ * row of bin k, the edge id eid[indptr[row] + s] of the row's slot s for
+ * s < degree and -1 after it; it saves the packed rows the indptr and eid
+ * lookups. Longer rows come as chunks, as in mdgl_segment_softmax. With
+ * `row_of_edge` (device, num_edges entries: the
  * CSR row of every edge id, i.e. the destination -- or source -- node) the
  * output is written by a second, edge-parallel pass in edge-id order
  * (coalesced stores) from a per-row (max, sum) table in the workspace;
@@ -166,11 +171,11 @@ int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, v
 int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
                        const int8_t* mask, const void* logits, void* dst, void* scratch,
                        int64_t num_nodes, int all_ones, int64_t d, const int32_t* order,
-                       const int64_t* bounds, int nbins, const int32_t* chunk_row,
-                       const int32_t* chunk_start, const int32_t* chunk_first,
-                       int64_t num_chunks, int64_t slots, const int32_t* row_of_edge,
-                       int64_t num_edges, void* workspace, int64_t workspace_bytes, int dtype,
-                       void* stream);
+                       const int64_t* bounds, int nbins, const int32_t* packed_eid,
+                       const int32_t* chunk_row, const int32_t* chunk_start,
+                       const int32_t* chunk_first, int64_t num_chunks, int64_t slots,
+                       const int32_t* row_of_edge, int64_t num_edges, void* workspace,
+                       int64_t workspace_bytes, int dtype, void* stream);
 
 /* Replaces capi.mojo:141-145 (`mdgl_segment_mm`): out rows of segment r are
  * a[rows] @ b[r]; seglen_a (device, int64, r entries) sums to at most n and

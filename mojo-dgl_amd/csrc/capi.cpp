@@ -538,9 +538,9 @@ namespace {
 int softmax_common(const char* what, const int32_t* indptr, const int32_t* eid,
                    const int8_t* mask, const void* logits, void* dst, int64_t num_rows, int64_t d,
                    const int32_t* order, const int64_t* bounds, int nbins,
-                   const int32_t* chunk_row, const int32_t* chunk_start,
-                   const int32_t* chunk_first, int64_t num_chunks, int64_t slots,
-                   const int32_t* row_of, int64_t num_edges, void* workspace,
+                   const int32_t* packed_eid, const int32_t* chunk_row,
+                   const int32_t* chunk_start, const int32_t* chunk_first, int64_t num_chunks,
+                   int64_t slots, const int32_t* row_of, int64_t num_edges, void* workspace,
                    int64_t workspace_bytes, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "%s: bad dtype %d", what, dtype);
   if (num_rows < 0 || d < 0 || num_chunks < 0) return fail(MDGL_EINVAL, "%s: negative size", what);
@@ -565,6 +565,8 @@ int softmax_common(const char* what, const int32_t* indptr, const int32_t* eid,
       if (bounds[k] > bounds[k + 1] || bounds[k] < 0)
         return fail(MDGL_EINVAL, "%s: bin bounds must be non-decreasing", what);
   }
+  if (packed_eid && !order)
+    return fail(MDGL_EINVAL, "%s: a packed edge list needs the row order it follows", what);
   if (num_chunks > 0 && (!chunk_row || !chunk_start || !chunk_first))
     return fail(MDGL_EINVAL, "%s: incomplete chunk list", what);
   if (row_of && num_edges < 0) return fail(MDGL_EINVAL, "%s: negative edge count", what);
@@ -582,6 +584,7 @@ int softmax_common(const char* what, const int32_t* indptr, const int32_t* eid,
   p.order = order;
   p.bounds = bounds;
   p.nbins = nbins;
+  p.packed_eid = packed_eid;
   p.num_chunks = num_chunks;
   p.chunk_row = chunk_row;
   p.chunk_start = chunk_start;
@@ -603,35 +606,35 @@ extern "C" {
 
 int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, void* scratch,
                          int64_t num_seg, int64_t d, int64_t n, const int32_t* order,
-                         const int64_t* bounds, int nbins, const int32_t* chunk_row,
-                         const int32_t* chunk_start, const int32_t* chunk_first,
-                         int64_t num_chunks, int64_t slots, void* workspace,
-                         int64_t workspace_bytes, int dtype, void* stream) {
+                         const int64_t* bounds, int nbins, const int32_t* packed_eid,
+                         const int32_t* chunk_row, const int32_t* chunk_start,
+                         const int32_t* chunk_first, int64_t num_chunks, int64_t slots,
+                         void* workspace, int64_t workspace_bytes, int dtype, void* stream) {
   (void)scratch;
   if (n < 0) return fail(MDGL_EINVAL, "segment_softmax: negative size");
   if (n >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "segment_softmax: 2**31 or more rows");
   if (n == 0) return MDGL_OK;
   return softmax_common("segment_softmax", offsets, nullptr, nullptr, value, dst, num_seg, d,
-                        order, bounds, nbins, chunk_row, chunk_start, chunk_first, num_chunks,
-                        slots, nullptr, 0, workspace, workspace_bytes, dtype, stream);
+                        order, bounds, nbins, packed_eid, chunk_row, chunk_start, chunk_first,
+                        num_chunks, slots, nullptr, 0, workspace, workspace_bytes, dtype, stream);
 }
 
 int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
                        const int8_t* mask, const void* logits, void* dst, void* scratch,
                        int64_t num_nodes, int all_ones, int64_t d, const int32_t* order,
-                       const int64_t* bounds, int nbins, const int32_t* chunk_row,
-                       const int32_t* chunk_start, const int32_t* chunk_first,
-                       int64_t num_chunks, int64_t slots, const int32_t* row_of_edge,
-                       int64_t num_edges, void* workspace, int64_t workspace_bytes, int dtype,
-                       void* stream) {
+                       const int64_t* bounds, int nbins, const int32_t* packed_eid,
+                       const int32_t* chunk_row, const int32_t* chunk_start,
+                       const int32_t* chunk_first, int64_t num_chunks, int64_t slots,
+                       const int32_t* row_of_edge, int64_t num_edges, void* workspace,
+                       int64_t workspace_bytes, int dtype, void* stream) {
   (void)indices;
   (void)scratch;
   if (num_nodes > 0 && d > 0 && !eid) return fail(MDGL_EINVAL, "edge_softmax: null eid");
   if (all_ones != 1 && !mask) return fail(MDGL_EINVAL, "edge_softmax: null mask");
   return softmax_common("edge_softmax", indptr, eid, all_ones == 1 ? nullptr : mask, logits, dst,
-                        num_nodes, d, order, bounds, nbins, chunk_row, chunk_start, chunk_first,
-                        num_chunks, slots, row_of_edge, num_edges, workspace, workspace_bytes,
-                        dtype, stream);
+                        num_nodes, d, order, bounds, nbins, packed_eid, chunk_row, chunk_start,
+                        chunk_first, num_chunks, slots, row_of_edge, num_edges, workspace,
+                        workspace_bytes, dtype, stream);
 }
 
 }  // extern "C"

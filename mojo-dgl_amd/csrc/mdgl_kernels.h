@@ -91,6 +91,9 @@ struct SoftmaxParams {
   const int32_t* order;
   const int64_t* bounds;  // host: nbins + 2 entries
   int nbins;
+  // null, or the edge ids of the packed rows slot by slot (2^k per row of
+  // bin k, -1 past the degree, bins one after the other)
+  const int32_t* packed_eid;
   int64_t num_chunks;
   const int32_t* chunk_row;
   const int32_t* chunk_start;

@@ -17,8 +17,11 @@
 //   * wavefront rows: up to CPL * Pw edges, CPL per slot;
 //   * chunked rows (longer): chunks of CPL * Pw edges; launch 1 writes each
 //     chunk's (max, sum of exp(x - max)) per column, launch 2 merges a row's
-//     chunks in chunk order (M = max m_c, S = sum s_c * exp(m_c - M)) and writes
-//     exp(x - M) / S over the chunk.
+//     chunks (M = max m_c, S = sum s_c * exp(m_c - M); slot s of the wavefront
+//     folds chunks s, s + Pw, ... in chunk order, the slots then combine by
+//     butterflies) and writes exp(x - M) / S over the chunk.
+// A packed row's slots find their edge ids in the plan's packed edge list
+// when there is one (one load), else through order -> indptr -> eid.
 // Launch 1 takes the chunks (their workgroups first, so the long rows start
 // early) and the wavefront rows; the packed rows run in a launch of their
 // own, whose kernel needs far fewer registers, each wavefront serving
@@ -50,6 +53,8 @@ struct SoftmaxArgs {
   const int32_t* order;          // rows sorted by degree, or null (natural order)
   int64_t bin_start[8];          // packed bin k (2^k slots): order[bin_start[k] .. bin_start[k+1])
   int64_t bin_wave[9];           // wavefronts before bin k (slabs included)
+  const int32_t* peid;           // packed edge ids, or null
+  int64_t bin_slot[8];           // entries of peid before bin k
   int64_t mid_start, mid_end;    // wavefront rows: order[mid_start .. mid_end) or all rows
   int64_t num_chunks;
   const int32_t* chunk_row;
@@ -143,30 +148,49 @@ __device__ __forceinline__ void soft_group(const SoftmaxArgs<T>& a, int mode, bo
   }
 
   if (mode == SM_WRITE) {
-    // merge this row's chunk partials in chunk order
+    // merge this row's chunk partials: slot s takes chunks s, s + Pr, ...
+    // (each slot's sequence in chunk order), then the slots combine by
+    // butterflies, so a row of many chunks costs ceil(chunks / Pr) rounds
     const int64_t c0 = a.chunk_first[chunk];
     const int64_t row = a.chunk_row[chunk];
     const int64_t nch = (a.indptr[row + 1] - a.indptr[row] + a.chunk_len - 1) / a.chunk_len;
+    T pmv[VEC], psv[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
       m[v] = ninf;
       sum[v] = T(0);
     }
     if (feat_ok) {
-      for (int64_t q = c0; q < c0 + nch; ++q)
+      for (int64_t q = c0 + s; q < c0 + nch; q += Pr)
 #pragma unroll
         for (int v = 0; v < VEC; ++v)
           if (k0 + v < a.d) {
             const T t = a.pm[q * a.d + k0 + v];
             m[v] = t > m[v] ? t : m[v];
           }
-      for (int64_t q = c0; q < c0 + nch; ++q)
+    }
+    for (int off = L; off < span; off <<= 1) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const T o = __shfl_xor(m[v], off);
+        m[v] = o > m[v] ? o : m[v];
+      }
+    }
+    if (feat_ok) {
+      for (int64_t q = c0 + s; q < c0 + nch; q += Pr) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+          pmv[v] = k0 + v < a.d ? a.pm[q * a.d + k0 + v] : ninf;
+          psv[v] = k0 + v < a.d ? a.ps[q * a.d + k0 + v] : T(0);
+        }
 #pragma unroll
         for (int v = 0; v < VEC; ++v)
-          if (k0 + v < a.d) {
-            const T t = a.pm[q * a.d + k0 + v];
-            if (t != ninf) sum[v] = sum[v] + a.ps[q * a.d + k0 + v] * exp_t(t - m[v]);
-          }
+          if (pmv[v] != ninf) sum[v] = sum[v] + psv[v] * exp_t(pmv[v] - m[v]);
+      }
+    }
+    for (int off = L; off < span; off <<= 1) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) sum[v] = sum[v] + __shfl_xor(sum[v], off);
     }
   } else {
 #pragma unroll
@@ -292,7 +316,7 @@ __device__ __forceinline__ void softmax_packed_u(const SoftmaxArgs<T>& a, int64_
   const int64_t b0 = a.bin_start[k], b1 = a.bin_start[k + 1];
   // indices are clamped into the bin (and rows have >= 1 edge), so every
   // load below is unconditional and in bounds; rok / ok mask the results
-  int64_t slab[PK_U], row[PK_U];
+  int64_t slab[PK_U], row[PK_U], ic[PK_U];
   bool rok[PK_U];
 #pragma unroll
   for (int r = 0; r < PK_U; ++r) {
@@ -300,22 +324,36 @@ __device__ __forceinline__ void softmax_packed_u(const SoftmaxArgs<T>& a, int64_
     slab[r] = local % a.S;
     const int64_t i = b0 + (local / a.S) * per + lane / (Pr * L);
     rok[r] = i < b1;
-    row[r] = a.order[rok[r] ? i : b0];
-  }
-  int start[PK_U], stop[PK_U];
-#pragma unroll
-  for (int r = 0; r < PK_U; ++r) {
-    start[r] = a.indptr[row[r]];
-    stop[r] = a.indptr[row[r] + 1];
+    ic[r] = rok[r] ? i : b0;
   }
   int64_t e[PK_U];
   bool ok[PK_U];
+  if (a.peid) {
+    // the plan lists every packed slot's edge id: one coalesced load per
+    // round instead of the chain order -> indptr -> eid (-1 past a row's
+    // degree; those lanes read edge 0, which exists, and are masked)
 #pragma unroll
-  for (int r = 0; r < PK_U; ++r) {
-    const int j = start[r] + sl;
-    ok[r] = rok[r] && j < stop[r];
-    const int jc = ok[r] ? j : start[r];
-    e[r] = a.eid ? (int64_t)a.eid[jc] : (int64_t)jc;
+    for (int r = 0; r < PK_U; ++r) {
+      const int32_t pe = a.peid[a.bin_slot[k] + (ic[r] - b0) * Pr + sl];
+      ok[r] = rok[r] && pe >= 0;
+      e[r] = pe >= 0 ? (int64_t)pe : 0;
+      row[r] = a.tab ? (int64_t)a.order[ic[r]] : 0;
+    }
+  } else {
+    int start[PK_U], stop[PK_U];
+#pragma unroll
+    for (int r = 0; r < PK_U; ++r) {
+      row[r] = a.order[ic[r]];
+      start[r] = a.indptr[row[r]];
+      stop[r] = a.indptr[row[r] + 1];
+    }
+#pragma unroll
+    for (int r = 0; r < PK_U; ++r) {
+      const int j = start[r] + sl;
+      ok[r] = rok[r] && j < stop[r];
+      const int jc = ok[r] ? j : start[r];
+      e[r] = a.eid ? (int64_t)a.eid[jc] : (int64_t)jc;
+    }
   }
   if (a.mask) {
 #pragma unroll
@@ -429,6 +467,12 @@ hipError_t launch_softmax_vec(const SoftmaxParams& p) {
   if (p.order) {
     a.nbins = p.nbins;
     for (int k = 0; k <= p.nbins; ++k) a.bin_start[k] = p.bounds[k];
+    a.peid = p.packed_eid;
+    int64_t slots_before = 0;
+    for (int k = 0; k < p.nbins; ++k) {
+      a.bin_slot[k] = slots_before;
+      slots_before += (a.bin_start[k + 1] - a.bin_start[k]) << k;
+    }
     for (int k = 0; k < p.nbins; ++k) {
       // padded to a multiple of PK_U: a wavefront of the packed launch
       // never straddles two bins

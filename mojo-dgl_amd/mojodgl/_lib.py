@@ -71,10 +71,10 @@ _SIGNATURES = {
     "mdgl_segment_reduce": ([_P, _P, _P, _I64, _I64, _C, _I64, _C, _C, _P], _C),
     "mdgl_softmax_geometry": ([_I64, _C, _P, _P, _P, _P], _C),
     "mdgl_softmax_workspace_bytes": ([_I64, _I64, _I64, _C], _I64),
-    "mdgl_segment_softmax": ([_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _C, _P, _P, _P, _I64,
-                              _I64, _P, _I64, _C, _P], _C),
+    "mdgl_segment_softmax": ([_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _C, _P, _P, _P, _P,
+                              _I64, _I64, _P, _I64, _C, _P], _C),
     "mdgl_edge_softmax_": ([_P, _P, _P, _P, _P, _P, _P, _I64, _C, _I64, _P, _P, _C, _P, _P, _P,
-                            _I64, _I64, _P, _I64, _P, _I64, _C, _P], _C),
+                            _P, _I64, _I64, _P, _I64, _P, _I64, _C, _P], _C),
     "mdgl_segment_mm": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _C, _P], _C),
     "mdgl_segment_mm_workspace_bytes": ([_I64, _I64, _I64, _I64, _C], _I64),
     "mdgl_gather_mm": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _C, _P], _C),

@@ -120,11 +120,12 @@ class _DeviceCSR:
         self._softmax = {}
 
     def softmax_plan(self, slots, chunk_len):
-        """Degree-sorted row order and chunks for a softmax lane layout (cached)."""
+        """Degree-sorted row order, packed edge ids and chunks for a softmax
+        lane layout (cached)."""
         key = (int(slots), int(chunk_len))
         if key not in self._softmax:
             self._softmax[key] = SoftmaxPlan.from_device(self.indptr, slots, chunk_len,
-                                                         ordered=True)
+                                                         ordered=True, eid=self.eid)
         return self._softmax[key]
 
 

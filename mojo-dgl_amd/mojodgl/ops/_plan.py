@@ -17,10 +17,30 @@ import torch
 from .. import _lib
 
 
-class SoftmaxPlan:
-    """Plan arrays on the GPU (order / chunks) and the host bin bounds."""
+def _packed_bin(rows, indptr, k, eid, xp):
+    """Edge ids of bin k's rows slot by slot: 2^k per row, -1 past the degree
+    (`xp` is numpy or torch; `eid` None means the slot index itself)."""
+    width = 1 << k
+    start = indptr[rows]
+    deg = indptr[rows + 1] - start
+    if xp is np:
+        slot = np.arange(width, dtype=np.int64)
+    else:
+        slot = torch.arange(width, dtype=torch.int64, device=rows.device)
+    valid = slot[None, :] < deg[:, None]
+    j = xp.where(valid, start[:, None] + slot[None, :], 0)
+    val = j if eid is None else eid[j]
+    if xp is not np:
+        val = val.to(torch.int64)
+    return xp.where(valid, val, -1).reshape(-1)
 
-    def __init__(self, indptr: np.ndarray, slots: int, chunk_len: int, ordered: bool):
+
+class SoftmaxPlan:
+    """Plan arrays on the GPU (order / packed edge ids / chunks) and the host
+    bin bounds."""
+
+    def __init__(self, indptr: np.ndarray, slots: int, chunk_len: int, ordered: bool,
+                 eid: np.ndarray | None = None):
         deg = np.diff(indptr)
         self.slots = int(slots)
         self.chunk_len = int(chunk_len)
@@ -42,25 +62,35 @@ class SoftmaxPlan:
             self.chunk_row = self.chunk_start = self.chunk_first = None
         self.order = None
         self.bounds = None
+        self.packed = None
         if ordered:
             rows = np.nonzero((deg > 0) & (deg <= chunk_len))[0]
             d = deg[rows]
             key = np.where(d <= slots, np.ceil(np.log2(np.maximum(d, 1))), self.nbins)
             key = key.astype(np.uint8)
             perm = np.argsort(key, kind="stable")
-            self.order = _lib.i32_device(rows[perm])
+            ordered_rows = rows[perm]
+            self.order = _lib.i32_device(ordered_rows)
             counts = np.bincount(key, minlength=self.nbins + 1)
             self.bounds = np.zeros(self.nbins + 2, dtype=np.int64)
             np.cumsum(counts, out=self.bounds[1:])
+            ip = np.asarray(indptr, dtype=np.int64)
+            parts = [_packed_bin(ordered_rows[self.bounds[k]:self.bounds[k + 1]], ip, k,
+                                 None if eid is None else np.asarray(eid, dtype=np.int64), np)
+                     for k in range(self.nbins) if self.bounds[k + 1] > self.bounds[k]]
+            if parts:
+                self.packed = _lib.i32_device(np.concatenate(parts))
 
     @classmethod
     def from_device(cls, indptr: torch.Tensor, slots: int, chunk_len: int, ordered: bool,
-                    num_chunks: int | None = None):
+                    num_chunks: int | None = None, eid: torch.Tensor | None = None):
         """The same plan built on the GPU from GPU offsets (int32 or int64):
         chunks of the long rows, and with `ordered` the rows with
         0 < degree <= chunk_len grouped by degree bin, stably (ascending row
-        id inside a bin), through the radix grouping of mdgl_build_csr.
-        `num_chunks`, when the caller knows it, saves a read back."""
+        id inside a bin), through the radix grouping of mdgl_build_csr, and
+        the packed rows' edge ids slot by slot (`eid` the CSR's edge ids, or
+        None for the slot index). `num_chunks`, when the caller knows it,
+        saves a read back."""
         from ..heterograph import build_device_csr
 
         self = cls.__new__(cls)
@@ -86,6 +116,7 @@ class SoftmaxPlan:
             self.chunk_first = cfirst.to(torch.int32)
         self.order = None
         self.bounds = None
+        self.packed = None
         if ordered:
             nb = self.nbins
             # bin k (ceil(log2(degree))) for degree <= slots, bin nb for the
@@ -98,6 +129,11 @@ class SoftmaxPlan:
             ptr, _, order = build_device_csr(key.to(torch.int32), None, nb + 2)
             self.order = order
             self.bounds = ptr[: nb + 2].cpu().numpy().astype(np.int64)
+            b = self.bounds
+            parts = [_packed_bin(order[b[k]:b[k + 1]].to(torch.int64), ip, k, eid, torch)
+                     for k in range(nb) if b[k + 1] > b[k]]
+            if parts:
+                self.packed = torch.cat(parts).to(torch.int32)
         return self
 
     def bounds_ptr(self):

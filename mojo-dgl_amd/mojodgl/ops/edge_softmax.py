@@ -133,14 +133,15 @@ def _edge_softmax(graph, logits, eids, norm_by):
             row_of = (vids if norm_by == "dst" else uids)[idx]
             indptr, _, eid = heterograph.build_device_csr(row_of, None, num_nodes)
             rows = num_nodes if idx.shape[0] else 0
-            plan = _plan.SoftmaxPlan.from_device(indptr, slots, chunk_len, ordered=True)
+            plan = _plan.SoftmaxPlan.from_device(indptr, slots, chunk_len, ordered=True,
+                                                 eid=eid)
         if rows:
             n_edges = lg.shape[0]
             ws, nbytes = _plan.workspace(plan, d, dtype, rows if row_of is not None else 0)
             rc = _lib.lib().mdgl_edge_softmax_(
                 indptr.data_ptr(), None, eid.data_ptr(), None, lg.data_ptr(), out.data_ptr(), None,
                 rows, 1, d, _lib.ptr(plan.order), plan.bounds_ptr(), plan.nbins,
-                _lib.ptr(plan.chunk_row), _lib.ptr(plan.chunk_start), _lib.ptr(plan.chunk_first),
+                _lib.ptr(plan.packed), _lib.ptr(plan.chunk_row), _lib.ptr(plan.chunk_start), _lib.ptr(plan.chunk_first),
                 plan.num_chunks, plan.slots, _lib.ptr(row_of), n_edges, _lib.ptr(ws), nbytes,
                 _lib.dtype_code(dtype), _lib.stream())
             _lib.check(rc, "edge_softmax")

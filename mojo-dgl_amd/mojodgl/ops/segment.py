@@ -175,7 +175,7 @@ def segment_softmax(seglen, value):
         ws, nbytes = _plan.workspace(plan, d, dtype)
         rc = _lib.lib().mdgl_segment_softmax(
             off.data_ptr(), val.data_ptr(), out.data_ptr(), None, num_seg, d, n,
-            _lib.ptr(plan.order), plan.bounds_ptr(), plan.nbins,
+            _lib.ptr(plan.order), plan.bounds_ptr(), plan.nbins, _lib.ptr(plan.packed),
             _lib.ptr(plan.chunk_row), _lib.ptr(plan.chunk_start), _lib.ptr(plan.chunk_first),
             plan.num_chunks, plan.slots, _lib.ptr(ws), nbytes, _lib.dtype_code(dtype),
             _lib.stream())

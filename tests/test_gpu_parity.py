@@ -299,9 +299,13 @@ def test_softmax_plan_built_on_the_gpu_equals_the_host_plan(slots, chunk_len):
                           [0, chunk_len, chunk_len + 1, slots, slots + 1, 1]])
     rng.shuffle(deg)
     indptr = np.concatenate([[0], np.cumsum(deg)])
-    host = _plan.SoftmaxPlan(indptr, slots, chunk_len, ordered=True)
-    dev = _plan.SoftmaxPlan.from_device(torch.from_numpy(indptr).cuda(), slots, chunk_len,
-                                        ordered=True)
+    eid = rng.permutation(int(indptr[-1])).astype(np.int32)
+    for ids in (None, eid):
+        host = _plan.SoftmaxPlan(indptr, slots, chunk_len, ordered=True, eid=ids)
+        dev = _plan.SoftmaxPlan.from_device(
+            torch.from_numpy(indptr).cuda(), slots, chunk_len, ordered=True,
+            eid=None if ids is None else torch.from_numpy(ids).cuda())
+        np.testing.assert_array_equal(dev.packed.cpu().numpy(), host.packed.cpu().numpy())
     assert dev.num_chunks == host.num_chunks and dev.nbins == host.nbins
     np.testing.assert_array_equal(dev.bounds, host.bounds)
     n = int(host.bounds[-1])
@@ -382,16 +386,23 @@ def test_segment_softmax_degree_plan_through_the_abi():
     off = torch.from_numpy(np.concatenate([[0], np.cumsum(seglen)]).astype(np.int32)).cuda()
     slots, chunk_len = _plan.geometry(d, np.float32, val, out)
     plan = _plan.SoftmaxPlan.from_device(off, slots, chunk_len, ordered=True)
+    assert plan.packed is not None
     ws, nbytes = _plan.workspace(plan, d, np.float32)
-    rc = _lib.lib().mdgl_segment_softmax(
-        off.data_ptr(), val.data_ptr(), out.data_ptr(), None, seglen.size, d, value.shape[0],
-        _lib.ptr(plan.order), plan.bounds_ptr(), plan.nbins, _lib.ptr(plan.chunk_row),
-        _lib.ptr(plan.chunk_start), _lib.ptr(plan.chunk_first), plan.num_chunks, plan.slots,
-        _lib.ptr(ws), nbytes, 0, _lib.stream())
-    _lib.check(rc, "segment_softmax")
     ref = oracle.segment_softmax(seglen, value, np.float64)
-    close(out.cpu().numpy(), ref, ref, np.float32, "segment_softmax degree plan")
-    np.testing.assert_array_equal(out.cpu().numpy(), ops.segment_softmax(seglen, value))
+    results = []
+    for packed in (plan.packed, None):  # packed slot list, and the indptr chain
+        out.zero_()
+        rc = _lib.lib().mdgl_segment_softmax(
+            off.data_ptr(), val.data_ptr(), out.data_ptr(), None, seglen.size, d,
+            value.shape[0], _lib.ptr(plan.order), plan.bounds_ptr(), plan.nbins,
+            _lib.ptr(packed), _lib.ptr(plan.chunk_row), _lib.ptr(plan.chunk_start),
+            _lib.ptr(plan.chunk_first), plan.num_chunks, plan.slots, _lib.ptr(ws), nbytes, 0,
+            _lib.stream())
+        _lib.check(rc, "segment_softmax")
+        close(out.cpu().numpy(), ref, ref, np.float32, "segment_softmax degree plan")
+        np.testing.assert_array_equal(out.cpu().numpy(), ops.segment_softmax(seglen, value))
+        results.append(out.cpu().numpy())
+    np.testing.assert_array_equal(results[0], results[1])
 
 
 def test_segment_gpu_lengths_are_validated():
@@ -747,16 +758,24 @@ def test_edge_softmax_power_law_and_mask_through_the_abi():
                                      want.ctypes.data, n, 0, 8, 1)
     sel = mask == 1
     _, vids = g._device_coo()
-    for row_of in (None, vids):  # one-pass and two-pass forms
-        out.fill_(-7.0)
-        ws, nbytes = _plan.workspace(plan, 8, np.float32, n if row_of is not None else 0)
-        rc = _lib.lib().mdgl_edge_softmax_(
-            csr.indptr.data_ptr(), None, csr.eid.data_ptr(), m.data_ptr(), lg.data_ptr(),
-            out.data_ptr(), None, n, 0, 8, _lib.ptr(plan.order), plan.bounds_ptr(), plan.nbins,
-            _lib.ptr(plan.chunk_row), _lib.ptr(plan.chunk_start), _lib.ptr(plan.chunk_first),
-            plan.num_chunks, plan.slots, _lib.ptr(row_of), e, _lib.ptr(ws), nbytes, 0,
-            _lib.stream())
-        assert rc == 0
-        got = out.cpu().numpy()
-        np.testing.assert_array_equal(got[~sel], -7.0)  # unselected rows untouched
-        close(got[sel], want[sel], want[sel], np.float32, "masked")
+    assert plan.packed is not None
+    first = None
+    # one-pass and two-pass forms, each with the packed slot list and with
+    # the indptr chain: all four write the same values
+    for row_of in (None, vids):
+        for packed in (plan.packed, None):
+            out.fill_(-7.0)
+            ws, nbytes = _plan.workspace(plan, 8, np.float32, n if row_of is not None else 0)
+            rc = _lib.lib().mdgl_edge_softmax_(
+                csr.indptr.data_ptr(), None, csr.eid.data_ptr(), m.data_ptr(), lg.data_ptr(),
+                out.data_ptr(), None, n, 0, 8, _lib.ptr(plan.order), plan.bounds_ptr(),
+                plan.nbins, _lib.ptr(packed), _lib.ptr(plan.chunk_row),
+                _lib.ptr(plan.chunk_start), _lib.ptr(plan.chunk_first), plan.num_chunks,
+                plan.slots, _lib.ptr(row_of), e, _lib.ptr(ws), nbytes, 0, _lib.stream())
+            assert rc == 0
+            got = out.cpu().numpy()
+            np.testing.assert_array_equal(got[~sel], -7.0)  # unselected rows untouched
+            close(got[sel], want[sel], want[sel], np.float32, "masked")
+            if first is None:
+                first = got
+            np.testing.assert_array_equal(got, first)

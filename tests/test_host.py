@@ -184,3 +184,29 @@ def test_chunk_plan():
         assert np.all(row[ptr[h]:ptr[h + 1]] == r)
         np.testing.assert_array_equal(starts, np.arange(indptr[r], indptr[r + 1], 16))
     assert row.size == sum((d + 15) // 16 for d in deg if d > 16)
+
+
+def test_packed_softmax_slots_list_each_rows_edges():
+    """The packed edge list of a softmax plan: for the rows of bin k (in plan
+    order), 2^k entries each, the edge ids of the row's CSR slots then -1."""
+    from mojodgl.ops._plan import _packed_bin
+
+    rng = np.random.default_rng(3)
+    deg = rng.integers(0, 9, 50)
+    indptr = np.concatenate([[0], np.cumsum(deg)]).astype(np.int64)
+    eid = rng.permutation(int(indptr[-1]))
+    for k in range(4):
+        rows = np.nonzero((deg > (1 << k) // 2) & (deg <= (1 << k)))[0]
+        rows = rng.permutation(rows)
+        for ids in (None, eid):
+            got = _packed_bin(rows, indptr, k, ids, np)
+            want = []
+            for r in rows:
+                for s in range(1 << k):
+                    j = indptr[r] + s
+                    want.append(-1 if s >= deg[r] else (j if ids is None else ids[j]))
+            np.testing.assert_array_equal(got, np.array(want, dtype=np.int64))
+    torch_rows = torch.tensor([3, 1, 4])
+    got = _packed_bin(torch_rows, torch.from_numpy(indptr), 3, torch.from_numpy(eid), torch)
+    np.testing.assert_array_equal(got.numpy(), _packed_bin(np.array([3, 1, 4]), indptr, 3, eid,
+                                                           np))
