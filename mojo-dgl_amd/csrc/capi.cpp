@@ -540,7 +540,8 @@ int softmax_common(const char* what, const int32_t* indptr, const int32_t* eid,
                    const int32_t* order, const int64_t* bounds, int nbins,
                    const int32_t* packed_eid, const int32_t* chunk_row,
                    const int32_t* chunk_start, const int32_t* chunk_first, int64_t num_chunks,
-                   int64_t slots, const int32_t* row_of, int64_t num_edges, void* workspace,
+                   int64_t slots, const int32_t* row_of, int64_t num_edges,
+                   int64_t num_slots, void* workspace,
                    int64_t workspace_bytes, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "%s: bad dtype %d", what, dtype);
   if (num_rows < 0 || d < 0 || num_chunks < 0) return fail(MDGL_EINVAL, "%s: negative size", what);
@@ -581,6 +582,7 @@ int softmax_common(const char* what, const int32_t* indptr, const int32_t* eid,
   p.out = dst;
   p.num_rows = num_rows;
   p.d = d;
+  p.num_slots = num_slots;
   p.order = order;
   p.bounds = bounds;
   p.nbins = nbins;
@@ -616,7 +618,8 @@ int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, v
   if (n == 0) return MDGL_OK;
   return softmax_common("segment_softmax", offsets, nullptr, nullptr, value, dst, num_seg, d,
                         order, bounds, nbins, packed_eid, chunk_row, chunk_start, chunk_first,
-                        num_chunks, slots, nullptr, 0, workspace, workspace_bytes, dtype, stream);
+                        num_chunks, slots, nullptr, 0, n, workspace, workspace_bytes, dtype,
+                        stream);
 }
 
 int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
@@ -633,8 +636,8 @@ int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int3
   if (all_ones != 1 && !mask) return fail(MDGL_EINVAL, "edge_softmax: null mask");
   return softmax_common("edge_softmax", indptr, eid, all_ones == 1 ? nullptr : mask, logits, dst,
                         num_nodes, d, order, bounds, nbins, packed_eid, chunk_row, chunk_start,
-                        chunk_first, num_chunks, slots, row_of_edge, num_edges, workspace,
-                        workspace_bytes, dtype, stream);
+                        chunk_first, num_chunks, slots, row_of_edge, num_edges,
+                        num_edges > 0 ? num_edges : 0, workspace, workspace_bytes, dtype, stream);
 }
 
 }  // extern "C"

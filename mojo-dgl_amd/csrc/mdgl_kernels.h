@@ -87,7 +87,8 @@ struct SoftmaxParams {
   const void* logits;
   void* out;
   int64_t num_rows, d;
-  int vec;  // elements per lane
+  int64_t num_slots;  // CSR entries (indptr[num_rows]) when known, else 0
+  int vec;            // elements per lane
   const int32_t* order;
   const int64_t* bounds;  // host: nbins + 2 entries
   int nbins;

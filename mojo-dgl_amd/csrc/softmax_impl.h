@@ -14,7 +14,9 @@
 // are cut into slabs, one wavefront per slab. Rows are served by degree:
 //   * packed: rows sorted by degree; a row of at most 2^k edges gets 2^k slots
 //     (one edge each), so a wavefront takes Pw / 2^k rows of one degree bin;
-//   * wavefront rows: up to CPL * Pw edges, CPL per slot;
+//   * wavefront rows: up to CPL * Pw edges, CPL per slot; in natural order
+//     (no row order) R consecutive rows share a wavefront, Pw / R slots each,
+//     when they fit (R from the mean degree);
 //   * chunked rows (longer): chunks of CPL * Pw edges; launch 1 writes each
 //     chunk's (max, sum of exp(x - max)) per column, launch 2 merges a row's
 //     chunks (M = max m_c, S = sum s_c * exp(m_c - M); slot s of the wavefront
@@ -56,6 +58,7 @@ struct SoftmaxArgs {
   const int32_t* peid;           // packed edge ids, or null
   int64_t bin_slot[8];           // entries of peid before bin k
   int64_t mid_start, mid_end;    // wavefront rows: order[mid_start .. mid_end) or all rows
+  int nat_r;                     // rows sharing a wavefront in natural order (else 1)
   int64_t num_chunks;
   const int32_t* chunk_row;
   const int32_t* chunk_start;
@@ -284,14 +287,37 @@ __global__ __launch_bounds__(BLOCK) void softmax_kernel(SoftmaxArgs<T> a) {
   const int64_t lb = xcd_remap(b - a.chunk_blocks, a.light_blocks);
   const int64_t w = lb * WAVES_PER_BLOCK + (threadIdx.x >> 6);
   if (w >= a.light_waves) return;
-  const int64_t nmid = (a.mid_end - a.mid_start) * a.S;
+  const int R = a.nat_r;
+  const int64_t nmid = ((a.mid_end - a.mid_start + R - 1) / R) * a.S;
   if (w < nmid) {
-    // one wavefront per row
-    const int64_t i = a.mid_start + w / a.S, slab = w % a.S;
-    const int64_t row = a.order ? (int64_t)a.order[i] : i;
-    const int start = a.indptr[row], stop = a.indptr[row + 1];
-    const bool ok = stop > start && stop - start <= a.chunk_len;
-    soft_group<T, VEC, SOFT_CPL>(a, SM_FULL, ok, row, start, stop, Pw, slab, lane, 0);
+    // R consecutive rows per wavefront (R = 1 with a row order): they share
+    // it, Pw / R slots each, when the longest of them fits those slots' CPL
+    // rounds; otherwise each takes the whole wavefront in turn (the choice
+    // is uniform per wavefront)
+    const int64_t slab = w % a.S;
+    const int64_t i0 = a.mid_start + (w / a.S) * R;
+    int Pr = Pw, iters = R;
+    if (R > 1) {
+      const int64_t i = i0 + (lane / a.L) / (Pw / R);
+      const int deg = i < a.mid_end ? a.indptr[i + 1] - a.indptr[i] : 0;
+      if (wave_max_int(deg) <= (Pw / R) * SOFT_CPL) {
+        Pr = Pw / R;
+        iters = 1;
+      }
+    }
+    for (int r = 0; r < iters; ++r) {
+      if (iters > 1 && i0 + r >= a.mid_end) break;  // uniform
+      const int64_t i = iters == 1 ? i0 + (lane / a.L) / Pr : i0 + r;
+      const bool in = i < a.mid_end;
+      const int64_t row = a.order ? (in ? (int64_t)a.order[i] : 0) : i;
+      int start = 0, stop = 0;
+      if (in) {
+        start = a.indptr[row];
+        stop = a.indptr[row + 1];
+      }
+      const bool ok = in && stop > start && stop - start <= a.chunk_len;
+      soft_group<T, VEC, SOFT_CPL>(a, SM_FULL, ok, row, start, stop, Pr, slab, lane, 0);
+    }
     return;
   }
 }
@@ -489,7 +515,16 @@ hipError_t launch_softmax_vec(const SoftmaxParams& p) {
     a.mid_end = p.num_rows;
   }
   const int64_t packed_waves = waves;
-  a.light_waves = (a.mid_end - a.mid_start) * a.S;
+  // natural order: R rows per wavefront, Pw / R slots each, sized so the
+  // mean row (slots / rows) fills at most ~60 % of its CPL rounds
+  a.nat_r = 1;
+  if (!p.order && p.num_slots > 0 && p.num_rows > 0) {
+    const double mean = double(p.num_slots) / double(p.num_rows);
+    int pr = 1;
+    while (pr < a.Pw && pr * SOFT_CPL < 1.6 * mean) pr <<= 1;
+    a.nat_r = a.Pw / pr;
+  }
+  a.light_waves = ((a.mid_end - a.mid_start + a.nat_r - 1) / a.nat_r) * a.S;
   a.light_blocks = (a.light_waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
   a.num_chunks = p.num_chunks;
   a.chunk_row = p.chunk_row;
