@@ -328,13 +328,28 @@ def workload_c1(args):
     t.record()
     torch.cuda.synchronize()
     gms = s.elapsed_time(t) / args.steps
+    # each op again with cold caches: a 512 MB write before every call evicts
+    # L2 and the 256 MB MALL (the four calls above run cache-resident)
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    cold = {}
+    for red in ("sum", "mean", "max", "min"):
+        tot = 0.0
+        for _ in range(args.steps):
+            flush.fill_(1)
+            s.record()
+            g.update_all(fn.u_mul_e("h", "e", "m"), getattr(fn, red)("m", "z"))
+            t.record()
+            torch.cuda.synchronize()
+            tot += s.elapsed_time(t)
+        cold["update_all_" + red] = round(tot / args.steps, 4)
     return {"metric": "gSpMM GEdge·feat/s, fp32, 1 GPU", "value": round(units / ms / 1e6, 2),
             "unit": "GEdge·feat/s", "ms_per_step": round(ms, 4), "dtype": "f32",
             "config": {"workload": "update_all u_mul_e + sum/mean/max/min, uniform graph",
                        "num_nodes": N, "num_edges": E, "feat": D},
             "breakdown_ms": {k: round(timer.avg_ms(k), 4) for k in timer.totals},
             "graph_replay": {"ms_per_step": round(gms, 4),
-                             "value": round(units / gms / 1e6, 2)}}
+                             "value": round(units / gms / 1e6, 2)},
+            "cold_caches_ms": cold}
 
 
 def workload_c3(args):
@@ -447,6 +462,21 @@ def workload_c5(args):
     timer = OpTimer()
     ms = run_steps(step, args.steps, args.warmup, timer)
     flops = 2.0 * n * K * K
+    # the vendor BLAS (torch.mm) on the same shape with one weight block and
+    # no grouping, for comparison (not part of the step)
+    torch.backends.cuda.matmul.allow_tf32 = False  # full float32, like the step
+    w0 = b[0].contiguous()
+    dst = torch.empty(n, K, device="cuda")
+    torch.mm(a, w0, out=dst)
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    t = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(args.steps):
+        torch.mm(a, w0, out=dst)
+    t.record()
+    torch.cuda.synchronize()
+    blas_ms = s.elapsed_time(t) / args.steps
     kern = {}
     for name in ("gather_mm", "segment_mm"):
         m = timer.avg_ms(name)
@@ -457,7 +487,9 @@ def workload_c5(args):
             "ms_per_step": round(ms, 4), "dtype": "f32",
             "config": {"workload": "RGCN relation transform: gather_mm + segment_mm",
                        "rows": n, "d1": K, "d2": K, "relations": R},
-            "kernels": kern}
+            "kernels": kern,
+            "vendor_blas_one_block": {"ms": round(blas_ms, 3),
+                                      "TFLOPs": round(flops / blas_ms / 1e9, 1)}}
 
 
 WORKLOADS = {"gat": workload_gat, "c1": workload_c1, "c3": workload_c3, "c4": workload_c4,
