@@ -17,7 +17,7 @@
  *
  * Conventions (as the reference, capi.mojo:1-17): the caller owns all
  * memory, nothing here allocates or frees, and launches are asynchronous on
- * `stream`. Unlike the reference every call returns a status: 0 on success,
+ * `stream`. Workspaces must be 256-byte aligned (hipMalloc's alignment). Unlike the reference every call returns a status: 0 on success,
  * a negative MDGL_E* code for an invalid argument (detected before anything
  * is launched; mdgl_last_error() names it), or a positive hipError_t from
  * the launch.
@@ -127,7 +127,8 @@ int mdgl_segment_reduce(const int32_t* offsets, const void* value, void* dst, in
 int mdgl_softmax_geometry(int64_t d, int dtype, const void* logits, const void* out,
                           int64_t* slots, int64_t* chunk_len);
 /* Workspace of a softmax call: partials of `num_chunks` chunks, plus a
- * (max, sum) table of `table_rows` rows for the two-pass edge_softmax. */
+ * (max, sum) table of `table_rows` rows for the two-pass edge_softmax:
+ * bounds[nbins + 1] + num_chunks with a row order, num_nodes without. */
 int64_t mdgl_softmax_workspace_bytes(int64_t num_chunks, int64_t table_rows, int64_t d,
                                      int dtype);
 
@@ -162,19 +163,21 @@ int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, v
  * row of bin k, the edge id eid[indptr[row] + s] of the row's slot s for
  * s < degree and -1 after it; it saves the packed rows the indptr and eid
  * lookups. Longer rows come as chunks, as in mdgl_segment_softmax. With
- * `row_of_edge` (device, num_edges entries: the
- * CSR row of every edge id, i.e. the destination -- or source -- node) the
- * output is written by a second, edge-parallel pass in edge-id order
- * (coalesced stores) from a per-row (max, sum) table in the workspace;
- * without it every row writes its own edges. `indices` and `scratch` are
- * accepted for signature compatibility and unused. */
+ * `slot_of_edge` (device, num_edges entries) the output is written by a
+ * second, edge-parallel pass in edge-id order (coalesced stores) from a
+ * (max, sum) table in the workspace: slot_of_edge[e] is the table slot of
+ * edge e's CSR row (its destination -- or source -- node), which is the row's
+ * position in `order`, bounds[nbins + 1] + the index of its first chunk for
+ * a chunked row, or, with `order` NULL, the row itself. Without it every row
+ * writes its own edges. `indices` and `scratch` are accepted for signature
+ * compatibility and unused. */
 int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
                        const int8_t* mask, const void* logits, void* dst, void* scratch,
                        int64_t num_nodes, int all_ones, int64_t d, const int32_t* order,
                        const int64_t* bounds, int nbins, const int32_t* packed_eid,
                        const int32_t* chunk_row, const int32_t* chunk_start,
                        const int32_t* chunk_first, int64_t num_chunks, int64_t slots,
-                       const int32_t* row_of_edge, int64_t num_edges, void* workspace,
+                       const int32_t* slot_of_edge, int64_t num_edges, void* workspace,
                        int64_t workspace_bytes, int dtype, void* stream);
 
 /* Replaces capi.mojo:141-145 (`mdgl_segment_mm`): out rows of segment r are

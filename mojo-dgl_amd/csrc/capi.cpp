@@ -42,6 +42,10 @@ bool aligned(const void* p, int64_t bytes) {
   return (reinterpret_cast<uintptr_t>(p) % (uintptr_t)bytes) == 0;
 }
 
+// Workspaces hold vector-accessed arrays at 256-byte offsets: the base must
+// be 256-byte aligned (hipMalloc and torch allocations are).
+constexpr int64_t WS_ALIGN = 256;
+
 // Builds the broadcast descriptor of two operands whose feature shapes are
 // padded to the same rank `nd`. For dot the last axis is contracted and
 // `red` receives its length. Returns 0 or a negative MDGL code.
@@ -173,6 +177,8 @@ int mdgl_build_csr(const int32_t* key, const int32_t* other, int64_t num_edges, 
   if (num_edges > 0 && !other != !indices)
     return fail(MDGL_EINVAL, "build_csr: `other` and `indices` come together or not at all");
   const int64_t need = csr_workspace_bytes(num_edges, num_rows);
+  if (need > 0 && workspace && !aligned(workspace, WS_ALIGN))
+    return fail(MDGL_EINVAL, "workspace must be %lld-byte aligned", (long long)WS_ALIGN);
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(MDGL_EWORKSPACE, "build_csr: workspace of %lld bytes needed, %lld given",
                 (long long)need, (long long)workspace_bytes);
@@ -421,6 +427,8 @@ int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* e
   p.heavy_ptr = heavy_ptr;
   if (num_chunks > 0) {
     const int64_t need = mdgl_gspmm_workspace_bytes(num_chunks, dout, reduce_op, dtype);
+    if (workspace && !aligned(workspace, WS_ALIGN))
+      return fail(MDGL_EINVAL, "workspace must be %lld-byte aligned", (long long)WS_ALIGN);
     if (!workspace || workspace_bytes < need)
       return fail(MDGL_EWORKSPACE, "gspmm: workspace of %lld bytes needed, %lld given",
                   (long long)need, (long long)workspace_bytes);
@@ -571,7 +579,12 @@ int softmax_common(const char* what, const int32_t* indptr, const int32_t* eid,
   if (num_chunks > 0 && (!chunk_row || !chunk_start || !chunk_first))
     return fail(MDGL_EINVAL, "%s: incomplete chunk list", what);
   if (row_of && num_edges < 0) return fail(MDGL_EINVAL, "%s: negative edge count", what);
-  const int64_t need = mdgl_softmax_workspace_bytes(num_chunks, row_of ? num_rows : 0, d, dtype);
+  // table slots of the two-pass form: the ordered rows then the chunked
+  // rows (one slot per chunk index), or one per row without an order
+  const int64_t table_rows = !row_of ? 0 : (order ? bounds[nbins + 1] + num_chunks : num_rows);
+  const int64_t need = mdgl_softmax_workspace_bytes(num_chunks, table_rows, d, dtype);
+  if (need > 0 && workspace && !aligned(workspace, WS_ALIGN))
+    return fail(MDGL_EINVAL, "workspace must be %lld-byte aligned", (long long)WS_ALIGN);
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(MDGL_EWORKSPACE, "%s: workspace of %lld bytes needed, %lld given", what,
                 (long long)need, (long long)workspace_bytes);
@@ -628,7 +641,7 @@ int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int3
                        const int64_t* bounds, int nbins, const int32_t* packed_eid,
                        const int32_t* chunk_row, const int32_t* chunk_start,
                        const int32_t* chunk_first, int64_t num_chunks, int64_t slots,
-                       const int32_t* row_of_edge, int64_t num_edges, void* workspace,
+                       const int32_t* slot_of_edge, int64_t num_edges, void* workspace,
                        int64_t workspace_bytes, int dtype, void* stream) {
   (void)indices;
   (void)scratch;
@@ -636,7 +649,7 @@ int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int3
   if (all_ones != 1 && !mask) return fail(MDGL_EINVAL, "edge_softmax: null mask");
   return softmax_common("edge_softmax", indptr, eid, all_ones == 1 ? nullptr : mask, logits, dst,
                         num_nodes, d, order, bounds, nbins, packed_eid, chunk_row, chunk_start,
-                        chunk_first, num_chunks, slots, row_of_edge, num_edges,
+                        chunk_first, num_chunks, slots, slot_of_edge, num_edges,
                         num_edges > 0 ? num_edges : 0, workspace, workspace_bytes, dtype, stream);
 }
 
@@ -663,6 +676,8 @@ int grouped_common(const void* a, const void* b, void* dst, const int64_t* idx_b
     return fail(MDGL_EINVAL, "%s: null buffer", what);
   const int64_t need = gather ? mdgl_gather_mm_workspace_bytes(n, d1, d2, r, dtype)
                               : mdgl_segment_mm_workspace_bytes(n, d1, d2, r, dtype);
+  if (workspace && !aligned(workspace, WS_ALIGN))
+    return fail(MDGL_EINVAL, "workspace must be %lld-byte aligned", (long long)WS_ALIGN);
   if (!workspace || workspace_bytes < need)
     return fail(MDGL_EWORKSPACE, "%s: workspace of %lld bytes needed, %lld given", what,
                 (long long)need, (long long)workspace_bytes);

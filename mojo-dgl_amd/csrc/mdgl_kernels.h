@@ -100,7 +100,8 @@ struct SoftmaxParams {
   const int32_t* chunk_start;
   const int32_t* chunk_first;
   void* part;
-  // two-pass form: the row of every edge id and a [num_rows][2][d] table
+  // two-pass form: the table slot of every edge id's row and a
+  // [slots][2][d] table
   const int32_t* row_of;
   int64_t num_edges;
   void* table;

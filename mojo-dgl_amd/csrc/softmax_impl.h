@@ -29,12 +29,15 @@
 // own, whose kernel needs far fewer registers, each wavefront serving
 // PK_U packed wavefronts' rows with its dependent loads interleaved.
 //
-// Two-pass form (edge_softmax with a row-of-edge array): a random 32-byte
+// Two-pass form (edge_softmax with a slot-of-edge array): a random 32-byte
 // write per edge costs more than the rest of the op, so the row pass then
-// only writes each row's (max, sum) to a node table tab[row][2][d], and an
+// only writes each row's (max, sum) to a table tab[slot][2][d], and an
 // edge-parallel pass in edge-id order writes out[e] = exp(x - max) / sum with
-// coalesced loads and stores, reading the table row of the edge's row. The
-// values are the ones the one-pass form writes.
+// coalesced loads and stores, reading the table row of the edge's slot. With
+// a row order a row's slot is its position in the order (chunked rows follow,
+// at hub_base + their first chunk), so the rows of a wavefront write
+// consecutive table rows; without one the slot is the row. The values are the
+// ones the one-pass form writes.
 #pragma once
 
 #include "mdgl_kernels.h"
@@ -68,7 +71,8 @@ struct SoftmaxArgs {
   T* ps;  // [num_chunks][d] chunk sums of exp(x - max)
   int64_t chunk_waves, chunk_blocks, light_waves, light_blocks;
   int mode2;  // launch 2: the chunk write pass
-  T* tab;     // two-pass form: [num_rows][2][d] (max, sum), else null
+  T* tab;     // two-pass form: [slots][2][d] (max, sum), else null
+  int64_t hub_base;  // table slot of the first chunked row (ordered plans)
 };
 
 __device__ __forceinline__ float exp_t(float x) { return expf(x); }
@@ -102,7 +106,7 @@ __device__ __forceinline__ void store_cols(T* __restrict__ p, int64_t k0, int64_
 // butterflies below always run on a full wavefront.
 template <class T, int VEC, int NQ>
 __device__ __forceinline__ void soft_group(const SoftmaxArgs<T>& a, int mode, bool row_ok,
-                                           int64_t row_id, int start, int stop, int Pr,
+                                           int64_t slot, int start, int stop, int Pr,
                                            int64_t slab, int lane, int64_t chunk) {
   const int L = a.L;
   const int s = (lane / L) % Pr, c = lane % L;
@@ -227,13 +231,11 @@ __device__ __forceinline__ void soft_group(const SoftmaxArgs<T>& a, int mode, bo
     const bool writer = mode == SM_WRITE ? (s == 0 && a.chunk_first[chunk] == chunk)
                                          : (row_ok && s == 0);
     if (writer) {
-      T* t = a.tab + row_id * 2 * a.d;
-#pragma unroll
-      for (int v = 0; v < VEC; ++v)
-        if (k0 + v < a.d) {
-          t[k0 + v] = m[v];
-          t[a.d + k0 + v] = sum[v];
-        }
+      // 16-byte stores when the columns allow (the table is 256-byte aligned
+      // and a table row is 2d values)
+      T* t = a.tab + slot * 2 * a.d;
+      store_cols<T, VEC>(t, k0, a.d, vec_io, m);
+      store_cols<T, VEC>(t + a.d, k0, a.d, vec_io, sum);
     }
     return;
   }
@@ -280,7 +282,9 @@ __global__ __launch_bounds__(BLOCK) void softmax_kernel(SoftmaxArgs<T> a) {
     const int start = a.chunk_start[chunk];
     const int end = a.indptr[row + 1];
     const int stop = end - start > a.chunk_len ? start + a.chunk_len : end;
-    soft_group<T, VEC, SOFT_CPL>(a, a.mode2 ? SM_WRITE : SM_STATS, true, row, start, stop, Pw,
+    // table slot of a chunked row: after the ordered rows, at its first chunk
+    const int64_t slot = a.order ? a.hub_base + chunk : row;
+    soft_group<T, VEC, SOFT_CPL>(a, a.mode2 ? SM_WRITE : SM_STATS, true, slot, start, stop, Pw,
                                  slab, lane, chunk);
     return;
   }
@@ -316,7 +320,8 @@ __global__ __launch_bounds__(BLOCK) void softmax_kernel(SoftmaxArgs<T> a) {
         stop = a.indptr[row + 1];
       }
       const bool ok = in && stop > start && stop - start <= a.chunk_len;
-      soft_group<T, VEC, SOFT_CPL>(a, SM_FULL, ok, row, start, stop, Pr, slab, lane, 0);
+      soft_group<T, VEC, SOFT_CPL>(a, SM_FULL, ok, a.order ? i : row, start, stop, Pr, slab,
+                                   lane, 0);
     }
     return;
   }
@@ -342,7 +347,7 @@ __device__ __forceinline__ void softmax_packed_u(const SoftmaxArgs<T>& a, int64_
   const int64_t b0 = a.bin_start[k], b1 = a.bin_start[k + 1];
   // indices are clamped into the bin (and rows have >= 1 edge), so every
   // load below is unconditional and in bounds; rok / ok mask the results
-  int64_t slab[PK_U], row[PK_U], ic[PK_U];
+  int64_t slab[PK_U], ic[PK_U];
   bool rok[PK_U];
 #pragma unroll
   for (int r = 0; r < PK_U; ++r) {
@@ -363,15 +368,14 @@ __device__ __forceinline__ void softmax_packed_u(const SoftmaxArgs<T>& a, int64_
       const int32_t pe = a.peid[a.bin_slot[k] + (ic[r] - b0) * Pr + sl];
       ok[r] = rok[r] && pe >= 0;
       e[r] = pe >= 0 ? (int64_t)pe : 0;
-      row[r] = a.tab ? (int64_t)a.order[ic[r]] : 0;
     }
   } else {
     int start[PK_U], stop[PK_U];
 #pragma unroll
     for (int r = 0; r < PK_U; ++r) {
-      row[r] = a.order[ic[r]];
-      start[r] = a.indptr[row[r]];
-      stop[r] = a.indptr[row[r] + 1];
+      const int64_t row = a.order[ic[r]];
+      start[r] = a.indptr[row];
+      stop[r] = a.indptr[row + 1];
     }
 #pragma unroll
     for (int r = 0; r < PK_U; ++r) {
@@ -416,13 +420,11 @@ __device__ __forceinline__ void softmax_packed_u(const SoftmaxArgs<T>& a, int64_
     if (!feat_ok) continue;
     if (a.tab) {
       if (rok[r] && sl == 0) {
-        T* t = a.tab + row[r] * 2 * a.d;
-#pragma unroll
-        for (int v = 0; v < VEC; ++v)
-          if (k0 + v < a.d) {
-            t[k0 + v] = m[v];
-            t[a.d + k0 + v] = sum[v];
-          }
+        // slot = position in the row order: a wavefront's rows write
+        // consecutive table rows (whole lines)
+        T* t = a.tab + ic[r] * 2 * a.d;
+        store_cols<T, VEC>(t, k0, a.d, a.vec_io, m);
+        store_cols<T, VEC>(t + a.d, k0, a.d, a.vec_io, sum);
       }
     } else if (ok[r]) {
       T y[VEC];
@@ -439,7 +441,7 @@ template <class T, int VEC>
 __global__ __launch_bounds__(BLOCK) void softmax_edge_kernel(const T* __restrict__ logits,
                                                              T* __restrict__ out,
                                                              const T* __restrict__ tab,
-                                                             const int32_t* __restrict__ row_of,
+                                                             const int32_t* __restrict__ slot_of,
                                                              const int8_t* __restrict__ mask,
                                                              int64_t num_edges, int64_t d, int L,
                                                              int S, int vec_io, int64_t nblocks) {
@@ -451,7 +453,7 @@ __global__ __launch_bounds__(BLOCK) void softmax_edge_kernel(const T* __restrict
   const int64_t k0 = (slab * L + lane % L) * VEC;
   if (e >= num_edges || k0 >= d) return;
   if (mask && mask[e] != 1) return;
-  const int64_t r = row_of[e];
+  const int64_t r = slot_of[e];
   T x[VEC], m[VEC], s[VEC];
   if (VEC > 1 && vec_io) {
     if constexpr (VEC > 1) load_n_stream<T, VEC>(logits + e * d + k0, x);
@@ -536,6 +538,7 @@ hipError_t launch_softmax_vec(const SoftmaxParams& p) {
   a.chunk_blocks = (a.chunk_waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
   a.mode2 = 0;
   a.tab = static_cast<T*>(p.table);
+  a.hub_base = p.order ? p.bounds[p.nbins + 1] : 0;
   // chunks and wavefront rows, then the packed rows in a launch of their own
   const int64_t blocks = a.chunk_blocks + a.light_blocks;
   if (blocks > 0) {

@@ -247,7 +247,8 @@ def on_device(f: Feat, dtype) -> torch.Tensor:
     tdt = torch_dtype(dtype)
     if f.is_torch:
         t = f.data
-        if t.is_cuda and t.dtype == tdt and t.is_contiguous():
+        if t.is_cuda and t.dtype == tdt and t.is_contiguous() \
+                and t.get_device() == torch.cuda.current_device():
             return t
     else:
         t = torch.from_numpy(f.data)

@@ -35,9 +35,47 @@ def _packed_bin(rows, indptr, k, eid, xp):
     return xp.where(valid, val, -1).reshape(-1)
 
 
+def _edge_slots(ordered_rows, chunk_row, chunk_first, indptr, eid):
+    """Table slot of every edge's row for the two-pass edge_softmax: a row's
+    position in the row order, or len(order) + the index of its first chunk
+    for a chunked row. Indexed by edge id (by CSR slot when `eid` is None).
+    numpy arrays give a numpy result, GPU tensors a GPU tensor (int32)."""
+    nord = ordered_rows.shape[0]
+    n_rows = indptr.shape[0] - 1
+    if isinstance(indptr, np.ndarray):
+        slot_of_row = np.full(n_rows, -1, dtype=np.int64)
+        slot_of_row[ordered_rows] = np.arange(nord)
+        if chunk_row is not None and chunk_row.shape[0]:
+            heads = np.nonzero(chunk_first == np.arange(chunk_row.shape[0]))[0]
+            slot_of_row[chunk_row[heads]] = nord + heads
+        per_slot = slot_of_row[np.repeat(np.arange(n_rows), np.diff(indptr))]
+        if eid is None:
+            return per_slot.astype(np.int32)
+        out = np.empty(per_slot.shape[0], dtype=np.int32)
+        out[np.asarray(eid, dtype=np.int64)] = per_slot
+        return out
+    dev = indptr.device
+    ip = indptr.to(torch.int64)
+    slot_of_row = torch.full((n_rows,), -1, dtype=torch.int64, device=dev)
+    slot_of_row[ordered_rows.to(torch.int64)] = torch.arange(nord, device=dev)
+    if chunk_row is not None and chunk_row.shape[0]:
+        heads = torch.nonzero(chunk_first.to(torch.int64)
+                              == torch.arange(chunk_row.shape[0], device=dev)).squeeze(1)
+        slot_of_row[chunk_row[heads].to(torch.int64)] = nord + heads
+    n_slots = int(eid.shape[0]) if eid is not None else int(ip[-1].item())
+    rows = torch.repeat_interleave(torch.arange(n_rows, device=dev), ip[1:] - ip[:-1],
+                                   output_size=n_slots)
+    per_slot = slot_of_row[rows].to(torch.int32)
+    if eid is None:
+        return per_slot
+    out = torch.empty(n_slots, dtype=torch.int32, device=dev)
+    out[eid.to(torch.int64)] = per_slot
+    return out
+
+
 class SoftmaxPlan:
-    """Plan arrays on the GPU (order / packed edge ids / chunks) and the host
-    bin bounds."""
+    """Plan arrays on the GPU (order / packed edge ids / chunks / table slot
+    of every edge) and the host bin bounds."""
 
     def __init__(self, indptr: np.ndarray, slots: int, chunk_len: int, ordered: bool,
                  eid: np.ndarray | None = None):
@@ -63,6 +101,8 @@ class SoftmaxPlan:
         self.order = None
         self.bounds = None
         self.packed = None
+        self.slot_of_edge = None
+        self.table_rows = int(deg.shape[0])
         if ordered:
             rows = np.nonzero((deg > 0) & (deg <= chunk_len))[0]
             d = deg[rows]
@@ -80,6 +120,9 @@ class SoftmaxPlan:
                      for k in range(self.nbins) if self.bounds[k + 1] > self.bounds[k]]
             if parts:
                 self.packed = _lib.i32_device(np.concatenate(parts))
+            self.table_rows = int(ordered_rows.size) + self.num_chunks
+            self.slot_of_edge = _lib.i32_device(_edge_slots(
+                ordered_rows, row if self.num_chunks else None, cfirst, ip, eid))
 
     @classmethod
     def from_device(cls, indptr: torch.Tensor, slots: int, chunk_len: int, ordered: bool,
@@ -117,6 +160,8 @@ class SoftmaxPlan:
         self.order = None
         self.bounds = None
         self.packed = None
+        self.slot_of_edge = None
+        self.table_rows = int(deg.shape[0])
         if ordered:
             nb = self.nbins
             # bin k (ceil(log2(degree))) for degree <= slots, bin nb for the
@@ -134,6 +179,10 @@ class SoftmaxPlan:
                      for k in range(nb) if b[k + 1] > b[k]]
             if parts:
                 self.packed = torch.cat(parts).to(torch.int32)
+            nord = int(b[nb + 1])
+            self.table_rows = nord + self.num_chunks
+            self.slot_of_edge = _edge_slots(order[:nord], self.chunk_row, self.chunk_first, ip,
+                                            eid)
         return self
 
     def bounds_ptr(self):

@@ -120,24 +120,23 @@ def _edge_softmax(graph, logits, eids, norm_by):
             csr = graph._device_csr("in" if norm_by == "dst" else "out")
             indptr, eid, rows = csr.indptr, csr.eid, num_nodes
             plan = csr.softmax_plan(slots, chunk_len)
-            # the row of an edge is its destination (source) node: the second,
-            # edge-parallel pass writes the output in edge-id order
-            uids, vids = graph._device_coo()
-            row_of = vids if norm_by == "dst" else uids
         else:
             # positions grouped by (endpoint, appearance): the stable grouping
             # of the selected edges' endpoints, on the GPU; rows are all nodes
             # (the ones no selected edge reaches are empty and skipped)
             uids, vids = graph._device_coo()
             idx = order if isinstance(order, torch.Tensor) else torch.from_numpy(order).to(gdev)
-            row_of = (vids if norm_by == "dst" else uids)[idx]
-            indptr, _, eid = heterograph.build_device_csr(row_of, None, num_nodes)
+            endpoint = (vids if norm_by == "dst" else uids)[idx]
+            indptr, _, eid = heterograph.build_device_csr(endpoint, None, num_nodes)
             rows = num_nodes if idx.shape[0] else 0
             plan = _plan.SoftmaxPlan.from_device(indptr, slots, chunk_len, ordered=True,
                                                  eid=eid)
         if rows:
             n_edges = lg.shape[0]
-            ws, nbytes = _plan.workspace(plan, d, dtype, rows if row_of is not None else 0)
+            # the second, edge-parallel pass writes the output in edge-id
+            # order from the (max, sum) table slot of each edge's row
+            row_of = plan.slot_of_edge
+            ws, nbytes = _plan.workspace(plan, d, dtype, plan.table_rows)
             rc = _lib.lib().mdgl_edge_softmax_(
                 indptr.data_ptr(), None, eid.data_ptr(), None, lg.data_ptr(), out.data_ptr(), None,
                 rows, 1, d, _lib.ptr(plan.order), plan.bounds_ptr(), plan.nbins,

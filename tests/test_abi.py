@@ -71,10 +71,13 @@ def test_invalid_arguments_are_rejected_without_launching(lib):
                         ls.ctypes.data, rs.ctypes.data, None, None, None, None, 0, 0, None, None,
                         0, None, 0, 0, 0, None)
     assert rc == -1 and "broadcastable" in err(lib)
-    # a chunk schedule without its workspace
+    # a chunk schedule without its workspace, or with a misaligned one
     rc = lib.mdgl_gspmm(1, 1, 1, 1, 1, 1, 10, 2, 4, 4, 4, 0, None, 0, None, None, None, None, 1,
                         1, 3, 8, 1, 1, 1, None, 0, 0, 0, None)
     assert rc == -2 and "workspace" in err(lib)
+    rc = lib.mdgl_gspmm(1, 1, 1, 1, 1, 1, 10, 2, 4, 4, 4, 0, None, 0, None, None, None, None, 1,
+                        1, 3, 8, 1, 1, 1, 4096 + 8, 1 << 20, 0, 0, None)
+    assert rc == -1 and "aligned" in err(lib)
     # too many b blocks for the GPU bucketing
     rc = lib.mdgl_gather_mm(1, 1, 1, 1, 100, 4, 4, 100000, 1, 1 << 40, 0, None)
     assert rc == -3
@@ -97,6 +100,9 @@ def test_build_csr_arguments(lib):
     assert rc == -1 and "null" in err(lib)
     rc = lib.mdgl_build_csr(8, 8, 5, 300, 8, 8, 8, None, 0, None)
     assert rc == -2 and "workspace" in err(lib)
+    # workspaces must be 256-byte aligned (their arrays are read 16 bytes at a time)
+    rc = lib.mdgl_build_csr(8, 8, 5, 300, 8, 8, 8, 4096 + 16, 1 << 20, None)
+    assert rc == -1 and "aligned" in err(lib)
     # one row or no edges: no workspace and no sort
     assert lib.mdgl_build_csr_workspace_bytes(1000, 1) == 0
     assert lib.mdgl_build_csr_workspace_bytes(0, 1000) == 0

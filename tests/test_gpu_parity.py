@@ -306,6 +306,9 @@ def test_softmax_plan_built_on_the_gpu_equals_the_host_plan(slots, chunk_len):
             torch.from_numpy(indptr).cuda(), slots, chunk_len, ordered=True,
             eid=None if ids is None else torch.from_numpy(ids).cuda())
         np.testing.assert_array_equal(dev.packed.cpu().numpy(), host.packed.cpu().numpy())
+        np.testing.assert_array_equal(dev.slot_of_edge.cpu().numpy(),
+                                      host.slot_of_edge.cpu().numpy())
+        assert dev.table_rows == host.table_rows
     assert dev.num_chunks == host.num_chunks and dev.nbins == host.nbins
     np.testing.assert_array_equal(dev.bounds, host.bounds)
     n = int(host.bounds[-1])
@@ -773,15 +776,15 @@ def test_edge_softmax_power_law_and_mask_through_the_abi():
                                                           dtype=np.float64).ctypes.data,
                                      want.ctypes.data, n, 0, 8, 1)
     sel = mask == 1
-    _, vids = g._device_coo()
-    assert plan.packed is not None
+    assert plan.packed is not None and plan.slot_of_edge is not None
     first = None
     # one-pass and two-pass forms, each with the packed slot list and with
     # the indptr chain: all four write the same values
-    for row_of in (None, vids):
+    for row_of in (None, plan.slot_of_edge):
         for packed in (plan.packed, None):
             out.fill_(-7.0)
-            ws, nbytes = _plan.workspace(plan, 8, np.float32, n if row_of is not None else 0)
+            ws, nbytes = _plan.workspace(plan, 8, np.float32,
+                                         plan.table_rows if row_of is not None else 0)
             rc = _lib.lib().mdgl_edge_softmax_(
                 csr.indptr.data_ptr(), None, csr.eid.data_ptr(), m.data_ptr(), lg.data_ptr(),
                 out.data_ptr(), None, n, 0, 8, _lib.ptr(plan.order), plan.bounds_ptr(),

@@ -210,3 +210,38 @@ def test_packed_softmax_slots_list_each_rows_edges():
     got = _packed_bin(torch_rows, torch.from_numpy(indptr), 3, torch.from_numpy(eid), torch)
     np.testing.assert_array_equal(got.numpy(), _packed_bin(np.array([3, 1, 4]), indptr, 3, eid,
                                                            np))
+
+
+def test_softmax_table_slots_of_edges():
+    """Two-pass edge_softmax table slots: an ordered row's slot is its
+    position in the row order, a chunked row's is len(order) + its first
+    chunk; every edge gets its row's slot (brute force over the CSR)."""
+    from mojodgl.ops._plan import _edge_slots
+
+    rng = np.random.default_rng(5)
+    deg = rng.integers(0, 7, 40)
+    deg[[3, 17]] = [25, 11]  # chunked at chunk_len 8
+    indptr = np.concatenate([[0], np.cumsum(deg)]).astype(np.int64)
+    E = int(indptr[-1])
+    eid = rng.permutation(E)
+    ordered = rng.permutation(np.nonzero((deg > 0) & (deg <= 8))[0])
+    heavy = np.nonzero(deg > 8)[0]
+    per = (deg[heavy] + 7) // 8
+    chunk_row = np.repeat(heavy, per)
+    firsts = np.concatenate([[0], np.cumsum(per)[:-1]])
+    chunk_first = np.repeat(firsts, per)
+    for ids in (None, eid):
+        got = _edge_slots(ordered, chunk_row, chunk_first, indptr, ids)
+        want = np.full(E, -1)
+        for r in range(deg.size):
+            if deg[r] == 0:
+                continue
+            slot = (int(np.nonzero(ordered == r)[0][0]) if r in ordered
+                    else ordered.size + int(firsts[list(heavy).index(r)]))
+            for j in range(indptr[r], indptr[r + 1]):
+                want[j if ids is None else ids[j]] = slot
+        np.testing.assert_array_equal(got, want)
+    t = _edge_slots(torch.from_numpy(ordered), torch.from_numpy(chunk_row),
+                    torch.from_numpy(chunk_first), torch.from_numpy(indptr), torch.from_numpy(eid))
+    np.testing.assert_array_equal(t.numpy(), _edge_slots(ordered, chunk_row, chunk_first,
+                                                         indptr, eid))
