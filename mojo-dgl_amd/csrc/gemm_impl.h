@@ -260,7 +260,9 @@ __device__ __forceinline__ void quad_transpose(float (&x)[4], int s) {
 
 template <class T, int NCH>
 __global__ __launch_bounds__(RB_THREADS) void grouped_gemm_resident_kernel(GemmArgs<T> p,
-                                                                           int64_t tiles_per_wg) {
+                                                                           int64_t tiles_per_wg,
+                                                                           const int32_t* __restrict__ tile_ptr,
+                                                                           const int32_t* __restrict__ group_off) {
   using M = Mfma<T>;
   using acc_t = typename M::acc_t;
   // a ring of DEPTH chunks (NCH a multiple of DEPTH, so the next tile's
@@ -271,25 +273,35 @@ __global__ __launch_bounds__(RB_THREADS) void grouped_gemm_resident_kernel(GemmA
   const int t = threadIdx.x;
   const int lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1;
   const int li = lane & 15, h = lane >> 4;
-  const int64_t total = p.tile_ptr[p.R];
+  const int64_t total = tile_ptr[p.R];
   const int64_t first = (int64_t)blockIdx.x * tiles_per_wg;
   const int64_t last = first + tiles_per_wg < total ? first + tiles_per_wg : total;
   if (first >= last) return;  // uniform per workgroup
   const int64_t n0 = (int64_t)blockIdx.y * GBN;
 
+  // Group metadata is read with scalar loads (uniform index, read-only
+  // arguments): a vector load here would be waited for with the vector
+  // memory counter, i.e. behind every a load and output store in flight.
+  auto uget = [](const int32_t* __restrict__ arr, int64_t i) -> int64_t {
+    return arr[__builtin_amdgcn_readfirstlane((int)i)];
+  };
   // rows of a tile for this lane: rid[i] = row of tile row wm*64 + 16i + li
   // (-1 past the group); base[i] = where its a fragments start (row 0 for
   // -1: read, never stored)
-  auto setup = [&](int64_t tl, int64_t gg, int64_t& m0, int64_t& m_end, int32_t (&rid)[4],
-                   const T* (&base)[4]) {
-    m0 = p.group_off[gg] + (tl - p.tile_ptr[gg]) * RB_TM;
-    m_end = p.group_off[gg + 1];
+  auto setup_rows = [&](int64_t tl, int64_t gg, int64_t& m0, int64_t& m_end,
+                        int32_t (&rid)[4]) {
+    m0 = uget(group_off, gg) + (tl - uget(tile_ptr, gg)) * RB_TM;
+    m_end = uget(group_off, gg + 1);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t pos = m0 + wm * 64 + i * 16 + li;
       rid[i] = pos < m_end ? (p.perm ? p.perm[pos] : (int32_t)pos) : -1;
-      base[i] = p.a + (int64_t)(rid[i] >= 0 ? rid[i] : 0) * p.K + 4 * h;
     }
+  };
+  auto bases = [&](const int32_t (&rid)[4], const T* (&base)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      base[i] = p.a + (int64_t)(rid[i] >= 0 ? rid[i] : 0) * p.K + 4 * h;
   };
 
   int64_t tile = first;
@@ -299,14 +311,15 @@ __global__ __launch_bounds__(RB_THREADS) void grouped_gemm_resident_kernel(GemmA
     int64_t lo = 0, hi = p.R - 1;
     while (lo < hi) {
       const int64_t mid = (lo + hi + 1) / 2;
-      if (p.tile_ptr[mid] <= tile) lo = mid; else hi = mid - 1;
+      if (uget(tile_ptr, mid) <= tile) lo = mid; else hi = mid - 1;
     }
     g = lo;
   }
   int64_t m0, m_end;
   int32_t rid[4];
   const T* base[4];
-  setup(tile, g, m0, m_end, rid, base);
+  setup_rows(tile, g, m0, m_end, rid);
+  bases(rid, base);
   // lane (li, h) holds a[row i][16c + 4h .. +3] of chunk c in ring slot c % DEPTH
   T af[DEPTH][4][4];
 #pragma unroll
@@ -315,7 +328,12 @@ __global__ __launch_bounds__(RB_THREADS) void grouped_gemm_resident_kernel(GemmA
     for (int i = 0; i < 4; ++i) load_global_n<T, 4>(base[i] + c * 16, af[c][i]);
 
   int64_t cur_g = -1;
-  while (true) {
+  // One tile: its b block (when the group changes), the K loop with the
+  // next tile's first loads, the output. The first tile is peeled off the
+  // loop below, so every loop iteration starts in the same state (the next
+  // tile's first a loads, then the last tile's stores, outstanding) and its
+  // first wait counts past the stores instead of waiting for them.
+  auto run_tile = [&]() -> bool {
     if (g != cur_g) {
       __syncthreads();  // every wavefront is done with the previous block
       const T* bt_g = p.bt + g * p.N * p.Kp;
@@ -329,15 +347,16 @@ __global__ __launch_bounds__(RB_THREADS) void grouped_gemm_resident_kernel(GemmA
       __syncthreads();
       cur_g = g;
     }
-    // the next tile's rows are looked up now; its first chunks are requested
-    // while this tile's last chunks multiply
+    // the next tile's rows are looked up now (their addresses are formed
+    // only where its first chunks are requested, while this tile's last
+    // chunks multiply, so the row loads are not waited for before)
     const bool has_next = tile + 1 < last;
     int64_t g_n = g, m0_n = 0, m_end_n = 0;
     int32_t rid_n[4] = {-1, -1, -1, -1};
     const T* base_n[4] = {base[0], base[1], base[2], base[3]};
     if (has_next) {
-      while (p.tile_ptr[g_n + 1] <= tile + 1) ++g_n;
-      setup(tile + 1, g_n, m0_n, m_end_n, rid_n, base_n);
+      while (uget(tile_ptr, g_n + 1) <= tile + 1) ++g_n;
+      setup_rows(tile + 1, g_n, m0_n, m_end_n, rid_n);
     }
     acc_t acc[4][4];
 #pragma unroll
@@ -364,6 +383,7 @@ __global__ __launch_bounds__(RB_THREADS) void grouped_gemm_resident_kernel(GemmA
         for (int i = 0; i < 4; ++i)
           load_global_n<T, 4>(base[i] + (c + DEPTH) * 16, af[c % DEPTH][i]);
       } else if (has_next) {
+        if (c + DEPTH == NCH) bases(rid_n, base_n);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           load_global_n<T, 4>(base_n[i] + (c + DEPTH - NCH) * 16, af[c % DEPTH][i]);
@@ -392,7 +412,7 @@ __global__ __launch_bounds__(RB_THREADS) void grouped_gemm_resident_kernel(GemmA
         }
       }
     }
-    if (!has_next) break;
+    if (!has_next) return false;
     ++tile;
     g = g_n;
     m0 = m0_n;
@@ -402,7 +422,11 @@ __global__ __launch_bounds__(RB_THREADS) void grouped_gemm_resident_kernel(GemmA
       rid[i] = rid_n[i];
       base[i] = base_n[i];
     }
-  }
+    return true;
+  };
+  if (run_tile())
+    while (run_tile()) {
+    }
 }
 
 // ---------------------------------------------------------------- grouping
@@ -645,10 +669,14 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather) {
       const int64_t per = (mt + wgs - 1) / wgs;
       const dim3 grid((unsigned)wgs, (unsigned)nt), block(RB_THREADS);
       switch (Kp / 16) {
-        case 2: hipLaunchKernelGGL((grouped_gemm_resident_kernel<T, 2>), grid, block, 0, L.stream, a, per); break;
-        case 4: hipLaunchKernelGGL((grouped_gemm_resident_kernel<T, 4>), grid, block, 0, L.stream, a, per); break;
-        case 6: hipLaunchKernelGGL((grouped_gemm_resident_kernel<T, 6>), grid, block, 0, L.stream, a, per); break;
-        default: hipLaunchKernelGGL((grouped_gemm_resident_kernel<T, 8>), grid, block, 0, L.stream, a, per); break;
+        case 2: hipLaunchKernelGGL((grouped_gemm_resident_kernel<T, 2>), grid, block, 0, L.stream, a, per,
+                             a.tile_ptr, a.group_off); break;
+        case 4: hipLaunchKernelGGL((grouped_gemm_resident_kernel<T, 4>), grid, block, 0, L.stream, a, per,
+                             a.tile_ptr, a.group_off); break;
+        case 6: hipLaunchKernelGGL((grouped_gemm_resident_kernel<T, 6>), grid, block, 0, L.stream, a, per,
+                             a.tile_ptr, a.group_off); break;
+        default: hipLaunchKernelGGL((grouped_gemm_resident_kernel<T, 8>), grid, block, 0, L.stream, a, per,
+                             a.tile_ptr, a.group_off); break;
       }
       return hipGetLastError();
     }
