@@ -59,6 +59,17 @@ int64_t mdgl_workers(void);
 /* Replaces capi.mojo:54-56. Inclusive int64 prefix sum, dst[i] = src[0..i]. */
 int mdgl_cumsum(const int64_t* src, int64_t* dst, int64_t n, void* stream);
 
+/* Segment offsets where the lengths live (the reference forms them on the
+ * host: [0] + cumsum(seglen) and its checks, python/mojodgl/ops/segment.py:19-38;
+ * no counterpart at its ABI): offsets[0] = 0, offsets[i + 1] = seglen[0] +
+ * ... + seglen[i] (int32, valid when the total is below 2**31), and stats
+ * (device, 3 int64) = (min length or 0 without segments, total, number of
+ * chunk_len-row chunks of the segments longer than chunk_len, 0 when
+ * chunk_len <= 0). Workspace: mdgl_segment_offsets_workspace_bytes(num). */
+int mdgl_segment_offsets(const int64_t* seglen, int64_t num, int64_t chunk_len, int32_t* offsets,
+                         int64_t* stats, void* workspace, int64_t workspace_bytes, void* stream);
+int64_t mdgl_segment_offsets_workspace_bytes(int64_t num);
+
 /* Replaces capi.mojo:59-61. dst[i] = 0 where src[i] is +-inf, else src[i]. */
 int mdgl_replace_inf_with_zero(const void* src, void* dst, int64_t n, int dtype, void* stream);
 

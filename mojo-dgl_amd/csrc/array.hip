@@ -1,5 +1,6 @@
 // Elementwise and scan helpers: replace_inf_with_zero (src/ported.mojo:157-177),
-// clamp on int64 (:181-190) and the inclusive int64 prefix sum (:145-151).
+// clamp on int64 (:181-190), the inclusive int64 prefix sum (:145-151), and
+// segment offsets with their validation figures (python/mojodgl/ops/segment.py:19-38).
 #include "mdgl_kernels.h"
 
 namespace mdgl {
@@ -63,6 +64,159 @@ __global__ __launch_bounds__(BLOCK) void gather_rows_kernel(const T* __restrict_
     const int64_t i = t / width, k = t % width;
     dst[t] = src[(int64_t)idx[i] * width + k];
   }
+}
+
+// Segment offsets from lengths (three launches: tile partials, a scan of
+// the tile totals, the tile rewrite). A tile is SEG_TILE lengths, 16
+// consecutive ones per thread. Integer sums are exact, so the offsets equal
+// the sequential [0] + cumsum.
+constexpr int SEG_THREADS = 256;
+constexpr int SEG_PER = 16;
+constexpr int SEG_TILE = SEG_THREADS * SEG_PER;
+
+__device__ __forceinline__ int64_t seg_chunks(int64_t len, int64_t chunk_len) {
+  return (chunk_len > 0 && len > chunk_len) ? (len + chunk_len - 1) / chunk_len : 0;
+}
+
+__global__ __launch_bounds__(SEG_THREADS) void seg_partials_kernel(
+    const int64_t* __restrict__ len, int64_t num, int64_t chunk_len, int64_t* __restrict__ tsum,
+    int64_t* __restrict__ tmin, int64_t* __restrict__ theavy) {
+  __shared__ int64_t ssum[SEG_THREADS], smin[SEG_THREADS], sheavy[SEG_THREADS];
+  const int t = threadIdx.x;
+  const int64_t lo = (int64_t)blockIdx.x * SEG_TILE + (int64_t)t * SEG_PER;
+  int64_t s = 0, m = INT64_MAX, h = 0;
+  for (int k = 0; k < SEG_PER; ++k) {
+    const int64_t i = lo + k;
+    if (i < num) {
+      const int64_t v = len[i];
+      s += v;
+      m = v < m ? v : m;
+      h += seg_chunks(v, chunk_len);
+    }
+  }
+  ssum[t] = s;
+  smin[t] = m;
+  sheavy[t] = h;
+  __syncthreads();
+  for (int off = SEG_THREADS / 2; off > 0; off >>= 1) {
+    if (t < off) {
+      ssum[t] += ssum[t + off];
+      smin[t] = smin[t + off] < smin[t] ? smin[t + off] : smin[t];
+      sheavy[t] += sheavy[t + off];
+    }
+    __syncthreads();
+  }
+  if (t == 0) {
+    tsum[blockIdx.x] = ssum[0];
+    tmin[blockIdx.x] = smin[0];
+    theavy[blockIdx.x] = sheavy[0];
+  }
+}
+
+// One workgroup: tsum becomes the exclusive scan of the tile totals;
+// stats = (min length, total, chunks of the long segments); offsets[0] = 0.
+// With no tiles (no segments) the pointers to the tile arrays are unused.
+__global__ __launch_bounds__(1024) void seg_tiles_kernel(int64_t* __restrict__ tsum,
+                                                         const int64_t* __restrict__ tmin,
+                                                         const int64_t* __restrict__ theavy,
+                                                         int64_t tiles, int64_t* __restrict__ stats,
+                                                         int32_t* __restrict__ offsets) {
+  __shared__ int64_t ssum[1024], smin[1024], sheavy[1024];
+  const int t = threadIdx.x;
+  const int64_t span = (tiles + 1023) / 1024;
+  const int64_t lo = t * span < tiles ? t * span : tiles;
+  const int64_t hi = lo + span < tiles ? lo + span : tiles;
+  int64_t s = 0, m = INT64_MAX, h = 0;
+  for (int64_t i = lo; i < hi; ++i) {
+    s += tsum[i];
+    m = tmin[i] < m ? tmin[i] : m;
+    h += theavy[i];
+  }
+  ssum[t] = s;
+  smin[t] = m;
+  sheavy[t] = h;
+  __syncthreads();
+  // inclusive scan of the span sums; min and heavy reduced alongside
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int64_t add = t >= off ? ssum[t - off] : 0;
+    const int64_t om = t >= off ? smin[t - off] : INT64_MAX;
+    const int64_t oh = t >= off ? sheavy[t - off] : 0;
+    __syncthreads();
+    ssum[t] += add;
+    smin[t] = om < smin[t] ? om : smin[t];
+    sheavy[t] += oh;
+    __syncthreads();
+  }
+  int64_t acc = t > 0 ? ssum[t - 1] : 0;
+  for (int64_t i = lo; i < hi; ++i) {
+    const int64_t v = tsum[i];
+    tsum[i] = acc;
+    acc += v;
+  }
+  if (t == 0) offsets[0] = 0;
+  if (t == 1023) {
+    stats[0] = tiles > 0 ? smin[1023] : 0;
+    stats[1] = ssum[1023];
+    stats[2] = sheavy[1023];
+  }
+}
+
+__global__ __launch_bounds__(SEG_THREADS) void seg_write_kernel(const int64_t* __restrict__ len,
+                                                                int64_t num,
+                                                                const int64_t* __restrict__ tsum,
+                                                                int32_t* __restrict__ offsets) {
+  __shared__ int64_t scan[SEG_THREADS];
+  const int t = threadIdx.x;
+  const int64_t lo = (int64_t)blockIdx.x * SEG_TILE + (int64_t)t * SEG_PER;
+  int64_t v[SEG_PER];
+  int64_t s = 0;
+  for (int k = 0; k < SEG_PER; ++k) {
+    const int64_t i = lo + k;
+    v[k] = i < num ? len[i] : 0;
+    s += v[k];
+  }
+  scan[t] = s;
+  __syncthreads();
+  for (int off = 1; off < SEG_THREADS; off <<= 1) {
+    const int64_t add = t >= off ? scan[t - off] : 0;
+    __syncthreads();
+    scan[t] += add;
+    __syncthreads();
+  }
+  int64_t acc = tsum[blockIdx.x] + (t > 0 ? scan[t - 1] : 0);
+  for (int k = 0; k < SEG_PER; ++k) {
+    const int64_t i = lo + k;
+    if (i < num) {
+      acc += v[k];
+      offsets[i + 1] = (int32_t)acc;
+    }
+  }
+}
+
+int64_t segment_offsets_workspace_bytes(int64_t num) {
+  const int64_t tiles = (num + SEG_TILE - 1) / SEG_TILE;
+  return tiles > 0 ? ((3 * tiles * 8 + 255) / 256) * 256 : 0;
+}
+
+hipError_t launch_segment_offsets(const int64_t* len, int64_t num, int64_t chunk_len,
+                                  int32_t* offsets, int64_t* stats, void* ws, hipStream_t s) {
+  const int64_t tiles = (num + SEG_TILE - 1) / SEG_TILE;
+  int64_t* tsum = static_cast<int64_t*>(ws);
+  int64_t* tmin = tsum + tiles;
+  int64_t* theavy = tmin + tiles;
+  if (tiles > 0)
+    hipLaunchKernelGGL(seg_partials_kernel, dim3((unsigned)tiles), dim3(SEG_THREADS), 0, s, len,
+                       num, chunk_len, tsum, tmin, theavy);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(seg_tiles_kernel, dim3(1), dim3(1024), 0, s, tsum, tmin, theavy, tiles,
+                     stats, offsets);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (tiles > 0)
+    hipLaunchKernelGGL(seg_write_kernel, dim3((unsigned)tiles), dim3(SEG_THREADS), 0, s, len, num,
+                       tsum, offsets);
+  return hipGetLastError();
 }
 
 static unsigned grid_for(int64_t n) {

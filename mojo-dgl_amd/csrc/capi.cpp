@@ -153,6 +153,28 @@ const char* mdgl_last_error(void) { return g_last_error.c_str(); }
 
 int64_t mdgl_workers(void) { return 256; }
 
+int64_t mdgl_segment_offsets_workspace_bytes(int64_t num) {
+  return num < 0 ? -1 : segment_offsets_workspace_bytes(num);
+}
+
+int mdgl_segment_offsets(const int64_t* seglen, int64_t num, int64_t chunk_len, int32_t* offsets,
+                         int64_t* stats, void* workspace, int64_t workspace_bytes,
+                         void* stream) {
+  if (num < 0) return fail(MDGL_EINVAL, "segment_offsets: negative count");
+  if (num >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "segment_offsets: 2**31 or more segments");
+  if (!offsets || !stats || (num > 0 && !seglen))
+    return fail(MDGL_EINVAL, "segment_offsets: null buffer");
+  const int64_t need = segment_offsets_workspace_bytes(num);
+  if (need > 0 && workspace && !aligned(workspace, WS_ALIGN))
+    return fail(MDGL_EINVAL, "workspace must be %lld-byte aligned", (long long)WS_ALIGN);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(MDGL_EWORKSPACE, "segment_offsets: workspace of %lld bytes needed, %lld given",
+                (long long)need, (long long)workspace_bytes);
+  return hip_status(launch_segment_offsets(seglen, num, chunk_len, offsets, stats, workspace,
+                                           (hipStream_t)stream),
+                    "segment_offsets");
+}
+
 int mdgl_cumsum(const int64_t* src, int64_t* dst, int64_t n, void* stream) {
   if (n < 0) return fail(MDGL_EINVAL, "cumsum: n must be >= 0");
   if (n > 0 && (!src || !dst)) return fail(MDGL_EINVAL, "cumsum: null buffer");

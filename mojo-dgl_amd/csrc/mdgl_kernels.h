@@ -149,5 +149,8 @@ hipError_t launch_build_csr(const int32_t* key, const int32_t* other, int64_t nu
                             int64_t num_rows, int32_t* indptr, int32_t* indices, int32_t* eid,
                             void* workspace, hipStream_t stream);
 hipError_t launch_cumsum_i64(const int64_t* src, int64_t* dst, int64_t n, hipStream_t s);
+int64_t segment_offsets_workspace_bytes(int64_t num);
+hipError_t launch_segment_offsets(const int64_t* len, int64_t num, int64_t chunk_len,
+                                  int32_t* offsets, int64_t* stats, void* ws, hipStream_t s);
 
 }  // namespace mdgl

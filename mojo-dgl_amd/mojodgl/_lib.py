@@ -61,6 +61,8 @@ _SIGNATURES = {
     "mdgl_last_error": ([], ctypes.c_char_p),
     "mdgl_workers": ([], _I64),
     "mdgl_cumsum": ([_P, _P, _I64, _P], _C),
+    "mdgl_segment_offsets": ([_P, _I64, _I64, _P, _P, _P, _I64, _P], _C),
+    "mdgl_segment_offsets_workspace_bytes": ([_I64], _I64),
     "mdgl_replace_inf_with_zero": ([_P, _P, _I64, _C, _P], _C),
     "mdgl_clamp_i64": ([_P, _P, _I64, _I64, _I64, _P], _C),
     "mdgl_gsddmm": ([_P, _P, _P, _P, _P, _I64, _C, _C, _C, _I64, _I64, _I64, _C, _P, _P, _C, _P],

@@ -49,28 +49,31 @@ class _Segments:
             self.heavy = 0
             if n >= 2 ** 31:
                 raise DGLError("segment operators take fewer than 2**31 rows, got {}".format(n))
-            if self.num:
-                stats = [sl.min(), sl.sum()]
-                if chunk_len is not None:
-                    stats.append(torch.where(sl > chunk_len, (sl + chunk_len - 1) // chunk_len,
-                                             0).sum())
-                got = torch.stack(stats).tolist()
-                if got[0] < 0 or got[1] != n:
-                    raise DGLError(
-                        "segment lengths must be non-negative and sum to {}, got offsets ending "
-                        "at {} for {} rows".format(n, got[1], n))
-                if chunk_len is not None:
-                    self.heavy = got[2]
-            off = torch.zeros(self.num + 1, dtype=torch.int64, device=sl.device)
-            torch.cumsum(sl, 0, out=off[1:])
-            self.off64 = off
-            self.off = off.to(torch.int32)
+            # offsets and the checks' figures in one pass (mdgl_segment_offsets),
+            # then one small read back
+            dev = sl.device
+            off = torch.empty(self.num + 1, dtype=torch.int32, device=dev)
+            stats = torch.empty(3, dtype=torch.int64, device=dev)
+            L = _lib.lib()
+            nbytes = L.mdgl_segment_offsets_workspace_bytes(self.num)
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes > 0 else None
+            _lib.check(L.mdgl_segment_offsets(sl.data_ptr(), self.num, chunk_len or 0,
+                                              off.data_ptr(), stats.data_ptr(), _lib.ptr(ws),
+                                              max(nbytes, 0), _lib.stream()),
+                       "segment_offsets")
+            low, total, heavy = stats.tolist()
+            if low < 0 or total != n:
+                raise DGLError(
+                    "segment lengths must be non-negative and sum to {}, got offsets ending "
+                    "at {} for {} rows".format(n, total, n))
+            if chunk_len is not None:
+                self.heavy = heavy
+            self.off = off
         else:
             sl = _lib.i64(seglen)
             self.num = sl.size
             self.host = _offsets(sl)
             _check_offsets(self.host, n)
-            self.off64 = None
             self.off = None
 
     def device(self):
@@ -170,7 +173,7 @@ def segment_softmax(seglen, value):
         if seg.host is not None:
             plan = _plan.SoftmaxPlan(seg.host, slots, chunk_len, ordered=False)
         else:
-            plan = _plan.SoftmaxPlan.from_device(seg.off64, slots, chunk_len, ordered=False,
+            plan = _plan.SoftmaxPlan.from_device(seg.off, slots, chunk_len, ordered=False,
                                                  num_chunks=seg.heavy)
         ws, nbytes = _plan.workspace(plan, d, dtype)
         rc = _lib.lib().mdgl_segment_softmax(

@@ -426,12 +426,42 @@ def test_segment_softmax_degree_plan_through_the_abi():
 
 def test_segment_gpu_lengths_are_validated():
     value = torch.ones(10, 2, device="cuda")
-    for bad in ([3, 3, 3], [12, -2], [4.5, 5.5]):
+    for bad in ([3, 3, 3], [12, -2], [4.5, 5.5], []):
         t = torch.tensor(bad, device="cuda")
         with pytest.raises(dgl.DGLError):
             ops.segment_reduce(t, value, "sum")
         with pytest.raises(dgl.DGLError):
             ops.segment_softmax(t, value)
+        with pytest.raises(dgl.DGLError):  # the host lengths are refused alike
+            ops.segment_reduce(np.array(bad), value.cpu().numpy(), "sum")
+
+
+@pytest.mark.parametrize("num", [0, 1, 4095, 4096, 4097, 1_000_003])
+def test_segment_offsets_through_the_abi(num):
+    """mdgl_segment_offsets: offsets equal [0] + cumsum (int32), stats equal
+    (min, sum, chunks of the long segments) from numpy."""
+    from mojodgl import _lib
+
+    rng = np.random.default_rng(70 + num)
+    seglen = rng.poisson(5, num).astype(np.int64)
+    if num > 10:
+        seglen[::7] = 0
+        seglen[3] = 700
+    L = _lib.lib()
+    sl = torch.from_numpy(seglen).cuda()
+    off = torch.full((num + 1,), -5, dtype=torch.int32, device="cuda")
+    stats = torch.full((3,), -5, dtype=torch.int64, device="cuda")
+    nbytes = L.mdgl_segment_offsets_workspace_bytes(num)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
+    for chunk_len in (0, 64):
+        assert L.mdgl_segment_offsets(sl.data_ptr(), num, chunk_len, off.data_ptr(),
+                                      stats.data_ptr(), ws.data_ptr(), nbytes,
+                                      _lib.stream()) == 0
+        want = np.concatenate([[0], np.cumsum(seglen)])
+        np.testing.assert_array_equal(off.cpu().numpy(), want)
+        heavy = int(np.where(seglen > chunk_len, -(-seglen // chunk_len), 0).sum()) \
+            if chunk_len else 0
+        assert stats.tolist() == [int(seglen.min()) if num else 0, int(seglen.sum()), heavy]
 
 
 # ------------------------------------------------------------------ dense
