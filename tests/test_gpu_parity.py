@@ -156,6 +156,34 @@ def test_gspmm_power_law_hubs_against_oracle():
     np.testing.assert_array_equal(ae, re_)
 
 
+@pytest.mark.parametrize("reduce_op", ["max", "min"])
+def test_gspmm_nan_messages_are_never_selected(reduce_op):
+    """max / min ignore NaN messages (strict comparison: a NaN never replaces
+    the running value, IEEE maxNum / minNum); a row of only NaN messages keeps
+    the identity, and update_all turns it into 0. Values and args against the
+    oracle bit for bit, in whole rows and in rows split into chunks."""
+    rng = np.random.default_rng(19)
+    n, e = 200, 5000
+    u, v = rand_graph(n, e, 20)
+    v[:1500] = 4  # a hub split into chunks
+    x = rng.normal(size=(n, 6)).astype(np.float32)
+    w = rng.normal(size=(e, 6)).astype(np.float32)
+    w[rng.random(e) < 0.2, 2] = np.nan
+    w[v == int(v[3000]), 4] = np.nan  # one row: column 4 only NaN messages
+    g = dgl.graph((u, v), num_nodes=n)
+    got, (au, ae) = ops.spmm._gspmm(g, "mul", reduce_op, x, w)
+    ref, ru, re_ = oracle.gspmm(u, v, n, "mul", reduce_op, x, w, np.float32, with_arg=True)
+    assert not np.isnan(got).any()
+    np.testing.assert_array_equal(got, ref)
+    np.testing.assert_array_equal(au, ru)
+    np.testing.assert_array_equal(ae, re_)
+    assert got[int(v[3000]), 4] == (-np.inf if reduce_op == "max" else np.inf)
+    g.ndata["x"] = x
+    g.edata["w"] = w
+    g.update_all(fn.u_mul_e("x", "w", "m"), getattr(fn, reduce_op)("m", "z"))
+    assert g.ndata["z"][int(v[3000]), 4] == 0
+
+
 def test_gspmm_zero_degree_and_empty_graph():
     u, v = np.array([0, 1]), np.array([1, 2])
     g = dgl.graph((u, v), num_nodes=5)
@@ -252,6 +280,36 @@ def test_edge_softmax(dtype, norm_by, shape):
     np.add.at(sums, key, flat)
     np.testing.assert_allclose(sums[np.bincount(key, minlength=n) > 0], 1.0,
                                atol=1e-4 if dtype == np.float32 else 1e-12)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_edge_softmax_special_values(dtype):
+    """-inf logits (masked attention) give 0 where a row has finite ones; a
+    row of only -inf, or one holding NaN or +inf, gives NaN for the whole row
+    and column, as the reference's max / exp / sum / divide; the same rows in
+    every row class (packed, wavefront, chunked hub)."""
+    n, e = 300, 4000
+    u, v = rand_graph(n, e, 17)
+    v[:700] = 7  # a chunked hub
+    rng = np.random.default_rng(18)
+    logits = rng.normal(size=(e, 2, 1)).astype(dtype)
+    rows = {"part_ninf": 7, "all_ninf": int(v[800]), "nan": int(v[900]), "pinf": int(v[1000])}
+    pick = lambda r: np.nonzero(v == r)[0]
+    logits[pick(rows["part_ninf"])[::3], 0] = -np.inf
+    logits[pick(rows["all_ninf"]), 1] = -np.inf
+    logits[pick(rows["nan"])[0], 0] = np.nan
+    logits[pick(rows["pinf"])[-1], 1] = np.inf
+    g = dgl.graph((u, v), num_nodes=n)
+    got = np.asarray(ops.edge_softmax(g, logits), dtype=np.float64)
+    ref = oracle.edge_softmax(u, v, n, logits, dtype=np.float64)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+    fin = ~np.isnan(ref)
+    close(got[fin], ref[fin], ref[fin], dtype, "edge_softmax special values")
+    assert np.isnan(got[pick(rows["all_ninf"]), 1]).all()
+    assert np.isnan(got[pick(rows["nan"]), 0]).all()
+    assert np.isnan(got[pick(rows["pinf"]), 1]).all()
+    hub = pick(rows["part_ninf"])
+    assert (got[hub[::3], 0] == 0).all() and np.isfinite(got[hub, 0]).all()
 
 
 @pytest.mark.parametrize("norm_by", ["dst", "src"])
