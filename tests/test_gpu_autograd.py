@@ -86,12 +86,16 @@ def assert_grads(got, ref, rtol=1e-9, atol=1e-12):
 
 
 # ------------------------------------------------------------------ gspmm
-@pytest.mark.parametrize("op", ["copy_lhs", "copy_rhs", "add", "sub", "mul", "div"])
+# copy_rhs has no broadcast form: only the full edge shape
+_OP_YSHAPE = [(op, ys) for op in ["copy_lhs", "copy_rhs", "add", "sub", "mul", "div"]
+              for ys in [(3, 4), (3, 1)] if not (op == "copy_rhs" and ys != (3, 4))]
+
+
+@pytest.mark.parametrize("op,yshape", _OP_YSHAPE,
+                         ids=["{}-{}".format(o, "full" if y == (3, 4) else "trailing-broadcast")
+                              for o, y in _OP_YSHAPE])
 @pytest.mark.parametrize("red", ["sum", "mean", "max", "min"])
-@pytest.mark.parametrize("yshape", [(3, 4), (3, 1)], ids=["full", "trailing-broadcast"])
 def test_gspmm_backward(op, red, yshape):
-    if op == "copy_rhs" and yshape != (3, 4):
-        pytest.skip("copy_rhs has no broadcast")
     n, e = 60, 700
     u, v = graph_with_loops(n, e, 50)
     E = u.size
