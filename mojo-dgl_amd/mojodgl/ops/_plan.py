@@ -130,10 +130,11 @@ class SoftmaxPlan:
         """The same plan built on the GPU from GPU offsets (int32 or int64):
         chunks of the long rows, and with `ordered` the rows with
         0 < degree <= chunk_len grouped by degree bin, stably (ascending row
-        id inside a bin), through the radix grouping of mdgl_build_csr, and
-        the packed rows' edge ids slot by slot (`eid` the CSR's edge ids, or
-        None for the slot index). `num_chunks`, when the caller knows it,
-        saves a read back."""
+        id inside a bin), through the radix grouping of mdgl_build_csr, the
+        packed rows' edge ids slot by slot (`eid` the CSR's edge ids, or None
+        for the slot index) and the two-pass table slot of every edge
+        (`slot_of_edge`, `table_rows`). `num_chunks`, when the caller knows
+        it, saves a read back."""
         from ..heterograph import build_device_csr
 
         self = cls.__new__(cls)
