@@ -513,7 +513,7 @@ def main():
                     help="HBM bytes per gspmm launch measured by rocprofv3 (reported as is)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU only: this build runs on a single MI355X and has no "
+        print("bench.py measures one GPU only: mojodgl runs on a single MI355X and has no "
               "multi-GPU path (--gpus {} requested)".format(args.gpus), file=sys.stderr)
         sys.exit(2)
     import torch

@@ -1,8 +1,9 @@
 """CPU oracle for the message-passing kernel layer.
 
 TEST INFRASTRUCTURE ONLY. Only `tests/`, `__graft_entry__.smoke()` and the
-`cpu_baseline` leg of `bench.py` import this package, and only as the checker
-(or as the timed CPU baseline). The product package `mojodgl` never imports it.
+`cpu_baseline` leg of `bench.py` import this package, and only as what GPU
+results are compared against (or as the timed CPU baseline). The product
+package `mojodgl` never imports it.
 
 `liboracle.so` (built from `mdgl_oracle.cpp` by `make -C oracle`) restates the
 reference's kernels (src/ported.mojo); this module restates the reference's
