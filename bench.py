@@ -432,6 +432,34 @@ def workload_c4(args):
         m = timer.avg_ms(name)
         kern[name] = {"ms": round(m, 4), "bytes": b, "GBps": round(b / m / 1e6, 1)}
     units = E * 128 + 3 * R * 16
+    # the reference's array helpers at the same sizes, outside the step:
+    # cumsum and clamp over the 1M int64 lengths, replace_inf over the values
+    from mojodgl import _lib
+
+    L = _lib.lib()
+    lens = seglen_d.to(torch.int64).contiguous()
+    ibuf = torch.empty_like(lens)
+    fbuf = torch.empty_like(val)
+    helpers = {
+        "cumsum": (lambda: L.mdgl_cumsum(lens.data_ptr(), ibuf.data_ptr(), S, _lib.stream()),
+                   16 * S),
+        "clamp_i64": (lambda: L.mdgl_clamp_i64(lens.data_ptr(), ibuf.data_ptr(), S, 1, R,
+                                               _lib.stream()), 16 * S),
+        "replace_inf_with_zero": (lambda: L.mdgl_replace_inf_with_zero(
+            val.data_ptr(), fbuf.data_ptr(), R * 16, 0, _lib.stream()), 8 * R * 16),
+    }
+    for name, (fn_, b) in helpers.items():
+        assert fn_() == 0
+        torch.cuda.synchronize()
+        s_ = torch.cuda.Event(enable_timing=True)
+        t_ = torch.cuda.Event(enable_timing=True)
+        s_.record()
+        for _ in range(args.steps):
+            fn_()
+        t_.record()
+        torch.cuda.synchronize()
+        m = s_.elapsed_time(t_) / args.steps
+        kern[name] = {"ms": round(m, 4), "bytes": b, "GBps": round(b / m / 1e6, 1)}
     return {"metric": "gSDDMM / segment GEdge·feat/s, fp32, 1 GPU",
             "value": round(units / ms / 1e6, 2), "unit": "GEdge·feat/s",
             "ms_per_step": round(ms, 4), "dtype": "f32",

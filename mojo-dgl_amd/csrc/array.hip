@@ -5,11 +5,28 @@
 
 namespace mdgl {
 
+// 16 bytes per thread and step when both buffers are 16-byte aligned (the
+// tail, or everything otherwise, one element at a time); each value is
+// read and written once, so the stream bypasses the caches' reuse.
 template <class T>
 __global__ __launch_bounds__(BLOCK) void replace_inf_kernel(const T* __restrict__ src,
-                                                            T* __restrict__ dst, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * BLOCK) {
+                                                            T* __restrict__ dst, int64_t n,
+                                                            int vec) {
+  constexpr int V = VecOf<T>::n;
+  const int64_t stride = (int64_t)gridDim.x * BLOCK;
+  int64_t done = 0;
+  if (vec) {
+    const int64_t nv = n / V;
+    for (int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < nv; i += stride) {
+      T x[V];
+      load_n_stream<T, V>(src + i * V, x);
+#pragma unroll
+      for (int k = 0; k < V; ++k) x[k] = is_inf(x[k]) ? T(0) : x[k];
+      store_n_stream<T, V>(dst + i * V, x);
+    }
+    done = nv * V;
+  }
+  for (int64_t i = done + (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < n; i += stride) {
     const T v = src[i];
     dst[i] = is_inf(v) ? T(0) : v;
   }
@@ -26,18 +43,56 @@ __global__ __launch_bounds__(BLOCK) void clamp_kernel(const int64_t* __restrict_
   }
 }
 
-// One workgroup: each thread sums a contiguous span, the span totals are
-// scanned in LDS, then every thread rewrites its span with its carry.
-// Integer addition is exact, so this equals the sequential prefix sum.
-__global__ __launch_bounds__(1024) void cumsum_kernel(const int64_t* __restrict__ src,
-                                                      int64_t* __restrict__ dst, int64_t n) {
+// Inclusive int64 prefix sum over tiles of CS_TILE values (16 consecutive
+// per thread), in dst itself, with no other memory: (1) every tile writes
+// its local inclusive scan; (2) one workgroup turns the tile totals (each
+// tile's last value) into running totals, which are final there; (3) every
+// tile but the first adds the previous tile's running total to its other
+// values. Integer addition is exact, so this equals the sequential sum.
+constexpr int CS_THREADS = 256;
+constexpr int CS_PER = 16;
+constexpr int CS_TILE = CS_THREADS * CS_PER;
+
+__global__ __launch_bounds__(CS_THREADS) void cumsum_tile_kernel(const int64_t* __restrict__ src,
+                                                                 int64_t* __restrict__ dst,
+                                                                 int64_t n) {
+  __shared__ int64_t scan[CS_THREADS];
+  const int t = threadIdx.x;
+  const int64_t lo = (int64_t)blockIdx.x * CS_TILE + (int64_t)t * CS_PER;
+  int64_t v[CS_PER];
+  int64_t s = 0;
+  for (int k = 0; k < CS_PER; ++k) {
+    v[k] = lo + k < n ? src[lo + k] : 0;
+    s += v[k];
+  }
+  scan[t] = s;
+  __syncthreads();
+  for (int off = 1; off < CS_THREADS; off <<= 1) {
+    const int64_t add = t >= off ? scan[t - off] : 0;
+    __syncthreads();
+    scan[t] += add;
+    __syncthreads();
+  }
+  int64_t acc = t > 0 ? scan[t - 1] : 0;
+  for (int k = 0; k < CS_PER; ++k) {
+    acc += v[k];
+    if (lo + k < n) dst[lo + k] = acc;
+  }
+}
+
+__global__ __launch_bounds__(1024) void cumsum_totals_kernel(int64_t* __restrict__ dst, int64_t n,
+                                                             int64_t tiles) {
   __shared__ int64_t tot[1024];
   const int t = threadIdx.x;
-  const int64_t span = (n + 1023) / 1024;
-  const int64_t lo = t * span < n ? t * span : n;
-  const int64_t hi = lo + span < n ? lo + span : n;
+  const int64_t span = (tiles + 1023) / 1024;
+  const int64_t lo = t * span < tiles ? t * span : tiles;
+  const int64_t hi = lo + span < tiles ? lo + span : tiles;
+  auto last = [&](int64_t b) {
+    const int64_t e = (b + 1) * CS_TILE - 1;
+    return e < n ? e : n - 1;
+  };
   int64_t s = 0;
-  for (int64_t i = lo; i < hi; ++i) s += src[i];
+  for (int64_t b = lo; b < hi; ++b) s += dst[last(b)];
   tot[t] = s;
   __syncthreads();
   for (int off = 1; off < 1024; off <<= 1) {
@@ -47,10 +102,18 @@ __global__ __launch_bounds__(1024) void cumsum_kernel(const int64_t* __restrict_
     __syncthreads();
   }
   int64_t acc = t > 0 ? tot[t - 1] : 0;
-  for (int64_t i = lo; i < hi; ++i) {
-    acc += src[i];
-    dst[i] = acc;
+  for (int64_t b = lo; b < hi; ++b) {
+    acc += dst[last(b)];
+    dst[last(b)] = acc;
   }
+}
+
+__global__ __launch_bounds__(CS_THREADS) void cumsum_carry_kernel(int64_t* __restrict__ dst,
+                                                                  int64_t n) {
+  const int64_t b = (int64_t)blockIdx.x + 1;  // tile 0 needs no carry
+  const int64_t carry = dst[b * CS_TILE - 1];  // running total through tile b - 1
+  const int64_t end = (b + 1) * CS_TILE - 1 < n ? (b + 1) * CS_TILE - 1 : n - 1;
+  for (int64_t i = b * CS_TILE + threadIdx.x; i < end; i += CS_THREADS) dst[i] += carry;
 }
 
 template <class T>
@@ -227,12 +290,16 @@ static unsigned grid_for(int64_t n) {
 
 hipError_t launch_replace_inf(const void* src, void* dst, int64_t n, int dtype, hipStream_t s) {
   if (n <= 0) return hipSuccess;
+  const int vec = (reinterpret_cast<uintptr_t>(src) % 16 == 0) &&
+                  (reinterpret_cast<uintptr_t>(dst) % 16 == 0);
+  const int64_t per = vec ? (dtype == 0 ? 4 : 2) : 1;
+  const unsigned grid = grid_for((n + per - 1) / per);
   if (dtype == 0)
-    hipLaunchKernelGGL(replace_inf_kernel<float>, dim3(grid_for(n)), dim3(BLOCK), 0, s,
-                       static_cast<const float*>(src), static_cast<float*>(dst), n);
+    hipLaunchKernelGGL(replace_inf_kernel<float>, dim3(grid), dim3(BLOCK), 0, s,
+                       static_cast<const float*>(src), static_cast<float*>(dst), n, vec);
   else
-    hipLaunchKernelGGL(replace_inf_kernel<double>, dim3(grid_for(n)), dim3(BLOCK), 0, s,
-                       static_cast<const double*>(src), static_cast<double*>(dst), n);
+    hipLaunchKernelGGL(replace_inf_kernel<double>, dim3(grid), dim3(BLOCK), 0, s,
+                       static_cast<const double*>(src), static_cast<double*>(dst), n, vec);
   return hipGetLastError();
 }
 
@@ -258,7 +325,16 @@ hipError_t launch_gather_rows(const void* src, const int32_t* idx, void* dst, in
 
 hipError_t launch_cumsum_i64(const int64_t* src, int64_t* dst, int64_t n, hipStream_t s) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(cumsum_kernel, dim3(1), dim3(1024), 0, s, src, dst, n);
+  const int64_t tiles = (n + CS_TILE - 1) / CS_TILE;
+  hipLaunchKernelGGL(cumsum_tile_kernel, dim3((unsigned)tiles), dim3(CS_THREADS), 0, s, src, dst,
+                     n);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || tiles == 1) return e;
+  hipLaunchKernelGGL(cumsum_totals_kernel, dim3(1), dim3(1024), 0, s, dst, n, tiles);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(cumsum_carry_kernel, dim3((unsigned)(tiles - 1)), dim3(CS_THREADS), 0, s, dst,
+                     n);
   return hipGetLastError();
 }
 

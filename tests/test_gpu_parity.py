@@ -522,6 +522,38 @@ def test_segment_offsets_through_the_abi(num):
         assert stats.tolist() == [int(seglen.min()) if num else 0, int(seglen.sum()), heavy]
 
 
+# ------------------------------------------------------------------ array helpers
+@pytest.mark.parametrize("n", [1, 100, 4095, 4096, 4097, 12289, 1_000_003])
+def test_cumsum_clamp_replace_inf_through_the_abi(n):
+    """mdgl_cumsum / mdgl_clamp_i64 / mdgl_replace_inf_with_zero (the
+    reference's capi helpers) against numpy's cumsum, clip and where: exact."""
+    from mojodgl import _lib
+
+    L = _lib.lib()
+    rng = np.random.default_rng(80 + n)
+    src = rng.integers(-2 ** 40, 2 ** 40, n)
+    a = torch.from_numpy(src).cuda()
+    out = torch.full_like(a, 7)
+    assert L.mdgl_cumsum(a.data_ptr(), out.data_ptr(), n, _lib.stream()) == 0
+    np.testing.assert_array_equal(out.cpu().numpy(), np.cumsum(src))
+    lo, hi = -2 ** 39, 2 ** 38
+    assert L.mdgl_clamp_i64(a.data_ptr(), out.data_ptr(), n, lo, hi, _lib.stream()) == 0
+    np.testing.assert_array_equal(out.cpu().numpy(), np.clip(src, lo, hi))
+    for dtype, code in ((np.float32, 0), (np.float64, 1)):
+        x = rng.normal(size=n).astype(dtype)
+        x[::5] = np.inf
+        x[1::7] = -np.inf
+        x[2::11] = np.nan
+        want = np.where(np.isinf(x), 0, x).astype(dtype)
+        t = torch.from_numpy(np.concatenate([[dtype(1)], x])).cuda()
+        y = torch.zeros_like(t)
+        # 16-byte aligned buffers, then views one element in (element loads)
+        for src, dst in ((t[1:].clone(), y[1:].clone()), (t[1:], y[1:])):
+            assert L.mdgl_replace_inf_with_zero(src.data_ptr(), dst.data_ptr(), n, code,
+                                                _lib.stream()) == 0
+            np.testing.assert_array_equal(dst.cpu().numpy(), want)
+
+
 # ------------------------------------------------------------------ dense
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("d1,d2,r", [(128, 128, 64), (5, 3, 7), (16, 16, 4), (33, 130, 3),
