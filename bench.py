@@ -204,9 +204,39 @@ def workload_gat(args):
     }
     result["graph_build"] = time_graph_build(g, u, v, N, args)
     result["edge_softmax_subset"] = time_subset_softmax(g, el, er, E, args)
+    result["forward_backward"] = time_gat_backward(g, el, er, h)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_gat(g, el, er, h, args)
     return result
+
+
+def time_gat_backward(g, el, er, h):
+    """The same layer with autograd (el, er, h requiring grad): forward plus
+    backward, not part of a step (HIP events, average of 3). The backward
+    reductions run on the forward kernels over the in- and out-CSR."""
+    import torch
+
+    import mojodgl.ops as ops
+
+    el_, er_, h_ = (t.clone().requires_grad_(True) for t in (el, er, h))
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    grad = torch.randn(h.shape, device="cuda", generator=gen)
+
+    def fb():
+        e = torch.nn.functional.leaky_relu(ops.u_add_v(g, el_, er_), 0.2)
+        out = ops.u_mul_e_sum(g, h_, ops.edge_softmax(g, e))
+        out.backward(grad)
+
+    fb()
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    t = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(3):
+        fb()
+    t.record()
+    torch.cuda.synchronize()
+    return {"ms": round(s.elapsed_time(t) / 3, 3)}
 
 
 def time_subset_softmax(g, el, er, E, args):

@@ -238,6 +238,29 @@ int mdgl_gspmm_edge_grad(const int32_t* vids, const int32_t* indptr, const void*
                          const int32_t* arg_e, void* dst, int64_t num_edges, int64_t d, int mean,
                          double alpha, int dtype, void* stream);
 
+/* mdgl_gspmm_mul_sum_dot: one pass for both gradients of a u_mul_e_sum whose
+ *   edge operand is constant over groups of D = dout / dr consecutive columns
+ *   (an edge operand of shape (E, ..., 1) against node rows (N, ..., D)),
+ *   run over the CSR of the reversed graph (rows = sources, indices =
+ *   destinations, the arguments of mdgl_gspmm with op mul, reduce sum):
+ *     dst[row][k]  = sum over the row's slots j, in CSR order, of
+ *                    lhs[indices[j]][k] * rhs[eid[j]][k / D]   (as mdgl_gspmm)
+ *     dot[j][c]    = sum over k in group c of lhs[indices[j]][k] * rowop[row][k]
+ *   i.e. with lhs = the output gradient and rowop = the node operand, the
+ *   node operand's gradient and, in CSR slot order, the edge operand's.
+ *   Needs 16-byte lanes (dout a multiple of 16 / sizeof(T), lhs, rowop and
+ *   the group's columns aligned) and D / (16 / sizeof(T)) a power of two up
+ *   to 64; other shapes return MDGL_ENOTSUP (compute the two with
+ *   mdgl_gspmm and mdgl_gsddmm then). No counterpart in the reference. */
+int mdgl_gspmm_mul_sum_dot(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
+                           const void* lhs, const void* rhs, const void* rowop, void* dst,
+                           void* dot, int64_t num_dst, int64_t dl, int64_t dr, int64_t dout,
+                           int nd, const int64_t* lhs_shape, const int64_t* rhs_shape,
+                           const int32_t* chunk_row, const int32_t* chunk_start,
+                           int64_t num_chunks, int32_t chunk_len, const int32_t* heavy_rows,
+                           const int32_t* heavy_ptr, int64_t num_heavy, void* workspace,
+                           int64_t workspace_bytes, int dtype, void* stream);
+
 /* dst[r, k] = src[r, k] / max(indptr[r+1] - indptr[r], 1): the mean's divisor on a
  * node-shaped gradient. */
 int mdgl_rows_by_degree(const int32_t* indptr, const void* src, void* dst, int64_t rows,

@@ -372,7 +372,8 @@ int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* e
                  int32_t* arg_e, const int32_t* chunk_row, const int32_t* chunk_start,
                  int64_t num_chunks, int32_t chunk_len, const int32_t* heavy_rows,
                  const int32_t* heavy_ptr, int64_t num_heavy, void* workspace,
-                 int64_t workspace_bytes, int flags, int dtype, void* stream, bool ident) {
+                 int64_t workspace_bytes, int flags, int dtype, void* stream, bool ident,
+                 const void* rowop = nullptr, void* dot_out = nullptr) {
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "gspmm: bad dtype %d", dtype);
   if (op < OP_ADD || op > OP_COPY_RHS || op == OP_DOT)
     return fail(MDGL_EINVAL, "gspmm: bad op %d (dot is a gsddmm operator)", op);
@@ -471,6 +472,30 @@ int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* e
   p.lmode = op == OP_COPY_RHS ? M_CONTIG : pick_mode(p.bc, true, dout, p.vec, dl, lhs, es);
   p.rmode = op == OP_COPY_LHS ? M_CONTIG : pick_mode(p.bc, false, dout, p.vec, dr, rhs, es);
   if (p.vec > 1 && aligned(dst, p.vec * es)) p.flags |= F_OUT_VEC;
+  if (dot_out) {
+    // the fused dot: mul / sum, 16-byte lanes, lhs rows contiguous, the edge
+    // operand constant over groups of D = dout / dr consecutive columns
+    // (D / vec lanes, a power of two up to 64), the row operand aligned
+    if (op != OP_MUL || reduce_op != RED_SUM)
+      return fail(MDGL_EINVAL, "gspmm dot: mul with sum only");
+    if (!rowop) return fail(MDGL_EINVAL, "gspmm dot: null row operand");
+    if (dr <= 0 || dout % dr != 0)
+      return fail(MDGL_EINVAL, "gspmm dot: dout %lld is not a multiple of dr %lld",
+                  (long long)dout, (long long)dr);
+    const int64_t D = dout / dr;
+    const int64_t lanes = D / vw;
+    bool ok = p.vec == vw && D % vw == 0 && lanes <= WAVE && (lanes & (lanes - 1)) == 0 &&
+              p.lmode == M_CONTIG && aligned(rowop, vw * es);
+    for (int64_t k = 0; ok && k < dout; ++k)
+      ok = bcast_off(p.bc, k, false) == k / D && bcast_off(p.bc, k, true) == k;
+    if (!ok)
+      return fail(MDGL_ENOTSUP, "gspmm dot: needs contiguous aligned rows and the edge operand "
+                  "splat over power-of-two groups of 16-byte lanes");
+    p.rowop = rowop;
+    p.dot_out = dot_out;
+    p.dot_lanes = (int)lanes;
+    p.rmode = M_SPLAT;
+  }
   hipError_t e;
   if (dtype == MDGL_FLOAT32) {
     e = p.red == RED_MAX ? launch_gspmm_red<float, RED_MAX>(p)
@@ -500,6 +525,21 @@ int mdgl_gspmm(const int32_t* indptr, const int32_t* indices, const int32_t* eid
                       deg, nd, lhs_shape, rhs_shape, arg_u, arg_e, chunk_row, chunk_start,
                       num_chunks, chunk_len, heavy_rows, heavy_ptr, num_heavy, workspace,
                       workspace_bytes, flags, dtype, stream, false);
+}
+
+int mdgl_gspmm_mul_sum_dot(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
+                           const void* lhs, const void* rhs, const void* rowop, void* dst,
+                           void* dot, int64_t num_dst, int64_t dl, int64_t dr, int64_t dout,
+                           int nd, const int64_t* lhs_shape, const int64_t* rhs_shape,
+                           const int32_t* chunk_row, const int32_t* chunk_start,
+                           int64_t num_chunks, int32_t chunk_len, const int32_t* heavy_rows,
+                           const int32_t* heavy_ptr, int64_t num_heavy, void* workspace,
+                           int64_t workspace_bytes, int dtype, void* stream) {
+  if (num_dst > 0 && dout > 0 && !dot) return fail(MDGL_EINVAL, "gspmm dot: null dot output");
+  return gspmm_common(indptr, indices, eid, lhs, rhs, dst, num_dst, OP_MUL, dl, dr, dout, RED_SUM,
+                      nullptr, nd, lhs_shape, rhs_shape, nullptr, nullptr, chunk_row, chunk_start,
+                      num_chunks, chunk_len, heavy_rows, heavy_ptr, num_heavy, workspace,
+                      workspace_bytes, 0, dtype, stream, false, rowop, dot);
 }
 
 int mdgl_segment_reduce(const int32_t* offsets, const void* value, void* dst, int64_t num_seg,

@@ -60,6 +60,9 @@ struct GspmmArgs {
   // so the rows of neighbouring units share cache lines across wavefronts)
   int64_t chunk_uwaves, row_uwaves;
   int slab_major;
+  const T* rowop;  // dot output (see GspmmParams), else null
+  T* dot_out;
+  int dot_lanes;
 };
 
 template <class T, int VEC, int M>
@@ -96,7 +99,8 @@ __device__ __forceinline__ void fetch_stream(const T* __restrict__ row, int mode
   }
 }
 
-template <class T, int OP, int RED, int VEC, int LM, int RM, bool WIDE, bool NT>
+template <class T, int OP, int RED, int VEC, int LM, int RM, bool WIDE, bool NT,
+          bool DOT = false>
 __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, int64_t wave,
                                            int lane) {
   constexpr int U = 4;
@@ -133,6 +137,14 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
     const int64_t k = (feat_ok && k0 + v < a.dout) ? k0 + v : (feat_ok ? k0 : 0);
     loff[v] = (int)bcast_off(a.bc, k, true);
     roff[v] = (int)bcast_off(a.bc, k, false);
+  }
+
+  // DOT: this row's own feature columns, dotted with every gathered lhs row
+  T rowv[VEC];
+  if constexpr (DOT) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) rowv[v] = T(0);
+    if (ok && feat_ok) load_n<T, VEC>(a.rowop + row * a.dout + k0, rowv);
   }
 
   T acc[VEC];
@@ -211,6 +223,24 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
           }
         }
       }
+      if constexpr (DOT) {
+        // per slot and column group: the lanes' partial dots, then a
+        // butterfly over the group's lanes; the group's first lane writes
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (j + u >= jmax) break;  // uniform in the wavefront
+          T pd = T(0);
+          if (j + u < cnt && feat_ok) {
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) pd = pd + x[u][v] * rowv[v];
+          }
+          for (int off = 1; off < a.dot_lanes; off <<= 1) pd = pd + __shfl_xor(pd, off);
+          if (j + u < cnt && feat_ok && (gl % a.dot_lanes) == 0) {
+            const int64_t slot = start + base + j + u;
+            a.dot_out[slot * a.dr + k0 / ((int64_t)a.dot_lanes * VEC)] = pd;
+          }
+        }
+      }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (j + u < cnt && feat_ok) {
@@ -283,7 +313,8 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
 // registers of its own path: whole-wavefront units (G = 64) with both
 // operands contiguous, with a splatted edge operand, or any modes; packed
 // units with contiguous operands, or any modes.
-enum { P_WIDE_CC = 0, P_WIDE_CS = 1, P_WIDE_DYN = 2, P_PACK_CC = 3, P_PACK_DYN = 4 };
+enum { P_WIDE_CC = 0, P_WIDE_CS = 1, P_WIDE_DYN = 2, P_PACK_CC = 3, P_PACK_DYN = 4,
+       P_WIDE_CS_DOT = 5, P_PACK_DYN_DOT = 6 };
 
 template <class T, int OP, int RED, int VEC, int PATH, bool NT>
 __global__ __launch_bounds__(BLOCK) void gspmm_kernel(GspmmArgs<T> a) {
@@ -304,6 +335,10 @@ __global__ __launch_bounds__(BLOCK) void gspmm_kernel(GspmmArgs<T> a) {
     gspmm_body<T, OP, RED, VEC, M_DYN, M_DYN, true, NT>(a, chunk, wave, lane);
   else if constexpr (PATH == P_PACK_CC)
     gspmm_body<T, OP, RED, VEC, M_CONTIG, M_CONTIG, false, NT>(a, chunk, wave, lane);
+  else if constexpr (PATH == P_WIDE_CS_DOT)
+    gspmm_body<T, OP, RED, VEC, M_CONTIG, M_SPLAT, true, NT, true>(a, chunk, wave, lane);
+  else if constexpr (PATH == P_PACK_DYN_DOT)
+    gspmm_body<T, OP, RED, VEC, M_DYN, M_DYN, false, NT, true>(a, chunk, wave, lane);
 
   else
     gspmm_body<T, OP, RED, VEC, M_DYN, M_DYN, false, NT>(a, chunk, wave, lane);
@@ -404,6 +439,9 @@ hipError_t launch_gspmm_op(const GspmmParams& p) {
   a.slab_major = a.S > 1;
   a.chunk_blocks = (a.chunk_waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
   a.num_blocks = a.chunk_blocks + (a.row_waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
+  a.rowop = static_cast<const T*>(p.rowop);
+  a.dot_out = static_cast<T*>(p.dot_out);
+  a.dot_lanes = p.dot_lanes;
   if (a.num_blocks > 0) {
     const bool copy_l = OP == OP_COPY_LHS, copy_r = OP == OP_COPY_RHS;
     const int lm = copy_r ? a.rmode : a.lmode;
@@ -411,13 +449,28 @@ hipError_t launch_gspmm_op(const GspmmParams& p) {
     const dim3 grid((unsigned)a.num_blocks), block(BLOCK);
     // edge rows are streamed unless they are consecutive (identity ids:
     // segment_reduce, which is copy_rhs)
-    if constexpr (OP == OP_COPY_RHS) {
-      if (a.flags & F_EID_IDENTITY)
-        launch_path<T, OP, RED, VEC, false>(a, grid, block, lm, rm, p.stream);
-      else
+    bool launched = false;
+    if constexpr (OP == OP_MUL && RED == RED_SUM) {
+      if (p.dot_out) {
+        // the caller checked: contiguous lhs rows, rhs splat over the groups
+        if (a.G == WAVE)
+          hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_WIDE_CS_DOT, true>), grid, block, 0,
+                             p.stream, a);
+        else
+          hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_PACK_DYN_DOT, true>), grid, block,
+                             0, p.stream, a);
+        launched = true;
+      }
+    }
+    if (!launched) {
+      if constexpr (OP == OP_COPY_RHS) {
+        if (a.flags & F_EID_IDENTITY)
+          launch_path<T, OP, RED, VEC, false>(a, grid, block, lm, rm, p.stream);
+        else
+          launch_path<T, OP, RED, VEC, true>(a, grid, block, lm, rm, p.stream);
+      } else {
         launch_path<T, OP, RED, VEC, true>(a, grid, block, lm, rm, p.stream);
-    } else {
-      launch_path<T, OP, RED, VEC, true>(a, grid, block, lm, rm, p.stream);
+      }
     }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;

@@ -46,6 +46,13 @@ struct GspmmParams {
   void* part_val;
   int32_t* part_u;
   int32_t* part_e;
+  // optional (mul / sum with the edge operand splat over groups of
+  // dot_lanes * vec columns): a feature row per CSR row and, per CSR slot and
+  // group, dot_out[slot][group] = sum over the group of lhs[indices[slot]] *
+  // rowop[row]
+  const void* rowop;
+  void* dot_out;
+  int dot_lanes;
   hipStream_t stream;
 };
 

@@ -50,6 +50,7 @@ TARGETS = {"u": SRC_CODE, "v": DST_CODE, "e": EDGE_CODE}
 FLOAT32, FLOAT64 = 0, 1
 REPLACE_INF = 1
 RHS_CSR_ORDER = 2
+EINVAL, EWORKSPACE, ENOTSUP = -1, -2, -3  # negative statuses of include/mdgl.h
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -70,6 +71,8 @@ _SIGNATURES = {
     "mdgl_gspmm": ([_P, _P, _P, _P, _P, _P, _I64, _C, _I64, _I64, _I64, _C, _P, _C, _P, _P, _P,
                     _P, _P, _P, _I64, _I32, _P, _P, _I64, _P, _I64, _C, _C, _P], _C),
     "mdgl_gspmm_workspace_bytes": ([_I64, _I64, _C, _C], _I64),
+    "mdgl_gspmm_mul_sum_dot": ([_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _C, _P,
+                                _P, _P, _P, _I64, _I32, _P, _P, _I64, _P, _I64, _C, _P], _C),
     "mdgl_segment_reduce": ([_P, _P, _P, _I64, _I64, _C, _I64, _C, _C, _P], _C),
     "mdgl_softmax_geometry": ([_I64, _C, _P, _P, _P, _P], _C),
     "mdgl_softmax_workspace_bytes": ([_I64, _I64, _I64, _C], _I64),

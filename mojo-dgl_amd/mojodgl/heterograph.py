@@ -118,6 +118,17 @@ class _DeviceCSR:
         self.chunks = _Chunks(self.host_indptr, chunk_len)
         self.params = int(chunk_len)
         self._softmax = {}
+        self._slot_of_eid = None
+
+    def slot_of_eid(self):
+        """The inverse of `eid`: the CSR slot of every edge id (cached)."""
+        if self._slot_of_eid is None:
+            E = self.eid.shape[0]
+            pos = torch.empty(E, dtype=torch.int32, device=self.eid.device)
+            pos[self.eid.to(torch.int64)] = torch.arange(E, dtype=torch.int32,
+                                                         device=self.eid.device)
+            self._slot_of_eid = pos
+        return self._slot_of_eid
 
     def softmax_plan(self, slots, chunk_len):
         """Degree-sorted row order, packed edge ids and chunks for a softmax

@@ -5,7 +5,11 @@ these follow the calculus of the forward ops and run on the same kernels:
 
 * gspmm(op, reduce) with node operand X, edge operand Y, output gradient G:
   - sum / mean: the gradient reaching edge e = (u, v) is G[v] (divided by
-    max(deg v, 1) for mean: ``mdgl_rows_by_degree`` on G first);
+    max(deg v, 1) for mean: ``mdgl_rows_by_degree`` on G first); for mul
+    with an edge operand constant over x's last axis (attention weights),
+    dX and dY come from one pass over the out-CSR
+    (``mdgl_gspmm_mul_sum_dot``: G[v] gathered once per edge, dY in CSR slot
+    order, then gathered to edge order);
     dX[u] = sum over u's out-edges of that gradient times d msg / dX, a
     gspmm over the out-CSR (copy for copy_lhs / add / sub, mul / div by Y for
     mul / div); dY[e] = gradient times d msg / dY, a gsddmm (copy of G[v],
@@ -155,6 +159,14 @@ class GSpMM(torch.autograd.Function):
         if red in ("sum", "mean"):
             if red == "mean":
                 G = _rows_by_degree(g._device_csr("in"), G)
+            if op == "mul" and need_x and need_y:
+                # both gradients in one pass over the out-CSR when the edge
+                # operand is constant over trailing groups of x (attention)
+                from .spmm import _mul_sum_dot
+
+                fused = _mul_sum_dot(g, G, y, x) if _trailing_groups(x, y) else None
+                if fused is not None:
+                    return (None, None, None) + fused + (None,)
             if need_x:
                 if op in ("copy_lhs", "add", "sub"):
                     dx = _gspmm(g, "copy_lhs", "sum", G, None, kind="out")
@@ -198,6 +210,16 @@ class GSpMM(torch.autograd.Function):
         if dy is not None:
             dy = dy.reshape(y.shape)
         return None, None, None, dx, dy, None
+
+
+def _trailing_groups(x, y):
+    """y (E, ...) is x's feature shape with its trailing axes collapsed to
+    one (y = (E, *lead, 1) against x = (N, *lead, D))."""
+    xs = tuple(x.shape[1:])
+    ys = tuple(y.shape[1:]) if y.dim() > 1 else (1,)
+    if len(ys) != len(xs) or not xs or ys[-1] != 1 or xs[-1] == 1:
+        return False
+    return ys[:-1] == xs[:-1]
 
 
 def _padded(shape, full):

@@ -121,6 +121,53 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
     return out, arg_u, arg_e, as_torch, dev
 
 
+def _mul_sum_dot(g, grad, y, x, kind="out"):
+    """Both gradients of a u_mul_e_sum whose edge operand `y` is constant
+    over trailing groups of the node operand `x`, in one pass over the `kind`
+    CSR (mdgl_gspmm_mul_sum_dot): returns (dx, dy) as GPU tensors shaped like
+    x and y, or None when the shapes do not fit the fused kernel (the caller
+    then runs gspmm and gsddmm)."""
+    G = grad.contiguous()
+    X = x.contiguous()
+    # y as (E, *x's leading feature axes, 1): the same rank as the node rows
+    Y = y.contiguous().reshape((y.shape[0],) + tuple(x.shape[1:-1]) + (1,))
+    if not (G.dtype == X.dtype == Y.dtype and G.dtype in (torch.float32, torch.float64)
+            and G.is_cuda and X.is_cuda and Y.is_cuda):
+        return None
+    dtype = np.float32 if G.dtype == torch.float32 else np.float64
+    nd, ls, rs = shape_args(G.shape, Y.shape)
+    dout = width(G.shape)
+    dr = width(Y.shape)
+    num_rows = g.number_of_nodes()
+    E = g.number_of_edges()
+    if X.shape != G.shape or Y.shape[0] != E or G.shape[0] != num_rows or dr == 0:
+        return None
+    csr = g._device_csr(kind)
+    sched = csr.chunks
+    gdev = _lib.device()
+    dx = torch.empty((num_rows, dout), dtype=G.dtype, device=gdev)
+    dot = torch.empty((E, dr), dtype=G.dtype, device=gdev)
+    nbytes = _lib.lib().mdgl_gspmm_workspace_bytes(sched.num_chunks, dout, REDUCERS["sum"],
+                                                     _lib.dtype_code(dtype))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=gdev) if nbytes else None
+    rc = _lib.lib().mdgl_gspmm_mul_sum_dot(
+        csr.indptr.data_ptr(), csr.indices.data_ptr(), csr.eid.data_ptr(), G.data_ptr(),
+        Y.data_ptr(), X.data_ptr(), dx.data_ptr(), dot.data_ptr(), num_rows, dout, dr, dout, nd,
+        ls.ctypes.data, rs.ctypes.data, _lib.ptr(sched.chunk_row), _lib.ptr(sched.chunk_start),
+        sched.num_chunks, sched.chunk_len, _lib.ptr(sched.heavy_rows), _lib.ptr(sched.heavy_ptr),
+        sched.num_heavy, _lib.ptr(ws), nbytes, _lib.dtype_code(dtype), _lib.stream())
+    if rc == _lib.ENOTSUP:
+        return None
+    _lib.check(rc, "gspmm_mul_sum_dot")
+    # the edge gradient came out in CSR slot order: gather it to edge-id order
+    dy = torch.empty((E, dr), dtype=G.dtype, device=gdev)
+    if E:
+        _lib.check(_lib.lib().mdgl_gather_rows(dot.data_ptr(), csr.slot_of_eid().data_ptr(),
+                                               dy.data_ptr(), E, dr, _lib.dtype_code(dtype),
+                                               _lib.stream()), "gather_rows")
+    return dx.reshape(x.shape), dy.reshape(y.shape)
+
+
 def gspmm(g, op, reduce_op, lhs_data, rhs_data):
     r"""Generalized Sparse Matrix Multiplication interface.
     It fuses two steps into one kernel.

@@ -108,6 +108,58 @@ def test_gspmm_backward(op, red, yshape):
     assert_grads(grads(out, [x, y], 3), grads(ref, [x, y], 3))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("xshape,yshape", [((8, 32), (8, 1)), ((4, 16), (4, 1)), ((64,), (1,)),
+                                           ((2, 6), (2, 1)), ((3, 128), (3, 1))],
+                         ids=["wide-8heads", "packed-4heads", "one-group", "unfusable-6",
+                              "slabs-3x128"])
+@pytest.mark.parametrize("red", ["sum", "mean"])
+def test_gspmm_mul_backward_fused_pass(dtype, xshape, yshape, red):
+    """u_mul_e sum / mean with the edge operand constant over x's last axis:
+    both gradients come from one pass over the out-CSR (hubs split into
+    chunks included). dX equals the separate gspmm bit for bit, dY the
+    separate per-head dot to rounding; both against torch autograd in float64
+    (shapes the fused kernel does not take fall back to the separate ops)."""
+    from mojodgl.ops import spmm
+
+    n, e = 300, 5000
+    u, v = graph_with_loops(n, e, 60)
+    u[:1200] = 11  # an out-degree hub (chunked in the out-CSR)
+    E = u.size
+    g = dgl.graph((u, v), num_nodes=n)
+    x = leaf((n,) + xshape, 61, dtype=dtype)
+    y = leaf((E,) + yshape, 62, dtype=dtype)
+    out = ops.gspmm(g, "mul", red, x, y)
+    gx, gy = grads(out, [x, y], 63)
+    x64, y64 = (t.detach().double().requires_grad_(True) for t in (x, y))
+    rx, ry = grads(ref_spmm(u, v, n, "mul", red, x64, y64), [x64, y64], 63)
+    # error bound: tol * the sum of the magnitudes of the terms (a hub's
+    # gradient folds ~1200 products)
+    wabs = torch.randn(out.shape, generator=torch.Generator(device=DEV).manual_seed(63),
+                       device=DEV, dtype=torch.float64).abs()
+    ud, vd = torch.from_numpy(u).to(DEV), torch.from_numpy(v).to(DEV)
+    bx = ref_spmm(v, u, n, "mul", "sum", wabs, y64.detach().abs())
+    by = (x64.detach().abs()[ud] * wabs[vd]).sum(-1, keepdim=True).reshape(ry.shape)
+    tol = 1e-5 if dtype == torch.float32 else 1e-12
+
+    def within(got, ref, bound):
+        assert bool(((got.double() - ref).abs() <= tol * bound + 1e-300).all())
+
+    within(gx, rx, bx.reshape(rx.shape))
+    within(gy, ry, by)
+    if red == "sum":
+        G = torch.randn(out.shape, generator=torch.Generator(device=DEV).manual_seed(63),
+                        device=DEV, dtype=torch.float64).to(dtype)
+        fused = spmm._mul_sum_dot(g, G, y.detach(), x.detach())
+        if xshape[-1] == 6:
+            assert fused is None  # 6 columns per group: not a power-of-two lane count
+        else:
+            dx, dy = fused
+            sep = ops.spmm._run(g, "mul", "sum", G, y.detach(), kind="out")[0]
+            assert torch.equal(dx, sep.reshape(dx.shape))
+            within(dy, ry, by)
+
+
 def test_gspmm_gradcheck():
     n, e = 12, 40
     u, v = graph_with_loops(n, e, 51)
