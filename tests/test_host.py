@@ -245,3 +245,18 @@ def test_softmax_table_slots_of_edges():
                     torch.from_numpy(chunk_first), torch.from_numpy(indptr), torch.from_numpy(eid))
     np.testing.assert_array_equal(t.numpy(), _edge_slots(ordered, chunk_row, chunk_first,
                                                          indptr, eid))
+
+
+def test_fused_backward_takes_trailing_group_operands_only():
+    """The one-pass u_mul_e backward applies when the edge operand is x's
+    feature shape with the last axis collapsed to one."""
+    from mojodgl.ops._autograd import _trailing_groups
+
+    x = torch.zeros(5, 8, 32)
+    assert _trailing_groups(x, torch.zeros(9, 8, 1))
+    assert not _trailing_groups(x, torch.zeros(9, 8, 32))  # elementwise
+    assert not _trailing_groups(x, torch.zeros(9, 1, 1))   # broadcast over heads too
+    assert not _trailing_groups(x, torch.zeros(9, 8))      # other rank
+    assert _trailing_groups(torch.zeros(5, 64), torch.zeros(9, 1))
+    assert _trailing_groups(torch.zeros(5, 64), torch.zeros(9))
+    assert not _trailing_groups(torch.zeros(5, 1), torch.zeros(9, 1))
