@@ -238,6 +238,14 @@ int mdgl_gspmm_edge_grad(const int32_t* vids, const int32_t* indptr, const void*
                          const int32_t* arg_e, void* dst, int64_t num_edges, int64_t d, int mean,
                          double alpha, int dtype, void* stream);
 
+/* mdgl_edge_softmax_grad: dst[e][k] = a[e][k] * (grad[e][k] - row_sum[row_of[e]][k]),
+ *   the last steps of the edge_softmax gradient (a the softmax output, row_sum
+ *   the per-row sums of grad * a over the CSR of norm_by, row_of the
+ *   destination -- or source -- node of every edge id). */
+int mdgl_edge_softmax_grad(const int32_t* row_of, const void* a, const void* grad,
+                           const void* row_sum, void* dst, int64_t num_edges, int64_t d, int dtype,
+                           void* stream);
+
 /* mdgl_gspmm_mul_sum_dot: one pass for both gradients of a u_mul_e_sum whose
  *   edge operand is constant over groups of D = dout / dr consecutive columns
  *   (an edge operand of shape (E, ..., 1) against node rows (N, ..., D)),

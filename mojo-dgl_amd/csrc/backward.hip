@@ -9,7 +9,8 @@
 //                output element receives it) or mean reduction, per edge;
 //   rows_by_degree: y[r, k] = x[r, k] / max(indptr[r + 1] - indptr[r], 1)
 //                (the mean's divisor applied to a node-shaped gradient);
-//   scale:       y = alpha * x (alpha = -1 for the sub / div gradients).
+//   scale:       y = alpha * x (alpha = -1 for the sub / div gradients);
+//   softmax_grad: dx = a * (g - s[row]) (edge_softmax, s the row sums of g * a).
 //
 // One multiply, divide or select per element, so the results are exact
 // functions of the inputs (no order-dependent sums).
@@ -67,7 +68,42 @@ __global__ __launch_bounds__(BLOCK) void scale_kernel(const T* __restrict__ x, T
     y[i] = alpha * x[i];
 }
 
+// dx[e, k] = a[e, k] * (g[e, k] - s[row_of[e], k]): the last two steps of
+// the edge_softmax gradient in one pass (coalesced edge rows, one row of s
+// per edge).
+template <class T>
+__global__ __launch_bounds__(BLOCK) void softmax_grad_kernel(const int32_t* __restrict__ row_of,
+                                                             const T* __restrict__ a,
+                                                             const T* __restrict__ g,
+                                                             const T* __restrict__ s,
+                                                             T* __restrict__ dx, int64_t num_edges,
+                                                             int64_t d) {
+  const int64_t total = num_edges * d;
+  for (int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * BLOCK) {
+    const int64_t e = i / d, k = i % d;
+    const T t = g[i] - s[(int64_t)row_of[e] * d + k];
+    dx[i] = a[i] * t;
+  }
+}
+
 }  // namespace
+
+hipError_t launch_softmax_grad(const int32_t* row_of, const void* a, const void* g,
+                               const void* s, void* dx, int64_t num_edges, int64_t d, int dtype,
+                               hipStream_t st) {
+  const int64_t n = num_edges * d;
+  if (n <= 0) return hipSuccess;
+  if (dtype == 0)
+    hipLaunchKernelGGL(softmax_grad_kernel<float>, dim3(grid_n(n)), dim3(BLOCK), 0, st, row_of,
+                       static_cast<const float*>(a), static_cast<const float*>(g),
+                       static_cast<const float*>(s), static_cast<float*>(dx), num_edges, d);
+  else
+    hipLaunchKernelGGL(softmax_grad_kernel<double>, dim3(grid_n(n)), dim3(BLOCK), 0, st, row_of,
+                       static_cast<const double*>(a), static_cast<const double*>(g),
+                       static_cast<const double*>(s), static_cast<double*>(dx), num_edges, d);
+  return hipGetLastError();
+}
 
 hipError_t launch_edge_grad(const int32_t* vids, const int32_t* indptr, const void* g,
                             const int32_t* arg_e, void* m, int64_t num_edges, int64_t d,

@@ -209,6 +209,20 @@ int mdgl_build_csr(const int32_t* key, const int32_t* other, int64_t num_edges, 
                     "build_csr");
 }
 
+int mdgl_edge_softmax_grad(const int32_t* row_of, const void* a, const void* grad,
+                           const void* row_sum, void* dst, int64_t num_edges, int64_t d, int dtype,
+                           void* stream) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "edge_softmax_grad: bad dtype %d", dtype);
+  if (num_edges < 0 || d < 0) return fail(MDGL_EINVAL, "edge_softmax_grad: negative size");
+  if (num_edges >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "edge_softmax_grad: 2**31 or more edges");
+  if (num_edges == 0 || d == 0) return MDGL_OK;
+  if (!row_of || !a || !grad || !row_sum || !dst)
+    return fail(MDGL_EINVAL, "edge_softmax_grad: null buffer");
+  return hip_status(launch_softmax_grad(row_of, a, grad, row_sum, dst, num_edges, d, dtype,
+                                        (hipStream_t)stream),
+                    "edge_softmax_grad");
+}
+
 int mdgl_gspmm_edge_grad(const int32_t* vids, const int32_t* indptr, const void* grad_out,
                          const int32_t* arg_e, void* dst, int64_t num_edges, int64_t d, int mean,
                          double alpha, int dtype, void* stream) {

@@ -143,6 +143,9 @@ hipError_t launch_clamp_i64(const int64_t* src, int64_t* dst, int64_t n, int64_t
 hipError_t launch_gather_rows(const void* src, const int32_t* idx, void* dst, int64_t n,
                               int64_t width, int dtype, hipStream_t s);
 // Backward helpers (backward.hip).
+hipError_t launch_softmax_grad(const int32_t* row_of, const void* a, const void* g,
+                               const void* s, void* dx, int64_t num_edges, int64_t d, int dtype,
+                               hipStream_t st);
 hipError_t launch_edge_grad(const int32_t* vids, const int32_t* indptr, const void* g,
                             const int32_t* arg_e, void* m, int64_t num_edges, int64_t d,
                             double alpha, int mean, int dtype, hipStream_t s);

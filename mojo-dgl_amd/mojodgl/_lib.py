@@ -90,6 +90,7 @@ _SIGNATURES = {
     "mdgl_rows_by_degree": ([_P, _P, _P, _I64, _I64, _C, _P], _C),
     "mdgl_scale": ([_P, _P, _I64, ctypes.c_double, _C, _P], _C),
     "mdgl_gather_rows": ([_P, _P, _P, _I64, _I64, _C, _P], _C),
+    "mdgl_edge_softmax_grad": ([_P, _P, _P, _P, _P, _I64, _I64, _C, _P], _C),
 }
 
 

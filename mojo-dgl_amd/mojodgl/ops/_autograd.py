@@ -23,8 +23,8 @@ these follow the calculus of the forward ops and run on the same kernels:
   d op / dX (dY) is reduced over the edges of each node of the operand's
   target by a gspmm copy_rhs sum (in-CSR for v, out-CSR for u; nothing for e);
 * edge_softmax: dX = a * (G - s[row]) with s[row] = sum over the row of G * a:
-  gsddmm e_mul_e, gspmm copy_rhs sum over the CSR of norm_by, gsddmm e_sub_v
-  (e_sub_u for norm_by='src'), gsddmm e_mul_e.
+  gsddmm e_mul_e, gspmm copy_rhs sum over the CSR of norm_by, then
+  ``mdgl_edge_softmax_grad`` (the subtraction and product in one pass).
 
 Gradients come back in the operand's shape: an operand broadcast along its
 trailing feature axes gets its gradient summed over them (a segmented sum,
@@ -314,7 +314,12 @@ class EdgeSoftmax(torch.autograd.Function):
         G = grad_out.contiguous().reshape(E, -1)
         p = _gsddmm(g, "mul", G, a2, "e", "e")
         row = "v" if norm_by == "dst" else "u"
-        s = _node_reduce(g, p, row)
-        dlt = _gsddmm(g, "sub", G, s, "e", row)
-        dx = _gsddmm(g, "mul", dlt, a2, "e", "e")
+        s = _node_reduce(g, p, row).contiguous()
+        # dx = a * (G - s[row]) in one pass
+        uids, vids = g._device_coo()
+        a2 = a2.contiguous()
+        dx = torch.empty_like(a2)
+        _lib.check(_lib.lib().mdgl_edge_softmax_grad(
+            (vids if row == "v" else uids).data_ptr(), a2.data_ptr(), G.data_ptr(), s.data_ptr(),
+            dx.data_ptr(), E, a2.shape[1], _code(a2), _lib.stream()), "edge_softmax_grad")
         return None, dx.reshape(a.shape), None

@@ -121,6 +121,14 @@ def test_backward_helper_arguments(lib):
     assert lib.mdgl_scale(None, None, 4, -1.0, 0, None) == -1
     assert lib.mdgl_scale(None, None, 0, -1.0, 0, None) == 0
     assert lib.mdgl_scale(None, None, 4, -1.0, 5, None) == -1
+    assert lib.mdgl_edge_softmax_grad(None, None, None, None, None, 5, 2, 7, None) == -1
+    rc = lib.mdgl_edge_softmax_grad(None, None, None, None, None, 5, 2, 0, None)
+    assert rc == -1 and "null" in err(lib)
+    assert lib.mdgl_edge_softmax_grad(None, None, None, None, None, 0, 2, 0, None) == 0
+    # the fused u_mul_e backward refuses other ops' shapes before launching
+    rc = lib.mdgl_gspmm_mul_sum_dot(1, 1, 1, 1, 1, None, 1, 1, 10, 12, 2, 12, 0, None, None,
+                                    None, None, 0, 0, None, None, 0, None, 0, 0, None)
+    assert rc in (-1, -3)
 
 
 def test_workspace_sizes(lib):
