@@ -223,6 +223,8 @@ def time_gat_backward(g, el, er, h):
     grad = torch.randn(h.shape, device="cuda", generator=gen)
 
     def fb():
+        for t in (el_, er_, h_):
+            t.grad = None  # as an optimizer's zero_grad(set_to_none=True)
         e = torch.nn.functional.leaky_relu(ops.u_add_v(g, el_, er_), 0.2)
         out = ops.u_mul_e_sum(g, h_, ops.edge_softmax(g, e))
         out.backward(grad)
