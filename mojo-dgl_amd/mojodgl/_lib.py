@@ -151,12 +151,20 @@ def device() -> torch.device:
 
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_get_device = getattr(torch._C, "_cuda_getDevice", None)
+
+
+def current_device() -> int:
+    """Index of the current GPU (torch's; cheap once torch's GPU state is up)."""
+    if _get_device is not None and _GPU_SEEN:
+        return _get_device()
+    return torch.cuda.current_device()
 
 
 def stream() -> int:
     """torch's current stream on the current device, as a raw hipStream_t."""
     if _raw_stream is not None:
-        return _raw_stream(torch.cuda.current_device())
+        return _raw_stream(current_device())
     return torch.cuda.current_stream().cuda_stream
 
 
@@ -171,16 +179,13 @@ _TORCH_TO_NP = {torch.float32: np.float32, torch.float64: np.float64}
 class Feat:
     """A validated feature operand: a float32/float64 numpy array or tensor."""
 
-    __slots__ = ("data", "is_torch", "device")
+    __slots__ = ("data", "is_torch", "device", "shape")
 
     def __init__(self, data, is_torch, dev):
         self.data = data
         self.is_torch = is_torch
         self.device = dev
-
-    @property
-    def shape(self):
-        return tuple(self.data.shape)
+        self.shape = tuple(data.shape)
 
     @property
     def dtype(self):
@@ -254,7 +259,7 @@ def on_device(f: Feat, dtype) -> torch.Tensor:
     if f.is_torch:
         t = f.data
         if t.is_cuda and t.dtype == tdt and t.is_contiguous() \
-                and t.get_device() == torch.cuda.current_device():
+                and t.get_device() == current_device():
             return t
     else:
         t = torch.from_numpy(f.data)

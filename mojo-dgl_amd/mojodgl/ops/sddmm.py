@@ -75,6 +75,8 @@ def out_feat_shape(lshape, rshape, dot=False):
         if lf[-1] != rf[-1]:
             raise DGLError("dot needs matching feature widths, {} vs {}".format(lf[-1], rf[-1]))
         lf, rf = lf[:-1], rf[:-1]
+    if lf == rf:
+        return lf + ((1,) if dot else ())
     try:
         out = tuple(np.broadcast_shapes(lf, rf))
     except ValueError:
@@ -82,12 +84,24 @@ def out_feat_shape(lshape, rshape, dot=False):
     return out + ((1,) if dot else ())
 
 
+_SHAPE_ARGS = {}
+
+
 def shape_args(lshape, rshape):
-    """(nd, lhs feature shape, rhs feature shape) host arrays for the C ABI."""
-    lf = np.ascontiguousarray(feat_shape(lshape), dtype=np.int64)
-    rf = np.ascontiguousarray(feat_shape(rshape), dtype=np.int64)
-    assert lf.size == rf.size
-    return int(lf.size), lf, rf
+    """(nd, lhs feature shape, rhs feature shape) host arrays for the C ABI
+    (kept per shape pair: the arrays are only read)."""
+    key = (feat_shape(lshape), feat_shape(rshape))
+    got = _SHAPE_ARGS.get(key)
+    if got is None:
+        lf = np.ascontiguousarray(key[0], dtype=np.int64)
+        rf = np.ascontiguousarray(key[1], dtype=np.int64)
+        assert lf.size == rf.size
+        lf.flags.writeable = False
+        rf.flags.writeable = False
+        got = (int(lf.size), lf, rf)
+        if len(_SHAPE_ARGS) < 4096:
+            _SHAPE_ARGS[key] = got
+    return got
 
 
 def _check_rows(a, want: int, what: str) -> None:

@@ -100,9 +100,11 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
             rhs = perm
             flags |= _lib.RHS_CSR_ORDER
         ws = None
-        nbytes = _lib.lib().mdgl_gspmm_workspace_bytes(sched.num_chunks, dout,
-                                                         REDUCERS[reduce_op],
-                                                         _lib.dtype_code(dtype))
+        nbytes = 0
+        if sched.num_chunks:
+            nbytes = _lib.lib().mdgl_gspmm_workspace_bytes(sched.num_chunks, dout,
+                                                             REDUCERS[reduce_op],
+                                                             _lib.dtype_code(dtype))
         if nbytes:
             ws = torch.empty(nbytes, dtype=torch.uint8, device=gdev)
         rc = _lib.lib().mdgl_gspmm(
