@@ -129,6 +129,27 @@ __global__ __launch_bounds__(BLOCK) void gather_rows_kernel(const T* __restrict_
   }
 }
 
+// The same with 16-byte chunks (width a multiple of the chunk, buffers
+// 16-byte aligned): a chunk per thread, the row found by a shift when the
+// chunks per row are a power of two; the gathered source rows are ordinary
+// loads, the output goes out with streaming stores.
+template <class T, bool POW2>
+__global__ __launch_bounds__(BLOCK) void gather_rows_vec_kernel(const T* __restrict__ src,
+                                                                const int32_t* __restrict__ idx,
+                                                                T* __restrict__ dst, int64_t n,
+                                                                int64_t cpr, int shift) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int64_t total = n * cpr;
+  for (int64_t t = (int64_t)blockIdx.x * BLOCK + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * BLOCK) {
+    const int64_t i = POW2 ? (t >> shift) : t / cpr;
+    const int64_t c = t - i * cpr;
+    T x[VEC];
+    load_n<T, VEC>(src + ((int64_t)idx[i] * cpr + c) * VEC, x);
+    store_n_stream<T, VEC>(dst + t * VEC, x);
+  }
+}
+
 // Segment offsets from lengths (three launches: tile partials, a scan of
 // the tile totals, the tile rewrite). A tile is SEG_TILE lengths, 16
 // consecutive ones per thread. Integer sums are exact, so the offsets equal
@@ -290,8 +311,7 @@ static unsigned grid_for(int64_t n) {
 
 hipError_t launch_replace_inf(const void* src, void* dst, int64_t n, int dtype, hipStream_t s) {
   if (n <= 0) return hipSuccess;
-  const int vec = (reinterpret_cast<uintptr_t>(src) % 16 == 0) &&
-                  (reinterpret_cast<uintptr_t>(dst) % 16 == 0);
+  const int vec = aligned16(src) && aligned16(dst);
   const int64_t per = vec ? (dtype == 0 ? 4 : 2) : 1;
   const unsigned grid = grid_for((n + per - 1) / per);
   if (dtype == 0)
@@ -314,6 +334,24 @@ hipError_t launch_gather_rows(const void* src, const int32_t* idx, void* dst, in
                               int64_t width, int dtype, hipStream_t s) {
   if (n <= 0 || width <= 0) return hipSuccess;
   const int64_t total = n * width;
+  const int64_t vec = dtype == 0 ? 4 : 2;
+  if (width % vec == 0 && aligned16(src) && aligned16(dst)) {
+    const int64_t cpr = width / vec;
+    int shift = 0;
+    while (((int64_t)1 << shift) < cpr) ++shift;
+    const bool pow2 = ((int64_t)1 << shift) == cpr;
+    const dim3 grid(grid_for(n * cpr));
+    if (dtype == 0) {
+      auto* f = pow2 ? gather_rows_vec_kernel<float, true> : gather_rows_vec_kernel<float, false>;
+      hipLaunchKernelGGL(f, grid, dim3(BLOCK), 0, s, static_cast<const float*>(src), idx,
+                         static_cast<float*>(dst), n, cpr, shift);
+    } else {
+      auto* f = pow2 ? gather_rows_vec_kernel<double, true> : gather_rows_vec_kernel<double, false>;
+      hipLaunchKernelGGL(f, grid, dim3(BLOCK), 0, s, static_cast<const double*>(src), idx,
+                         static_cast<double*>(dst), n, cpr, shift);
+    }
+    return hipGetLastError();
+  }
   if (dtype == 0)
     hipLaunchKernelGGL(gather_rows_kernel<float>, dim3(grid_for(total)), dim3(BLOCK), 0, s,
                        static_cast<const float*>(src), idx, static_cast<float*>(dst), n, width);

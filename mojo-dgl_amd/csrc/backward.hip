@@ -87,6 +87,41 @@ __global__ __launch_bounds__(BLOCK) void softmax_grad_kernel(const int32_t* __re
   }
 }
 
+// The same with 16-byte chunks (d a multiple of the chunk, buffers 16-byte
+// aligned): a and g stream in and dx streams out, s is an ordinary load
+// (rows of it are shared by an edge's neighbours in the same row).
+template <class T, bool POW2>
+__global__ __launch_bounds__(BLOCK) void softmax_grad_vec_kernel(
+    const int32_t* __restrict__ row_of, const T* __restrict__ a, const T* __restrict__ g,
+    const T* __restrict__ s, T* __restrict__ dx, int64_t num_edges, int64_t cpr, int shift) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int64_t total = num_edges * cpr;
+  for (int64_t t = (int64_t)blockIdx.x * BLOCK + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * BLOCK) {
+    const int64_t e = POW2 ? (t >> shift) : t / cpr;
+    const int64_t c = t - e * cpr;
+    T av[VEC], gv[VEC], sv[VEC];
+    load_n_stream<T, VEC>(a + t * VEC, av);
+    load_n_stream<T, VEC>(g + t * VEC, gv);
+    load_n<T, VEC>(s + ((int64_t)row_of[e] * cpr + c) * VEC, sv);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) av[v] = av[v] * (gv[v] - sv[v]);
+    store_n_stream<T, VEC>(dx + t * VEC, av);
+  }
+}
+
+template <class T>
+void softmax_grad_vec(const int32_t* row_of, const T* a, const T* g, const T* s, T* dx,
+                      int64_t num_edges, int64_t d, hipStream_t st) {
+  const int64_t cpr = d / (16 / (int64_t)sizeof(T));
+  int shift = 0;
+  while (((int64_t)1 << shift) < cpr) ++shift;
+  auto* f = ((int64_t)1 << shift) == cpr ? softmax_grad_vec_kernel<T, true>
+                                          : softmax_grad_vec_kernel<T, false>;
+  hipLaunchKernelGGL(f, dim3(grid_n(num_edges * cpr)), dim3(BLOCK), 0, st, row_of, a, g, s, dx,
+                     num_edges, cpr, shift);
+}
+
 }  // namespace
 
 hipError_t launch_softmax_grad(const int32_t* row_of, const void* a, const void* g,
@@ -94,6 +129,16 @@ hipError_t launch_softmax_grad(const int32_t* row_of, const void* a, const void*
                                hipStream_t st) {
   const int64_t n = num_edges * d;
   if (n <= 0) return hipSuccess;
+  if (d % (dtype == 0 ? 4 : 2) == 0 && aligned16(a) && aligned16(g) && aligned16(s) &&
+      aligned16(dx)) {
+    if (dtype == 0)
+      softmax_grad_vec(row_of, static_cast<const float*>(a), static_cast<const float*>(g),
+                       static_cast<const float*>(s), static_cast<float*>(dx), num_edges, d, st);
+    else
+      softmax_grad_vec(row_of, static_cast<const double*>(a), static_cast<const double*>(g),
+                       static_cast<const double*>(s), static_cast<double*>(dx), num_edges, d, st);
+    return hipGetLastError();
+  }
   if (dtype == 0)
     hipLaunchKernelGGL(softmax_grad_kernel<float>, dim3(grid_n(n)), dim3(BLOCK), 0, st, row_of,
                        static_cast<const float*>(a), static_cast<const float*>(g),

@@ -123,6 +123,12 @@ __device__ __forceinline__ void store_n(T* p, const T (&in)[N]) {
   *reinterpret_cast<V*>(p) = v;
 }
 
+// True when p sits on a 16-byte boundary (the condition of the 16-byte
+// vector paths).
+__host__ __device__ inline bool aligned16(const void* p) {
+  return reinterpret_cast<uintptr_t>(p) % 16 == 0;
+}
+
 // Streaming (non-temporal) 16-byte store / load: data written or read once,
 // kept from displacing reused lines (gathered rows, node tables) in the
 // caches.

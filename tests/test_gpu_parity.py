@@ -554,6 +554,45 @@ def test_cumsum_clamp_replace_inf_through_the_abi(n):
             np.testing.assert_array_equal(dst.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("width", [1, 2, 3, 4, 6, 8, 12, 16, 33])
+def test_gather_rows_and_softmax_grad_through_the_abi(dtype, width):
+    """mdgl_gather_rows (dst[i] = src[idx[i]]) and mdgl_edge_softmax_grad
+    (a * (g - s[row_of])) against torch indexing and the formula, exact:
+    16-byte aligned buffers (the 16-byte chunk path where the width allows,
+    with chunks per row a power of two or not) and views one element in (the
+    element path)."""
+    from mojodgl import _lib
+
+    L = _lib.lib()
+    code = 0 if dtype == np.float32 else 1
+    tdt = torch.float32 if dtype == np.float32 else torch.float64
+    rng = np.random.default_rng(90 + width)
+    rows, n = 1000, 7001
+    src = torch.from_numpy(rng.normal(size=rows * width + 1).astype(dtype)).cuda()
+    idx = torch.from_numpy(rng.integers(0, rows, n).astype(np.int32)).cuda()
+    out = torch.zeros(n * width + 1, dtype=tdt, device="cuda")
+    for off in (0, 1):
+        s_ = src[off:off + rows * width]
+        o_ = out[off:off + n * width]
+        assert L.mdgl_gather_rows(s_.data_ptr(), idx.data_ptr(), o_.data_ptr(), n, width, code,
+                                  _lib.stream()) == 0
+        want = s_.reshape(rows, width)[idx.long()].reshape(-1)
+        assert torch.equal(o_, want)
+    a = torch.from_numpy(rng.random(n * width + 1).astype(dtype)).cuda()
+    g = torch.from_numpy(rng.normal(size=n * width + 1).astype(dtype)).cuda()
+    for off in (0, 1):
+        a_, g_ = a[off:off + n * width], g[off:off + n * width]
+        s_ = src[off:off + rows * width]
+        o_ = out[off:off + n * width]
+        assert L.mdgl_edge_softmax_grad(idx.data_ptr(), a_.data_ptr(), g_.data_ptr(),
+                                        s_.data_ptr(), o_.data_ptr(), n, width, code,
+                                        _lib.stream()) == 0
+        want = (a_.reshape(n, width) * (g_.reshape(n, width)
+                                        - s_.reshape(rows, width)[idx.long()])).reshape(-1)
+        assert torch.equal(o_, want)
+
+
 # ------------------------------------------------------------------ dense
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("d1,d2,r", [(128, 128, 64), (5, 3, 7), (16, 16, 4), (33, 130, 3),
