@@ -24,7 +24,10 @@ these follow the calculus of the forward ops and run on the same kernels:
   target by a gspmm copy_rhs sum (in-CSR for v, out-CSR for u; nothing for e);
 * edge_softmax: dX = a * (G - s[row]) with s[row] = sum over the row of G * a:
   gsddmm e_mul_e, gspmm copy_rhs sum over the CSR of norm_by, then
-  ``mdgl_edge_softmax_grad`` (the subtraction and product in one pass).
+  ``mdgl_edge_softmax_grad`` (the subtraction and product in one pass); over a
+  subset of eids the rows are the forward's groups of positions (their sums by
+  ``segment_reduce`` after the products are put in group order), and the rows
+  past the selection, constant zero, get zero.
 
 Gradients come back in the operand's shape: an operand broadcast along its
 trailing feature axes gets its gradient summed over them (a segmented sum,
@@ -295,13 +298,48 @@ class GSDDMM(torch.autograd.Function):
         return None, None, dx, dy, None, None
 
 
+def _subset_softmax_grad(grouping, a, grad_out):
+    """Gradient of edge_softmax over a subset of eids: position i < k (the
+    selection's length) belongs to the group of its endpoint, so
+    dx[i] = a[i] * (G[i] - s[endpoint i]) with s the per-group sums of G * a
+    (folded in the group's order of appearance); rows past k are zero."""
+    L = a.shape[0]
+    a2 = a.reshape(L, -1)
+    d = a2.shape[1]
+    dx = torch.zeros_like(a2)
+    endpoint = grouping.get("endpoint")
+    if endpoint is None or endpoint.numel() == 0 or d == 0:
+        return dx.reshape(a.shape)
+    k = endpoint.numel()
+    indptr, eid = grouping["indptr"], grouping["eid"]
+    ak = a2[:k]
+    gk = grad_out.contiguous().reshape(L, -1)[:k]
+    code, st, lib = _code(a2), _lib.stream(), _lib.lib()
+    p = torch.empty_like(ak)
+    _lib.check(lib.mdgl_gsddmm(None, None, gk.data_ptr(), ak.data_ptr(), p.data_ptr(), k,
+                               _lib.TARGETS["e"], _lib.TARGETS["e"], _lib.BINARY_OPS["mul"], d,
+                               d, d, 0, None, None, code, st), "gsddmm")
+    pg = torch.empty_like(p)
+    _lib.check(lib.mdgl_gather_rows(p.data_ptr(), eid.data_ptr(), pg.data_ptr(), k, d, code, st),
+               "gather_rows")
+    rows = indptr.numel() - 1
+    s = torch.empty((rows, d), dtype=a2.dtype, device=a2.device)
+    _lib.check(lib.mdgl_segment_reduce(indptr.data_ptr(), pg.data_ptr(), s.data_ptr(), rows, d,
+                                       _lib.REDUCERS["sum"], k, 0, code, st), "segment_reduce")
+    _lib.check(lib.mdgl_edge_softmax_grad(endpoint.data_ptr(), ak.data_ptr(), gk.data_ptr(),
+                                          s.data_ptr(), dx.data_ptr(), k, d, code, st),
+               "edge_softmax_grad")
+    return dx.reshape(a.shape)
+
+
 class EdgeSoftmax(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, g, logits, norm_by):
+    def forward(ctx, g, logits, norm_by, eids=None):
         from .edge_softmax import _edge_softmax
 
-        out = _edge_softmax(g, logits, None, norm_by)
-        ctx.g, ctx.norm_by = g, norm_by
+        keep = None if eids is None else {}
+        out = _edge_softmax(g, logits, eids, norm_by, keep)
+        ctx.g, ctx.norm_by, ctx.grouping = g, norm_by, keep
         ctx.save_for_backward(out)
         return out
 
@@ -309,6 +347,8 @@ class EdgeSoftmax(torch.autograd.Function):
     def backward(ctx, grad_out):
         g, norm_by = ctx.g, ctx.norm_by
         (a,) = ctx.saved_tensors
+        if ctx.grouping is not None:
+            return None, _subset_softmax_grad(ctx.grouping, a, grad_out), None, None
         E = a.shape[0]
         a2 = a.reshape(E, -1)
         G = grad_out.contiguous().reshape(E, -1)
@@ -322,4 +362,4 @@ class EdgeSoftmax(torch.autograd.Function):
         _lib.check(_lib.lib().mdgl_edge_softmax_grad(
             (vids if row == "v" else uids).data_ptr(), a2.data_ptr(), G.data_ptr(), s.data_ptr(),
             dx.data_ptr(), E, a2.shape[1], _code(a2), _lib.stream()), "edge_softmax_grad")
-        return None, dx.reshape(a.shape), None
+        return None, dx.reshape(a.shape), None, None

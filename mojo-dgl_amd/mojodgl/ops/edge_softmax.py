@@ -44,7 +44,8 @@ def edge_softmax(graph, logits, eids=ALL, norm_by="dst"):
     Returns
     -------
     Softmax values, of the same shape as ``logits``. With a torch tensor that
-    requires grad (and eids=ALL) the result takes part in autograd.
+    requires grad the result takes part in autograd (with a subset ``eids``
+    the rows past len(eids) are constant zero and get no gradient).
 
     Examples
     --------
@@ -58,17 +59,18 @@ def edge_softmax(graph, logits, eids=ALL, norm_by="dst"):
            [0.33333333]])
     """
     if _autograd.needs_grad(logits):
-        if not is_all(eids):
-            raise DGLError("backward through edge_softmax over a subset of eids is not "
-                           "supported; pass eids=ALL")
         if norm_by not in ("dst", "src"):
             raise DGLError("norm_by must be 'src' or 'dst'")
-        return _autograd.EdgeSoftmax.apply(graph, logits, norm_by)
+        return _autograd.EdgeSoftmax.apply(graph, logits, norm_by,
+                                           None if is_all(eids) else eids)
     return _edge_softmax(graph, logits, eids, norm_by)
 
 
-def _edge_softmax(graph, logits, eids, norm_by):
-    """edge_softmax without autograd (`eids` None or ALL means every edge)."""
+def _edge_softmax(graph, logits, eids, norm_by, keep=None):
+    """edge_softmax without autograd (`eids` None or ALL means every edge).
+    With a subset and a dict `keep`, the grouping of the selected positions
+    is left in it for the backward: `endpoint` (int32 node of each position),
+    `indptr` / `eid` (positions grouped by node, in order of appearance)."""
     if eids is None:
         eids = ALL
     num_edges = graph.number_of_edges()
@@ -128,6 +130,8 @@ def _edge_softmax(graph, logits, eids, norm_by):
             idx = order if isinstance(order, torch.Tensor) else torch.from_numpy(order).to(gdev)
             endpoint = (vids if norm_by == "dst" else uids)[idx]
             indptr, _, eid = heterograph.build_device_csr(endpoint, None, num_nodes)
+            if keep is not None:
+                keep.update(endpoint=endpoint, indptr=indptr, eid=eid)
             rows = num_nodes if idx.shape[0] else 0
             plan = _plan.SoftmaxPlan.from_device(indptr, slots, chunk_len, ordered=True,
                                                  eid=eid)

@@ -239,12 +239,45 @@ def test_edge_softmax_backward(norm_by, shape):
     assert torch.autograd.gradcheck(lambda t: ops.edge_softmax(gs, t, norm_by=norm_by), (z,))
 
 
-def test_edge_softmax_subset_backward_is_refused():
-    u, v = graph_with_loops(10, 30, 56)
-    g = dgl.graph((u, v), num_nodes=10)
-    z = leaf((u.size, 1), 17)
-    with pytest.raises(dgl.DGLError):
-        ops.edge_softmax(g, z, eids=np.arange(5))
+@pytest.mark.parametrize("norm_by", ["dst", "src"])
+@pytest.mark.parametrize("sel", ["every-third", "repeats", "all-in-order", "empty"])
+def test_edge_softmax_subset_backward(norm_by, sel):
+    """edge_softmax over a subset of eids (the positional rule: position i
+    belongs to the group of eids[i]'s endpoint, rows past len(eids) are zero):
+    values and gradients against the float64 restatement applied to the
+    selected positions, zero gradient past the selection; with every edge in
+    order the gradient equals the eids=ALL one bit for bit; finite differences
+    on a small graph."""
+    n, e = 70, 900
+    u, v = graph_with_loops(n, e, 58)
+    g = dgl.graph((u, v), num_nodes=n)
+    E = u.size
+    rng = np.random.default_rng(59)
+    eids = {"every-third": np.arange(0, E, 3),
+            "repeats": rng.integers(0, E, E // 2),
+            "all-in-order": np.arange(E),
+            "empty": np.arange(0)}[sel]
+    k = eids.size
+    logits = leaf((E, 4, 1), 23)
+    out = ops.edge_softmax(g, logits, eids=eids, norm_by=norm_by)
+    if k:
+        ref = ref_edge_softmax(u[eids], v[eids], n, logits[:k], norm_by)
+    else:
+        ref = logits[:0] * 0
+    ref = torch.cat([ref, logits[k:] * 0])
+    torch.testing.assert_close(out, ref, rtol=1e-12, atol=1e-14)
+    got = grads(out, [logits], 24)
+    assert_grads(got, grads(ref, [logits], 24))
+    assert torch.count_nonzero(got[0][k:]) == 0
+    if sel == "all-in-order":
+        full = ops.edge_softmax(g, logits, norm_by=norm_by)
+        assert torch.equal(got[0], grads(full, [logits], 24)[0])
+    small_u, small_v = graph_with_loops(10, 30, 60)
+    gs = dgl.graph((small_u, small_v), num_nodes=10)
+    z = leaf((small_u.size, 2, 1), 25)
+    sub = np.arange(0, small_u.size, 2)[::-1].copy()
+    assert torch.autograd.gradcheck(
+        lambda t: ops.edge_softmax(gs, t, eids=sub, norm_by=norm_by), (z,))
 
 
 # ------------------------------------------------------------------ a GAT layer, float32
