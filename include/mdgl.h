@@ -129,6 +129,20 @@ int64_t mdgl_gspmm_workspace_bytes(int64_t num_chunks, int64_t dout, int reduce_
 int mdgl_segment_reduce(const int32_t* offsets, const void* value, void* dst, int64_t num_seg,
                         int64_t d, int reduce_op, int64_t n, int flags, int dtype, void* stream);
 
+/* mdgl_segment_reduce for max / min that also writes arg[s][k] (int32), the
+ * row of the selected value: the first in row order among equal values, NaN
+ * never selected, 0 for an empty segment. No counterpart in the reference
+ * (it emits no arg); the gradient of segment max / min flows to that row. */
+int mdgl_segment_reduce_arg(const int32_t* offsets, const void* value, void* dst, int32_t* arg,
+                            int64_t num_seg, int64_t d, int reduce_op, int64_t n, int flags,
+                            int dtype, void* stream);
+
+/* dst[i] (int32) = the segment holding row i, for the n rows of the segments
+ * offsets[0..num_seg] (non-decreasing, 0 to n). No counterpart in the
+ * reference: the row -> segment map of the segment gradients. */
+int mdgl_segment_ids(const int32_t* offsets, int64_t num_seg, int64_t n, int32_t* dst,
+                     void* stream);
+
 /* Softmax planning. A softmax call serves rows by degree, with a lane layout
  * that depends on d, the dtype and the 16-byte alignment of the two buffers:
  * `slots` edge slots per wavefront. Rows of up to `chunk_len` (= 8 * slots)

@@ -150,6 +150,25 @@ __global__ __launch_bounds__(BLOCK) void gather_rows_vec_kernel(const T* __restr
   }
 }
 
+// dst[i] = the segment holding row i: the last s with offsets[s] <= i, by a
+// binary search over offsets[0 .. num_seg) (empty segments share their
+// offset with the next one and are passed over). The search stays inside
+// the offsets whatever they hold.
+__global__ __launch_bounds__(BLOCK) void segment_ids_kernel(const int32_t* __restrict__ offsets,
+                                                            int64_t num_seg, int64_t n,
+                                                            int32_t* __restrict__ dst) {
+  for (int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * BLOCK) {
+    int64_t lo = 0, hi = num_seg - 1;
+    while (lo < hi) {
+      const int64_t mid = lo + (hi - lo + 1) / 2;
+      if (offsets[mid] <= i) lo = mid;
+      else hi = mid - 1;
+    }
+    dst[i] = (int32_t)lo;
+  }
+}
+
 // Segment offsets from lengths (three launches: tile partials, a scan of
 // the tile totals, the tile rewrite). A tile is SEG_TILE lengths, 16
 // consecutive ones per thread. Integer sums are exact, so the offsets equal
@@ -358,6 +377,14 @@ hipError_t launch_gather_rows(const void* src, const int32_t* idx, void* dst, in
   else
     hipLaunchKernelGGL(gather_rows_kernel<double>, dim3(grid_for(total)), dim3(BLOCK), 0, s,
                        static_cast<const double*>(src), idx, static_cast<double*>(dst), n, width);
+  return hipGetLastError();
+}
+
+hipError_t launch_segment_ids(const int32_t* offsets, int64_t num_seg, int64_t n, int32_t* dst,
+                              hipStream_t s) {
+  if (n <= 0 || num_seg <= 0) return hipSuccess;
+  hipLaunchKernelGGL(segment_ids_kernel, dim3(grid_for(n)), dim3(BLOCK), 0, s, offsets, num_seg, n,
+                     dst);
   return hipGetLastError();
 }
 

@@ -573,6 +573,37 @@ int mdgl_segment_reduce(const int32_t* offsets, const void* value, void* dst, in
                       0, 0, nullptr, nullptr, 0, nullptr, 0, flags, dtype, stream, true);
 }
 
+int mdgl_segment_reduce_arg(const int32_t* offsets, const void* value, void* dst, int32_t* arg,
+                            int64_t num_seg, int64_t d, int reduce_op, int64_t n, int flags,
+                            int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "segment_reduce_arg: bad dtype %d", dtype);
+  if (reduce_op != RED_MAX && reduce_op != RED_MIN)
+    return fail(MDGL_EINVAL, "segment_reduce_arg: reduce_op must be max or min, got %d", reduce_op);
+  if (num_seg < 0 || d < 0 || n < 0) return fail(MDGL_EINVAL, "segment_reduce_arg: negative size");
+  if (num_seg >= (int64_t(1) << 31) || n >= (int64_t(1) << 31))
+    return fail(MDGL_EINVAL, "segment_reduce_arg: 2**31 or more segments or rows");
+  if (!row_widths_fit(d, dsize(dtype)))
+    return fail(MDGL_EINVAL, "segment_reduce_arg: rows too wide");
+  if (num_seg == 0 || d == 0) return MDGL_OK;
+  if (!offsets || !dst || !arg || (n > 0 && !value))
+    return fail(MDGL_EINVAL, "segment_reduce_arg: null buffer");
+  return gspmm_common(offsets, nullptr, nullptr, value, value, dst, num_seg, OP_COPY_RHS, d, d, d,
+                      reduce_op, nullptr, 0, nullptr, nullptr, nullptr, arg, nullptr, nullptr, 0,
+                      0, nullptr, nullptr, 0, nullptr, 0, flags, dtype, stream, true);
+}
+
+int mdgl_segment_ids(const int32_t* offsets, int64_t num_seg, int64_t n, int32_t* dst,
+                     void* stream) {
+  if (num_seg < 0 || n < 0) return fail(MDGL_EINVAL, "segment_ids: negative size");
+  if (num_seg >= (int64_t(1) << 31) || n >= (int64_t(1) << 31))
+    return fail(MDGL_EINVAL, "segment_ids: 2**31 or more segments or rows");
+  if (n == 0) return MDGL_OK;
+  if (num_seg == 0) return fail(MDGL_EINVAL, "segment_ids: %lld rows and no segments", (long long)n);
+  if (!offsets || !dst) return fail(MDGL_EINVAL, "segment_ids: null buffer");
+  return hip_status(launch_segment_ids(offsets, num_seg, n, dst, (hipStream_t)stream),
+                    "segment_ids");
+}
+
 // Softmax geometry for (d, dtype) and the two buffers: the vector width
 // follows d and the buffers' alignment, the lane layout follows the width.
 static void softmax_geom(int64_t d, int dtype, const void* logits, const void* out, int* vec,

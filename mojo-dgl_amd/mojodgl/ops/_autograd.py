@@ -27,7 +27,11 @@ these follow the calculus of the forward ops and run on the same kernels:
   ``mdgl_edge_softmax_grad`` (the subtraction and product in one pass); over a
   subset of eids the rows are the forward's groups of positions (their sums by
   ``segment_reduce`` after the products are put in group order), and the rows
-  past the selection, constant zero, get zero.
+  past the selection, constant zero, get zero;
+* segment_reduce / segment_softmax: the segments are CSR rows over the value
+  rows themselves (``mdgl_segment_ids`` maps rows to segments): sum / mean /
+  max / min as gspmm copy_rhs (max / min through the arg row of
+  ``mdgl_segment_reduce_arg``), softmax as edge_softmax.
 
 Gradients come back in the operand's shape: an operand broadcast along its
 trailing feature axes gets its gradient summed over them (a segmented sum,
@@ -43,7 +47,7 @@ import torch
 from .. import _lib
 from ..base import DGLError
 
-__all__ = ["needs_grad", "GSpMM", "GSDDMM", "EdgeSoftmax"]
+__all__ = ["needs_grad", "GSpMM", "GSDDMM", "EdgeSoftmax", "SegmentReduce", "SegmentSoftmax"]
 
 
 def needs_grad(*xs) -> bool:
@@ -298,6 +302,33 @@ class GSDDMM(torch.autograd.Function):
         return None, None, dx, dy, None, None
 
 
+def _group_softmax_grad(y, g, row_of, offsets, num_groups, order=None, out=None):
+    """dx = y * (g - s[row_of]) for a softmax over groups of rows (y its
+    output, g the output gradient, both (k, d) contiguous on the GPU): s[r] is
+    the sum of g * y over group r, whose rows are order[offsets[r] ..
+    offsets[r + 1]) (int32 positions; None: the rows themselves, groups
+    contiguous), folded in that order. Written into `out` when given."""
+    k, d = y.shape
+    code, st, lib = _code(y), _lib.stream(), _lib.lib()
+    p = torch.empty_like(y)
+    _lib.check(lib.mdgl_gsddmm(None, None, g.data_ptr(), y.data_ptr(), p.data_ptr(), k,
+                               _lib.TARGETS["e"], _lib.TARGETS["e"], _lib.BINARY_OPS["mul"], d,
+                               d, d, 0, None, None, code, st), "gsddmm")
+    if order is not None:
+        pg = torch.empty_like(p)
+        _lib.check(lib.mdgl_gather_rows(p.data_ptr(), order.data_ptr(), pg.data_ptr(), k, d, code,
+                                        st), "gather_rows")
+        p = pg
+    s = torch.empty((num_groups, d), dtype=y.dtype, device=y.device)
+    _lib.check(lib.mdgl_segment_reduce(offsets.data_ptr(), p.data_ptr(), s.data_ptr(), num_groups,
+                                       d, _lib.REDUCERS["sum"], k, 0, code, st), "segment_reduce")
+    dx = torch.empty_like(y) if out is None else out
+    _lib.check(lib.mdgl_edge_softmax_grad(row_of.data_ptr(), y.data_ptr(), g.data_ptr(),
+                                          s.data_ptr(), dx.data_ptr(), k, d, code, st),
+               "edge_softmax_grad")
+    return dx
+
+
 def _subset_softmax_grad(grouping, a, grad_out):
     """Gradient of edge_softmax over a subset of eids: position i < k (the
     selection's length) belongs to the group of its endpoint, so
@@ -311,25 +342,84 @@ def _subset_softmax_grad(grouping, a, grad_out):
     if endpoint is None or endpoint.numel() == 0 or d == 0:
         return dx.reshape(a.shape)
     k = endpoint.numel()
-    indptr, eid = grouping["indptr"], grouping["eid"]
-    ak = a2[:k]
+    indptr = grouping["indptr"]
     gk = grad_out.contiguous().reshape(L, -1)[:k]
-    code, st, lib = _code(a2), _lib.stream(), _lib.lib()
-    p = torch.empty_like(ak)
-    _lib.check(lib.mdgl_gsddmm(None, None, gk.data_ptr(), ak.data_ptr(), p.data_ptr(), k,
-                               _lib.TARGETS["e"], _lib.TARGETS["e"], _lib.BINARY_OPS["mul"], d,
-                               d, d, 0, None, None, code, st), "gsddmm")
-    pg = torch.empty_like(p)
-    _lib.check(lib.mdgl_gather_rows(p.data_ptr(), eid.data_ptr(), pg.data_ptr(), k, d, code, st),
-               "gather_rows")
-    rows = indptr.numel() - 1
-    s = torch.empty((rows, d), dtype=a2.dtype, device=a2.device)
-    _lib.check(lib.mdgl_segment_reduce(indptr.data_ptr(), pg.data_ptr(), s.data_ptr(), rows, d,
-                                       _lib.REDUCERS["sum"], k, 0, code, st), "segment_reduce")
-    _lib.check(lib.mdgl_edge_softmax_grad(endpoint.data_ptr(), ak.data_ptr(), gk.data_ptr(),
-                                          s.data_ptr(), dx.data_ptr(), k, d, code, st),
-               "edge_softmax_grad")
+    _group_softmax_grad(a2[:k], gk, endpoint, indptr, indptr.numel() - 1,
+                        order=grouping["eid"], out=dx[:k])
     return dx.reshape(a.shape)
+
+
+def _segment_ids(seg, n):
+    """int32 segment of each of the n rows of validated segments `seg`."""
+    off = seg.device()
+    ids = torch.empty(n, dtype=torch.int32, device=off.device)
+    _lib.check(_lib.lib().mdgl_segment_ids(off.data_ptr(), seg.num, n, ids.data_ptr(),
+                                           _lib.stream()), "segment_ids")
+    return ids
+
+
+def _flat(shape):
+    return 1 if len(shape) < 2 else int(np.prod(shape[1:], dtype=np.int64))
+
+
+class SegmentReduce(torch.autograd.Function):
+    """segment_reduce with a gradient: row i of segment s receives dout[s]
+    (sum), dout[s] / max(len s, 1) (mean), or dout[s][k] when it is the row
+    max / min selected for column k (``mdgl_segment_reduce_arg``), through
+    ``mdgl_gspmm_edge_grad`` with the segments as CSR rows."""
+
+    @staticmethod
+    def forward(ctx, seglen, value, reducer):
+        from .segment import _segment_reduce
+
+        out, seg, arg = _segment_reduce(seglen, value, reducer, want_arg=True)
+        ctx.seg, ctx.arg, ctx.reducer = seg, arg, reducer
+        ctx.vshape, ctx.vdev = tuple(value.shape), value.device
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        seg, vshape = ctx.seg, ctx.vshape
+        n = vshape[0] if len(vshape) else 0
+        d = _flat(vshape)
+        gdev = _lib.device()
+        dv = torch.zeros((n, d), dtype=grad_out.dtype, device=gdev)
+        if n and d and seg.num:
+            G = grad_out.to(gdev).contiguous().reshape(seg.num, d)
+            ids = _segment_ids(seg, n)
+            _lib.check(_lib.lib().mdgl_gspmm_edge_grad(
+                ids.data_ptr(), seg.device().data_ptr(), G.data_ptr(), _lib.ptr(ctx.arg),
+                dv.data_ptr(), n, d, 1 if ctx.reducer == "mean" else 0, 1.0, _code(G),
+                _lib.stream()), "gspmm_edge_grad")
+        return None, dv.reshape(vshape).to(ctx.vdev), None
+
+
+class SegmentSoftmax(torch.autograd.Function):
+    """segment_softmax with a gradient: dx = y * (g - s[segment]) with s the
+    per-segment sums of g * y (rows in order)."""
+
+    @staticmethod
+    def forward(ctx, seglen, value):
+        from .segment import _segment_softmax
+
+        out, seg = _segment_softmax(seglen, value)
+        ctx.seg, ctx.vdev = seg, value.device
+        ctx.save_for_backward(out)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        (y,) = ctx.saved_tensors
+        seg, shape = ctx.seg, tuple(y.shape)
+        n = shape[0] if len(shape) else 0
+        d = _flat(shape)
+        gdev = _lib.device()
+        dx = torch.zeros((n, d), dtype=y.dtype, device=gdev)
+        if n and d and seg.num:
+            Y = y.to(gdev).contiguous().reshape(n, d)
+            G = grad_out.to(gdev).contiguous().reshape(n, d)
+            dx = _group_softmax_grad(Y, G, _segment_ids(seg, n), seg.device(), seg.num)
+        return None, dx.reshape(shape).to(ctx.vdev)
 
 
 class EdgeSoftmax(torch.autograd.Function):

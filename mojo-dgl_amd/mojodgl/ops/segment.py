@@ -16,7 +16,7 @@ import torch
 from .. import _lib
 from .._lib import REDUCERS
 from ..base import DGLError
-from . import _plan
+from . import _autograd, _plan
 
 __all__ = ["segment_reduce", "segment_softmax", "segment_mm"]
 
@@ -104,6 +104,8 @@ def segment_reduce(seglen, value, reducer="sum"):
     -------
     Aggregated values of shape ``(len(seglen), value.shape[1:])`` (a 1-D value
     gives ``(len(seglen), 1)``). Empty segments give 0 for every reducer.
+    With a torch tensor that requires grad the result takes part in autograd
+    (max / min pass the gradient to the selected row).
 
     Examples
     --------
@@ -115,9 +117,17 @@ def segment_reduce(seglen, value, reducer="sum"):
            [5., 5., 5.],
            [4., 4., 4.]])
     """
-    V = _lib.feature(value)
     if reducer not in ("sum", "max", "min", "mean"):
         raise DGLError("reducer {} not recognized.".format(reducer))
+    if _autograd.needs_grad(value):
+        return _autograd.SegmentReduce.apply(seglen, value, reducer)
+    return _segment_reduce(seglen, value, reducer)[0]
+
+
+def _segment_reduce(seglen, value, reducer, want_arg=False):
+    """segment_reduce returning (result, validated segments, arg): arg is the
+    (num_seg, d) int32 row of each max / min with `want_arg`, else None."""
+    V = _lib.feature(value)
     n = V.shape[0] if V.ndim else 0
     seg = _Segments(seglen, n)
     d = _flat_width(V.shape)
@@ -126,15 +136,23 @@ def segment_reduce(seglen, value, reducer="sum"):
     dtype = V.dtype
     gdev = _lib.device()
     out = torch.empty((num_seg, d), dtype=_lib.torch_dtype(dtype), device=gdev)
+    arg = None
     if num_seg and d:
         val = _lib.on_device(V, dtype)
         off = seg.device()
         flags = _lib.REPLACE_INF if reducer in ("max", "min") else 0
-        rc = _lib.lib().mdgl_segment_reduce(off.data_ptr(), val.data_ptr(), out.data_ptr(),
-                                            num_seg, d, REDUCERS[reducer], n, flags,
-                                            _lib.dtype_code(dtype), _lib.stream())
+        if want_arg and reducer in ("max", "min"):
+            arg = torch.empty((num_seg, d), dtype=torch.int32, device=gdev)
+            rc = _lib.lib().mdgl_segment_reduce_arg(off.data_ptr(), val.data_ptr(),
+                                                    out.data_ptr(), arg.data_ptr(), num_seg, d,
+                                                    REDUCERS[reducer], n, flags,
+                                                    _lib.dtype_code(dtype), _lib.stream())
+        else:
+            rc = _lib.lib().mdgl_segment_reduce(off.data_ptr(), val.data_ptr(), out.data_ptr(),
+                                                num_seg, d, REDUCERS[reducer], n, flags,
+                                                _lib.dtype_code(dtype), _lib.stream())
         _lib.check(rc, "segment_reduce")
-    return _lib.give_back(out.reshape((num_seg,) + fshape), V.is_torch, V.device)
+    return _lib.give_back(out.reshape((num_seg,) + fshape), V.is_torch, V.device), seg, arg
 
 
 def segment_softmax(seglen, value):
@@ -146,8 +164,16 @@ def segment_softmax(seglen, value):
 
     Returns
     -------
-    Result of the same shape as ``value``.
+    Result of the same shape as ``value``. With a torch tensor that requires
+    grad the result takes part in autograd.
     """
+    if _autograd.needs_grad(value):
+        return _autograd.SegmentSoftmax.apply(seglen, value)
+    return _segment_softmax(seglen, value)[0]
+
+
+def _segment_softmax(seglen, value):
+    """segment_softmax returning (result, validated segments)."""
     V = _lib.feature(value)
     shape = V.shape
     n = shape[0] if len(shape) else 0
@@ -183,7 +209,7 @@ def segment_softmax(seglen, value):
             plan.num_chunks, plan.slots, _lib.ptr(ws), nbytes, _lib.dtype_code(dtype),
             _lib.stream())
         _lib.check(rc, "segment_softmax")
-    return _lib.give_back(out.reshape(shape), V.is_torch, V.device)
+    return _lib.give_back(out.reshape(shape), V.is_torch, V.device), seg
 
 
 def _grouped_mm(a, b, idx_b, seglen, gather, covered):

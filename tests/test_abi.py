@@ -125,6 +125,18 @@ def test_backward_helper_arguments(lib):
     rc = lib.mdgl_edge_softmax_grad(None, None, None, None, None, 5, 2, 0, None)
     assert rc == -1 and "null" in err(lib)
     assert lib.mdgl_edge_softmax_grad(None, None, None, None, None, 0, 2, 0, None) == 0
+    # segment gradients: the row -> segment map and max / min with their rows
+    assert lib.mdgl_segment_ids(None, -1, 4, None, None) == -1
+    rc = lib.mdgl_segment_ids(None, 0, 4, None, None)
+    assert rc == -1 and "no segments" in err(lib)
+    rc = lib.mdgl_segment_ids(None, 2, 4, None, None)
+    assert rc == -1 and "null" in err(lib)
+    assert lib.mdgl_segment_ids(None, 0, 0, None, None) == 0
+    rc = lib.mdgl_segment_reduce_arg(None, None, None, None, 3, 2, 0, 6, 0, 0, None)
+    assert rc == -1 and "max or min" in err(lib)
+    rc = lib.mdgl_segment_reduce_arg(1, 1, 1, None, 3, 2, 1, 6, 0, 0, None)
+    assert rc == -1 and "null" in err(lib)
+    assert lib.mdgl_segment_reduce_arg(None, None, None, None, 0, 2, 2, 0, 0, 0, None) == 0
     # the fused u_mul_e backward refuses other ops' shapes before launching
     rc = lib.mdgl_gspmm_mul_sum_dot(1, 1, 1, 1, 1, None, 1, 1, 10, 12, 2, 12, 0, None, None,
                                     None, None, 0, 0, None, None, 0, None, 0, 0, None)

@@ -1,4 +1,5 @@
-"""Backward passes of gspmm / gsddmm / edge_softmax on the GPU.
+"""Backward passes of gspmm / gsddmm / edge_softmax / segment_reduce /
+segment_softmax on the GPU.
 
 The reference has no backward (README.md:110-114), so there is no oracle
 vector to match; the gradients are pinned by the mathematics instead:
@@ -278,6 +279,80 @@ def test_edge_softmax_subset_backward(norm_by, sel):
     sub = np.arange(0, small_u.size, 2)[::-1].copy()
     assert torch.autograd.gradcheck(
         lambda t: ops.edge_softmax(gs, t, eids=sub, norm_by=norm_by), (z,))
+
+
+# ------------------------------------------------------------------ segments
+SEGLEN = [3, 0, 1, 7, 0, 2, 40, 5, 0, 1, 600, 4]
+
+
+def ref_segment_ids(seglen):
+    sl = torch.as_tensor(seglen, device=DEV)
+    return torch.repeat_interleave(torch.arange(len(seglen), device=DEV), sl)
+
+
+def ref_segment_reduce(seglen, value, reducer):
+    ids = ref_segment_ids(seglen)
+    flat = value.reshape(value.shape[0], -1)
+    S, d = len(seglen), flat.shape[1]
+    if reducer in ("sum", "mean"):
+        out = torch.zeros((S, d), dtype=flat.dtype, device=DEV).index_add(0, ids, flat)
+        if reducer == "mean":
+            cnt = torch.as_tensor(seglen, device=DEV).clamp(min=1).to(flat.dtype)
+            out = out / cnt[:, None]
+    else:
+        init = -float("inf") if reducer == "max" else float("inf")
+        out = torch.full((S, d), init, dtype=flat.dtype, device=DEV)
+        out = out.scatter_reduce(0, ids[:, None].expand_as(flat), flat,
+                                 "amax" if reducer == "max" else "amin", include_self=True)
+        out = torch.where(torch.isinf(out), torch.zeros_like(out), out)
+    return out.reshape((S,) + (tuple(value.shape[1:]) if value.dim() > 1 else (1,)))
+
+
+def ref_segment_softmax(seglen, value):
+    ids = ref_segment_ids(seglen)
+    flat = value.reshape(value.shape[0], -1)
+    S = len(seglen)
+    mx = torch.full((S, flat.shape[1]), -float("inf"), dtype=flat.dtype, device=DEV)
+    mx = mx.scatter_reduce(0, ids[:, None].expand_as(flat), flat, "amax", include_self=True)
+    ex = torch.exp(flat - mx[ids])
+    s = torch.zeros((S, flat.shape[1]), dtype=flat.dtype, device=DEV).index_add(0, ids, ex)
+    return (ex / s[ids]).reshape(value.shape)
+
+
+@pytest.mark.parametrize("reducer", ["sum", "mean", "max", "min"])
+@pytest.mark.parametrize("shape", [(3, 2), ()], ids=["rows-3x2", "1-D"])
+@pytest.mark.parametrize("lengths_on", ["host", "gpu"])
+def test_segment_reduce_backward(reducer, shape, lengths_on):
+    """segment_reduce gradients (sum, mean, max / min through the selected
+    row, empty segments included) against torch autograd through the float64
+    restatement, and finite differences."""
+    n = sum(SEGLEN)
+    seglen = SEGLEN if lengths_on == "host" else torch.tensor(SEGLEN, device=DEV)
+    value = leaf((n,) + shape, 26)
+    out = ops.segment_reduce(seglen, value, reducer)
+    ref = ref_segment_reduce(SEGLEN, value, reducer)
+    torch.testing.assert_close(out, ref, rtol=1e-12, atol=1e-12)
+    assert_grads(grads(out, [value], 27), grads(ref, [value], 27))
+    small = [2, 0, 3, 1]
+    z = leaf((sum(small), 2), 28)
+    assert torch.autograd.gradcheck(lambda t: ops.segment_reduce(small, t, reducer), (z,))
+
+
+@pytest.mark.parametrize("shape", [(4,), (2, 3), ()], ids=["rows-4", "rows-2x3", "1-D"])
+@pytest.mark.parametrize("lengths_on", ["host", "gpu"])
+def test_segment_softmax_backward(shape, lengths_on):
+    """segment_softmax gradient against torch autograd through the float64
+    restatement (a 600-row segment included) and finite differences."""
+    n = sum(SEGLEN)
+    seglen = SEGLEN if lengths_on == "host" else torch.tensor(SEGLEN, device=DEV)
+    value = leaf((n,) + shape, 29)
+    out = ops.segment_softmax(seglen, value)
+    ref = ref_segment_softmax(SEGLEN, value)
+    torch.testing.assert_close(out, ref, rtol=1e-12, atol=1e-14)
+    assert_grads(grads(out, [value], 30), grads(ref, [value], 30))
+    small = [2, 0, 3, 1]
+    z = leaf((sum(small), 2), 31)
+    assert torch.autograd.gradcheck(lambda t: ops.segment_softmax(small, t), (z,))
 
 
 # ------------------------------------------------------------------ a GAT layer, float32
