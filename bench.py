@@ -241,6 +241,25 @@ def time_gat_backward(g, el, er, h):
     return {"ms": round(s.elapsed_time(t) / 3, 3)}
 
 
+def time_grouped_backward(fn, a, b, grad, steps):
+    """Average ms of the backward of fn(a, b) (both gradients, no
+    accumulation into .grad), HIP events over `steps` calls."""
+    import torch
+
+    a_, b_ = a.clone().requires_grad_(True), b.clone().requires_grad_(True)
+    out = fn(a_, b_)
+    torch.autograd.grad(out, [a_, b_], grad, retain_graph=True)
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    t = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        torch.autograd.grad(out, [a_, b_], grad, retain_graph=True)
+    t.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(t) / steps
+
+
 def time_subset_softmax(g, el, er, E, args):
     """edge_softmax over a subset of edge ids (every other edge, a GPU
     tensor), not part of a step: the positional grouping by endpoint and its
@@ -585,6 +604,13 @@ def workload_c5(args):
         m = timer.avg_ms(name)
         kern[name] = {"ms": round(m, 3), "TFLOPs": round(flops / m / 1e9, 1),
                       "mfma_frac": round(flops / m / 1e9 / MFMA_F32_PEAK_TFLOPS, 4)}
+    # backward (not part of the step): both gradients, da = G b^T and
+    # db = a^T G per relation, 2 * flops
+    gg = torch.randn(n, K, device="cuda", generator=gen)
+    for name, fn_ in (("gather_mm", lambda x, y: ops.gather_mm(x, y, idx_b=idx)),
+                      ("segment_mm", lambda x, y: ops.segment_mm(x, y, seglen))):
+        m = time_grouped_backward(fn_, a, b, gg, args.steps)
+        kern[name]["backward"] = {"ms": round(m, 3), "TFLOPs": round(2 * flops / m / 1e9, 1)}
     return {"metric": "gather_mm / segment_mm TFLOP/s, fp32, 1 GPU",
             "value": round(2 * flops / ms / 1e9, 2), "unit": "TFLOP/s",
             "ms_per_step": round(ms, 4), "dtype": "f32",

@@ -224,6 +224,32 @@ int mdgl_gather_mm(const void* a, const void* b, const int64_t* idx_b, void* dst
                    int dtype, void* stream);
 int64_t mdgl_gather_mm_workspace_bytes(int64_t n, int64_t d1, int64_t d2, int64_t r, int dtype);
 
+/* Gradients of mdgl_segment_mm / mdgl_gather_mm (no counterpart in the
+ * reference, which has no backward): with grad_out (n x d2) the gradient of
+ * their output,
+ *   grad_a[i] = grad_out[i] @ b[g(i)]^T            (n x d1; rows in no group
+ *                                                  -- past the segments'
+ *                                                  sum -- are left as they are)
+ *   grad_b[g] = sum over the rows i of group g of a[i]^T grad_out[i]
+ *                                                  (r x d1 x d2, 0 for an
+ *                                                  empty group),
+ * g(i) the segment of row i or idx_b[i]. Either output may be null. grad_b
+ * is formed per chunk of a group's rows on the matrix cores and the chunks
+ * are added in order, so it is the same on every run. Workspace:
+ * mdgl_*_mm_grad_workspace_bytes. */
+int mdgl_segment_mm_grad(const void* a, const void* b, const void* grad_out,
+                         const int64_t* seglen_a, void* grad_a, void* grad_b, int64_t n,
+                         int64_t d1, int64_t r, int64_t d2, void* workspace,
+                         int64_t workspace_bytes, int dtype, void* stream);
+int64_t mdgl_segment_mm_grad_workspace_bytes(int64_t n, int64_t d1, int64_t d2, int64_t r,
+                                             int dtype);
+int mdgl_gather_mm_grad(const void* a, const void* b, const int64_t* idx_b, const void* grad_out,
+                        void* grad_a, void* grad_b, int64_t n, int64_t d1, int64_t d2,
+                        int64_t r, void* workspace, int64_t workspace_bytes, int dtype,
+                        void* stream);
+int64_t mdgl_gather_mm_grad_workspace_bytes(int64_t n, int64_t d1, int64_t d2, int64_t r,
+                                            int dtype);
+
 /* Graph build: replaces DGLGraph._build_csr (python/mojodgl/heterograph.py:69-86),
  * which the reference runs in numpy on the host. Groups the edges 0..num_edges-1
  * (COO in edge-id order, int32 on the GPU) by `key` (v for the in-CSR, u for

@@ -805,9 +805,83 @@ int grouped_common(const void* a, const void* b, void* dst, const int64_t* idx_b
   return hip_status(e, what);
 }
 
+int grouped_grad_common(const void* a, const void* b, const void* grad, void* da, void* db,
+                        const int64_t* idx_b, const int64_t* seglen, int64_t n, int64_t d1,
+                        int64_t d2, int64_t r, void* workspace, int64_t workspace_bytes,
+                        int dtype, void* stream, bool gather) {
+  const char* what = gather ? "gather_mm_grad" : "segment_mm_grad";
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "%s: bad dtype %d", what, dtype);
+  if (n < 0 || d1 < 0 || d2 < 0 || r < 0) return fail(MDGL_EINVAL, "%s: negative size", what);
+  if (n >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "%s: 2**31 or more rows", what);
+  if (gather && r > MAX_GATHER_BLOCKS)
+    return fail(MDGL_ENOTSUP, "%s: at most %lld b blocks supported, got %lld", what,
+                (long long)MAX_GATHER_BLOCKS, (long long)r);
+  if (((d1 + 127) / 128) * ((d2 + 127) / 128) > 65535)
+    return fail(MDGL_ENOTSUP, "%s: d1 x d2 of %lld x %lld is too large", what, (long long)d1,
+                (long long)d2);
+  if (n == 0 || d1 == 0 || d2 == 0 || (!da && !db)) return MDGL_OK;
+  if (r == 0) return fail(MDGL_EINVAL, "%s: rows but no b blocks", what);
+  if (!a || !b || !grad || (gather ? !idx_b : !seglen))
+    return fail(MDGL_EINVAL, "%s: null buffer", what);
+  const int64_t need = gather ? mdgl_gather_mm_grad_workspace_bytes(n, d1, d2, r, dtype)
+                              : mdgl_segment_mm_grad_workspace_bytes(n, d1, d2, r, dtype);
+  if (workspace && !aligned(workspace, WS_ALIGN))
+    return fail(MDGL_EINVAL, "workspace must be %lld-byte aligned", (long long)WS_ALIGN);
+  if (!workspace || workspace_bytes < need)
+    return fail(MDGL_EWORKSPACE, "%s: workspace of %lld bytes needed, %lld given", what,
+                (long long)need, (long long)workspace_bytes);
+  GemmGradLaunch L{};
+  L.a = a;
+  L.b = b;
+  L.grad = grad;
+  L.da = da;
+  L.db = db;
+  L.idx_b = idx_b;
+  L.seglen = seglen;
+  L.n = n;
+  L.D1 = d1;
+  L.D2 = d2;
+  L.R = r;
+  L.workspace = workspace;
+  L.stream = (hipStream_t)stream;
+  hipError_t e = dtype == MDGL_FLOAT32 ? launch_grouped_grad<float>(L, gather)
+                                       : launch_grouped_grad<double>(L, gather);
+  return hip_status(e, what);
+}
+
 }  // namespace
 
 extern "C" {
+
+int64_t mdgl_segment_mm_grad_workspace_bytes(int64_t n, int64_t d1, int64_t d2, int64_t r,
+                                             int dtype) {
+  if (n < 0 || d1 < 0 || d2 < 0 || r < 0 || !dtype_ok(dtype)) return -1;
+  return dtype == MDGL_FLOAT32 ? grouped_grad_workspace_bytes<float>(n, d1, d2, r, false)
+                               : grouped_grad_workspace_bytes<double>(n, d1, d2, r, false);
+}
+
+int64_t mdgl_gather_mm_grad_workspace_bytes(int64_t n, int64_t d1, int64_t d2, int64_t r,
+                                            int dtype) {
+  if (n < 0 || d1 < 0 || d2 < 0 || r < 0 || !dtype_ok(dtype)) return -1;
+  return dtype == MDGL_FLOAT32 ? grouped_grad_workspace_bytes<float>(n, d1, d2, r, true)
+                               : grouped_grad_workspace_bytes<double>(n, d1, d2, r, true);
+}
+
+int mdgl_segment_mm_grad(const void* a, const void* b, const void* grad_out,
+                         const int64_t* seglen_a, void* grad_a, void* grad_b, int64_t n,
+                         int64_t d1, int64_t r, int64_t d2, void* workspace,
+                         int64_t workspace_bytes, int dtype, void* stream) {
+  return grouped_grad_common(a, b, grad_out, grad_a, grad_b, nullptr, seglen_a, n, d1, d2, r,
+                             workspace, workspace_bytes, dtype, stream, false);
+}
+
+int mdgl_gather_mm_grad(const void* a, const void* b, const int64_t* idx_b, const void* grad_out,
+                        void* grad_a, void* grad_b, int64_t n, int64_t d1, int64_t d2,
+                        int64_t r, void* workspace, int64_t workspace_bytes, int dtype,
+                        void* stream) {
+  return grouped_grad_common(a, b, grad_out, grad_a, grad_b, idx_b, nullptr, n, d1, d2, r,
+                             workspace, workspace_bytes, dtype, stream, true);
+}
 
 int mdgl_segment_mm(const void* a, const void* b, void* dst, const int64_t* seglen_a, int64_t n,
                     int64_t d1, int64_t r, int64_t d2, void* workspace, int64_t workspace_bytes,

@@ -71,16 +71,19 @@ struct GemmArgs {
   int out_vec;  // rows of out allow 16-byte stores
 };
 
-// bt[g][n][k] = b[g][k][n], zero for k in [K, Kp).
+// bt[g][n][k] = b[g][k][n], zero for k in [K, Kp); with `given_t` b is
+// already [g][n][k] (a product with the blocks' transposes) and is copied.
 template <class T>
 __global__ __launch_bounds__(BLOCK) void transpose_b_kernel(const T* __restrict__ b,
                                                             T* __restrict__ bt, int64_t R,
-                                                            int64_t K, int64_t Kp, int64_t N) {
+                                                            int64_t K, int64_t Kp, int64_t N,
+                                                            int given_t) {
   const int64_t total = R * N * Kp;
   for (int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * BLOCK) {
     const int64_t k = i % Kp, n = (i / Kp) % N, g = i / (Kp * N);
-    bt[i] = k < K ? b[(g * K + k) * N + n] : T(0);
+    if (k >= K) bt[i] = T(0);
+    else bt[i] = given_t ? b[(g * N + n) * K + k] : b[(g * K + k) * N + n];
   }
 }
 
@@ -580,17 +583,56 @@ inline int64_t gemm_kp(int64_t K) {
   return kp < bk ? bk : kp;
 }
 
-// Workspace of one grouped GEMM: bt, group_off, tile_ptr and, to gather,
-// the per-chunk counts and the row permutation.
-template <class T>
-int64_t grouped_workspace_bytes(int64_t n, int64_t K, int64_t N, int64_t R, bool gather) {
-  int64_t b = ws_align(R * N * gemm_kp<T>(K) * (int64_t)sizeof(T));
-  b += 2 * ws_align((R + 1) * 4);
+// Workspace of the grouping: group_off, tile_ptr and, to gather, the
+// per-chunk counts, the row permutation and the group totals.
+inline int64_t plan_workspace_bytes(int64_t n, int64_t R, bool gather) {
+  int64_t b = 2 * ws_align((R + 1) * 4);
   if (gather) {
     const int64_t nb = (n + SORT_CHUNK - 1) / SORT_CHUNK;
     b += ws_align(nb * R * 4) + ws_align(n * 4) + ws_align(R * 8);
   }
   return b;
+}
+
+// The groups of rows: group_off[g] (first row position of group g),
+// tile_ptr[g] (tiles of `tm` rows before group g) and, to gather, perm
+// (row of each sorted position; null for segment_mm's consecutive groups).
+inline hipError_t plan_groups(const int64_t* idx_b, const int64_t* seglen, int64_t n, int64_t R,
+                              int tm, bool gather, char* w, int32_t** group_off,
+                              int32_t** tile_ptr, int32_t** perm, hipStream_t s) {
+  *group_off = reinterpret_cast<int32_t*>(w);
+  w += ws_align((R + 1) * 4);
+  *tile_ptr = reinterpret_cast<int32_t*>(w);
+  w += ws_align((R + 1) * 4);
+  *perm = nullptr;
+  if (gather) {
+    const int64_t nb = (n + SORT_CHUNK - 1) / SORT_CHUNK;
+    int32_t* counts = reinterpret_cast<int32_t*>(w);
+    w += ws_align(nb * R * 4);
+    *perm = reinterpret_cast<int32_t*>(w);
+    w += ws_align(n * 4);
+    int64_t* totals = reinterpret_cast<int64_t*>(w);
+    int bits = 0;
+    while ((int64_t(1) << bits) < R) ++bits;
+    hipLaunchKernelGGL(bucket_count_kernel, dim3((unsigned)nb), dim3(BLOCK), (size_t)(R * 4), s,
+                       idx_b, counts, n, R);
+    hipLaunchKernelGGL(bucket_colscan_kernel, dim3((unsigned)R), dim3(BLOCK), 0, s, counts,
+                       totals, nb, R);
+    hipLaunchKernelGGL(bucket_plan_kernel, dim3(1), dim3(64), 0, s, totals, *group_off,
+                       *tile_ptr, R, tm);
+    hipLaunchKernelGGL(bucket_scatter_kernel, dim3((unsigned)nb), dim3(BLOCK),
+                       (size_t)(5 * R * 4), s, idx_b, counts, totals, *perm, n, R, bits);
+  } else {
+    hipLaunchKernelGGL(seg_plan_kernel, dim3(1), dim3(64), 0, s, seglen, *group_off, *tile_ptr,
+                       R, tm);
+  }
+  return hipGetLastError();
+}
+
+// Workspace of one grouped GEMM: bt, then the grouping.
+template <class T>
+int64_t grouped_workspace_bytes(int64_t n, int64_t K, int64_t N, int64_t R, bool gather) {
+  return ws_align(R * N * gemm_kp<T>(K) * (int64_t)sizeof(T)) + plan_workspace_bytes(n, R, gather);
 }
 
 template <class T>
@@ -604,43 +646,18 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather) {
   char* w = static_cast<char*>(L.workspace);
   T* bt = reinterpret_cast<T*>(w);
   w += ws_align(L.R * L.N * Kp * (int64_t)sizeof(T));
-  int32_t* group_off = reinterpret_cast<int32_t*>(w);
-  w += ws_align((L.R + 1) * 4);
-  int32_t* tile_ptr = reinterpret_cast<int32_t*>(w);
-  w += ws_align((L.R + 1) * 4);
-  int32_t* perm = nullptr;
 
   const int64_t tot = L.R * L.N * Kp;
   int64_t tb = (tot + BLOCK - 1) / BLOCK;
   if (tb > 65536) tb = 65536;
   hipLaunchKernelGGL((transpose_b_kernel<T>), dim3((unsigned)tb), dim3(BLOCK), 0, L.stream,
-                     static_cast<const T*>(L.b), bt, L.R, L.K, Kp, L.N);
+                     static_cast<const T*>(L.b), bt, L.R, L.K, Kp, L.N, L.trans_b);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
 
-  if (gather) {
-    const int64_t nb = (L.n + SORT_CHUNK - 1) / SORT_CHUNK;
-    int32_t* counts = reinterpret_cast<int32_t*>(w);
-    w += ws_align(nb * L.R * 4);
-    perm = reinterpret_cast<int32_t*>(w);
-    w += ws_align(L.n * 4);
-    int64_t* totals = reinterpret_cast<int64_t*>(w);
-    int bits = 0;
-    while ((int64_t(1) << bits) < L.R) ++bits;
-    hipLaunchKernelGGL(bucket_count_kernel, dim3((unsigned)nb), dim3(BLOCK),
-                       (size_t)(L.R * 4), L.stream, L.idx_b, counts, L.n, L.R);
-    hipLaunchKernelGGL(bucket_colscan_kernel, dim3((unsigned)L.R), dim3(BLOCK), 0, L.stream,
-                       counts, totals, nb, L.R);
-    hipLaunchKernelGGL(bucket_plan_kernel, dim3(1), dim3(64), 0, L.stream, totals, group_off,
-                       tile_ptr, L.R, tm);
-    hipLaunchKernelGGL(bucket_scatter_kernel, dim3((unsigned)nb), dim3(BLOCK),
-                       (size_t)(5 * L.R * 4), L.stream, L.idx_b, counts, totals, perm, L.n, L.R,
-                       bits);
-  } else {
-    hipLaunchKernelGGL(seg_plan_kernel, dim3(1), dim3(64), 0, L.stream, L.seglen, group_off,
-                       tile_ptr, L.R, tm);
-  }
-  e = hipGetLastError();
+  int32_t *group_off, *tile_ptr, *perm;
+  e = plan_groups(L.idx_b, L.seglen, L.n, L.R, tm, gather, w, &group_off, &tile_ptr, &perm,
+                  L.stream);
   if (e != hipSuccess) return e;
 
   GemmArgs<T> a;
@@ -687,8 +704,242 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather) {
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- gradient of b
+// db[g] = sum over the rows of group g of a[row]^T grad[row] (D1 x D2 per
+// group). A group's rows are cut into chunks of `ch` rows; a workgroup (4
+// wavefronts, 2 x 2, each 64 x 64 of the tile as 4 x 4 MFMA blocks) forms the
+// 128 x 128 tile blockIdx.y of one chunk's product. The rows are the
+// contracted axis, walked BK at a time through row-major LDS tiles (double
+// buffered like the forward kernel): lane l feeds a[row k0 + l / 16][m0 + l %
+// 16] as A^T and grad[row k0 + l / 16][n0 + l % 16] as B; a row stride of 144
+// elements puts the four rows one 64-lane read touches in distinct banks.
+// Chunk products go to partials that tn_fold_kernel adds per group in chunk
+// order, so db is the same on every run.
+template <class T>
+struct TnArgs {
+  const T* a;
+  const T* g;
+  T* part;                   // [chunk][D1][D2]
+  const int32_t* perm;       // null: group rows are contiguous
+  const int32_t* group_off;  // R + 1
+  const int32_t* chunk_ptr;  // R + 1, chunks per group (prefix)
+  int64_t R, D1, D2, ch;
+  int a_vec, g_vec, tiles_n;
+};
+
+template <class T>
+__global__ __launch_bounds__(BLOCK) void grouped_tn_kernel(TnArgs<T> p) {
+  using M = Mfma<T>;
+  using acc_t = typename M::acc_t;
+  constexpr int BK = M::BK;
+  constexpr int LD = GBM + 16;
+  constexpr int EV = 16 / sizeof(T);   // elements per 16-byte load
+  constexpr int CPR = GBM / EV;        // 16-byte chunks per 128-wide tile row
+  constexpr int RPP = BLOCK / CPR;     // tile rows per pass of the block
+  constexpr int PASSES = BK / RPP;
+  __shared__ __align__(16) T As[2][BK][LD];
+  __shared__ __align__(16) T Bs[2][BK][LD];
+
+  const int64_t c = blockIdx.x;
+  if (c >= p.chunk_ptr[p.R]) return;  // uniform per workgroup
+  int64_t lo = 0, hi = p.R - 1;       // group: last g with chunk_ptr[g] <= c
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) / 2;
+    if (p.chunk_ptr[mid] <= c) lo = mid; else hi = mid - 1;
+  }
+  const int64_t grp = lo;
+  const int64_t r0 = p.group_off[grp] + (c - p.chunk_ptr[grp]) * p.ch;
+  const int64_t g_end = p.group_off[grp + 1];
+  const int64_t r_end = r0 + p.ch < g_end ? r0 + p.ch : g_end;
+  const int64_t m0 = (int64_t)(blockIdx.y / p.tiles_n) * GBM;
+  const int64_t n0 = (int64_t)(blockIdx.y % p.tiles_n) * GBN;
+  const int t = threadIdx.x;
+  const int lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1;
+  const int li = lane & 15, h = lane >> 4;
+
+  T ra[PASSES][EV], rb[PASSES][EV];
+  auto load_stage = [&](int64_t k0) {
+#pragma unroll
+    for (int q = 0; q < PASSES; ++q) {
+      const int r = q * RPP + t / CPR;
+      const int col = (t % CPR) * EV;
+      const int64_t pos = k0 + r;
+      const bool ok = pos < r_end;
+      const int64_t rid = ok ? (p.perm ? (int64_t)p.perm[pos] : pos) : 0;
+      const int64_t ca = m0 + col, cb = n0 + col;
+      if (ok && p.a_vec && ca + EV <= p.D1) {
+        load_vec<T>(p.a + rid * p.D1 + ca, ra[q]);
+      } else {
+#pragma unroll
+        for (int v = 0; v < EV; ++v) ra[q][v] = (ok && ca + v < p.D1) ? p.a[rid * p.D1 + ca + v] : T(0);
+      }
+      if (ok && p.g_vec && cb + EV <= p.D2) {
+        load_vec<T>(p.g + rid * p.D2 + cb, rb[q]);
+      } else {
+#pragma unroll
+        for (int v = 0; v < EV; ++v) rb[q][v] = (ok && cb + v < p.D2) ? p.g[rid * p.D2 + cb + v] : T(0);
+      }
+    }
+  };
+  auto store_stage = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < PASSES; ++q) {
+      const int r = q * RPP + t / CPR;
+      const int col = (t % CPR) * EV;
+      store_vec<T>(&As[buf][r][col], ra[q]);
+      store_vec<T>(&Bs[buf][r][col], rb[q]);
+    }
+  };
+
+  acc_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = T(0);
+
+  const int64_t nstages = (r_end - r0 + BK - 1) / BK;  // a chunk holds at least one row
+  load_stage(r0);
+  store_stage(0);
+  __syncthreads();
+  for (int64_t s = 0; s < nstages; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < nstages) load_stage(r0 + (s + 1) * BK);
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 4) {
+      T af[4], bf[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        af[i] = As[buf][kk + h][wm * 64 + i * 16 + li];
+        bf[i] = Bs[buf][kk + h][wn * 64 + i * 16 + li];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = M::step(af[i], bf[j], acc[i][j]);
+    }
+    if (s + 1 < nstages) {
+      store_stage(buf ^ 1);
+      __syncthreads();
+    }
+  }
+
+  T* out = p.part + c * p.D1 * p.D2;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t d1 = m0 + wm * 64 + i * 16 + M::row(h, r);
+      if (d1 >= p.D1) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t d2 = n0 + wn * 64 + j * 16 + li;
+        if (d2 < p.D2) out[d1 * p.D2 + d2] = acc[i][j][r];
+      }
+    }
+  }
+}
+
+// db[g][e] = sum of part[c][e] over g's chunks in order (0 for an empty group).
+template <class T>
+__global__ __launch_bounds__(BLOCK) void tn_fold_kernel(const T* __restrict__ part,
+                                                        const int32_t* __restrict__ chunk_ptr,
+                                                        T* __restrict__ db, int64_t R, int64_t E) {
+  const int64_t total = R * E;
+  for (int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * BLOCK) {
+    const int64_t g = i / E, e = i - g * E;
+    T acc = T(0);
+    for (int64_t c = chunk_ptr[g]; c < chunk_ptr[g + 1]; ++c) acc += part[c * E + e];
+    db[i] = acc;
+  }
+}
+
+constexpr int64_t TN_CH = 4096;                 // rows per chunk, at least
+constexpr int64_t TN_PART_BYTES = 256ll << 20;  // partials kept below this when rows allow
+
+// Rows per chunk: TN_CH, doubled until the partials of the chunks (at most
+// n / ch + R of them) fit TN_PART_BYTES, and at most n (n < 2**31).
+inline int64_t tn_chunk_rows(int64_t n, int64_t D1, int64_t D2, int64_t R, int64_t es) {
+  int64_t ch = TN_CH;
+  while (ch < n && ((n + ch - 1) / ch + R) * D1 * D2 * es > TN_PART_BYTES) ch *= 2;
+  return ch < n ? ch : (n > 0 ? n : 1);
+}
+
+template <class T>
+int64_t grouped_grad_workspace_bytes(int64_t n, int64_t D1, int64_t D2, int64_t R, bool gather) {
+  const int64_t es = sizeof(T);
+  const int64_t ch = tn_chunk_rows(n, D1, D2, R, es);
+  const int64_t chunks = (n + ch - 1) / ch + R;
+  // da's grouped GEMM (K = D2, N = D1), then db's grouping and partials
+  return grouped_workspace_bytes<T>(n, D2, D1, R, gather) + plan_workspace_bytes(n, R, gather) +
+         ws_align(chunks * D1 * D2 * es);
+}
+
+template <class T>
+hipError_t launch_grouped_grad(const GemmGradLaunch& L, bool gather) {
+  if (L.n <= 0 || L.R <= 0 || L.D1 <= 0 || L.D2 <= 0) return hipSuccess;
+  char* w = static_cast<char*>(L.workspace);
+  if (L.da) {
+    GemmLaunch g{};
+    g.a = L.grad;
+    g.b = L.b;
+    g.out = L.da;
+    g.idx_b = L.idx_b;
+    g.seglen = L.seglen;
+    g.n = L.n;
+    g.K = L.D2;
+    g.N = L.D1;
+    g.R = L.R;
+    g.workspace = w;
+    g.stream = L.stream;
+    g.trans_b = 1;
+    hipError_t e = launch_grouped<T>(g, gather);
+    if (e != hipSuccess) return e;
+  }
+  w += grouped_workspace_bytes<T>(L.n, L.D2, L.D1, L.R, gather);
+  if (!L.db) return hipSuccess;
+  const int64_t ch = tn_chunk_rows(L.n, L.D1, L.D2, L.R, sizeof(T));
+  const int64_t max_chunks = (L.n + ch - 1) / ch + L.R;
+  int32_t *group_off, *chunk_ptr, *perm;
+  hipError_t e = plan_groups(L.idx_b, L.seglen, L.n, L.R, (int)ch, gather, w, &group_off,
+                             &chunk_ptr, &perm, L.stream);
+  if (e != hipSuccess) return e;
+  w += plan_workspace_bytes(L.n, L.R, gather);
+  TnArgs<T> a;
+  a.a = static_cast<const T*>(L.a);
+  a.g = static_cast<const T*>(L.grad);
+  a.part = reinterpret_cast<T*>(w);
+  a.perm = perm;
+  a.group_off = group_off;
+  a.chunk_ptr = chunk_ptr;
+  a.R = L.R;
+  a.D1 = L.D1;
+  a.D2 = L.D2;
+  a.ch = ch;
+  constexpr int EV = 16 / sizeof(T);
+  a.a_vec = (L.D1 % EV == 0) && (reinterpret_cast<uintptr_t>(L.a) % 16 == 0);
+  a.g_vec = (L.D2 % EV == 0) && (reinterpret_cast<uintptr_t>(L.grad) % 16 == 0);
+  const int64_t tiles_m = (L.D1 + GBM - 1) / GBM;
+  a.tiles_n = (int)((L.D2 + GBN - 1) / GBN);
+  hipLaunchKernelGGL((grouped_tn_kernel<T>), dim3((unsigned)max_chunks, (unsigned)(tiles_m * a.tiles_n)),
+                     dim3(BLOCK), 0, L.stream, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t E = L.D1 * L.D2;
+  int64_t fb = (L.R * E + BLOCK - 1) / BLOCK;
+  if (fb > 65536) fb = 65536;
+  hipLaunchKernelGGL((tn_fold_kernel<T>), dim3((unsigned)fb), dim3(BLOCK), 0, L.stream, a.part,
+                     chunk_ptr, static_cast<T*>(L.db), L.R, E);
+  return hipGetLastError();
+}
+
 }  // namespace mdgl
 
 #define MDGL_INSTANTIATE_GEMM(T)                                                               \
   template int64_t mdgl::grouped_workspace_bytes<T>(int64_t, int64_t, int64_t, int64_t, bool); \
-  template hipError_t mdgl::launch_grouped<T>(const mdgl::GemmLaunch&, bool);
+  template hipError_t mdgl::launch_grouped<T>(const mdgl::GemmLaunch&, bool);                  \
+  template int64_t mdgl::grouped_grad_workspace_bytes<T>(int64_t, int64_t, int64_t, int64_t,   \
+                                                         bool);                                 \
+  template hipError_t mdgl::launch_grouped_grad<T>(const mdgl::GemmGradLaunch&, bool);

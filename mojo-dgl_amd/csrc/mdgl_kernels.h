@@ -129,11 +129,31 @@ struct GemmLaunch {
   int64_t n, K, N, R;
   void* workspace;
   hipStream_t stream;
+  int trans_b;  // b given as [R][N][K] (multiplying by each block's transpose)
 };
 template <class T>
 int64_t grouped_workspace_bytes(int64_t n, int64_t K, int64_t N, int64_t R, bool gather);
 template <class T>
 hipError_t launch_grouped(const GemmLaunch& L, bool gather);
+// Gradients of out = a @ b[group] (a: n x D1, b: R x D1 x D2, grad: n x D2):
+// da = grad @ b[group]^T and db[g] = sum over g's rows of a^T grad; either
+// output may be null.
+struct GemmGradLaunch {
+  const void* a;
+  const void* b;
+  const void* grad;
+  void* da;
+  void* db;
+  const int64_t* idx_b;
+  const int64_t* seglen;
+  int64_t n, D1, D2, R;
+  void* workspace;
+  hipStream_t stream;
+};
+template <class T>
+int64_t grouped_grad_workspace_bytes(int64_t n, int64_t D1, int64_t D2, int64_t R, bool gather);
+template <class T>
+hipError_t launch_grouped_grad(const GemmGradLaunch& L, bool gather);
 
 // Elementwise helpers.
 hipError_t launch_replace_inf(const void* src, void* dst, int64_t n, int dtype, hipStream_t s);

@@ -86,6 +86,12 @@ _SIGNATURES = {
     "mdgl_segment_mm_workspace_bytes": ([_I64, _I64, _I64, _I64, _C], _I64),
     "mdgl_gather_mm": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _C, _P], _C),
     "mdgl_gather_mm_workspace_bytes": ([_I64, _I64, _I64, _I64, _C], _I64),
+    "mdgl_segment_mm_grad": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _C, _P],
+                             _C),
+    "mdgl_segment_mm_grad_workspace_bytes": ([_I64, _I64, _I64, _I64, _C], _I64),
+    "mdgl_gather_mm_grad": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _C, _P],
+                            _C),
+    "mdgl_gather_mm_grad_workspace_bytes": ([_I64, _I64, _I64, _I64, _C], _I64),
     "mdgl_build_csr": ([_P, _P, _I64, _I64, _P, _P, _P, _P, _I64, _P], _C),
     "mdgl_build_csr_workspace_bytes": ([_I64, _I64], _I64),
     "mdgl_gspmm_edge_grad": ([_P, _P, _P, _P, _P, _I64, _I64, _C, ctypes.c_double, _C, _P], _C),

@@ -28,6 +28,10 @@ these follow the calculus of the forward ops and run on the same kernels:
   subset of eids the rows are the forward's groups of positions (their sums by
   ``segment_reduce`` after the products are put in group order), and the rows
   past the selection, constant zero, get zero;
+* segment_mm / gather_mm (out[i] = a[i] @ b[g(i)]): da = grad @ b[g]^T on the
+  grouped GEMM with the blocks taken transposed, db[g] = sum over g's rows of
+  a^T grad per chunk of rows on the matrix cores, chunks added in order
+  (``mdgl_segment_mm_grad`` / ``mdgl_gather_mm_grad``);
 * segment_reduce / segment_softmax: the segments are CSR rows over the value
   rows themselves (``mdgl_segment_ids`` maps rows to segments): sum / mean /
   max / min as gspmm copy_rhs (max / min through the arg row of
@@ -47,7 +51,8 @@ import torch
 from .. import _lib
 from ..base import DGLError
 
-__all__ = ["needs_grad", "GSpMM", "GSDDMM", "EdgeSoftmax", "SegmentReduce", "SegmentSoftmax"]
+__all__ = ["needs_grad", "GSpMM", "GSDDMM", "EdgeSoftmax", "SegmentReduce", "SegmentSoftmax",
+           "SegmentMM", "GatherMM"]
 
 
 def needs_grad(*xs) -> bool:
@@ -453,3 +458,108 @@ class EdgeSoftmax(torch.autograd.Function):
             (vids if row == "v" else uids).data_ptr(), a2.data_ptr(), G.data_ptr(), s.data_ptr(),
             dx.data_ptr(), E, a2.shape[1], _code(a2), _lib.stream()), "edge_softmax_grad")
         return None, dx.reshape(a.shape), None, None
+
+
+def _grouped_grad(a, b, grad_out, seglen, idx, covered, need_a, need_b):
+    """(da, db) of out[i] = a[i] @ b[g(i)] (segment_mm with `seglen`, gather_mm
+    with `idx`): rows of a past `covered` (in no segment) get zero."""
+    from .gather_mm import GATHER_MAX_BLOCKS
+
+    A, B = _lib.feature(a), _lib.feature(b)
+    dtype = _lib.common_dtype(A, B)
+    tdt, code, gdev = _lib.torch_dtype(dtype), _lib.dtype_code(dtype), _lib.device()
+    Ad, Bd = _lib.on_device(A, dtype), _lib.on_device(B, dtype)
+    n, d1 = Ad.shape
+    r, _, d2 = Bd.shape
+    if covered == 0 or d1 == 0 or d2 == 0 or not (need_a or need_b):
+        zeros = (lambda *shape: torch.zeros(shape, dtype=tdt, device=gdev))
+        return (zeros(n, d1) if need_a else None), (zeros(r, d1, d2) if need_b else None)
+    # the kernels write every row of a group and every element of db
+    da = torch.empty((n, d1), dtype=tdt, device=gdev) if need_a else None
+    if da is not None and covered < n:
+        da[covered:].zero_()
+    db = torch.empty((r, d1, d2), dtype=tdt, device=gdev) if need_b else None
+    G = grad_out.to(device=gdev, dtype=tdt).contiguous()
+    L = _lib.lib()
+    if idx is not None and r > GATHER_MAX_BLOCKS:
+        # too many blocks to bucket: rows sorted by block (stable), then the
+        # segment form, as the forward's sorted route
+        perm = torch.sort(idx, stable=True).indices
+        sl = torch.bincount(idx, minlength=r)
+        da_s, db = _grouped_grad(Ad.index_select(0, perm), Bd, G.index_select(0, perm), sl, None,
+                                 n, need_a, need_b)
+        if da is not None:
+            da.index_copy_(0, perm, da_s)
+        return da, db
+    if idx is not None:
+        nbytes = L.mdgl_gather_mm_grad_workspace_bytes(n, d1, d2, r, code)
+    else:
+        nbytes = L.mdgl_segment_mm_grad_workspace_bytes(n, d1, d2, r, code)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=gdev)
+    if idx is not None:
+        rc = L.mdgl_gather_mm_grad(Ad.data_ptr(), Bd.data_ptr(), idx.data_ptr(), G.data_ptr(),
+                                   _lib.ptr(da), _lib.ptr(db), n, d1, d2, r, ws.data_ptr(), nbytes,
+                                   code, _lib.stream())
+        _lib.check(rc, "gather_mm_grad")
+    else:
+        sl = torch.as_tensor(seglen, dtype=torch.int64).to(gdev).contiguous()
+        rc = L.mdgl_segment_mm_grad(Ad.data_ptr(), Bd.data_ptr(), G.data_ptr(), sl.data_ptr(),
+                                    _lib.ptr(da), _lib.ptr(db), n, d1, r, d2, ws.data_ptr(),
+                                    nbytes, code, _lib.stream())
+        _lib.check(rc, "segment_mm_grad")
+    return da, db
+
+
+def _back(g, like):
+    """A gradient in the operand's dtype and on its device (None for numpy)."""
+    if g is None or not isinstance(like, torch.Tensor):
+        return None
+    return g.to(device=like.device, dtype=like.dtype)
+
+
+def _save_operands(ctx, a, b):
+    """Tensors through save_for_backward; a numpy operand (no gradient) kept as is."""
+    ta, tb = (x if isinstance(x, torch.Tensor) else None for x in (a, b))
+    ctx.save_for_backward(ta, tb)
+    ctx.host = (None if ta is not None else a, None if tb is not None else b)
+
+
+def _saved_operands(ctx):
+    ta, tb = ctx.saved_tensors
+    return (ta if ta is not None else ctx.host[0]), (tb if tb is not None else ctx.host[1])
+
+
+class SegmentMM(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, a, b, seglen):
+        from .segment import _segment_mm
+
+        out, sl, covered = _segment_mm(a, b, seglen)
+        ctx.sl, ctx.covered = sl, covered
+        _save_operands(ctx, a, b)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        a, b = _saved_operands(ctx)
+        da, db = _grouped_grad(a, b, grad_out, ctx.sl, None, ctx.covered,
+                               ctx.needs_input_grad[0], ctx.needs_input_grad[1])
+        return _back(da, a), _back(db, b), None
+
+
+class GatherMM(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, a, b, idx_b):
+        from .gather_mm import _gather_mm
+
+        out, idx = _gather_mm(a, b, idx_b)
+        ctx.idx = idx
+        _save_operands(ctx, a, b)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        a, b = _saved_operands(ctx)
+        da, db = _grouped_grad(a, b, grad_out, None, ctx.idx, a.shape[0],
+                               ctx.needs_input_grad[0], ctx.needs_input_grad[1])
+        return _back(da, a), _back(db, b), None

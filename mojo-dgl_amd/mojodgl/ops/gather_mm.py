@@ -15,6 +15,7 @@ import torch
 
 from .. import _lib
 from ..base import DGLError
+from . import _autograd
 from .segment import _grouped_mm
 
 __all__ = ["gather_mm"]
@@ -22,6 +23,9 @@ __all__ = ["gather_mm"]
 # D1 * D2 above which the sorted segment_mm route is taken (the reference's
 # switch, overridable by the same environment variable).
 _SEGMENT_BLOCK = int(os.environ.get("MOJODGL_GATHER_MM_SEGMENT_BLOCK", 16384))
+# b blocks the bucketed route takes (mdgl_gather_mm keeps 5 ints per block in
+# LDS); more go the sorted route
+GATHER_MAX_BLOCKS = 2048
 
 
 def gather_mm(a, b, *, idx_b):
@@ -40,8 +44,16 @@ def gather_mm(a, b, *, idx_b):
 
     Returns
     -------
-    The (N, D2) product.
+    The (N, D2) product. With torch tensors that require grad the result
+    takes part in autograd.
     """
+    if _autograd.needs_grad(a, b):
+        return _autograd.GatherMM.apply(a, b, idx_b)
+    return _gather_mm(a, b, idx_b)[0]
+
+
+def _gather_mm(a, b, idx_b):
+    """gather_mm returning (result, idx_b as a GPU int64 tensor)."""
     A = _lib.feature(a)
     B = _lib.feature(b)
     if A.ndim != 2 or B.ndim != 3:
@@ -68,7 +80,7 @@ def gather_mm(a, b, *, idx_b):
     if not on_gpu:
         idx = torch.from_numpy(idx).to(_lib.device())
     as_torch, dev = _lib.wants_torch(A, B), _lib.out_device(A, B)
-    if D1 * D2 > _SEGMENT_BLOCK:
+    if D1 * D2 > _SEGMENT_BLOCK or R > GATHER_MAX_BLOCKS:
         # stable sort on the GPU: the same permutation as the reference's
         # stable host argsort
         perm = torch.sort(idx, stable=True).indices
@@ -81,4 +93,4 @@ def gather_mm(a, b, *, idx_b):
         out.index_copy_(0, perm, out_sorted)
     else:
         out = _grouped_mm(A, B, idx, None, gather=True, covered=N)
-    return _lib.give_back(out, as_torch, dev)
+    return _lib.give_back(out, as_torch, dev), idx

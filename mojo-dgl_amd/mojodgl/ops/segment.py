@@ -265,8 +265,16 @@ def segment_mm(a, b, seglen_a):
 
     Returns
     -------
-    The (N, D2) product; rows past ``sum(seglen_a)`` are zero.
+    The (N, D2) product; rows past ``sum(seglen_a)`` are zero. With torch
+    tensors that require grad the result takes part in autograd.
     """
+    if _autograd.needs_grad(a, b):
+        return _autograd.SegmentMM.apply(a, b, seglen_a)
+    return _segment_mm(a, b, seglen_a)[0]
+
+
+def _segment_mm(a, b, seglen_a):
+    """segment_mm returning (result, seglen as int64 numpy, rows covered)."""
     A = _lib.feature(a)
     B = _lib.feature(b)
     if A.ndim != 2 or B.ndim != 3:
@@ -286,8 +294,9 @@ def segment_mm(a, b, seglen_a):
             raise DGLError(
                 "segment lengths must be non-negative and sum to {}, got a minimum of {} and a "
                 "sum of {}".format(n, lo, total))
-    out = _grouped_mm(A, B, None, seglen_a, gather=False, covered=total if r else 0)
-    return _lib.give_back(out, _lib.wants_torch(A, B), _lib.out_device(A, B))
+    covered = total if r else 0
+    out = _grouped_mm(A, B, None, seglen_a, gather=False, covered=covered)
+    return _lib.give_back(out, _lib.wants_torch(A, B), _lib.out_device(A, B)), seglen_a, covered
 
 
 def _replace_inf_with_zero(x):

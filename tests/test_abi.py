@@ -137,6 +137,16 @@ def test_backward_helper_arguments(lib):
     rc = lib.mdgl_segment_reduce_arg(1, 1, 1, None, 3, 2, 1, 6, 0, 0, None)
     assert rc == -1 and "null" in err(lib)
     assert lib.mdgl_segment_reduce_arg(None, None, None, None, 0, 2, 2, 0, 0, 0, None) == 0
+    # grouped GEMM gradients: sizes, outputs, workspace
+    assert lib.mdgl_segment_mm_grad_workspace_bytes(-1, 4, 4, 2, 0) == -1
+    assert lib.mdgl_gather_mm_grad_workspace_bytes(10, 4, 4, 2, 0) > 0
+    rc = lib.mdgl_segment_mm_grad(1, 1, 1, 1, 1, 1, 10, 4, 2, 4, None, 0, 0, None)
+    assert rc == -2 and "workspace" in err(lib)
+    assert lib.mdgl_segment_mm_grad(1, 1, 1, 1, None, None, 10, 4, 2, 4, None, 0, 0, None) == 0
+    rc = lib.mdgl_gather_mm_grad(1, 1, 1, 1, 1, 1, 10, 4, 4, 4096, None, 0, 0, None)
+    assert rc == -3 and "blocks" in err(lib)
+    rc = lib.mdgl_gather_mm_grad(1, 1, None, 1, 1, 1, 10, 4, 4, 2, None, 0, 0, None)
+    assert rc == -1 and "null" in err(lib)
     # the fused u_mul_e backward refuses other ops' shapes before launching
     rc = lib.mdgl_gspmm_mul_sum_dot(1, 1, 1, 1, 1, None, 1, 1, 10, 12, 2, 12, 0, None, None,
                                     None, None, 0, 0, None, None, 0, None, 0, 0, None)

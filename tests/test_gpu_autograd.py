@@ -355,6 +355,106 @@ def test_segment_softmax_backward(shape, lengths_on):
     assert torch.autograd.gradcheck(lambda t: ops.segment_softmax(small, t), (z,))
 
 
+# ------------------------------------------------------------------ segment_mm / gather_mm
+def check_by_terms(got, want, bound, dtype):
+    """|got - want| <= tol * bound, bound the same sum over absolute terms."""
+    tol = 1e-5 if dtype == torch.float32 else 1e-12
+    err = (got.double() - want).abs()
+    assert bool((err <= tol * bound + 1e-30).all()), float((err / (bound + 1e-300)).max())
+
+
+def ref_grouped_grads(a, b, groups, G):
+    """float64 da, db of out[i] = a[i] @ b[groups[i]] (rows with group -1 give
+    zero), and the bounds sum |terms| of each."""
+    a64, b64, G64 = a.detach().double(), b.detach().double(), G.double()
+    gi = torch.as_tensor(groups, device=DEV)
+    live = gi >= 0
+    bsel = b64[gi.clamp(min=0)]                                   # n x d1 x d2
+    da = torch.bmm(G64[:, None, :], bsel.transpose(1, 2).contiguous())[:, 0] * live[:, None]
+    da_b = torch.bmm(G64.abs()[:, None, :], bsel.abs().transpose(1, 2).contiguous())[:, 0]
+    outer = a64[:, :, None] * G64[:, None, :] * live[:, None, None]
+    db = torch.zeros_like(b64).index_add(0, gi.clamp(min=0), outer)
+    db_b = torch.zeros_like(b64).index_add(0, gi.clamp(min=0), outer.abs())
+    return da, db, da_b, db_b
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("n,d1,d2,r", [(3000, 128, 128, 8), (20000, 16, 16, 2), (900, 5, 3, 7),
+                                       (1500, 33, 130, 3), (700, 130, 200, 2)])
+def test_segment_mm_backward(dtype, n, d1, d2, r):
+    """segment_mm gradients (da = G b^T per segment, db = a^T G summed per
+    segment in chunks of rows, empty segments and rows past the segments
+    included) against float64 sums, within the term-magnitude tolerance; run
+    to run bit-identical."""
+    rng = np.random.default_rng(70 + d1 + r)
+    seglen = rng.multinomial(n, rng.dirichlet(np.full(r, 0.5)))
+    seglen[r // 2] = 0
+    rows = int(seglen.sum()) + 37                     # 37 rows in no segment
+    a = leaf((rows, d1), 71, dtype=dtype)
+    b = leaf((r, d1, d2), 72, dtype=dtype)
+    G = torch.randn((rows, d2), generator=torch.Generator(device=DEV).manual_seed(73),
+                    device=DEV, dtype=dtype)
+    out = ops.segment_mm(a, b, seglen)
+    out.backward(G)
+    groups = np.concatenate([np.repeat(np.arange(r), seglen), np.full(37, -1)])
+    da, db, da_b, db_b = ref_grouped_grads(a, b, groups, G)
+    check_by_terms(a.grad, da, da_b, dtype)
+    check_by_terms(b.grad, db, db_b, dtype)
+    first = (a.grad.clone(), b.grad.clone())
+    a.grad = b.grad = None
+    ops.segment_mm(a, b, seglen).backward(G)
+    assert torch.equal(a.grad, first[0]) and torch.equal(b.grad, first[1])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("n,d1,d2,r", [(3000, 128, 128, 8), (9000, 16, 16, 3), (900, 5, 3, 7),
+                                       (600, 4, 4, 2100)],
+                         ids=["128x128", "multi-chunk", "odd", "sorted-route-2100-blocks"])
+def test_gather_mm_backward(dtype, n, d1, d2, r):
+    """gather_mm gradients (rows bucketed by idx_b, one block unused) against
+    float64 sums, and with more blocks than the bucketed route takes (the
+    sorted route); run to run bit-identical."""
+    rng = np.random.default_rng(80 + d1 + r)
+    idx = rng.integers(0, r, n)
+    idx[idx == 1] = 0                                  # block 1 unused
+    a = leaf((n, d1), 81, dtype=dtype)
+    b = leaf((r, d1, d2), 82, dtype=dtype)
+    G = torch.randn((n, d2), generator=torch.Generator(device=DEV).manual_seed(83), device=DEV,
+                    dtype=dtype)
+    idx_t = torch.from_numpy(idx).to(DEV)
+    out = ops.gather_mm(a, b, idx_b=idx_t)
+    a64, b64 = a.detach().double(), b.detach().double()
+    want = torch.bmm(a64[:, None, :], b64[idx_t])[:, 0]
+    bound = torch.bmm(a64.abs()[:, None, :], b64[idx_t].abs())[:, 0]
+    check_by_terms(out.detach(), want, bound, dtype)
+    out.backward(G)
+    da, db, da_b, db_b = ref_grouped_grads(a, b, idx, G)
+    check_by_terms(a.grad, da, da_b, dtype)
+    check_by_terms(b.grad, db, db_b, dtype)
+    assert torch.count_nonzero(b.grad[1]) == 0
+    first = (a.grad.clone(), b.grad.clone())
+    a.grad = b.grad = None
+    ops.gather_mm(a, b, idx_b=idx).backward(G)
+    assert torch.equal(a.grad, first[0]) and torch.equal(b.grad, first[1])
+
+
+def test_segment_mm_and_gather_mm_gradcheck():
+    """Finite differences (float64) through both ops, and a numpy b (no
+    gradient for it)."""
+    a = leaf((12, 3), 84)
+    b = leaf((3, 3, 2), 85)
+    seglen = [5, 0, 4]
+    assert torch.autograd.gradcheck(lambda x, y: ops.segment_mm(x, y, seglen), (a, b))
+    idx = torch.tensor([2, 0, 0, 1, 2, 2, 0, 1, 1, 0, 2, 2], device=DEV)
+    assert torch.autograd.gradcheck(lambda x, y: ops.gather_mm(x, y, idx_b=idx), (a, b))
+    bn = b.detach().cpu().numpy()
+    out = ops.gather_mm(a, bn, idx_b=idx)
+    assert out.device == a.device
+    (ga,) = torch.autograd.grad(out.sum(), [a])
+    # d(sum of a[i] @ b[idx i]) / da[i] = the row sums of b[idx i]
+    torch.testing.assert_close(ga, b.detach()[idx].sum(-1), rtol=1e-12, atol=1e-12)
+
+
 # ------------------------------------------------------------------ a GAT layer, float32
 def test_gat_layer_backward_float32():
     """gsddmm u_add_v -> leaky_relu -> edge_softmax -> gspmm u_mul_e_sum, and
