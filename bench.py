@@ -18,7 +18,8 @@ the stream it is launched on) and the CPU baseline (the oracle, a C++
 restatement of the reference's kernels, timed on this host on a sample).
 
 Other workloads (--workload c1|c3|c4|c5) print their own line; they are
-measurement runs for the other configurations, not the headline.
+measurement runs for the other configurations, not the headline, and so is
+--workload gat_train (the same layer with autograd: forward + backward).
 """
 
 from __future__ import annotations
@@ -563,6 +564,51 @@ def workload_c4(args):
             "kernels": kern}
 
 
+def workload_gat_train(args):
+    """The GAT layer with autograd on el, er and h: one step is the forward
+    and the backward (gradients set to None before each, as an optimizer's
+    zero_grad). Per-op times: the forward ops, then `backward` for the whole
+    backward pass."""
+    import torch
+
+    import mojodgl as dgl
+    import mojodgl.ops as ops
+
+    N, E, H, D = args.nodes, args.edges, 8, 32
+    log("generating power-law graph N={} E={}".format(N, E))
+    u, v, gstats = power_law_graph(1, N, E)
+    g = dgl.graph((u, v), num_nodes=N)
+    g._device_csr("in")
+    g._device_csr("out")
+    g._device_coo()
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    el = torch.randn(N, H, 1, device="cuda", generator=gen).requires_grad_(True)
+    er = torch.randn(N, H, 1, device="cuda", generator=gen).requires_grad_(True)
+    h = torch.randn(N, H, D, device="cuda", generator=gen).requires_grad_(True)
+    grad = torch.randn(N, H, D, device="cuda", generator=gen)
+    torch.cuda.synchronize()
+
+    def step(t):
+        run = t if t is not None else (lambda name, fn: fn())
+        for x in (el, er, h):
+            x.grad = None
+        e = run("gsddmm_u_add_v", lambda: ops.u_add_v(g, el, er))
+        e = run("leaky_relu", lambda: torch.nn.functional.leaky_relu(e, 0.2))
+        a = run("edge_softmax", lambda: ops.edge_softmax(g, e))
+        out = run("gspmm_u_mul_e_sum", lambda: ops.u_mul_e_sum(g, h, a))
+        run("backward", lambda: out.backward(grad))
+
+    timer = OpTimer()
+    ms = run_steps(step, args.steps, args.warmup, timer)
+    units = E * H + E * H + E * H * D
+    return {"metric": "GAT layer forward + backward, fp32, 1 GPU",
+            "value": round(units / (ms * 1e-3) / 1e9, 2), "unit": "GEdge·feat/s (forward units)",
+            "ms_per_step": round(ms, 4), "dtype": "f32",
+            "config": {"workload": "GAT layer forward + backward on a power-law graph",
+                       "num_nodes": N, "num_edges": E, "heads": H, "head_dim": D, **gstats},
+            "breakdown_ms": {k: round(timer.avg_ms(k), 4) for k in timer.totals}}
+
+
 def workload_c5(args):
     import torch
 
@@ -621,8 +667,8 @@ def workload_c5(args):
                                       "TFLOPs": round(flops / blas_ms / 1e9, 1)}}
 
 
-WORKLOADS = {"gat": workload_gat, "c1": workload_c1, "c3": workload_c3, "c4": workload_c4,
-             "c5": workload_c5}
+WORKLOADS = {"gat": workload_gat, "gat_train": workload_gat_train, "c1": workload_c1,
+             "c3": workload_c3, "c4": workload_c4, "c5": workload_c5}
 
 
 def main():
