@@ -233,7 +233,8 @@ int64_t mdgl_gather_mm_workspace_bytes(int64_t n, int64_t d1, int64_t d2, int64_
  *   grad_b[g] = sum over the rows i of group g of a[i]^T grad_out[i]
  *                                                  (r x d1 x d2, 0 for an
  *                                                  empty group),
- * g(i) the segment of row i or idx_b[i]. Either output may be null. grad_b
+ * g(i) the segment of row i or idx_b[i]. Either output may be null; with
+ * n, d1 or d2 zero nothing is written. grad_b
  * is formed per chunk of a group's rows on the matrix cores and the chunks
  * are added in order, so it is the same on every run. Workspace:
  * mdgl_*_mm_grad_workspace_bytes. */
