@@ -710,7 +710,8 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather) {
 // wavefronts, 2 x 2, each 64 x 64 of the tile as 4 x 4 MFMA blocks) forms the
 // 128 x 128 tile blockIdx.y of one chunk's product. The rows are the
 // contracted axis, walked BK at a time through row-major LDS tiles (double
-// buffered like the forward kernel): lane l feeds a[row k0 + l / 16][m0 + l %
+// buffered like the forward kernel; BK rows per stage, 16 when the rows come
+// through gather_mm's permutation): lane l feeds a[row k0 + l / 16][m0 + l %
 // 16] as A^T and grad[row k0 + l / 16][n0 + l % 16] as B; a row stride of 144
 // elements puts the four rows one 64-lane read touches in distinct banks.
 // Chunk products go to partials that tn_fold_kernel adds per group in chunk
@@ -727,11 +728,10 @@ struct TnArgs {
   int a_vec, g_vec, tiles_n;
 };
 
-template <class T>
+template <class T, int BK>
 __global__ __launch_bounds__(BLOCK) void grouped_tn_kernel(TnArgs<T> p) {
   using M = Mfma<T>;
   using acc_t = typename M::acc_t;
-  constexpr int BK = M::BK;
   constexpr int LD = GBM + 16;
   constexpr int EV = 16 / sizeof(T);   // elements per 16-byte load
   constexpr int CPR = GBM / EV;        // 16-byte chunks per 128-wide tile row
@@ -923,8 +923,13 @@ hipError_t launch_grouped_grad(const GemmGradLaunch& L, bool gather) {
   a.g_vec = (L.D2 % EV == 0) && (reinterpret_cast<uintptr_t>(L.grad) % 16 == 0);
   const int64_t tiles_m = (L.D1 + GBM - 1) / GBM;
   a.tiles_n = (int)((L.D2 + GBN - 1) / GBN);
-  hipLaunchKernelGGL((grouped_tn_kernel<T>), dim3((unsigned)max_chunks, (unsigned)(tiles_m * a.tiles_n)),
-                     dim3(BLOCK), 0, L.stream, a);
+  // rows gathered through the permutation wait longer: shallower stages,
+  // half the LDS, twice the workgroups per CU to cover them
+  const dim3 grid((unsigned)max_chunks, (unsigned)(tiles_m * a.tiles_n));
+  if (perm)
+    hipLaunchKernelGGL((grouped_tn_kernel<T, 16>), grid, dim3(BLOCK), 0, L.stream, a);
+  else
+    hipLaunchKernelGGL((grouped_tn_kernel<T, Mfma<T>::BK>), grid, dim3(BLOCK), 0, L.stream, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t E = L.D1 * L.D2;
