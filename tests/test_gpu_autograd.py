@@ -438,6 +438,34 @@ def test_gather_mm_backward(dtype, n, d1, d2, r):
     assert torch.equal(a.grad, first[0]) and torch.equal(b.grad, first[1])
 
 
+@pytest.mark.parametrize("route", ["segment", "gather"])
+def test_grouped_mm_backward_misaligned_operands(route):
+    """a and the output gradient one element off a 16-byte boundary (the
+    element loads of both gradient kernels) give the gradients of aligned
+    copies: db bit for bit (the same kernel), da to rounding (the aligned
+    case may take the resident forward kernel, which orders k differently)."""
+    n, d1, d2, r = 2000, 16, 8, 3
+    rng = np.random.default_rng(90)
+    base = leaf((n * d1 + 1,), 91, dtype=torch.float32)
+    b = leaf((r, d1, d2), 92, dtype=torch.float32)
+    gbase = torch.randn(n * d2 + 1, device=DEV)
+    G = gbase[1:].view(n, d2)
+    a = base[1:].view(n, d1)
+    if route == "segment":
+        seglen = rng.multinomial(n, np.ones(r) / r)
+        run = (lambda x, y: ops.segment_mm(x, y, seglen))
+    else:
+        idx = torch.from_numpy(rng.integers(0, r, n)).to(DEV)
+        run = (lambda x, y: ops.gather_mm(x, y, idx_b=idx))
+    run(a, b).backward(G)
+    got = (base.grad[1:].clone(), b.grad.clone())
+    a2 = a.detach().clone().requires_grad_(True)
+    b2 = b.detach().clone().requires_grad_(True)
+    run(a2, b2).backward(G.clone())
+    torch.testing.assert_close(got[0], a2.grad.reshape(-1), rtol=1e-5, atol=1e-5)
+    assert torch.equal(got[1], b2.grad)
+
+
 def test_segment_mm_and_gather_mm_gradcheck():
     """Finite differences (float64) through both ops, and a numpy b (no
     gradient for it)."""
