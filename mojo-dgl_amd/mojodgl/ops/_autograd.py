@@ -37,6 +37,9 @@ these follow the calculus of the forward ops and run on the same kernels:
   max / min as gspmm copy_rhs (max / min through the arg row of
   ``mdgl_segment_reduce_arg``), softmax as edge_softmax.
 
+The backward passes run on the library's kernels, outside torch's graph, so
+they are differentiable once: a second derivative through them raises.
+
 Gradients come back in the operand's shape: an operand broadcast along its
 trailing feature axes gets its gradient summed over them (a segmented sum,
 ``segment_reduce``); other broadcast layouts raise DGLError in backward.
@@ -47,6 +50,7 @@ from __future__ import annotations
 
 import numpy as np
 import torch
+from torch.autograd.function import once_differentiable
 
 from .. import _lib
 from ..base import DGLError
@@ -161,6 +165,7 @@ class GSpMM(torch.autograd.Function):
         return out
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, grad_out):
         g, op, red = ctx.g, ctx.op, ctx.red
         x, y, arg_e = ctx.saved_tensors
@@ -275,6 +280,7 @@ class GSDDMM(torch.autograd.Function):
         return out
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, grad_out):
         g, op, tx, ty = ctx.g, ctx.op, ctx.tx, ctx.ty
         x, y = ctx.saved_tensors
@@ -383,6 +389,7 @@ class SegmentReduce(torch.autograd.Function):
         return out
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, grad_out):
         seg, vshape = ctx.seg, ctx.vshape
         n = vshape[0] if len(vshape) else 0
@@ -413,6 +420,7 @@ class SegmentSoftmax(torch.autograd.Function):
         return out
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, grad_out):
         (y,) = ctx.saved_tensors
         seg, shape = ctx.seg, tuple(y.shape)
@@ -439,6 +447,7 @@ class EdgeSoftmax(torch.autograd.Function):
         return out
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, grad_out):
         g, norm_by = ctx.g, ctx.norm_by
         (a,) = ctx.saved_tensors
@@ -540,6 +549,7 @@ class SegmentMM(torch.autograd.Function):
         return out
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, grad_out):
         a, b = _saved_operands(ctx)
         da, db = _grouped_grad(a, b, grad_out, ctx.sl, None, ctx.covered,
@@ -558,6 +568,7 @@ class GatherMM(torch.autograd.Function):
         return out
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, grad_out):
         a, b = _saved_operands(ctx)
         da, db = _grouped_grad(a, b, grad_out, None, ctx.idx, a.shape[0],

@@ -483,6 +483,19 @@ def test_segment_mm_and_gather_mm_gradcheck():
     torch.testing.assert_close(ga, b.detach()[idx].sum(-1), rtol=1e-12, atol=1e-12)
 
 
+def test_second_derivatives_raise():
+    """The backward passes are not themselves differentiable: asking for a
+    second derivative raises instead of returning a silently wrong one."""
+    u, v = graph_with_loops(20, 60, 95)
+    g = dgl.graph((u, v), num_nodes=20)
+    x = leaf((20, 3), 96)
+    y = leaf((u.size, 3), 97)
+    out = ops.u_mul_e_sum(g, x, y)
+    (gx,) = torch.autograd.grad(out.sum(), [x], create_graph=True)
+    with pytest.raises(RuntimeError):
+        gx.sum().backward()
+
+
 # ------------------------------------------------------------------ a GAT layer, float32
 def test_gat_layer_backward_float32():
     """gsddmm u_add_v -> leaky_relu -> edge_softmax -> gspmm u_mul_e_sum, and
