@@ -64,6 +64,12 @@ def needs_grad(*xs) -> bool:
         isinstance(x, torch.Tensor) and x.requires_grad for x in xs)
 
 
+def _gpu(t):
+    """A saved operand or an incoming gradient on the library's GPU (host
+    tensors copied): the backward kernels read device memory only."""
+    return None if t is None else t.to(_lib.device())
+
+
 def _code(t):
     return 0 if t.dtype == torch.float32 else 1
 
@@ -156,20 +162,21 @@ class GSpMM(torch.autograd.Function):
     def forward(ctx, g, op, red, x, y, replace_inf):
         from .spmm import _run
 
-        out, _, arg_e, _, _ = _run(g, op, red, x, y, replace_inf=replace_inf,
-                                   want_arg=red in ("max", "min"), arg_dtype=torch.int32)
+        out, _, arg_e, _, dev = _run(g, op, red, x, y, replace_inf=replace_inf,
+                                     want_arg=red in ("max", "min"), arg_dtype=torch.int32)
         ctx.g, ctx.op, ctx.red = g, op, red
         ctx.save_for_backward(x if isinstance(x, torch.Tensor) else None,
                               y if isinstance(y, torch.Tensor) else None, arg_e)
         ctx.out_shape = out.shape
-        return out
+        return _lib.give_back(out, True, dev)
 
     @staticmethod
     @once_differentiable
     def backward(ctx, grad_out):
         g, op, red = ctx.g, ctx.op, ctx.red
-        x, y, arg_e = ctx.saved_tensors
-        G = grad_out.contiguous()
+        x0, y0, arg_e = ctx.saved_tensors
+        x, y = _gpu(x0), _gpu(y0)
+        G = _gpu(grad_out).contiguous()
         need_x = ctx.needs_input_grad[3] and x is not None
         need_y = ctx.needs_input_grad[4] and y is not None
         dx = dy = None
@@ -183,7 +190,7 @@ class GSpMM(torch.autograd.Function):
 
                 fused = _mul_sum_dot(g, G, y, x) if _trailing_groups(x, y) else None
                 if fused is not None:
-                    return (None, None, None) + fused + (None,)
+                    return None, None, None, _back(fused[0], x0), _back(fused[1], y0), None
             if need_x:
                 if op in ("copy_lhs", "add", "sub"):
                     dx = _gspmm(g, "copy_lhs", "sum", G, None, kind="out")
@@ -226,7 +233,7 @@ class GSpMM(torch.autograd.Function):
             dx = dx.reshape(x.shape)
         if dy is not None:
             dy = dy.reshape(y.shape)
-        return None, None, None, dx, dy, None
+        return None, None, None, _back(dx, x0), _back(dy, y0), None
 
 
 def _trailing_groups(x, y):
@@ -283,8 +290,9 @@ class GSDDMM(torch.autograd.Function):
     @once_differentiable
     def backward(ctx, grad_out):
         g, op, tx, ty = ctx.g, ctx.op, ctx.tx, ctx.ty
-        x, y = ctx.saved_tensors
-        G = grad_out.contiguous()
+        x0, y0 = ctx.saved_tensors
+        x, y = _gpu(x0), _gpu(y0)
+        G = _gpu(grad_out).contiguous()
         need_x = ctx.needs_input_grad[2] and x is not None
         need_y = ctx.needs_input_grad[3] and y is not None
         dx = dy = None
@@ -310,7 +318,7 @@ class GSDDMM(torch.autograd.Function):
                 p = _scale(_gsddmm(g, "div", t, y, "e", ty), -1.0)
             p = _node_reduce(g, p, ty)
             dy = _reduce_to(p, _padded(y.shape, p.shape)).reshape(y.shape)
-        return None, None, dx, dy, None, None
+        return None, None, _back(dx, x0), _back(dy, y0), None, None
 
 
 def _group_softmax_grad(y, g, row_of, offsets, num_groups, order=None, out=None):
@@ -443,6 +451,7 @@ class EdgeSoftmax(torch.autograd.Function):
         keep = None if eids is None else {}
         out = _edge_softmax(g, logits, eids, norm_by, keep)
         ctx.g, ctx.norm_by, ctx.grouping = g, norm_by, keep
+        ctx.like = torch.empty(0, dtype=logits.dtype, device=logits.device)
         ctx.save_for_backward(out)
         return out
 
@@ -450,9 +459,11 @@ class EdgeSoftmax(torch.autograd.Function):
     @once_differentiable
     def backward(ctx, grad_out):
         g, norm_by = ctx.g, ctx.norm_by
-        (a,) = ctx.saved_tensors
+        (a0,) = ctx.saved_tensors
+        a, grad_out = _gpu(a0), _gpu(grad_out)
         if ctx.grouping is not None:
-            return None, _subset_softmax_grad(ctx.grouping, a, grad_out), None, None
+            dx = _subset_softmax_grad(ctx.grouping, a, grad_out)
+            return None, _back(dx, ctx.like), None, None
         E = a.shape[0]
         a2 = a.reshape(E, -1)
         G = grad_out.contiguous().reshape(E, -1)
@@ -466,7 +477,7 @@ class EdgeSoftmax(torch.autograd.Function):
         _lib.check(_lib.lib().mdgl_edge_softmax_grad(
             (vids if row == "v" else uids).data_ptr(), a2.data_ptr(), G.data_ptr(), s.data_ptr(),
             dx.data_ptr(), E, a2.shape[1], _code(a2), _lib.stream()), "edge_softmax_grad")
-        return None, dx.reshape(a.shape), None, None
+        return None, _back(dx.reshape(a.shape), ctx.like), None, None
 
 
 def _grouped_grad(a, b, grad_out, seglen, idx, covered, need_a, need_b):

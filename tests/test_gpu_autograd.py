@@ -483,6 +483,29 @@ def test_segment_mm_and_gather_mm_gradcheck():
     torch.testing.assert_close(ga, b.detach()[idx].sum(-1), rtol=1e-12, atol=1e-12)
 
 
+def test_cpu_tensors_take_part_in_autograd():
+    """Operands that live on the host (torch CPU tensors requiring grad):
+    results and gradients come back on the host, equal to the GPU run."""
+    u, v = graph_with_loops(30, 200, 98)
+    g = dgl.graph((u, v), num_nodes=30)
+    E = u.size
+    xg, yg = leaf((30, 2, 4), 99), leaf((E, 2, 1), 100)
+    xc = xg.detach().cpu().requires_grad_(True)
+    yc = yg.detach().cpu().requires_grad_(True)
+    lg = leaf((E, 2, 1), 101)
+    lc = lg.detach().cpu().requires_grad_(True)
+    for mine in ((xg, yg, lg), (xc, yc, lc)):
+        x, y, lo = mine
+        a = ops.edge_softmax(g, lo)
+        out = ops.u_mul_e_sum(g, x, y * a) + ops.copy_u_max(g, x)
+        e = ops.u_dot_v(g, x, x)
+        out.sum().backward()
+        e.sum().backward()
+    for gpu_t, cpu_t in ((xg, xc), (yg, yc), (lg, lc)):
+        assert cpu_t.grad.device.type == "cpu"
+        torch.testing.assert_close(cpu_t.grad, gpu_t.grad.cpu(), rtol=1e-12, atol=1e-12)
+
+
 def test_second_derivatives_raise():
     """The backward passes are not themselves differentiable: asking for a
     second derivative raises instead of returning a silently wrong one."""
