@@ -504,6 +504,21 @@ def test_cpu_tensors_take_part_in_autograd():
     for gpu_t, cpu_t in ((xg, xc), (yg, yc), (lg, lc)):
         assert cpu_t.grad.device.type == "cpu"
         torch.testing.assert_close(cpu_t.grad, gpu_t.grad.cpu(), rtol=1e-12, atol=1e-12)
+    # segment ops and the grouped GEMMs the same way
+    seglen = [3, 0, 5, 2]
+    vg, bg = leaf((10, 4), 102), leaf((4, 4, 3), 103)
+    vc = vg.detach().cpu().requires_grad_(True)
+    bc = bg.detach().cpu().requires_grad_(True)
+    idx = [0, 3, 3, 1, 2, 0, 1, 2, 3, 0]
+    for v_, b_ in ((vg, bg), (vc, bc)):
+        out = (ops.segment_reduce(seglen, v_, "max").sum() + ops.segment_softmax(seglen, v_).sum()
+               + (ops.segment_softmax(seglen, v_) * v_).sum()
+               + ops.segment_mm(v_, b_, seglen).sum() + ops.gather_mm(v_, b_, idx_b=idx).sum())
+        assert out.device == v_.device
+        out.backward()
+    for gpu_t, cpu_t in ((vg, vc), (bg, bc)):
+        assert cpu_t.grad.device.type == "cpu"
+        torch.testing.assert_close(cpu_t.grad, gpu_t.grad.cpu(), rtol=1e-12, atol=1e-12)
 
 
 def test_second_derivatives_raise():
