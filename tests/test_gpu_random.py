@@ -102,3 +102,29 @@ def check_case(seed):
 def test_random_cases(block):
     for seed in range(block * 50, (block + 1) * 50):
         check_case(seed)
+
+
+@pytest.mark.parametrize("block", range(2))
+def test_random_grouped_mm(block):
+    """gather_mm (both routes) and segment_mm over random row counts, widths
+    (odd, not multiples of 4, past one 128-wide tile) and block counts."""
+    for seed in range(block * 40, (block + 1) * 40):
+        rng = np.random.default_rng(5000 + seed)
+        dtype = np.float32 if rng.random() < 0.7 else np.float64
+        n = int(rng.integers(0, 6000))
+        d1 = int(rng.choice([1, 3, 4, 16, 32, 64, 96, 128, 130, 200]))
+        d2 = int(rng.choice([1, 2, 5, 16, 64, 128, 129, 256]))
+        r = int(rng.integers(1, 80))
+        a = rng.standard_normal((n, d1)).astype(dtype)
+        b = rng.standard_normal((r, d1, d2)).astype(dtype)
+        idx = rng.integers(0, r, n)
+        case = "seed {} {} n {} d1 {} d2 {} r {}".format(seed, dtype.__name__, n, d1, d2, r)
+        at, bt = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+        got = ops.gather_mm(at, bt, idx_b=torch.from_numpy(idx).cuda()).cpu().numpy()
+        close(got, oracle.gather_mm(a, b, idx, np.float64),
+              oracle.gather_mm(np.abs(a), np.abs(b), idx, np.float64), dtype, "gather " + case)
+        seglen = rng.multinomial(int(n * rng.random()), np.ones(r) / r)
+        got = ops.segment_mm(at, bt, seglen).cpu().numpy()
+        close(got, oracle.segment_mm(a, b, seglen, np.float64),
+              oracle.segment_mm(np.abs(a), np.abs(b), seglen, np.float64), dtype,
+              "segment " + case)
