@@ -119,6 +119,16 @@ class _DeviceCSR:
         self.params = int(chunk_len)
         self._softmax = {}
         self._slot_of_eid = None
+        self._split = {}
+
+    def chunks_for(self, chunk_len):
+        """The heavy-row schedule for another chunk length (cached)."""
+        if int(chunk_len) == self.chunks.chunk_len:
+            return self.chunks
+        got = self._split.get(int(chunk_len))
+        if got is None:
+            got = self._split[int(chunk_len)] = _Chunks(self.host_indptr, int(chunk_len))
+        return got
 
     def slot_of_eid(self):
         """The inverse of `eid`: the CSR slot of every edge id (cached)."""

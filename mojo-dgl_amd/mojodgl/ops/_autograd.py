@@ -108,10 +108,17 @@ def _edge_grad(g, grad, arg_e, mean, alpha):
     return out
 
 
+# Rows longer than this are split in the backward passes' reductions when
+# several rows share a wavefront (narrow features): on skewed degrees a
+# wavefront otherwise waits on its longest row (GAT backward on the power-law
+# graph: 24.4 -> 23.3 ms).
+NARROW_SPLIT = 64
+
+
 def _gspmm(g, op, red, x, y, kind="in"):
     from .spmm import _run
 
-    out, _, _, _, _ = _run(g, op, red, x, y, kind=kind)
+    out, _, _, _, _ = _run(g, op, red, x, y, kind=kind, narrow_split=NARROW_SPLIT)
     return out
 
 

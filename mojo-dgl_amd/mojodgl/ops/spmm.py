@@ -22,6 +22,14 @@ from .sddmm import _check_rows, feat_shape, out_feat_shape, reshape_lhs_rhs, sha
 __all__ = ["gspmm"]
 
 
+def _packed(dout, dtype):
+    """Whether several rows share a wavefront: a row's lanes (by the lane
+    width rule of mdgl_gspmm below) number 32 or fewer."""
+    vw = 4 if dtype == np.float32 else 2
+    vec = vw if dout % vw == 0 else (2 if dtype == np.float32 and dout % 2 == 0 else 1)
+    return -(-dout // vec) <= 32
+
+
 def _slabs(dout, dtype):
     """Column slabs of 64 lanes the kernel cuts an output row into (the lane
     width rule of mdgl_gspmm: 16-byte lanes, else 8-byte for even float32
@@ -32,11 +40,15 @@ def _slabs(dout, dtype):
 
 
 def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False,
-         arg_dtype=torch.int64, kind="in"):
+         arg_dtype=torch.int64, kind="in", narrow_split=None):
     """Validate, launch, and return device tensors (out, arg_u, arg_e) plus
     the caller-container info. `kind` "out" reduces over the out-CSR instead
     (the reversed graph: rows are sources, the node operand is read at the
-    destinations), which the backward passes use."""
+    destinations), which the backward passes use. `narrow_split`: when
+    several rows share a wavefront, split rows longer than this (instead of
+    the graph's chunk length) so a wavefront's rows have bounded lengths --
+    their sums then fold in chunks, within the tolerance rule rather than
+    bit for bit (the backward passes' reductions use it)."""
     if reduce_op not in REDUCERS:
         raise DGLError("reduce_op {} not recognized".format(reduce_op))
     if op not in list(BINARY_OPS) + ["copy_lhs", "copy_rhs"]:
@@ -87,6 +99,8 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
         rhs = _lib.on_device(R, dtype) if R is not None else None
         csr = g._device_csr(kind)
         sched = csr.chunks
+        if narrow_split and _packed(dout, dtype) and narrow_split < sched.chunk_len:
+            sched = csr.chunks_for(narrow_split)
         flags = _lib.REPLACE_INF if replace_inf else 0
         if rhs is not None and code not in (OP_COPY_LHS, OP_COPY_RHS) and dr == 1 \
                 and num_edges and _slabs(dout, dtype) > 1:
