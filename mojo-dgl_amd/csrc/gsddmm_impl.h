@@ -153,9 +153,18 @@ __global__ __launch_bounds__(BLOCK) void gsddmm_dot_kernel(GsddmmArgs<T> a) {
     task[u] = (wave * DOT_U + u) * per_round + grp;
     lp[u] = rp[u] = nullptr;
     if (task[u] < a.num_tasks) {
-      const int64_t e = task[u] / a.dout, col = task[u] % a.dout;
-      lp[u] = a.lhs + target_row(a.lt, a.uids, a.vids, e) * a.dl + bcast_off(a.bc, col, true) * a.red;
-      rp[u] = a.rhs + target_row(a.rt, a.uids, a.vids, e) * a.dr + bcast_off(a.bc, col, false) * a.red;
+      if (a.dout == 1) {
+        // one output column per edge (u_dot_v on (n, d) rows): the task is
+        // the edge and the broadcast offsets are 0 -- no 64-bit divides
+        lp[u] = a.lhs + target_row(a.lt, a.uids, a.vids, task[u]) * a.dl;
+        rp[u] = a.rhs + target_row(a.rt, a.uids, a.vids, task[u]) * a.dr;
+      } else {
+        const int64_t e = task[u] / a.dout, col = task[u] % a.dout;
+        lp[u] = a.lhs + target_row(a.lt, a.uids, a.vids, e) * a.dl +
+                bcast_off(a.bc, col, true) * a.red;
+        rp[u] = a.rhs + target_row(a.rt, a.uids, a.vids, e) * a.dr +
+                bcast_off(a.bc, col, false) * a.red;
+      }
     }
   }
   T part[DOT_U];
