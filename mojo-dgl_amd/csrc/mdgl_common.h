@@ -46,11 +46,16 @@ struct Bcast {
   int64_t rstride[MAX_DIMS];
 };
 
+// Every figure here (k, the dims, strides and the offset) is below a feature
+// row's width, which the C ABI keeps under 2 GiB, so the divides are 32-bit:
+// a 64-bit divide is several times the instructions, and kernels form these
+// offsets for every row or task.
 __host__ __device__ inline int64_t bcast_off(const Bcast& b, int64_t k, bool lhs) {
-  int64_t off = 0;
+  const uint32_t kk = (uint32_t)k;
+  uint32_t off = 0;
   for (int d = 0; d < b.nd; ++d) {
-    int64_t c = (k / b.div[d]) % b.shape[d];
-    off += c * (lhs ? b.lstride[d] : b.rstride[d]);
+    const uint32_t c = (kk / (uint32_t)b.div[d]) % (uint32_t)b.shape[d];
+    off += c * (uint32_t)(lhs ? b.lstride[d] : b.rstride[d]);
   }
   return off;
 }
