@@ -203,9 +203,10 @@ def workload_gat(args):
         "breakdown_ms": breakdown,
         "kernels": kernels,
     }
-    result["graph_build"] = time_graph_build(g, u, v, N, args)
-    result["edge_softmax_subset"] = time_subset_softmax(g, el, er, E, args)
-    result["forward_backward"] = time_gat_backward(g, el, er, h)
+    if not args.step_only:
+        result["graph_build"] = time_graph_build(g, u, v, N, args)
+        result["edge_softmax_subset"] = time_subset_softmax(g, el, er, E, args)
+        result["forward_backward"] = time_gat_backward(g, el, er, h)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_gat(g, el, er, h, args)
     return result
@@ -680,6 +681,10 @@ def main():
     ap.add_argument("--nodes", type=int, default=2_500_000)
     ap.add_argument("--edges", type=int, default=60_000_000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--step-only", action="store_true",
+                    help="skip the measurements outside the step (graph build, edge_softmax "
+                         "over a subset, forward + backward), so a profile holds the step's "
+                         "kernels only")
     ap.add_argument("--cpu-fraction", type=float, default=0.1)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", action="store_true",
