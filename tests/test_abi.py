@@ -159,3 +159,19 @@ def test_workspace_sizes(lib):
     assert lib.mdgl_gspmm_workspace_bytes(10, 64, 1, 1) >= 10 * 64 * (8 + 4 + 4)
     assert lib.mdgl_gather_mm_workspace_bytes(1000, 128, 128, 64, 0) >= 64 * 128 * 128 * 4 + 4000
     assert lib.mdgl_segment_mm_workspace_bytes(1000, 5, 3, 7, 1) > 0
+    # gradients: the forward's workspace for da (b's blocks as [D1][D2]), the
+    # grouping again for db, and one D1 x D2 partial per chunk of rows (at
+    # most n / 4096 + r chunks at 4096 rows; longer chunks keep the partials
+    # near 256 MB when D1 x D2 is large)
+    for gather in (False, True):
+        grad = lib.mdgl_gather_mm_grad_workspace_bytes if gather \
+            else lib.mdgl_segment_mm_grad_workspace_bytes
+        fwd = lib.mdgl_gather_mm_workspace_bytes if gather \
+            else lib.mdgl_segment_mm_workspace_bytes
+        n, d1, d2, r = 10 ** 7, 128, 128, 64
+        small = grad(n, d1, d2, r, 0)
+        assert small >= fwd(n, d2, d1, r, 0) + (n // 4096 + r) * d1 * d2 * 4
+        assert grad(2 * n, d1, d2, r, 0) >= small
+        wide = grad(n, 2048, 2048, r, 0)
+        assert wide - fwd(n, 2048, 2048, r, 0) < (1 << 28) + r * 2048 * 2048 * 4 + (1 << 27)
+        assert grad(n, d1, d2, r, 1) > small
