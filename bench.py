@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the message-passing kernel layer on one MI355X.
 
-Default workload (one "step"): the GAT attention layer on the power-law
+Headline workload (one "step"): the GAT attention layer on the power-law
 graph -- N = 2,500,000 nodes, E = 60,000,000 edges, in-degrees Zipf(2.1)
 capped at 20,000, uniform sources, H = 8 heads of 32 features, float32:
 
@@ -17,14 +17,26 @@ carries the roofline of the dominant kernel (gspmm, timed with HIP events on
 the stream it is launched on) and the CPU baseline (the oracle, a C++
 restatement of the reference's kernels, timed on this host on a sample).
 
-Other workloads (--workload c1|c3|c4|c5) print their own line; they are
-measurement runs for the other configurations, not the headline, and so is
---workload gat_train (the same layer with autograd: forward + backward).
+After the headline the default run measures every other configuration and
+adds them under "configs" (each op: HIP-event median and best over
+repetitions that each start with the L2 and the 256 MB MALL flushed by a
+512 MB write, algorithmic bytes or flops, the fraction of the HBM or MFMA
+peak, and the oracle's CPU rate on a stated sample):
+
+  c1  update_all u_mul_e + sum / mean / max / min, uniform 10k-node graph
+  c2_f64  gspmm u_mul_e_sum of the headline graph in float64
+  c3  GCN aggregation on a 50-block community graph (114M edges x 602)
+  c4  gsddmm u_dot_v (20M edges x 128), segment_reduce, segment_softmax
+  c5  gather_mm and segment_mm (1e7 rows, 128 x 128, 64 relations) on MFMA
+
+--workload c1|c3|c4|c5 runs one of them alone as its own line, and
+--workload gat_train the headline layer with autograd (forward + backward).
 """
 
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -38,10 +50,15 @@ for _p in (ROOT, os.path.join(ROOT, "mojo-dgl_amd")):
 import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
-# HBM bytes per launch of the gspmm kernel on the default workload, from
-# rocprofv3 FETCH_SIZE / WRITE_SIZE scaled by a 1 GiB copy (profiles/gat_power_law_kernels.md)
-GSPMM_TRAFFIC_BYTES = 72.35e9
 MFMA_F32_PEAK_TFLOPS = 157.3
+MFMA_F64_PEAK_TFLOPS = 78.6
+# HBM bytes per launch of the gspmm kernel on the headline workload, from
+# rocprofv3 FETCH_SIZE / WRITE_SIZE scaled by a 1 GiB copy
+GSPMM_TRAFFIC_BYTES = 72.35e9
+GSPMM_TRAFFIC_SOURCE = ("profiles/gat_power_law_kernels.md (rocprofv3 FETCH_SIZE and WRITE_SIZE "
+                        "of one launch, each scaled by the counter's reading for a 1 GiB copy); "
+                        "not measured in this run")
+FLUSH_BYTES = 512 << 20
 
 
 def log(*a):
@@ -135,6 +152,65 @@ def run_steps(step, steps, warmup, timer):
     return (t1 - t0) * 1e3 / steps
 
 
+class ColdTimer:
+    """Per-op GPU time: `warmup` untimed calls, then `reps` calls, each
+    between two HIP events on torch's current stream (where libmdgl
+    launches) and each after a 512 MB write that evicts the L2 and the
+    256 MB MALL; returns the median and the best in ms."""
+
+    def __init__(self, reps, warmup):
+        import torch
+
+        self.torch = torch
+        self.reps = max(1, int(reps))
+        self.warmup = max(0, int(warmup))
+        self.flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda")
+
+    def __call__(self, fn, flush=True):
+        torch = self.torch
+        for _ in range(self.warmup):
+            fn()
+        s = torch.cuda.Event(enable_timing=True)
+        t = torch.cuda.Event(enable_timing=True)
+        times = []
+        for _ in range(self.reps):
+            if flush:
+                self.flush.fill_(1)
+            s.record()
+            fn()
+            t.record()
+            t.synchronize()
+            times.append(s.elapsed_time(t))
+        return {"median_ms": round(float(np.median(times)), 4), "best_ms": round(min(times), 4)}
+
+
+def hbm_entry(times, nbytes, units=None, cache_note=False):
+    """One op's line: times, algorithmic bytes, GB/s and fraction of the
+    8 TB/s HBM peak at the median (and the edge-feature rate)."""
+    med = times["median_ms"]
+    out = dict(times)
+    out["bytes"] = int(nbytes)
+    gbs = nbytes / med / 1e6
+    out["GBps"] = round(gbs, 1)
+    out["frac"] = round(gbs / HBM_PEAK_GBS, 4)
+    if units is not None:
+        out["GEdge_feat_s"] = round(units / med / 1e6, 2)
+    if cache_note and gbs > HBM_PEAK_GBS:
+        out["cache_assisted"] = True
+    return out
+
+
+def mfma_entry(times, flops, nbytes, peak_tflops):
+    med = times["median_ms"]
+    out = dict(times)
+    out["flops"] = int(flops)
+    out["bytes"] = int(nbytes)
+    tf = flops / med / 1e9
+    out["TFLOPs"] = round(tf, 1)
+    out["frac"] = round(tf / peak_tflops, 4)
+    return out
+
+
 def cpu_cores():
     try:
         return len(os.sched_getaffinity(0))
@@ -142,7 +218,57 @@ def cpu_cores():
         return os.cpu_count() or 1
 
 
-# ---------------------------------------------------------------- workloads
+def cpu_rate(once, units, seconds, unit, sample, cores, scale=1e9):
+    """The oracle's rate on a sample: one warm-up, then repetitions until
+    `seconds` have passed (at least 3), best and median (the reference's
+    method, bench/profile_deep.py:29-34)."""
+    once()
+    times = []
+    while (sum(times) < seconds or len(times) < 3) and len(times) < 500:
+        t0 = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - t0)
+    best, med = min(times), float(np.median(times))
+    return {"value": round(units / best / scale, 4), "median_value": round(units / med / scale, 4),
+            "unit": unit, "cores": cores, "kind": "port",
+            "sample": "{}; best of {} repetitions ({:.1f} s)".format(sample, len(times),
+                                                                    sum(times))}
+
+
+def oracle_setup():
+    """The oracle with its static split at min(32, host cores) workers, as the
+    reference's 32 workers capped at what this host gives the process."""
+    import oracle
+
+    cores = min(32, cpu_cores())
+    oracle.set_workers(cores)
+    return oracle, oracle.lib(), cores
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def csr_sample(g, fraction):
+    """The first rows of g's in-CSR holding about `fraction` of the edges:
+    (rows, slots, indptr, indices, eid) as host int64 arrays."""
+    indptr, indices, eid = g._in_csr()
+    target = int(indices.size * fraction)
+    S = max(1, int(np.searchsorted(indptr, target)))
+    nnz = int(indptr[S])
+    return (S, nnz, np.ascontiguousarray(indptr[:S + 1]), np.ascontiguousarray(indices[:nnz]),
+            np.ascontiguousarray(eid[:nnz]))
+
+
+def free_gpu():
+    import torch
+
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+# ---------------------------------------------------------------- headline
 def workload_gat(args):
     import torch
 
@@ -169,6 +295,7 @@ def workload_gat(args):
         a = run("edge_softmax", lambda: ops.edge_softmax(g, e))
         return run("gspmm_u_mul_e_sum", lambda: ops.u_mul_e_sum(g, h, a))
 
+    log("timing the step")
     timer = OpTimer()
     ms = run_steps(step, args.steps, args.warmup, timer)
     units = E * H + E * H + E * H * D
@@ -198,17 +325,26 @@ def workload_gat(args):
                    "edge_feat_units_per_step": units, **gstats},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": args.traffic, "kernel": "gspmm u_mul_e_sum",
-                     "algorithmic_bytes": spmm_bytes, "avg_ms": round(spmm_ms, 4)},
+                     "traffic": args.traffic, "traffic_source": GSPMM_TRAFFIC_SOURCE,
+                     "kernel": "gspmm u_mul_e_sum", "algorithmic_bytes": spmm_bytes,
+                     "avg_ms": round(spmm_ms, 4)},
         "breakdown_ms": breakdown,
         "kernels": kernels,
     }
     if not args.step_only:
+        log("outside the step: graph build, edge_softmax over a subset, forward + backward")
         result["graph_build"] = time_graph_build(g, u, v, N, args)
         result["edge_softmax_subset"] = time_subset_softmax(g, el, er, E, args)
         result["forward_backward"] = time_gat_backward(g, el, er, h)
     if not args.no_cpu_baseline:
+        log("CPU baseline (oracle) of the step on a sample")
         result["cpu_baseline"] = cpu_baseline_gat(g, el, er, h, args)
+    if not args.headline_only:
+        del el, er
+        free_gpu()
+        result["c2_f64"] = section_c2_f64(g, h, args)
+    del g, h
+    free_gpu()
     return result
 
 
@@ -317,57 +453,43 @@ def cpu_baseline_gat(g, el, er, h, args):
     32-way static split capped at this host's cores) on the first rows of the
     destination CSR: their in-edges through gsddmm u_add_v, edge_softmax and
     gspmm u_mul_e_sum, kernel-only (prebuilt CSR, preallocated outputs)."""
-    import oracle
-
-    indptr, indices, eid = g._in_csr()
+    oracle, L, cores = oracle_setup()
     N = g.number_of_nodes()
-    target = int(indices.size * args.cpu_fraction)
-    S = int(np.searchsorted(indptr, target))
-    nnz = int(indptr[S])
+    S, nnz, ip, src, _ = csr_sample(g, args.cpu_fraction)
+    E = g.number_of_edges()
     H, D = 8, 32
     elh = el.reshape(N, H).cpu().numpy()
     erh = er.reshape(N, H).cpu().numpy()
     hh = h.reshape(N, H * D).cpu().numpy()
-    src = np.ascontiguousarray(indices[:nnz])
-    dst = np.repeat(np.arange(S, dtype=np.int64), np.diff(indptr[:S + 1]))
-    ip = np.ascontiguousarray(indptr[:S + 1])
+    dst = np.repeat(np.arange(S, dtype=np.int64), np.diff(ip))
     local = np.arange(nnz, dtype=np.int64)
-    cores = min(32, cpu_cores())
-    oracle.set_workers(cores)
-    L = oracle.lib()
     logits = np.empty((nnz, H), dtype=np.float32)
     soft = np.empty((nnz, H), dtype=np.float32)
     out = np.empty((S, H * D), dtype=np.float32)
     _, loff, roff, _ = oracle.bcast((N, H, D), (nnz, H, 1))
     deg = np.diff(ip)
     mask = np.ones(1, dtype=np.int8)
-    p = lambda a: a.ctypes.data  # noqa: E731
 
     def once():
-        L.oracle_gsddmm(p(src), p(dst), p(elh), p(erh), p(logits), nnz, 0, 1, 0, H, H, H, None,
-                        None, 1, 0)
+        L.oracle_gsddmm(_p(src), _p(dst), _p(elh), _p(erh), _p(logits), nnz, 0, 1, 0, H, H, H,
+                        None, None, 1, 0)
         np.maximum(logits, 0.2 * logits, out=logits)  # leaky_relu
-        L.oracle_edge_softmax(p(ip), p(local), p(mask), p(logits), p(soft), S, 1, H, 0)
-        L.oracle_gspmm(p(ip), p(src), p(local), p(hh), p(soft), p(out), S, 2, H * D, H, H * D, 0,
-                       p(deg), p(loff), p(roff), None, None, 0)
+        L.oracle_edge_softmax(_p(ip), _p(local), _p(mask), _p(logits), _p(soft), S, 1, H, 0)
+        L.oracle_gspmm(_p(ip), _p(src), _p(local), _p(hh), _p(soft), _p(out), S, 2, H * D, H,
+                       H * D, 0, _p(deg), _p(loff), _p(roff), None, None, 0)
 
-    once()  # warm-up
-    reps, t = 0, 0.0
-    while t < args.cpu_seconds and reps < 100:
-        t0 = time.perf_counter()
-        once()
-        t += time.perf_counter() - t0
-        reps += 1
-    units = nnz * (H + H + H * D)
-    return {"value": round(units * reps / t / 1e9, 4), "unit": "GEdge·feat/s", "cores": cores,
-            "kind": "port",
-            "sample": "the in-edges of the first {} destination rows ({} edges, {:.1%} of E) "
-                      "through gsddmm u_add_v, leaky_relu, edge_softmax and gspmm u_mul_e_sum in "
-                      "float32, {} repetitions, {:.1f} s".format(S, nnz, nnz / indices.size,
-                                                                  reps, t)}
+    return cpu_rate(once, nnz * (H + H + H * D), args.cpu_seconds, "GEdge·feat/s",
+                    "the in-edges of the first {} destination rows ({} edges, {:.1%} of E) "
+                    "through gsddmm u_add_v, leaky_relu, edge_softmax and gspmm u_mul_e_sum in "
+                    "float32".format(S, nnz, nnz / E), cores)
 
 
-def workload_c1(args):
+# ---------------------------------------------------------------- configs
+def section_c1(args):
+    """update_all u_mul_e with sum / mean / max / min on the uniform graph
+    (N = 10,000, E = 100,000, 64 features): warm back-to-back calls (the
+    step), each call alone with cold caches, the step replayed from a HIP
+    graph, and pull / numpy-input variants outside the step."""
     import torch
 
     import mojodgl as dgl
@@ -376,20 +498,33 @@ def workload_c1(args):
     N, E, D = 10_000, 100_000, 64
     u, v = uniform_graph(0, N, E)
     rng = np.random.default_rng(0)
+    hx = rng.standard_normal((N, D), dtype=np.float32)
+    ex = rng.random((E, D), dtype=np.float32)
     g = dgl.graph((u, v), num_nodes=N)
-    g.ndata["h"] = torch.from_numpy(rng.standard_normal((N, D), dtype=np.float32)).cuda()
-    g.edata["e"] = torch.from_numpy(rng.random((E, D), dtype=np.float32)).cuda()
+    g.ndata["h"] = torch.from_numpy(hx).cuda()
+    g.edata["e"] = torch.from_numpy(ex).cuda()
+    reds = ("sum", "mean", "max", "min")
+
+    def call(red):
+        g.update_all(fn.u_mul_e("h", "e", "m"), getattr(fn, red)("m", "z"))
 
     def step(t):
         run = t if t is not None else (lambda name, fn_: fn_())
-        for red in ("sum", "mean", "max", "min"):
-            run("update_all_" + red, lambda: g.update_all(fn.u_mul_e("h", "e", "m"),
-                                                          getattr(fn, red)("m", "z")))
+        for red in reds:
+            run("update_all_" + red, lambda: call(red))
 
     timer = OpTimer()
     ms = run_steps(step, args.steps, args.warmup, timer)
-    units = 4 * E * D
-    # the same step captured once in a HIP graph and replayed: the launches
+    units = E * D
+    base = 4 * (N + 1) + 8 * E + 4 * E * D + 4 * E * D + 4 * N * D
+    cold = ColdTimer(args.reps, 3)
+    ops_out = {}
+    for red in reds:
+        nbytes = base + (8 * N * D if red in ("max", "min") else 0)
+        ent = hbm_entry(cold(lambda: call(red)), nbytes, units)
+        ent["warm_ms"] = round(timer.avg_ms("update_all_" + red), 4)
+        ops_out["update_all_u_mul_e_" + red] = ent
+    # the four calls captured once in a HIP graph and replayed: the launches
     # without the Python dispatch (update_all makes no host syncs)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
@@ -404,27 +539,10 @@ def workload_c1(args):
     t.record()
     torch.cuda.synchronize()
     gms = s.elapsed_time(t) / args.steps
-    # each op again with cold caches: a 512 MB write before every call evicts
-    # L2 and the 256 MB MALL (the four calls above run cache-resident)
-    flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
-    cold = {}
-    for red in ("sum", "mean", "max", "min"):
-        tot = 0.0
-        for _ in range(args.steps):
-            flush.fill_(1)
-            s.record()
-            g.update_all(fn.u_mul_e("h", "e", "m"), getattr(fn, red)("m", "z"))
-            t.record()
-            torch.cuda.synchronize()
-            tot += s.elapsed_time(t)
-        cold["update_all_" + red] = round(tot / args.steps, 4)
-    # pull on every other node (the in-edges selected and the subgraph built
-    # on the GPU), and update_all with numpy features (copies to and from the
-    # GPU inside each call), outside the step
     pull_nodes = np.arange(0, N, 2)
     g2 = dgl.graph((u, v), num_nodes=N)
-    g2.ndata["h"] = g.ndata["h"].cpu().numpy()
-    g2.edata["e"] = g.edata["e"].cpu().numpy()
+    g2.ndata["h"] = hx
+    g2.edata["e"] = ex
     extra = {}
     for name, f in (("pull_u_mul_e_sum", lambda: g.pull(pull_nodes, fn.u_mul_e("h", "e", "m"),
                                                          fn.sum("m", "z"))),
@@ -437,18 +555,80 @@ def workload_c1(args):
             f()
         torch.cuda.synchronize()
         extra[name] = round((time.perf_counter() - t0) * 1e3 / args.steps, 4)
-    return {"metric": "gSpMM GEdge·feat/s, fp32, 1 GPU", "value": round(units / ms / 1e6, 2),
-            "unit": "GEdge·feat/s", "ms_per_step": round(ms, 4), "dtype": "f32",
-            "config": {"workload": "update_all u_mul_e + sum/mean/max/min, uniform graph",
-                       "num_nodes": N, "num_edges": E, "feat": D},
-            "breakdown_ms": {k: round(timer.avg_ms(k), 4) for k in timer.totals},
-            "graph_replay": {"ms_per_step": round(gms, 4),
-                             "value": round(units / gms / 1e6, 2)},
-            "cold_caches_ms": cold,
-            "outside_step_ms": extra}
+    out = {"workload": "update_all u_mul_e + sum/mean/max/min, uniform graph, float32",
+           "num_nodes": N, "num_edges": E, "feat": D,
+           "note": "cache-resident and launch-bound: 55-60 MB of algorithmic bytes per call",
+           "step_ms": round(ms, 4), "value": round(4 * units / ms / 1e6, 2),
+           "unit": "GEdge·feat/s", "ops": ops_out,
+           "graph_replay": {"ms_per_step": round(gms, 4),
+                            "value": round(4 * units / gms / 1e6, 2)},
+           "outside_step_ms": extra}
+    if not args.no_cpu_baseline:
+        oracle, L, cores = oracle_setup()
+        indptr, indices, eid = oracle.csr(u, v, N, "dst")
+        deg = np.diff(indptr)
+        z = np.empty((N, D), dtype=np.float32)
+        zr = np.empty_like(z)
+
+        def once():
+            for red in range(4):
+                L.oracle_gspmm(_p(indptr), _p(indices), _p(eid), _p(hx), _p(ex), _p(z), N, 2, D,
+                               D, D, red, _p(deg), None, None, None, None, 0)
+                if red in (1, 2):  # update_all's +-inf -> 0, a separate pass there
+                    L.oracle_replace_inf_with_zero(_p(z), _p(zr), z.size, 0)
+
+        out["cpu_baseline"] = cpu_rate(once, 4 * units, args.cpu_seconds_extra, "GEdge·feat/s",
+                                       "the whole graph, the four update_all reductions "
+                                       "kernel-only (gspmm, then +-inf -> 0 for max / min)",
+                                       cores)
+    return out
 
 
-def workload_c3(args):
+def section_c2_f64(g, h32, args):
+    """gspmm u_mul_e_sum of the headline graph in float64: h (N, 8, 32),
+    a (E, 8, 1)."""
+    import torch
+
+    import mojodgl.ops as ops
+
+    N, E, H, D = g.number_of_nodes(), g.number_of_edges(), 8, 32
+    log("float64 gspmm on the power-law graph")
+    h = h32.to(torch.float64)
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    a = torch.rand(E, H, 1, device="cuda", dtype=torch.float64, generator=gen)
+    cold = ColdTimer(args.reps, 2)
+    nbytes = 4 * (N + 1) + 8 * E + 8 * E * H * D + 8 * E * H + 8 * N * H * D
+    out = {"workload": "gspmm u_mul_e_sum, h (N, 8, 32) x a (E, 8, 1), float64, power-law graph",
+           "num_nodes": N, "num_edges": E,
+           "ops": {"gspmm_u_mul_e_sum": hbm_entry(cold(lambda: ops.u_mul_e_sum(g, h, a)), nbytes,
+                                                  E * H * D)}}
+    if not args.no_cpu_baseline:
+        oracle, L, cores = oracle_setup()
+        S, nnz, ip, src, eid = csr_sample(g, args.cpu_fraction)
+        hh = h.reshape(N, H * D).cpu().numpy()
+        ah = a.reshape(E, H).cpu().numpy()
+        z = np.empty((S, H * D), dtype=np.float64)
+        _, loff, roff, _ = oracle.bcast((N, H, D), (E, H, 1))
+        deg = np.diff(ip)
+
+        def once():
+            L.oracle_gspmm(_p(ip), _p(src), _p(eid), _p(hh), _p(ah), _p(z), S, 2, H * D, H,
+                           H * D, 0, _p(deg), _p(loff), _p(roff), None, None, 1)
+
+        out["cpu_baseline"] = cpu_rate(
+            once, nnz * H * D, args.cpu_seconds_extra, "GEdge·feat/s",
+            "the in-edges of the first {} destination rows ({} edges, {:.1%} of E) through gspmm "
+            "u_mul_e_sum in float64 (restated kernel + broadcast extension)".format(S, nnz,
+                                                                                 nnz / E), cores)
+    del h, a
+    free_gpu()
+    return out
+
+
+def section_c3(args):
+    """GCN aggregation on the community graph: u_mul_e_sum with
+    w = 1/sqrt(outdeg(u) indeg(v)) (E, 1), copy_u_mean, copy_u_max with
+    arg_u / arg_e."""
     import torch
 
     import mojodgl as dgl
@@ -461,77 +641,100 @@ def workload_c3(args):
     F = 602
     g = dgl.graph((u, v), num_nodes=N)
     g._device_csr("in")
-    indeg = np.maximum(g.in_degrees(), 1).astype(np.float64)
-    outdeg = np.maximum(g.out_degrees(), 1).astype(np.float64)
-    w = torch.from_numpy((1.0 / np.sqrt(outdeg[u] * indeg[v])).astype(np.float32)
-                         .reshape(E, 1)).cuda()
+    indeg = np.maximum(np.bincount(v, minlength=N), 1).astype(np.float64)
+    outdeg = np.maximum(np.bincount(u, minlength=N), 1).astype(np.float64)
+    wh = (1.0 / np.sqrt(outdeg[u] * indeg[v])).astype(np.float32).reshape(E, 1)
+    w = torch.from_numpy(wh).cuda()
     gen = torch.Generator(device="cuda").manual_seed(2)
     h = torch.randn(N, F, device="cuda", generator=gen)
-
-    def step(t):
-        run = t if t is not None else (lambda name, fn_: fn_())
-        run("u_mul_e_sum", lambda: ops.u_mul_e_sum(g, h, w))
-        run("copy_u_mean", lambda: ops.copy_u_mean(g, h))
-        run("copy_u_max_arg", lambda: spmm._run(g, "copy_lhs", "max", h, None, want_arg=True,
-                                                arg_dtype=torch.int32))
-
-    timer = OpTimer()
-    ms = run_steps(step, args.steps, args.warmup, timer)
-    units = 3 * E * F
+    calls = {
+        "u_mul_e_sum": lambda: ops.u_mul_e_sum(g, h, w),
+        "copy_u_mean": lambda: ops.copy_u_mean(g, h),
+        "copy_u_max_arg": lambda: spmm._run(g, "copy_lhs", "max", h, None, want_arg=True,
+                                            arg_dtype=torch.int32),
+    }
     b_mul = 4 * (N + 1) + 8 * E + 4 * E * F + 4 * E + 4 * N * F
     b_mean = 4 * (N + 1) + 4 * E + 4 * E * F + 4 * N * F
     b_max = b_mean + 4 * N * F
-    kern = {}
-    for name, b in (("u_mul_e_sum", b_mul), ("copy_u_mean", b_mean), ("copy_u_max_arg", b_max)):
-        m = timer.avg_ms(name)
-        kern[name] = {"ms": round(m, 3), "bytes": b, "GBps_algorithmic": round(b / m / 1e6, 1)}
-    return {"metric": "gSpMM GEdge·feat/s, fp32, 1 GPU", "value": round(units / ms / 1e6, 2),
-            "unit": "GEdge·feat/s", "ms_per_step": round(ms, 4), "dtype": "f32",
-            "config": {"workload": "GCN aggregation on a 50-block community graph",
-                       "num_nodes": N, "num_edges": E, "feat": F},
-            "kernels": kern}
+    cold = ColdTimer(args.reps, 2)
+    log("timing c3")
+    ops_out = {name: hbm_entry(cold(fn_), b, E * F, cache_note=True)
+               for (name, fn_), b in zip(calls.items(), (b_mul, b_mean, b_max))}
+    out = {"workload": "GCN aggregation on a 50-block community graph, float32",
+           "num_nodes": N, "num_edges": E, "feat": F,
+           "note": "95% of the edges stay inside 4,600-node blocks, so the L2 and the MALL serve "
+                   "most source rows: rates above the HBM peak are cache-assisted "
+                   "(compulsory bytes 2.48 GB)",
+           "ops": ops_out}
+    if not args.no_cpu_baseline:
+        oracle, L, cores = oracle_setup()
+        S, nnz, ip, src, eid = csr_sample(g, args.cpu_fraction_c3)
+        hh = h.cpu().numpy()
+        deg = np.diff(ip)
+        z = np.empty((S, F), dtype=np.float32)
+        zr = np.empty_like(z)
+        au = np.empty((S, F), dtype=np.int64)
+        ae = np.empty((S, F), dtype=np.int64)
+        loff = np.arange(F, dtype=np.int64)
+        roff = np.zeros(F, dtype=np.int64)
+
+        def once():
+            L.oracle_gspmm(_p(ip), _p(src), _p(eid), _p(hh), _p(wh), _p(z), S, 2, F, 1, F, 0,
+                           _p(deg), _p(loff), _p(roff), None, None, 0)
+            L.oracle_gspmm(_p(ip), _p(src), _p(eid), _p(hh), _p(hh), _p(z), S, 5, F, F, F, 3,
+                           _p(deg), None, None, None, None, 0)
+            L.oracle_gspmm(_p(ip), _p(src), _p(eid), _p(hh), _p(hh), _p(z), S, 5, F, F, F, 1,
+                           _p(deg), None, None, _p(au), _p(ae), 0)
+            L.oracle_replace_inf_with_zero(_p(z), _p(zr), z.size, 0)
+
+        out["cpu_baseline"] = cpu_rate(
+            once, 3 * nnz * F, args.cpu_seconds_extra, "GEdge·feat/s",
+            "the in-edges of the first {} destination rows ({} edges, {:.1%} of E) through "
+            "u_mul_e_sum (restated kernel + broadcast extension: w is (E, 1)), copy_u_mean and "
+            "copy_u_max with arg outputs, float32".format(S, nnz, nnz / E), cores)
+    del g, h, w, calls
+    free_gpu()
+    return out
 
 
-def workload_c4(args):
+def section_c4(args):
+    """gsddmm u_dot_v on a uniform graph (N = 1e6, E = 2e7, 128 features),
+    segment_reduce sum / max and segment_softmax over 1e6 Poisson(20)
+    segments of 16 columns, and the reference's array helpers at those
+    sizes."""
     import torch
 
     import mojodgl as dgl
     import mojodgl.ops as ops
+    from mojodgl import _lib
 
-    N, E = 1_000_000, 20_000_000
+    N, E, F = 1_000_000, 20_000_000, 128
+    log("generating uniform graph and segments")
     u, v = uniform_graph(3, N, E)
     g = dgl.graph((u, v), num_nodes=N)
     g._device_coo()
     gen = torch.Generator(device="cuda").manual_seed(3)
-    h = torch.randn(N, 128, device="cuda", generator=gen) * (1.0 / np.sqrt(128))
+    h = torch.randn(N, F, device="cuda", generator=gen) * (1.0 / np.sqrt(F))
     rng = np.random.default_rng(3)
     seglen = rng.poisson(20, 1_000_000)
+    S = seglen.size
     R = int(seglen.sum())
     val = torch.randn(R, 16, device="cuda", generator=gen)
     seglen_d = torch.from_numpy(seglen).cuda()  # lengths resident on the GPU like the values
-
-    def step(t):
-        run = t if t is not None else (lambda name, fn_: fn_())
-        run("u_dot_v", lambda: ops.u_dot_v(g, h, h))
-        run("segment_sum", lambda: ops.segment_reduce(seglen_d, val, "sum"))
-        run("segment_max", lambda: ops.segment_reduce(seglen_d, val, "max"))
-        run("segment_softmax", lambda: ops.segment_softmax(seglen_d, val))
-
-    timer = OpTimer()
-    ms = run_steps(step, args.steps, args.warmup, timer)
-    S = seglen.size
-    kern = {}
-    for name, b in (("u_dot_v", 8 * E + 4 * E * 128 * 2 + 4 * E),
-                    ("segment_sum", 4 * (S + 1) + 4 * R * 16 + 4 * S * 16),
-                    ("segment_max", 4 * (S + 1) + 4 * R * 16 + 4 * S * 16),
-                    ("segment_softmax", 4 * (S + 1) + 4 * R * 16 * 2)):
-        m = timer.avg_ms(name)
-        kern[name] = {"ms": round(m, 4), "bytes": b, "GBps": round(b / m / 1e6, 1)}
-    units = E * 128 + 3 * R * 16
-    # the reference's array helpers at the same sizes, outside the step:
-    # cumsum and clamp over the 1M int64 lengths, replace_inf over the values
-    from mojodgl import _lib
-
+    calls = {
+        "u_dot_v": (lambda: ops.u_dot_v(g, h, h), 8 * E + 4 * E * F * 2 + 4 * E, E * F),
+        "segment_reduce_sum": (lambda: ops.segment_reduce(seglen_d, val, "sum"),
+                               4 * (S + 1) + 4 * R * 16 + 4 * S * 16, R * 16),
+        "segment_reduce_max": (lambda: ops.segment_reduce(seglen_d, val, "max"),
+                               4 * (S + 1) + 4 * R * 16 + 4 * S * 16, R * 16),
+        "segment_softmax": (lambda: ops.segment_softmax(seglen_d, val),
+                            4 * (S + 1) + 4 * R * 16 * 2, R * 16),
+    }
+    cold = ColdTimer(args.reps, 3)
+    log("timing c4")
+    ops_out = {name: hbm_entry(cold(fn_), b, units) for name, (fn_, b, units) in calls.items()}
+    # the reference's array helpers at the same sizes: cumsum and clamp over
+    # the 1M int64 lengths, replace_inf over the values
     L = _lib.lib()
     lens = seglen_d.to(torch.int64).contiguous()
     ibuf = torch.empty_like(lens)
@@ -546,23 +749,116 @@ def workload_c4(args):
     }
     for name, (fn_, b) in helpers.items():
         assert fn_() == 0
-        torch.cuda.synchronize()
-        s_ = torch.cuda.Event(enable_timing=True)
-        t_ = torch.cuda.Event(enable_timing=True)
-        s_.record()
-        for _ in range(args.steps):
-            fn_()
-        t_.record()
-        torch.cuda.synchronize()
-        m = s_.elapsed_time(t_) / args.steps
-        kern[name] = {"ms": round(m, 4), "bytes": b, "GBps": round(b / m / 1e6, 1)}
-    return {"metric": "gSDDMM / segment GEdge·feat/s, fp32, 1 GPU",
-            "value": round(units / ms / 1e6, 2), "unit": "GEdge·feat/s",
-            "ms_per_step": round(ms, 4), "dtype": "f32",
-            "config": {"workload": "u_dot_v link scoring + segment_reduce sum/max + "
-                                   "segment_softmax", "num_nodes": N, "num_edges": E,
-                       "segments": S, "rows": R},
-            "kernels": kern}
+        ops_out[name] = hbm_entry(cold(fn_), b)
+    out = {"workload": "u_dot_v link scoring + segment_reduce sum/max + segment_softmax, float32",
+           "num_nodes": N, "num_edges": E, "segments": S, "rows": R, "ops": ops_out}
+    if not args.no_cpu_baseline:
+        oracle, Lo, cores = oracle_setup()
+        ne = int(E * args.cpu_fraction_c4)
+        hh = h.cpu().numpy()
+        us, vs = np.ascontiguousarray(u[:ne]), np.ascontiguousarray(v[:ne])
+        score = np.empty((ne, 1), dtype=np.float32)
+        ns = int(S * args.cpu_fraction_c4)
+        offs = oracle.offsets_of(seglen[:ns])
+        nr = int(offs[-1])
+        vh = val[:nr].cpu().numpy()
+        sred = np.empty((ns, 16), dtype=np.float32)
+        sres = np.empty_like(sred)
+        ssm = np.zeros((nr, 16), dtype=np.float32)
+
+        def once_dot():
+            Lo.oracle_gsddmm(_p(us), _p(vs), _p(hh), _p(hh), _p(score), ne, 0, 1, 4, F, F, 1,
+                             None, None, F, 0)
+
+        def once_seg():
+            Lo.oracle_segment_reduce(_p(offs), _p(vh), _p(sred), ns, 16, 0, nr, 0)
+            Lo.oracle_segment_reduce(_p(offs), _p(vh), _p(sred), ns, 16, 1, nr, 0)
+            Lo.oracle_replace_inf_with_zero(_p(sred), _p(sres), sred.size, 0)
+            Lo.oracle_segment_softmax(_p(offs), _p(vh), _p(ssm), ns, 16, nr, 0)
+
+        out["cpu_baseline"] = {
+            "u_dot_v": cpu_rate(once_dot, ne * F, args.cpu_seconds_extra, "GEdge·feat/s",
+                                "the first {} edges ({:.0%} of E), float32".format(
+                                    ne, ne / E), cores),
+            "segments": cpu_rate(once_seg, 3 * nr * 16, args.cpu_seconds_extra,
+                                 "G row·feat/s",
+                                 "the first {} segments ({} rows) through segment_reduce sum, "
+                                 "max (+ replace_inf) and segment_softmax, float32".format(ns, nr),
+                                 cores)}
+    del g, h, val, seglen_d, lens, ibuf, fbuf, calls, helpers
+    free_gpu()
+    return out
+
+
+def section_c5(args):
+    """gather_mm and segment_mm: a (1e7, 128), b (64, 128, 128), idx_b
+    uniform, seglen multinomial over Dirichlet(0.5) weights; the vendor BLAS
+    on one block of the same shape beside them; both gradients."""
+    import torch
+
+    import mojodgl.ops as ops
+
+    n, K, R = 10_000_000, 128, 64
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    a = torch.randn(n, K, device="cuda", generator=gen)
+    b = torch.randn(R, K, K, device="cuda", generator=gen) * (1.0 / np.sqrt(K))
+    rng = np.random.default_rng(4)
+    idx_h = rng.integers(0, R, n)
+    idx = torch.from_numpy(idx_h).cuda()
+    seglen = rng.multinomial(n, rng.dirichlet(0.5 * np.ones(R)))
+    flops = 2.0 * n * K * K
+    cold = ColdTimer(args.reps, 3)
+    log("timing c5")
+    ops_out = {
+        "gather_mm": mfma_entry(cold(lambda: ops.gather_mm(a, b, idx_b=idx)), flops,
+                                4 * n * K * 2 + 8 * n + 4 * R * K * K, MFMA_F32_PEAK_TFLOPS),
+        "segment_mm": mfma_entry(cold(lambda: ops.segment_mm(a, b, seglen)), flops,
+                                 4 * n * K * 2 + 4 * R * K * K + 8 * R, MFMA_F32_PEAK_TFLOPS),
+    }
+    # the vendor BLAS (torch.mm, full float32) on the same shape with one
+    # weight block and no grouping, for comparison
+    torch.backends.cuda.matmul.allow_tf32 = False
+    w0 = b[0].contiguous()
+    dst = torch.empty(n, K, device="cuda")
+    blas = mfma_entry(cold(lambda: torch.mm(a, w0, out=dst)), flops, 4 * n * K * 2 + 4 * K * K,
+                      MFMA_F32_PEAK_TFLOPS)
+    del dst
+    gg = torch.randn(n, K, device="cuda", generator=gen)
+    for name, fn_ in (("gather_mm", lambda x, y: ops.gather_mm(x, y, idx_b=idx)),
+                      ("segment_mm", lambda x, y: ops.segment_mm(x, y, seglen))):
+        m = time_grouped_backward(fn_, a, b, gg, args.steps)
+        ops_out[name]["backward"] = {"ms": round(m, 3), "TFLOPs": round(2 * flops / m / 1e9, 1)}
+    del gg
+    out = {"workload": "RGCN relation transform: gather_mm + segment_mm, float32",
+           "rows": n, "d1": K, "d2": K, "relations": R, "ops": ops_out,
+           "vendor_blas_one_block": blas}
+    if not args.no_cpu_baseline:
+        oracle, L, cores = oracle_setup()
+        ng = args.cpu_rows_c5
+        ah = a[:ng].cpu().numpy()
+        bh = b.cpu().numpy()
+        ih = np.ascontiguousarray(idx_h[:ng])
+        og = np.empty((ng, K), dtype=np.float32)
+        sl = (seglen * (args.cpu_rows_c5_serial / n)).astype(np.int64)
+        ns = int(sl.sum())
+        os_ = np.zeros((ns, K), dtype=np.float32)
+        ahs = np.ascontiguousarray(ah[:ns]) if ns <= ng else a[:ns].cpu().numpy()
+
+        def once_g():
+            L.oracle_gather_mm(_p(ah), _p(bh), _p(ih), _p(og), ng, K, K, 0)
+
+        def once_s():
+            L.oracle_segment_mm(_p(ahs), _p(bh), _p(os_), _p(sl), ns, K, R, K, 0)
+
+        out["cpu_baseline"] = {
+            "gather_mm": cpu_rate(once_g, 2.0 * ng * K * K, args.cpu_seconds_extra, "GFLOP/s",
+                                  "the first {} rows, float32".format(ng), cores),
+            "segment_mm": cpu_rate(once_s, 2.0 * ns * K * K, args.cpu_seconds_extra, "GFLOP/s",
+                                   "{} rows in 64 segments of the same proportions, float32; "
+                                   "serial, as the reference's kernel".format(ns), 1)}
+    del a, b, idx, w0
+    free_gpu()
+    return out
 
 
 def workload_gat_train(args):
@@ -610,66 +906,26 @@ def workload_gat_train(args):
             "breakdown_ms": {k: round(timer.avg_ms(k), 4) for k in timer.totals}}
 
 
-def workload_c5(args):
-    import torch
-
-    import mojodgl.ops as ops
-
-    n, K, R = 10_000_000, 128, 64
-    gen = torch.Generator(device="cuda").manual_seed(4)
-    a = torch.randn(n, K, device="cuda", generator=gen)
-    b = torch.randn(R, K, K, device="cuda", generator=gen) * (1.0 / np.sqrt(K))
-    rng = np.random.default_rng(4)
-    idx = torch.from_numpy(rng.integers(0, R, n)).cuda()
-    seglen = rng.multinomial(n, rng.dirichlet(0.5 * np.ones(R)))
-
-    def step(t):
-        run = t if t is not None else (lambda name, fn_: fn_())
-        run("gather_mm", lambda: ops.gather_mm(a, b, idx_b=idx))
-        run("segment_mm", lambda: ops.segment_mm(a, b, seglen))
-
-    timer = OpTimer()
-    ms = run_steps(step, args.steps, args.warmup, timer)
-    flops = 2.0 * n * K * K
-    # the vendor BLAS (torch.mm) on the same shape with one weight block and
-    # no grouping, for comparison (not part of the step)
-    torch.backends.cuda.matmul.allow_tf32 = False  # full float32, like the step
-    w0 = b[0].contiguous()
-    dst = torch.empty(n, K, device="cuda")
-    torch.mm(a, w0, out=dst)
-    torch.cuda.synchronize()
-    s = torch.cuda.Event(enable_timing=True)
-    t = torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(args.steps):
-        torch.mm(a, w0, out=dst)
-    t.record()
-    torch.cuda.synchronize()
-    blas_ms = s.elapsed_time(t) / args.steps
-    kern = {}
-    for name in ("gather_mm", "segment_mm"):
-        m = timer.avg_ms(name)
-        kern[name] = {"ms": round(m, 3), "TFLOPs": round(flops / m / 1e9, 1),
-                      "mfma_frac": round(flops / m / 1e9 / MFMA_F32_PEAK_TFLOPS, 4)}
-    # backward (not part of the step): both gradients, da = G b^T and
-    # db = a^T G per relation, 2 * flops
-    gg = torch.randn(n, K, device="cuda", generator=gen)
-    for name, fn_ in (("gather_mm", lambda x, y: ops.gather_mm(x, y, idx_b=idx)),
-                      ("segment_mm", lambda x, y: ops.segment_mm(x, y, seglen))):
-        m = time_grouped_backward(fn_, a, b, gg, args.steps)
-        kern[name]["backward"] = {"ms": round(m, 3), "TFLOPs": round(2 * flops / m / 1e9, 1)}
-    return {"metric": "gather_mm / segment_mm TFLOP/s, fp32, 1 GPU",
-            "value": round(2 * flops / ms / 1e9, 2), "unit": "TFLOP/s",
-            "ms_per_step": round(ms, 4), "dtype": "f32",
-            "config": {"workload": "RGCN relation transform: gather_mm + segment_mm",
-                       "rows": n, "d1": K, "d2": K, "relations": R},
-            "kernels": kern,
-            "vendor_blas_one_block": {"ms": round(blas_ms, 3),
-                                      "TFLOPs": round(flops / blas_ms / 1e9, 1)}}
+SECTIONS = {"c1": section_c1, "c3": section_c3, "c4": section_c4, "c5": section_c5}
 
 
-WORKLOADS = {"gat": workload_gat, "gat_train": workload_gat_train, "c1": workload_c1,
-             "c3": workload_c3, "c4": workload_c4, "c5": workload_c5}
+def workload_section(name):
+    """One configuration alone, printed as its own line."""
+
+    def run(args):
+        sec = SECTIONS[name](args)
+        ops_out = sec["ops"]
+        first = next(iter(ops_out.values()))
+        rate = ("TFLOPs", "TFLOP/s") if "TFLOPs" in first else ("GBps", "GB/s")
+        return {"metric": "{} per op, 1 GPU".format(rate[1]), "value": first[rate[0]],
+                "unit": rate[1], "ms_per_step": first["median_ms"], "dtype": "f32",
+                "config": {"workload": sec.pop("workload")}, **sec}
+
+    return run
+
+
+WORKLOADS = {"gat": workload_gat, "gat_train": workload_gat_train,
+             **{k: workload_section(k) for k in SECTIONS}}
 
 
 def main():
@@ -680,13 +936,22 @@ def main():
     ap.add_argument("--workload", default="gat", choices=sorted(WORKLOADS))
     ap.add_argument("--nodes", type=int, default=2_500_000)
     ap.add_argument("--edges", type=int, default=60_000_000)
+    ap.add_argument("--reps", type=int, default=20,
+                    help="cold-cache repetitions per op in the configuration sections")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="measure the GAT step only (no configuration sections)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--step-only", action="store_true",
                     help="skip the measurements outside the step (graph build, edge_softmax "
                          "over a subset, forward + backward), so a profile holds the step's "
                          "kernels only")
     ap.add_argument("--cpu-fraction", type=float, default=0.1)
+    ap.add_argument("--cpu-fraction-c3", type=float, default=0.01)
+    ap.add_argument("--cpu-fraction-c4", type=float, default=0.05)
+    ap.add_argument("--cpu-rows-c5", type=int, default=100_000)
+    ap.add_argument("--cpu-rows-c5-serial", type=int, default=20_000)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds-extra", type=float, default=3.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="finish with a 1 GiB device-to-device copy (counter calibration)")
     ap.add_argument("--traffic", type=float, default=GSPMM_TRAFFIC_BYTES,
@@ -702,7 +967,16 @@ def main():
         print("bench.py needs the GPU", file=sys.stderr)
         sys.exit(1)
     torch.cuda.set_device(0)
+    t_start = time.perf_counter()
     res = WORKLOADS[args.workload](args)
+    if args.workload == "gat" and not args.headline_only:
+        configs = {"c2_f64": res.pop("c2_f64")}
+        for name, fn_ in SECTIONS.items():
+            log("section", name)
+            configs[name] = fn_(args)
+        res["configs"] = {"c1": configs["c1"], "c2_f64": configs["c2_f64"],
+                          "c3": configs["c3"], "c4": configs["c4"], "c5": configs["c5"]}
+    res["bench_wall_s"] = round(time.perf_counter() - t_start, 1)
     if args.calibrate_copy:
         # a plain device copy of 1 GiB, for scaling rocprofv3 byte counters
         src = torch.empty(1 << 28, dtype=torch.float32, device="cuda")

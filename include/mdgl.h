@@ -63,9 +63,12 @@ int mdgl_cumsum(const int64_t* src, int64_t* dst, int64_t n, void* stream);
  * host: [0] + cumsum(seglen) and its checks, python/mojodgl/ops/segment.py:19-38;
  * no counterpart at its ABI): offsets[0] = 0, offsets[i + 1] = seglen[0] +
  * ... + seglen[i] (int32, valid when the total is below 2**31), and stats
- * (device, 3 int64) = (min length or 0 without segments, total, number of
+ * (device, 4 int64) = (min length or 0 without segments, total, number of
  * chunk_len-row chunks of the segments longer than chunk_len, 0 when
- * chunk_len <= 0). Workspace: mdgl_segment_offsets_workspace_bytes(num). */
+ * chunk_len <= 0, max length or 0 without segments). The total wraps
+ * around in int64 like the reference's cumsum: a caller checks min >= 0 and
+ * max <= the row count before trusting it. Workspace:
+ * mdgl_segment_offsets_workspace_bytes(num). */
 int mdgl_segment_offsets(const int64_t* seglen, int64_t num, int64_t chunk_len, int32_t* offsets,
                          int64_t* stats, void* workspace, int64_t workspace_bytes, void* stream);
 int64_t mdgl_segment_offsets_workspace_bytes(int64_t num);
@@ -319,6 +322,13 @@ int mdgl_rows_by_degree(const int32_t* indptr, const void* src, void* dst, int64
  * gspmm put in CSR slot order with idx = eid). No counterpart in the reference. */
 int mdgl_gather_rows(const void* src, const int32_t* idx, void* dst, int64_t n, int64_t width,
                      int dtype, void* stream);
+
+/* dst[idx[i], :] = src[i, :] for rows of `width` elements, the inverse of
+ * mdgl_gather_rows when idx is a permutation (rows of gather_mm's sorted
+ * route put back in their original order; with repeated indices which row
+ * lands is unspecified). No counterpart in the reference. */
+int mdgl_scatter_rows(const void* src, const int32_t* idx, void* dst, int64_t n, int64_t width,
+                      int dtype, void* stream);
 
 /* dst[i] = alpha * src[i]. */
 int mdgl_scale(const void* src, void* dst, int64_t n, double alpha, int dtype, void* stream);

@@ -116,7 +116,9 @@ __global__ __launch_bounds__(CS_THREADS) void cumsum_carry_kernel(int64_t* __res
   for (int64_t i = b * CS_TILE + threadIdx.x; i < end; i += CS_THREADS) dst[i] += carry;
 }
 
-template <class T>
+// Rows moved by an index: gather dst[i] = src[idx[i]] or, with SCATTER,
+// dst[idx[i]] = src[i] (a permutation's inverse when idx is one).
+template <class T, bool SCATTER>
 __global__ __launch_bounds__(BLOCK) void gather_rows_kernel(const T* __restrict__ src,
                                                             const int32_t* __restrict__ idx,
                                                             T* __restrict__ dst, int64_t n,
@@ -125,15 +127,18 @@ __global__ __launch_bounds__(BLOCK) void gather_rows_kernel(const T* __restrict_
   for (int64_t t = (int64_t)blockIdx.x * BLOCK + threadIdx.x; t < total;
        t += (int64_t)gridDim.x * BLOCK) {
     const int64_t i = t / width, k = t % width;
-    dst[t] = src[(int64_t)idx[i] * width + k];
+    if (SCATTER)
+      dst[(int64_t)idx[i] * width + k] = src[t];
+    else
+      dst[t] = src[(int64_t)idx[i] * width + k];
   }
 }
 
 // The same with 16-byte chunks (width a multiple of the chunk, buffers
 // 16-byte aligned): a chunk per thread, the row found by a shift when the
-// chunks per row are a power of two; the gathered source rows are ordinary
-// loads, the output goes out with streaming stores.
-template <class T, bool POW2>
+// chunks per row are a power of two; the rows addressed through idx use
+// ordinary accesses, the ones in order stream.
+template <class T, bool POW2, bool SCATTER>
 __global__ __launch_bounds__(BLOCK) void gather_rows_vec_kernel(const T* __restrict__ src,
                                                                 const int32_t* __restrict__ idx,
                                                                 T* __restrict__ dst, int64_t n,
@@ -145,8 +150,13 @@ __global__ __launch_bounds__(BLOCK) void gather_rows_vec_kernel(const T* __restr
     const int64_t i = POW2 ? (t >> shift) : t / cpr;
     const int64_t c = t - i * cpr;
     T x[VEC];
-    load_n<T, VEC>(src + ((int64_t)idx[i] * cpr + c) * VEC, x);
-    store_n_stream<T, VEC>(dst + t * VEC, x);
+    if (SCATTER) {
+      load_n_stream<T, VEC>(src + t * VEC, x);
+      store_n<T, VEC>(dst + ((int64_t)idx[i] * cpr + c) * VEC, x);
+    } else {
+      load_n<T, VEC>(src + ((int64_t)idx[i] * cpr + c) * VEC, x);
+      store_n_stream<T, VEC>(dst + t * VEC, x);
+    }
   }
 }
 
@@ -183,29 +193,33 @@ __device__ __forceinline__ int64_t seg_chunks(int64_t len, int64_t chunk_len) {
 
 __global__ __launch_bounds__(SEG_THREADS) void seg_partials_kernel(
     const int64_t* __restrict__ len, int64_t num, int64_t chunk_len, int64_t* __restrict__ tsum,
-    int64_t* __restrict__ tmin, int64_t* __restrict__ theavy) {
-  __shared__ int64_t ssum[SEG_THREADS], smin[SEG_THREADS], sheavy[SEG_THREADS];
+    int64_t* __restrict__ tmin, int64_t* __restrict__ theavy, int64_t* __restrict__ tmax) {
+  __shared__ int64_t ssum[SEG_THREADS], smin[SEG_THREADS], sheavy[SEG_THREADS],
+      smax[SEG_THREADS];
   const int t = threadIdx.x;
   const int64_t lo = (int64_t)blockIdx.x * SEG_TILE + (int64_t)t * SEG_PER;
-  int64_t s = 0, m = INT64_MAX, h = 0;
+  int64_t s = 0, m = INT64_MAX, h = 0, x = INT64_MIN;
   for (int k = 0; k < SEG_PER; ++k) {
     const int64_t i = lo + k;
     if (i < num) {
       const int64_t v = len[i];
       s += v;
       m = v < m ? v : m;
+      x = v > x ? v : x;
       h += seg_chunks(v, chunk_len);
     }
   }
   ssum[t] = s;
   smin[t] = m;
   sheavy[t] = h;
+  smax[t] = x;
   __syncthreads();
   for (int off = SEG_THREADS / 2; off > 0; off >>= 1) {
     if (t < off) {
       ssum[t] += ssum[t + off];
       smin[t] = smin[t + off] < smin[t] ? smin[t + off] : smin[t];
       sheavy[t] += sheavy[t + off];
+      smax[t] = smax[t + off] > smax[t] ? smax[t + off] : smax[t];
     }
     __syncthreads();
   }
@@ -213,41 +227,48 @@ __global__ __launch_bounds__(SEG_THREADS) void seg_partials_kernel(
     tsum[blockIdx.x] = ssum[0];
     tmin[blockIdx.x] = smin[0];
     theavy[blockIdx.x] = sheavy[0];
+    tmax[blockIdx.x] = smax[0];
   }
 }
 
 // One workgroup: tsum becomes the exclusive scan of the tile totals;
-// stats = (min length, total, chunks of the long segments); offsets[0] = 0.
-// With no tiles (no segments) the pointers to the tile arrays are unused.
+// stats = (min length, total, chunks of the long segments, max length);
+// offsets[0] = 0. With no tiles (no segments) the pointers to the tile
+// arrays are unused.
 __global__ __launch_bounds__(1024) void seg_tiles_kernel(int64_t* __restrict__ tsum,
                                                          const int64_t* __restrict__ tmin,
                                                          const int64_t* __restrict__ theavy,
+                                                         const int64_t* __restrict__ tmax,
                                                          int64_t tiles, int64_t* __restrict__ stats,
                                                          int32_t* __restrict__ offsets) {
-  __shared__ int64_t ssum[1024], smin[1024], sheavy[1024];
+  __shared__ int64_t ssum[1024], smin[1024], sheavy[1024], smax[1024];
   const int t = threadIdx.x;
   const int64_t span = (tiles + 1023) / 1024;
   const int64_t lo = t * span < tiles ? t * span : tiles;
   const int64_t hi = lo + span < tiles ? lo + span : tiles;
-  int64_t s = 0, m = INT64_MAX, h = 0;
+  int64_t s = 0, m = INT64_MAX, h = 0, x = INT64_MIN;
   for (int64_t i = lo; i < hi; ++i) {
     s += tsum[i];
     m = tmin[i] < m ? tmin[i] : m;
     h += theavy[i];
+    x = tmax[i] > x ? tmax[i] : x;
   }
   ssum[t] = s;
   smin[t] = m;
   sheavy[t] = h;
+  smax[t] = x;
   __syncthreads();
-  // inclusive scan of the span sums; min and heavy reduced alongside
+  // inclusive scan of the span sums; min, max and heavy reduced alongside
   for (int off = 1; off < 1024; off <<= 1) {
     const int64_t add = t >= off ? ssum[t - off] : 0;
     const int64_t om = t >= off ? smin[t - off] : INT64_MAX;
     const int64_t oh = t >= off ? sheavy[t - off] : 0;
+    const int64_t ox = t >= off ? smax[t - off] : INT64_MIN;
     __syncthreads();
     ssum[t] += add;
     smin[t] = om < smin[t] ? om : smin[t];
     sheavy[t] += oh;
+    smax[t] = ox > smax[t] ? ox : smax[t];
     __syncthreads();
   }
   int64_t acc = t > 0 ? ssum[t - 1] : 0;
@@ -261,6 +282,7 @@ __global__ __launch_bounds__(1024) void seg_tiles_kernel(int64_t* __restrict__ t
     stats[0] = tiles > 0 ? smin[1023] : 0;
     stats[1] = ssum[1023];
     stats[2] = sheavy[1023];
+    stats[3] = tiles > 0 ? smax[1023] : 0;
   }
 }
 
@@ -298,7 +320,7 @@ __global__ __launch_bounds__(SEG_THREADS) void seg_write_kernel(const int64_t* _
 
 int64_t segment_offsets_workspace_bytes(int64_t num) {
   const int64_t tiles = (num + SEG_TILE - 1) / SEG_TILE;
-  return tiles > 0 ? ((3 * tiles * 8 + 255) / 256) * 256 : 0;
+  return tiles > 0 ? ((4 * tiles * 8 + 255) / 256) * 256 : 0;
 }
 
 hipError_t launch_segment_offsets(const int64_t* len, int64_t num, int64_t chunk_len,
@@ -307,13 +329,14 @@ hipError_t launch_segment_offsets(const int64_t* len, int64_t num, int64_t chunk
   int64_t* tsum = static_cast<int64_t*>(ws);
   int64_t* tmin = tsum + tiles;
   int64_t* theavy = tmin + tiles;
+  int64_t* tmax = theavy + tiles;
   if (tiles > 0)
     hipLaunchKernelGGL(seg_partials_kernel, dim3((unsigned)tiles), dim3(SEG_THREADS), 0, s, len,
-                       num, chunk_len, tsum, tmin, theavy);
+                       num, chunk_len, tsum, tmin, theavy, tmax);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(seg_tiles_kernel, dim3(1), dim3(1024), 0, s, tsum, tmin, theavy, tiles,
-                     stats, offsets);
+  hipLaunchKernelGGL(seg_tiles_kernel, dim3(1), dim3(1024), 0, s, tsum, tmin, theavy, tmax,
+                     tiles, stats, offsets);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (tiles > 0)
@@ -349,34 +372,39 @@ hipError_t launch_clamp_i64(const int64_t* src, int64_t* dst, int64_t n, int64_t
   return hipGetLastError();
 }
 
-hipError_t launch_gather_rows(const void* src, const int32_t* idx, void* dst, int64_t n,
-                              int64_t width, int dtype, hipStream_t s) {
-  if (n <= 0 || width <= 0) return hipSuccess;
-  const int64_t total = n * width;
-  const int64_t vec = dtype == 0 ? 4 : 2;
+namespace {
+
+template <class T, bool SCATTER>
+void move_rows(const void* src, const int32_t* idx, void* dst, int64_t n, int64_t width,
+               hipStream_t s) {
+  const int64_t vec = 16 / sizeof(T);
   if (width % vec == 0 && aligned16(src) && aligned16(dst)) {
     const int64_t cpr = width / vec;
     int shift = 0;
     while (((int64_t)1 << shift) < cpr) ++shift;
     const bool pow2 = ((int64_t)1 << shift) == cpr;
-    const dim3 grid(grid_for(n * cpr));
-    if (dtype == 0) {
-      auto* f = pow2 ? gather_rows_vec_kernel<float, true> : gather_rows_vec_kernel<float, false>;
-      hipLaunchKernelGGL(f, grid, dim3(BLOCK), 0, s, static_cast<const float*>(src), idx,
-                         static_cast<float*>(dst), n, cpr, shift);
-    } else {
-      auto* f = pow2 ? gather_rows_vec_kernel<double, true> : gather_rows_vec_kernel<double, false>;
-      hipLaunchKernelGGL(f, grid, dim3(BLOCK), 0, s, static_cast<const double*>(src), idx,
-                         static_cast<double*>(dst), n, cpr, shift);
-    }
-    return hipGetLastError();
+    auto* f = pow2 ? gather_rows_vec_kernel<T, true, SCATTER>
+                   : gather_rows_vec_kernel<T, false, SCATTER>;
+    hipLaunchKernelGGL(f, dim3(grid_for(n * cpr)), dim3(BLOCK), 0, s,
+                       static_cast<const T*>(src), idx, static_cast<T*>(dst), n, cpr, shift);
+    return;
   }
-  if (dtype == 0)
-    hipLaunchKernelGGL(gather_rows_kernel<float>, dim3(grid_for(total)), dim3(BLOCK), 0, s,
-                       static_cast<const float*>(src), idx, static_cast<float*>(dst), n, width);
-  else
-    hipLaunchKernelGGL(gather_rows_kernel<double>, dim3(grid_for(total)), dim3(BLOCK), 0, s,
-                       static_cast<const double*>(src), idx, static_cast<double*>(dst), n, width);
+  hipLaunchKernelGGL((gather_rows_kernel<T, SCATTER>), dim3(grid_for(n * width)), dim3(BLOCK), 0,
+                     s, static_cast<const T*>(src), idx, static_cast<T*>(dst), n, width);
+}
+
+}  // namespace
+
+hipError_t launch_gather_rows(const void* src, const int32_t* idx, void* dst, int64_t n,
+                              int64_t width, int dtype, hipStream_t s, bool scatter) {
+  if (n <= 0 || width <= 0) return hipSuccess;
+  if (dtype == 0) {
+    if (scatter) move_rows<float, true>(src, idx, dst, n, width, s);
+    else move_rows<float, false>(src, idx, dst, n, width, s);
+  } else {
+    if (scatter) move_rows<double, true>(src, idx, dst, n, width, s);
+    else move_rows<double, false>(src, idx, dst, n, width, s);
+  }
   return hipGetLastError();
 }
 

@@ -257,6 +257,16 @@ int mdgl_gather_rows(const void* src, const int32_t* idx, void* dst, int64_t n, 
                     "gather_rows");
 }
 
+int mdgl_scatter_rows(const void* src, const int32_t* idx, void* dst, int64_t n, int64_t width,
+                      int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "scatter_rows: bad dtype %d", dtype);
+  if (n < 0 || width < 0) return fail(MDGL_EINVAL, "scatter_rows: negative size");
+  if (n == 0 || width == 0) return MDGL_OK;
+  if (!src || !idx || !dst) return fail(MDGL_EINVAL, "scatter_rows: null buffer");
+  return hip_status(launch_gather_rows(src, idx, dst, n, width, dtype, (hipStream_t)stream, true),
+                    "scatter_rows");
+}
+
 int mdgl_scale(const void* src, void* dst, int64_t n, double alpha, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "scale: bad dtype %d", dtype);
   if (n < 0) return fail(MDGL_EINVAL, "scale: n must be >= 0");

@@ -161,7 +161,7 @@ hipError_t launch_clamp_i64(const int64_t* src, int64_t* dst, int64_t n, int64_t
                             hipStream_t s);
 // dst[i, :] = src[idx[i], :] (rows of `width` elements; array.hip).
 hipError_t launch_gather_rows(const void* src, const int32_t* idx, void* dst, int64_t n,
-                              int64_t width, int dtype, hipStream_t s);
+                              int64_t width, int dtype, hipStream_t s, bool scatter = false);
 // dst[i] = the segment holding row i (offsets: num_seg + 1 entries; array.hip).
 hipError_t launch_segment_ids(const int32_t* offsets, int64_t num_seg, int64_t n, int32_t* dst,
                               hipStream_t s);

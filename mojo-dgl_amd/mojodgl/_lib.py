@@ -19,6 +19,7 @@ kernel raises RuntimeError.
 from __future__ import annotations
 
 import ctypes
+import hashlib
 import os
 import subprocess
 
@@ -98,18 +99,55 @@ _SIGNATURES = {
     "mdgl_rows_by_degree": ([_P, _P, _P, _I64, _I64, _C, _P], _C),
     "mdgl_scale": ([_P, _P, _I64, ctypes.c_double, _C, _P], _C),
     "mdgl_gather_rows": ([_P, _P, _P, _I64, _I64, _C, _P], _C),
+    "mdgl_scatter_rows": ([_P, _P, _P, _I64, _I64, _C, _P], _C),
     "mdgl_edge_softmax_grad": ([_P, _P, _P, _P, _P, _I64, _I64, _C, _P], _C),
 }
 
 
+def _sources_digest() -> str:
+    """sha256 of what libmdgl.so is built from, in the Makefile's order
+    (`STAMPED`: the csrc sources sorted by name, the C ABI header, the
+    Makefile); the build writes the same digest to LIB + '.sources'."""
+    names = sorted(n for n in os.listdir(CSRC) if n.endswith((".hip", ".h", ".cpp")))
+    paths = [os.path.join(CSRC, n) for n in names]
+    paths += [os.path.join(os.path.dirname(ROOT), "include", "mdgl.h"),
+              os.path.join(CSRC, "Makefile")]
+    h = hashlib.sha256()
+    for path in paths:
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+def is_current(path: str = None) -> bool:
+    """Whether the library at `path` (default LIB) exists and was built from
+    the sources as they are now."""
+    path = path or LIB
+    try:
+        with open(path + ".sources") as f:
+            stamp = f.read().strip()
+    except OSError:
+        return False
+    return os.path.exists(path) and stamp == _sources_digest()
+
+
 def build(force: bool = False) -> str:
-    """Compile csrc/ into lib/libmdgl.so with hipcc (make decides what is stale)."""
-    cmd = ["make", "-C", CSRC, "-j8"]
+    """Compile csrc/ into LIB with hipcc when it is missing or stale (its
+    source stamp differs from the sources), or always with `force`; as the
+    reference's build (_lib.py:89-110). MOJODGL_LIB names another output
+    path. Raises BuildError when the compiler fails."""
+    if not force and is_current():
+        return LIB
+    cmd = ["make", "-C", CSRC, "-j8", "OUT=" + os.path.abspath(LIB)]
     if force:
-        subprocess.run(["make", "-C", CSRC, "clean"], check=False, capture_output=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True, timeout=1800)
-    if proc.returncode != 0 or not os.path.exists(LIB):
-        raise BuildError((proc.stderr or proc.stdout).strip()[-4000:])
+        cmd.insert(1, "-B")
+    try:
+        proc = subprocess.run(cmd, capture_output=True, text=True, timeout=1800)
+    except OSError as exc:  # no make
+        raise BuildError("cannot run make: {}".format(exc)) from exc
+    if proc.returncode != 0 or not is_current():
+        raise BuildError("building {} failed:\n{}".format(
+            LIB, (proc.stderr or proc.stdout).strip()[-4000:]))
     return LIB
 
 
@@ -117,13 +155,11 @@ _lib = None
 
 
 def lib() -> ctypes.CDLL:
-    """The loaded libmdgl.so. It is never built implicitly: run `build()`."""
+    """The loaded libmdgl.so, built first if it is missing or stale (the
+    reference's lazy build, _lib.py:116-124)."""
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB):
-            raise BuildError(
-                "{} is missing; build it with mojodgl.build() or `make -C {}`".format(LIB, CSRC))
-        handle = ctypes.CDLL(LIB)
+        handle = ctypes.CDLL(build())
         for name, (argtypes, restype) in _SIGNATURES.items():
             fn = getattr(handle, name)
             fn.argtypes = argtypes

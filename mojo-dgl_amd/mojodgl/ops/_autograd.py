@@ -490,7 +490,7 @@ class EdgeSoftmax(torch.autograd.Function):
 def _grouped_grad(a, b, grad_out, seglen, idx, covered, need_a, need_b):
     """(da, db) of out[i] = a[i] @ b[g(i)] (segment_mm with `seglen`, gather_mm
     with `idx`): rows of a past `covered` (in no segment) get zero."""
-    from .gather_mm import GATHER_MAX_BLOCKS
+    from .gather_mm import GATHER_MAX_BLOCKS, group_rows, move_rows
 
     A, B = _lib.feature(a), _lib.feature(b)
     dtype = _lib.common_dtype(A, B)
@@ -509,15 +509,12 @@ def _grouped_grad(a, b, grad_out, seglen, idx, covered, need_a, need_b):
     G = grad_out.to(device=gdev, dtype=tdt).contiguous()
     L = _lib.lib()
     if idx is not None and r > GATHER_MAX_BLOCKS:
-        # too many blocks to bucket: rows sorted by block (stable), then the
+        # too many blocks to bucket: rows grouped by block (stably), then the
         # segment form, as the forward's sorted route
-        perm = torch.sort(idx, stable=True).indices
-        sl = torch.bincount(idx, minlength=r)
-        da_s, db = _grouped_grad(Ad.index_select(0, perm), Bd, G.index_select(0, perm), sl, None,
-                                 n, need_a, need_b)
-        if da is not None:
-            da.index_copy_(0, perm, da_s)
-        return da, db
+        perm, sl = group_rows(idx, r)
+        da_s, db = _grouped_grad(move_rows(Ad, perm), Bd, move_rows(G, perm), sl, None, n,
+                                 need_a, need_b)
+        return (move_rows(da_s, perm, scatter=True) if need_a else None), db
     if idx is not None:
         nbytes = L.mdgl_gather_mm_grad_workspace_bytes(n, d1, d2, r, code)
     else:

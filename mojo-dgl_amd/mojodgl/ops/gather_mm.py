@@ -1,10 +1,12 @@
 """gather_mm (reference python/mojodgl/ops/gather_mm.py).
 
 Same arguments and validation. Both of the reference's routes are kept and
-give the same numbers: above `_SEGMENT_BLOCK` (D1 * D2) the rows are sorted
-by `idx_b` (a stable sort, on the GPU) and multiplied with segment_mm, as the
-reference does; otherwise one mdgl_gather_mm call buckets the rows on the
-GPU and multiplies them block by block on the matrix cores.
+give the same numbers: above `_SEGMENT_BLOCK` (D1 * D2) the rows are grouped
+by `idx_b` (stably, as the reference's argsort: libmdgl's radix grouping,
+mdgl_build_csr), gathered in that order, multiplied with segment_mm and put
+back (mdgl_gather_rows / mdgl_scatter_rows), as the reference does;
+otherwise one mdgl_gather_mm call buckets the rows on the GPU and multiplies
+them block by block on the matrix cores.
 """
 
 from __future__ import annotations
@@ -26,6 +28,32 @@ _SEGMENT_BLOCK = int(os.environ.get("MOJODGL_GATHER_MM_SEGMENT_BLOCK", 16384))
 # b blocks the bucketed route takes (mdgl_gather_mm keeps 5 ints per block in
 # LDS); more go the sorted route
 GATHER_MAX_BLOCKS = 2048
+
+
+def group_rows(idx: torch.Tensor, num_groups: int):
+    """(perm, seglen) of the rows grouped by `idx` (a GPU int64 tensor with
+    values in [0, num_groups)): perm (int32) lists the rows of group 0, then
+    of group 1, ..., each group in row order -- numpy's stable argsort of idx
+    -- and seglen (int64) the group sizes; by libmdgl's stable radix
+    grouping (mdgl_build_csr with idx as the key)."""
+    from ..heterograph import build_device_csr
+
+    indptr, _, perm = build_device_csr(idx.to(torch.int32), None, num_groups)
+    return perm, (indptr[1:] - indptr[:-1]).to(torch.int64)
+
+
+def move_rows(x: torch.Tensor, perm: torch.Tensor, scatter: bool = False) -> torch.Tensor:
+    """Rows of the 2-D GPU tensor x taken in `perm`'s order (out[i] = x[perm[i]],
+    mdgl_gather_rows) or put back (out[perm[i]] = x[i], mdgl_scatter_rows)."""
+    x = x.contiguous()
+    out = torch.empty_like(x)
+    n, width = x.shape
+    code = _lib.FLOAT32 if x.dtype == torch.float32 else _lib.FLOAT64
+    L = _lib.lib()
+    fn = L.mdgl_scatter_rows if scatter else L.mdgl_gather_rows
+    _lib.check(fn(x.data_ptr(), perm.data_ptr(), out.data_ptr(), n, width, code, _lib.stream()),
+               "scatter_rows" if scatter else "gather_rows")
+    return out
 
 
 def gather_mm(a, b, *, idx_b):
@@ -81,16 +109,13 @@ def _gather_mm(a, b, idx_b):
         idx = torch.from_numpy(idx).to(_lib.device())
     as_torch, dev = _lib.wants_torch(A, B), _lib.out_device(A, B)
     if D1 * D2 > _SEGMENT_BLOCK or R > GATHER_MAX_BLOCKS:
-        # stable sort on the GPU: the same permutation as the reference's
-        # stable host argsort
-        perm = torch.sort(idx, stable=True).indices
-        seglen = torch.bincount(idx, minlength=R)
-        gdev = _lib.device()
-        a_sorted = _lib.on_device(A, _lib.common_dtype(A, B)).index_select(0, perm)
-        out_sorted = _grouped_mm(_lib.Feat(a_sorted, True, gdev), B, None, seglen, gather=False,
-                                 covered=N)
-        out = torch.empty_like(out_sorted)
-        out.index_copy_(0, perm, out_sorted)
+        # the rows grouped by block in a stable order: the reference's stable
+        # host argsort (gather_mm.py:79-87), on the GPU
+        perm, seglen = group_rows(idx, R)
+        a_sorted = move_rows(_lib.on_device(A, _lib.common_dtype(A, B)), perm)
+        out_sorted = _grouped_mm(_lib.Feat(a_sorted, True, _lib.device()), B, None, seglen,
+                                 gather=False, covered=N)
+        out = move_rows(out_sorted, perm, scatter=True)
     else:
         out = _grouped_mm(A, B, idx, None, gather=True, covered=N)
     return _lib.give_back(out, as_torch, dev), idx

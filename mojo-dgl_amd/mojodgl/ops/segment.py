@@ -27,6 +27,15 @@ def _offsets(seglen: np.ndarray) -> np.ndarray:
     return out
 
 
+def _check_lengths(seglen: np.ndarray, n: int) -> None:
+    """Each length in [0, n]: with that, the int64 offsets cannot wrap
+    around, so a sum that lands on n is the true sum."""
+    if seglen.size and (int(seglen.min()) < 0 or int(seglen.max()) > n):
+        raise DGLError(
+            "segment lengths must be non-negative and sum to {}, got lengths in [{}, {}]".format(
+                n, int(seglen.min()), int(seglen.max())))
+
+
 def _check_offsets(offsets, n):
     if offsets.size and (int(offsets[-1]) != n or bool(np.any(np.diff(offsets) < 0))):
         raise DGLError(
@@ -53,7 +62,7 @@ class _Segments:
             # then one small read back
             dev = sl.device
             off = torch.empty(self.num + 1, dtype=torch.int32, device=dev)
-            stats = torch.empty(3, dtype=torch.int64, device=dev)
+            stats = torch.empty(4, dtype=torch.int64, device=dev)
             L = _lib.lib()
             nbytes = L.mdgl_segment_offsets_workspace_bytes(self.num)
             ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes > 0 else None
@@ -61,17 +70,19 @@ class _Segments:
                                               off.data_ptr(), stats.data_ptr(), _lib.ptr(ws),
                                               max(nbytes, 0), _lib.stream()),
                        "segment_offsets")
-            low, total, heavy = stats.tolist()
-            if low < 0 or total != n:
+            low, total, heavy, high = stats.tolist()
+            # every length in [0, n] first: then the total cannot have wrapped
+            if low < 0 or high > n or total != n:
                 raise DGLError(
-                    "segment lengths must be non-negative and sum to {}, got offsets ending "
-                    "at {} for {} rows".format(n, total, n))
+                    "segment lengths must be non-negative and sum to {}, got lengths in "
+                    "[{}, {}] summing to {}".format(n, low, high, total))
             if chunk_len is not None:
                 self.heavy = heavy
             self.off = off
         else:
             sl = _lib.i64(seglen)
             self.num = sl.size
+            _check_lengths(sl, n)
             self.host = _offsets(sl)
             _check_offsets(self.host, n)
             self.off = None
@@ -288,9 +299,10 @@ def _segment_mm(a, b, seglen_a):
         raise DGLError("seglen_a must have one entry per b block: {} != {}".format(
             seglen_a.size, r))
     if seglen_a.size:
-        lo = int(seglen_a.min())
-        total = int(seglen_a.sum())
-        if lo < 0 or total > n:
+        lo, hi = int(seglen_a.min()), int(seglen_a.max())
+        # each length in [0, n] before the sum: no int64 wrap-around
+        total = int(seglen_a.sum()) if hi <= n else n + 1
+        if lo < 0 or hi > n or total > n:
             raise DGLError(
                 "segment lengths must be non-negative and sum to {}, got a minimum of {} and a "
                 "sum of {}".format(n, lo, total))

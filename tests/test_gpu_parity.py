@@ -497,7 +497,7 @@ def test_segment_gpu_lengths_are_validated():
 @pytest.mark.parametrize("num", [0, 1, 4095, 4096, 4097, 1_000_003])
 def test_segment_offsets_through_the_abi(num):
     """mdgl_segment_offsets: offsets equal [0] + cumsum (int32), stats equal
-    (min, sum, chunks of the long segments) from numpy."""
+    (min, sum, chunks of the long segments, max) from numpy."""
     from mojodgl import _lib
 
     rng = np.random.default_rng(70 + num)
@@ -508,7 +508,7 @@ def test_segment_offsets_through_the_abi(num):
     L = _lib.lib()
     sl = torch.from_numpy(seglen).cuda()
     off = torch.full((num + 1,), -5, dtype=torch.int32, device="cuda")
-    stats = torch.full((3,), -5, dtype=torch.int64, device="cuda")
+    stats = torch.full((4,), -5, dtype=torch.int64, device="cuda")
     nbytes = L.mdgl_segment_offsets_workspace_bytes(num)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
     for chunk_len in (0, 64):
@@ -519,7 +519,24 @@ def test_segment_offsets_through_the_abi(num):
         np.testing.assert_array_equal(off.cpu().numpy(), want)
         heavy = int(np.where(seglen > chunk_len, -(-seglen // chunk_len), 0).sum()) \
             if chunk_len else 0
-        assert stats.tolist() == [int(seglen.min()) if num else 0, int(seglen.sum()), heavy]
+        assert stats.tolist() == [int(seglen.min()) if num else 0, int(seglen.sum()), heavy,
+                                  int(seglen.max()) if num else 0]
+
+
+def test_wrapping_gpu_lengths_are_refused_before_any_launch():
+    """GPU lengths whose int64 sum wraps around to the row count: refused from
+    the offsets' stats (a length above the row count), before the segment
+    kernels run."""
+    n = 4
+    wrap = np.array([2 ** 62, 2 ** 62, 2 ** 62, 2 ** 62 + n], dtype=np.int64)
+    assert int(wrap.sum()) == n  # numpy's int64 sum wraps too
+    value = torch.ones(n, 3, device="cuda")
+    sl = torch.from_numpy(wrap).cuda()
+    for call in (lambda: ops.segment_reduce(sl, value, "sum"),
+                 lambda: ops.segment_reduce(sl, value, "max"),
+                 lambda: ops.segment_softmax(sl, value)):
+        with pytest.raises(dgl.DGLError, match="lengths"):
+            call()
 
 
 # ------------------------------------------------------------------ array helpers

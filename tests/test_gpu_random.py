@@ -76,7 +76,7 @@ def check_case(seed):
     got = (ops.edge_softmax(g, lt_, norm_by=norm_by) if eids is None
            else ops.edge_softmax(g, lt_, eids=eids, norm_by=norm_by)).cpu().numpy()
     ref = oracle.edge_softmax(u, v, n, logits, eids=eids, norm_by=norm_by, dtype=np.float64)
-    close(got, ref, np.ones_like(ref), dtype, "{}: edge_softmax {} {}".format(case, heads, norm_by))
+    close(got, ref, ref, dtype, "{}: edge_softmax {} {}".format(case, heads, norm_by))
 
     S = int(rng.integers(0, 2000))
     seglen = rng.poisson(float(rng.choice([1, 5, 20, 200])), S)
@@ -95,7 +95,7 @@ def check_case(seed):
                                                                                    d))
     got = ops.segment_softmax(sl, vt).cpu().numpy()
     ref = oracle.segment_softmax(seglen, val, dtype=np.float64)
-    close(got, ref, np.ones_like(ref), dtype, "{}: segment_softmax S {} d {}".format(case, S, d))
+    close(got, ref, ref, dtype, "{}: segment_softmax S {} d {}".format(case, S, d))
 
 
 @pytest.mark.parametrize("block", range(4))

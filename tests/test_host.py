@@ -163,6 +163,22 @@ def test_validation_errors_come_before_the_gpu():
             call()
 
 
+def test_wrapping_host_lengths_are_refused():
+    """Lengths whose int64 sum wraps around to the row count (each above the
+    row count): refused on the host before anything reaches the GPU."""
+    n = 4
+    wrap = np.array([2 ** 62, 2 ** 62, 2 ** 62, 2 ** 62 + n], dtype=np.int64)
+    assert int(wrap.sum()) == n
+    for call in (lambda: ops.segment_reduce(wrap, np.ones((n, 2)), "sum"),
+                 lambda: ops.segment_reduce(wrap, np.ones((n, 2)), "mean"),
+                 lambda: ops.segment_softmax(wrap, np.ones((n, 2))),
+                 lambda: ops.segment_mm(np.ones((n, 3)), np.ones((4, 3, 2)), wrap),
+                 lambda: ops.segment_mm(np.ones((n, 3)), np.ones((2, 3, 2)),
+                                        np.array([2 ** 63 - 1, 2], dtype=np.int64))):
+        with pytest.raises(dgl.DGLError, match="lengths"):
+            call()
+
+
 def test_no_gpu_means_a_loud_error():
     if torch.cuda.is_available():
         pytest.skip("a GPU is visible")
@@ -260,3 +276,92 @@ def test_fused_backward_takes_trailing_group_operands_only():
     assert _trailing_groups(torch.zeros(5, 64), torch.zeros(9, 1))
     assert _trailing_groups(torch.zeros(5, 64), torch.zeros(9))
     assert not _trailing_groups(torch.zeros(5, 1), torch.zeros(9, 1))
+
+
+def test_udf_batches_on_host_features():
+    g = dgl.graph((U, V))
+    x = np.arange(6, dtype=np.float64).reshape(3, 2)
+    w = np.arange(4, dtype=np.float32).reshape(4, 1) + 10
+    g.ndata["x"] = x
+    g.edata["w"] = w
+    edges = dgl.EdgeBatch(g, np.arange(4))
+    np.testing.assert_array_equal(edges.src["x"], x[U])
+    np.testing.assert_array_equal(edges.dst["x"], x[V])
+    np.testing.assert_array_equal(edges.data["w"], w)
+    assert "x" in edges.src and "w" in edges.data and "w" not in edges.src
+    assert set(edges.src) == {"x"} and len(edges.data) == 1
+    assert edges.number_of_edges == 4 and edges.number_of_nodes == 3
+    assert edges.batch_num_edges() == [4] and edges.batch_num_nodes() == [3]
+    sub = dgl.EdgeBatch(g, np.array([3, 3, 1]))  # a selection, repeats kept
+    np.testing.assert_array_equal(sub.src["x"], x[U[[3, 3, 1]]])
+    np.testing.assert_array_equal(sub.data["w"], w[[3, 3, 1]])
+    t = dgl.EdgeBatch(g, np.array([2, 0]))
+    g.ndata["y"] = torch.arange(6.0).reshape(3, 2)  # tensors are gathered as tensors
+    got = t.dst["y"]
+    assert isinstance(got, torch.Tensor)
+    np.testing.assert_array_equal(got.numpy(), np.arange(6.0).reshape(3, 2)[V[[2, 0]]])
+    nodes = dgl.NodeBatch(data={"h": x}, mailbox={"h": x + 1, "m": x * 2}, num_nodes=3)
+    np.testing.assert_array_equal(nodes["h"], x + 1)  # the mailbox is looked at first
+    np.testing.assert_array_equal(nodes["m"], x * 2)
+    np.testing.assert_array_equal(nodes.data["h"], x)
+    assert nodes.num_nodes() == 3 and nodes.batch_num_nodes() == [3]
+    with pytest.raises(KeyError):
+        nodes["missing"]
+    empty = dgl.NodeBatch(num_nodes=2)
+    assert dict(empty.mailbox) == {} and dict(empty.data) == {}
+
+
+def test_feature_store_mapping():
+    g = dgl.graph((U, V))
+    g.ndata["a"] = [[1], [2], [3]]
+    g.edata["b"] = np.ones((4, 2), dtype=np.float32)
+    assert len(g.ndata) == 1 and list(g.ndata) == ["a"] and "a" in g.ndata
+    assert g.ndata["a"].flags["C_CONTIGUOUS"] and g.ndata["a"].dtype == np.float64
+    assert set(g.edata.keys()) == {"b"} and len(g.edata.items()) == 1
+    assert g.ndata.pop("a").shape == (3, 1) and "a" not in g.ndata
+    assert g.ndata.pop("a", None) is None
+    g.ndata["c"] = np.zeros((3, 2))
+    del g.ndata["c"]
+    with pytest.raises(KeyError):
+        g.ndata["c"]
+    with pytest.raises(ValueError):
+        g.edata["b"] = np.ones((3, 2))
+    with pytest.raises(ValueError):
+        g.ndata["s"] = 1.0
+    with pytest.raises(ValueError):
+        g.ndata["t"] = torch.ones(2, 2)
+
+
+def test_library_build_stamp_matches_the_sources():
+    from mojodgl import _lib
+
+    path = _lib.build()  # builds only when missing or stale
+    assert path == _lib.LIB and _lib.is_current()
+    with open(path + ".sources") as f:
+        assert f.read().strip() == _lib._sources_digest()
+
+
+def test_missing_library_at_mojodgl_lib_is_built_or_refused(tmp_path):
+    """MOJODGL_LIB names the library (reference _lib.py:16); a missing one
+    is built there on first use (_lib.py:116-124), and a failed build is a
+    BuildError naming it. Here the compiler is replaced by /bin/false, so
+    the build must fail loudly and nothing is loaded."""
+    import os
+    import subprocess
+    import sys
+
+    target = tmp_path / "nowhere" / "libmdgl.so"
+    env = dict(os.environ, MOJODGL_LIB=str(target), HIPCC="/bin/false")
+    code = ("import sys; sys.path.insert(0, {!r})\n"
+            "from mojodgl import _lib\n"
+            "try:\n"
+            "    _lib.lib()\n"
+            "except _lib.BuildError as exc:\n"
+            "    print('BuildError', {!r} in str(exc))\n"
+            "else:\n"
+            "    print('loaded')\n").format(os.path.dirname(os.path.dirname(dgl.__file__)),
+                                            str(target))
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                         timeout=300)
+    assert out.stdout.strip() == "BuildError True", out.stdout + out.stderr
+    assert not target.exists()
