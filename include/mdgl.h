@@ -124,6 +124,31 @@ int mdgl_gspmm(const int32_t* indptr, const int32_t* indices, const int32_t* eid
 /* Workspace mdgl_gspmm needs for `num_chunks` chunk partials. */
 int64_t mdgl_gspmm_workspace_bytes(int64_t num_chunks, int64_t dout, int reduce_op, int dtype);
 
+/* Bytes of the device scratch array of mdgl_gspmm_noalloc: one per GPU the
+ * library runs on, held until the process ends. */
+#define MDGL_NOALLOC_SCRATCH_BYTES (64ll << 20)
+
+/* mdgl_gspmm without a workspace argument. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc); nothing in
+ * it allocates. Arguments and results are those of mdgl_gspmm; the heavy-row
+ * partials go to a fixed device array of MDGL_NOALLOC_SCRATCH_BYTES per GPU
+ * (the current device's: `stream` must belong to it). A call whose partials
+ * need more (mdgl_gspmm_workspace_bytes(num_chunks, dout, reduce_op, dtype)
+ * > MDGL_NOALLOC_SCRATCH_BYTES) returns MDGL_EWORKSPACE before launching.
+ * Every call on one GPU shares that GPU's array, which keeps the last call's
+ * contents (nothing in it needs to start at zero: a call writes every
+ * partial it reads), so calls that overlap on one GPU -- on different
+ * streams, or from threads without ordering -- race. */
+int mdgl_gspmm_noalloc(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
+                       const void* lhs, const void* rhs, void* dst, int64_t num_dst, int op,
+                       int64_t dl, int64_t dr, int64_t dout, int reduce_op, const int32_t* deg,
+                       int nd, const int64_t* lhs_shape, const int64_t* rhs_shape,
+                       int32_t* arg_u, int32_t* arg_e, const int32_t* chunk_row,
+                       const int32_t* chunk_start, int64_t num_chunks, int32_t chunk_len,
+                       const int32_t* heavy_rows, const int32_t* heavy_ptr, int64_t num_heavy,
+                       int flags, int dtype, void* stream);
+
 /* Replaces capi.mojo:119-129 (`mdgl_segment_reduce`): dst[s] = reduce of
  * value rows offsets[s]..offsets[s+1], in row order; mean divides by
  * max(length, 1) (= the reference's clamp(seglen, 1, n) divide,

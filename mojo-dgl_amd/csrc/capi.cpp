@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -908,3 +909,72 @@ int mdgl_gather_mm(const void* a, const void* b, const int64_t* idx_b, void* dst
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// mdgl_gspmm_noalloc: mdgl_gspmm with its heavy-row partials in a fixed device
+// array instead of a caller workspace, for callers that cannot allocate.
+//
+// `scratch` is a host-side stand-in for the device array: host code never
+// passes it to a kernel. Its device address is looked up once per device
+// (hipGetSymbolAddress, with that device current, on the entry point's first
+// call there) and kept in g_scratch_ptr; every use goes through that pointer.
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[MDGL_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES] = {};
+
+// The current device's scratch address, resolved on first use.
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "gspmm_noalloc: hipGetDevice");
+  if (dev < 0 || dev >= MAX_DEVICES)
+    return fail(MDGL_ENOTSUP, "gspmm_noalloc: device %d beyond the %d supported", dev,
+                MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e, "gspmm_noalloc: hipGetSymbolAddress(scratch)");
+    if (!p) return fail(MDGL_EWORKSPACE, "gspmm_noalloc: no device address for the scratch");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MDGL_OK;
+}
+
+}  // namespace
+
+extern "C" int mdgl_gspmm_noalloc(const int32_t* indptr, const int32_t* indices,
+                                  const int32_t* eid, const void* lhs, const void* rhs,
+                                  void* dst, int64_t num_dst, int op, int64_t dl, int64_t dr,
+                                  int64_t dout, int reduce_op, const int32_t* deg, int nd,
+                                  const int64_t* lhs_shape, const int64_t* rhs_shape,
+                                  int32_t* arg_u, int32_t* arg_e, const int32_t* chunk_row,
+                                  const int32_t* chunk_start, int64_t num_chunks,
+                                  int32_t chunk_len, const int32_t* heavy_rows,
+                                  const int32_t* heavy_ptr, int64_t num_heavy, int flags,
+                                  int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "gspmm_noalloc: bad dtype %d", dtype);
+  if (num_chunks < 0 || dout < 0) return fail(MDGL_EINVAL, "gspmm_noalloc: negative size");
+  if (!row_widths_fit(dout, dsize(dtype)) || num_chunks >= (int64_t(1) << 31))
+    return fail(MDGL_EINVAL, "gspmm_noalloc: rows too wide or too many chunks");
+  const int64_t need = mdgl_gspmm_workspace_bytes(num_chunks, dout, reduce_op, dtype);
+  if (need > MDGL_NOALLOC_SCRATCH_BYTES)
+    return fail(MDGL_EWORKSPACE, "gspmm_noalloc: %lld chunks of %lld columns need %lld bytes of "
+                "partials, the scratch holds %lld; use mdgl_gspmm with a workspace",
+                (long long)num_chunks, (long long)dout, (long long)need,
+                (long long)MDGL_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need > 0) {
+    int rc = scratch_of_current_device(&ws);
+    if (rc) return rc;
+  }
+  return gspmm_common(indptr, indices, eid, lhs, rhs, dst, num_dst, op, dl, dr, dout, reduce_op,
+                      deg, nd, lhs_shape, rhs_shape, arg_u, arg_e, chunk_row, chunk_start,
+                      num_chunks, chunk_len, heavy_rows, heavy_ptr, num_heavy, ws,
+                      need > 0 ? MDGL_NOALLOC_SCRATCH_BYTES : 0, flags, dtype, stream, false);
+}
