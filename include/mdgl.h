@@ -47,6 +47,11 @@ extern "C" {
 /* flags of mdgl_gspmm / mdgl_segment_reduce */
 #define MDGL_REPLACE_INF 1 /* +-inf results become 0 (heterograph.py:232-239) */
 #define MDGL_RHS_CSR_ORDER 2 /* mdgl_gspmm: rhs row i belongs to CSR slot i (not edge eid[i]) */
+/* mdgl_segment_reduce(_arg): the caller knows that no segment has more than
+ * MDGL_SEGMENT_SPLIT_ROWS rows, so the pass that splits longer segments is
+ * not launched (a longer segment is then still reduced whole, in row order) */
+#define MDGL_SEGMENTS_SHORT 4
+#define MDGL_SEGMENT_SPLIT_ROWS 4096
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* mdgl_last_error(void);
@@ -153,7 +158,11 @@ int mdgl_gspmm_noalloc(const int32_t* indptr, const int32_t* indices, const int3
  * value rows offsets[s]..offsets[s+1], in row order; mean divides by
  * max(length, 1) (= the reference's clamp(seglen, 1, n) divide,
  * segment.py:99-105). offsets has num_seg + 1 entries, non-decreasing, from
- * 0 to n. */
+ * 0 to n (each is clamped into [0, n]). flags: MDGL_REPLACE_INF,
+ * MDGL_SEGMENTS_SHORT. Segments longer than MDGL_SEGMENT_SPLIT_ROWS are
+ * reduced by a workgroup of row streams whose partials are added in a fixed
+ * order (max / min and their args unchanged, a sum to rounding); every
+ * other segment is folded row by row. */
 int mdgl_segment_reduce(const int32_t* offsets, const void* value, void* dst, int64_t num_seg,
                         int64_t d, int reduce_op, int64_t n, int flags, int dtype, void* stream);
 

@@ -567,40 +567,54 @@ int mdgl_gspmm_mul_sum_dot(const int32_t* indptr, const int32_t* indices, const 
                       workspace_bytes, 0, dtype, stream, false, rowop, dot);
 }
 
+namespace {
+
+// segment_reduce and its arg form (arg null: none)
+int segment_common(const char* what, const int32_t* offsets, const void* value, void* dst,
+                   int32_t* arg, int64_t num_seg, int64_t d, int reduce_op, int64_t n, int flags,
+                   int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "%s: bad dtype %d", what, dtype);
+  if (reduce_op < RED_SUM || reduce_op > RED_MEAN)
+    return fail(MDGL_EINVAL, "%s: bad reduce_op %d", what, reduce_op);
+  if (num_seg < 0 || d < 0 || n < 0) return fail(MDGL_EINVAL, "%s: negative size", what);
+  if (num_seg >= (int64_t(1) << 31) || n >= (int64_t(1) << 31))
+    return fail(MDGL_EINVAL, "%s: 2**31 or more segments or rows", what);
+  if (!row_widths_fit(d, dsize(dtype))) return fail(MDGL_EINVAL, "%s: rows too wide", what);
+  if (num_seg == 0 || d == 0) return MDGL_OK;
+  if (!offsets || !dst || (n > 0 && !value)) return fail(MDGL_EINVAL, "%s: null buffer", what);
+  SegmentParams p{};
+  p.offsets = offsets;
+  p.value = value;
+  p.out = dst;
+  p.arg = (reduce_op == RED_MAX || reduce_op == RED_MIN) ? arg : nullptr;
+  p.num_seg = num_seg;
+  p.n = n;
+  p.d = d;
+  p.red = reduce_op == RED_MEAN ? RED_SUM : reduce_op;
+  p.flags = (reduce_op == RED_MEAN ? F_MEAN : 0) | ((flags & MDGL_REPLACE_INF) ? F_REPLACE_INF : 0);
+  p.skip_long = (flags & MDGL_SEGMENTS_SHORT) ? 0 : 1;
+  p.stream = (hipStream_t)stream;
+  hipError_t e = dtype == MDGL_FLOAT32 ? launch_segment_reduce<float>(p)
+                                       : launch_segment_reduce<double>(p);
+  return hip_status(e, what);
+}
+
+}  // namespace
+
 int mdgl_segment_reduce(const int32_t* offsets, const void* value, void* dst, int64_t num_seg,
                         int64_t d, int reduce_op, int64_t n, int flags, int dtype, void* stream) {
-  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "segment_reduce: bad dtype %d", dtype);
-  if (reduce_op < RED_SUM || reduce_op > RED_MEAN)
-    return fail(MDGL_EINVAL, "segment_reduce: bad reduce_op %d", reduce_op);
-  if (num_seg < 0 || d < 0 || n < 0) return fail(MDGL_EINVAL, "segment_reduce: negative size");
-  if (num_seg >= (int64_t(1) << 31) || n >= (int64_t(1) << 31))
-    return fail(MDGL_EINVAL, "segment_reduce: 2**31 or more segments or rows");
-  if (!row_widths_fit(d, dsize(dtype))) return fail(MDGL_EINVAL, "segment_reduce: rows too wide");
-  if (num_seg == 0 || d == 0) return MDGL_OK;
-  if (!offsets || !dst || (n > 0 && !value)) return fail(MDGL_EINVAL, "segment_reduce: null buffer");
-  // a segment is a CSR row whose slots are the value rows themselves
-  return gspmm_common(offsets, nullptr, nullptr, value, value, dst, num_seg, OP_COPY_RHS, d, d, d,
-                      reduce_op, nullptr, 0, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
-                      0, 0, nullptr, nullptr, 0, nullptr, 0, flags, dtype, stream, true);
+  return segment_common("segment_reduce", offsets, value, dst, nullptr, num_seg, d, reduce_op, n,
+                        flags, dtype, stream);
 }
 
 int mdgl_segment_reduce_arg(const int32_t* offsets, const void* value, void* dst, int32_t* arg,
                             int64_t num_seg, int64_t d, int reduce_op, int64_t n, int flags,
                             int dtype, void* stream) {
-  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "segment_reduce_arg: bad dtype %d", dtype);
   if (reduce_op != RED_MAX && reduce_op != RED_MIN)
     return fail(MDGL_EINVAL, "segment_reduce_arg: reduce_op must be max or min, got %d", reduce_op);
-  if (num_seg < 0 || d < 0 || n < 0) return fail(MDGL_EINVAL, "segment_reduce_arg: negative size");
-  if (num_seg >= (int64_t(1) << 31) || n >= (int64_t(1) << 31))
-    return fail(MDGL_EINVAL, "segment_reduce_arg: 2**31 or more segments or rows");
-  if (!row_widths_fit(d, dsize(dtype)))
-    return fail(MDGL_EINVAL, "segment_reduce_arg: rows too wide");
-  if (num_seg == 0 || d == 0) return MDGL_OK;
-  if (!offsets || !dst || !arg || (n > 0 && !value))
-    return fail(MDGL_EINVAL, "segment_reduce_arg: null buffer");
-  return gspmm_common(offsets, nullptr, nullptr, value, value, dst, num_seg, OP_COPY_RHS, d, d, d,
-                      reduce_op, nullptr, 0, nullptr, nullptr, nullptr, arg, nullptr, nullptr, 0,
-                      0, nullptr, nullptr, 0, nullptr, 0, flags, dtype, stream, true);
+  if (num_seg > 0 && d > 0 && !arg) return fail(MDGL_EINVAL, "segment_reduce_arg: null buffer");
+  return segment_common("segment_reduce_arg", offsets, value, dst, arg, num_seg, d, reduce_op, n,
+                        flags, dtype, stream);
 }
 
 int mdgl_segment_ids(const int32_t* offsets, int64_t num_seg, int64_t n, int32_t* dst,

@@ -59,6 +59,25 @@ struct GspmmParams {
 template <class T, int RED>
 hipError_t launch_gspmm_red(const GspmmParams& p);
 
+// segment_reduce: out[s, k] = red over value rows offsets[s] .. offsets[s+1]
+// (segment_impl.h). red in {SUM, MAX, MIN}, mean is F_MEAN; arg (max / min,
+// optional) receives the selected row. Unless skip_long is 0, segments
+// longer than SEG_SPLIT_ROWS are reduced by a separate split pass.
+constexpr int SEG_SPLIT_ROWS = 4096;
+struct SegmentParams {
+  const int32_t* offsets;
+  const void* value;
+  void* out;
+  int32_t* arg;
+  int64_t num_seg, n, d;
+  int red, flags;
+  int skip_long;
+  hipStream_t stream;
+};
+
+template <class T>
+hipError_t launch_segment_reduce(const SegmentParams& p);
+
 // gsddmm: out[e, o] = op(lhs[t_l(e)], rhs[t_r(e)]) (or the dot over `red`).
 struct GsddmmParams {
   const int32_t* uids;

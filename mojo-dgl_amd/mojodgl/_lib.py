@@ -51,6 +51,8 @@ TARGETS = {"u": SRC_CODE, "v": DST_CODE, "e": EDGE_CODE}
 FLOAT32, FLOAT64 = 0, 1
 REPLACE_INF = 1
 RHS_CSR_ORDER = 2
+SEGMENTS_SHORT = 4  # mdgl_segment_reduce: no segment longer than SEGMENT_SPLIT_ROWS
+SEGMENT_SPLIT_ROWS = 4096
 EINVAL, EWORKSPACE, ENOTSUP = -1, -2, -3  # negative statuses of include/mdgl.h
 
 _P = ctypes.c_void_p

@@ -48,7 +48,8 @@ class _Segments:
     int64 host offsets when the lengths came from the host (None when they
     were a GPU tensor, whose offsets are formed and checked on the GPU with
     one small read back), `heavy` the number of chunks of `chunk_len` rows
-    the segments longer than `chunk_len` split into (GPU lengths only)."""
+    the segments longer than `chunk_len` split into (GPU lengths only),
+    `longest` the largest length."""
 
     def __init__(self, seglen, n, chunk_len=None):
         if isinstance(seglen, torch.Tensor) and seglen.device.type == "cuda":
@@ -78,11 +79,13 @@ class _Segments:
                     "[{}, {}] summing to {}".format(n, low, high, total))
             if chunk_len is not None:
                 self.heavy = heavy
+            self.longest = high
             self.off = off
         else:
             sl = _lib.i64(seglen)
             self.num = sl.size
             _check_lengths(sl, n)
+            self.longest = int(sl.max()) if sl.size else 0
             self.host = _offsets(sl)
             _check_offsets(self.host, n)
             self.off = None
@@ -152,6 +155,8 @@ def _segment_reduce(seglen, value, reducer, want_arg=False):
         val = _lib.on_device(V, dtype)
         off = seg.device()
         flags = _lib.REPLACE_INF if reducer in ("max", "min") else 0
+        if seg.longest <= _lib.SEGMENT_SPLIT_ROWS:
+            flags |= _lib.SEGMENTS_SHORT  # no split pass needed
         if want_arg and reducer in ("max", "min"):
             arg = torch.empty((num_seg, d), dtype=torch.int32, device=gdev)
             rc = _lib.lib().mdgl_segment_reduce_arg(off.data_ptr(), val.data_ptr(),

@@ -1,0 +1,164 @@
+"""segment_reduce's kernels: rows staged through LDS (narrow rows), row
+streams (wide rows) and the split pass for segments longer than
+MDGL_SEGMENT_SPLIT_ROWS, against the oracle under the tolerance rule of
+test_gpu_parity.py.
+
+Segments folded row by row (every segment when none is longer than the
+split threshold) are bit-identical to the oracle in the same precision;
+split segments are exact for max / min and their arg rows and within the
+tolerance for sums. The arg row is pinned by brute force: the first row of
+the segment holding the selected value (NaN never selected)."""
+
+import numpy as np
+import pytest
+import torch
+
+import mojodgl.ops as ops
+import oracle
+from mojodgl import _lib
+from test_gpu_parity import close
+
+pytestmark = pytest.mark.gpu
+
+SPLIT = 4096  # MDGL_SEGMENT_SPLIT_ROWS
+
+
+def lengths(rng, S, mean, long_rows=()):
+    seglen = rng.poisson(mean, S)
+    seglen[::11] = 0
+    for i, n in enumerate(long_rows):
+        seglen[(i * 37 + 5) % S] = n
+    return seglen
+
+
+def first_arg(seglen, value, reducer):
+    """Row of the first max / min of each segment and column (0 when empty)."""
+    off = np.concatenate([[0], np.cumsum(seglen)])
+    d = value.shape[1]
+    out = np.zeros((seglen.size, d), dtype=np.int64)
+    for s in range(seglen.size):
+        rows = value[off[s]:off[s + 1]]
+        if rows.shape[0] == 0:
+            continue
+        for k in range(d):
+            col = rows[:, k]
+            ok = ~np.isnan(col)
+            if not ok.any():
+                continue
+            best = np.max(col[ok]) if reducer == "max" else np.min(col[ok])
+            if np.isinf(best) and (best < 0 if reducer == "max" else best > 0):
+                continue  # never beats the identity
+            out[s, k] = off[s] + int(np.nonzero(col == best)[0][0])
+    return out
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("d", [1, 2, 3, 5, 16, 33, 64, 130, 602])
+@pytest.mark.parametrize("reducer", ["sum", "max", "mean"])
+def test_segment_reduce_widths_bit_exact(dtype, d, reducer):
+    """No segment above the split threshold: every kernel folds row by row."""
+    rng = np.random.default_rng(d * 3 + len(reducer))
+    S = 1500 if d < 100 else 300
+    seglen = lengths(rng, S, 20, long_rows=(SPLIT, 1000))
+    value = rng.standard_normal((int(seglen.sum()), d)).astype(dtype)
+    for lens in (seglen, torch.from_numpy(seglen).cuda()):
+        got = ops.segment_reduce(lens, torch.from_numpy(value).cuda(), reducer)
+        np.testing.assert_array_equal(got.cpu().numpy(),
+                                      oracle.segment_reduce(seglen, value, reducer, dtype),
+                                      err_msg="{} d {}".format(reducer, d))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("d", [1, 3, 16, 40, 300])
+def test_segment_reduce_long_segments_split(dtype, d):
+    """Segments above the split threshold (one of them 1M rows for narrow
+    rows) among short ones: max / min exact, sums within the tolerance,
+    the short segments still bit-identical."""
+    rng = np.random.default_rng(100 + d)
+    big = (1_000_000, SPLIT + 1, 9000) if d <= 16 else (SPLIT + 1, 20000)
+    seglen = lengths(rng, 700, 15, long_rows=big)
+    value = rng.standard_normal((int(seglen.sum()), d)).astype(dtype)
+    vt = torch.from_numpy(value).cuda()
+    short = seglen <= SPLIT
+    for lens in (seglen, torch.from_numpy(seglen).cuda()):
+        for reducer in ("sum", "mean", "max", "min"):
+            got = ops.segment_reduce(lens, vt, reducer).cpu().numpy()
+            same = oracle.segment_reduce(seglen, value, reducer, dtype)
+            if reducer in ("max", "min"):
+                np.testing.assert_array_equal(got, same, err_msg=reducer)
+            else:
+                np.testing.assert_array_equal(got[short], same[short], err_msg=reducer)
+                ref = oracle.segment_reduce(seglen, value, reducer, np.float64)
+                bound = oracle.segment_reduce(seglen, np.abs(value), reducer, np.float64)
+                close(got, ref, bound, dtype, "segment_reduce {} d {}".format(reducer, d))
+
+
+@pytest.mark.parametrize("d", [1, 4, 16, 33, 200])
+def test_segment_reduce_arg_rows(d):
+    """mdgl_segment_reduce_arg: the selected row is the first reaching the
+    value, in folded and in split segments, with ties and NaN present."""
+    rng = np.random.default_rng(200 + d)
+    seglen = lengths(rng, 400, 12, long_rows=(SPLIT + 300, 7000))
+    n = int(seglen.sum())
+    value = np.round(rng.standard_normal((n, d)) * 2).astype(np.float32)  # many ties
+    value[rng.random((n, d)) < 0.05] = np.nan
+    off = torch.from_numpy(np.concatenate([[0], np.cumsum(seglen)]).astype(np.int32)).cuda()
+    vt = torch.from_numpy(value).cuda()
+    L = _lib.lib()
+    for reducer in ("max", "min"):
+        for flags in (0, _lib.SEGMENTS_SHORT):  # split pass, or every segment folded whole
+            out = torch.empty(seglen.size, d, device="cuda")
+            arg = torch.full((seglen.size, d), -9, dtype=torch.int32, device="cuda")
+            rc = L.mdgl_segment_reduce_arg(off.data_ptr(), vt.data_ptr(), out.data_ptr(),
+                                           arg.data_ptr(), seglen.size, d,
+                                           _lib.REDUCERS[reducer], n, flags, _lib.FLOAT32,
+                                           _lib.stream())
+            _lib.check(rc, "segment_reduce_arg")
+            want = oracle.segment_reduce(seglen, value, reducer, np.float32)
+            got = out.cpu().numpy()
+            got = np.where(np.isinf(got), 0, got)  # the oracle's +-inf -> 0
+            np.testing.assert_array_equal(got, want, err_msg="{} {}".format(reducer, flags))
+            np.testing.assert_array_equal(arg.cpu().numpy(), first_arg(seglen, value, reducer),
+                                          err_msg="{} args {}".format(reducer, flags))
+
+
+def test_short_segment_hint_is_only_a_hint():
+    """MDGL_SEGMENTS_SHORT with a segment above the threshold: that segment is
+    folded whole, in row order (bit-identical), not skipped."""
+    rng = np.random.default_rng(300)
+    seglen = lengths(rng, 300, 10, long_rows=(20000,))
+    n = int(seglen.sum())
+    value = rng.standard_normal((n, 8)).astype(np.float32)
+    off = torch.from_numpy(np.concatenate([[0], np.cumsum(seglen)]).astype(np.int32)).cuda()
+    vt = torch.from_numpy(value).cuda()
+    out = torch.full((seglen.size, 8), float("nan"), device="cuda")
+    rc = _lib.lib().mdgl_segment_reduce(off.data_ptr(), vt.data_ptr(), out.data_ptr(), seglen.size,
+                                        8, _lib.REDUCERS["sum"], n, _lib.SEGMENTS_SHORT,
+                                        _lib.FLOAT32, _lib.stream())
+    _lib.check(rc, "segment_reduce")
+    np.testing.assert_array_equal(out.cpu().numpy(),
+                                  oracle.segment_reduce(seglen, value, "sum", np.float32))
+
+
+def test_segment_reduce_clamps_offsets_into_the_rows():
+    """Offsets past the row count (here only through the C ABI: the API
+    refuses them) read as segments clipped to the rows, never beyond."""
+    rng = np.random.default_rng(301)
+    n, d = 5000, 16
+    value = rng.standard_normal((n, d)).astype(np.float32)
+    raw = np.array([0, 100, 4000, 6000, 9000, 200], dtype=np.int32)  # ends past n, one backwards
+    off = torch.from_numpy(raw).cuda()
+    out = torch.empty(raw.size - 1, d, device="cuda")
+    rc = _lib.lib().mdgl_segment_reduce(off.data_ptr(), torch.from_numpy(value).cuda().data_ptr(),
+                                        out.data_ptr(), raw.size - 1, d, _lib.REDUCERS["max"], n, 0,
+                                        _lib.FLOAT32, _lib.stream())
+    _lib.check(rc, "segment_reduce")
+    clipped = np.clip(raw.astype(np.int64), 0, n)
+    lens = np.maximum(np.diff(clipped), 0)
+    lens[-1] = 0
+    starts = clipped[:-1]
+    got = out.cpu().numpy()
+    for s in range(raw.size - 1):
+        rows = value[starts[s]:starts[s] + lens[s]]
+        want = rows.max(axis=0) if lens[s] else np.full(d, -np.inf, dtype=np.float32)
+        np.testing.assert_array_equal(got[s], want, err_msg=str(s))
