@@ -36,7 +36,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+# MDGL_ORACLE_LIB names another build of mdgl_oracle.cpp (the sanitizer build of the tests)
+LIB_PATH = os.environ.get("MDGL_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 
 SRC, DST, EDGE = 0, 1, 2
 OPS = {"add": 0, "sub": 1, "mul": 2, "div": 3, "dot": 4, "copy_lhs": 5, "copy_rhs": 6}
