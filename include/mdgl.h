@@ -106,7 +106,9 @@ int mdgl_gsddmm(const int32_t* uids, const int32_t* vids, const void* lhs, const
  * (0, -inf, +inf) unless MDGL_REPLACE_INF is set.
  * Extensions: broadcasting as in mdgl_gsddmm; arg_u / arg_e (nullable, max
  * and min only) receive the source node and edge id of the selected message
- * (the first in CSR order among ties, 0 for an empty row); rows longer than
+ * (the first in CSR order among ties; -1 when no message was selected -- an
+ * empty row, or only messages that never beat the identity -- and where
+ * MDGL_REPLACE_INF replaced the value); rows longer than
  * chunk_len are split into the num_chunks chunks (chunk_row[c],
  * chunk_start[c]: each covers up to chunk_len slots) whose partials are
  * reduced in order per heavy row (heavy_rows[h], chunks
@@ -168,7 +170,9 @@ int mdgl_segment_reduce(const int32_t* offsets, const void* value, void* dst, in
 
 /* mdgl_segment_reduce for max / min that also writes arg[s][k] (int32), the
  * row of the selected value: the first in row order among equal values, NaN
- * never selected, 0 for an empty segment. No counterpart in the reference
+ * never selected, -1 when no row was selected (an empty segment, or only
+ * values that never beat the identity) or MDGL_REPLACE_INF replaced the
+ * value. No counterpart in the reference
  * (it emits no arg); the gradient of segment max / min flows to that row. */
 int mdgl_segment_reduce_arg(const int32_t* offsets, const void* value, void* dst, int32_t* arg,
                             int64_t num_seg, int64_t d, int reduce_op, int64_t n, int flags,
@@ -363,6 +367,13 @@ int mdgl_gather_rows(const void* src, const int32_t* idx, void* dst, int64_t n, 
  * lands is unspecified). No counterpart in the reference. */
 int mdgl_scatter_rows(const void* src, const int32_t* idx, void* dst, int64_t n, int64_t width,
                       int dtype, void* stream);
+
+/* dst[i] = mask[i] != 0 ? src[i] : 0 (mask, src and dst of one dtype): the
+ * per-edge terms of a max / min gradient made exactly zero on the edges no
+ * output selected, whatever the other operand holds there. No counterpart
+ * in the reference. */
+int mdgl_keep_where(const void* mask, const void* src, void* dst, int64_t n, int dtype,
+                    void* stream);
 
 /* dst[i] = alpha * src[i]. */
 int mdgl_scale(const void* src, void* dst, int64_t n, double alpha, int dtype, void* stream);

@@ -68,6 +68,18 @@ __global__ __launch_bounds__(BLOCK) void scale_kernel(const T* __restrict__ x, T
     y[i] = alpha * x[i];
 }
 
+// y[i] = mask[i] != 0 ? x[i] : 0. The terms of a max / min gradient that
+// come from an edge no output selected are exactly zero, even where x holds
+// 0 times an infinite or NaN operand.
+template <class T>
+__global__ __launch_bounds__(BLOCK) void keep_where_kernel(const T* __restrict__ mask,
+                                                           const T* __restrict__ x,
+                                                           T* __restrict__ y, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * BLOCK)
+    y[i] = mask[i] != T(0) ? x[i] : T(0);
+}
+
 // dx[e, k] = a[e, k] * (g[e, k] - s[row_of[e], k]): the last two steps of
 // the edge_softmax gradient in one pass (coalesced edge rows, one row of s
 // per edge).
@@ -188,6 +200,20 @@ hipError_t launch_scale(const void* x, void* y, int64_t n, double alpha, int dty
   else
     hipLaunchKernelGGL(scale_kernel<double>, dim3(grid_n(n)), dim3(BLOCK), 0, s,
                        static_cast<const double*>(x), static_cast<double*>(y), n, alpha);
+  return hipGetLastError();
+}
+
+hipError_t launch_keep_where(const void* mask, const void* x, void* y, int64_t n, int dtype,
+                             hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  if (dtype == 0)
+    hipLaunchKernelGGL(keep_where_kernel<float>, dim3(grid_n(n)), dim3(BLOCK), 0, s,
+                       static_cast<const float*>(mask), static_cast<const float*>(x),
+                       static_cast<float*>(y), n);
+  else
+    hipLaunchKernelGGL(keep_where_kernel<double>, dim3(grid_n(n)), dim3(BLOCK), 0, s,
+                       static_cast<const double*>(mask), static_cast<const double*>(x),
+                       static_cast<double*>(y), n);
   return hipGetLastError();
 }
 

@@ -268,6 +268,15 @@ int mdgl_scatter_rows(const void* src, const int32_t* idx, void* dst, int64_t n,
                     "scatter_rows");
 }
 
+int mdgl_keep_where(const void* mask, const void* src, void* dst, int64_t n, int dtype,
+                    void* stream) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "keep_where: bad dtype %d", dtype);
+  if (n < 0) return fail(MDGL_EINVAL, "keep_where: n must be >= 0");
+  if (n > 0 && (!mask || !src || !dst)) return fail(MDGL_EINVAL, "keep_where: null buffer");
+  return hip_status(launch_keep_where(mask, src, dst, n, dtype, (hipStream_t)stream),
+                    "keep_where");
+}
+
 int mdgl_scale(const void* src, void* dst, int64_t n, double alpha, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "scale: bad dtype %d", dtype);
   if (n < 0) return fail(MDGL_EINVAL, "scale: n must be >= 0");

@@ -152,8 +152,8 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
 #pragma unroll
   for (int v = 0; v < VEC; ++v) {
     acc[v] = seed<T>(RED);
-    au[v] = 0;
-    ae[v] = 0;
+    au[v] = -1;  // nothing selected yet
+    ae[v] = -1;
   }
 
   const bool ident = a.flags & F_EID_IDENTITY;
@@ -288,7 +288,11 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
   if (a.flags & F_REPLACE_INF) {
 #pragma unroll
     for (int v = 0; v < VEC; ++v)
-      if (is_inf(acc[v])) acc[v] = T(0);
+      if (is_inf(acc[v])) {
+        acc[v] = T(0);  // a replaced value has no message behind it
+        au[v] = -1;
+        ae[v] = -1;
+      }
   }
   const int64_t o = row * a.dout + k0;
   if (VEC > 1 && (a.flags & F_OUT_VEC)) {
@@ -357,7 +361,7 @@ __global__ __launch_bounds__(BLOCK) void gspmm_combine_kernel(
   const int64_t h = t / dout, k = t % dout;
   const int64_t row = heavy_rows[h];
   T acc = seed<T>(RED);
-  int au = 0, ae = 0;
+  int au = -1, ae = -1;
   for (int c = heavy_ptr[h]; c < heavy_ptr[h + 1]; ++c) {
     const T v = part_val[(int64_t)c * dout + k];
     if constexpr (RED == RED_MAX) {
@@ -373,7 +377,10 @@ __global__ __launch_bounds__(BLOCK) void gspmm_combine_kernel(
     if (sc < T(1)) sc = T(1);
     acc = acc / sc;
   }
-  if ((flags & F_REPLACE_INF) && is_inf(acc)) acc = T(0);
+  if ((flags & F_REPLACE_INF) && is_inf(acc)) {
+    acc = T(0);
+    au = ae = -1;
+  }
   out[row * dout + k] = acc;
   if constexpr (RED == RED_MAX || RED == RED_MIN) {
     if (arg_u) arg_u[row * dout + k] = au;

@@ -193,6 +193,8 @@ hipError_t launch_edge_grad(const int32_t* vids, const int32_t* indptr, const vo
                             double alpha, int mean, int dtype, hipStream_t s);
 hipError_t launch_rows_by_degree(const int32_t* indptr, const void* x, void* y, int64_t rows,
                                  int64_t d, int dtype, hipStream_t s);
+hipError_t launch_keep_where(const void* mask, const void* x, void* y, int64_t n, int dtype,
+                             hipStream_t s);
 hipError_t launch_scale(const void* x, void* y, int64_t n, double alpha, int dtype,
                         hipStream_t s);
 // COO -> CSR by `key` (csr.hip).

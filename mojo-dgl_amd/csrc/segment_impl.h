@@ -30,7 +30,8 @@
 // of a long segment's sum (within the rounding of the float64 tolerance);
 // max and min stay exact, with the arg the first row reaching the value
 // (strict comparison, the smaller row wins ties when partials combine, NaN
-// never selected).
+// never selected; -1 when no row was selected or the value was replaced
+// by 0).
 //
 // Offsets are clamped into [0, n] and a negative length reads as empty, so
 // no access leaves the value block whatever the offsets hold.
@@ -100,7 +101,7 @@ __device__ __forceinline__ void seg_combine(T (&acc)[VEC], int (&ag)[VEC], const
 // starting at column k0 of segment s.
 template <class T, int RED, int VEC, bool ARG>
 __device__ __forceinline__ void seg_store(const SegArgs<T>& a, int64_t s, int64_t k0, int len,
-                                          T (&acc)[VEC], const int (&ag)[VEC]) {
+                                          T (&acc)[VEC], int (&ag)[VEC]) {
   if ((a.flags & F_MEAN) && len > 0) {
 #pragma unroll
     for (int v = 0; v < VEC; ++v) acc[v] = acc[v] / T(len);
@@ -108,7 +109,10 @@ __device__ __forceinline__ void seg_store(const SegArgs<T>& a, int64_t s, int64_
   if (a.flags & F_REPLACE_INF) {
 #pragma unroll
     for (int v = 0; v < VEC; ++v)
-      if (is_inf(acc[v])) acc[v] = T(0);
+      if (is_inf(acc[v])) {
+        acc[v] = T(0);  // a replaced value has no row behind it
+        ag[v] = -1;
+      }
   }
   const int64_t o = s * a.d + k0;
   if (VEC > 1 && a.out_vec && k0 + VEC <= a.d) {
@@ -151,7 +155,7 @@ __global__ __launch_bounds__(BLOCK) void seg_stage_kernel(SegArgs<T> a) {
 #pragma unroll
   for (int v = 0; v < VEC; ++v) {
     acc[v] = seed<T>(RED);
-    ag[v] = 0;
+    ag[v] = -1;  // nothing selected yet
   }
   T st[PER][VEC];
   // the window of rows [w0, w0 + WR) (clipped at rend) as chunks into st
@@ -217,7 +221,7 @@ __global__ __launch_bounds__(BLOCK) void seg_wide_kernel(SegArgs<T> a) {
 #pragma unroll
   for (int v = 0; v < VEC; ++v) {
     acc[v] = seed<T>(RED);
-    ag[v] = 0;
+    ag[v] = -1;  // nothing selected yet
   }
   if (col) {
     const T* p = a.val + (int64_t)lo * a.d + q * VEC;
@@ -276,7 +280,7 @@ __global__ __launch_bounds__(BLOCK) void seg_split_kernel(SegArgs<T> a) {
 #pragma unroll
         for (int v = 0; v < VEC; ++v) {
           acc[v] = seed<T>(RED);
-          ag[v] = 0;
+          ag[v] = -1;  // nothing selected yet
         }
         if (act) {
           for (int r = lo + j; r < hi; r += SEG_U * rs) {
@@ -307,7 +311,7 @@ __global__ __launch_bounds__(BLOCK) void seg_split_kernel(SegArgs<T> a) {
 #pragma unroll
           for (int v = 0; v < VEC; ++v) {
             res[v] = seed<T>(RED);
-            rag[v] = 0;
+            rag[v] = -1;
           }
           for (int jj = 0; jj < rs; ++jj) {
 #pragma unroll

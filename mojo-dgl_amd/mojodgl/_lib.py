@@ -102,6 +102,7 @@ _SIGNATURES = {
     "mdgl_gspmm_edge_grad": ([_P, _P, _P, _P, _P, _I64, _I64, _C, ctypes.c_double, _C, _P], _C),
     "mdgl_rows_by_degree": ([_P, _P, _P, _I64, _I64, _C, _P], _C),
     "mdgl_scale": ([_P, _P, _I64, ctypes.c_double, _C, _P], _C),
+    "mdgl_keep_where": ([_P, _P, _P, _I64, _C, _P], _C),
     "mdgl_gather_rows": ([_P, _P, _P, _I64, _I64, _C, _P], _C),
     "mdgl_scatter_rows": ([_P, _P, _P, _I64, _I64, _C, _P], _C),
     "mdgl_edge_softmax_grad": ([_P, _P, _P, _P, _P, _I64, _I64, _C, _P], _C),

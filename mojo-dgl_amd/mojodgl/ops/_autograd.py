@@ -217,12 +217,16 @@ class GSpMM(torch.autograd.Function):
                     dy = _scale(_gsddmm(g, "div", t, y, "e", "e"), -1.0)
                 dy = _reduce_to(dy, _padded(y.shape, dy.shape))
         else:
+            # only the selected edge of each output element receives its
+            # gradient (none where nothing was selected or update_all replaced
+            # an infinite value: the kernel's arg is -1 there); the terms of
+            # the other edges are exactly zero, not 0 times their operand
             M = _edge_grad(g, G, arg_e, False, 1.0)
             if need_x:
                 if op in ("copy_lhs", "add", "sub"):
                     p = M
                 else:
-                    p = _gsddmm(g, op, M, y, "e", "e")
+                    p = _keep_where(M, _gsddmm(g, op, M, y, "e", "e"))
                 dx = _reduce_to(_node_reduce(g, p, "u"), _padded(x.shape, M.shape))
             if need_y:
                 if op in ("copy_rhs", "add"):
@@ -230,17 +234,27 @@ class GSpMM(torch.autograd.Function):
                 elif op == "sub":
                     dy = _scale(M, -1.0)
                 elif op == "mul":
-                    dy = _gsddmm(g, "mul", x, M, "u", "e")
+                    dy = _keep_where(M, _gsddmm(g, "mul", x, M, "u", "e"))
                 else:
                     t = _gsddmm(g, "mul", x, M, "u", "e")
                     t = _gsddmm(g, "div", t, y, "e", "e")
-                    dy = _scale(_gsddmm(g, "div", t, y, "e", "e"), -1.0)
+                    dy = _keep_where(M, _scale(_gsddmm(g, "div", t, y, "e", "e"), -1.0))
                 dy = _reduce_to(dy, _padded(y.shape, dy.shape))
         if dx is not None:
             dx = dx.reshape(x.shape)
         if dy is not None:
             dy = dy.reshape(y.shape)
         return None, None, None, _back(dx, x0), _back(dy, y0), None
+
+
+def _keep_where(mask, t):
+    """t where mask is non-zero, else exactly 0 (same shape and dtype;
+    mdgl_keep_where)."""
+    mask, t = mask.contiguous(), t.contiguous()
+    out = torch.empty_like(t)
+    _lib.check(_lib.lib().mdgl_keep_where(mask.data_ptr(), t.data_ptr(), out.data_ptr(),
+                                          t.numel(), _code(t), _lib.stream()), "keep_where")
+    return out
 
 
 def _trailing_groups(x, y):

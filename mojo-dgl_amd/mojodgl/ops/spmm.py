@@ -221,7 +221,8 @@ def _gspmm(g, op, reduce_op, lhs_data, rhs_data):
 
     arg_u / arg_e hold, per output element, the source node and the edge id
     of the message selected by max/min: the first in CSR order (smallest edge
-    id) among equal values, 0 for a node with no in-edges.
+    id) among equal values; -1 where no message was selected (a node with no
+    in-edges, or only messages that never beat the identity).
     """
     out, au, ae, as_torch, dev = _run(g, op, reduce_op, lhs_data, rhs_data, want_arg=True)
     res = _lib.give_back(out, as_torch, dev)

@@ -25,8 +25,9 @@
 //     upstream DGL's BcastOff. With null tables the kernels are exactly the
 //     reference's (dl == dr == dout).
 //   * arg outputs for gspmm max/min: strict comparison, first in CSR order
-//     wins (= smallest edge id among ties), NaN never selected, 0 for a row
-//     with no in-edges. The reference emits no arg indices at all.
+//     wins (= smallest edge id among ties), NaN never selected, -1 when no
+//     message was selected (a row with no in-edges, or only messages that
+//     never beat the identity). The reference emits no arg indices at all.
 //   * float32 instantiations; the reference is float64 only.
 //
 // Parity status of each function is listed in oracle/README.txt.
@@ -184,7 +185,7 @@ void gspmm(const int64_t* indptr, const int64_t* indices, const int64_t* eid, co
         const int64_t lo = lhs_off ? lhs_off[o] : o;
         const int64_t ro = rhs_off ? rhs_off[o] : o;
         T acc = seed<T>(red);
-        int64_t au = 0, ae = 0;
+        int64_t au = -1, ae = -1;
         for (int64_t i = start; i < stop; ++i) {
           T m = message_at<T>(op, lhs, indices[i] * dl + lo, rhs, eid[i] * dr + ro);
           if (red == RED_MAX) {

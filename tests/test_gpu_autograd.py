@@ -566,3 +566,87 @@ def test_gat_layer_backward_float32():
     z = g.ndata["z"]
     ref = ref_spmm(u, v, n, "mul", "max", x, g.edata["w"])
     assert_grads(grads(z, [x, g.edata["w"]], 24), grads(ref, [x, g.edata["w"]], 24))
+
+
+# ------------------------------------------------------------------ max / min without a selection
+def brute_max_min_grads(u, v, n, red, x, y):
+    """Gradients of sum(gspmm(u_mul_e, red)) by brute force: each output
+    element's first message (row order) reaching its value, if any beats the
+    identity, passes y[e] to x[u[e]] and x[u[e]] to y[e]; no other term."""
+    x, y = x.detach().cpu().numpy(), y.detach().cpu().numpy()
+    gx, gy = np.zeros_like(x), np.zeros_like(y)
+    for node in range(n):
+        edges = np.nonzero(v == node)[0]
+        for k in range(x.shape[1]):
+            best, arg = (-np.inf if red == "max" else np.inf), -1
+            for e in edges:
+                m = x[u[e], k] * y[e, k]
+                if (m > best) if red == "max" else (m < best):
+                    best, arg = m, e
+            if arg >= 0:
+                gx[u[arg], k] += y[arg, k]
+                gy[arg, k] += x[u[arg], k]
+    return gx, gy
+
+
+@pytest.mark.parametrize("red", ["max", "min"])
+def test_max_min_gradient_reaches_no_edge_without_a_selection(red):
+    """A row whose messages never beat the identity (all -inf for max, all
+    +inf for min, or NaN) has no selected edge: no gradient term comes from
+    any of its edges -- in particular none reaches edge 0, which lies in
+    that row, and none is 0 times an infinite operand -- while every other
+    output passes its gradient through its selected edge (brute force)."""
+    n = 6
+    u = np.array([1, 2, 3, 0, 4, 5, 1, 2])
+    v = np.array([0, 0, 0, 1, 1, 2, 2, 3])  # edge 0 is in row 0
+    bad = np.inf if red == "min" else -np.inf
+    x = leaf((n, 3), 401, positive=True)
+    yv = torch.randn((u.size, 3), generator=torch.Generator(device=DEV).manual_seed(402),
+                     device=DEV, dtype=torch.float64).abs() + 0.5
+    yv[:3, 1] = bad            # row 0, column 1: only identity-valued messages
+    yv[:3, 2] = float("nan")   # row 0, column 2: only NaN messages
+    y = yv.requires_grad_(True)
+    out = ops.gspmm(dgl.graph((u, v), num_nodes=n), "mul", red, x, y)
+    assert torch.isinf(out[0, 1]) and torch.isinf(out[0, 2])
+    gx, gy = torch.autograd.grad(out[torch.isfinite(out)].sum(), (x, y))
+    wx, wy = brute_max_min_grads(u, v, n, red, x, y)
+    np.testing.assert_array_equal(gy.cpu().numpy(), wy)
+    np.testing.assert_array_equal(gx.cpu().numpy(), wx)
+    assert torch.all(gy[:3, 1:] == 0)
+
+
+@pytest.mark.parametrize("red", ["max", "min"])
+def test_update_all_gradient_is_zero_where_inf_became_zero(red):
+    """update_all replaces a +-inf max / min with 0 (reference
+    heterograph.py:232-239): that output is a constant, so the edge whose
+    infinite message produced it receives no gradient; the rest as without
+    the replacement."""
+    n = 5
+    u = np.array([0, 1, 2, 3, 4, 0, 1])
+    v = np.array([1, 1, 2, 2, 3, 4, 4])
+    sign = np.inf if red == "max" else -np.inf
+    x = leaf((n, 2), 411, positive=True)
+    yv = torch.randn((u.size, 2), generator=torch.Generator(device=DEV).manual_seed(412),
+                     device=DEV, dtype=torch.float64).abs() + 0.5
+    yv[2, 0] = sign  # row 2, column 0: an infinite message wins
+    y = yv.requires_grad_(True)
+    g = dgl.graph((u, v), num_nodes=n)
+    g.ndata["x"] = x
+    g.edata["y"] = y
+    g.update_all(fn.u_mul_e("x", "y", "m"), getattr(fn, red)("m", "z"))
+    z = g.ndata["z"]
+    assert z[2, 0] == 0 and z[0, 0] == 0 and z[0, 1] == 0  # replaced inf; node 0 has no in-edge
+    gx, gy = torch.autograd.grad(z.sum(), (x, y))
+    assert gy[2, 0] == 0 and gx[u[2], 0] == 0
+    # every other selected edge gets its row's gradient
+    plain = ops.gspmm(g, "mul", red, x.detach(), y.detach())
+    for e in range(u.size):
+        for k in range(2):
+            if (e, k) == (2, 0):
+                continue
+            sel = float(plain[v[e], k]) == float(x[u[e], k] * y[e, k]) and np.isfinite(
+                float(plain[v[e], k]))
+            first = sel and all(not (float(x[u[f], k] * y[f, k]) == float(plain[v[e], k]))
+                                for f in range(e) if v[f] == v[e])
+            want = float(x[u[e], k]) if first else 0.0
+            assert float(gy[e, k]) == want, (e, k)

@@ -235,14 +235,14 @@ def test_c3_aggregations(c3):
     ae = arg_e.long()
     assert torch.equal(vd[ae][has], torch.arange(N, device="cuda")[:, None].expand_as(ae)[has])
     assert torch.equal(ud[ae][has], arg_u.long()[has])
-    assert not bool(arg_u[~has].any()) and not bool(arg_e[~has].any())
+    assert bool((arg_u[~has] == -1).all()) and bool((arg_e[~has] == -1).all())
     # sampled rows: values and arg indices bit-exact against the oracle
     ro, rau, rae = oracle.gspmm(None, None, rows.size, "copy_lhs", "max", hh, None, np.float32,
                                 with_arg=True, graph_csr=csr_s)
     full = (np.diff(sub) > 0)[:, None]
     np.testing.assert_array_equal(out[rows_d].cpu().numpy(), ro)
     np.testing.assert_array_equal(arg_u[rows_d].cpu().numpy(), rau)
-    np.testing.assert_array_equal(arg_e[rows_d].cpu().numpy(), np.where(full, eids[rae], 0))
+    np.testing.assert_array_equal(arg_e[rows_d].cpu().numpy(), np.where(full, eids[rae], -1))
 
 
 # ------------------------------------------------------------------ C4

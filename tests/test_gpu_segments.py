@@ -32,10 +32,11 @@ def lengths(rng, S, mean, long_rows=()):
 
 
 def first_arg(seglen, value, reducer):
-    """Row of the first max / min of each segment and column (0 when empty)."""
+    """Row of the first max / min of each segment and column (-1 when none
+    is selected)."""
     off = np.concatenate([[0], np.cumsum(seglen)])
     d = value.shape[1]
-    out = np.zeros((seglen.size, d), dtype=np.int64)
+    out = np.full((seglen.size, d), -1, dtype=np.int64)
     for s in range(seglen.size):
         rows = value[off[s]:off[s + 1]]
         if rows.shape[0] == 0:

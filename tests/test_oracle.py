@@ -97,7 +97,7 @@ def test_gspmm_max_min_values_and_args(dtype, reduce_op):
         edges = np.nonzero(v == node)[0]  # ascending edge id
         for k in range(d):
             if edges.size == 0:
-                assert au[node, k] == 0 and ae[node, k] == 0
+                assert au[node, k] == -1 and ae[node, k] == -1
                 continue
             first = edges[np.nonzero(m[edges, k] == want[node, k])[0][0]]
             assert ae[node, k] == first and au[node, k] == u[first]
