@@ -336,6 +336,7 @@ def workload_gat(args):
         result["graph_build"] = time_graph_build(g, u, v, N, args)
         result["edge_softmax_subset"] = time_subset_softmax(g, el, er, E, args)
         result["forward_backward"] = time_gat_backward(g, el, er, h)
+        result["gather_ceilings"] = time_gather_ceilings(g, N, E, H, args)
     if not args.no_cpu_baseline:
         log("CPU baseline (oracle) of the step on a sample")
         result["cpu_baseline"] = cpu_baseline_gat(g, el, er, h, args)
@@ -346,6 +347,49 @@ def workload_gat(args):
     del g, h
     free_gpu()
     return result
+
+
+def time_gather_ceilings(g, N, E, H, args):
+    """The access patterns of gsddmm u_add_v and of edge_softmax's two passes
+    alone, through mdgl_gather_rows (rows of a table gathered by an index,
+    written in index order; no arithmetic), cold caches, median of reps:
+      * rows_32B_by_edge_id: 32-byte rows (H float32) of an (E, H) table by
+        a random permutation of the edges (the row pass reading the logits
+        of a row's edges);
+      * rows_32B_by_node: 32-byte rows of an (N, H) table by each edge's
+        destination, twice the bytes of one gsddmm operand;
+      * rows_64B_by_node: 64-byte rows of an (N, 2H) table by each edge's
+        destination (the write pass reading a row's (max, sum)).
+    Each figure is GB/s of bytes moved per launch (4 index + gathered + written
+    per edge)."""
+    import torch
+
+    from mojodgl import _lib
+
+    L = _lib.lib()
+    cold = ColdTimer(max(3, args.reps // 2), 1)
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    perm = torch.randperm(E, device="cuda", generator=gen).to(torch.int32)
+    vd = g._device_coo()[1]
+    out = {}
+    for name, rows, width, idx in (("rows_32B_by_edge_id", E, H, perm),
+                                   ("rows_32B_by_node", N, H, vd),
+                                   ("rows_64B_by_node", N, 2 * H, vd)):
+        table = torch.randn(rows, width, device="cuda", generator=gen)
+        dst = torch.empty(E, width, device="cuda")
+
+        def run():
+            _lib.check(L.mdgl_gather_rows(table.data_ptr(), idx.data_ptr(), dst.data_ptr(), E,
+                                          width, _lib.FLOAT32, _lib.stream()), "gather_rows")
+
+        t = cold(run)
+        nbytes = E * (4 + 8 * width)
+        out[name] = dict(t, bytes=nbytes, GBps=round(nbytes / t["median_ms"] / 1e6, 1),
+                         table_MB=round(rows * width * 4 / 1e6, 1))
+        del table, dst
+    del perm
+    free_gpu()
+    return out
 
 
 def time_gat_backward(g, el, er, h):

@@ -691,7 +691,7 @@ int softmax_common(const char* what, const int32_t* indptr, const int32_t* eid,
                    const int32_t* chunk_start, const int32_t* chunk_first, int64_t num_chunks,
                    int64_t slots, const int32_t* row_of, int64_t num_edges,
                    int64_t num_slots, void* workspace,
-                   int64_t workspace_bytes, int dtype, void* stream) {
+                   int64_t workspace_bytes, int dtype, void* stream, bool stage = false) {
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "%s: bad dtype %d", what, dtype);
   if (num_rows < 0 || d < 0 || num_chunks < 0) return fail(MDGL_EINVAL, "%s: negative size", what);
   if (num_rows >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "%s: 2**31 or more rows", what);
@@ -752,6 +752,17 @@ int softmax_common(const char* what, const int32_t* indptr, const int32_t* eid,
     p.table = static_cast<char*>(workspace) + ((2 * num_chunks * d * dsize(dtype) + 255) / 256) * 256;
   }
   p.stream = (hipStream_t)stream;
+  if (stage && !order && num_chunks == 0) {
+    // segments in their own order, none chunked: every one fits a staging
+    // window (chunk_len rows never exceed it), so the LDS-staged kernel takes
+    // them when the rows are narrow enough
+    hipError_t se = dtype == MDGL_FLOAT32
+                        ? launch_segment_softmax_stage<float>(indptr, logits, dst, num_rows,
+                                                              num_slots, d, p.stream)
+                        : launch_segment_softmax_stage<double>(indptr, logits, dst, num_rows,
+                                                               num_slots, d, p.stream);
+    if (se != hipErrorNotSupported) return hip_status(se, what);
+  }
   hipError_t e = dtype == MDGL_FLOAT32 ? launch_softmax<float>(p) : launch_softmax<double>(p);
   return hip_status(e, what);
 }
@@ -773,7 +784,7 @@ int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, v
   return softmax_common("segment_softmax", offsets, nullptr, nullptr, value, dst, num_seg, d,
                         order, bounds, nbins, packed_eid, chunk_row, chunk_start, chunk_first,
                         num_chunks, slots, nullptr, 0, n, workspace, workspace_bytes, dtype,
-                        stream);
+                        stream, true);
 }
 
 int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int32_t* eid,

@@ -78,6 +78,12 @@ struct SegmentParams {
 template <class T>
 hipError_t launch_segment_reduce(const SegmentParams& p);
 
+// segment_softmax of segments that fit an 8 KB window each, rows of at most
+// 32 lane vectors (segment_impl.h); hipErrorNotSupported for wider rows.
+template <class T>
+hipError_t launch_segment_softmax_stage(const int32_t* offsets, const void* value, void* out,
+                                        int64_t num_seg, int64_t n, int64_t d, hipStream_t st);
+
 // gsddmm: out[e, o] = op(lhs[t_l(e)], rhs[t_r(e)]) (or the dot over `red`).
 struct GsddmmParams {
   const int32_t* uids;

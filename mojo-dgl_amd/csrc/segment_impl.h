@@ -336,6 +336,208 @@ __global__ __launch_bounds__(BLOCK) void seg_split_kernel(SegArgs<T> a) {
   }
 }
 
+// ---------------------------------------------------------------- segment_softmax
+// Per segment and column: m = max, e = exp(x - m), s = sum of e in row order,
+// out = e / s (the reference's three passes, src/ported.mojo:679-768), for
+// rows of at most 32 lane vectors. A wavefront owns P = 64 / G consecutive
+// segments, G lanes each. A window is a run of whole segments of at most WR
+// rows (8 KB): it is read with coalesced 16-byte loads into LDS; each lane
+// group takes its segment's max (and records which rows are its own); then
+// all 64 lanes turn the window's values into e in place, each lane group
+// sums its segment's e in row order, and all lanes write e times the
+// reciprocal of s with coalesced stores. The next window is in registers meanwhile. A segment
+// longer than a window (which the caller's plan only hands over as chunks,
+// so it does not reach this kernel) would be streamed by its lane group.
+__device__ __forceinline__ float seg_exp(float x) { return expf(x); }
+__device__ __forceinline__ double seg_exp(double x) { return exp(x); }
+
+// One lane's VEC columns of a row (VEC > 1: aligned 16-byte access).
+template <class T, int VEC>
+__device__ __forceinline__ void seg_load_cols(const T* p, T (&x)[VEC]) {
+  if constexpr (VEC > 1) load_n<T, VEC>(p, x);
+  else x[0] = *p;
+}
+template <class T, int VEC>
+__device__ __forceinline__ void seg_store_cols(T* p, const T (&x)[VEC]) {
+  if constexpr (VEC > 1) store_n<T, VEC>(p, x);
+  else *p = x[0];
+}
+
+template <class T, int VEC>
+__global__ __launch_bounds__(BLOCK) void seg_softmax_stage_kernel(SegArgs<T> a) {
+  constexpr int CH = SEG_WB / (VEC * (int)sizeof(T));  // chunks per window
+  constexpr int PER = CH / WAVE;
+  constexpr int SV = WAVE * 16 / (int)sizeof(T);       // m / s entries: P * nvec * VEC <= SV
+  __shared__ __align__(16) T buf[WAVES_PER_BLOCK][SEG_WB / sizeof(T)];
+  __shared__ __align__(16) T mx[WAVES_PER_BLOCK][SV];
+  __shared__ __align__(16) T sm[WAVES_PER_BLOCK][SV];
+  __shared__ unsigned char owner[WAVES_PER_BLOCK][CH];  // lane group of each window row
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_BLOCK + w;
+  const int64_t s0 = wave * a.P;
+  if (s0 >= a.S) return;  // uniform per wavefront
+  const int grp = lane / a.G, gl = lane % a.G;
+  const int64_t seg = s0 + grp;
+  int lo = 0, hi = 0;
+  if (seg < a.S) seg_range(a.off, seg, a.n, lo, hi);
+  const bool col = gl < a.nvec;
+  const int64_t k0 = (int64_t)gl * VEC;
+  const int nv = a.nvec;
+  const int WR = CH / nv;
+  const int mslot = (grp * nv + gl) * VEC;  // this lane's m / s entries
+  bool done = hi <= lo;  // empty segments (and lanes past the last segment) write nothing
+
+  // window [w0, e0): w0 the first row of the first unfinished segment, e0
+  // the end of the last unfinished segment that ends within w0 + WR (w0
+  // when even the first does not fit)
+  auto window = [&](bool dn, int& w0, int& e0) {
+    w0 = wave_min_int(dn ? 0x7fffffff : lo);
+    if (w0 == 0x7fffffff) {
+      e0 = w0;
+      return;
+    }
+    e0 = wave_max_int(!dn && hi <= w0 + WR ? hi : w0);
+  };
+  T st[PER][VEC];
+  auto fetch = [&](int w0, int e0) {
+    const int64_t b0 = (int64_t)w0 * a.d, b1 = (int64_t)e0 * a.d;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int64_t e = b0 + (int64_t)(lane + i * WAVE) * VEC;
+      if (e < b1) {
+        if constexpr (VEC > 1) load_n_stream<T, VEC>(a.val + e, st[i]);
+        else st[i][0] = __builtin_nontemporal_load(a.val + e);
+      } else {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) st[i][v] = T(0);
+      }
+    }
+  };
+  int W, E;
+  window(done, W, E);
+  if (E > W) fetch(W, E);
+  while (W != 0x7fffffff) {  // uniform per wavefront
+    if (E > W) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        if constexpr (VEC > 1) store_n<T, VEC>(&buf[w][(lane + i * WAVE) * VEC], st[i]);
+        else buf[w][lane + i * WAVE] = st[i][0];
+      }
+      wave_sync_lds();
+      const bool mine = !done && lo >= W && hi <= E;
+      int Wn, En;
+      window(done || mine, Wn, En);
+      if (En > Wn) fetch(Wn, En);
+      const int nch = (E - W) * nv;  // chunks of this window
+      const int base = ((lo - W) * nv + gl) * VEC, step = nv * VEC;
+      // 1. max per segment and column, in the group; the group's first lane
+      //    marks the rows it owns
+      if (mine && col) {
+        T m[VEC], x[VEC];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) m[v] = -__builtin_huge_val();
+        for (int r = lo, c = base; r < hi; ++r, c += step) {
+          if constexpr (VEC > 1) load_n<T, VEC>(&buf[w][c], x);
+          else x[0] = buf[w][c];
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) m[v] = x[v] > m[v] ? x[v] : m[v];
+        }
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) mx[w][mslot + v] = m[v];
+        if (gl == 0)
+          for (int r = lo; r < hi; ++r) owner[w][r - W] = (unsigned char)grp;
+      }
+      wave_sync_lds();
+      // 2. e = exp(x - m) over the whole window, every lane, in place
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int c = lane + i * WAVE;
+        if (c < nch) {
+          const int r = c / nv, q = c - r * nv;
+          const int ms = (owner[w][r] * nv + q) * VEC;
+          T x[VEC];
+          if constexpr (VEC > 1) load_n<T, VEC>(&buf[w][c * VEC], x);
+          else x[0] = buf[w][c];
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) x[v] = seg_exp(x[v] - mx[w][ms + v]);
+          if constexpr (VEC > 1) store_n<T, VEC>(&buf[w][c * VEC], x);
+          else buf[w][c] = x[0];
+        }
+      }
+      wave_sync_lds();
+      // 3. s = sum of e per segment and column, in row order, in the group
+      if (mine && col) {
+        T su[VEC], x[VEC];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) su[v] = T(0);
+        for (int r = lo, c = base; r < hi; ++r, c += step) {
+          if constexpr (VEC > 1) load_n<T, VEC>(&buf[w][c], x);
+          else x[0] = buf[w][c];
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) su[v] = su[v] + x[v];
+        }
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) sm[w][mslot + v] = T(1) / su[v];
+      }
+      wave_sync_lds();
+      // 4. out = e * (1 / s) over the whole window, every lane, coalesced
+      //    stores (one correctly rounded reciprocal per segment and column
+      //    instead of a divide per value: within two roundings of e / s)
+      const int64_t b0 = (int64_t)W * a.d;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int c = lane + i * WAVE;
+        if (c < nch) {
+          const int r = c / nv, q = c - r * nv;
+          const int ms = (owner[w][r] * nv + q) * VEC;
+          T y[VEC];
+          if constexpr (VEC > 1) load_n<T, VEC>(&buf[w][c * VEC], y);
+          else y[0] = buf[w][c];
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) y[v] = y[v] * sm[w][ms + v];
+          if constexpr (VEC > 1) store_n_stream<T, VEC>(a.out + b0 + (int64_t)c * VEC, y);
+          else a.out[b0 + c] = y[0];
+        }
+      }
+      wave_sync_lds();
+      done = done || mine;
+      W = Wn;
+      E = En;
+    } else {
+      // the first unfinished segment is longer than a window: its group
+      // streams it from memory, three passes
+      const bool mine = !done && lo == W;
+      if (mine && col) {
+        T m[VEC], su[VEC], x[VEC];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+          m[v] = -__builtin_huge_val();
+          su[v] = T(0);
+        }
+        for (int r = lo; r < hi; ++r) {
+          seg_load_cols<T, VEC>(a.val + (int64_t)r * a.d + k0, x);
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) m[v] = x[v] > m[v] ? x[v] : m[v];
+        }
+        for (int r = lo; r < hi; ++r) {
+          seg_load_cols<T, VEC>(a.val + (int64_t)r * a.d + k0, x);
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) su[v] = su[v] + seg_exp(x[v] - m[v]);
+        }
+        for (int r = lo; r < hi; ++r) {
+          seg_load_cols<T, VEC>(a.val + (int64_t)r * a.d + k0, x);
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) x[v] = seg_exp(x[v] - m[v]) / su[v];
+          seg_store_cols<T, VEC>(a.out + (int64_t)r * a.d + k0, x);
+        }
+      }
+      done = done || mine;
+      window(done, W, E);
+      if (E > W) fetch(W, E);
+    }
+  }
+}
+
 template <class T, int RED, int VEC, bool ARG>
 hipError_t launch_seg(SegArgs<T> a, hipStream_t st) {
   const bool stage = a.nvec <= 32;
@@ -400,7 +602,42 @@ hipError_t launch_segment_reduce(const SegmentParams& p) {
   }
 }
 
+// segment_softmax through seg_softmax_stage_kernel; hipErrorNotSupported
+// when the rows are wider than 32 lane vectors (the caller then takes the
+// CSR softmax kernel).
+template <class T>
+hipError_t launch_segment_softmax_stage(const int32_t* offsets, const void* value, void* out,
+                                        int64_t num_seg, int64_t n, int64_t d, hipStream_t st) {
+  if (num_seg <= 0 || d <= 0 || n <= 0) return hipSuccess;
+  constexpr int V = 16 / sizeof(T);
+  const bool vec = d % V == 0 && aligned16(value) && aligned16(out);
+  const int64_t nvec = vec ? d / V : d;
+  if (nvec > 32) return hipErrorNotSupported;
+  SegArgs<T> a{};
+  a.off = offsets;
+  a.val = static_cast<const T*>(value);
+  a.out = static_cast<T*>(out);
+  a.S = num_seg;
+  a.n = n;
+  a.d = d;
+  a.nvec = (int)nvec;
+  int G = 1;
+  while (G < a.nvec) G <<= 1;
+  a.G = G;
+  a.P = WAVE / G;
+  const int64_t waves = (num_seg + a.P - 1) / a.P;
+  const dim3 grid((unsigned)((waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK)), block(BLOCK);
+  if (vec)
+    hipLaunchKernelGGL((seg_softmax_stage_kernel<T, V>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((seg_softmax_stage_kernel<T, 1>), grid, block, 0, st, a);
+  return hipGetLastError();
+}
+
 }  // namespace mdgl
 
-#define MDGL_INSTANTIATE_SEGMENT(T) \
-  template hipError_t mdgl::launch_segment_reduce<T>(const mdgl::SegmentParams&);
+#define MDGL_INSTANTIATE_SEGMENT(T)                                                         \
+  template hipError_t mdgl::launch_segment_reduce<T>(const mdgl::SegmentParams&);          \
+  template hipError_t mdgl::launch_segment_softmax_stage<T>(const int32_t*, const void*, void*, \
+                                                            int64_t, int64_t, int64_t,      \
+                                                            hipStream_t);
