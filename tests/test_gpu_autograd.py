@@ -639,14 +639,15 @@ def test_update_all_gradient_is_zero_where_inf_became_zero(red):
     gx, gy = torch.autograd.grad(z.sum(), (x, y))
     assert gy[2, 0] == 0 and gx[u[2], 0] == 0
     # every other selected edge gets its row's gradient
-    plain = ops.gspmm(g, "mul", red, x.detach(), y.detach())
+    xd, yd = x.detach(), y.detach()
+    plain = ops.gspmm(g, "mul", red, xd, yd)
     for e in range(u.size):
         for k in range(2):
             if (e, k) == (2, 0):
                 continue
-            sel = float(plain[v[e], k]) == float(x[u[e], k] * y[e, k]) and np.isfinite(
+            sel = float(plain[v[e], k]) == float(xd[u[e], k] * yd[e, k]) and np.isfinite(
                 float(plain[v[e], k]))
-            first = sel and all(not (float(x[u[f], k] * y[f, k]) == float(plain[v[e], k]))
+            first = sel and all(not (float(xd[u[f], k] * yd[f, k]) == float(plain[v[e], k]))
                                 for f in range(e) if v[f] == v[e])
-            want = float(x[u[e], k]) if first else 0.0
+            want = float(xd[u[e], k]) if first else 0.0
             assert float(gy[e, k]) == want, (e, k)
