@@ -222,18 +222,26 @@ __global__ __launch_bounds__(BLOCK) void grouped_gemm_kernel(GemmArgs<T> p) {
 
 // ---------------------------------------------------------------- b resident
 // float32, K a multiple of 32 up to 128, rows of a 16-byte aligned (the host
-// checks; other shapes take grouped_gemm_kernel): the group's whole b block
-// (128 columns x K) sits in
-// LDS, loaded once per group a workgroup meets, and the a fragments go from
-// global memory straight into registers, up to four 16-k chunks ahead of the
-// MFMAs (across tile boundaries: the next tile's first chunks are requested
-// while this tile's last ones multiply), so the K loop has no barrier and no
-// LDS traffic for a. A workgroup (8 wavefronts, 4 x 2, each 64 x 64 of the
-// output) walks a contiguous range of 256-row tiles; ranges follow the group
-// order, so b changes rarely.
-constexpr int RB_TM = 256;      // rows per tile
-constexpr int RB_KMAX = 128;    // largest padded K held in LDS
-constexpr int RB_THREADS = 512;
+// checks; other shapes take grouped_gemm_kernel). A workgroup (4 wavefronts,
+// two per CU) keeps the group's b block (128 columns x K) in LDS, loaded once
+// per group it meets, and walks a contiguous range of 128-row tiles; ranges
+// follow the group order, so b changes rarely. Each wavefront owns 32 rows of
+// the tile and all 128 columns: four 32 x 32 blocks of
+// v_mfma_f32_32x32x2f32, so every row of a is read by one wavefront only,
+// straight from global memory into registers (no LDS, no barrier in the K
+// loop), a whole tile ahead of the MFMAs that use it. The K axis goes in
+// 16-wide chunks; in MFMA step s of chunk c, lane half h (lanes 32h..32h+31)
+// supplies k = 16c + 8h + s, so a lane's a operands for a chunk are 8
+// consecutive floats of its row (two 16-byte loads) and its b operands 8
+// consecutive floats of a row of the LDS block (two 16-byte LDS reads, a
+// 528-byte row stride keeps 16 lanes on distinct banks). A tile's results
+// are stored while the next tile multiplies: after a 4 x 4 transpose in each
+// DPP quad they wait in registers and leave as 16-byte stores (eight rows x
+// 128 contiguous bytes per instruction) spread over the next tile's chunks.
+constexpr int RB_WAVES = 4;
+constexpr int RB_TM = 32 * RB_WAVES;   // rows per tile
+constexpr int RB_KMAX = 128;           // largest padded K held in LDS
+constexpr int RB_THREADS = 64 * RB_WAVES;
 constexpr int RB_LD = RB_KMAX + 4;
 
 // Within each quad of lanes (s = lane % 4), x[r] = M[r][s] becomes
@@ -261,21 +269,16 @@ __device__ __forceinline__ void quad_transpose(float (&x)[4], int s) {
     if ((r & 2) != (s & 2)) x[r] = t[r];
 }
 
-template <class T, int NCH>
-__global__ __launch_bounds__(RB_THREADS) void grouped_gemm_resident_kernel(GemmArgs<T> p,
-                                                                           int64_t tiles_per_wg,
-                                                                           const int32_t* __restrict__ tile_ptr,
-                                                                           const int32_t* __restrict__ group_off) {
-  using M = Mfma<T>;
-  using acc_t = typename M::acc_t;
-  // a ring of DEPTH chunks (NCH a multiple of DEPTH, so the next tile's
-  // chunk k lands in ring slot k % DEPTH too)
-  constexpr int DEPTH = NCH == 6 ? 3 : (NCH < 4 ? NCH : 4);
-  static_assert(NCH % DEPTH == 0, "ring depth");
-  __shared__ __align__(16) T Bs[GBN][RB_LD];
+template <int NCH>
+__global__ __launch_bounds__(RB_THREADS, 2) void grouped_gemm_resident_kernel(
+    GemmArgs<float> p, int64_t tiles_per_wg, const int32_t* __restrict__ tile_ptr,
+    const int32_t* __restrict__ group_off) {
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  __shared__ __align__(16) float Bs[GBN][RB_LD];
   const int t = threadIdx.x;
-  const int lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1;
-  const int li = lane & 15, h = lane >> 4;
+  const int lane = t & 63, w = t >> 6;
+  const int lr = lane & 31, hf = lane >> 5;
+  const int s4 = lane & 3, k4 = lr >> 2;
   const int64_t total = tile_ptr[p.R];
   const int64_t first = (int64_t)blockIdx.x * tiles_per_wg;
   const int64_t last = first + tiles_per_wg < total ? first + tiles_per_wg : total;
@@ -288,23 +291,36 @@ __global__ __launch_bounds__(RB_THREADS) void grouped_gemm_resident_kernel(GemmA
   auto uget = [](const int32_t* __restrict__ arr, int64_t i) -> int64_t {
     return arr[__builtin_amdgcn_readfirstlane((int)i)];
   };
-  // rows of a tile for this lane: rid[i] = row of tile row wm*64 + 16i + li
-  // (-1 past the group); base[i] = where its a fragments start (row 0 for
-  // -1: read, never stored)
-  auto setup_rows = [&](int64_t tl, int64_t gg, int64_t& m0, int64_t& m_end,
-                        int32_t (&rid)[4]) {
-    m0 = uget(group_off, gg) + (tl - uget(tile_ptr, gg)) * RB_TM;
-    m_end = uget(group_off, gg + 1);
+  // the row of a behind tile row 32w + lr (-1 past the group; its loads then
+  // read row 0, never stored)
+  auto row_of = [&](int64_t tl, int64_t gg) -> int32_t {
+    const int64_t m0 = uget(group_off, gg) + (tl - uget(tile_ptr, gg)) * RB_TM;
+    const int64_t pos = m0 + w * 32 + lr;
+    return pos < uget(group_off, gg + 1) ? (p.perm ? p.perm[pos] : (int32_t)pos) : -1;
+  };
+  auto base_of = [&](int32_t r) -> const float* {
+    return p.a + (int64_t)(r >= 0 ? r : 0) * p.K + 8 * hf;
+  };
+  // 8 consecutive floats (two 16-byte loads) from a row of a / of the block
+  auto load_chunk = [&](const float* q, float (&d)[8]) {
+    float x[4], y[4];
+    load_global_n<float, 4>(q, x);
+    load_global_n<float, 4>(q + 4, y);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t pos = m0 + wm * 64 + i * 16 + li;
-      rid[i] = pos < m_end ? (p.perm ? p.perm[pos] : (int32_t)pos) : -1;
+      d[i] = x[i];
+      d[4 + i] = y[i];
     }
   };
-  auto bases = [&](const int32_t (&rid)[4], const T* (&base)[4]) {
+  auto lds_chunk = [&](const float* q, float (&d)[8]) {
+    float x[4], y[4];
+    load_n<float, 4>(q, x);
+    load_n<float, 4>(q + 4, y);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      base[i] = p.a + (int64_t)(rid[i] >= 0 ? rid[i] : 0) * p.K + 4 * h;
+    for (int i = 0; i < 4; ++i) {
+      d[i] = x[i];
+      d[4 + i] = y[i];
+    }
   };
 
   int64_t tile = first;
@@ -318,118 +334,113 @@ __global__ __launch_bounds__(RB_THREADS) void grouped_gemm_resident_kernel(GemmA
     }
     g = lo;
   }
-  int64_t m0, m_end;
-  int32_t rid[4];
-  const T* base[4];
-  setup_rows(tile, g, m0, m_end, rid);
-  bases(rid, base);
-  // lane (li, h) holds a[row i][16c + 4h .. +3] of chunk c in ring slot c % DEPTH
-  T af[DEPTH][4][4];
+  int32_t rid = row_of(tile, g);
+  const float* base = base_of(rid);
+  float af[NCH][8];  // the tile's a operands, chunk by chunk
 #pragma unroll
-  for (int c = 0; c < DEPTH; ++c)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) load_global_n<T, 4>(base[i] + c * 16, af[c][i]);
+  for (int c = 0; c < NCH; ++c) load_chunk(base + 16 * c, af[c]);
 
+  // results of the previous tile: ob[q][j] is row 8q + 4hf + s4 of the
+  // tile, columns 32j + 4k4 .. +3, for output row orow[q]
+  float ob[4][4][4];
+  int32_t orow[4] = {-1, -1, -1, -1};
+  auto store_q = [&](int q) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t n = n0 + 32 * j + 4 * k4;
+      if (orow[q] < 0 || n >= p.N) continue;
+      float* o = p.out + (int64_t)orow[q] * p.N + n;
+      if (p.out_vec && n + 4 <= p.N) {
+        store_n<float, 4>(o, ob[q][j]);
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (n + v < p.N) o[v] = ob[q][j][v];
+      }
+    }
+  };
+  bool pending = false;
   int64_t cur_g = -1;
   // One tile: its b block (when the group changes), the K loop with the
-  // next tile's first loads, the output. The first tile is peeled off the
-  // loop below, so every loop iteration starts in the same state (the next
-  // tile's first a loads, then the last tile's stores, outstanding) and its
-  // first wait counts past the stores instead of waiting for them.
+  // previous tile's stores and the next tile's loads, the results kept.
   auto run_tile = [&]() -> bool {
     if (g != cur_g) {
       __syncthreads();  // every wavefront is done with the previous block
-      const T* bt_g = p.bt + g * p.N * p.Kp;
+      const float* bt_g = p.bt + g * p.N * p.Kp;
       constexpr int CPR = NCH * 4;  // 16-byte chunks per row of the block
       for (int c = t; c < GBN * CPR; c += RB_THREADS) {
         const int r = c / CPR, k = (c % CPR) * 4;
-        T v[4] = {T(0), T(0), T(0), T(0)};
-        if (n0 + r < p.N) load_global_n<T, 4>(bt_g + (n0 + r) * p.Kp + k, v);
-        store_n<T, 4>(&Bs[r][k], v);
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        if (n0 + r < p.N) load_global_n<float, 4>(bt_g + (n0 + r) * p.Kp + k, v);
+        store_n<float, 4>(&Bs[r][k], v);
       }
       __syncthreads();
       cur_g = g;
     }
-    // the next tile's rows are looked up now (their addresses are formed
-    // only where its first chunks are requested, while this tile's last
-    // chunks multiply, so the row loads are not waited for before)
     const bool has_next = tile + 1 < last;
-    int64_t g_n = g, m0_n = 0, m_end_n = 0;
-    int32_t rid_n[4] = {-1, -1, -1, -1};
-    const T* base_n[4] = {base[0], base[1], base[2], base[3]};
+    int64_t g_n = g;
+    int32_t rid_n = -1;
+    const float* base_n = base;
     if (has_next) {
       while (uget(tile_ptr, g_n + 1) <= tile + 1) ++g_n;
-      setup_rows(tile + 1, g_n, m0_n, m_end_n, rid_n);
+      rid_n = row_of(tile + 1, g_n);
+      base_n = base_of(rid_n);
     }
-    acc_t acc[4][4];
+    f32x16 acc[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[i][j][r] = T(0);
+      for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      T bf[4][4];
+      // blocks in pairs, so consecutive MFMAs never update the same block
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        load_n<T, 4>(&Bs[wn * 64 + j * 16 + li][c * 16 + 4 * h], bf[j]);
+      for (int jp = 0; jp < 2; ++jp) {
+        float b0[8], b1[8];
+        lds_chunk(&Bs[64 * jp + lr][16 * c + 8 * hf], b0);
+        lds_chunk(&Bs[64 * jp + 32 + lr][16 * c + 8 * hf], b1);
 #pragma unroll
-      for (int sstep = 0; sstep < 4; ++sstep)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            acc[i][j] = M::step(af[c % DEPTH][i][sstep], bf[j][sstep], acc[i][j]);
-      if (c + DEPTH < NCH) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          load_global_n<T, 4>(base[i] + (c + DEPTH) * 16, af[c % DEPTH][i]);
-      } else if (has_next) {
-        if (c + DEPTH == NCH) bases(rid_n, base_n);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          load_global_n<T, 4>(base_n[i] + (c + DEPTH - NCH) * 16, af[c % DEPTH][i]);
-      }
-    }
-    // Output. Lane (li, h) holds column li of block rows 4h + r (r = 0..3).
-    // A 4 x 4 transpose inside each DPP quad (lanes 4q..4q+3) gives lane
-    // 4q + s row 4h + s at columns 4q..4q+3, stored as one 16-byte write.
-    const int s4 = li & 3, q4 = li >> 2;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int orow = __shfl(rid[i], 4 * h + s4);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        T x[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-        quad_transpose(x, s4);
-        const int64_t n = n0 + wn * 64 + j * 16 + 4 * q4;
-        if (orow >= 0 && n < p.N) {
-          if (p.out_vec && n + 4 <= p.N) {
-            store_n<T, 4>(p.out + (int64_t)orow * p.N + n, x);
-          } else {
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-              if (n + v < p.N) p.out[(int64_t)orow * p.N + n + v] = x[v];
-          }
+        for (int s = 0; s < 8; ++s) {
+          acc[2 * jp] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[c][s], b0[s], acc[2 * jp], 0, 0, 0);
+          acc[2 * jp + 1] =
+              __builtin_amdgcn_mfma_f32_32x32x2f32(af[c][s], b1[s], acc[2 * jp + 1], 0, 0, 0);
         }
       }
+      // chunk c's operands are used: request the next tile's chunk c
+      if (has_next) load_chunk(base_n + 16 * c, af[c]);
+      // the previous tile's rows 8q.. leave over the chunks
+      if (pending) {
+#pragma unroll
+        for (int q = (4 * c) / NCH; q < (4 * (c + 1)) / NCH; ++q) store_q(q);
+      }
     }
-    if (!has_next) return false;
+    // lane (lr, hf) holds column lr of rows 8q + 4hf + r in acc[j][4q + r];
+    // the quad transpose gives lane 4k4 + s4 row 8q + 4hf + s4 at columns
+    // 4k4 .. 4k4 + 3
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      orow[q] = __shfl(rid, 8 * q + 4 * hf + s4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) ob[q][j][v] = acc[j][4 * q + v];
+        quad_transpose(ob[q][j], s4);
+      }
+    }
+    pending = true;
+    if (!has_next) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) store_q(q);
+      return false;
+    }
     ++tile;
     g = g_n;
-    m0 = m0_n;
-    m_end = m_end_n;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      rid[i] = rid_n[i];
-      base[i] = base_n[i];
-    }
+    rid = rid_n;
+    base = base_n;
     return true;
   };
-  if (run_tile())
-    while (run_tile()) {
-    }
+  while (run_tile()) {
+  }
 }
 
 // ---------------------------------------------------------------- grouping
@@ -677,22 +688,22 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather) {
   const int64_t nt = (L.N + GBN - 1) / GBN;
   if constexpr (sizeof(T) == 4) {
     if (resident) {
-      // upper bound of the tile count; one resident workgroup per CU (its
-      // registers), each a contiguous range of tiles
+      // upper bound of the tile count; two resident workgroups per CU (their
+      // LDS blocks), each a contiguous range of tiles
       const int64_t mt = (L.n + RB_TM - 1) / RB_TM + L.R;
-      int64_t wgs = 256 / nt;
+      int64_t wgs = 512 / nt;
       if (wgs < 1) wgs = 1;
       if (wgs > mt) wgs = mt;
       const int64_t per = (mt + wgs - 1) / wgs;
       const dim3 grid((unsigned)wgs, (unsigned)nt), block(RB_THREADS);
       switch (Kp / 16) {
-        case 2: hipLaunchKernelGGL((grouped_gemm_resident_kernel<T, 2>), grid, block, 0, L.stream, a, per,
+        case 2: hipLaunchKernelGGL((grouped_gemm_resident_kernel<2>), grid, block, 0, L.stream, a, per,
                              a.tile_ptr, a.group_off); break;
-        case 4: hipLaunchKernelGGL((grouped_gemm_resident_kernel<T, 4>), grid, block, 0, L.stream, a, per,
+        case 4: hipLaunchKernelGGL((grouped_gemm_resident_kernel<4>), grid, block, 0, L.stream, a, per,
                              a.tile_ptr, a.group_off); break;
-        case 6: hipLaunchKernelGGL((grouped_gemm_resident_kernel<T, 6>), grid, block, 0, L.stream, a, per,
+        case 6: hipLaunchKernelGGL((grouped_gemm_resident_kernel<6>), grid, block, 0, L.stream, a, per,
                              a.tile_ptr, a.group_off); break;
-        default: hipLaunchKernelGGL((grouped_gemm_resident_kernel<T, 8>), grid, block, 0, L.stream, a, per,
+        default: hipLaunchKernelGGL((grouped_gemm_resident_kernel<8>), grid, block, 0, L.stream, a, per,
                              a.tile_ptr, a.group_off); break;
       }
       return hipGetLastError();

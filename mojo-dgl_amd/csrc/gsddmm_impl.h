@@ -199,10 +199,27 @@ __global__ __launch_bounds__(BLOCK) void gsddmm_dot_kernel(GsddmmArgs<T> a) {
   }
   // butterfly inside the lane group; every lane of the wavefront runs it
 #pragma unroll
-  for (int u = 0; u < DOT_U; ++u) {
-    T pu = part[u];
-    for (int off = G >> 1; off >= 1; off >>= 1) pu = pu + __shfl_xor(pu, off);
-    if (lp[u] && gl == 0) __builtin_nontemporal_store(pu, a.out + task[u]);
+  for (int u = 0; u < DOT_U; ++u)
+    for (int off = G >> 1; off >= 1; off >>= 1) part[u] = part[u] + __shfl_xor(part[u], off);
+  if (G >= DOT_U) {
+    // the wavefront's DOT_U * 64 / G tasks are consecutive: lane t takes
+    // task wave * nt + t from its group's lanes and the results leave as one
+    // coalesced store (one partial-line store per round wrote every output
+    // line back about five times)
+    const int pr = WAVE / G, nt = DOT_U * pr;
+    const int su = lane / pr, src = (lane % pr) * G;
+    T val = T(0);
+#pragma unroll
+    for (int u = 0; u < DOT_U; ++u) {
+      const T s = __shfl(part[u], src);
+      if (su == u) val = s;
+    }
+    const int64_t t = wave * nt + lane;
+    if (lane < nt && t < a.num_tasks) a.out[t] = val;
+  } else {
+#pragma unroll
+    for (int u = 0; u < DOT_U; ++u)
+      if (lp[u] && gl == 0) __builtin_nontemporal_store(part[u], a.out + task[u]);
   }
 }
 
