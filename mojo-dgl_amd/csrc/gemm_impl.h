@@ -399,12 +399,16 @@ __global__ __launch_bounds__(RB_THREADS, 2) void grouped_gemm_resident_kernel(
         float b0[8], b1[8];
         lds_chunk(&Bs[64 * jp + lr][16 * c + 8 * hf], b0);
         lds_chunk(&Bs[64 * jp + 32 + lr][16 * c + 8 * hf], b1);
+        // the wavefront issuing MFMAs goes first while the other one on its
+        // SIMD waits on memory or transposes results
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
           acc[2 * jp] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[c][s], b0[s], acc[2 * jp], 0, 0, 0);
           acc[2 * jp + 1] =
               __builtin_amdgcn_mfma_f32_32x32x2f32(af[c][s], b1[s], acc[2 * jp + 1], 0, 0, 0);
         }
+        __builtin_amdgcn_s_setprio(0);
       }
       // chunk c's operands are used: request the next tile's chunk c
       if (has_next) load_chunk(base_n + 16 * c, af[c]);
