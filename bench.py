@@ -218,6 +218,18 @@ def cpu_cores():
         return os.cpu_count() or 1
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_rate(once, units, seconds, unit, sample, cores, scale=1e9):
     """The oracle's rate on a sample: one warm-up, then repetitions until
     `seconds` have passed (at least 3), best and median (the reference's
@@ -232,7 +244,8 @@ def cpu_rate(once, units, seconds, unit, sample, cores, scale=1e9):
     return {"value": round(units / best / scale, 4), "median_value": round(units / med / scale, 4),
             "unit": unit, "cores": cores, "kind": "port",
             "sample": "{}; best of {} repetitions ({:.1f} s)".format(sample, len(times),
-                                                                    sum(times))}
+                                                                    sum(times)),
+            "host": {"cpus_available": cpu_cores(), "model": cpu_model()}}
 
 
 def oracle_setup():

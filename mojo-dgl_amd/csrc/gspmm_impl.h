@@ -103,7 +103,7 @@ template <class T, int OP, int RED, int VEC, int LM, int RM, bool WIDE, bool NT,
           bool DOT = false>
 __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, int64_t wave,
                                            int lane) {
-  constexpr int U = 4;
+  constexpr int U = 8;
   const int G = WIDE ? WAVE : a.G;
   const int grp = lane / G, gl = lane % G, gbase = grp * G;
   const int64_t uw = chunk ? a.chunk_uwaves : a.row_uwaves;
