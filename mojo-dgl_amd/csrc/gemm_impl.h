@@ -821,6 +821,7 @@ __global__ __launch_bounds__(BLOCK) void grouped_tn_kernel(TnArgs<T> p) {
   for (int64_t s = 0; s < nstages; ++s) {
     const int buf = s & 1;
     if (s + 1 < nstages) load_stage(r0 + (s + 1) * BK);
+    __builtin_amdgcn_s_setprio(1);  // MFMA issue first (as in the forward kernel)
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 4) {
       T af[4], bf[4];
@@ -834,6 +835,7 @@ __global__ __launch_bounds__(BLOCK) void grouped_tn_kernel(TnArgs<T> p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = M::step(af[i], bf[j], acc[i][j]);
     }
+    __builtin_amdgcn_s_setprio(0);
     if (s + 1 < nstages) {
       store_stage(buf ^ 1);
       __syncthreads();

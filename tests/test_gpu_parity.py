@@ -1038,3 +1038,38 @@ def test_results_are_deterministic_run_to_run():
     first = [t.clone() for t in run()]
     for x, y in zip(first, run()):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("d1", [32, 64, 96, 128])
+@pytest.mark.parametrize("d2", [1, 5, 128, 130, 256])
+def test_grouped_mm_block_resident_shapes(d1, d2):
+    """The float32 kernel that keeps a b block in LDS (K a multiple of 32 up
+    to 128, rows of a 16-byte aligned): every chunk count, output widths
+    below, at and past one 128-column tile (odd widths store element by
+    element), groups that are empty, shorter than a 128-row tile or span
+    many tiles; segment_mm (consecutive groups) and gather_mm (rows through
+    the bucketing permutation) against the oracle, and gather_mm against
+    segment_mm on the stably sorted rows bit for bit (same kernel, same
+    per-row arithmetic)."""
+    rng = np.random.default_rng(d1 * 1000 + d2)
+    r = 9
+    seglen = np.array([0, 1, 127, 128, 129, 700, 0, 3, 2000])
+    n = int(seglen.sum())
+    a = rng.normal(size=(n, d1)).astype(np.float32)
+    b = (rng.normal(size=(r, d1, d2)) / np.sqrt(d1)).astype(np.float32)
+    got = ops.segment_mm(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda(), seglen)
+    got = got.cpu().numpy()
+    close(got, oracle.segment_mm(a, b, seglen, np.float64),
+          oracle.segment_mm(np.abs(a), np.abs(b), seglen, np.float64), np.float32,
+          "segment_mm d1 {} d2 {}".format(d1, d2))
+    idx = np.repeat(np.arange(r), seglen)
+    rng.shuffle(idx)
+    gm = ops.gather_mm(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda(),
+                       idx_b=torch.from_numpy(idx).cuda()).cpu().numpy()
+    close(gm, oracle.gather_mm(a, b, idx, np.float64),
+          oracle.gather_mm(np.abs(a), np.abs(b), idx, np.float64), np.float32,
+          "gather_mm d1 {} d2 {}".format(d1, d2))
+    perm = np.argsort(idx, kind="stable")
+    want = np.empty_like(gm)
+    want[perm] = ops.segment_mm(a[perm], b, np.bincount(idx, minlength=r))
+    np.testing.assert_array_equal(gm, want)
