@@ -365,3 +365,17 @@ def test_missing_library_at_mojodgl_lib_is_built_or_refused(tmp_path):
                          timeout=300)
     assert out.stdout.strip() == "BuildError True", out.stdout + out.stderr
     assert not target.exists()
+
+
+def test_bench_measures_one_gpu_only():
+    """bench.py --gpus N with N above 1 exits with a message instead of
+    measuring: there is no multi-GPU path."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    out = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                         capture_output=True, text=True, timeout=120)
+    assert out.returncode == 2
+    assert "one GPU" in out.stderr
