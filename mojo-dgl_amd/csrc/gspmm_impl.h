@@ -103,7 +103,9 @@ template <class T, int OP, int RED, int VEC, int LM, int RM, bool WIDE, bool NT,
           bool DOT = false>
 __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, int64_t wave,
                                            int lane) {
-  constexpr int U = 8;
+  // edges in flight per lane: 8 (4 in the dot pass, whose per-edge
+  // butterflies already hide the loads; 8 there cost 14 %)
+  constexpr int U = DOT ? 4 : 8;
   const int G = WIDE ? WAVE : a.G;
   const int grp = lane / G, gl = lane % G, gbase = grp * G;
   const int64_t uw = chunk ? a.chunk_uwaves : a.row_uwaves;
