@@ -369,8 +369,9 @@ __global__ __launch_bounds__(BLOCK) void seg_softmax_stage_kernel(SegArgs<T> a) 
   constexpr int PER = CH / WAVE;
   constexpr int SV = WAVE * 16 / (int)sizeof(T);       // m / s entries: P * nvec * VEC <= SV
   __shared__ __align__(16) T buf[WAVES_PER_BLOCK][SEG_WB / sizeof(T)];
+  // per segment and column: the maximum (passes 1-2), then 1 / sum (3-4);
+  // one array, so four workgroups fit a CU
   __shared__ __align__(16) T mx[WAVES_PER_BLOCK][SV];
-  __shared__ __align__(16) T sm[WAVES_PER_BLOCK][SV];
   __shared__ unsigned char owner[WAVES_PER_BLOCK][CH];  // lane group of each window row
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_BLOCK + w;
@@ -449,7 +450,7 @@ __global__ __launch_bounds__(BLOCK) void seg_softmax_stage_kernel(SegArgs<T> a) 
       }
       wave_sync_lds();
       // 2. e = exp(x - m) over the whole window, every lane, in place
-#pragma unroll
+#pragma unroll 2
       for (int i = 0; i < PER; ++i) {
         const int c = lane + i * WAVE;
         if (c < nch) {
@@ -477,14 +478,14 @@ __global__ __launch_bounds__(BLOCK) void seg_softmax_stage_kernel(SegArgs<T> a) 
           for (int v = 0; v < VEC; ++v) su[v] = su[v] + x[v];
         }
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) sm[w][mslot + v] = T(1) / su[v];
+        for (int v = 0; v < VEC; ++v) mx[w][mslot + v] = T(1) / su[v];
       }
       wave_sync_lds();
       // 4. out = e * (1 / s) over the whole window, every lane, coalesced
       //    stores (one correctly rounded reciprocal per segment and column
       //    instead of a divide per value: within two roundings of e / s)
       const int64_t b0 = (int64_t)W * a.d;
-#pragma unroll
+#pragma unroll 2
       for (int i = 0; i < PER; ++i) {
         const int c = lane + i * WAVE;
         if (c < nch) {
@@ -494,7 +495,7 @@ __global__ __launch_bounds__(BLOCK) void seg_softmax_stage_kernel(SegArgs<T> a) 
           if constexpr (VEC > 1) load_n<T, VEC>(&buf[w][c * VEC], y);
           else y[0] = buf[w][c];
 #pragma unroll
-          for (int v = 0; v < VEC; ++v) y[v] = y[v] * sm[w][ms + v];
+          for (int v = 0; v < VEC; ++v) y[v] = y[v] * mx[w][ms + v];
           if constexpr (VEC > 1) store_n_stream<T, VEC>(a.out + b0 + (int64_t)c * VEC, y);
           else a.out[b0 + c] = y[0];
         }
