@@ -448,24 +448,54 @@ __global__ __launch_bounds__(RB_THREADS, 2) void grouped_gemm_resident_kernel(
 }
 
 // ---------------------------------------------------------------- grouping
-// offsets[g] = exclusive prefix of seglen; tile_ptr[g] = exclusive prefix of
-// ceil(len / tm), tm the kernel's tile height. One thread; R is small (number
-// of b blocks).
-static __global__ __launch_bounds__(1024) void seg_plan_kernel(const int64_t* __restrict__ seglen,
-                                                        int32_t* __restrict__ group_off,
-                                                        int32_t* __restrict__ tile_ptr, int64_t R,
-                                                        int tm) {
-  if (threadIdx.x != 0) return;
-  int64_t off = 0, tiles = 0;
-  for (int64_t g = 0; g < R; ++g) {
-    group_off[g] = (int32_t)off;
-    tile_ptr[g] = (int32_t)tiles;
-    const int64_t len = seglen[g];
-    off += len;
-    tiles += (len + tm - 1) / tm;
+// Exclusive prefixes of the group lengths and of their tile counts
+// ceil(len / tm), 1024 groups at a time by one workgroup (a scan in LDS per
+// step, the running totals carried in registers). With `first` (bucketing)
+// each group's first sorted position is written there too.
+constexpr int PLAN_T = 1024;
+
+__device__ __forceinline__ void plan_scan(const int64_t* len,  // may be `first`
+                                          int32_t* __restrict__ group_off,
+                                          int32_t* __restrict__ tile_ptr, int64_t* first,
+                                          int64_t R, int tm) {
+  __shared__ int64_t so[PLAN_T], st[PLAN_T];
+  const int t = threadIdx.x;
+  int64_t carry_o = 0, carry_t = 0;
+  for (int64_t base = 0; base < R; base += PLAN_T) {
+    const int64_t g = base + t;
+    const int64_t l = g < R ? len[g] : 0;
+    so[t] = l;
+    st[t] = (l + tm - 1) / tm;
+    __syncthreads();
+    for (int off = 1; off < PLAN_T; off <<= 1) {  // inclusive scan
+      const int64_t ao = t >= off ? so[t - off] : 0, at = t >= off ? st[t - off] : 0;
+      __syncthreads();
+      so[t] += ao;
+      st[t] += at;
+      __syncthreads();
+    }
+    if (g < R) {
+      const int64_t eo = carry_o + so[t] - l;
+      group_off[g] = (int32_t)eo;
+      tile_ptr[g] = (int32_t)(carry_t + st[t] - (l + tm - 1) / tm);
+      if (first) first[g] = eo;  // len[g] was read above by this thread only
+    }
+    carry_o += so[PLAN_T - 1];
+    carry_t += st[PLAN_T - 1];
+    __syncthreads();  // so / st are rewritten by the next step
   }
-  group_off[R] = (int32_t)off;
-  tile_ptr[R] = (int32_t)tiles;
+  if (t == 0) {
+    group_off[R] = (int32_t)carry_o;
+    tile_ptr[R] = (int32_t)carry_t;
+  }
+}
+
+// group_off / tile_ptr from segment_mm's lengths (the host checked them).
+static __global__ __launch_bounds__(PLAN_T) void seg_plan_kernel(const int64_t* __restrict__ seglen,
+                                                          int32_t* __restrict__ group_off,
+                                                          int32_t* __restrict__ tile_ptr, int64_t R,
+                                                          int tm) {
+  plan_scan(seglen, group_off, tile_ptr, nullptr, R, tm);
 }
 
 constexpr int SORT_CHUNK = 8192;  // rows per counting-sort workgroup
@@ -519,22 +549,13 @@ static __global__ __launch_bounds__(BLOCK) void bucket_colscan_kernel(int32_t* _
   if (t == BLOCK - 1) totals[g] = part[BLOCK - 1];
 }
 
-// group_off / tile_ptr from the group totals (one thread; R is small), and
-// the totals turned into each group's first sorted position.
-static __global__ void bucket_plan_kernel(int64_t* __restrict__ totals, int32_t* __restrict__ group_off,
-                                   int32_t* __restrict__ tile_ptr, int64_t R, int tm) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  int64_t off = 0, tiles = 0;
-  for (int64_t g = 0; g < R; ++g) {
-    const int64_t c = totals[g];
-    group_off[g] = (int32_t)off;
-    tile_ptr[g] = (int32_t)tiles;
-    totals[g] = off;
-    off += c;
-    tiles += (c + tm - 1) / tm;
-  }
-  group_off[R] = (int32_t)off;
-  tile_ptr[R] = (int32_t)tiles;
+// group_off / tile_ptr from the group totals, and the totals turned into
+// each group's first sorted position.
+static __global__ __launch_bounds__(PLAN_T) void bucket_plan_kernel(int64_t* __restrict__ totals,
+                                                             int32_t* __restrict__ group_off,
+                                                             int32_t* __restrict__ tile_ptr,
+                                                             int64_t R, int tm) {
+  plan_scan(totals, group_off, tile_ptr, totals, R, tm);
 }
 
 // perm[sorted position] = row, stable: rows of a group keep their order.
@@ -633,12 +654,12 @@ inline hipError_t plan_groups(const int64_t* idx_b, const int64_t* seglen, int64
                        idx_b, counts, n, R);
     hipLaunchKernelGGL(bucket_colscan_kernel, dim3((unsigned)R), dim3(BLOCK), 0, s, counts,
                        totals, nb, R);
-    hipLaunchKernelGGL(bucket_plan_kernel, dim3(1), dim3(64), 0, s, totals, *group_off,
+    hipLaunchKernelGGL(bucket_plan_kernel, dim3(1), dim3(PLAN_T), 0, s, totals, *group_off,
                        *tile_ptr, R, tm);
     hipLaunchKernelGGL(bucket_scatter_kernel, dim3((unsigned)nb), dim3(BLOCK),
                        (size_t)(5 * R * 4), s, idx_b, counts, totals, *perm, n, R, bits);
   } else {
-    hipLaunchKernelGGL(seg_plan_kernel, dim3(1), dim3(64), 0, s, seglen, *group_off, *tile_ptr,
+    hipLaunchKernelGGL(seg_plan_kernel, dim3(1), dim3(PLAN_T), 0, s, seglen, *group_off, *tile_ptr,
                        R, tm);
   }
   return hipGetLastError();
