@@ -43,14 +43,14 @@ __global__ __launch_bounds__(BLOCK) void clamp_kernel(const int64_t* __restrict_
   }
 }
 
-// Inclusive int64 prefix sum over tiles of CS_TILE values (16 consecutive
-// per thread), in dst itself, with no other memory: (1) every tile writes
+// Inclusive int64 prefix sum over tiles of CS_TILE values (4 consecutive
+// per thread, so a wavefront's loads span 2 KB), in dst itself, with no other memory: (1) every tile writes
 // its local inclusive scan; (2) one workgroup turns the tile totals (each
 // tile's last value) into running totals, which are final there; (3) every
 // tile but the first adds the previous tile's running total to its other
 // values. Integer addition is exact, so this equals the sequential sum.
 constexpr int CS_THREADS = 256;
-constexpr int CS_PER = 16;
+constexpr int CS_PER = 4;
 constexpr int CS_TILE = CS_THREADS * CS_PER;
 
 __global__ __launch_bounds__(CS_THREADS) void cumsum_tile_kernel(const int64_t* __restrict__ src,
@@ -180,11 +180,11 @@ __global__ __launch_bounds__(BLOCK) void segment_ids_kernel(const int32_t* __res
 }
 
 // Segment offsets from lengths (three launches: tile partials, a scan of
-// the tile totals, the tile rewrite). A tile is SEG_TILE lengths, 16
-// consecutive ones per thread. Integer sums are exact, so the offsets equal
-// the sequential [0] + cumsum.
+// the tile totals, the tile rewrite). A tile is SEG_TILE lengths, 4
+// consecutive ones per thread (1M lengths: 977 tiles). Integer sums are
+// exact, so the offsets equal the sequential [0] + cumsum.
 constexpr int SEG_THREADS = 256;
-constexpr int SEG_PER = 16;
+constexpr int SEG_PER = 4;
 constexpr int SEG_TILE = SEG_THREADS * SEG_PER;
 
 __device__ __forceinline__ int64_t seg_chunks(int64_t len, int64_t chunk_len) {
