@@ -10,6 +10,8 @@ one small read back.
 
 from __future__ import annotations
 
+import threading
+
 import numpy as np
 import torch
 
@@ -43,15 +45,38 @@ def _check_offsets(offsets, n):
             "{} rows".format(n, int(offsets[-1]) if offsets.size else 0, n))
 
 
+_PINNED = threading.local()
+
+
+def _pinned_stats(dev):
+    """This thread's pinned host buffer for one device's four offsets
+    statistics (allocated once: pinned allocations are slow)."""
+    bufs = getattr(_PINNED, "bufs", None)
+    if bufs is None:
+        bufs = _PINNED.bufs = {}
+    key = dev.index if dev.index is not None else _lib.current_device()
+    buf = bufs.get(key)
+    if buf is None:
+        buf = bufs[key] = torch.empty(4, dtype=torch.int64, pin_memory=True)
+    return buf
+
+
 class _Segments:
     """Validated segments: `off` is the int32 GPU offsets tensor, `host` the
     int64 host offsets when the lengths came from the host (None when they
     were a GPU tensor, whose offsets are formed and checked on the GPU with
     one small read back), `heavy` the number of chunks of `chunk_len` rows
     the segments longer than `chunk_len` split into (GPU lengths only),
-    `longest` the largest length."""
+    `longest` the largest length.
 
-    def __init__(self, seglen, n, chunk_len=None):
+    With `defer` the read back of GPU lengths' checks is only started: the
+    caller may queue kernels that read the offsets (they clamp every
+    offset into the rows, so invalid lengths cannot send them out of
+    bounds) and must call verify() before it returns anything; until then
+    `longest` is None."""
+
+    def __init__(self, seglen, n, chunk_len=None, defer=False):
+        self._pending = None
         if isinstance(seglen, torch.Tensor) and seglen.device.type == "cuda":
             sl = _lib.i64_device(seglen).reshape(-1)
             self.num = sl.numel()
@@ -71,16 +96,17 @@ class _Segments:
                                               off.data_ptr(), stats.data_ptr(), _lib.ptr(ws),
                                               max(nbytes, 0), _lib.stream()),
                        "segment_offsets")
-            low, total, heavy, high = stats.tolist()
-            # every length in [0, n] first: then the total cannot have wrapped
-            if low < 0 or high > n or total != n:
-                raise DGLError(
-                    "segment lengths must be non-negative and sum to {}, got lengths in "
-                    "[{}, {}] summing to {}".format(n, low, high, total))
-            if chunk_len is not None:
-                self.heavy = heavy
-            self.longest = high
             self.off = off
+            self.longest = None
+            self._n, self._chunked = n, chunk_len is not None
+            if defer:
+                host = _pinned_stats(dev)
+                host.copy_(stats, non_blocking=True)
+                done = torch.cuda.Event()
+                done.record()
+                self._pending = (host, done, stats)
+            else:
+                self._check(stats.tolist())
         else:
             sl = _lib.i64(seglen)
             self.num = sl.size
@@ -89,6 +115,26 @@ class _Segments:
             self.host = _offsets(sl)
             _check_offsets(self.host, n)
             self.off = None
+
+    def _check(self, figures):
+        low, total, heavy, high = figures
+        n = self._n
+        # every length in [0, n] first: then the total cannot have wrapped
+        if low < 0 or high > n or total != n:
+            raise DGLError(
+                "segment lengths must be non-negative and sum to {}, got lengths in "
+                "[{}, {}] summing to {}".format(n, low, high, total))
+        if self._chunked:
+            self.heavy = heavy
+        self.longest = high
+
+    def verify(self):
+        """Finish a deferred check (a no-op otherwise)."""
+        if self._pending is not None:
+            host, done, _ = self._pending
+            self._pending = None
+            done.synchronize()
+            self._check(host.tolist())
 
     def device(self):
         if self.off is None:
@@ -143,7 +189,8 @@ def _segment_reduce(seglen, value, reducer, want_arg=False):
     (num_seg, d) int32 row of each max / min with `want_arg`, else None."""
     V = _lib.feature(value)
     n = V.shape[0] if V.ndim else 0
-    seg = _Segments(seglen, n)
+    # GPU lengths: their checks come back while the reduction runs
+    seg = _Segments(seglen, n, defer=True)
     d = _flat_width(V.shape)
     fshape = tuple(V.shape[1:]) if V.ndim > 1 else (1,)
     num_seg = seg.num
@@ -155,7 +202,7 @@ def _segment_reduce(seglen, value, reducer, want_arg=False):
         val = _lib.on_device(V, dtype)
         off = seg.device()
         flags = _lib.REPLACE_INF if reducer in ("max", "min") else 0
-        if seg.longest <= _lib.SEGMENT_SPLIT_ROWS:
+        if seg.longest is not None and seg.longest <= _lib.SEGMENT_SPLIT_ROWS:
             flags |= _lib.SEGMENTS_SHORT  # no split pass needed
         if want_arg and reducer in ("max", "min"):
             arg = torch.empty((num_seg, d), dtype=torch.int32, device=gdev)
@@ -168,6 +215,7 @@ def _segment_reduce(seglen, value, reducer, want_arg=False):
                                                 num_seg, d, REDUCERS[reducer], n, flags,
                                                 _lib.dtype_code(dtype), _lib.stream())
         _lib.check(rc, "segment_reduce")
+    seg.verify()  # raises for invalid GPU lengths before anything is returned
     return _lib.give_back(out.reshape((num_seg,) + fshape), V.is_torch, V.device), seg, arg
 
 

@@ -523,10 +523,12 @@ def test_segment_offsets_through_the_abi(num):
                                   int(seglen.max()) if num else 0]
 
 
-def test_wrapping_gpu_lengths_are_refused_before_any_launch():
+def test_wrapping_gpu_lengths_are_refused():
     """GPU lengths whose int64 sum wraps around to the row count: refused from
-    the offsets' stats (a length above the row count), before the segment
-    kernels run."""
+    the offsets' stats (a length above the row count) before any result is
+    returned. segment_softmax checks before its kernels run; segment_reduce
+    reads the checks back while its kernels run, which clamp every offset
+    into the rows."""
     n = 4
     wrap = np.array([2 ** 62, 2 ** 62, 2 ** 62, 2 ** 62 + n], dtype=np.int64)
     assert int(wrap.sum()) == n  # numpy's int64 sum wraps too
