@@ -22,6 +22,7 @@ import ctypes
 import hashlib
 import os
 import subprocess
+import threading
 
 import numpy as np
 import torch  # loads the HIP runtime libmdgl.so then binds to
@@ -215,6 +216,35 @@ def stream() -> int:
     if _raw_stream is not None:
         return _raw_stream(current_device())
     return torch.cuda.current_stream().cuda_stream
+
+
+_PINNED = threading.local()
+
+
+class Readback:
+    """A small GPU int64 tensor copied to pinned host memory behind the work
+    queued so far, without waiting: the GPU goes on with what the caller
+    queues next, and values() waits for the copy only. One pinned buffer per
+    thread, device and purpose, reused across calls."""
+
+    def __init__(self, src: torch.Tensor, purpose: str):
+        bufs = getattr(_PINNED, "bufs", None)
+        if bufs is None:
+            bufs = _PINNED.bufs = {}
+        dev = src.device.index if src.device.index is not None else current_device()
+        key = (purpose, dev, src.numel())
+        buf = bufs.get(key)
+        if buf is None:
+            buf = bufs[key] = torch.empty(src.numel(), dtype=torch.int64, pin_memory=True)
+        buf.copy_(src.reshape(-1), non_blocking=True)
+        self._buf, self._src = buf, src  # src lives until the copy is done
+        self._done = torch.cuda.Event()
+        self._done.record()
+
+    def values(self) -> list:
+        self._done.synchronize()
+        self._src = None
+        return self._buf.tolist()
 
 
 def ptr(t) -> int | None:

@@ -91,24 +91,27 @@ def _gather_mm(a, b, idx_b):
     if b_d1 != D1:
         raise DGLError("inner dimensions do not match: a is {} wide, b blocks are {}".format(
             D1, b_d1))
-    # GPU indices are checked on the GPU (one small read back); host indices
-    # on the host, before any GPU work
+    # GPU indices are checked on the GPU (their minimum and maximum read
+    # back); host indices on the host, before any GPU work
     on_gpu = isinstance(idx_b, torch.Tensor) and idx_b.device.type == "cuda"
     idx = _lib.i64_device(idx_b) if on_gpu else _lib.i64(idx_b)
     if idx.ndim != 1 or idx.shape[0] != N:
         raise DGLError("idx_b must be 1-D with one index per row of a: got shape {} for "
                        "N={}".format(tuple(idx.shape), N))
+    sorted_route = D1 * D2 > _SEGMENT_BLOCK or R > GATHER_MAX_BLOCKS
+    pending = None
     if N:
         if on_gpu:
-            lo, hi = torch.stack((idx.min(), idx.max())).tolist()
+            pending = _lib.Readback(torch.stack(torch.aminmax(idx)), "gather_mm_range")
+            if sorted_route:  # the grouping needs valid keys: check first
+                _check_range(pending.values(), R)
+                pending = None
         else:
-            lo, hi = int(idx.min()), int(idx.max())
-        if lo < 0 or hi >= R:
-            raise DGLError("idx_b must be in [0, {}), got [{}, {})".format(R, lo, hi + 1))
+            _check_range((int(idx.min()), int(idx.max())), R)
     if not on_gpu:
         idx = torch.from_numpy(idx).to(_lib.device())
     as_torch, dev = _lib.wants_torch(A, B), _lib.out_device(A, B)
-    if D1 * D2 > _SEGMENT_BLOCK or R > GATHER_MAX_BLOCKS:
+    if sorted_route:
         # the rows grouped by block in a stable order: the reference's stable
         # host argsort (gather_mm.py:79-87), on the GPU
         perm, seglen = group_rows(idx, R)
@@ -117,5 +120,15 @@ def _gather_mm(a, b, idx_b):
                                  gather=False, covered=N)
         out = move_rows(out_sorted, perm, scatter=True)
     else:
+        # the bucketing counts and places only indices in [0, R), so the
+        # kernels may run before the range comes back
         out = _grouped_mm(A, B, idx, None, gather=True, covered=N)
+        if pending is not None:
+            _check_range(pending.values(), R)
     return _lib.give_back(out, as_torch, dev), idx
+
+
+def _check_range(lo_hi, R):
+    lo, hi = lo_hi
+    if lo < 0 or hi >= R:
+        raise DGLError("idx_b must be in [0, {}), got [{}, {})".format(R, lo, hi + 1))

@@ -10,8 +10,6 @@ one small read back.
 
 from __future__ import annotations
 
-import threading
-
 import numpy as np
 import torch
 
@@ -43,22 +41,6 @@ def _check_offsets(offsets, n):
         raise DGLError(
             "segment lengths must be non-negative and sum to {}, got offsets ending at {} for "
             "{} rows".format(n, int(offsets[-1]) if offsets.size else 0, n))
-
-
-_PINNED = threading.local()
-
-
-def _pinned_stats(dev):
-    """This thread's pinned host buffer for one device's four offsets
-    statistics (allocated once: pinned allocations are slow)."""
-    bufs = getattr(_PINNED, "bufs", None)
-    if bufs is None:
-        bufs = _PINNED.bufs = {}
-    key = dev.index if dev.index is not None else _lib.current_device()
-    buf = bufs.get(key)
-    if buf is None:
-        buf = bufs[key] = torch.empty(4, dtype=torch.int64, pin_memory=True)
-    return buf
 
 
 class _Segments:
@@ -100,11 +82,7 @@ class _Segments:
             self.longest = None
             self._n, self._chunked = n, chunk_len is not None
             if defer:
-                host = _pinned_stats(dev)
-                host.copy_(stats, non_blocking=True)
-                done = torch.cuda.Event()
-                done.record()
-                self._pending = (host, done, stats)
+                self._pending = _lib.Readback(stats, "segment_offsets")
             else:
                 self._check(stats.tolist())
         else:
@@ -131,10 +109,8 @@ class _Segments:
     def verify(self):
         """Finish a deferred check (a no-op otherwise)."""
         if self._pending is not None:
-            host, done, _ = self._pending
-            self._pending = None
-            done.synchronize()
-            self._check(host.tolist())
+            pending, self._pending = self._pending, None
+            self._check(pending.values())
 
     def device(self):
         if self.off is None:
