@@ -397,8 +397,7 @@ int64_t mdgl_gspmm_workspace_bytes(int64_t num_chunks, int64_t dout, int reduce_
 
 namespace {
 
-// gspmm proper; `ident` makes the edge id of CSR slot i be i (segment
-// reduce, where the slots are the value rows).
+// gspmm proper.
 int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
                  const void* lhs, const void* rhs, void* dst, int64_t num_dst, int op, int64_t dl,
                  int64_t dr, int64_t dout, int reduce_op, const int32_t* deg, int nd,
@@ -406,7 +405,7 @@ int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* e
                  int32_t* arg_e, const int32_t* chunk_row, const int32_t* chunk_start,
                  int64_t num_chunks, int32_t chunk_len, const int32_t* heavy_rows,
                  const int32_t* heavy_ptr, int64_t num_heavy, void* workspace,
-                 int64_t workspace_bytes, int flags, int dtype, void* stream, bool ident,
+                 int64_t workspace_bytes, int flags, int dtype, void* stream,
                  const void* rowop = nullptr, void* dot_out = nullptr) {
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "gspmm: bad dtype %d", dtype);
   if (op < OP_ADD || op > OP_COPY_RHS || op == OP_DOT)
@@ -466,14 +465,14 @@ int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* e
   }
   if (num_dst == 0 || dout == 0) return MDGL_OK;
   if (!indptr || !dst) return fail(MDGL_EINVAL, "gspmm: null indptr or output");
-  if (op != OP_COPY_LHS && !eid && !ident) return fail(MDGL_EINVAL, "gspmm: null eid");
+  if (op != OP_COPY_LHS && !eid) return fail(MDGL_EINVAL, "gspmm: null eid");
   if (op != OP_COPY_RHS && !indices) return fail(MDGL_EINVAL, "gspmm: null indices");
   if ((op != OP_COPY_RHS && !lhs) || (op != OP_COPY_LHS && !rhs))
     return fail(MDGL_EINVAL, "gspmm: null operand");
-  if (arg && p.arg_e && !eid && !ident) return fail(MDGL_EINVAL, "gspmm: arg_e needs eid");
+  if (arg && p.arg_e && !eid) return fail(MDGL_EINVAL, "gspmm: arg_e needs eid");
   if (arg && p.arg_u && !indices) return fail(MDGL_EINVAL, "gspmm: arg_u needs indices");
   // copy_lhs without edge ids never reads edge data: slot ids stand in
-  if (ident || (op == OP_COPY_LHS && !eid)) p.flags |= F_EID_IDENTITY;
+  if (op == OP_COPY_LHS && !eid) p.flags |= F_EID_IDENTITY;
   if (op == OP_COPY_RHS && !p.arg_u) p.indices = nullptr;
   p.num_chunks = num_chunks;
   p.chunk_row = chunk_row;
@@ -558,7 +557,7 @@ int mdgl_gspmm(const int32_t* indptr, const int32_t* indices, const int32_t* eid
   return gspmm_common(indptr, indices, eid, lhs, rhs, dst, num_dst, op, dl, dr, dout, reduce_op,
                       deg, nd, lhs_shape, rhs_shape, arg_u, arg_e, chunk_row, chunk_start,
                       num_chunks, chunk_len, heavy_rows, heavy_ptr, num_heavy, workspace,
-                      workspace_bytes, flags, dtype, stream, false);
+                      workspace_bytes, flags, dtype, stream);
 }
 
 int mdgl_gspmm_mul_sum_dot(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
@@ -573,7 +572,7 @@ int mdgl_gspmm_mul_sum_dot(const int32_t* indptr, const int32_t* indices, const 
   return gspmm_common(indptr, indices, eid, lhs, rhs, dst, num_dst, OP_MUL, dl, dr, dout, RED_SUM,
                       nullptr, nd, lhs_shape, rhs_shape, nullptr, nullptr, chunk_row, chunk_start,
                       num_chunks, chunk_len, heavy_rows, heavy_ptr, num_heavy, workspace,
-                      workspace_bytes, 0, dtype, stream, false, rowop, dot);
+                      workspace_bytes, 0, dtype, stream, rowop, dot);
 }
 
 namespace {
@@ -1010,5 +1009,5 @@ extern "C" int mdgl_gspmm_noalloc(const int32_t* indptr, const int32_t* indices,
   return gspmm_common(indptr, indices, eid, lhs, rhs, dst, num_dst, op, dl, dr, dout, reduce_op,
                       deg, nd, lhs_shape, rhs_shape, arg_u, arg_e, chunk_row, chunk_start,
                       num_chunks, chunk_len, heavy_rows, heavy_ptr, num_heavy, ws,
-                      need > 0 ? MDGL_NOALLOC_SCRATCH_BYTES : 0, flags, dtype, stream, false);
+                      need > 0 ? MDGL_NOALLOC_SCRATCH_BYTES : 0, flags, dtype, stream);
 }

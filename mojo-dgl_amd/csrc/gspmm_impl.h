@@ -1,5 +1,5 @@
-// CSR reduce kernel behind gspmm and segment_reduce (included once per
-// (dtype, reducer) translation unit).
+// CSR reduce kernel behind gspmm (included once per (dtype, reducer)
+// translation unit).
 //
 // Work list. A "unit" is either a chunk of a heavy row (written as a
 // partial) or a whole row (rows longer than chunk_len are skipped there).
@@ -185,13 +185,10 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int jj = (j + u < G) ? j + u : G - 1;
-        // copy_rhs over identity edge ids (segment_reduce) needs no ids from
-        // other lanes: the slot is the edge, and the source only for an arg
+        // copy_rhs needs the source only for an arg
         constexpr bool NEED_S = OP != OP_COPY_RHS || ARG_OUT;
         int s = 0, e;
-        if (OP == OP_COPY_RHS && ident) {
-          e = start + base + jj;
-        } else if constexpr (WIDE) {
+        if constexpr (WIDE) {
           e = readlane_int(my_e, jj);
         } else {
           e = __shfl(my_e, gbase + jj);
@@ -216,7 +213,6 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
             if (!(SCALAR_E && scalar_e)) {
               const int64_t rrow = rhs_csr ? (int64_t)(start + base + j + u) : (int64_t)e;
               // a row gathered by a random edge id is read once: stream it
-              // (NT); consecutive rows (identity ids) share lines: cache them
               if constexpr (NT)
                 fetch_stream<T, VEC, RM>(a.rhs + rrow * a.dr, a.rmode, roff, y[u]);
               else
@@ -456,8 +452,8 @@ hipError_t launch_gspmm_op(const GspmmParams& p) {
     const int lm = copy_r ? a.rmode : a.lmode;
     const int rm = copy_l ? a.lmode : a.rmode;
     const dim3 grid((unsigned)a.num_blocks), block(BLOCK);
-    // edge rows are streamed unless they are consecutive (identity ids:
-    // segment_reduce, which is copy_rhs)
+    // edge rows are streamed (NT = true: every caller gathers them by edge
+    // id or reads each once in CSR order)
     bool launched = false;
     if constexpr (OP == OP_MUL && RED == RED_SUM) {
       if (p.dot_out) {
@@ -471,16 +467,7 @@ hipError_t launch_gspmm_op(const GspmmParams& p) {
         launched = true;
       }
     }
-    if (!launched) {
-      if constexpr (OP == OP_COPY_RHS) {
-        if (a.flags & F_EID_IDENTITY)
-          launch_path<T, OP, RED, VEC, false>(a, grid, block, lm, rm, p.stream);
-        else
-          launch_path<T, OP, RED, VEC, true>(a, grid, block, lm, rm, p.stream);
-      } else {
-        launch_path<T, OP, RED, VEC, true>(a, grid, block, lm, rm, p.stream);
-      }
-    }
+    if (!launched) launch_path<T, OP, RED, VEC, true>(a, grid, block, lm, rm, p.stream);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }

@@ -12,7 +12,7 @@ enum {
   F_MEAN = 1,          // divide the sum by max(degree, 1)
   F_REPLACE_INF = 2,   // +-inf -> 0 on the final value (update_all max/min)
   F_OUT_VEC = 4,       // output rows allow 16-byte stores
-  F_EID_IDENTITY = 8,  // edge id of CSR slot i is i (segment reduce)
+  F_EID_IDENTITY = 8,  // edge id of CSR slot i is i (copy_lhs given no edge ids)
   F_RHS_CSR = 16,      // the edge operand is in CSR slot order (rhs row i for slot i)
 };
 
