@@ -3,9 +3,11 @@
 //
 // Work list. A "unit" is either a chunk of a heavy row (written as a
 // partial) or a whole row (rows longer than chunk_len are skipped there).
-// The first chunk_blocks workgroups take the chunks, in dispatch order so
-// that they spread over all XCDs and start first; the remaining workgroups
-// take the rows through the XCD remap. A unit is processed
+// The first chunk_blocks workgroups take the chunks (so they start first),
+// the remaining workgroups the rows; both ranges go through the XCD remap,
+// so each XCD serves a contiguous run of units and the rows of a block of
+// neighbouring destinations share its L2 (a community graph's chunks dealt
+// round-robin over the XCDs held its L2 hit rate at 70 %). A unit is processed
 // by G consecutive lanes (G = the power of two covering the row's vectors,
 // at most 64), so a wavefront packs 64 / G units; output rows wider than
 // 64 * VEC are cut into S slabs, one wavefront per slab.
@@ -323,7 +325,7 @@ __global__ __launch_bounds__(BLOCK) void gspmm_kernel(GspmmArgs<T> a) {
   const int64_t b = blockIdx.x;
   const bool chunk = b < a.chunk_blocks;
   const int64_t blk =
-      chunk ? b : xcd_remap(b - a.chunk_blocks, a.num_blocks - a.chunk_blocks);
+      chunk ? xcd_remap(b, a.chunk_blocks) : xcd_remap(b - a.chunk_blocks, a.num_blocks - a.chunk_blocks);
   const int lane = threadIdx.x & (WAVE - 1);
   // every lane of a wavefront takes the same path below, so shuffles and
   // readlanes always see a full wavefront
