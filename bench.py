@@ -345,6 +345,8 @@ def workload_gat(args):
         "kernels": kernels,
     }
     if not args.step_only:
+        log("the step's ops alone with cold caches")
+        result["cold_caches"] = time_gat_ops_cold(g, el, er, h, N, E, H, D, args)
         log("outside the step: graph build, edge_softmax over a subset, forward + backward")
         result["graph_build"] = time_graph_build(g, u, v, N, args)
         result["edge_softmax_subset"] = time_subset_softmax(g, el, er, E, args)
@@ -360,6 +362,30 @@ def workload_gat(args):
     del g, h
     free_gpu()
     return result
+
+
+def time_gat_ops_cold(g, el, er, h, N, E, H, D, args):
+    """The step's three libmdgl ops one at a time, each after a 512 MB write
+    that evicts the L2 and the MALL (median and best of --reps, HIP events),
+    with the same algorithmic bytes as the step's figures."""
+    import torch
+
+    import mojodgl.ops as ops
+
+    cold = ColdTimer(args.reps, 1)
+    e = torch.nn.functional.leaky_relu(ops.u_add_v(g, el, er), 0.2)
+    a = ops.edge_softmax(g, e)
+    ops_ = (
+        ("gsddmm_u_add_v", lambda: ops.u_add_v(g, el, er), 8 * E + 4 * E * H * 2 + 4 * E * H,
+         E * H),
+        ("edge_softmax", lambda: ops.edge_softmax(g, e), 4 * (N + 1) + 4 * E + 4 * E * H * 2,
+         E * H),
+        ("gspmm_u_mul_e_sum", lambda: ops.u_mul_e_sum(g, h, a),
+         4 * (N + 1) + 8 * E + 4 * E * H * D + 4 * E * H + 4 * N * H * D, E * H * D),
+    )
+    out = {name: hbm_entry(cold(fn), nbytes, units) for name, fn, nbytes, units in ops_}
+    del e, a
+    return out
 
 
 def time_gather_ceilings(g, N, E, H, args):
