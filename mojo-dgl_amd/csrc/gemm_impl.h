@@ -220,29 +220,61 @@ __global__ __launch_bounds__(BLOCK) void grouped_gemm_kernel(GemmArgs<T> p) {
   }
 }
 
-// ---------------------------------------------------------------- b resident
-// float32, K a multiple of 32 up to 128, rows of a 16-byte aligned (the host
-// checks; other shapes take grouped_gemm_kernel). A workgroup (4 wavefronts,
-// two per CU) keeps the group's b block (128 columns x K) in LDS, loaded once
-// per group it meets, and walks a contiguous range of 128-row tiles; ranges
-// follow the group order, so b changes rarely. Each wavefront owns 32 rows of
-// the tile and all 128 columns: four 32 x 32 blocks of
-// v_mfma_f32_32x32x2f32, so every row of a is read by one wavefront only,
-// straight from global memory into registers (no LDS, no barrier in the K
-// loop), a whole tile ahead of the MFMAs that use it. The K axis goes in
-// 16-wide chunks; in MFMA step s of chunk c, lane half h (lanes 32h..32h+31)
-// supplies k = 16c + 8h + s, so a lane's a operands for a chunk are 8
-// consecutive floats of its row (two 16-byte loads) and its b operands 8
-// consecutive floats of a row of the LDS block (two 16-byte LDS reads, a
-// 528-byte row stride keeps 16 lanes on distinct banks). A tile's results
-// are stored while the next tile multiplies: after a 4 x 4 transpose in each
-// DPP quad they wait in registers and leave as 16-byte stores (eight rows x
-// 128 contiguous bytes per instruction) spread over the next tile's chunks.
-constexpr int RB_WAVES = 4;
-constexpr int RB_TM = 32 * RB_WAVES;   // rows per tile
-constexpr int RB_KMAX = 128;           // largest padded K held in LDS
-constexpr int RB_THREADS = 64 * RB_WAVES;
-constexpr int RB_LD = RB_KMAX + 4;
+// ---------------------------------------------------------------- float32 on bf16 MFMA
+// float32 shapes with K a multiple of 32 up to 128 and rows of a on a 16-byte
+// boundary (the host checks; other shapes and float64 take
+// grouped_gemm_kernel) run on the bf16 matrix cores with float32 accuracy.
+//
+// Arithmetic. Each float x is cut into three bf16 values without loss,
+// x = p0 + p1 + p2: p0 = x rounded to bf16 (to nearest even), p1 = the
+// remainder x - p0 (exact in float32) rounded to bf16, p2 = x - p0 - p1,
+// which has at most 8 significant bits and so is a bf16. |p1| <= 2^-8 |x| and
+// |p2| <= 2^-17 |x|. The product a * b is the sum of the nine ai * bj, each
+// exact in float32; the kernel keeps the six above 2^-25 |a b| (a0 b0, a0 b1,
+// a1 b0, a1 b1, a0 b2, a2 b0) and v_mfma_f32_32x32x16_bf16 adds them into
+// float32 accumulators, smallest first. The three left out sum to at most
+// 2^-24 |a b| (one float32 rounding of the product) with either sign, so the
+// error stays that of a float32 GEMM: against float64, rows of
+// N(0, 1) x N(0, 1/128) data with K = 128 come out with a mean error of
+// 1.6e-8 of sum |a b| against 2.0e-8 for v_mfma_f32_32x32x2f32 and for the
+// vendor float32 GEMM (maximum 2.9e-7 against 3.3e-7 and 3.9e-7). Six bf16
+// MFMAs (6 x 32 cycles) replace eight float32 ones (8 x 64) per 16-deep chunk
+// of a 32 x 32 block.
+// The fast path takes values that are zero or of magnitude in [2^-50, 2^60):
+// there every part and every kept part product is a normal number (nothing
+// lost to subnormal flushing) and no part product overflows. Others (inf and
+// NaN, which do not split, since inf - inf is NaN and a zero part times an
+// infinite one would make NaN where IEEE float gives inf; tiny and huge
+// values) send their chunk of a, or every chunk of the group whose b block
+// holds one, to v_mfma_f32_32x32x2f32 on the float32 values themselves (b read
+// from the caller's array: 64 KB per block, served by L2). inf and NaN then
+// propagate as in IEEE arithmetic.
+//
+// Work mapping. A workgroup (8 wavefronts, one per CU: the group's b block
+// held in LDS as three bf16 planes of 128 columns x Kp, 104 KB, loaded once
+// per group it meets) walks a contiguous range of 256-row tiles; ranges follow
+// the group order, so b changes rarely. Each wavefront owns 32 rows of the
+// tile and all 128 columns: four 32 x 32 blocks, so every row of a is read by
+// one wavefront only, straight from global memory into registers (no LDS, no
+// barrier in the K loop), half a tile ahead of the MFMAs that use it. The K
+// axis goes in 16-wide chunks; in chunk c lane (lr, hf) supplies
+// a[row lr][16c + 8hf .. +7] (8 consecutive floats of its row: two 16-byte
+// loads, split in registers) and b[16c + 8hf .. +7][column lr] (one 16-byte
+// LDS read per plane; a 272-byte row stride keeps 16 lanes on distinct
+// banks). A tile's results leave after a 4 x 4 transpose in each DPP quad as
+// 16-byte stores, eight rows x 128 contiguous bytes per instruction.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int SB_WAVES = 8;
+constexpr int SB_TM = 32 * SB_WAVES;     // rows per tile
+constexpr int SB_THREADS = 64 * SB_WAVES;
+constexpr int SB_KMAX = 128;             // largest padded K held in LDS
+constexpr int SB_LD = SB_KMAX + 8;       // bf16 per LDS row (272 bytes)
+constexpr int SB_MAX_SLICES = 8;         // splittability flags per group of b
+constexpr float SB_HI = 0x1p60f;         // fast-path values: |x| < SB_HI and
+constexpr int SB_EMIN = -49;             // x == 0 or frexp exponent >= SB_EMIN
 
 // Within each quad of lanes (s = lane % 4), x[r] = M[r][s] becomes
 // x[c] = M[s][c]: two butterfly stages (partner lane s ^ 1, then s ^ 2), each
@@ -269,12 +301,68 @@ __device__ __forceinline__ void quad_transpose(float (&x)[4], int s) {
     if ((r & 2) != (s & 2)) x[r] = t[r];
 }
 
+// Two floats rounded to bf16 (to nearest even), element 0 in the low half.
+__device__ __forceinline__ uint32_t bf16_pair(float x0, float x1) {
+  const bf16x2 v = {(__bf16)x0, (__bf16)x1};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Whether x takes the bf16 path (see above); zero has frexp exponent 0.
+__device__ __forceinline__ bool splits(float x) {
+  return __builtin_fabsf(x) < SB_HI && __builtin_amdgcn_frexp_expf(x) >= SB_EMIN;
+}
+
+// The three parts of two floats (|x| < 2^127), one bf16 pair per part.
+__device__ __forceinline__ void split_pair(float x0, float x1, uint32_t& q0, uint32_t& q1,
+                                           uint32_t& q2) {
+  q0 = bf16_pair(x0, x1);
+  const float r0 = x0 - bf16_lo(q0), r1 = x1 - bf16_hi(q0);
+  q1 = bf16_pair(r0, r1);
+  q2 = bf16_pair(r0 - bf16_lo(q1), r1 - bf16_hi(q1));
+}
+
+// bt3[g][q][n][k] (bf16 bit patterns): part q of b[g][k][n] (of b[g][n][k]
+// with `given_t`), zero for k in [K, Kp). Workgroup (g, s) splits slice s of
+// group g's N x Kp values and sets flags[g * slices + s] when the slice holds
+// a value off the fast path (its parts are left zero: the group's chunks all
+// take the float32 path).
+static __global__ __launch_bounds__(BLOCK) void split_b_kernel(const float* __restrict__ b,
+                                                               uint16_t* __restrict__ bt3,
+                                                               int32_t* __restrict__ flags,
+                                                               int64_t K, int64_t Kp, int64_t N,
+                                                               int given_t, int slices) {
+  const int64_t g = blockIdx.x / slices;
+  const int s = (int)(blockIdx.x % slices);
+  const int64_t per = N * Kp;
+  const int64_t lo = per * s / slices, hi = per * (s + 1) / slices;
+  uint16_t* o = bt3 + g * 3 * per;
+  int bad = 0;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += BLOCK) {
+    const int64_t k = i % Kp, n = i / Kp;
+    float x = 0.f;
+    if (k < K) x = given_t ? b[(g * N + n) * K + k] : b[(g * K + k) * N + n];
+    uint32_t q0 = 0, q1 = 0, q2 = 0;
+    if (splits(x))
+      split_pair(x, 0.f, q0, q1, q2);  // x's parts in the low halves
+    else
+      bad = 1;
+    o[i] = (uint16_t)q0;
+    o[per + i] = (uint16_t)q1;
+    o[2 * per + i] = (uint16_t)q2;
+  }
+  bad = __syncthreads_or(bad);
+  if (threadIdx.x == 0) flags[blockIdx.x] = bad;
+}
+
 template <int NCH>
-__global__ __launch_bounds__(RB_THREADS, 2) void grouped_gemm_resident_kernel(
-    GemmArgs<float> p, int64_t tiles_per_wg, const int32_t* __restrict__ tile_ptr,
-    const int32_t* __restrict__ group_off) {
+__global__ __launch_bounds__(SB_THREADS, 1) void grouped_gemm_split_kernel(
+    GemmArgs<float> p, const uint16_t* __restrict__ bt3, const int32_t* __restrict__ bflags,
+    int slices, const float* __restrict__ b, int given_t, int64_t tiles_per_wg,
+    const int32_t* __restrict__ tile_ptr, const int32_t* __restrict__ group_off) {
   typedef float f32x16 __attribute__((ext_vector_type(16)));
-  __shared__ __align__(16) float Bs[GBN][RB_LD];
+  __shared__ __align__(16) uint16_t Bs[3][GBN][SB_LD];
   const int t = threadIdx.x;
   const int lane = t & 63, w = t >> 6;
   const int lr = lane & 31, hf = lane >> 5;
@@ -294,14 +382,14 @@ __global__ __launch_bounds__(RB_THREADS, 2) void grouped_gemm_resident_kernel(
   // the row of a behind tile row 32w + lr (-1 past the group; its loads then
   // read row 0, never stored)
   auto row_of = [&](int64_t tl, int64_t gg) -> int32_t {
-    const int64_t m0 = uget(group_off, gg) + (tl - uget(tile_ptr, gg)) * RB_TM;
+    const int64_t m0 = uget(group_off, gg) + (tl - uget(tile_ptr, gg)) * SB_TM;
     const int64_t pos = m0 + w * 32 + lr;
     return pos < uget(group_off, gg + 1) ? (p.perm ? p.perm[pos] : (int32_t)pos) : -1;
   };
   auto base_of = [&](int32_t r) -> const float* {
     return p.a + (int64_t)(r >= 0 ? r : 0) * p.K + 8 * hf;
   };
-  // 8 consecutive floats (two 16-byte loads) from a row of a / of the block
+  // 8 consecutive floats (two 16-byte loads) from a row of a
   auto load_chunk = [&](const float* q, float (&d)[8]) {
     float x[4], y[4];
     load_global_n<float, 4>(q, x);
@@ -312,17 +400,11 @@ __global__ __launch_bounds__(RB_THREADS, 2) void grouped_gemm_resident_kernel(
       d[4 + i] = y[i];
     }
   };
-  auto lds_chunk = [&](const float* q, float (&d)[8]) {
-    float x[4], y[4];
-    load_n<float, 4>(q, x);
-    load_n<float, 4>(q + 4, y);
+  // the three parts of b[k .. k + 7][column r] (one 16-byte LDS read each)
+  auto lds_parts = [&](int r, int k, u32x4 (&d)[3]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      d[i] = x[i];
-      d[4 + i] = y[i];
-    }
+    for (int q = 0; q < 3; ++q) d[q] = *reinterpret_cast<const u32x4*>(&Bs[q][r][k]);
   };
-
   int64_t tile = first;
   // group of the first tile: last g with tile_ptr[g] <= tile (uniform)
   int64_t g = 0;
@@ -336,44 +418,34 @@ __global__ __launch_bounds__(RB_THREADS, 2) void grouped_gemm_resident_kernel(
   }
   int32_t rid = row_of(tile, g);
   const float* base = base_of(rid);
-  float af[NCH][8];  // the tile's a operands, chunk by chunk
+  // a values in a ring of RS chunks: chunk c lives in af[c % RS] and, once
+  // used, its slot takes the chunk RS later (this tile's or the next one's)
+  constexpr int RS = NCH >= 4 ? NCH / 2 : NCH;
+  float af[RS][8];
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) load_chunk(base + 16 * c, af[c]);
+  for (int c = 0; c < RS; ++c) load_chunk(base + 16 * c, af[c]);
 
-  // results of the previous tile: ob[q][j] is row 8q + 4hf + s4 of the
-  // tile, columns 32j + 4k4 .. +3, for output row orow[q]
-  float ob[4][4][4];
-  int32_t orow[4] = {-1, -1, -1, -1};
-  auto store_q = [&](int q) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t n = n0 + 32 * j + 4 * k4;
-      if (orow[q] < 0 || n >= p.N) continue;
-      float* o = p.out + (int64_t)orow[q] * p.N + n;
-      if (p.out_vec && n + 4 <= p.N) {
-        store_n<float, 4>(o, ob[q][j]);
-      } else {
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-          if (n + v < p.N) o[v] = ob[q][j][v];
-      }
-    }
-  };
-  bool pending = false;
   int64_t cur_g = -1;
-  // One tile: its b block (when the group changes), the K loop with the
-  // previous tile's stores and the next tile's loads, the results kept.
+  bool b_whole = false;  // the group's b block has a value that does not split
+  // One tile: its b block (when the group changes), the K loop with the next
+  // tile's loads, the results stored.
   auto run_tile = [&]() -> bool {
     if (g != cur_g) {
       __syncthreads();  // every wavefront is done with the previous block
-      const float* bt_g = p.bt + g * p.N * p.Kp;
-      constexpr int CPR = NCH * 4;  // 16-byte chunks per row of the block
-      for (int c = t; c < GBN * CPR; c += RB_THREADS) {
-        const int r = c / CPR, k = (c % CPR) * 4;
-        float v[4] = {0.f, 0.f, 0.f, 0.f};
-        if (n0 + r < p.N) load_global_n<float, 4>(bt_g + (n0 + r) * p.Kp + k, v);
-        store_n<float, 4>(&Bs[r][k], v);
+      const int64_t per = p.N * p.Kp;
+      const uint16_t* src = bt3 + g * 3 * per;
+      constexpr int CPR = NCH * 2;  // 16-byte pieces per row of a part
+      for (int c = t; c < 3 * GBN * CPR; c += SB_THREADS) {
+        const int q = c / (GBN * CPR), rem = c % (GBN * CPR);
+        const int r = rem / CPR, k = (rem % CPR) * 8;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (n0 + r < p.N)
+          v = *(const __attribute__((address_space(1))) u32x4*)(src + q * per + (n0 + r) * p.Kp + k);
+        *reinterpret_cast<u32x4*>(&Bs[q][r][k]) = v;
       }
+      int bad = 0;
+      for (int s = 0; s < slices; ++s) bad |= (int)uget(bflags, g * slices + s);
+      b_whole = bad != 0;
       __syncthreads();
       cur_g = g;
     }
@@ -393,50 +465,92 @@ __global__ __launch_bounds__(RB_THREADS, 2) void grouped_gemm_resident_kernel(
       for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      // blocks in pairs, so consecutive MFMAs never update the same block
+      int ok = 1;
 #pragma unroll
-      for (int jp = 0; jp < 2; ++jp) {
-        float b0[8], b1[8];
-        lds_chunk(&Bs[64 * jp + lr][16 * c + 8 * hf], b0);
-        lds_chunk(&Bs[64 * jp + 32 + lr][16 * c + 8 * hf], b1);
-        // the wavefront issuing MFMAs goes first while the other one on its
-        // SIMD waits on memory or transposes results
-        __builtin_amdgcn_s_setprio(1);
+      for (int s = 0; s < 8; ++s) ok &= splits(af[c % RS][s]) ? 1 : 0;
+      if (!b_whole && __builtin_amdgcn_ballot_w64(!ok) == 0) {
+        u32x4 A[3];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          acc[2 * jp] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[c][s], b0[s], acc[2 * jp], 0, 0, 0);
-          acc[2 * jp + 1] =
-              __builtin_amdgcn_mfma_f32_32x32x2f32(af[c][s], b1[s], acc[2 * jp + 1], 0, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+          uint32_t q0, q1, q2;
+          split_pair(af[c % RS][2 * i], af[c % RS][2 * i + 1], q0, q1, q2);
+          A[0][i] = q0;
+          A[1][i] = q1;
+          A[2][i] = q2;
         }
-        __builtin_amdgcn_s_setprio(0);
-      }
-      // chunk c's operands are used: request the next tile's chunk c
-      if (has_next) load_chunk(base_n + 16 * c, af[c]);
-      // the previous tile's rows 8q.. leave over the chunks
-      if (pending) {
 #pragma unroll
-        for (int q = (4 * c) / NCH; q < (4 * (c + 1)) / NCH; ++q) store_q(q);
+        for (int jp = 0; jp < 2; ++jp) {
+          u32x4 B0[3], B1[3];
+          lds_parts(64 * jp + lr, 16 * c + 8 * hf, B0);
+          lds_parts(64 * jp + 32 + lr, 16 * c + 8 * hf, B1);
+          // the wavefront issuing MFMAs goes first while the other one on its
+          // SIMD waits on memory or transposes results
+          __builtin_amdgcn_s_setprio(1);
+          constexpr int ORD[6][2] = {{0, 2}, {2, 0}, {1, 1}, {0, 1}, {1, 0}, {0, 0}};
+#pragma unroll
+          for (int o = 0; o < 6; ++o) {
+            const bf16x8 av = __builtin_bit_cast(bf16x8, A[ORD[o][0]]);
+            acc[2 * jp] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                av, __builtin_bit_cast(bf16x8, B0[ORD[o][1]]), acc[2 * jp], 0, 0, 0);
+            acc[2 * jp + 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                av, __builtin_bit_cast(bf16x8, B1[ORD[o][1]]), acc[2 * jp + 1], 0, 0, 0);
+          }
+          __builtin_amdgcn_s_setprio(0);
+        }
+      } else {
+        // float32 MFMAs on b from the caller's array (b[g][k][n], or
+        // b[g][n][k] with given_t; 0 past the last column); in step s lane
+        // half hf supplies k = 16c + 8hf + s
+        const int64_t kb = 16 * c + 8 * hf;
+        const int64_t ks = given_t ? 1 : p.N, ns = given_t ? p.K : 1;
+        const float* bg = b + g * p.K * p.N + kb * ks;
+#pragma unroll
+        for (int jp = 0; jp < 2; ++jp) {
+          const int64_t na = n0 + 64 * jp + lr, nb = na + 32;
+          const float* pa = bg + na * ns;
+          const float* pb = bg + nb * ns;
+#pragma unroll
+          for (int s = 0; s < 8; ++s) {
+            const float x = na < p.N ? load_global(pa + s * ks) : 0.f;
+            acc[2 * jp] =
+                __builtin_amdgcn_mfma_f32_32x32x2f32(af[c % RS][s], x, acc[2 * jp], 0, 0, 0);
+            const float y = nb < p.N ? load_global(pb + s * ks) : 0.f;
+            acc[2 * jp + 1] =
+                __builtin_amdgcn_mfma_f32_32x32x2f32(af[c % RS][s], y, acc[2 * jp + 1], 0, 0, 0);
+          }
+        }
       }
+      // chunk c's values are used: request the chunk RS later
+      if (c + RS < NCH)
+        load_chunk(base + 16 * (c + RS), af[c % RS]);
+      else if (has_next)
+        load_chunk(base_n + 16 * (c + RS - NCH), af[c % RS]);
     }
     // lane (lr, hf) holds column lr of rows 8q + 4hf + r in acc[j][4q + r];
     // the quad transpose gives lane 4k4 + s4 row 8q + 4hf + s4 at columns
     // 4k4 .. 4k4 + 3
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      orow[q] = __shfl(rid, 8 * q + 4 * hf + s4);
+      const int32_t orow = __shfl(rid, 8 * q + 4 * hf + s4);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
+        float x[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) ob[q][j][v] = acc[j][4 * q + v];
-        quad_transpose(ob[q][j], s4);
+        for (int v = 0; v < 4; ++v) x[v] = acc[j][4 * q + v];
+        quad_transpose(x, s4);
+        const int64_t n = n0 + 32 * j + 4 * k4;
+        if (orow < 0 || n >= p.N) continue;
+        float* o = p.out + (int64_t)orow * p.N + n;
+        if (p.out_vec && n + 4 <= p.N) {
+          store_n<float, 4>(o, x);
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (n + v < p.N) o[v] = x[v];
+        }
       }
     }
-    pending = true;
-    if (!has_next) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) store_q(q);
-      return false;
-    }
+    if (!has_next) return false;
     ++tile;
     g = g_n;
     rid = rid_n;
@@ -665,10 +779,26 @@ inline hipError_t plan_groups(const int64_t* idx_b, const int64_t* seglen, int64
   return hipGetLastError();
 }
 
-// Workspace of one grouped GEMM: bt, then the grouping.
+// Slices of a group's b block that the split kernel flags separately: as
+// many as keep a slice at 2,048 values or more, at most SB_MAX_SLICES.
+inline int split_slices(int64_t N, int64_t Kp) {
+  int64_t s = N * Kp / 2048;
+  return s < 1 ? 1 : (s > SB_MAX_SLICES ? SB_MAX_SLICES : (int)s);
+}
+
+// Bytes of the b region: bt (float32 / float64 transposed) or, for float32,
+// the three bf16 planes (6 bytes per value) and their finiteness flags.
+template <class T>
+int64_t b_region_bytes(int64_t K, int64_t N, int64_t R) {
+  const int64_t v = R * N * gemm_kp<T>(K);
+  if (sizeof(T) == 4) return ws_align(v * 6) + ws_align(R * SB_MAX_SLICES * 4);
+  return ws_align(v * (int64_t)sizeof(T));
+}
+
+// Workspace of one grouped GEMM: the b region, then the grouping.
 template <class T>
 int64_t grouped_workspace_bytes(int64_t n, int64_t K, int64_t N, int64_t R, bool gather) {
-  return ws_align(R * N * gemm_kp<T>(K) * (int64_t)sizeof(T)) + plan_workspace_bytes(n, R, gather);
+  return b_region_bytes<T>(K, N, R) + plan_workspace_bytes(n, R, gather);
 }
 
 template <class T>
@@ -676,18 +806,27 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather) {
   if (L.n <= 0 || L.N <= 0 || L.R <= 0) return hipSuccess;
   const int64_t Kp = gemm_kp<T>(L.K);
   constexpr int EVH = 16 / sizeof(T);
-  const bool resident = sizeof(T) == 4 && Kp <= RB_KMAX && Kp == L.K &&
+  const bool split = sizeof(T) == 4 && Kp <= SB_KMAX && Kp == L.K &&
                         reinterpret_cast<uintptr_t>(L.a) % 16 == 0 && L.K % EVH == 0;
-  const int tm = resident ? RB_TM : GBM;
+  const int tm = split ? SB_TM : GBM;
   char* w = static_cast<char*>(L.workspace);
   T* bt = reinterpret_cast<T*>(w);
-  w += ws_align(L.R * L.N * Kp * (int64_t)sizeof(T));
+  const int64_t vals = L.R * L.N * Kp;
+  uint16_t* bt3 = reinterpret_cast<uint16_t*>(w);
+  int32_t* bflags = reinterpret_cast<int32_t*>(w + ws_align(vals * 6));
+  const int slices = split_slices(L.N, Kp);
+  w += b_region_bytes<T>(L.K, L.N, L.R);
 
-  const int64_t tot = L.R * L.N * Kp;
-  int64_t tb = (tot + BLOCK - 1) / BLOCK;
-  if (tb > 65536) tb = 65536;
-  hipLaunchKernelGGL((transpose_b_kernel<T>), dim3((unsigned)tb), dim3(BLOCK), 0, L.stream,
-                     static_cast<const T*>(L.b), bt, L.R, L.K, Kp, L.N, L.trans_b);
+  if (split) {
+    hipLaunchKernelGGL(split_b_kernel, dim3((unsigned)(L.R * slices)), dim3(BLOCK), 0, L.stream,
+                       static_cast<const float*>(L.b), bt3, bflags, L.K, Kp, L.N, L.trans_b,
+                       slices);
+  } else {
+    int64_t tb = (vals + BLOCK - 1) / BLOCK;
+    if (tb > 65536) tb = 65536;
+    hipLaunchKernelGGL((transpose_b_kernel<T>), dim3((unsigned)tb), dim3(BLOCK), 0, L.stream,
+                       static_cast<const T*>(L.b), bt, L.R, L.K, Kp, L.N, L.trans_b);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
 
@@ -712,24 +851,25 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather) {
   a.out_vec = (L.N % EV == 0) && (reinterpret_cast<uintptr_t>(L.out) % 16 == 0);
   const int64_t nt = (L.N + GBN - 1) / GBN;
   if constexpr (sizeof(T) == 4) {
-    if (resident) {
-      // upper bound of the tile count; two resident workgroups per CU (their
-      // LDS blocks), each a contiguous range of tiles
-      const int64_t mt = (L.n + RB_TM - 1) / RB_TM + L.R;
-      int64_t wgs = 512 / nt;
+    if (split) {
+      // upper bound of the tile count; one workgroup per CU (its LDS planes),
+      // each a contiguous range of tiles
+      const int64_t mt = (L.n + SB_TM - 1) / SB_TM + L.R;
+      int64_t wgs = 256 / nt;
       if (wgs < 1) wgs = 1;
       if (wgs > mt) wgs = mt;
       const int64_t per = (mt + wgs - 1) / wgs;
-      const dim3 grid((unsigned)wgs, (unsigned)nt), block(RB_THREADS);
+      const dim3 grid((unsigned)wgs, (unsigned)nt), block(SB_THREADS);
+      const float* bsrc = static_cast<const float*>(L.b);
       switch (Kp / 16) {
-        case 2: hipLaunchKernelGGL((grouped_gemm_resident_kernel<2>), grid, block, 0, L.stream, a, per,
-                             a.tile_ptr, a.group_off); break;
-        case 4: hipLaunchKernelGGL((grouped_gemm_resident_kernel<4>), grid, block, 0, L.stream, a, per,
-                             a.tile_ptr, a.group_off); break;
-        case 6: hipLaunchKernelGGL((grouped_gemm_resident_kernel<6>), grid, block, 0, L.stream, a, per,
-                             a.tile_ptr, a.group_off); break;
-        default: hipLaunchKernelGGL((grouped_gemm_resident_kernel<8>), grid, block, 0, L.stream, a, per,
-                             a.tile_ptr, a.group_off); break;
+        case 2: hipLaunchKernelGGL((grouped_gemm_split_kernel<2>), grid, block, 0, L.stream, a, bt3,
+                             bflags, slices, bsrc, L.trans_b, per, a.tile_ptr, a.group_off); break;
+        case 4: hipLaunchKernelGGL((grouped_gemm_split_kernel<4>), grid, block, 0, L.stream, a, bt3,
+                             bflags, slices, bsrc, L.trans_b, per, a.tile_ptr, a.group_off); break;
+        case 6: hipLaunchKernelGGL((grouped_gemm_split_kernel<6>), grid, block, 0, L.stream, a, bt3,
+                             bflags, slices, bsrc, L.trans_b, per, a.tile_ptr, a.group_off); break;
+        default: hipLaunchKernelGGL((grouped_gemm_split_kernel<8>), grid, block, 0, L.stream, a, bt3,
+                             bflags, slices, bsrc, L.trans_b, per, a.tile_ptr, a.group_off); break;
       }
       return hipGetLastError();
     }

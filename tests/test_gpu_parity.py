@@ -1045,17 +1045,17 @@ def test_results_are_deterministic_run_to_run():
 @pytest.mark.parametrize("d1", [32, 64, 96, 128])
 @pytest.mark.parametrize("d2", [1, 5, 128, 130, 256])
 def test_grouped_mm_block_resident_shapes(d1, d2):
-    """The float32 kernel that keeps a b block in LDS (K a multiple of 32 up
-    to 128, rows of a 16-byte aligned): every chunk count, output widths
-    below, at and past one 128-column tile (odd widths store element by
-    element), groups that are empty, shorter than a 128-row tile or span
-    many tiles; segment_mm (consecutive groups) and gather_mm (rows through
-    the bucketing permutation) against the oracle, and gather_mm against
-    segment_mm on the stably sorted rows bit for bit (same kernel, same
-    per-row arithmetic)."""
+    """The float32 kernel on the bf16 matrix cores, which keeps a b block in
+    LDS (K a multiple of 32 up to 128, rows of a 16-byte aligned): every
+    chunk count, output widths below, at and past one 128-column tile (odd
+    widths store element by element), groups that are empty, shorter than a
+    256-row tile or span many tiles; segment_mm (consecutive groups) and
+    gather_mm (rows through the bucketing permutation) against the oracle,
+    and gather_mm against segment_mm on the stably sorted rows bit for bit
+    (same kernel, same per-row arithmetic)."""
     rng = np.random.default_rng(d1 * 1000 + d2)
-    r = 9
-    seglen = np.array([0, 1, 127, 128, 129, 700, 0, 3, 2000])
+    r = 11
+    seglen = np.array([0, 1, 127, 255, 256, 257, 700, 0, 3, 2000, 129])
     n = int(seglen.sum())
     a = rng.normal(size=(n, d1)).astype(np.float32)
     b = (rng.normal(size=(r, d1, d2)) / np.sqrt(d1)).astype(np.float32)
@@ -1075,3 +1075,74 @@ def test_grouped_mm_block_resident_shapes(d1, d2):
     want = np.empty_like(gm)
     want[perm] = ops.segment_mm(a[perm], b, np.bincount(idx, minlength=r))
     np.testing.assert_array_equal(gm, want)
+
+
+def _grouped_both(a, b, seglen, idx):
+    """segment_mm and gather_mm of the same rows on the GPU (numpy out)."""
+    at, bt = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    seg = ops.segment_mm(at, bt, seglen).cpu().numpy()
+    gat = ops.gather_mm(at, bt, idx_b=torch.from_numpy(idx).cuda()).cpu().numpy()
+    return seg, gat
+
+
+def test_grouped_mm_non_finite_and_out_of_range_values():
+    """Values the bf16 split does not take (inf, NaN, magnitudes from 2^60
+    up and below 2^-50 but non-zero) send their chunk of a, or every chunk of
+    a group whose b holds one, to float32 MFMAs: inf and NaN land where IEEE
+    arithmetic puts them (the oracle in float64 on the same float32 values),
+    every finite result stays within the tolerance rule, and rows that share
+    a chunk with such a value are unaffected."""
+    rng = np.random.default_rng(71)
+    k, r = 128, 6
+    seglen = np.array([300, 40, 500, 256, 7, 400])
+    n = int(seglen.sum())
+    a = rng.normal(size=(n, k)).astype(np.float32)
+    b = (rng.normal(size=(r, k, k)) / np.sqrt(k)).astype(np.float32)
+    a[3, 5] = np.inf           # group 0
+    a[10, 0] = -np.inf
+    a[20, 77] = np.nan
+    a[350, :16] = 1e30         # group 2: huge, finite products
+    a[351, 3] = 1e-30          # tiny next to normal values in its chunk
+    a[360] *= 1e-30            # a whole row of tiny values
+    a[1100:1110] = 0.0         # exact zeros take the bf16 path
+    b[1, 9, 1] = np.inf        # group 1: every chunk on float32 MFMAs
+    b[3, 0, :] = 1e-30         # group 3: tiny b values
+    b[5, 4, 4] = 3e20          # group 5: a huge b value
+    idx = np.repeat(np.arange(r), seglen)
+    seg, gat = _grouped_both(a, b, seglen, idx)
+    with np.errstate(all="ignore"):
+        ref = oracle.segment_mm(a, b, seglen, np.float64)
+        bound = oracle.segment_mm(np.abs(a), np.abs(b), seglen, np.float64)
+    for got, what in ((seg, "segment_mm"), (gat, "gather_mm")):
+        fin = np.isfinite(ref)
+        assert np.array_equal(np.isnan(got), np.isnan(ref)), what
+        assert np.array_equal(got[np.isinf(ref)], ref[np.isinf(ref)].astype(np.float32)), what
+        assert int((~fin).sum()) > 0
+        close(got[fin], ref[fin], bound[fin], np.float32, what)
+    np.testing.assert_array_equal(seg, gat)
+
+
+def test_grouped_mm_float32_accuracy():
+    """The bf16-split products keep float32 accuracy: against float64, the
+    error relative to sum |a b| over 20,000 rows (K = 128) is no larger than
+    that of the vendor float32 GEMM (torch.mm, used here only as the
+    yardstick) on the same rows, and within float32's unit roundoff
+    (2^-24 = 6e-8) on average."""
+    rng = np.random.default_rng(72)
+    k, r, n = 128, 4, 20000
+    seglen = np.full(r, n // r)
+    a = rng.normal(size=(n, k)).astype(np.float32)
+    b = (rng.normal(size=(r, k, k)) / np.sqrt(k)).astype(np.float32)
+    idx = np.repeat(np.arange(r), seglen)
+    seg, gat = _grouped_both(a, b, seglen, idx)
+    ref = oracle.segment_mm(a, b, seglen, np.float64)
+    scale = oracle.segment_mm(np.abs(a), np.abs(b), seglen, np.float64)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    at = torch.from_numpy(a).cuda()
+    vendor = torch.cat([at[i * (n // r):(i + 1) * (n // r)] @ torch.from_numpy(b[i]).cuda()
+                        for i in range(r)]).cpu().numpy()
+    e_v = np.abs(vendor - ref) / scale
+    for got in (seg, gat):
+        e = np.abs(got - ref) / scale
+        assert e.mean() <= 1.1 * e_v.mean() and e.mean() < 2 ** -24, (e.mean(), e_v.mean())
+        assert e.max() <= 1.5 * e_v.max(), (e.max(), e_v.max())
