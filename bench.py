@@ -208,6 +208,8 @@ def mfma_entry(times, flops, nbytes, peak_tflops):
     tf = flops / med / 1e9
     out["TFLOPs"] = round(tf, 1)
     out["frac"] = round(tf / peak_tflops, 4)
+    out["GBps"] = round(nbytes / med / 1e6, 1)
+    out["hbm_frac"] = round(nbytes / med / 1e6 / HBM_PEAK_GBS, 4)
     return out
 
 
@@ -914,6 +916,10 @@ def section_c5(args):
     del gg
     out = {"workload": "RGCN relation transform: gather_mm + segment_mm, float32",
            "rows": n, "d1": K, "d2": K, "relations": R, "ops": ops_out,
+           "arithmetic": "float32 in and out; each product formed from exact three-way bf16 "
+                         "splits of both operands (six part products on "
+                         "v_mfma_f32_32x32x16_bf16, float32 accumulation); frac is against "
+                         "the 157.3 TFLOP/s float32 MFMA peak, hbm_frac against 8 TB/s",
            "vendor_blas_one_block": blas}
     if not args.no_cpu_baseline:
         oracle, L, cores = oracle_setup()
