@@ -443,7 +443,7 @@ def test_grouped_mm_backward_misaligned_operands(route):
     """a and the output gradient one element off a 16-byte boundary (the
     element loads of both gradient kernels) give the gradients of aligned
     copies: db bit for bit (the same kernel), da to rounding (the aligned
-    case may take the resident forward kernel, which orders k differently)."""
+    case may take the bf16-split forward kernel, which orders k differently)."""
     n, d1, d2, r = 2000, 16, 8, 3
     rng = np.random.default_rng(90)
     base = leaf((n * d1 + 1,), 91, dtype=torch.float32)
@@ -464,6 +464,33 @@ def test_grouped_mm_backward_misaligned_operands(route):
     run(a2, b2).backward(G.clone())
     torch.testing.assert_close(got[0], a2.grad.reshape(-1), rtol=1e-5, atol=1e-5)
     assert torch.equal(got[1], b2.grad)
+
+
+def test_grouped_mm_backward_values_off_the_fast_path():
+    """Gradients through segment_mm when a and the output gradient hold inf,
+    NaN, tiny and huge values: the chunks (da) and row stages (db) holding
+    them run on float32 MFMAs, inf and NaN land where float64 IEEE arithmetic
+    puts them, and every finite entry stays within the tolerance."""
+    n, d1, d2, r = 3000, 128, 128, 4
+    seglen = np.array([1000, 700, 800, 500])
+    a = leaf((n, d1), 96, dtype=torch.float32)
+    b = leaf((r, d1, d2), 97, dtype=torch.float32)
+    G = torch.randn((n, d2), generator=torch.Generator(device=DEV).manual_seed(98), device=DEV)
+    with torch.no_grad():
+        a[5, 3] = float("inf")
+        a[1200, 7] = float("nan")
+        a[1800] *= 1e-30
+        a[2600, :4] = 1e30
+    G[10, 9] = float("-inf")
+    G[2000, 0] = 3e20
+    ops.segment_mm(a, b, seglen).backward(G)
+    da, db, da_b, db_b = ref_grouped_grads(a, b, np.repeat(np.arange(r), seglen), G)
+    for got, want, bound in ((a.grad, da, da_b), (b.grad, db, db_b)):
+        assert torch.equal(torch.isnan(got), torch.isnan(want))
+        inf = torch.isinf(want)
+        assert bool(inf.any()) and torch.equal(got[inf], want[inf].float())
+        fin = torch.isfinite(want)
+        check_by_terms(got[fin], want[fin], bound[fin], torch.float32)
 
 
 def test_segment_mm_and_gather_mm_gradcheck():
