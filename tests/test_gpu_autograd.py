@@ -467,10 +467,11 @@ def test_grouped_mm_backward_misaligned_operands(route):
 
 
 def test_grouped_mm_backward_values_off_the_fast_path():
-    """Gradients through segment_mm when a and the output gradient hold inf,
-    NaN, tiny and huge values: the chunks (da) and row stages (db) holding
-    them run on float32 MFMAs, inf and NaN land where float64 IEEE arithmetic
-    puts them, and every finite entry stays within the tolerance."""
+    """Gradients through segment_mm when a, b and the output gradient hold
+    inf, NaN, tiny and huge values: da's chunks holding them (and every chunk
+    of the group whose block of b holds one, read transposed) run on float32
+    MFMAs, inf and NaN land where float64 IEEE arithmetic puts them, and every
+    finite entry stays within the tolerance."""
     n, d1, d2, r = 3000, 128, 128, 4
     seglen = np.array([1000, 700, 800, 500])
     a = leaf((n, d1), 96, dtype=torch.float32)
@@ -481,6 +482,7 @@ def test_grouped_mm_backward_values_off_the_fast_path():
         a[1200, 7] = float("nan")
         a[1800] *= 1e-30
         a[2600, :4] = 1e30
+        b[2, 5, 7] = float("inf")
     G[10, 9] = float("-inf")
     G[2000, 0] = 3e20
     ops.segment_mm(a, b, seglen).backward(G)
