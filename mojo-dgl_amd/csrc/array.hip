@@ -179,25 +179,60 @@ __global__ __launch_bounds__(BLOCK) void segment_ids_kernel(const int32_t* __res
   }
 }
 
-// Segment offsets from lengths (three launches: tile partials, a scan of
-// the tile totals, the tile rewrite). A tile is SEG_TILE lengths, 4
-// consecutive ones per thread (1M lengths: 977 tiles). Integer sums are
-// exact, so the offsets equal the sequential [0] + cumsum.
+// Segment offsets from lengths in two launches: per-tile figures (sum,
+// min, max, chunks of the long segments), then every tile writes its
+// offsets after summing the earlier tiles' totals itself (at most a few
+// thousand values, read from L2), and tile 0 also writes the figures over
+// all tiles. A tile is SEG_TILE lengths, 4 consecutive ones per thread (1M
+// lengths: 977 tiles); reductions and the scan run in wavefront shuffles
+// with one barrier per workgroup. Integer sums are exact, so the offsets
+// equal the sequential [0] + cumsum.
 constexpr int SEG_THREADS = 256;
 constexpr int SEG_PER = 4;
 constexpr int SEG_TILE = SEG_THREADS * SEG_PER;
+constexpr int SEG_WAVES = SEG_THREADS / WAVE;
 
 __device__ __forceinline__ int64_t seg_chunks(int64_t len, int64_t chunk_len) {
   return (chunk_len > 0 && len > chunk_len) ? (len + chunk_len - 1) / chunk_len : 0;
 }
 
+// Sum, min, max over the wavefront (every lane gets the result).
+__device__ __forceinline__ void wave_figures(int64_t& s, int64_t& m, int64_t& h, int64_t& x) {
+  for (int off = 32; off >= 1; off >>= 1) {
+    s += __shfl_xor(s, off);
+    h += __shfl_xor(h, off);
+    const int64_t om = __shfl_xor(m, off), ox = __shfl_xor(x, off);
+    m = om < m ? om : m;
+    x = ox > x ? ox : x;
+  }
+}
+
+// The four figures of a workgroup, combined through LDS (valid in thread 0).
+__device__ __forceinline__ void block_figures(int64_t& s, int64_t& m, int64_t& h, int64_t& x) {
+  __shared__ int64_t f[4][SEG_WAVES];
+  const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+  wave_figures(s, m, h, x);
+  if (lane == 0) {
+    f[0][w] = s;
+    f[1][w] = m;
+    f[2][w] = h;
+    f[3][w] = x;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int q = 1; q < SEG_WAVES; ++q) {
+      s += f[0][q];
+      m = f[1][q] < m ? f[1][q] : m;
+      h += f[2][q];
+      x = f[3][q] > x ? f[3][q] : x;
+    }
+  }
+}
+
 __global__ __launch_bounds__(SEG_THREADS) void seg_partials_kernel(
     const int64_t* __restrict__ len, int64_t num, int64_t chunk_len, int64_t* __restrict__ tsum,
     int64_t* __restrict__ tmin, int64_t* __restrict__ theavy, int64_t* __restrict__ tmax) {
-  __shared__ int64_t ssum[SEG_THREADS], smin[SEG_THREADS], sheavy[SEG_THREADS],
-      smax[SEG_THREADS];
-  const int t = threadIdx.x;
-  const int64_t lo = (int64_t)blockIdx.x * SEG_TILE + (int64_t)t * SEG_PER;
+  const int64_t lo = (int64_t)blockIdx.x * SEG_TILE + (int64_t)threadIdx.x * SEG_PER;
   int64_t s = 0, m = INT64_MAX, h = 0, x = INT64_MIN;
   for (int k = 0; k < SEG_PER; ++k) {
     const int64_t i = lo + k;
@@ -209,89 +244,28 @@ __global__ __launch_bounds__(SEG_THREADS) void seg_partials_kernel(
       h += seg_chunks(v, chunk_len);
     }
   }
-  ssum[t] = s;
-  smin[t] = m;
-  sheavy[t] = h;
-  smax[t] = x;
-  __syncthreads();
-  for (int off = SEG_THREADS / 2; off > 0; off >>= 1) {
-    if (t < off) {
-      ssum[t] += ssum[t + off];
-      smin[t] = smin[t + off] < smin[t] ? smin[t + off] : smin[t];
-      sheavy[t] += sheavy[t + off];
-      smax[t] = smax[t + off] > smax[t] ? smax[t + off] : smax[t];
-    }
-    __syncthreads();
-  }
-  if (t == 0) {
-    tsum[blockIdx.x] = ssum[0];
-    tmin[blockIdx.x] = smin[0];
-    theavy[blockIdx.x] = sheavy[0];
-    tmax[blockIdx.x] = smax[0];
+  block_figures(s, m, h, x);
+  if (threadIdx.x == 0) {
+    tsum[blockIdx.x] = s;
+    tmin[blockIdx.x] = m;
+    theavy[blockIdx.x] = h;
+    tmax[blockIdx.x] = x;
   }
 }
 
-// One workgroup: tsum becomes the exclusive scan of the tile totals;
-// stats = (min length, total, chunks of the long segments, max length);
-// offsets[0] = 0. With no tiles (no segments) the pointers to the tile
-// arrays are unused.
-__global__ __launch_bounds__(1024) void seg_tiles_kernel(int64_t* __restrict__ tsum,
-                                                         const int64_t* __restrict__ tmin,
-                                                         const int64_t* __restrict__ theavy,
-                                                         const int64_t* __restrict__ tmax,
-                                                         int64_t tiles, int64_t* __restrict__ stats,
-                                                         int32_t* __restrict__ offsets) {
-  __shared__ int64_t ssum[1024], smin[1024], sheavy[1024], smax[1024];
-  const int t = threadIdx.x;
-  const int64_t span = (tiles + 1023) / 1024;
-  const int64_t lo = t * span < tiles ? t * span : tiles;
-  const int64_t hi = lo + span < tiles ? lo + span : tiles;
-  int64_t s = 0, m = INT64_MAX, h = 0, x = INT64_MIN;
-  for (int64_t i = lo; i < hi; ++i) {
-    s += tsum[i];
-    m = tmin[i] < m ? tmin[i] : m;
-    h += theavy[i];
-    x = tmax[i] > x ? tmax[i] : x;
-  }
-  ssum[t] = s;
-  smin[t] = m;
-  sheavy[t] = h;
-  smax[t] = x;
-  __syncthreads();
-  // inclusive scan of the span sums; min, max and heavy reduced alongside
-  for (int off = 1; off < 1024; off <<= 1) {
-    const int64_t add = t >= off ? ssum[t - off] : 0;
-    const int64_t om = t >= off ? smin[t - off] : INT64_MAX;
-    const int64_t oh = t >= off ? sheavy[t - off] : 0;
-    const int64_t ox = t >= off ? smax[t - off] : INT64_MIN;
-    __syncthreads();
-    ssum[t] += add;
-    smin[t] = om < smin[t] ? om : smin[t];
-    sheavy[t] += oh;
-    smax[t] = ox > smax[t] ? ox : smax[t];
-    __syncthreads();
-  }
-  int64_t acc = t > 0 ? ssum[t - 1] : 0;
-  for (int64_t i = lo; i < hi; ++i) {
-    const int64_t v = tsum[i];
-    tsum[i] = acc;
-    acc += v;
-  }
-  if (t == 0) offsets[0] = 0;
-  if (t == 1023) {
-    stats[0] = tiles > 0 ? smin[1023] : 0;
-    stats[1] = ssum[1023];
-    stats[2] = sheavy[1023];
-    stats[3] = tiles > 0 ? smax[1023] : 0;
-  }
-}
-
-__global__ __launch_bounds__(SEG_THREADS) void seg_write_kernel(const int64_t* __restrict__ len,
-                                                                int64_t num,
-                                                                const int64_t* __restrict__ tsum,
-                                                                int32_t* __restrict__ offsets) {
-  __shared__ int64_t scan[SEG_THREADS];
-  const int t = threadIdx.x;
+// offsets[i + 1] for the lengths of tile blockIdx.x; tile 0 also writes
+// offsets[0] = 0 and stats = (min length, total, chunks of the long
+// segments, max length), zeros without tiles (launched with one workgroup).
+__global__ __launch_bounds__(SEG_THREADS) void seg_write_kernel(
+    const int64_t* __restrict__ len, int64_t num, int64_t tiles, const int64_t* __restrict__ tsum,
+    const int64_t* __restrict__ tmin, const int64_t* __restrict__ theavy,
+    const int64_t* __restrict__ tmax, int64_t* __restrict__ stats, int32_t* __restrict__ offsets) {
+  __shared__ int64_t wpre[SEG_WAVES], wtot[SEG_WAVES];
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  // the earlier tiles' total, and this thread's lengths
+  int64_t pre = 0;
+  for (int64_t i = t; i < (int64_t)blockIdx.x; i += SEG_THREADS) pre += tsum[i];
+  for (int off = 32; off >= 1; off >>= 1) pre += __shfl_xor(pre, off);
   const int64_t lo = (int64_t)blockIdx.x * SEG_TILE + (int64_t)t * SEG_PER;
   int64_t v[SEG_PER];
   int64_t s = 0;
@@ -300,20 +274,40 @@ __global__ __launch_bounds__(SEG_THREADS) void seg_write_kernel(const int64_t* _
     v[k] = i < num ? len[i] : 0;
     s += v[k];
   }
-  scan[t] = s;
-  __syncthreads();
-  for (int off = 1; off < SEG_THREADS; off <<= 1) {
-    const int64_t add = t >= off ? scan[t - off] : 0;
-    __syncthreads();
-    scan[t] += add;
-    __syncthreads();
+  // inclusive scan of the threads' sums within the wavefront
+  int64_t incl = s;
+  for (int off = 1; off < WAVE; off <<= 1) {
+    const int64_t o = __shfl_up(incl, off);
+    if (lane >= off) incl += o;
   }
-  int64_t acc = tsum[blockIdx.x] + (t > 0 ? scan[t - 1] : 0);
+  if (lane == 0) wpre[w] = pre;
+  if (lane == WAVE - 1) wtot[w] = incl;
+  __syncthreads();
+  int64_t acc = incl - s;
+  for (int q = 0; q < SEG_WAVES; ++q) acc += wpre[q];
+  for (int q = 0; q < w; ++q) acc += wtot[q];
   for (int k = 0; k < SEG_PER; ++k) {
     const int64_t i = lo + k;
     if (i < num) {
       acc += v[k];
       offsets[i + 1] = (int32_t)acc;
+    }
+  }
+  if (blockIdx.x == 0) {
+    int64_t su = 0, m = INT64_MAX, h = 0, x = INT64_MIN;
+    for (int64_t i = t; i < tiles; i += SEG_THREADS) {
+      su += tsum[i];
+      m = tmin[i] < m ? tmin[i] : m;
+      h += theavy[i];
+      x = tmax[i] > x ? tmax[i] : x;
+    }
+    block_figures(su, m, h, x);
+    if (t == 0) {
+      offsets[0] = 0;
+      stats[0] = tiles > 0 ? m : 0;
+      stats[1] = su;
+      stats[2] = h;
+      stats[3] = tiles > 0 ? x : 0;
     }
   }
 }
@@ -335,13 +329,8 @@ hipError_t launch_segment_offsets(const int64_t* len, int64_t num, int64_t chunk
                        num, chunk_len, tsum, tmin, theavy, tmax);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(seg_tiles_kernel, dim3(1), dim3(1024), 0, s, tsum, tmin, theavy, tmax,
-                     tiles, stats, offsets);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  if (tiles > 0)
-    hipLaunchKernelGGL(seg_write_kernel, dim3((unsigned)tiles), dim3(SEG_THREADS), 0, s, len, num,
-                       tsum, offsets);
+  hipLaunchKernelGGL(seg_write_kernel, dim3((unsigned)(tiles > 0 ? tiles : 1)), dim3(SEG_THREADS),
+                     0, s, len, num, tiles, tsum, tmin, theavy, tmax, stats, offsets);
   return hipGetLastError();
 }
 
