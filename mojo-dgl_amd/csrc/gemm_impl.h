@@ -7,6 +7,11 @@
 // gather_mm's are the rows with idx_b == g, found by a stable counting sort
 // on the GPU (count per block, scan, ballot-ranked scatter) into `perm`.
 //
+// Two forward kernels: float32 with K a multiple of 32 up to 128 and rows of
+// a on a 16-byte boundary runs on the bf16 matrix cores through exact
+// three-way splits (grouped_gemm_split_kernel, described where it is
+// defined); every other shape, and float64, takes grouped_gemm_kernel:
+//
 // Tiles. A workgroup (4 wavefronts, 2 x 2) computes a 128 x 128 output tile
 // of one group: 128 rows of the group x 128 columns. Wavefront (wm, wn) owns
 // 64 x 64 of it as 4 x 4 blocks of v_mfma_{f32,f64}_16x16x4. The K axis is
