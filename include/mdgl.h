@@ -52,6 +52,14 @@ extern "C" {
  * not launched (a longer segment is then still reduced whole, in row order) */
 #define MDGL_SEGMENTS_SHORT 4
 #define MDGL_SEGMENT_SPLIT_ROWS 4096
+/* mdgl_segment_reduce(_arg), for callers that learn the longest segment
+ * only after the call (lengths on the GPU): SKIP_LONG reduces every segment
+ * of at most MDGL_SEGMENT_SPLIT_ROWS rows and leaves the longer ones
+ * unwritten; a second call with LONG_ONLY then reduces just those. The two
+ * calls write what one call without either flag writes. At most one of
+ * SHORT, SKIP_LONG and LONG_ONLY. */
+#define MDGL_SEGMENTS_SKIP_LONG 8
+#define MDGL_SEGMENTS_LONG_ONLY 16
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* mdgl_last_error(void);
@@ -215,6 +223,17 @@ int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, v
                          const int32_t* chunk_row, const int32_t* chunk_start,
                          const int32_t* chunk_first, int64_t num_chunks, int64_t slots,
                          void* workspace, int64_t workspace_bytes, int dtype, void* stream);
+
+/* mdgl_segment_softmax without a plan for the segments of at most
+ * `chunk_len` rows (mdgl_softmax_geometry's, for these buffers): the
+ * LDS-staged kernel writes their rows; the rows of longer segments are left
+ * unwritten. Returns MDGL_ENOTSUP when the rows are too wide for that kernel
+ * (more than 32 16-byte vectors). No counterpart in the reference: for
+ * callers whose lengths are on the GPU, so the softmax can start before the
+ * longest length is known on the host (a longer segment then needs the full
+ * call with its chunk plan, which rewrites every row). */
+int mdgl_segment_softmax_short(const int32_t* offsets, const void* value, void* dst,
+                               int64_t num_seg, int64_t d, int64_t n, int dtype, void* stream);
 
 /* Replaces capi.mojo:149-165 (`mdgl_edge_softmax_`): per CSR row, per
  * column, softmax of logits[eid[i]] over the row's slots whose edge is

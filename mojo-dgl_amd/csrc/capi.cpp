@@ -584,6 +584,11 @@ int segment_common(const char* what, const int32_t* offsets, const void* value, 
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "%s: bad dtype %d", what, dtype);
   if (reduce_op < RED_SUM || reduce_op > RED_MEAN)
     return fail(MDGL_EINVAL, "%s: bad reduce_op %d", what, reduce_op);
+  const int pass_flags = flags & (MDGL_SEGMENTS_SHORT | MDGL_SEGMENTS_SKIP_LONG |
+                                  MDGL_SEGMENTS_LONG_ONLY);
+  if (pass_flags & (pass_flags - 1))
+    return fail(MDGL_EINVAL, "%s: at most one of MDGL_SEGMENTS_SHORT, MDGL_SEGMENTS_SKIP_LONG "
+                "and MDGL_SEGMENTS_LONG_ONLY", what);
   if (num_seg < 0 || d < 0 || n < 0) return fail(MDGL_EINVAL, "%s: negative size", what);
   if (num_seg >= (int64_t(1) << 31) || n >= (int64_t(1) << 31))
     return fail(MDGL_EINVAL, "%s: 2**31 or more segments or rows", what);
@@ -601,6 +606,9 @@ int segment_common(const char* what, const int32_t* offsets, const void* value, 
   p.red = reduce_op == RED_MEAN ? RED_SUM : reduce_op;
   p.flags = (reduce_op == RED_MEAN ? F_MEAN : 0) | ((flags & MDGL_REPLACE_INF) ? F_REPLACE_INF : 0);
   p.skip_long = (flags & MDGL_SEGMENTS_SHORT) ? 0 : 1;
+  p.passes = (flags & MDGL_SEGMENTS_SKIP_LONG)   ? SEG_PASS_ROWS
+             : (flags & MDGL_SEGMENTS_LONG_ONLY) ? SEG_PASS_SPLIT
+                                                 : SEG_PASS_ROWS | SEG_PASS_SPLIT;
   p.stream = (hipStream_t)stream;
   hipError_t e = dtype == MDGL_FLOAT32 ? launch_segment_reduce<float>(p)
                                        : launch_segment_reduce<double>(p);
@@ -757,9 +765,9 @@ int softmax_common(const char* what, const int32_t* indptr, const int32_t* eid,
     // them when the rows are narrow enough
     hipError_t se = dtype == MDGL_FLOAT32
                         ? launch_segment_softmax_stage<float>(indptr, logits, dst, num_rows,
-                                                              num_slots, d, p.stream)
+                                                              num_slots, d, 0, p.stream)
                         : launch_segment_softmax_stage<double>(indptr, logits, dst, num_rows,
-                                                               num_slots, d, p.stream);
+                                                               num_slots, d, 0, p.stream);
     if (se != hipErrorNotSupported) return hip_status(se, what);
   }
   hipError_t e = dtype == MDGL_FLOAT32 ? launch_softmax<float>(p) : launch_softmax<double>(p);
@@ -784,6 +792,31 @@ int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, v
                         order, bounds, nbins, packed_eid, chunk_row, chunk_start, chunk_first,
                         num_chunks, slots, nullptr, 0, n, workspace, workspace_bytes, dtype,
                         stream, true);
+}
+
+int mdgl_segment_softmax_short(const int32_t* offsets, const void* value, void* dst,
+                               int64_t num_seg, int64_t d, int64_t n, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "segment_softmax_short: bad dtype %d", dtype);
+  if (num_seg < 0 || d < 0 || n < 0) return fail(MDGL_EINVAL, "segment_softmax_short: negative size");
+  if (num_seg >= (int64_t(1) << 31) || n >= (int64_t(1) << 31))
+    return fail(MDGL_EINVAL, "segment_softmax_short: 2**31 or more segments or rows");
+  if (!row_widths_fit(d, dsize(dtype)))
+    return fail(MDGL_EINVAL, "segment_softmax_short: rows too wide");
+  if (num_seg == 0 || d == 0 || n == 0) return MDGL_OK;
+  if (!offsets || !value || !dst) return fail(MDGL_EINVAL, "segment_softmax_short: null buffer");
+  int vec;
+  int64_t slots, chunk_len;
+  softmax_geom(d, dtype, value, dst, &vec, &slots, &chunk_len);
+  const hipStream_t st = (hipStream_t)stream;
+  hipError_t e = dtype == MDGL_FLOAT32
+                     ? launch_segment_softmax_stage<float>(offsets, value, dst, num_seg, n, d,
+                                                           chunk_len, st)
+                     : launch_segment_softmax_stage<double>(offsets, value, dst, num_seg, n, d,
+                                                            chunk_len, st);
+  if (e == hipErrorNotSupported)
+    return fail(MDGL_ENOTSUP, "segment_softmax_short: rows of %lld values are too wide for the "
+                "staged kernel", (long long)d);
+  return hip_status(e, "segment_softmax_short");
 }
 
 int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int32_t* eid,

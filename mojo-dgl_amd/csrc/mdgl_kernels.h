@@ -62,8 +62,11 @@ hipError_t launch_gspmm_red(const GspmmParams& p);
 // segment_reduce: out[s, k] = red over value rows offsets[s] .. offsets[s+1]
 // (segment_impl.h). red in {SUM, MAX, MIN}, mean is F_MEAN; arg (max / min,
 // optional) receives the selected row. Unless skip_long is 0, segments
-// longer than SEG_SPLIT_ROWS are reduced by a separate split pass.
+// longer than SEG_SPLIT_ROWS are left to a separate split pass. `passes`
+// picks the launches: SEG_PASS_ROWS the row-order kernels, SEG_PASS_SPLIT
+// the split pass (which only runs with skip_long).
 constexpr int SEG_SPLIT_ROWS = 4096;
+enum { SEG_PASS_ROWS = 1, SEG_PASS_SPLIT = 2 };
 struct SegmentParams {
   const int32_t* offsets;
   const void* value;
@@ -72,6 +75,7 @@ struct SegmentParams {
   int64_t num_seg, n, d;
   int red, flags;
   int skip_long;
+  int passes;
   hipStream_t stream;
 };
 
@@ -80,9 +84,12 @@ hipError_t launch_segment_reduce(const SegmentParams& p);
 
 // segment_softmax of segments that fit an 8 KB window each, rows of at most
 // 32 lane vectors (segment_impl.h); hipErrorNotSupported for wider rows.
+// Segments of more than max_rows rows are not written (max_rows <= 0: no
+// limit).
 template <class T>
 hipError_t launch_segment_softmax_stage(const int32_t* offsets, const void* value, void* out,
-                                        int64_t num_seg, int64_t n, int64_t d, hipStream_t st);
+                                        int64_t num_seg, int64_t n, int64_t d, int64_t max_rows,
+                                        hipStream_t st);
 
 // gsddmm: out[e, o] = op(lhs[t_l(e)], rhs[t_r(e)]) (or the dot over `red`).
 struct GsddmmParams {

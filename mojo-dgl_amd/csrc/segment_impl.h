@@ -56,6 +56,7 @@ struct SegArgs {
   int out_vec;    // 16-byte output stores
   int64_t slabs;  // wide kernel: 64-vector slabs per row
   int64_t spb;    // split kernel: segments scanned per workgroup
+  int max_rows;   // softmax: segments of more rows are not written (0: none skipped)
 };
 
 __device__ __forceinline__ int wave_min_int(int v) {
@@ -386,18 +387,27 @@ __global__ __launch_bounds__(BLOCK) void seg_softmax_stage_kernel(SegArgs<T> a) 
   const int nv = a.nvec;
   const int WR = CH / nv;
   const int mslot = (grp * nv + gl) * VEC;  // this lane's m / s entries
-  bool done = hi <= lo;  // empty segments (and lanes past the last segment) write nothing
+  // empty segments (and lanes past the last segment) write nothing, nor do
+  // segments over the row limit (the caller serves them another way)
+  const bool skipped = a.max_rows > 0 && hi - lo > a.max_rows;
+  bool done = hi <= lo || skipped;
 
   // window [w0, e0): w0 the first row of the first unfinished segment, e0
   // the end of the last unfinished segment that ends within w0 + WR (w0
-  // when even the first does not fit)
+  // when even the first does not fit); with a row limit it also stops at
+  // the first skipped segment, whose rows it must not write
   auto window = [&](bool dn, int& w0, int& e0) {
     w0 = wave_min_int(dn ? 0x7fffffff : lo);
     if (w0 == 0x7fffffff) {
       e0 = w0;
       return;
     }
-    e0 = wave_max_int(!dn && hi <= w0 + WR ? hi : w0);
+    int lim = w0 + WR;
+    if (a.max_rows > 0) {
+      const int sk = wave_min_int(skipped && lo >= w0 ? lo : 0x7fffffff);
+      lim = sk < lim ? sk : lim;
+    }
+    e0 = wave_max_int(!dn && hi <= lim ? hi : w0);
   };
   T st[PER][VEC];
   auto fetch = [&](int w0, int e0) {
@@ -540,9 +550,11 @@ __global__ __launch_bounds__(BLOCK) void seg_softmax_stage_kernel(SegArgs<T> a) 
 }
 
 template <class T, int RED, int VEC, bool ARG>
-hipError_t launch_seg(SegArgs<T> a, hipStream_t st) {
+hipError_t launch_seg(SegArgs<T> a, int passes, hipStream_t st) {
   const bool stage = a.nvec <= 32;
-  if (stage) {
+  if (!(passes & SEG_PASS_ROWS)) {
+    // the split pass alone
+  } else if (stage) {
     int G = 1;
     while (G < a.nvec) G <<= 1;
     a.G = G;
@@ -559,7 +571,7 @@ hipError_t launch_seg(SegArgs<T> a, hipStream_t st) {
                        st, a);
   }
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || !a.skip_long) return e;
+  if (e != hipSuccess || !a.skip_long || !(passes & SEG_PASS_SPLIT)) return e;
   int64_t blocks = 2048;
   if (blocks > a.S) blocks = a.S;
   a.spb = (a.S + blocks - 1) / blocks;
@@ -586,10 +598,10 @@ hipError_t launch_seg_vec(const SegmentParams& p) {
   a.out_vec = vec && aligned16(p.out);
   if (vec) {
     a.nvec = (int)((p.d / V) < 0x7fffffff ? p.d / V : 0x7fffffff);
-    return launch_seg<T, RED, V, ARG>(a, p.stream);
+    return launch_seg<T, RED, V, ARG>(a, p.passes, p.stream);
   }
   a.nvec = (int)(p.d < 0x7fffffff ? p.d : 0x7fffffff);
-  return launch_seg<T, RED, 1, ARG>(a, p.stream);
+  return launch_seg<T, RED, 1, ARG>(a, p.passes, p.stream);
 }
 
 template <class T>
@@ -608,7 +620,8 @@ hipError_t launch_segment_reduce(const SegmentParams& p) {
 // CSR softmax kernel).
 template <class T>
 hipError_t launch_segment_softmax_stage(const int32_t* offsets, const void* value, void* out,
-                                        int64_t num_seg, int64_t n, int64_t d, hipStream_t st) {
+                                        int64_t num_seg, int64_t n, int64_t d, int64_t max_rows,
+                                        hipStream_t st) {
   if (num_seg <= 0 || d <= 0 || n <= 0) return hipSuccess;
   constexpr int V = 16 / sizeof(T);
   const bool vec = d % V == 0 && aligned16(value) && aligned16(out);
@@ -622,6 +635,7 @@ hipError_t launch_segment_softmax_stage(const int32_t* offsets, const void* valu
   a.n = n;
   a.d = d;
   a.nvec = (int)nvec;
+  a.max_rows = max_rows > 0 && max_rows < n ? (int)max_rows : 0;
   int G = 1;
   while (G < a.nvec) G <<= 1;
   a.G = G;
@@ -641,4 +655,4 @@ hipError_t launch_segment_softmax_stage(const int32_t* offsets, const void* valu
   template hipError_t mdgl::launch_segment_reduce<T>(const mdgl::SegmentParams&);          \
   template hipError_t mdgl::launch_segment_softmax_stage<T>(const int32_t*, const void*, void*, \
                                                             int64_t, int64_t, int64_t,      \
-                                                            hipStream_t);
+                                                            int64_t, hipStream_t);

@@ -53,6 +53,8 @@ FLOAT32, FLOAT64 = 0, 1
 REPLACE_INF = 1
 RHS_CSR_ORDER = 2
 SEGMENTS_SHORT = 4  # mdgl_segment_reduce: no segment longer than SEGMENT_SPLIT_ROWS
+SEGMENTS_SKIP_LONG = 8  # mdgl_segment_reduce: longer segments left for a LONG_ONLY call
+SEGMENTS_LONG_ONLY = 16  # mdgl_segment_reduce: only the segments longer than SEGMENT_SPLIT_ROWS
 SEGMENT_SPLIT_ROWS = 4096
 EINVAL, EWORKSPACE, ENOTSUP = -1, -2, -3  # negative statuses of include/mdgl.h
 
@@ -86,6 +88,7 @@ _SIGNATURES = {
     "mdgl_softmax_workspace_bytes": ([_I64, _I64, _I64, _C], _I64),
     "mdgl_segment_softmax": ([_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _C, _P, _P, _P, _P,
                               _I64, _I64, _P, _I64, _C, _P], _C),
+    "mdgl_segment_softmax_short": ([_P, _P, _P, _I64, _I64, _I64, _C, _P], _C),
     "mdgl_edge_softmax_": ([_P, _P, _P, _P, _P, _P, _P, _I64, _C, _I64, _P, _P, _C, _P, _P, _P,
                             _P, _I64, _I64, _P, _I64, _P, _I64, _C, _P], _C),
     "mdgl_segment_mm": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _C, _P], _C),
@@ -221,13 +224,28 @@ def stream() -> int:
 _PINNED = threading.local()
 
 
-class Readback:
-    """A small GPU int64 tensor copied to pinned host memory behind the work
-    queued so far, without waiting: the GPU goes on with what the caller
-    queues next, and values() waits for the copy only. One pinned buffer per
-    thread, device and purpose, reused across calls."""
+def _side_stream(dev: int) -> torch.cuda.Stream:
+    """A second stream per thread and device (default priority) for small
+    copies that should not sit between the caller's kernels."""
+    streams = getattr(_PINNED, "side", None)
+    if streams is None:
+        streams = _PINNED.side = {}
+    st = streams.get(dev)
+    if st is None:
+        st = streams[dev] = torch.cuda.Stream(device=dev)
+    return st
 
-    def __init__(self, src: torch.Tensor, purpose: str):
+
+class Readback:
+    """A small GPU int64 tensor copied to pinned host memory without waiting:
+    the GPU goes on with what the caller queues next, and values() waits for
+    the copy only. With `after` (an event recorded on the current stream right
+    after the kernel that writes `src`), the copy runs on a side stream behind
+    that event, so kernels the caller queued since then do not wait for it;
+    otherwise it follows the work queued so far on the current stream. One
+    pinned buffer per thread, device and purpose, reused across calls."""
+
+    def __init__(self, src: torch.Tensor, purpose: str, after=None):
         bufs = getattr(_PINNED, "bufs", None)
         if bufs is None:
             bufs = _PINNED.bufs = {}
@@ -236,10 +254,18 @@ class Readback:
         buf = bufs.get(key)
         if buf is None:
             buf = bufs[key] = torch.empty(src.numel(), dtype=torch.int64, pin_memory=True)
-        buf.copy_(src.reshape(-1), non_blocking=True)
         self._buf, self._src = buf, src  # src lives until the copy is done
         self._done = torch.cuda.Event()
-        self._done.record()
+        if after is None:
+            buf.copy_(src.reshape(-1), non_blocking=True)
+            self._done.record()
+        else:
+            side = _side_stream(dev)
+            side.wait_event(after)
+            with torch.cuda.stream(side):
+                buf.copy_(src.reshape(-1), non_blocking=True)
+                self._done.record(side)
+            src.record_stream(side)  # its memory is not reused before the copy is done
 
     def values(self) -> list:
         self._done.synchronize()

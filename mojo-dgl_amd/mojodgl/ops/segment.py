@@ -51,14 +51,16 @@ class _Segments:
     the segments longer than `chunk_len` split into (GPU lengths only),
     `longest` the largest length.
 
-    With `defer` the read back of GPU lengths' checks is only started: the
-    caller may queue kernels that read the offsets (they clamp every
-    offset into the rows, so invalid lengths cannot send them out of
-    bounds) and must call verify() before it returns anything; until then
-    `longest` is None."""
+    With `defer` the checks of GPU lengths come back later: the caller may
+    queue kernels that read the offsets (they clamp every offset into the
+    rows, so invalid lengths cannot send them out of bounds) and must call
+    verify() before it returns anything; until then `longest` is None. The
+    figures are then copied on a side stream behind the offsets kernel, so
+    the caller's kernels do not queue behind the copy."""
 
     def __init__(self, seglen, n, chunk_len=None, defer=False):
         self._pending = None
+        self._stats = None
         if isinstance(seglen, torch.Tensor) and seglen.device.type == "cuda":
             sl = _lib.i64_device(seglen).reshape(-1)
             self.num = sl.numel()
@@ -82,7 +84,9 @@ class _Segments:
             self.longest = None
             self._n, self._chunked = n, chunk_len is not None
             if defer:
-                self._pending = _lib.Readback(stats, "segment_offsets")
+                self._ready = torch.cuda.Event()
+                self._ready.record()
+                self._stats = stats
             else:
                 self._check(stats.tolist())
         else:
@@ -106,8 +110,16 @@ class _Segments:
             self.heavy = heavy
         self.longest = high
 
+    def start_check(self):
+        """Start the read back of a deferred check (after the caller queued
+        its kernels; a no-op otherwise)."""
+        if self._stats is not None:
+            stats, self._stats = self._stats, None
+            self._pending = _lib.Readback(stats, "segment_offsets", after=self._ready)
+
     def verify(self):
         """Finish a deferred check (a no-op otherwise)."""
+        self.start_check()
         if self._pending is not None:
             pending, self._pending = self._pending, None
             self._check(pending.values())
@@ -165,33 +177,50 @@ def _segment_reduce(seglen, value, reducer, want_arg=False):
     (num_seg, d) int32 row of each max / min with `want_arg`, else None."""
     V = _lib.feature(value)
     n = V.shape[0] if V.ndim else 0
-    # GPU lengths: their checks come back while the reduction runs
-    seg = _Segments(seglen, n, defer=True)
     d = _flat_width(V.shape)
     fshape = tuple(V.shape[1:]) if V.ndim > 1 else (1,)
-    num_seg = seg.num
     dtype = V.dtype
+    on_gpu = isinstance(seglen, torch.Tensor) and seglen.device.type == "cuda"
+    if not on_gpu:
+        seg = _Segments(seglen, n)  # host lengths: checked before any GPU work
     gdev = _lib.device()
+    num_seg = seglen.numel() if on_gpu else seg.num
+    # the output and the value block first, so that the offsets kernels of GPU
+    # lengths and the reduction are queued back to back
     out = torch.empty((num_seg, d), dtype=_lib.torch_dtype(dtype), device=gdev)
+    val = _lib.on_device(V, dtype) if num_seg and d else None
+    if on_gpu:
+        # their checks come back while the reduction runs
+        seg = _Segments(seglen, n, defer=True)
     arg = None
     if num_seg and d:
-        val = _lib.on_device(V, dtype)
         off = seg.device()
+        L = _lib.lib()
         flags = _lib.REPLACE_INF if reducer in ("max", "min") else 0
-        if seg.longest is not None and seg.longest <= _lib.SEGMENT_SPLIT_ROWS:
+        if seg.longest is None:
+            # longest length not known yet: segments over the split length
+            # are left for a second call, made once the check is back
+            flags |= _lib.SEGMENTS_SKIP_LONG
+        elif seg.longest <= _lib.SEGMENT_SPLIT_ROWS:
             flags |= _lib.SEGMENTS_SHORT  # no split pass needed
         if want_arg and reducer in ("max", "min"):
             arg = torch.empty((num_seg, d), dtype=torch.int32, device=gdev)
-            rc = _lib.lib().mdgl_segment_reduce_arg(off.data_ptr(), val.data_ptr(),
-                                                    out.data_ptr(), arg.data_ptr(), num_seg, d,
-                                                    REDUCERS[reducer], n, flags,
-                                                    _lib.dtype_code(dtype), _lib.stream())
-        else:
-            rc = _lib.lib().mdgl_segment_reduce(off.data_ptr(), val.data_ptr(), out.data_ptr(),
-                                                num_seg, d, REDUCERS[reducer], n, flags,
-                                                _lib.dtype_code(dtype), _lib.stream())
-        _lib.check(rc, "segment_reduce")
-    seg.verify()  # raises for invalid GPU lengths before anything is returned
+
+        def run(fl):
+            if arg is not None:
+                return L.mdgl_segment_reduce_arg(off.data_ptr(), val.data_ptr(), out.data_ptr(),
+                                                 arg.data_ptr(), num_seg, d, REDUCERS[reducer], n,
+                                                 fl, _lib.dtype_code(dtype), _lib.stream())
+            return L.mdgl_segment_reduce(off.data_ptr(), val.data_ptr(), out.data_ptr(), num_seg,
+                                         d, REDUCERS[reducer], n, fl, _lib.dtype_code(dtype),
+                                         _lib.stream())
+
+        _lib.check(run(flags), "segment_reduce")
+        seg.verify()  # raises for invalid GPU lengths before anything is returned
+        if flags & _lib.SEGMENTS_SKIP_LONG and seg.longest > _lib.SEGMENT_SPLIT_ROWS:
+            _lib.check(run((flags & ~_lib.SEGMENTS_SKIP_LONG) | _lib.SEGMENTS_LONG_ONLY),
+                       "segment_reduce")
+    seg.verify()
     return _lib.give_back(out.reshape((num_seg,) + fshape), V.is_torch, V.device), seg, arg
 
 
@@ -230,7 +259,21 @@ def _segment_softmax(seglen, value):
     if val is not None:
         slots, chunk_len = _plan.geometry(d, dtype, val, out)
     if on_gpu:
-        seg = _Segments(seglen, n, chunk_len)
+        seg = _Segments(seglen, n, chunk_len, defer=True)
+        if seg.num and n and d:
+            # start without the longest length: the staged kernel takes every
+            # segment of at most chunk_len rows; a longer one (known once the
+            # check is back) sends the call through the chunk plan below,
+            # which rewrites every row
+            rc = _lib.lib().mdgl_segment_softmax_short(
+                seg.off.data_ptr(), val.data_ptr(), out.data_ptr(), seg.num, d, n,
+                _lib.dtype_code(dtype), _lib.stream())
+            seg.verify()
+            if rc != _lib.ENOTSUP:
+                _lib.check(rc, "segment_softmax")
+                if seg.heavy == 0:
+                    return _lib.give_back(out.reshape(shape), V.is_torch, V.device), seg
+        seg.verify()
     num_seg = seg.num
     if num_seg and n and d:
         off = seg.device()

@@ -78,6 +78,15 @@ def test_invalid_arguments_are_rejected_without_launching(lib):
     rc = lib.mdgl_gspmm(1, 1, 1, 1, 1, 1, 10, 2, 4, 4, 4, 0, None, 0, None, None, None, None, 1,
                         1, 3, 8, 1, 1, 1, 4096 + 8, 1 << 20, 0, 0, None)
     assert rc == -1 and "aligned" in err(lib)
+    # segment_reduce pass flags: at most one of SHORT, SKIP_LONG and LONG_ONLY
+    rc = lib.mdgl_segment_reduce(None, None, None, 4, 2, 0, 8, 4 | 8, 0, None)
+    assert rc == -1 and "at most one" in err(lib)
+    rc = lib.mdgl_segment_reduce(None, None, None, 4, 2, 0, 8, 8 | 16, 0, None)
+    assert rc == -1 and "at most one" in err(lib)
+    rc = lib.mdgl_segment_softmax_short(None, None, None, 4, 2, 8, 7, None)
+    assert rc == -1 and "dtype" in err(lib)
+    rc = lib.mdgl_segment_softmax_short(None, None, None, 4, 2, 8, 0, None)
+    assert rc == -1 and "null" in err(lib)
     # too many b blocks for the GPU bucketing
     rc = lib.mdgl_gather_mm(1, 1, 1, 1, 100, 4, 4, 100000, 1, 1 << 40, 0, None)
     assert rc == -3
@@ -89,6 +98,7 @@ def test_empty_problems_are_no_ops(lib):
                           None) == 0
     assert lib.mdgl_segment_mm(None, None, None, None, 0, 4, 2, 3, None, 0, 0, None) == 0
     assert lib.mdgl_cumsum(None, None, 0, None) == 0
+    assert lib.mdgl_segment_softmax_short(None, None, None, 0, 4, 0, 0, None) == 0
 
 
 def test_build_csr_arguments(lib):

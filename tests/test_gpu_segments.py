@@ -163,3 +163,82 @@ def test_segment_reduce_clamps_offsets_into_the_rows():
         rows = value[starts[s]:starts[s] + lens[s]]
         want = rows.max(axis=0) if lens[s] else np.full(d, -np.inf, dtype=np.float32)
         np.testing.assert_array_equal(got[s], want, err_msg=str(s))
+
+
+@pytest.mark.parametrize("d", [3, 16, 40])
+def test_skip_long_then_long_only_equals_one_call(d):
+    """MDGL_SEGMENTS_SKIP_LONG leaves the segments above the split threshold
+    unwritten and MDGL_SEGMENTS_LONG_ONLY writes only those: the two calls
+    together write what one call without either flag writes, values and
+    arg rows alike (the order segment_reduce uses for GPU lengths, whose
+    longest length is known only after the first call is queued)."""
+    rng = np.random.default_rng(400 + d)
+    seglen = lengths(rng, 500, 14, long_rows=(SPLIT + 1, 12000, SPLIT))
+    n = int(seglen.sum())
+    value = np.round(rng.standard_normal((n, d)) * 3).astype(np.float32)
+    off = torch.from_numpy(np.concatenate([[0], np.cumsum(seglen)]).astype(np.int32)).cuda()
+    vt = torch.from_numpy(value).cuda()
+    long_ = seglen > SPLIT
+    L = _lib.lib()
+    for reducer in ("sum", "max"):
+        red = _lib.REDUCERS[reducer]
+        results = []
+        for passes in ((0,), (_lib.SEGMENTS_SKIP_LONG, _lib.SEGMENTS_LONG_ONLY)):
+            out = torch.full((seglen.size, d), 12345.0, device="cuda")
+            arg = torch.full((seglen.size, d), -9, dtype=torch.int32, device="cuda")
+            for i, flags in enumerate(passes):
+                if reducer == "max":
+                    rc = L.mdgl_segment_reduce_arg(off.data_ptr(), vt.data_ptr(), out.data_ptr(),
+                                                   arg.data_ptr(), seglen.size, d, red, n, flags,
+                                                   _lib.FLOAT32, _lib.stream())
+                else:
+                    rc = L.mdgl_segment_reduce(off.data_ptr(), vt.data_ptr(), out.data_ptr(),
+                                               seglen.size, d, red, n, flags, _lib.FLOAT32,
+                                               _lib.stream())
+                _lib.check(rc, "segment_reduce")
+                if flags == _lib.SEGMENTS_SKIP_LONG:
+                    first = out.cpu().numpy()
+                    assert (first[long_] == 12345.0).all(), "long segments written by SKIP_LONG"
+                    assert (first[~long_] != 12345.0).all()
+                    if reducer == "max":
+                        assert (arg.cpu().numpy()[long_] == -9).all()
+            results.append((out.cpu().numpy(), arg.cpu().numpy()))
+        np.testing.assert_array_equal(results[0][0], results[1][0], err_msg=reducer)
+        if reducer == "max":
+            np.testing.assert_array_equal(results[0][1], results[1][1], err_msg="args")
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("d", [1, 16, 33])
+def test_segment_softmax_short_leaves_long_segments(dtype, d):
+    """mdgl_segment_softmax_short: the rows of segments of at most chunk_len
+    rows are the softmax (against the oracle), the rows of longer segments
+    are left as they were."""
+    from mojodgl.ops import _plan
+
+    rng = np.random.default_rng(500 + d)
+    probe = torch.zeros(4, d, dtype=torch.float32 if dtype == np.float32 else torch.float64,
+                        device="cuda")
+    slots, chunk_len = _plan.geometry(d, dtype, probe, torch.zeros_like(probe))
+    seglen = rng.poisson(10, 800)
+    seglen[::13] = 0
+    seglen[[5, 300]] = [chunk_len + 1, 3 * chunk_len]
+    seglen[[6, 301]] = [chunk_len, 1]
+    n = int(seglen.sum())
+    value = (rng.normal(size=(n, d)) * 2).astype(dtype)
+    val = torch.from_numpy(value).cuda()
+    out = torch.full_like(val, 7.0)
+    off = torch.from_numpy(np.concatenate([[0], np.cumsum(seglen)]).astype(np.int32)).cuda()
+    rc = _lib.lib().mdgl_segment_softmax_short(off.data_ptr(), val.data_ptr(), out.data_ptr(),
+                                               seglen.size, d, n, _lib.dtype_code(dtype),
+                                               _lib.stream())
+    V = 16 // np.dtype(dtype).itemsize
+    if (d // V if d % V == 0 else d) > 32:  # wider than the staged kernel takes
+        assert rc == _lib.ENOTSUP
+        return
+    _lib.check(rc, "segment_softmax_short")
+    got = out.cpu().numpy()
+    row_long = np.repeat(seglen > chunk_len, seglen)
+    assert (got[row_long] == 7.0).all()
+    ref = oracle.segment_softmax(seglen, value, np.float64)
+    close(got[~row_long], ref[~row_long], ref[~row_long], dtype, "segment_softmax_short")
