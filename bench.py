@@ -400,9 +400,14 @@ def time_gather_ceilings(g, N, E, H, args):
       * rows_32B_by_node: 32-byte rows of an (N, H) table by each edge's
         destination, twice the bytes of one gsddmm operand;
       * rows_64B_by_node: 64-byte rows of an (N, 2H) table by each edge's
-        destination (the write pass reading a row's (max, sum)).
+        destination (the write pass reading a row's (max, sum));
+      * rows_1KB_by_source: 1 KB rows (the H x D floats of a node) of an
+        (N, H * D) table by N random edge sources (gspmm's source-row reads);
+      * rows_1KB_in_order: the same table by 0 .. N - 1, a streaming copy;
+      * rows_1KB_streamed: the same table read once in order and hardly
+        written (segment_reduce sum over runs of 64 rows): a streaming read.
     Each figure is GB/s of bytes moved per launch (4 index + gathered + written
-    per edge)."""
+    per row; read + written for the streaming read)."""
     import torch
 
     from mojodgl import _lib
@@ -411,24 +416,43 @@ def time_gather_ceilings(g, N, E, H, args):
     cold = ColdTimer(max(3, args.reps // 2), 1)
     gen = torch.Generator(device="cuda").manual_seed(9)
     perm = torch.randperm(E, device="cuda", generator=gen).to(torch.int32)
-    vd = g._device_coo()[1]
+    ud, vd = g._device_coo()
+    in_order = torch.arange(N, dtype=torch.int32, device="cuda")
     out = {}
     for name, rows, width, idx in (("rows_32B_by_edge_id", E, H, perm),
                                    ("rows_32B_by_node", N, H, vd),
-                                   ("rows_64B_by_node", N, 2 * H, vd)):
+                                   ("rows_64B_by_node", N, 2 * H, vd),
+                                   ("rows_1KB_by_source", N, 256, ud[:N]),
+                                   ("rows_1KB_in_order", N, 256, in_order)):
         table = torch.randn(rows, width, device="cuda", generator=gen)
-        dst = torch.empty(E, width, device="cuda")
+        n_idx = idx.numel()
+        dst = torch.empty(n_idx, width, device="cuda")
 
         def run():
-            _lib.check(L.mdgl_gather_rows(table.data_ptr(), idx.data_ptr(), dst.data_ptr(), E,
+            _lib.check(L.mdgl_gather_rows(table.data_ptr(), idx.data_ptr(), dst.data_ptr(), n_idx,
                                           width, _lib.FLOAT32, _lib.stream()), "gather_rows")
 
         t = cold(run)
-        nbytes = E * (4 + 8 * width)
+        nbytes = n_idx * (4 + 8 * width)
         out[name] = dict(t, bytes=nbytes, GBps=round(nbytes / t["median_ms"] / 1e6, 1),
                          table_MB=round(rows * width * 4 / 1e6, 1))
         del table, dst
-    del perm
+    del perm, in_order
+    import mojodgl.ops as ops
+
+    table = torch.randn(N, 256, device="cuda", generator=gen)
+    runs = torch.full((N // 64,), 64, dtype=torch.int64, device="cuda")
+    rows = int(runs.numel()) * 64
+    view = table[:rows]
+
+    def stream():
+        ops.segment_reduce(runs, view, "sum")
+
+    t = cold(stream)
+    nbytes = rows * 1024 + runs.numel() * 1024
+    out["rows_1KB_streamed"] = dict(t, bytes=nbytes, GBps=round(nbytes / t["median_ms"] / 1e6, 1),
+                                    table_MB=round(rows * 1024 / 1e6, 1))
+    del table, runs, view
     free_gpu()
     return out
 
