@@ -47,6 +47,10 @@ extern "C" {
 /* flags of mdgl_gspmm / mdgl_segment_reduce */
 #define MDGL_REPLACE_INF 1 /* +-inf results become 0 (heterograph.py:232-239) */
 #define MDGL_RHS_CSR_ORDER 2 /* mdgl_gspmm: rhs row i belongs to CSR slot i (not edge eid[i]) */
+/* mdgl_gspmm: lhs rows start on 128-byte lines: row r at lhs + r * stride
+ * elements, stride = dl rounded up to a multiple of 128 bytes (lhs itself
+ * 128-byte aligned) */
+#define MDGL_LHS_LINE_ROWS 8
 /* mdgl_segment_reduce(_arg): the caller knows that no segment has more than
  * MDGL_SEGMENT_SPLIT_ROWS rows, so the pass that splits longer segments is
  * not launched (a longer segment is then still reduced whole, in row order) */
@@ -126,7 +130,11 @@ int mdgl_gsddmm(const int32_t* uids, const int32_t* vids, const void* lhs, const
  * flags: MDGL_REPLACE_INF; MDGL_RHS_CSR_ORDER when the edge operand has been
  * put in CSR slot order (mdgl_gather_rows with eid), which turns its random
  * reads into streaming ones -- worth it for a narrow edge operand read by
- * several column slabs; arg_e still reports edge ids. */
+ * several column slabs; arg_e still reports edge ids; MDGL_LHS_LINE_ROWS when
+ * the node operand has been copied to rows that each start on a 128-byte
+ * line (a row of dl elements whose size is no multiple of 128 bytes
+ * otherwise starts mid-line, and every slab of its columns touches one line
+ * more) -- worth it when each node row is gathered many times. */
 int mdgl_gspmm(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
                const void* lhs, const void* rhs, void* dst, int64_t num_dst, int op, int64_t dl,
                int64_t dr, int64_t dout, int reduce_op, const int32_t* deg, int nd,

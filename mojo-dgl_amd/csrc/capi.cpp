@@ -124,11 +124,13 @@ void identity_bcast(int64_t width, Bcast* bc) {
 }
 
 // Load mode of one operand for lanes owning `vec` consecutive output
-// columns. Contiguous 16-byte loads need aligned rows and groups.
+// columns. Contiguous 16-byte loads need aligned rows and groups; with
+// `padded` rows (a stride that is a multiple of vec, past the row's width)
+// the lane holding the last columns may read a whole vector.
 int pick_mode(const Bcast& bc, bool lhs, int64_t dout, int vec, int64_t width, const void* base,
-              int64_t esize) {
+              int64_t esize, bool padded = false) {
   if (vec == 1) return M_CONTIG;  // VEC = 1 kernels load one element whatever the mode
-  bool contig = dout % vec == 0 && width % vec == 0 && aligned(base, vec * esize);
+  bool contig = (padded || (dout % vec == 0 && width % vec == 0)) && aligned(base, vec * esize);
   bool splat = true;
   for (int64_t g = 0; g < dout && (contig || splat); g += vec) {
     const int64_t o0 = bcast_off(bc, g, lhs);
@@ -433,6 +435,7 @@ int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* e
   p.out = dst;
   p.num_rows = num_dst;
   p.dl = dl;
+  p.lstride = dl;
   p.dr = dr;
   p.dout = dout;
   p.op = op;
@@ -498,13 +501,21 @@ int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* e
       p.part_e = reinterpret_cast<int32_t*>(w);
     }
   }
+  if ((flags & MDGL_LHS_LINE_ROWS) && op != OP_COPY_RHS) {
+    if (!aligned(lhs, 128))
+      return fail(MDGL_EINVAL, "gspmm: MDGL_LHS_LINE_ROWS needs lhs on a 128-byte boundary");
+    p.lstride = (dl * es + 127) / 128 * 128 / es;
+  }
   const int vw = vec_width(dtype);
-  // 16-byte lanes when the width allows, else 8-byte lanes for even float32
-  // widths, else one element per lane
-  p.vec = dout % vw == 0 ? vw : (dtype == MDGL_FLOAT32 && dout % 2 == 0 ? 2 : 1);
-  p.lmode = op == OP_COPY_RHS ? M_CONTIG : pick_mode(p.bc, true, dout, p.vec, dl, lhs, es);
+  const bool lined = p.lstride != dl;  // node rows on 128-byte lines
+  // 16-byte lanes when the width allows (or the node rows are padded to
+  // lines, so the last lane may read a whole vector of them), else 8-byte
+  // lanes for even float32 widths, else one element per lane
+  p.vec = (dout % vw == 0 || (lined && !dot_out)) ? vw
+          : (dtype == MDGL_FLOAT32 && dout % 2 == 0 ? 2 : 1);
+  p.lmode = op == OP_COPY_RHS ? M_CONTIG : pick_mode(p.bc, true, dout, p.vec, dl, lhs, es, lined);
   p.rmode = op == OP_COPY_LHS ? M_CONTIG : pick_mode(p.bc, false, dout, p.vec, dr, rhs, es);
-  if (p.vec > 1 && aligned(dst, p.vec * es)) p.flags |= F_OUT_VEC;
+  if (p.vec > 1 && dout % p.vec == 0 && aligned(dst, p.vec * es)) p.flags |= F_OUT_VEC;
   if (dot_out) {
     // the fused dot: mul / sum, 16-byte lanes, lhs rows contiguous, the edge
     // operand constant over groups of D = dout / dr consecutive columns

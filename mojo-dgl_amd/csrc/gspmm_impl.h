@@ -48,6 +48,7 @@ struct GspmmArgs {
   int32_t* arg_u;
   int32_t* arg_e;
   int64_t num_rows, dl, dr, dout;
+  int64_t lstride;  // elements between lhs rows
   Bcast bc;
   int lmode, rmode, flags, G, S, vec;
   int64_t num_chunks;
@@ -210,7 +211,7 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
         }
         if (j + u < cnt && feat_ok) {
           if constexpr (OP != OP_COPY_RHS)
-            fetch<T, VEC, LM>(a.lhs + (int64_t)s * a.dl, a.lmode, loff, x[u]);
+            fetch<T, VEC, LM>(a.lhs + (int64_t)s * a.lstride, a.lmode, loff, x[u]);
           if constexpr (OP != OP_COPY_LHS) {
             if (!(SCALAR_E && scalar_e)) {
               const int64_t rrow = rhs_csr ? (int64_t)(start + base + j + u) : (int64_t)e;
@@ -419,6 +420,7 @@ hipError_t launch_gspmm_op(const GspmmParams& p) {
   a.arg_e = p.arg_e;
   a.num_rows = p.num_rows;
   a.dl = p.dl;
+  a.lstride = p.lstride > 0 ? p.lstride : p.dl;
   a.dr = p.dr;
   a.dout = p.dout;
   a.bc = p.bc;

@@ -31,6 +31,7 @@ struct GspmmParams {
   int32_t* arg_u;  // optional, max/min only
   int32_t* arg_e;
   int64_t num_rows, dl, dr, dout;
+  int64_t lstride;  // elements between lhs rows (dl, or more for rows on 128-byte lines)
   Bcast bc;
   int lmode, rmode;
   int op, red;  // red in {SUM, MAX, MIN}; mean is F_MEAN

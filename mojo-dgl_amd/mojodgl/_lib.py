@@ -52,6 +52,7 @@ TARGETS = {"u": SRC_CODE, "v": DST_CODE, "e": EDGE_CODE}
 FLOAT32, FLOAT64 = 0, 1
 REPLACE_INF = 1
 RHS_CSR_ORDER = 2
+LHS_LINE_ROWS = 8  # mdgl_gspmm: lhs rows copied to start on 128-byte lines
 SEGMENTS_SHORT = 4  # mdgl_segment_reduce: no segment longer than SEGMENT_SPLIT_ROWS
 SEGMENTS_SKIP_LONG = 8  # mdgl_segment_reduce: longer segments left for a LONG_ONLY call
 SEGMENTS_LONG_ONLY = 16  # mdgl_segment_reduce: only the segments longer than SEGMENT_SPLIT_ROWS

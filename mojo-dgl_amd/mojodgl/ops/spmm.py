@@ -39,6 +39,23 @@ def _slabs(dout, dtype):
     return -(-(-(-dout // vec)) // 64)
 
 
+def _line_rows(lhs, rows, dl, num_edges, dtype):
+    """lhs copied to rows that each start on a 128-byte line (the layout of
+    mdgl_gspmm's MDGL_LHS_LINE_ROWS), or None when that does not pay: rows of
+    a size that is no multiple of 128 bytes start mid-line, so every column
+    slab of them touches one line more than it needs; the copy reads and
+    writes the table once, worth it for rows of a slab or more that the
+    edges gather at least 8 times each."""
+    es = np.dtype(dtype).itemsize
+    row_bytes = dl * es
+    if row_bytes % 128 == 0 or row_bytes < 512 or rows == 0 or num_edges < 8 * rows:
+        return None
+    stride = -(-row_bytes // 128) * 128 // es
+    padded = torch.empty((rows, stride), dtype=lhs.dtype, device=lhs.device)
+    padded[:, :dl].copy_(lhs.reshape(rows, dl))
+    return padded
+
+
 def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False,
          arg_dtype=torch.int64, kind="in", narrow_split=None):
     """Validate, launch, and return device tensors (out, arg_u, arg_e) plus
@@ -102,6 +119,11 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
         if narrow_split and _packed(dout, dtype) and narrow_split < sched.chunk_len:
             sched = csr.chunks_for(narrow_split)
         flags = _lib.REPLACE_INF if replace_inf else 0
+        if lhs is not None and code != OP_COPY_RHS:
+            lined = _line_rows(lhs, lt.shape[0], dl, num_edges, dtype)
+            if lined is not None:
+                lhs = lined
+                flags |= _lib.LHS_LINE_ROWS
         if rhs is not None and code not in (OP_COPY_LHS, OP_COPY_RHS) and dr == 1 \
                 and num_edges and _slabs(dout, dtype) > 1:
             # a scalar edge operand read by several column slabs: put it in

@@ -78,6 +78,10 @@ def test_invalid_arguments_are_rejected_without_launching(lib):
     rc = lib.mdgl_gspmm(1, 1, 1, 1, 1, 1, 10, 2, 4, 4, 4, 0, None, 0, None, None, None, None, 1,
                         1, 3, 8, 1, 1, 1, 4096 + 8, 1 << 20, 0, 0, None)
     assert rc == -1 and "aligned" in err(lib)
+    # node rows on 128-byte lines need an lhs on a 128-byte boundary
+    rc = lib.mdgl_gspmm(1, 1, 1, 8, 16, 16, 10, 2, 4, 4, 4, 0, None, 0, None, None, None, None,
+                        None, None, 0, 0, None, None, 0, None, 0, 8, 0, None)
+    assert rc == -1 and "128-byte" in err(lib)
     # segment_reduce pass flags: at most one of SHORT, SKIP_LONG and LONG_ONLY
     rc = lib.mdgl_segment_reduce(None, None, None, 4, 2, 0, 8, 4 | 8, 0, None)
     assert rc == -1 and "at most one" in err(lib)

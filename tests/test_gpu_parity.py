@@ -134,6 +134,35 @@ def test_gspmm_broadcast(lshape, rshape, chunk_len):
     np.testing.assert_array_equal(ae, re_)
 
 
+@pytest.mark.parametrize("dtype,d", [(np.float32, 602), (np.float32, 130), (np.float64, 602),
+                                     (np.float64, 70)])
+def test_gspmm_line_aligned_rows(dtype, d):
+    """Node rows whose size is no multiple of 128 bytes, gathered many times
+    (here 33 per row): gspmm copies them to rows on 128-byte lines
+    (MDGL_LHS_LINE_ROWS) and the results stay bit-identical to the oracle,
+    values and args, for the C3 shapes (a scalar edge weight, copy_u)."""
+    from mojodgl.ops import spmm
+
+    rng = np.random.default_rng(30 + d)
+    n, e = 600, 20000
+    u, v = rand_graph(n, e, 31)
+    x = rng.normal(size=(n, d)).astype(dtype)
+    w = rng.random((e, 1)).astype(dtype)
+    lined = spmm._line_rows(torch.from_numpy(x).cuda(), n, d, e, dtype)
+    assert lined is not None and lined.stride(0) * lined.element_size() % 128 == 0
+    g = dgl.graph((u, v), num_nodes=n)
+    for oop, red, L, R in (("mul", "sum", x, w), ("mul", "mean", x, w),
+                           ("copy_lhs", "max", x, None), ("mul", "min", x, w)):
+        got, (au, ae) = spmm._gspmm(g, oop, red, L, R)
+        if red in ("max", "min"):
+            want, ru, re_ = oracle.gspmm(u, v, n, oop, red, L, R, dtype, with_arg=True)
+            np.testing.assert_array_equal(au, ru, err_msg=red)
+            np.testing.assert_array_equal(ae, re_, err_msg=red)
+        else:
+            want = oracle.gspmm(u, v, n, oop, red, L, R, dtype)
+        np.testing.assert_array_equal(got, want, err_msg="{} {} d={}".format(oop, red, d))
+
+
 def test_gspmm_power_law_hubs_against_oracle():
     """Degrees spanning 0 .. 5000 with the default split threshold."""
     rng = np.random.default_rng(7)
