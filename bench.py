@@ -747,7 +747,7 @@ def section_c3(args):
     log("generating community graph")
     u, v, N = community_graph()
     E = u.size
-    F = 602
+    F = args.c3_feat
     g = dgl.graph((u, v), num_nodes=N)
     g._device_csr("in")
     indeg = np.maximum(np.bincount(v, minlength=N), 1).astype(np.float64)
@@ -1060,6 +1060,8 @@ def main():
                          "kernels only")
     ap.add_argument("--cpu-fraction", type=float, default=0.1)
     ap.add_argument("--cpu-fraction-c3", type=float, default=0.01)
+    ap.add_argument("--c3-feat", type=int, default=602,
+                    help="node feature width of the community-graph section (the config: 602)")
     ap.add_argument("--cpu-fraction-c4", type=float, default=0.05)
     ap.add_argument("--cpu-rows-c5", type=int, default=100_000)
     ap.add_argument("--cpu-rows-c5-serial", type=int, default=20_000)
