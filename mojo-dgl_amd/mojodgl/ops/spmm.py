@@ -51,6 +51,9 @@ def _line_rows(lhs, rows, dl, num_edges, dtype):
     if row_bytes % 128 == 0 or row_bytes < 512 or rows == 0 or num_edges < 8 * rows:
         return None
     stride = -(-row_bytes // 128) * 128 // es
+    free, _ = torch.cuda.mem_get_info(lhs.device)
+    if rows * stride * es > free // 4:  # the copy must not crowd out the caller's memory
+        return None
     padded = torch.empty((rows, stride), dtype=lhs.dtype, device=lhs.device)
     padded[:, :dl].copy_(lhs.reshape(rows, dl))
     return padded
