@@ -171,13 +171,15 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
   const bool scalar_e = SCALAR_E && a.dr == 1;
   // the edge operand may come in CSR slot order (row i of rhs for slot i)
   const bool rhs_csr = a.flags & F_RHS_CSR;
+  // edge ids are read only for an arg or an edge operand in edge-id order
+  const bool need_e = ARG_OUT || (OP != OP_COPY_LHS && !rhs_csr);
   for (int base = 0; base < nmax; base += G) {
     int my_s = 0, my_e = 0;
     T my_w = T(0);
     if (base + gl < n) {
       const int i = start + base + gl;
       if (a.indices) my_s = __builtin_nontemporal_load(a.indices + i);
-      my_e = ident ? i : __builtin_nontemporal_load(a.eid + i);
+      my_e = ident ? i : (need_e ? __builtin_nontemporal_load(a.eid + i) : 0);
       if (SCALAR_E && scalar_e) my_w = a.rhs[rhs_csr ? (int64_t)i : (int64_t)my_e];
     }
     const int cnt = n - base < G ? n - base : G;  // may be <= 0 on finished groups

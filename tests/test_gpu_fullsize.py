@@ -172,7 +172,7 @@ def test_c2_gat_layer(c2):
     within(zs, ref64, bound, "gspmm u_mul_e_sum sampled rows")
     ref32 = oracle.gspmm(None, None, rows.size, "mul", "sum", hh.reshape(-1, 8, 32),
                          a_s.reshape(-1, 8, 1), np.float32, graph_csr=csr_s).reshape(-1, 256)
-    whole = np.diff(sub) <= hg.CHUNK_LEN
+    whole = np.diff(sub) <= g._device_csr("in").chunks.chunk_len  # rows not split
     log("C2: {} sampled rows, {} not split, max degree {}".format(
         rows.size, int(whole.sum()), int(np.diff(sub).max())))
     np.testing.assert_array_equal(zs[whole], ref32[whole])
@@ -204,7 +204,7 @@ def test_c3_aggregations(c3):
     csr_s = (sub, src, local)
     hh = h.cpu().numpy()
     rows_d = torch.from_numpy(rows).cuda()
-    whole = np.diff(sub) <= hg.CHUNK_LEN
+    whole = np.diff(sub) <= g._device_csr("in").chunks.chunk_len  # rows not split
 
     z = ops.u_mul_e_sum(g, h, torch.from_numpy(w).cuda())[rows_d].cpu().numpy()
     w_s = w[eids]

@@ -187,6 +187,21 @@ def test_no_gpu_means_a_loud_error():
         ops.u_mul_e_sum(g, np.ones((3, 2)), np.ones((4, 2)))
 
 
+def test_split_length_leaves_rows_a_quarter_over_a_chunk_whole():
+    def ip(deg):
+        return np.concatenate([[0], np.cumsum(deg)]).astype(np.int64)
+
+    assert hg.split_length(ip([3, 512, 640, 7]), 512) == 640  # none split
+    assert hg.split_length(ip([3, 512, 641, 7]), 512) == 512  # rows > 512 split
+    assert hg.split_length(ip([3, 512, 20000]), 512) == 512
+    assert hg.split_length(ip([3, 500]), 512) == 512  # nothing to split
+    assert hg.split_length(ip([5, 4]), 4) == 5
+    assert hg.split_length(ip([6, 4]), 4) == 4
+    assert hg.split_length(np.zeros(1, dtype=np.int64), 512) == 512  # no rows
+    heavy, _, _, _ = hg.chunk_plan(ip([3, 512, 640, 7]), hg.split_length(ip([3, 512, 640, 7]), 512))
+    assert heavy.size == 0
+
+
 def test_chunk_plan():
     rng = np.random.default_rng(0)
     deg = rng.integers(0, 40, 200)
