@@ -1062,6 +1062,9 @@ def main():
     ap.add_argument("--cpu-fraction-c3", type=float, default=0.01)
     ap.add_argument("--c3-feat", type=int, default=602,
                     help="node feature width of the community-graph section (the config: 602)")
+    ap.add_argument("--chunk-len", type=int, default=None,
+                    help="gspmm heavy-row chunk length (mojodgl.heterograph.CHUNK_LEN; "
+                         "default 512)")
     ap.add_argument("--cpu-fraction-c4", type=float, default=0.05)
     ap.add_argument("--cpu-rows-c5", type=int, default=100_000)
     ap.add_argument("--cpu-rows-c5-serial", type=int, default=20_000)
@@ -1082,6 +1085,10 @@ def main():
         print("bench.py needs the GPU", file=sys.stderr)
         sys.exit(1)
     torch.cuda.set_device(0)
+    if args.chunk_len is not None:
+        import mojodgl.heterograph as hg
+
+        hg.CHUNK_LEN = args.chunk_len
     t_start = time.perf_counter()
     res = WORKLOADS[args.workload](args)
     if args.workload == "gat" and not args.headline_only:
