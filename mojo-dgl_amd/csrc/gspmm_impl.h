@@ -167,7 +167,7 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
   const int nmax = WIDE ? n : wave_max_int(n);
   // a scalar edge operand (one value per edge, splatted over the columns) is
   // loaded with the ids, one edge per lane, and broadcast like them
-  constexpr bool SCALAR_E = WIDE && RM == M_SPLAT && OP != OP_COPY_LHS;
+  constexpr bool SCALAR_E = RM == M_SPLAT && OP != OP_COPY_LHS;
   const bool scalar_e = SCALAR_E && a.dr == 1;
   // the edge operand may come in CSR slot order (row i of rhs for slot i)
   const bool rhs_csr = a.flags & F_RHS_CSR;
@@ -206,7 +206,9 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
         se[u] = e;
         if constexpr (SCALAR_E) {
           if (scalar_e) {
-            const T w = readlane_val(my_w, jj);
+            T w;
+            if constexpr (WIDE) w = readlane_val(my_w, jj);
+            else w = __shfl(my_w, gbase + jj);
 #pragma unroll
             for (int v = 0; v < VEC; ++v) y[u][v] = w;
           }
@@ -319,9 +321,12 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
 // Kernel variants, one body each so that every launch only carries the
 // registers of its own path: whole-wavefront units (G = 64) with both
 // operands contiguous, with a splatted edge operand, or any modes; packed
-// units with contiguous operands, or any modes.
+// units likewise. A scalar edge operand (one value per edge) is loaded with
+// the ids and broadcast by v_readlane or ds_bpermute in both layouts: read
+// per lane and edge through the any-modes path it cost a GCN aggregation over
+// 128 columns 4x the time of the same gather without the weight.
 enum { P_WIDE_CC = 0, P_WIDE_CS = 1, P_WIDE_DYN = 2, P_PACK_CC = 3, P_PACK_DYN = 4,
-       P_WIDE_CS_DOT = 5, P_PACK_DYN_DOT = 6 };
+       P_WIDE_CS_DOT = 5, P_PACK_DYN_DOT = 6, P_PACK_CS = 7 };
 
 template <class T, int OP, int RED, int VEC, int PATH, bool NT>
 __global__ __launch_bounds__(BLOCK) void gspmm_kernel(GspmmArgs<T> a) {
@@ -342,6 +347,8 @@ __global__ __launch_bounds__(BLOCK) void gspmm_kernel(GspmmArgs<T> a) {
     gspmm_body<T, OP, RED, VEC, M_DYN, M_DYN, true, NT>(a, chunk, wave, lane);
   else if constexpr (PATH == P_PACK_CC)
     gspmm_body<T, OP, RED, VEC, M_CONTIG, M_CONTIG, false, NT>(a, chunk, wave, lane);
+  else if constexpr (PATH == P_PACK_CS)
+    gspmm_body<T, OP, RED, VEC, M_CONTIG, M_SPLAT, false, NT>(a, chunk, wave, lane);
   else if constexpr (PATH == P_WIDE_CS_DOT)
     gspmm_body<T, OP, RED, VEC, M_CONTIG, M_SPLAT, true, NT, true>(a, chunk, wave, lane);
   else if constexpr (PATH == P_PACK_DYN_DOT)
@@ -403,6 +410,8 @@ void launch_path(const GspmmArgs<T>& a, dim3 grid, dim3 block, int lm, int rm, h
   } else {
     if (lm == M_CONTIG && rm == M_CONTIG)
       hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_PACK_CC, NT>), grid, block, 0, st, a);
+    else if (lm == M_CONTIG && rm == M_SPLAT)
+      hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_PACK_CS, NT>), grid, block, 0, st, a);
     else
       hipLaunchKernelGGL((gspmm_kernel<T, OP, RED, VEC, P_PACK_DYN, NT>), grid, block, 0, st, a);
   }

@@ -110,6 +110,38 @@ def test_gspmm_feature_widths(d):
                                       err_msg="{} d={}".format(name, d))
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("d", [1, 4, 12, 32, 128, 256])
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
+def test_gspmm_scalar_edge_operand(dtype, d, op, chunk_len):
+    """One value per edge over every column of the node row (the GCN edge
+    weight): loaded with the ids and broadcast across the lane group, for rows
+    packed several to a wavefront and for whole-wavefront rows alike."""
+    n, e = 400, 6000
+    u, v = rand_graph(n, e, 11)
+    v[:700] = 5  # a hub destination, split into chunks when chunk_len is set
+    rng = np.random.default_rng(12)
+    x = rng.normal(size=(n, d)).astype(dtype)
+    w = (rng.random((e, 1)) + 0.5).astype(dtype)
+    g = dgl.graph((u, v), num_nodes=n)
+    for red in ("sum", "max", "min", "mean"):
+        got, (au, ae) = ops.spmm._gspmm(g, op, red, x, w)
+        what = "{} {} d={}".format(op, red, d)
+        assert got.shape == (n, d) and got.dtype == dtype, what
+        if red in ("max", "min"):
+            same, ru, re_ = oracle.gspmm(u, v, n, op, red, x, w, dtype, with_arg=True)
+            np.testing.assert_array_equal(got, same, err_msg=what)
+            np.testing.assert_array_equal(au, ru, err_msg=what)
+            np.testing.assert_array_equal(ae, re_, err_msg=what)
+            continue
+        if chunk_len is None:
+            np.testing.assert_array_equal(got, oracle.gspmm(u, v, n, op, red, x, w, dtype),
+                                          err_msg=what)
+        ref64 = oracle.gspmm(u, v, n, op, red, x, w, np.float64)
+        bound = oracle.gspmm(u, v, n, ABS_OP[op], red, np.abs(x), np.abs(w), np.float64)
+        close(got, ref64, bound, dtype, what)
+
+
 @pytest.mark.parametrize("lshape,rshape", [((8, 32), (8, 1)), ((602,), (1,)), ((4, 3), (4, 1)),
                                            ((1,), (6,)), ((2, 3, 4), (2, 1, 4)),
                                            ((3, 1), (1, 5))])
