@@ -22,6 +22,12 @@ from .sddmm import _check_rows, feat_shape, out_feat_shape, reshape_lhs_rhs, sha
 __all__ = ["gspmm"]
 
 
+# a scalar edge operand of this many edges or more is put in CSR slot order
+# before a one-slab whole-wavefront gspmm (below that the extra launch costs
+# more than it saves)
+CSR_ORDER_MIN_EDGES = 1 << 20
+
+
 def _packed(dout, dtype):
     """Whether several rows share a wavefront: a row's lanes (by the lane
     width rule of mdgl_gspmm below) number 32 or fewer."""
@@ -128,9 +134,14 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
                 lhs = lined
                 flags |= _lib.LHS_LINE_ROWS
         if rhs is not None and code not in (OP_COPY_LHS, OP_COPY_RHS) and dr == 1 \
-                and num_edges and _slabs(dout, dtype) > 1:
+                and num_edges and (_slabs(dout, dtype) > 1
+                                   or (not _packed(dout, dtype)
+                                       and num_edges >= CSR_ORDER_MIN_EDGES)):
             # a scalar edge operand read by several column slabs: put it in
-            # CSR slot order once, so every slab streams it
+            # CSR slot order once, so every slab streams it; also for rows of
+            # one whole-wavefront slab, whose walk would otherwise wait on a
+            # gather by edge id every 64 slots (256 columns: 3-7 % faster;
+            # packed rows, several to a wavefront, do better without it)
             perm = torch.empty(num_edges, dtype=tdt, device=gdev)
             _lib.check(_lib.lib().mdgl_gather_rows(rhs.data_ptr(), csr.eid.data_ptr(),
                                                    perm.data_ptr(), num_edges, 1,
