@@ -694,8 +694,9 @@ def section_c1(args):
 
 
 def section_c2_f64(g, h32, args):
-    """gspmm u_mul_e_sum of the headline graph in float64: h (N, 8, 32),
-    a (E, 8, 1)."""
+    """The headline graph's ops in float64, the reference's precision:
+    gspmm u_mul_e_sum h (N, 8, 32) x a (E, 8, 1), gsddmm u_add_v and
+    edge_softmax alone (cold caches), and the whole GAT step."""
     import torch
 
     import mojodgl.ops as ops
@@ -707,10 +708,34 @@ def section_c2_f64(g, h32, args):
     a = torch.rand(E, H, 1, device="cuda", dtype=torch.float64, generator=gen)
     cold = ColdTimer(args.reps, 2)
     nbytes = 4 * (N + 1) + 8 * E + 8 * E * H * D + 8 * E * H + 8 * N * H * D
-    out = {"workload": "gspmm u_mul_e_sum, h (N, 8, 32) x a (E, 8, 1), float64, power-law graph",
+    el = torch.randn(N, H, 1, device="cuda", dtype=torch.float64, generator=gen)
+    er = torch.randn(N, H, 1, device="cuda", dtype=torch.float64, generator=gen)
+    logits = ops.u_add_v(g, el, er)
+    sddmm_bytes = 8 * E + 8 * E * H * 2 + 8 * E * H
+    soft_bytes = 4 * (N + 1) + 4 * E + 8 * E * H * 2
+    out = {"workload": "the GAT layer's ops in float64 (the reference's precision) on the "
+                       "power-law graph: gsddmm u_add_v, edge_softmax (E, 8, 1), gspmm "
+                       "u_mul_e_sum h (N, 8, 32) x a (E, 8, 1)",
            "num_nodes": N, "num_edges": E,
            "ops": {"gspmm_u_mul_e_sum": hbm_entry(cold(lambda: ops.u_mul_e_sum(g, h, a)), nbytes,
-                                                  E * H * D)}}
+                                                  E * H * D),
+                   "gsddmm_u_add_v": hbm_entry(cold(lambda: ops.u_add_v(g, el, er)), sddmm_bytes,
+                                               E * H),
+                   "edge_softmax": hbm_entry(cold(lambda: ops.edge_softmax(g, logits)),
+                                             soft_bytes, E * H)}}
+    del logits
+
+    def step(t):
+        e = ops.u_add_v(g, el, er)
+        torch.nn.functional.leaky_relu(e, 0.2, inplace=True)
+        return ops.u_mul_e_sum(g, h, ops.edge_softmax(g, e))
+
+    ms = run_steps(step, max(3, args.steps // 2), args.warmup, OpTimer())
+    units = E * H + E * H + E * H * D
+    out["step"] = {"ms": round(ms, 4), "GEdge_feat_s": round(units / (ms * 1e-3) / 1e9, 2),
+                   "note": "the headline step (gsddmm u_add_v, leaky_relu, edge_softmax, gspmm "
+                           "u_mul_e_sum) with float64 features, warm, as the headline"}
+    del el, er
     if not args.no_cpu_baseline:
         oracle, L, cores = oracle_setup()
         S, nnz, ip, src, eid = csr_sample(g, args.cpu_fraction)
