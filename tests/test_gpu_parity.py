@@ -110,6 +110,41 @@ def test_gspmm_feature_widths(d):
                                       err_msg="{} d={}".format(name, d))
 
 
+@pytest.mark.parametrize("longest", [600, 640, 641])
+def test_gspmm_rows_just_over_a_chunk(longest):
+    """With 512-slot chunks, rows of up to 640 slots stay whole when no row is
+    longer (sums then fold in CSR order, bit for bit the oracle's float32
+    fold); one row of 641 slots splits every row over 512 again."""
+    n = 300
+    deg = np.full(n, 20)
+    deg[[3, 50, 200]] = [513, 580, longest]
+    rng = np.random.default_rng(13)
+    v = np.repeat(np.arange(n), deg)
+    perm = rng.permutation(v.size)
+    v = v[perm]
+    u = rng.integers(0, n, v.size)
+    x = rng.normal(size=(n, 24)).astype(np.float32)
+    w = rng.random((v.size, 1)).astype(np.float32)
+    g = dgl.graph((u, v), num_nodes=n)
+    got = ops.u_mul_e_sum(g, x, w)
+    split = g._device_csr("in").chunks.num_chunks > 0
+    assert split == (longest > 640)
+    same = oracle.gspmm(u, v, n, "mul", "sum", x, w, np.float32)
+    if split:
+        whole = deg <= 512
+        np.testing.assert_array_equal(got[whole], same[whole])
+        ref64 = oracle.gspmm(u, v, n, "mul", "sum", x, w, np.float64)
+        bound = oracle.gspmm(u, v, n, "mul", "sum", np.abs(x), w, np.float64)
+        close(got, ref64, bound, np.float32, "split rows")
+    else:
+        np.testing.assert_array_equal(got, same)
+    gmax, (au, ae) = ops.spmm._gspmm(g, "mul", "max", x, w)
+    rmax, ru, re_ = oracle.gspmm(u, v, n, "mul", "max", x, w, np.float32, with_arg=True)
+    np.testing.assert_array_equal(gmax, rmax)
+    np.testing.assert_array_equal(au, ru)
+    np.testing.assert_array_equal(ae, re_)
+
+
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("d", [1, 4, 12, 32, 128, 256])
 @pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
