@@ -148,14 +148,18 @@ def test_gspmm_rows_just_over_a_chunk(longest):
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("d", [1, 4, 12, 32, 128, 256])
 @pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
-@pytest.mark.parametrize("csr_order", [False, True], ids=["edge-order", "csr-order"])
+@pytest.mark.parametrize("csr_order", ["no", "wide", "all"],
+                         ids=["edge-order", "csr-order-wide", "csr-order-all"])
 def test_gspmm_scalar_edge_operand(dtype, d, op, chunk_len, csr_order, monkeypatch):
     """One value per edge over every column of the node row (the GCN edge
     weight): loaded with the ids and broadcast across the lane group, for rows
     packed several to a wavefront and for whole-wavefront rows alike; with
-    `csr_order` whole-wavefront rows get the weight put in CSR slot order
-    first, as large graphs do."""
-    monkeypatch.setattr(ops.spmm, "CSR_ORDER_MIN_EDGES", 0 if csr_order else 1 << 62)
+    `csr_order` "wide" whole-wavefront rows get the weight put in CSR slot
+    order first (MDGL_RHS_CSR_ORDER), as large graphs do, with "all" every
+    width does (packed rows then read it by slot, as a C caller may ask)."""
+    monkeypatch.setattr(ops.spmm, "CSR_ORDER_MIN_EDGES", 1 << 62 if csr_order == "no" else 0)
+    if csr_order == "all":
+        monkeypatch.setattr(ops.spmm, "_slabs", lambda dout, dtype: 2)
     n, e = 400, 6000
     u, v = rand_graph(n, e, 11)
     v[:700] = 5  # a hub destination, split into chunks when chunk_len is set
