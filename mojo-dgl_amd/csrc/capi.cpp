@@ -515,6 +515,24 @@ int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* e
           : (dtype == MDGL_FLOAT32 && dout % 2 == 0 ? 2 : 1);
   p.lmode = op == OP_COPY_RHS ? M_CONTIG : pick_mode(p.bc, true, dout, p.vec, dl, lhs, es, lined);
   p.rmode = op == OP_COPY_LHS ? M_CONTIG : pick_mode(p.bc, false, dout, p.vec, dr, rhs, es);
+  // a lane whose columns straddle broadcast groups (heads of 2, 3, 6 columns
+  // ...) would gather element by element through the any-layout kernel;
+  // narrower lanes keep compile-time layouts (per-element offsets at one
+  // element per lane: on a 60M-edge graph, 48 columns as 8 heads of 6 with
+  // one weight per head, 12.0 -> 3.8 ms; 12 columns as 4 heads of 3, 7.4 -> 2.7 ms)
+  if (!dot_out && !lined && p.vec > 1 && (p.lmode == M_GATHER || p.rmode == M_GATHER)) {
+    for (int nv = p.vec / 2; nv >= 1; nv /= 2) {
+      if (nv > 1 && dout % nv != 0) continue;
+      const int lm = op == OP_COPY_RHS ? M_CONTIG : pick_mode(p.bc, true, dout, nv, dl, lhs, es);
+      const int rm = op == OP_COPY_LHS ? M_CONTIG : pick_mode(p.bc, false, dout, nv, dr, rhs, es);
+      if (lm != M_GATHER && rm != M_GATHER) {
+        p.vec = nv;
+        p.lmode = lm;
+        p.rmode = rm;
+        break;
+      }
+    }
+  }
   if (p.vec > 1 && dout % p.vec == 0 && aligned(dst, p.vec * es)) p.flags |= F_OUT_VEC;
   if (dot_out) {
     // the fused dot: mul / sum, 16-byte lanes, lhs rows contiguous, the edge
