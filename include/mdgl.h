@@ -144,6 +144,17 @@ int mdgl_gspmm(const int32_t* indptr, const int32_t* indices, const int32_t* eid
                const int32_t* heavy_ptr, int64_t num_heavy, void* workspace,
                int64_t workspace_bytes, int flags, int dtype, void* stream);
 
+/* The lane width (values per lane: 1, 2 or 4 in float32, 1 or 2 in
+ * float64) mdgl_gspmm picks for these operands, shapes, alignments and
+ * flags, so a caller can tell how many rows share a wavefront (a row takes
+ * ceil(dout / vec) lanes; 32 or fewer: several rows per wavefront) and how
+ * many 64-lane column slabs a row is cut into. No counterpart in the
+ * reference (its kernel is a CPU loop, src/ported.mojo:352-423); it is the
+ * planning query behind the host's scheduling choices for a gspmm call. */
+int mdgl_gspmm_lanes(int op, int64_t dl, int64_t dr, int64_t dout, int nd,
+                     const int64_t* lhs_shape, const int64_t* rhs_shape, const void* lhs,
+                     const void* rhs, int flags, int dtype, int64_t* vec);
+
 /* Workspace mdgl_gspmm needs for `num_chunks` chunk partials. */
 int64_t mdgl_gspmm_workspace_bytes(int64_t num_chunks, int64_t dout, int reduce_op, int dtype);
 

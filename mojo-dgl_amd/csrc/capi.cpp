@@ -399,6 +399,64 @@ int64_t mdgl_gspmm_workspace_bytes(int64_t num_chunks, int64_t dout, int reduce_
 
 namespace {
 
+// Lane width and operand load modes of a gspmm (p.bc and p.lstride set):
+// 16-byte lanes when the width allows (or the node rows are padded to
+// lines, so the last lane may read a whole vector of them), else 8-byte
+// lanes for even float32 widths, else one element per lane; a lane whose
+// columns straddle broadcast groups (heads of 2, 3, 6 columns ...) would
+// gather element by element through the any-layout kernel, so narrower
+// lanes keep compile-time layouts (per-element offsets at one element per
+// lane: on a 60M-edge graph, 48 columns as 8 heads of 6 with one weight per
+// head, 12.0 -> 3.8 ms; 12 columns as 4 heads of 3, 7.4 -> 2.7 ms).
+void choose_gspmm_lanes(GspmmParams& p, int op, int64_t dl, int64_t dr, int64_t dout,
+                        const void* lhs, const void* rhs, int64_t es, int dtype, bool dot) {
+  const int vw = vec_width(dtype);
+  const bool lined = p.lstride != dl;  // node rows on 128-byte lines
+  p.vec = (dout % vw == 0 || (lined && !dot)) ? vw
+          : (dtype == MDGL_FLOAT32 && dout % 2 == 0 ? 2 : 1);
+  p.lmode = op == OP_COPY_RHS ? M_CONTIG : pick_mode(p.bc, true, dout, p.vec, dl, lhs, es, lined);
+  p.rmode = op == OP_COPY_LHS ? M_CONTIG : pick_mode(p.bc, false, dout, p.vec, dr, rhs, es);
+  if (!dot && !lined && p.vec > 1 && (p.lmode == M_GATHER || p.rmode == M_GATHER)) {
+    for (int nv = p.vec / 2; nv >= 1; nv /= 2) {
+      if (nv > 1 && dout % nv != 0) continue;
+      const int lm = op == OP_COPY_RHS ? M_CONTIG : pick_mode(p.bc, true, dout, nv, dl, lhs, es);
+      const int rm = op == OP_COPY_LHS ? M_CONTIG : pick_mode(p.bc, false, dout, nv, dr, rhs, es);
+      if (lm != M_GATHER && rm != M_GATHER) {
+        p.vec = nv;
+        p.lmode = lm;
+        p.rmode = rm;
+        break;
+      }
+    }
+  }
+}
+
+// The broadcast descriptor of a gspmm's operands (copy ops and nd = 0: the
+// identity); 0 or a failure status.
+int gspmm_bcast(int op, int64_t dl, int64_t dr, int64_t dout, int nd, const int64_t* lhs_shape,
+                const int64_t* rhs_shape, Bcast* bc) {
+  if (op == OP_COPY_LHS || op == OP_COPY_RHS) {
+    const int64_t w = op == OP_COPY_LHS ? dl : dr;
+    if (dout != w) return fail(MDGL_EINVAL, "gspmm: copy output width %lld != operand width %lld",
+                               (long long)dout, (long long)w);
+    identity_bcast(dout, bc);
+  } else if (nd > 0) {
+    if (!lhs_shape || !rhs_shape) return fail(MDGL_EINVAL, "gspmm: null shape");
+    int64_t red, lw, rw, ow;
+    int rc = make_bcast(nd, lhs_shape, rhs_shape, false, bc, &red, &lw, &rw, &ow);
+    if (rc) return rc;
+    if (lw != dl || rw != dr || ow != dout)
+      return fail(MDGL_EINVAL, "gspmm: widths (%lld, %lld, %lld) do not match the shapes "
+                  "(%lld, %lld, %lld)", (long long)dl, (long long)dr, (long long)dout,
+                  (long long)lw, (long long)rw, (long long)ow);
+  } else {
+    if (dl != dr || dl != dout)
+      return fail(MDGL_EINVAL, "gspmm: without shapes dl, dr and dout must be equal");
+    identity_bcast(dout, bc);
+  }
+  return MDGL_OK;
+}
+
 // gspmm proper.
 int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
                  const void* lhs, const void* rhs, void* dst, int64_t num_dst, int op, int64_t dl,
@@ -446,26 +504,7 @@ int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* e
   p.arg_u = arg ? arg_u : nullptr;
   p.arg_e = arg ? arg_e : nullptr;
   p.stream = (hipStream_t)stream;
-  const bool copy = op == OP_COPY_LHS || op == OP_COPY_RHS;
-  if (copy) {
-    const int64_t w = op == OP_COPY_LHS ? dl : dr;
-    if (dout != w) return fail(MDGL_EINVAL, "gspmm: copy output width %lld != operand width %lld",
-                               (long long)dout, (long long)w);
-    identity_bcast(dout, &p.bc);
-  } else if (nd > 0) {
-    if (!lhs_shape || !rhs_shape) return fail(MDGL_EINVAL, "gspmm: null shape");
-    int64_t red, lw, rw, ow;
-    int rc = make_bcast(nd, lhs_shape, rhs_shape, false, &p.bc, &red, &lw, &rw, &ow);
-    if (rc) return rc;
-    if (lw != dl || rw != dr || ow != dout)
-      return fail(MDGL_EINVAL, "gspmm: widths (%lld, %lld, %lld) do not match the shapes "
-                  "(%lld, %lld, %lld)", (long long)dl, (long long)dr, (long long)dout,
-                  (long long)lw, (long long)rw, (long long)ow);
-  } else {
-    if (dl != dr || dl != dout)
-      return fail(MDGL_EINVAL, "gspmm: without shapes dl, dr and dout must be equal");
-    identity_bcast(dout, &p.bc);
-  }
+  if (int rc = gspmm_bcast(op, dl, dr, dout, nd, lhs_shape, rhs_shape, &p.bc)) return rc;
   if (num_dst == 0 || dout == 0) return MDGL_OK;
   if (!indptr || !dst) return fail(MDGL_EINVAL, "gspmm: null indptr or output");
   if (op != OP_COPY_LHS && !eid) return fail(MDGL_EINVAL, "gspmm: null eid");
@@ -507,32 +546,7 @@ int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* e
     p.lstride = (dl * es + 127) / 128 * 128 / es;
   }
   const int vw = vec_width(dtype);
-  const bool lined = p.lstride != dl;  // node rows on 128-byte lines
-  // 16-byte lanes when the width allows (or the node rows are padded to
-  // lines, so the last lane may read a whole vector of them), else 8-byte
-  // lanes for even float32 widths, else one element per lane
-  p.vec = (dout % vw == 0 || (lined && !dot_out)) ? vw
-          : (dtype == MDGL_FLOAT32 && dout % 2 == 0 ? 2 : 1);
-  p.lmode = op == OP_COPY_RHS ? M_CONTIG : pick_mode(p.bc, true, dout, p.vec, dl, lhs, es, lined);
-  p.rmode = op == OP_COPY_LHS ? M_CONTIG : pick_mode(p.bc, false, dout, p.vec, dr, rhs, es);
-  // a lane whose columns straddle broadcast groups (heads of 2, 3, 6 columns
-  // ...) would gather element by element through the any-layout kernel;
-  // narrower lanes keep compile-time layouts (per-element offsets at one
-  // element per lane: on a 60M-edge graph, 48 columns as 8 heads of 6 with
-  // one weight per head, 12.0 -> 3.8 ms; 12 columns as 4 heads of 3, 7.4 -> 2.7 ms)
-  if (!dot_out && !lined && p.vec > 1 && (p.lmode == M_GATHER || p.rmode == M_GATHER)) {
-    for (int nv = p.vec / 2; nv >= 1; nv /= 2) {
-      if (nv > 1 && dout % nv != 0) continue;
-      const int lm = op == OP_COPY_RHS ? M_CONTIG : pick_mode(p.bc, true, dout, nv, dl, lhs, es);
-      const int rm = op == OP_COPY_LHS ? M_CONTIG : pick_mode(p.bc, false, dout, nv, dr, rhs, es);
-      if (lm != M_GATHER && rm != M_GATHER) {
-        p.vec = nv;
-        p.lmode = lm;
-        p.rmode = rm;
-        break;
-      }
-    }
-  }
+  choose_gspmm_lanes(p, op, dl, dr, dout, lhs, rhs, es, dtype, dot_out != nullptr);
   if (p.vec > 1 && dout % p.vec == 0 && aligned(dst, p.vec * es)) p.flags |= F_OUT_VEC;
   if (dot_out) {
     // the fused dot: mul / sum, 16-byte lanes, lhs rows contiguous, the edge
@@ -587,6 +601,27 @@ int mdgl_gspmm(const int32_t* indptr, const int32_t* indices, const int32_t* eid
                       deg, nd, lhs_shape, rhs_shape, arg_u, arg_e, chunk_row, chunk_start,
                       num_chunks, chunk_len, heavy_rows, heavy_ptr, num_heavy, workspace,
                       workspace_bytes, flags, dtype, stream);
+}
+
+int mdgl_gspmm_lanes(int op, int64_t dl, int64_t dr, int64_t dout, int nd,
+                     const int64_t* lhs_shape, const int64_t* rhs_shape, const void* lhs,
+                     const void* rhs, int flags, int dtype, int64_t* vec) {
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "gspmm_lanes: bad dtype %d", dtype);
+  if (op < OP_ADD || op > OP_COPY_RHS || op == OP_DOT)
+    return fail(MDGL_EINVAL, "gspmm_lanes: bad op %d", op);
+  if (dl < 0 || dr < 0 || dout < 0 || !vec) return fail(MDGL_EINVAL, "gspmm_lanes: bad arguments");
+  GspmmParams p{};
+  if (int rc = gspmm_bcast(op, dl, dr, dout, nd, lhs_shape, rhs_shape, &p.bc)) return rc;
+  const int64_t es = dsize(dtype);
+  p.lstride = dl;
+  if ((flags & MDGL_LHS_LINE_ROWS) && op != OP_COPY_RHS) {
+    if (!aligned(lhs, 128))
+      return fail(MDGL_EINVAL, "gspmm_lanes: MDGL_LHS_LINE_ROWS needs lhs on a 128-byte boundary");
+    p.lstride = (dl * es + 127) / 128 * 128 / es;
+  }
+  choose_gspmm_lanes(p, op, dl, dr, dout, lhs, rhs, es, dtype, false);
+  *vec = p.vec;
+  return MDGL_OK;
 }
 
 int mdgl_gspmm_mul_sum_dot(const int32_t* indptr, const int32_t* indices, const int32_t* eid,

@@ -374,6 +374,7 @@ __global__ __launch_bounds__(BLOCK) void seg_softmax_stage_kernel(SegArgs<T> a) 
   // one array, so four workgroups fit a CU
   __shared__ __align__(16) T mx[WAVES_PER_BLOCK][SV];
   __shared__ unsigned char owner[WAVES_PER_BLOCK][CH];  // lane group of each window row
+  constexpr unsigned char NO_OWNER = 0xff;              // lane groups are 0 .. 63
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_BLOCK + w;
   const int64_t s0 = wave * a.P;
@@ -434,6 +435,10 @@ __global__ __launch_bounds__(BLOCK) void seg_softmax_stage_kernel(SegArgs<T> a) 
         if constexpr (VEC > 1) store_n<T, VEC>(&buf[w][(lane + i * WAVE) * VEC], st[i]);
         else buf[w][lane + i * WAVE] = st[i][0];
       }
+      // rows of the window start unowned; offsets that run backwards can
+      // leave rows inside [W, E) that no segment of this window claims, and
+      // passes 2 and 4 skip those rows
+      for (int r = lane; r < E - W; r += WAVE) owner[w][r] = NO_OWNER;
       wave_sync_lds();
       const bool mine = !done && lo >= W && hi <= E;
       int Wn, En;
@@ -463,8 +468,8 @@ __global__ __launch_bounds__(BLOCK) void seg_softmax_stage_kernel(SegArgs<T> a) 
 #pragma unroll 2
       for (int i = 0; i < PER; ++i) {
         const int c = lane + i * WAVE;
-        if (c < nch) {
-          const int r = c / nv, q = c - r * nv;
+        const int r = c / nv, q = c - r * nv;
+        if (c < nch && owner[w][r] != NO_OWNER) {
           const int ms = (owner[w][r] * nv + q) * VEC;
           T x[VEC];
           if constexpr (VEC > 1) load_n<T, VEC>(&buf[w][c * VEC], x);
@@ -498,8 +503,8 @@ __global__ __launch_bounds__(BLOCK) void seg_softmax_stage_kernel(SegArgs<T> a) 
 #pragma unroll 2
       for (int i = 0; i < PER; ++i) {
         const int c = lane + i * WAVE;
-        if (c < nch) {
-          const int r = c / nv, q = c - r * nv;
+        const int r = c / nv, q = c - r * nv;
+        if (c < nch && owner[w][r] != NO_OWNER) {
           const int ms = (owner[w][r] * nv + q) * VEC;
           T y[VEC];
           if constexpr (VEC > 1) load_n<T, VEC>(&buf[w][c * VEC], y);

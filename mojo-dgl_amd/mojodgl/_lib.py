@@ -78,6 +78,7 @@ _SIGNATURES = {
     "mdgl_gspmm": ([_P, _P, _P, _P, _P, _P, _I64, _C, _I64, _I64, _I64, _C, _P, _C, _P, _P, _P,
                     _P, _P, _P, _I64, _I32, _P, _P, _I64, _P, _I64, _C, _C, _P], _C),
     "mdgl_gspmm_workspace_bytes": ([_I64, _I64, _C, _C], _I64),
+    "mdgl_gspmm_lanes": ([_C, _I64, _I64, _I64, _C, _P, _P, _P, _P, _C, _C, _P], _C),
     "mdgl_gspmm_noalloc": ([_P, _P, _P, _P, _P, _P, _I64, _C, _I64, _I64, _I64, _C, _P, _C, _P, _P,
                             _P, _P, _P, _P, _I64, _I32, _P, _P, _I64, _C, _C, _P], _C),
     "mdgl_gspmm_mul_sum_dot": ([_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _C, _P,
@@ -153,6 +154,12 @@ def build(force: bool = False) -> str:
         cmd.insert(1, "-B")
     try:
         proc = subprocess.run(cmd, capture_output=True, text=True, timeout=1800)
+        if proc.returncode == 0 and not force and not is_current():
+            # make found every target newer than its prerequisites while the
+            # digest differs (a source deleted or renamed, or one restored
+            # with an older time): rebuild everything once
+            proc = subprocess.run(cmd[:1] + ["-B"] + cmd[1:], capture_output=True, text=True,
+                                  timeout=1800)
     except OSError as exc:  # no make
         raise BuildError("cannot run make: {}".format(exc)) from exc
     if proc.returncode != 0 or not is_current():

@@ -8,6 +8,7 @@ not produce (its kernel writes values only, src/ported.mojo:352-423).
 
 from __future__ import annotations
 
+import ctypes
 import sys
 
 import numpy as np
@@ -28,21 +29,18 @@ __all__ = ["gspmm"]
 CSR_ORDER_MIN_EDGES = 1 << 20
 
 
-def _packed(dout, dtype):
-    """Whether several rows share a wavefront: a row's lanes (by the lane
-    width rule of mdgl_gspmm below) number 32 or fewer."""
-    vw = 4 if dtype == np.float32 else 2
-    vec = vw if dout % vw == 0 else (2 if dtype == np.float32 and dout % 2 == 0 else 1)
-    return -(-dout // vec) <= 32
-
-
-def _slabs(dout, dtype):
-    """Column slabs of 64 lanes the kernel cuts an output row into (the lane
-    width rule of mdgl_gspmm: 16-byte lanes, else 8-byte for even float32
-    widths, else one element)."""
-    vw = 4 if dtype == np.float32 else 2
-    vec = vw if dout % vw == 0 else (2 if dtype == np.float32 and dout % 2 == 0 else 1)
-    return -(-(-(-dout // vec)) // 64)
+def _lanes(code, dl, dr, dout, nd, ls, rs, lhs, rhs, flags, dtype):
+    """(packed, slabs) of the lane layout mdgl_gspmm picks for these operands
+    (mdgl_gspmm_lanes): whether several rows share a wavefront (a row's
+    lanes number 32 or fewer) and how many 64-lane column slabs a row is cut
+    into."""
+    vec = ctypes.c_int64()
+    _lib.check(_lib.lib().mdgl_gspmm_lanes(
+        code, dl, dr, dout, nd, None if ls is None else ls.ctypes.data,
+        None if rs is None else rs.ctypes.data, _lib.ptr(lhs), _lib.ptr(rhs), flags,
+        _lib.dtype_code(dtype), ctypes.byref(vec)), "gspmm_lanes")
+    lanes = -(-dout // vec.value)
+    return lanes <= 32, -(-lanes // 64)
 
 
 def _line_rows(lhs, rows, dl, num_edges, dtype):
@@ -124,19 +122,18 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
         lhs = _lib.on_device(L, dtype) if L is not None else None
         rhs = _lib.on_device(R, dtype) if R is not None else None
         csr = g._device_csr(kind)
-        sched = csr.chunks
-        if narrow_split and _packed(dout, dtype) and narrow_split < sched.chunk_len:
-            sched = csr.chunks_for(narrow_split)
         flags = _lib.REPLACE_INF if replace_inf else 0
         if lhs is not None and code != OP_COPY_RHS:
             lined = _line_rows(lhs, lt.shape[0], dl, num_edges, dtype)
             if lined is not None:
                 lhs = lined
                 flags |= _lib.LHS_LINE_ROWS
+        packed, slabs = _lanes(code, dl, dr, dout, nd, ls, rs, lhs, rhs, flags, dtype)
+        sched = csr.chunks
+        if narrow_split and packed and narrow_split < sched.chunk_len:
+            sched = csr.chunks_for(narrow_split)
         if rhs is not None and code not in (OP_COPY_LHS, OP_COPY_RHS) and dr == 1 \
-                and num_edges and (_slabs(dout, dtype) > 1
-                                   or (not _packed(dout, dtype)
-                                       and num_edges >= CSR_ORDER_MIN_EDGES)):
+                and num_edges and (slabs > 1 or (not packed and num_edges >= CSR_ORDER_MIN_EDGES)):
             # a scalar edge operand read by several column slabs: put it in
             # CSR slot order once, so every slab streams it; also for rows of
             # one whole-wavefront slab, whose walk would otherwise wait on a

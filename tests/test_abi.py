@@ -46,6 +46,46 @@ def err(lib):
     return lib.mdgl_last_error().decode()
 
 
+def test_gspmm_lane_query(lib):
+    """mdgl_gspmm_lanes reports the lane width mdgl_gspmm launches with
+    (host pointers stand in: the query reads only their alignment)."""
+    import numpy as np
+    from mojodgl import _lib
+
+    buf = np.zeros(4096, dtype=np.float64)
+    base = (buf.ctypes.data + 255) // 256 * 256          # 256-byte aligned
+    mul, cl = _lib.BINARY_OPS["mul"], _lib.OP_COPY_LHS
+
+    def vec(op, dl, dr, dout, lshape=None, rshape=None, lhs=base, rhs=base, flags=0, dt=0):
+        out = ctypes.c_int64(-1)
+        nd = 0 if lshape is None else len(lshape)
+        ls = None if lshape is None else (ctypes.c_int64 * nd)(*lshape)
+        rs = None if rshape is None else (ctypes.c_int64 * nd)(*rshape)
+        rc = lib.mdgl_gspmm_lanes(op, dl, dr, dout, nd, ls, rs, lhs, rhs, flags, dt,
+                                  ctypes.byref(out))
+        assert rc == 0, err(lib)
+        return out.value
+
+    assert vec(cl, 64, 64, 64) == 4                      # 16-byte float32 lanes
+    assert vec(cl, 64, 64, 64, dt=1) == 2                # 16-byte float64 lanes
+    assert vec(cl, 602, 602, 602) == 2                   # even float32 width: 8-byte lanes
+    assert vec(cl, 601, 601, 601) == 1
+    assert vec(cl, 602, 602, 602, flags=_lib.LHS_LINE_ROWS) == 4   # rows padded to lines
+    assert vec(cl, 64, 64, 64, lhs=base + 4) == 1        # a misaligned node operand
+    # GAT heads: 8 heads of 32 columns, one weight per head: 16-byte lanes
+    assert vec(mul, 256, 8, 256, (8, 32), (8, 1)) == 4
+    # heads of 6 columns: 16-byte lanes would straddle heads, 8-byte ones do not
+    assert vec(mul, 48, 8, 48, (8, 6), (8, 1)) == 2
+    # heads of 3 columns: one element per lane
+    assert vec(mul, 12, 4, 12, (4, 3), (4, 1)) == 1
+    rc = lib.mdgl_gspmm_lanes(_lib.BINARY_OPS["dot"], 4, 4, 4, 0, None, None, base, base, 0, 0,
+                              ctypes.byref(ctypes.c_int64()))
+    assert rc == -1 and "op" in err(lib)
+    rc = lib.mdgl_gspmm_lanes(cl, 64, 64, 64, 0, None, None, base + 16, base,
+                              _lib.LHS_LINE_ROWS, 0, ctypes.byref(ctypes.c_int64()))
+    assert rc == -1 and "128-byte" in err(lib)
+
+
 def test_invalid_arguments_are_rejected_without_launching(lib):
     # bad op / reducer / dtype / target codes: negative status, named in the message
     rc = lib.mdgl_gspmm(None, None, None, None, None, None, 10, 4, 1, 1, 1, 0, None, 0, None,

@@ -159,7 +159,8 @@ def test_gspmm_scalar_edge_operand(dtype, d, op, chunk_len, csr_order, monkeypat
     width does (packed rows then read it by slot, as a C caller may ask)."""
     monkeypatch.setattr(ops.spmm, "CSR_ORDER_MIN_EDGES", 1 << 62 if csr_order == "no" else 0)
     if csr_order == "all":
-        monkeypatch.setattr(ops.spmm, "_slabs", lambda dout, dtype: 2)
+        lanes = ops.spmm._lanes
+        monkeypatch.setattr(ops.spmm, "_lanes", lambda *a: (lanes(*a)[0], 2))
     n, e = 400, 6000
     u, v = rand_graph(n, e, 11)
     v[:700] = 5  # a hub destination, split into chunks when chunk_len is set
@@ -630,9 +631,9 @@ def test_segment_offsets_through_the_abi(num):
 def test_wrapping_gpu_lengths_are_refused():
     """GPU lengths whose int64 sum wraps around to the row count: refused from
     the offsets' stats (a length above the row count) before any result is
-    returned. segment_softmax checks before its kernels run; segment_reduce
-    reads the checks back while its kernels run, which clamp every offset
-    into the rows."""
+    returned. Both segment_reduce and segment_softmax read the checks back
+    while their first kernels run (those clamp every offset into the rows
+    and skip rows that no segment claims) and raise before returning."""
     n = 4
     wrap = np.array([2 ** 62, 2 ** 62, 2 ** 62, 2 ** 62 + n], dtype=np.int64)
     assert int(wrap.sum()) == n  # numpy's int64 sum wraps too

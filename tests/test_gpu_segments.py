@@ -165,6 +165,36 @@ def test_segment_reduce_clamps_offsets_into_the_rows():
         np.testing.assert_array_equal(got[s], want, err_msg=str(s))
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("d", [1, 16])
+def test_segment_softmax_short_with_backward_offsets(dtype, d):
+    """Offsets that run backwards (only through the C ABI: GPU lengths are
+    checked after this call, and the API then raises) leave rows inside a
+    staged window that no segment claims: [10, 12, 0, 2, 2, 5] gives the
+    segments [10, 12), [0, 2) and [2, 5) in one window of rows [0, 12), with
+    rows 5-9 in none. Those rows, and the rows past the segments, are left as
+    they were; the claimed rows hold their segment's softmax."""
+    rng = np.random.default_rng(302 + d)
+    n = 40
+    value = rng.standard_normal((n, d)).astype(dtype)
+    raw = np.array([10, 12, 0, 2, 2, 5], dtype=np.int32)
+    off = torch.from_numpy(raw).cuda()
+    out = torch.full((n, d), 7.0, dtype=torch.float32 if dtype == np.float32 else torch.float64,
+                     device="cuda")
+    rc = _lib.lib().mdgl_segment_softmax_short(
+        off.data_ptr(), torch.from_numpy(value).cuda().data_ptr(), out.data_ptr(), raw.size - 1,
+        d, n, _lib.FLOAT32 if dtype == np.float32 else _lib.FLOAT64, _lib.stream())
+    _lib.check(rc, "segment_softmax_short")
+    got = out.cpu().numpy()
+    want = np.full((n, d), 7.0, dtype=dtype)
+    for lo, hi in ((10, 12), (0, 2), (2, 5)):
+        want[lo:hi] = oracle.segment_softmax(np.array([hi - lo]), value[lo:hi], dtype)
+    tol = 1e-6 if dtype == np.float32 else 1e-15
+    np.testing.assert_allclose(got, want, rtol=tol, atol=0)
+    np.testing.assert_array_equal(got[5:10], 7.0)
+    np.testing.assert_array_equal(got[12:], 7.0)
+
+
 @pytest.mark.parametrize("d", [3, 16, 40])
 def test_skip_long_then_long_only_equals_one_call(d):
     """MDGL_SEGMENTS_SKIP_LONG leaves the segments above the split threshold

@@ -356,6 +356,44 @@ def test_library_build_stamp_matches_the_sources():
         assert f.read().strip() == _lib._sources_digest()
 
 
+def test_stale_stamp_that_make_sees_as_current_rebuilds_everything(tmp_path):
+    """When make finds nothing out of date but the source digest differs (a
+    source deleted, renamed, or restored with an older time), build() runs
+    make once more with -B instead of failing with an empty log. `make` is
+    replaced on PATH by a stand-in that logs its arguments and, only under
+    -B, writes the library and its stamp."""
+    import os
+    import stat
+    import subprocess
+    import sys
+
+    pkg = os.path.dirname(os.path.dirname(dgl.__file__))
+    fake = tmp_path / "bin" / "make"
+    fake.parent.mkdir()
+    log = tmp_path / "make.log"
+    fake.write_text(
+        "#!{py}\nimport sys\nsys.path.insert(0, {pkg!r})\nfrom mojodgl import _lib\n"
+        "args = sys.argv[1:]\nopen({log!r}, 'a').write(' '.join(args) + '\\n')\n"
+        "out = [a[4:] for a in args if a.startswith('OUT=')][0]\n"
+        "if '-B' in args:\n"
+        "    open(out, 'w').write('lib')\n"
+        "    open(out + '.sources', 'w').write(_lib._sources_digest())\n".format(
+            py=sys.executable, pkg=pkg, log=str(log)))
+    fake.chmod(fake.stat().st_mode | stat.S_IEXEC)
+    target = tmp_path / "libmdgl.so"
+    target.write_text("old")
+    (tmp_path / "libmdgl.so.sources").write_text("a digest of other sources")
+    env = dict(os.environ, MOJODGL_LIB=str(target),
+               PATH=str(fake.parent) + os.pathsep + os.environ["PATH"])
+    code = ("import sys; sys.path.insert(0, {!r})\nfrom mojodgl import _lib\n"
+            "print(_lib.build() == {!r}, _lib.is_current())\n").format(pkg, str(target))
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                         timeout=120)
+    assert out.stdout.strip() == "True True", out.stdout + out.stderr
+    calls = log.read_text().splitlines()
+    assert len(calls) == 2 and "-B" not in calls[0].split() and "-B" in calls[1].split()
+
+
 def test_missing_library_at_mojodgl_lib_is_built_or_refused(tmp_path):
     """MOJODGL_LIB names the library (reference _lib.py:16); a missing one
     is built there on first use (_lib.py:116-124), and a failed build is a
