@@ -284,6 +284,39 @@ int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int3
                        const int32_t* slot_of_edge, int64_t num_edges, void* workspace,
                        int64_t workspace_bytes, int dtype, void* stream);
 
+/* edge_softmax over a subset of edge ids, the whole call on the GPU with no
+ * host read. Replaces the positional branch of the reference's host code
+ * (python/mojodgl/ops/edge_softmax.py:119-158, the per-call Python grouping
+ * loop before its mdgl_edge_softmax_ call, capi.mojo:149-165): position i
+ * (0 <= i < num_sel) of `eids` (device, int64) belongs to the group of node
+ * ends[eids[i]] (`ends`: device int32, the destination of every edge id for
+ * norm_by 'dst', the source for 'src'), groups in ascending node id with
+ * their positions in the order they appear, and reads logits[i]; dst rows
+ * 0 .. num_sel - 1 receive the softmax of their group per column (rows past
+ * num_sel are the caller's). Outputs for a backward pass: endpoint[i]
+ * (num_sel), the grouping group_ptr (num_nodes + 1) / group_pos (num_sel,
+ * positions grouped). id_range (device, 2 int64) receives the min and max of
+ * eids: ids outside [0, num_edges) are clamped for every read (no access is
+ * out of bounds) and make the results meaningless, so the caller checks
+ * id_range before using them; `range_event` (a hipEvent_t, nullable) is
+ * recorded on `stream` as soon as id_range is written, so the caller can copy
+ * it back without waiting for the rest of the call. Needs `workspace`
+ * (mdgl_edge_softmax_positional_workspace_bytes with the same d, buffers
+ * and dtype). */
+int mdgl_edge_softmax_positional(const int32_t* ends, int64_t num_edges, const int64_t* eids,
+                                 int64_t num_sel, int64_t num_nodes, const void* logits,
+                                 void* dst, int64_t d, int32_t* endpoint, int32_t* group_ptr,
+                                 int32_t* group_pos, int64_t* id_range, void* range_event,
+                                 void* workspace, int64_t workspace_bytes, int dtype,
+                                 void* stream);
+
+/* Workspace of mdgl_edge_softmax_positional (the logits and dst pointers
+ * decide the lane width, as for mdgl_softmax_geometry); -1 for invalid
+ * arguments. */
+int64_t mdgl_edge_softmax_positional_workspace_bytes(int64_t num_sel, int64_t num_nodes,
+                                                     int64_t d, const void* logits,
+                                                     const void* dst, int dtype);
+
 /* Replaces capi.mojo:141-145 (`mdgl_segment_mm`): out rows of segment r are
  * a[rows] @ b[r]; seglen_a (device, int64, r entries) sums to at most n and
  * rows past the sum are left as they are. Needs `workspace`

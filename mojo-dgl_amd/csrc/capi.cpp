@@ -905,6 +905,136 @@ int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int3
 
 namespace {
 
+// Workspace layout of mdgl_edge_softmax_positional (each part 256-byte
+// aligned): the launch figures, the row order, the packed position lists,
+// the chunk arrays, the chunk partials and the (max, sum) table by node, then
+// the plan's scratch.
+struct PosLayout {
+  int64_t dyn, order, packed, chunks, soft, scratch, total;
+};
+
+PosLayout pos_layout(int64_t num_sel, int64_t num_nodes, int64_t d, int dtype, int64_t max_chunks) {
+  auto al = [](int64_t b) { return (b + 255) / 256 * 256; };
+  PosLayout l{};
+  l.dyn = 0;
+  l.order = l.dyn + al(sizeof(SoftDyn));
+  l.packed = l.order + al(num_nodes * 4);
+  l.chunks = l.packed + al(2 * num_sel * 4);
+  l.soft = l.chunks + 3 * al(max_chunks * 4);
+  l.scratch = l.soft + al(mdgl_softmax_workspace_bytes(max_chunks, num_nodes, d, dtype));
+  l.total = l.scratch + al(positional_scratch_bytes(num_sel, num_nodes));
+  return l;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t mdgl_edge_softmax_positional_workspace_bytes(int64_t num_sel, int64_t num_nodes,
+                                                     int64_t d, const void* logits,
+                                                     const void* dst, int dtype) {
+  if (num_sel < 0 || num_nodes < 0 || d < 0 || !dtype_ok(dtype)) return -1;
+  if (num_sel == 0 || d == 0) return 0;
+  int vec;
+  int64_t slots, chunk_len;
+  softmax_geom(d, dtype, logits, dst, &vec, &slots, &chunk_len);
+  return pos_layout(num_sel, num_nodes, d, dtype, positional_max_chunks(num_sel, chunk_len)).total;
+}
+
+int mdgl_edge_softmax_positional(const int32_t* ends, int64_t num_edges, const int64_t* eids,
+                                 int64_t num_sel, int64_t num_nodes, const void* logits,
+                                 void* dst, int64_t d, int32_t* endpoint, int32_t* group_ptr,
+                                 int32_t* group_pos, int64_t* id_range, void* range_event,
+                                 void* workspace, int64_t workspace_bytes, int dtype,
+                                 void* stream) {
+  const char* what = "edge_softmax_positional";
+  if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "%s: bad dtype %d", what, dtype);
+  if (num_edges < 0 || num_sel < 0 || num_nodes < 0 || d < 0)
+    return fail(MDGL_EINVAL, "%s: negative size", what);
+  if (num_edges >= (int64_t(1) << 31) || num_sel >= (int64_t(1) << 31) ||
+      num_nodes >= (int64_t(1) << 31))
+    return fail(MDGL_EINVAL, "%s: 2**31 or more edges, positions or nodes", what);
+  if (!row_widths_fit(d, dsize(dtype))) return fail(MDGL_EINVAL, "%s: rows too wide", what);
+  if (num_sel == 0 || d == 0) return MDGL_OK;
+  if (num_edges == 0 || num_nodes == 0)
+    return fail(MDGL_EINVAL, "%s: %lld edge ids selected from a graph without edges", what,
+                (long long)num_sel);
+  if (!ends || !eids || !logits || !dst || !endpoint || !group_ptr || !group_pos || !id_range)
+    return fail(MDGL_EINVAL, "%s: null buffer", what);
+  SoftmaxParams p{};
+  int64_t slots, chunk_len;
+  softmax_geom(d, dtype, logits, dst, &p.vec, &slots, &chunk_len);
+  const int64_t max_chunks = positional_max_chunks(num_sel, chunk_len);
+  const PosLayout l = pos_layout(num_sel, num_nodes, d, dtype, max_chunks);
+  if (!aligned(workspace, WS_ALIGN))
+    return fail(MDGL_EINVAL, "workspace must be %lld-byte aligned", (long long)WS_ALIGN);
+  if (!workspace || workspace_bytes < l.total)
+    return fail(MDGL_EWORKSPACE, "%s: workspace of %lld bytes needed, %lld given", what,
+                (long long)l.total, (long long)workspace_bytes);
+  char* w = static_cast<char*>(workspace);
+  int nbins = 0;
+  while ((int64_t(1) << nbins) < slots) ++nbins;
+  ++nbins;
+  const int64_t nvec = (d + p.vec - 1) / p.vec;
+  int L = 1;
+  while (L < nvec && L < WAVE) L <<= 1;
+  PositionalPlan pp{};
+  pp.ends = ends;
+  pp.num_edges = num_edges;
+  pp.eids = eids;
+  pp.num_sel = num_sel;
+  pp.num_nodes = num_nodes;
+  pp.slots = (int)slots;
+  pp.chunk_len = (int)chunk_len;
+  pp.nbins = nbins;
+  pp.Pw = WAVE / L;
+  pp.S = (int)((nvec + L - 1) / L);
+  pp.endpoint = endpoint;
+  pp.group_ptr = group_ptr;
+  pp.group_pos = group_pos;
+  pp.id_range = id_range;
+  pp.order = reinterpret_cast<int32_t*>(w + l.order);
+  pp.packed = reinterpret_cast<int32_t*>(w + l.packed);
+  const int64_t cstride = (max_chunks * 4 + 255) / 256 * 256;
+  pp.chunk_row = reinterpret_cast<int32_t*>(w + l.chunks);
+  pp.chunk_start = reinterpret_cast<int32_t*>(w + l.chunks + cstride);
+  pp.chunk_first = reinterpret_cast<int32_t*>(w + l.chunks + 2 * cstride);
+  pp.max_chunks = max_chunks;
+  pp.dyn = reinterpret_cast<SoftDyn*>(w + l.dyn);
+  pp.scratch = w + l.scratch;
+  pp.range_event = (hipEvent_t)range_event;
+  const hipStream_t st = (hipStream_t)stream;
+  hipError_t e = launch_positional_plan(pp, st);
+  if (e != hipSuccess) return hip_status(e, what);
+  p.indptr = group_ptr;
+  p.eid = group_pos;
+  p.logits = logits;
+  p.out = dst;
+  p.num_rows = num_nodes;
+  p.d = d;
+  p.num_slots = num_sel;
+  p.order = pp.order;
+  p.nbins = nbins;
+  p.packed_eid = pp.packed;
+  p.num_chunks = max_chunks;
+  p.chunk_row = pp.chunk_row;
+  p.chunk_start = pp.chunk_start;
+  p.chunk_first = pp.chunk_first;
+  p.part = w + l.soft;
+  p.table = w + l.soft + ((2 * max_chunks * d * dsize(dtype) + 255) / 256) * 256;
+  p.row_of = endpoint;
+  p.num_edges = num_sel;
+  p.row_slots = 1;
+  p.dyn = pp.dyn;
+  p.stream = st;
+  e = dtype == MDGL_FLOAT32 ? launch_softmax<float>(p) : launch_softmax<double>(p);
+  return hip_status(e, what);
+}
+
+}  // extern "C"
+
+namespace {
+
 constexpr int64_t MAX_GATHER_BLOCKS = 2048;  // bucketing keeps 5 * r ints in LDS
 
 int grouped_common(const void* a, const void* b, void* dst, const int64_t* idx_b,

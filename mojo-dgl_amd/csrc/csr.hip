@@ -76,15 +76,49 @@ __global__ __launch_bounds__(BLOCK) void radix_colscan_kernel(int32_t* __restric
 // Stable scatter of chunk b: key i goes to digit_start[d] + counts[b][d] +
 // (keys of digit d before it in the chunk). vals_in null means the edge ids
 // 0..n-1 (the first pass).
+//
+// Wavefront w owns the chunk's quarter [w * Q, (w + 1) * Q) (Q = RADIX_PER *
+// 64 keys) and loads it at once, RADIX_PER keys per lane (coalesced rows of
+// 64). It ranks its keys in order, 64 at a time, with ballots (lanes whose
+// digit agrees bit by bit) and a per-wavefront digit cursor in LDS, with no
+// workgroup barrier. One barrier later each digit's count per wavefront is
+// known: the chunk's keys are placed in LDS in digit order (digit, then
+// wavefront, then rank: the input order within a digit), and the workgroup
+// writes them out from there in that order, so each digit's keys leave as one
+// contiguous run instead of single scattered elements.
+constexpr int RADIX_PER = RADIX_CHUNK / BLOCK;  // keys per lane
+static_assert(RADIX_PER * BLOCK == RADIX_CHUNK, "a chunk is RADIX_PER keys per lane");
+
 __global__ __launch_bounds__(BLOCK) void radix_scatter_kernel(
     const int32_t* __restrict__ keys_in, const int32_t* __restrict__ vals_in,
     int32_t* __restrict__ keys_out, int32_t* __restrict__ vals_out,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ totals, int64_t n,
     int shift) {
-  __shared__ int32_t cursor[RADIX];
-  __shared__ int32_t wcount[WAVES_PER_BLOCK][RADIX];
   __shared__ int32_t scan[RADIX];
+  __shared__ int32_t cur[WAVES_PER_BLOCK][RADIX];  // per wavefront: keys of each digit so far
+  __shared__ int32_t gbase[RADIX];                 // output index of sorted slot 0 of digit d
+  __shared__ int32_t skey[RADIX_CHUNK];
+  __shared__ int32_t sval[RADIX_CHUNK];
   const int t = threadIdx.x;
+  const int lane = t & (WAVE - 1), w = t >> 6;
+  const uint64_t below = lane ? (~uint64_t(0) >> (64 - lane)) : 0;
+  const int64_t lo = (int64_t)blockIdx.x * RADIX_CHUNK;
+  const int nk = (int)(n - lo < RADIX_CHUNK ? n - lo : RADIX_CHUNK);
+  // this wavefront's keys: row j of its quarter is keys [q0 + 64 j, q0 + 64 j + 64)
+  const int q0 = w * (RADIX_PER * WAVE);
+  int32_t key[RADIX_PER], val[RADIX_PER];
+#pragma unroll
+  for (int j = 0; j < RADIX_PER; ++j) {
+    const int i = q0 + j * WAVE + lane;
+    key[j] = 0;
+    val[j] = 0;
+    if (i < nk) {
+      key[j] = keys_in[lo + i];
+      val[j] = vals_in ? vals_in[lo + i] : (int32_t)(lo + i);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < WAVES_PER_BLOCK; ++q) cur[q][t] = 0;
   // digit starts: exclusive scan of the totals
   scan[t] = totals[t];
   __syncthreads();
@@ -94,45 +128,72 @@ __global__ __launch_bounds__(BLOCK) void radix_scatter_kernel(
     scan[t] += add;
     __syncthreads();
   }
-  cursor[t] = scan[t] - totals[t] + counts[blockIdx.x * RADIX + t];
-  const int lane = t & (WAVE - 1), w = t >> 6;
-  const uint64_t below = lane ? (~uint64_t(0) >> (64 - lane)) : 0;
-  const int64_t lo = (int64_t)blockIdx.x * RADIX_CHUNK;
-  const int64_t hi = lo + RADIX_CHUNK < n ? lo + RADIX_CHUNK : n;
-  __syncthreads();
-  for (int64_t base = lo; base < hi; base += BLOCK) {
+  const int32_t dstart = scan[t] - totals[t] + counts[blockIdx.x * RADIX + t];
+  // rank within the wavefront, in input order
+  int32_t rank[RADIX_PER];
 #pragma unroll
-    for (int q = 0; q < WAVES_PER_BLOCK; ++q) wcount[q][t] = 0;
-    __syncthreads();
-    const int64_t i = base + t;
-    const bool ok = i < hi;
-    int32_t key = 0, val = 0;
-    if (ok) {
-      key = keys_in[i];
-      val = vals_in ? vals_in[i] : (int32_t)i;
-    }
-    const int dg = digit_of(key, shift);
+  for (int j = 0; j < RADIX_PER; ++j) {
+    const bool ok = q0 + j * WAVE + lane < nk;
+    const int dg = digit_of(key[j], shift);
     uint64_t same = __ballot(ok);
 #pragma unroll
     for (int bit = 0; bit < 8; ++bit) {
       const uint64_t ones = __ballot(ok && ((dg >> bit) & 1));
       same &= ((dg >> bit) & 1) ? ones : ~ones;  // lanes whose digit agrees on this bit
     }
-    const int rank = __popcll(same & below);
-    if (ok && rank == 0) wcount[w][dg] = __popcll(same);
-    __syncthreads();
-    if (ok) {
-      int32_t pos = cursor[dg] + rank;
-      for (int q = 0; q < w; ++q) pos += wcount[q][dg];
-      keys_out[pos] = key;
-      vals_out[pos] = val;
-    }
-    __syncthreads();
-    int32_t add = 0;
+    const int r = __popcll(same & below);
+    const int32_t base = ok ? cur[w][dg] : 0;
+    rank[j] = base + r;
+    __builtin_amdgcn_wave_barrier();
+    if (ok && r == 0) cur[w][dg] = base + __popcll(same);
+    __builtin_amdgcn_wave_barrier();
+  }
+  __syncthreads();
+  // digit t: its keys per wavefront -> the slots of each wavefront's run in
+  // the chunk's digit order, and where the digit's run goes in the output
+  int32_t c[WAVES_PER_BLOCK];
+  int32_t tot = 0;
 #pragma unroll
-    for (int q = 0; q < WAVES_PER_BLOCK; ++q) add += wcount[q][t];
-    cursor[t] += add;
+  for (int q = 0; q < WAVES_PER_BLOCK; ++q) {
+    c[q] = cur[q][t];
+    tot += c[q];
+  }
+  __syncthreads();
+  scan[t] = tot;
+  __syncthreads();
+  for (int off = 1; off < RADIX; off <<= 1) {
+    const int32_t add = t >= off ? scan[t - off] : 0;
     __syncthreads();
+    scan[t] += add;
+    __syncthreads();
+  }
+  const int32_t lstart = scan[t] - tot;  // first slot of digit t in the chunk's digit order
+  int32_t run = lstart;
+#pragma unroll
+  for (int q = 0; q < WAVES_PER_BLOCK; ++q) {
+    cur[q][t] = run;  // now: the first slot of wavefront q's keys of digit t
+    run += c[q];
+  }
+  gbase[t] = dstart - lstart;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < RADIX_PER; ++j) {
+    if (q0 + j * WAVE + lane < nk) {
+      const int s = cur[w][digit_of(key[j], shift)] + rank[j];
+      skey[s] = key[j];
+      sval[s] = val[j];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < RADIX_PER; ++j) {
+    const int s = j * BLOCK + t;
+    if (s < nk) {
+      const int32_t k = skey[s];
+      const int32_t pos = gbase[digit_of(k, shift)] + s;
+      keys_out[pos] = k;
+      vals_out[pos] = sval[s];
+    }
   }
 }
 

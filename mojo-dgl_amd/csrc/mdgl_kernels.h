@@ -119,6 +119,22 @@ hipError_t launch_gsddmm(const GsddmmParams& p);
 // the chunk length come as chunks (chunk_row / chunk_start / chunk_first)
 // whose partials live in `part` (2 * num_chunks * d values).
 constexpr int SOFT_CPL = 8;  // logits cached per lane in a wavefront row of the softmax
+constexpr int SOFT_MAX_BINS = 7;  // packed degree bins: 1 .. 64 slots per wavefront
+constexpr int SOFT_PK_U = 4;      // packed wavefronts served per wavefront of the packed launch
+
+// A softmax plan's launch figures kept in device memory (a plan built on the
+// GPU, whose sizes the host never reads): the kernels of such a launch take
+// their bin bounds and work counts from here and walk their work with a
+// fixed grid.
+struct SoftDyn {
+  int64_t bin_start[SOFT_MAX_BINS + 1];  // packed bin k: order[bin_start[k] .. bin_start[k+1])
+  int64_t bin_wave[SOFT_MAX_BINS + 1];   // packed wavefronts before bin k
+  int64_t bin_slot[SOFT_MAX_BINS + 1];   // packed edge-list entries before bin k
+  int64_t mid_start, mid_end;            // wavefront rows: order[mid_start .. mid_end)
+  int64_t light_waves;                   // wavefronts of those rows (slabs included)
+  int64_t packed_tasks;                  // wavefronts of the packed launch
+  int64_t num_chunks, chunk_waves;       // chunks of the long rows, their wavefronts
+};
 
 struct SoftmaxParams {
   const int32_t* indptr;
@@ -145,6 +161,13 @@ struct SoftmaxParams {
   const int32_t* row_of;
   int64_t num_edges;
   void* table;
+  // the table is indexed by row id (row_of then holds each edge's row), not
+  // by position in the row order
+  int row_slots;
+  // a plan built on the GPU: its figures (SoftDyn) in device memory, `order`,
+  // the packed list and the chunk arrays device-resident and sized for
+  // `num_chunks` chunks at most (the partials too); `bounds` unused
+  const SoftDyn* dyn;
   hipStream_t stream;
 };
 
@@ -217,6 +240,34 @@ hipError_t launch_build_csr(const int32_t* key, const int32_t* other, int64_t nu
                             int64_t num_rows, int32_t* indptr, int32_t* indices, int32_t* eid,
                             void* workspace, hipStream_t stream);
 hipError_t launch_cumsum_i64(const int64_t* src, int64_t* dst, int64_t n, hipStream_t s);
+// The positional edge_softmax plan built on the GPU (softmax_plan.hip):
+// positions grouped by the endpoint of their edge, rows binned by degree,
+// chunks of the long rows, the packed edge lists and the SoftDyn figures.
+struct PositionalPlan {
+  const int32_t* ends;   // endpoint of every edge id
+  int64_t num_edges;
+  const int64_t* eids;   // the selected edge id of every position
+  int64_t num_sel, num_nodes;
+  int slots, chunk_len, nbins, S, Pw;
+  // outputs
+  int32_t* endpoint;     // [num_sel] endpoint of each position
+  int32_t* group_ptr;    // [num_nodes + 1]
+  int32_t* group_pos;    // [num_sel] positions grouped by endpoint
+  int64_t* id_range;     // [2] min and max of eids
+  hipEvent_t range_event;  // recorded once id_range is written (nullable)
+  // plan arrays (workspace)
+  int32_t* order;        // [num_nodes]
+  int32_t* packed;       // [2 * num_sel]
+  int32_t* chunk_row;    // [max_chunks] x3
+  int32_t* chunk_start;
+  int32_t* chunk_first;
+  int64_t max_chunks;
+  SoftDyn* dyn;
+  void* scratch;         // positional_scratch_bytes(num_sel, num_nodes)
+};
+int64_t positional_max_chunks(int64_t num_sel, int64_t chunk_len);
+int64_t positional_scratch_bytes(int64_t num_sel, int64_t num_nodes);
+hipError_t launch_positional_plan(const PositionalPlan& p, hipStream_t s);
 int64_t segment_offsets_workspace_bytes(int64_t num);
 hipError_t launch_segment_offsets(const int64_t* len, int64_t num, int64_t chunk_len,
                                   int32_t* offsets, int64_t* stats, void* ws, hipStream_t s);

@@ -73,6 +73,8 @@ struct SoftmaxArgs {
   int mode2;  // launch 2: the chunk write pass
   T* tab;     // two-pass form: [slots][2][d] (max, sum), else null
   int64_t hub_base;  // table slot of the first chunked row (ordered plans)
+  int row_slots;     // table slot = row id (else the order position / hub slot)
+  const SoftDyn* dyn;  // device plan: figures in device memory (DYN kernels)
 };
 
 __device__ __forceinline__ float exp_t(float x) { return expf(x); }
@@ -253,77 +255,133 @@ __device__ __forceinline__ void soft_group(const SoftmaxArgs<T>& a, int mode, bo
 // (one slot per edge, fewer registers) in another.
 enum { PART_WIDE = 1, PART_PACKED = 2 };
 
-constexpr int PK_U = 4;  // packed wavefronts per wavefront of the packed launch
+constexpr int PK_U = SOFT_PK_U;
 
-template <class T, int VEC>
+// Figures of the plan: kernel arguments, or device memory for a plan built
+// on the GPU (DYN).
+template <bool DYN, class T>
+__device__ __forceinline__ int64_t bin_start_of(const SoftmaxArgs<T>& a, int k) {
+  if constexpr (DYN) return a.dyn->bin_start[k];
+  else return a.bin_start[k];
+}
+template <bool DYN, class T>
+__device__ __forceinline__ int64_t bin_wave_of(const SoftmaxArgs<T>& a, int k) {
+  if constexpr (DYN) return a.dyn->bin_wave[k];
+  else return a.bin_wave[k];
+}
+template <bool DYN, class T>
+__device__ __forceinline__ int64_t bin_slot_of(const SoftmaxArgs<T>& a, int k) {
+  if constexpr (DYN) return a.dyn->bin_slot[k];
+  else return a.bin_slot[k];
+}
+
+template <class T, int VEC, bool DYN>
 __device__ __forceinline__ void softmax_packed_u(const SoftmaxArgs<T>& a, int64_t w, int lane);
 
-template <class T, int VEC, int PART>
+// Wavefront w of the chunks: chunk w / S, column slab w % S (statistics in
+// launch 1, the write in launch 2).
+template <class T, int VEC>
+__device__ __forceinline__ void softmax_chunk_task(const SoftmaxArgs<T>& a, int64_t w, int lane) {
+  const int64_t chunk = w / a.S, slab = w % a.S;
+  // two-pass merge: the first chunk of each row writes the row's table entry
+  if (a.mode2 && a.tab && a.chunk_first[chunk] != chunk) return;
+  const int64_t row = a.chunk_row[chunk];
+  const int start = a.chunk_start[chunk];
+  const int end = a.indptr[row + 1];
+  const int stop = end - start > a.chunk_len ? start + a.chunk_len : end;
+  // table slot of a chunked row: after the ordered rows, at its first chunk
+  // (or the row itself)
+  const int64_t slot = a.order && !a.row_slots ? a.hub_base + chunk : row;
+  soft_group<T, VEC, SOFT_CPL>(a, a.mode2 ? SM_WRITE : SM_STATS, true, slot, start, stop, a.Pw,
+                               slab, lane, chunk);
+}
+
+// Wavefront w of the wavefront rows (rows of up to chunk_len edges).
+template <class T, int VEC, bool DYN>
+__device__ __forceinline__ void softmax_light_task(const SoftmaxArgs<T>& a, int64_t w, int lane) {
+  const int Pw = a.Pw;
+  const int R = a.nat_r;
+  int64_t mid_start, mid_end;
+  if constexpr (DYN) {
+    mid_start = a.dyn->mid_start;
+    mid_end = a.dyn->mid_end;
+  } else {
+    mid_start = a.mid_start;
+    mid_end = a.mid_end;
+  }
+  const int64_t nmid = ((mid_end - mid_start + R - 1) / R) * a.S;
+  if (w >= nmid) return;
+  // R consecutive rows per wavefront (R = 1 with a row order): they share
+  // it, Pw / R slots each, when the longest of them fits those slots' CPL
+  // rounds; otherwise each takes the whole wavefront in turn (the choice
+  // is uniform per wavefront)
+  const int64_t slab = w % a.S;
+  const int64_t i0 = mid_start + (w / a.S) * R;
+  int Pr = Pw, iters = R;
+  if (R > 1) {
+    const int64_t i = i0 + (lane / a.L) / (Pw / R);
+    const int deg = i < mid_end ? a.indptr[i + 1] - a.indptr[i] : 0;
+    if (wave_max_int(deg) <= (Pw / R) * SOFT_CPL) {
+      Pr = Pw / R;
+      iters = 1;
+    }
+  }
+  for (int r = 0; r < iters; ++r) {
+    if (iters > 1 && i0 + r >= mid_end) break;  // uniform
+    const int64_t i = iters == 1 ? i0 + (lane / a.L) / Pr : i0 + r;
+    const bool in = i < mid_end;
+    const int64_t row = a.order ? (in ? (int64_t)a.order[i] : 0) : i;
+    int start = 0, stop = 0;
+    if (in) {
+      start = a.indptr[row];
+      stop = a.indptr[row + 1];
+    }
+    const bool ok = in && stop > start && stop - start <= a.chunk_len;
+    soft_group<T, VEC, SOFT_CPL>(a, SM_FULL, ok, a.order && !a.row_slots ? i : row, start, stop,
+                                 Pr, slab, lane, 0);
+  }
+}
+
+template <class T, int VEC, int PART, bool DYN>
 __global__ __launch_bounds__(BLOCK) void softmax_kernel(SoftmaxArgs<T> a) {
   const int lane = threadIdx.x & (WAVE - 1);
-  const int64_t b = blockIdx.x;
-  const int Pw = a.Pw;
-  if constexpr (PART == PART_PACKED) {
-    // packed rows only (their own launch: one slot per edge, few registers)
-    const int64_t lb = xcd_remap(b, a.light_blocks);
+  if constexpr (DYN) {
+    // a plan built on the GPU: the work counts are in device memory, and a
+    // fixed grid walks the work (every wavefront's loop bound is uniform)
+    const int64_t stride = (int64_t)gridDim.x * WAVES_PER_BLOCK;
+    const int64_t w0 = (int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
+    if constexpr (PART == PART_PACKED) {
+      const int64_t tasks = a.dyn->packed_tasks;
+      for (int64_t w = w0; w < tasks; w += stride) softmax_packed_u<T, VEC, true>(a, w, lane);
+    } else {
+      const int64_t cw = a.dyn->chunk_waves;
+      const int64_t total = a.mode2 ? cw : cw + a.dyn->light_waves;
+      for (int64_t w = w0; w < total; w += stride) {
+        if (w < cw) softmax_chunk_task<T, VEC>(a, w, lane);
+        else softmax_light_task<T, VEC, true>(a, w - cw, lane);
+      }
+    }
+    return;
+  } else {
+    const int64_t b = blockIdx.x;
+    if constexpr (PART == PART_PACKED) {
+      // packed rows only (their own launch: one slot per edge, few registers)
+      const int64_t lb = xcd_remap(b, a.light_blocks);
+      const int64_t w = lb * WAVES_PER_BLOCK + (threadIdx.x >> 6);
+      if (w * PK_U >= a.light_waves) return;  // uniform per wavefront
+      softmax_packed_u<T, VEC, false>(a, w, lane);
+      return;
+    }
+    if (b < a.chunk_blocks) {
+      const int64_t w = b * WAVES_PER_BLOCK + (threadIdx.x >> 6);
+      if (w >= a.chunk_waves) return;
+      softmax_chunk_task<T, VEC>(a, w, lane);
+      return;
+    }
+    const int64_t lb = xcd_remap(b - a.chunk_blocks, a.light_blocks);
     const int64_t w = lb * WAVES_PER_BLOCK + (threadIdx.x >> 6);
-    if (w * PK_U >= a.light_waves) return;  // uniform per wavefront
-    softmax_packed_u<T, VEC>(a, w, lane);
-    return;
-  }
-  if (b < a.chunk_blocks) {
-    // chunks of the long rows (statistics in launch 1, the write in launch 2)
-    const int64_t w = b * WAVES_PER_BLOCK + (threadIdx.x >> 6);
-    if (w >= a.chunk_waves) return;
-    const int64_t chunk = w / a.S, slab = w % a.S;
-    // two-pass merge: the first chunk of each row writes the row's table entry
-    if (a.mode2 && a.tab && a.chunk_first[chunk] != chunk) return;
-    const int64_t row = a.chunk_row[chunk];
-    const int start = a.chunk_start[chunk];
-    const int end = a.indptr[row + 1];
-    const int stop = end - start > a.chunk_len ? start + a.chunk_len : end;
-    // table slot of a chunked row: after the ordered rows, at its first chunk
-    const int64_t slot = a.order ? a.hub_base + chunk : row;
-    soft_group<T, VEC, SOFT_CPL>(a, a.mode2 ? SM_WRITE : SM_STATS, true, slot, start, stop, Pw,
-                                 slab, lane, chunk);
-    return;
-  }
-  const int64_t lb = xcd_remap(b - a.chunk_blocks, a.light_blocks);
-  const int64_t w = lb * WAVES_PER_BLOCK + (threadIdx.x >> 6);
-  if (w >= a.light_waves) return;
-  const int R = a.nat_r;
-  const int64_t nmid = ((a.mid_end - a.mid_start + R - 1) / R) * a.S;
-  if (w < nmid) {
-    // R consecutive rows per wavefront (R = 1 with a row order): they share
-    // it, Pw / R slots each, when the longest of them fits those slots' CPL
-    // rounds; otherwise each takes the whole wavefront in turn (the choice
-    // is uniform per wavefront)
-    const int64_t slab = w % a.S;
-    const int64_t i0 = a.mid_start + (w / a.S) * R;
-    int Pr = Pw, iters = R;
-    if (R > 1) {
-      const int64_t i = i0 + (lane / a.L) / (Pw / R);
-      const int deg = i < a.mid_end ? a.indptr[i + 1] - a.indptr[i] : 0;
-      if (wave_max_int(deg) <= (Pw / R) * SOFT_CPL) {
-        Pr = Pw / R;
-        iters = 1;
-      }
-    }
-    for (int r = 0; r < iters; ++r) {
-      if (iters > 1 && i0 + r >= a.mid_end) break;  // uniform
-      const int64_t i = iters == 1 ? i0 + (lane / a.L) / Pr : i0 + r;
-      const bool in = i < a.mid_end;
-      const int64_t row = a.order ? (in ? (int64_t)a.order[i] : 0) : i;
-      int start = 0, stop = 0;
-      if (in) {
-        start = a.indptr[row];
-        stop = a.indptr[row + 1];
-      }
-      const bool ok = in && stop > start && stop - start <= a.chunk_len;
-      soft_group<T, VEC, SOFT_CPL>(a, SM_FULL, ok, a.order ? i : row, start, stop, Pr, slab,
-                                   lane, 0);
-    }
-    return;
+    if (w >= a.light_waves) return;
+    softmax_light_task<T, VEC, false>(a, w, lane);
   }
 }
 
@@ -331,7 +389,7 @@ __global__ __launch_bounds__(BLOCK) void softmax_kernel(SoftmaxArgs<T> a) {
 // wavefronts' rows, walking the chain order -> indptr -> eid -> logits for
 // all of them at once, so every dependent load has PK_U requests per lane in
 // flight instead of one.
-template <class T, int VEC>
+template <class T, int VEC, bool DYN>
 __device__ __forceinline__ void softmax_packed_u(const SoftmaxArgs<T>& a, int64_t w, int lane) {
   const int L = a.L, Pw = a.Pw;
   const int c = lane % L;
@@ -339,19 +397,20 @@ __device__ __forceinline__ void softmax_packed_u(const SoftmaxArgs<T>& a, int64_
   // this wavefront lie in one bin k (found once, uniform)
   const int64_t pw0 = w * PK_U;
   int k = 0;
-  while (k + 1 < a.nbins && a.bin_wave[k + 1] <= pw0) ++k;
+  while (k + 1 < a.nbins && bin_wave_of<DYN>(a, k + 1) <= pw0) ++k;
   const int Pr = 1 << k;
   const int per = Pw / Pr;
   const int span = L * Pr;
   const int sl = (lane / L) % Pr;
-  const int64_t b0 = a.bin_start[k], b1 = a.bin_start[k + 1];
+  const int64_t b0 = bin_start_of<DYN>(a, k), b1 = bin_start_of<DYN>(a, k + 1);
+  const int64_t bw = bin_wave_of<DYN>(a, k);
   // indices are clamped into the bin (and rows have >= 1 edge), so every
   // load below is unconditional and in bounds; rok / ok mask the results
   int64_t slab[PK_U], ic[PK_U];
   bool rok[PK_U];
 #pragma unroll
   for (int r = 0; r < PK_U; ++r) {
-    const int64_t local = pw0 + r - a.bin_wave[k];
+    const int64_t local = pw0 + r - bw;
     slab[r] = local % a.S;
     const int64_t i = b0 + (local / a.S) * per + lane / (Pr * L);
     rok[r] = i < b1;
@@ -363,9 +422,10 @@ __device__ __forceinline__ void softmax_packed_u(const SoftmaxArgs<T>& a, int64_
     // the plan lists every packed slot's edge id: one coalesced load per
     // round instead of the chain order -> indptr -> eid (-1 past a row's
     // degree; those lanes read edge 0, which exists, and are masked)
+    const int64_t bs = bin_slot_of<DYN>(a, k);
 #pragma unroll
     for (int r = 0; r < PK_U; ++r) {
-      const int32_t pe = a.peid[a.bin_slot[k] + (ic[r] - b0) * Pr + sl];
+      const int32_t pe = a.peid[bs + (ic[r] - b0) * Pr + sl];
       ok[r] = rok[r] && pe >= 0;
       e[r] = pe >= 0 ? (int64_t)pe : 0;
     }
@@ -421,8 +481,9 @@ __device__ __forceinline__ void softmax_packed_u(const SoftmaxArgs<T>& a, int64_
     if (a.tab) {
       if (rok[r] && sl == 0) {
         // slot = position in the row order: a wavefront's rows write
-        // consecutive table rows (whole lines)
-        T* t = a.tab + ic[r] * 2 * a.d;
+        // consecutive table rows (whole lines); or the row id
+        const int64_t slot = a.row_slots ? (int64_t)a.order[ic[r]] : ic[r];
+        T* t = a.tab + slot * 2 * a.d;
         store_cols<T, VEC>(t, k0, a.d, a.vec_io, m);
         store_cols<T, VEC>(t + a.d, k0, a.d, a.vec_io, sum);
       }
@@ -471,6 +532,67 @@ __global__ __launch_bounds__(BLOCK) void softmax_edge_kernel(const T* __restrict
   }
 }
 
+// The edge-parallel write of the two-pass form over p.num_edges edges.
+template <class T, int VEC>
+hipError_t launch_softmax_edges(const SoftmaxParams& p, const SoftmaxArgs<T>& a) {
+  const int64_t waves = ((p.num_edges + (WAVE / a.L) - 1) / (WAVE / a.L)) * a.S;
+  const int64_t nb = (waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
+  hipLaunchKernelGGL((softmax_edge_kernel<T, VEC>), dim3((unsigned)nb), dim3(BLOCK), 0, p.stream,
+                     a.logits, a.out, a.tab, p.row_of, a.mask, p.num_edges, p.d, a.L, a.S,
+                     a.vec_io, nb);
+  return hipGetLastError();
+}
+
+// Workgroups of a launch that walks device-counted work: 8 per CU (32
+// wavefronts, the residency the kernels reach), fewer when the work cannot
+// fill them.
+constexpr int64_t DYN_BLOCKS = 256 * 8;
+
+// A plan built on the GPU (p.dyn): the same three launches, on fixed grids
+// whose wavefronts walk the work the device figures count; the chunk write
+// pass is always launched (it finds no chunks when there are none).
+template <class T, int VEC>
+hipError_t launch_softmax_dyn(const SoftmaxParams& p, SoftmaxArgs<T> a) {
+  a.nbins = p.nbins;
+  a.peid = p.packed_eid;
+  a.nat_r = 1;
+  a.num_chunks = p.num_chunks;  // capacity: the partials are laid out for it
+  a.chunk_row = p.chunk_row;
+  a.chunk_start = p.chunk_start;
+  a.chunk_first = p.chunk_first;
+  a.pm = static_cast<T*>(p.part);
+  a.ps = a.pm ? a.pm + p.num_chunks * p.d : nullptr;
+  a.tab = static_cast<T*>(p.table);
+  a.hub_base = 0;
+  auto grid = [](int64_t waves) {
+    const int64_t b = (waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
+    return (unsigned)(b < 1 ? 1 : (b > DYN_BLOCKS ? DYN_BLOCKS : b));
+  };
+  // upper bounds of the work, only to keep tiny plans from launching the
+  // full grid: every row is packed, a wavefront row, or chunked
+  const int64_t rows = p.num_rows, edges = p.num_slots;
+  const int64_t wide = (p.num_chunks + rows) * a.S;
+  const int64_t packed = (2 * edges / a.Pw + p.nbins + 1) * a.S / PK_U + p.nbins + 1;
+  a.mode2 = 0;
+  hipLaunchKernelGGL((softmax_kernel<T, VEC, PART_WIDE, true>), dim3(grid(wide)), dim3(BLOCK), 0,
+                     p.stream, a);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL((softmax_kernel<T, VEC, PART_PACKED, true>), dim3(grid(packed)), dim3(BLOCK),
+                     0, p.stream, a);
+  err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  if (p.num_chunks > 0) {
+    a.mode2 = 1;
+    hipLaunchKernelGGL((softmax_kernel<T, VEC, PART_WIDE, true>),
+                       dim3(grid(p.num_chunks * a.S)), dim3(BLOCK), 0, p.stream, a);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  if (a.tab && p.num_edges > 0) return launch_softmax_edges<T, VEC>(p, a);
+  return hipSuccess;
+}
+
 template <class T, int VEC>
 hipError_t launch_softmax_vec(const SoftmaxParams& p) {
   SoftmaxArgs<T> a{};
@@ -491,6 +613,9 @@ hipError_t launch_softmax_vec(const SoftmaxParams& p) {
   a.chunk_len = SOFT_CPL * a.Pw;
   a.order = p.order;
   a.nbins = 0;
+  a.row_slots = p.row_slots;
+  a.dyn = p.dyn;
+  if (p.dyn) return launch_softmax_dyn<T, VEC>(p, a);
   int64_t waves = 0;
   if (p.order) {
     a.nbins = p.nbins;
@@ -542,8 +667,8 @@ hipError_t launch_softmax_vec(const SoftmaxParams& p) {
   // chunks and wavefront rows, then the packed rows in a launch of their own
   const int64_t blocks = a.chunk_blocks + a.light_blocks;
   if (blocks > 0) {
-    hipLaunchKernelGGL((softmax_kernel<T, VEC, PART_WIDE>), dim3((unsigned)blocks), dim3(BLOCK), 0,
-                       p.stream, a);
+    hipLaunchKernelGGL((softmax_kernel<T, VEC, PART_WIDE, false>), dim3((unsigned)blocks),
+                       dim3(BLOCK), 0, p.stream, a);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
@@ -552,8 +677,8 @@ hipError_t launch_softmax_vec(const SoftmaxParams& p) {
     b.light_waves = packed_waves;
     const int64_t pk_waves = (packed_waves + PK_U - 1) / PK_U;
     b.light_blocks = (pk_waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
-    hipLaunchKernelGGL((softmax_kernel<T, VEC, PART_PACKED>), dim3((unsigned)b.light_blocks),
-                       dim3(BLOCK), 0, p.stream, b);
+    hipLaunchKernelGGL((softmax_kernel<T, VEC, PART_PACKED, false>),
+                       dim3((unsigned)b.light_blocks), dim3(BLOCK), 0, p.stream, b);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
@@ -561,19 +686,12 @@ hipError_t launch_softmax_vec(const SoftmaxParams& p) {
     a.mode2 = 1;
     a.light_waves = 0;
     a.light_blocks = 0;
-    hipLaunchKernelGGL((softmax_kernel<T, VEC, PART_WIDE>), dim3((unsigned)a.chunk_blocks),
+    hipLaunchKernelGGL((softmax_kernel<T, VEC, PART_WIDE, false>), dim3((unsigned)a.chunk_blocks),
                        dim3(BLOCK), 0, p.stream, a);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
-  if (a.tab && p.num_edges > 0) {
-    const int64_t waves = ((p.num_edges + (WAVE / L) - 1) / (WAVE / L)) * a.S;
-    const int64_t nb = (waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
-    hipLaunchKernelGGL((softmax_edge_kernel<T, VEC>), dim3((unsigned)nb), dim3(BLOCK), 0,
-                       p.stream, a.logits, a.out, a.tab, p.row_of, a.mask, p.num_edges, p.d, L,
-                       a.S, a.vec_io, nb);
-    return hipGetLastError();
-  }
+  if (a.tab && p.num_edges > 0) return launch_softmax_edges<T, VEC>(p, a);
   return hipSuccess;
 }
 

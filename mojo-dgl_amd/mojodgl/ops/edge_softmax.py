@@ -4,9 +4,10 @@ Same arguments, shapes and errors as the reference, including its positional
 `eids` rule (edge_softmax.py:119-158): with a subset `eids`, the positions of
 `eids` are grouped by endpoint (groups in ascending endpoint id, positions in
 the order they appear), position i reads `logits[i]`, and the result is as
-long as `logits` with rows past len(eids) zero. The grouping is one stable
-radix grouping on the GPU (mdgl_build_csr) instead of a Python loop; logits
-keep float32/float64.
+long as `logits` with rows past len(eids) zero. The grouping (a stable radix
+grouping), the softmax plan and the softmax run in one library call on the
+GPU (mdgl_edge_softmax_positional) instead of a Python loop; logits keep
+float32/float64.
 """
 
 from __future__ import annotations
@@ -14,7 +15,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from .. import _lib, heterograph
+from .. import _lib
 from ..base import ALL, DGLError, is_all
 from . import _autograd, _plan
 
@@ -85,18 +86,16 @@ def _edge_softmax(graph, logits, eids, norm_by, keep=None):
     if norm_by not in ("dst", "src"):
         raise DGLError("norm_by must be 'src' or 'dst'")
     num_nodes = graph.number_of_nodes()
+    on_gpu = False
     if is_all(eids):
         order = None
     else:
-        # GPU ids are checked on the GPU (one small read back), host ids on
-        # the host before any GPU work
+        # host ids are checked on the host before any GPU work; GPU ids by
+        # the library, whose id range is read back as soon as it is known
         on_gpu = isinstance(eids, torch.Tensor) and eids.device.type == "cuda"
         order = _lib.i64_device(eids).reshape(-1) if on_gpu else _lib.i64(eids).reshape(-1)
-        if order.shape[0]:
-            if on_gpu:
-                lo, hi = torch.stack((order.min(), order.max())).tolist()
-            else:
-                lo, hi = int(order.min()), int(order.max())
+        if order.shape[0] and not on_gpu:
+            lo, hi = int(order.min()), int(order.max())
             if lo < 0 or hi >= num_edges:
                 raise DGLError("edge ids must be in [0, {}), got [{}, {})".format(
                     num_edges, lo, hi + 1))
@@ -113,39 +112,67 @@ def _edge_softmax(graph, logits, eids, norm_by, keep=None):
     # row is written; a subset leaves the rows past len(eids) at zero
     alloc = torch.empty if order is None else torch.zeros
     out = alloc((out_len, d), dtype=_lib.torch_dtype(dtype), device=gdev)
-    if out_len and d:
+    if out_len and d and order is not None:
+        m = order.shape[0]
+        if m:
+            if on_gpu and num_edges == 0:
+                raise DGLError("edge ids must be in [0, 0), got {} ids".format(m))
+            lg = _lib.on_device(X, dtype).reshape(out_len, d)
+            _positional(graph, lg, out, order, m, norm_by, on_gpu, keep)
+    elif out_len and d:
         lg = _lib.on_device(X, dtype).reshape(out_len, d)
-        if order is not None:
-            lg = lg[: order.shape[0]].contiguous()
         slots, chunk_len = _plan.geometry(d, dtype, lg, out)
-        if order is None:
-            csr = graph._device_csr("in" if norm_by == "dst" else "out")
-            indptr, eid, rows = csr.indptr, csr.eid, num_nodes
-            plan = csr.softmax_plan(slots, chunk_len)
-        else:
-            # positions grouped by (endpoint, appearance): the stable grouping
-            # of the selected edges' endpoints, on the GPU; rows are all nodes
-            # (the ones no selected edge reaches are empty and skipped)
-            uids, vids = graph._device_coo()
-            idx = order if isinstance(order, torch.Tensor) else torch.from_numpy(order).to(gdev)
-            endpoint = (vids if norm_by == "dst" else uids)[idx]
-            indptr, _, eid = heterograph.build_device_csr(endpoint, None, num_nodes)
-            if keep is not None:
-                keep.update(endpoint=endpoint, indptr=indptr, eid=eid)
-            rows = num_nodes if idx.shape[0] else 0
-            plan = _plan.SoftmaxPlan.from_device(indptr, slots, chunk_len, ordered=True,
-                                                 eid=eid)
-        if rows:
-            n_edges = lg.shape[0]
+        csr = graph._device_csr("in" if norm_by == "dst" else "out")
+        plan = csr.softmax_plan(slots, chunk_len)
+        if num_nodes:
             # the second, edge-parallel pass writes the output in edge-id
             # order from the (max, sum) table slot of each edge's row
-            row_of = plan.slot_of_edge
             ws, nbytes = _plan.workspace(plan, d, dtype, plan.table_rows)
             rc = _lib.lib().mdgl_edge_softmax_(
-                indptr.data_ptr(), None, eid.data_ptr(), None, lg.data_ptr(), out.data_ptr(), None,
-                rows, 1, d, _lib.ptr(plan.order), plan.bounds_ptr(), plan.nbins,
-                _lib.ptr(plan.packed), _lib.ptr(plan.chunk_row), _lib.ptr(plan.chunk_start), _lib.ptr(plan.chunk_first),
-                plan.num_chunks, plan.slots, _lib.ptr(row_of), n_edges, _lib.ptr(ws), nbytes,
+                csr.indptr.data_ptr(), None, csr.eid.data_ptr(), None, lg.data_ptr(),
+                out.data_ptr(), None, num_nodes, 1, d, _lib.ptr(plan.order), plan.bounds_ptr(),
+                plan.nbins, _lib.ptr(plan.packed), _lib.ptr(plan.chunk_row),
+                _lib.ptr(plan.chunk_start), _lib.ptr(plan.chunk_first), plan.num_chunks,
+                plan.slots, _lib.ptr(plan.slot_of_edge), lg.shape[0], _lib.ptr(ws), nbytes,
                 _lib.dtype_code(dtype), _lib.stream())
             _lib.check(rc, "edge_softmax")
     return _lib.give_back(out.reshape(shape), X.is_torch, X.device)
+
+
+def _positional(graph, lg, out, order, m, norm_by, on_gpu, keep):
+    """The positional rule in one library call (mdgl_edge_softmax_positional):
+    positions grouped by the endpoint of their edge on the GPU, the softmax
+    plan built there too, no host read in between. GPU ids are checked from
+    the id range the call writes first, copied back while the rest runs."""
+    gdev = lg.device
+    num_nodes = graph.number_of_nodes()
+    d = lg.shape[1]
+    code = _lib.dtype_code(np.float32 if lg.dtype == torch.float32 else np.float64)
+    uids, vids = graph._device_coo()
+    ends = vids if norm_by == "dst" else uids
+    idx = order if isinstance(order, torch.Tensor) else torch.from_numpy(order).to(gdev)
+    endpoint = torch.empty(m, dtype=torch.int32, device=gdev)
+    group_ptr = torch.empty(num_nodes + 1, dtype=torch.int32, device=gdev)
+    group_pos = torch.empty(m, dtype=torch.int32, device=gdev)
+    id_range = torch.empty(2, dtype=torch.int64, device=gdev)
+    L = _lib.lib()
+    nbytes = L.mdgl_edge_softmax_positional_workspace_bytes(m, num_nodes, d, lg.data_ptr(),
+                                                            out.data_ptr(), code)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=gdev)
+    ranged = None
+    if on_gpu:
+        ranged = torch.cuda.Event()
+        ranged.record()  # creates the event; the call records it again once the range is known
+    rc = L.mdgl_edge_softmax_positional(
+        ends.data_ptr(), ends.shape[0], idx.data_ptr(), m, num_nodes, lg.data_ptr(),
+        out.data_ptr(), d, endpoint.data_ptr(), group_ptr.data_ptr(), group_pos.data_ptr(),
+        id_range.data_ptr(), ranged.cuda_event if ranged is not None else None, ws.data_ptr(),
+        nbytes, code, _lib.stream())
+    _lib.check(rc, "edge_softmax")
+    if ranged is not None:
+        lo, hi = _lib.Readback(id_range, "eids_range", after=ranged).values()
+        if lo < 0 or hi >= ends.shape[0]:
+            raise DGLError("edge ids must be in [0, {}), got [{}, {})".format(
+                ends.shape[0], lo, hi + 1))
+    if keep is not None:
+        keep.update(endpoint=endpoint, indptr=group_ptr, eid=group_pos)

@@ -453,6 +453,92 @@ def test_edge_softmax_positional_eids_large_and_on_the_gpu(norm_by):
         ops.edge_softmax(g, logits, eids=torch.tensor([0, e], device="cuda"), norm_by=norm_by)
 
 
+def _positional_abi(ends, eids, n, logits, dtype):
+    """mdgl_edge_softmax_positional on GPU copies; numpy results (out,
+    endpoint, group_ptr, group_pos, id_range) after waiting on the range
+    event the call records."""
+    from mojodgl import _lib
+
+    m, d = eids.size, logits.shape[1]
+    tdt = torch.float32 if dtype == np.float32 else torch.float64
+    et = torch.from_numpy(ends.astype(np.int32)).cuda()
+    it = torch.from_numpy(eids.astype(np.int64)).cuda()
+    lg = torch.from_numpy(logits).cuda()
+    out = torch.zeros((m, d), dtype=tdt, device="cuda")
+    endpoint = torch.empty(m, dtype=torch.int32, device="cuda")
+    gptr = torch.empty(n + 1, dtype=torch.int32, device="cuda")
+    gpos = torch.empty(m, dtype=torch.int32, device="cuda")
+    rng_ = torch.empty(2, dtype=torch.int64, device="cuda")
+    code = _lib.dtype_code(dtype)
+    L = _lib.lib()
+    nbytes = L.mdgl_edge_softmax_positional_workspace_bytes(m, n, d, lg.data_ptr(),
+                                                            out.data_ptr(), code)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
+    ev = torch.cuda.Event()
+    ev.record()
+    rc = L.mdgl_edge_softmax_positional(et.data_ptr(), ends.size, it.data_ptr(), m, n,
+                                        lg.data_ptr(), out.data_ptr(), d, endpoint.data_ptr(),
+                                        gptr.data_ptr(), gpos.data_ptr(), rng_.data_ptr(),
+                                        ev.cuda_event, ws.data_ptr(), nbytes, code,
+                                        _lib.stream())
+    _lib.check(rc, "edge_softmax_positional")
+    ev.synchronize()
+    id_range = rng_.cpu().numpy()
+    torch.cuda.synchronize()
+    return (out.cpu().numpy(), endpoint.cpu().numpy(), gptr.cpu().numpy(), gpos.cpu().numpy(),
+            id_range)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("case", ["mixed", "all-chunked", "all-packed", "one-node", "wide"])
+def test_edge_softmax_positional_through_the_abi(dtype, case):
+    """The library's positional call: endpoint[i] = ends[eids[i]], the
+    grouping equals numpy's stable argsort of the endpoints (group_ptr from
+    bincount), id_range the ids' min and max (read once the range event has
+    fired), and the softmax the oracle's positional rule; plans with every
+    row chunked, every row packed, a single node, and rows wider than one
+    64-lane slab (the device figures then hold empty bins)."""
+    rng = np.random.default_rng(49)
+    n, e, d = {"mixed": (3000, 50000, 8), "all-chunked": (4, 50000, 1),
+               "all-packed": (5000, 6000, 4), "one-node": (1, 3000, 3),
+               "wide": (500, 20000, 300)}[case]
+    u, v = rng.integers(0, n, e), rng.integers(0, n, e)
+    if case == "mixed":
+        v[:6000] = 17
+    if case == "all-packed":
+        v = np.arange(e) % n  # degrees of 1 and 2 only
+    m = int(0.7 * e)
+    eids = rng.choice(e, size=m, replace=True)
+    logits = (rng.normal(size=(m, d)) * 2).astype(dtype)
+    out, endpoint, gptr, gpos, id_range = _positional_abi(v, eids, n, logits, dtype)
+    np.testing.assert_array_equal(endpoint, v[eids])
+    np.testing.assert_array_equal(gpos, np.argsort(v[eids], kind="stable"))
+    np.testing.assert_array_equal(gptr, np.concatenate([[0], np.cumsum(np.bincount(
+        v[eids], minlength=n))]))
+    assert list(id_range) == [eids.min(), eids.max()]
+    full = np.zeros((e, d), dtype=dtype)
+    full[:m] = logits
+    ref = oracle.edge_softmax(u, v, n, full, eids=eids, norm_by="dst")[:m]
+    close(out, ref, ref, dtype, "positional " + case)
+    again = _positional_abi(v, eids, n, logits, dtype)[0]
+    np.testing.assert_array_equal(out, again)
+
+
+def test_edge_softmax_positional_clamps_ids_outside_the_edges():
+    """Ids outside [0, E) (the API refuses them from id_range) are clamped
+    for every read: the call completes and reports their true range."""
+    rng = np.random.default_rng(50)
+    n, e = 100, 2000
+    v = rng.integers(0, n, e)
+    eids = rng.integers(0, e, 500)
+    eids[[3, 77]] = [-5, e + 40]
+    logits = rng.normal(size=(500, 2)).astype(np.float32)
+    out, endpoint, gptr, gpos, id_range = _positional_abi(v, eids, n, logits, np.float32)
+    assert list(id_range) == [-5, e + 40]
+    np.testing.assert_array_equal(endpoint, v[np.clip(eids, 0, e - 1)])
+    assert np.isfinite(out).all()
+
+
 @pytest.mark.parametrize("slots,chunk_len", [(16, 128), (64, 512), (1, 8)])
 def test_softmax_plan_built_on_the_gpu_equals_the_host_plan(slots, chunk_len):
     from mojodgl.ops import _plan
