@@ -52,13 +52,26 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 MFMA_F32_PEAK_TFLOPS = 157.3
 MFMA_F64_PEAK_TFLOPS = 78.6
-# HBM bytes per launch of the gspmm kernel on the headline workload, from
-# rocprofv3 FETCH_SIZE / WRITE_SIZE scaled by a 1 GiB copy
-GSPMM_TRAFFIC_BYTES = 72.35e9
-GSPMM_TRAFFIC_SOURCE = ("profiles/gat_power_law_kernels.md (rocprofv3 FETCH_SIZE and WRITE_SIZE "
-                        "of one launch, each scaled by the counter's reading for a 1 GiB copy); "
-                        "not measured in this run")
 FLUSH_BYTES = 512 << 20
+# Fabric read requests leave the L2 as 32-, 64- or 128-byte transactions. On
+# this GPU the 128-byte count (TCC_BUBBLE) reads 0, which makes FETCH_SIZE
+# report half of a plain copy; the bytes are therefore formed from the total
+# and the 32- and 64-byte counts (a 1 GiB copy reads 8.39M requests = 1 GiB).
+# Writes are 32- or 64-byte transactions (WRITE_SIZE's own formula).
+READ_COUNTERS = ("TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum")
+WRITE_COUNTERS = ("TCC_EA0_WRREQ_sum", "TCC_EA0_WRREQ_64B_sum")
+
+
+def read_bytes(c):
+    """Fabric read bytes from the request counts (READ_COUNTERS)."""
+    total, r32, r64 = (c.get(k, 0.0) for k in READ_COUNTERS)
+    return 128.0 * (total - r32 - r64) + 64.0 * r64 + 32.0 * r32
+
+
+def write_bytes(c):
+    """Fabric write bytes from the transaction counts (WRITE_COUNTERS)."""
+    total, w64 = (c.get(k, 0.0) for k in WRITE_COUNTERS)
+    return 32.0 * (total - w64) + 64.0 * w64
 
 
 def log(*a):
@@ -101,6 +114,97 @@ def community_graph(seed=2, blocks=50, per_block=4_600, e=114_000_000, intra=0.9
     v = np.concatenate([b + rng.integers(0, per_block, e_in), rng.integers(0, n, e - e_in)])
     perm = rng.permutation(e)
     return u[perm], v[perm], n
+
+
+# ---------------------------------------------------------------- counters
+TRAFFIC_CALLS = 3
+
+
+def workload_gspmm_traffic(args):
+    """The headline graph's gspmm u_mul_e_sum, TRAFFIC_CALLS calls and nothing
+    else of the library: run under rocprofv3 --pmc by measure_traffic."""
+    import torch
+
+    import mojodgl as dgl
+    import mojodgl.ops as ops
+
+    N, E, H, D = args.nodes, args.edges, 8, 32
+    u, v, _ = power_law_graph(1, N, E)
+    g = dgl.graph((u, v), num_nodes=N)
+    g._device_csr("in")
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    h = torch.randn(N, H, D, device="cuda", generator=gen)
+    a = torch.rand(E, H, 1, device="cuda", generator=gen)
+    torch.cuda.synchronize()
+    for _ in range(TRAFFIC_CALLS):
+        ops.u_mul_e_sum(g, h, a)
+    torch.cuda.synchronize()
+    return {"calls": TRAFFIC_CALLS}
+
+
+def pmc_totals(db_path, kernel_substr):
+    """{counter: sum over the dispatches of kernels whose name holds
+    kernel_substr} from a rocprofv3 database, and the dispatch count."""
+    import sqlite3
+
+    con = sqlite3.connect(db_path)
+    sums, disp = {}, set()
+    for d, name, cname, val in con.execute(
+            "select dispatch_id, kernel_name, counter_name, value from counters_collection"):
+        if kernel_substr in name:
+            sums[cname] = sums.get(cname, 0.0) + float(val)
+            disp.add(d)
+    con.close()
+    return sums, len(disp)
+
+
+def measure_traffic(args):
+    """Fabric bytes per gspmm u_mul_e_sum call on the headline graph, live:
+    two child runs of this script (--workload gspmm_traffic) under
+    rocprofv3 --pmc, one per counter group, each under its own time limit
+    (the whole process group is killed past it). Started before this process
+    touches the GPU. Returns the traffic entry, with the reason when a pass
+    fails (then no bytes)."""
+    import shutil
+    import signal
+    import subprocess
+    import tempfile
+
+    exe = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    tmp = tempfile.mkdtemp(prefix="mdgl_traffic_")
+    totals, dispatches = {}, {}
+    for name, counters in (("read", READ_COUNTERS), ("write", WRITE_COUNTERS)):
+        cmd = [exe, "--pmc", *counters, "--kernel-include-regex", "gspmm_kernel", "-d", tmp,
+               "-o", name, "--", sys.executable, os.path.abspath(__file__), "--workload",
+               "gspmm_traffic", "--nodes", str(args.nodes), "--edges", str(args.edges)]
+        log("rocprofv3 pass ({}): {}".format(name, " ".join(counters)))
+        proc = subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True,
+                                start_new_session=True)
+        try:
+            out, err = proc.communicate(timeout=args.traffic_timeout)
+        except subprocess.TimeoutExpired:
+            os.killpg(proc.pid, signal.SIGKILL)
+            proc.communicate()
+            return {"bytes": None, "reason": "rocprofv3 pass {} passed {} s".format(
+                name, args.traffic_timeout)}
+        db = os.path.join(tmp, name + "_results.db")
+        if '"calls"' not in out or not os.path.exists(db):
+            return {"bytes": None, "reason": "rocprofv3 pass {} ended with status {}: {}".format(
+                name, proc.returncode, (err or out).strip()[-300:])}
+        sums, nd = pmc_totals(db, "gspmm_kernel")
+        totals.update(sums)
+        dispatches[name] = nd
+    rd, wr = read_bytes(totals), write_bytes(totals)
+    shutil.rmtree(tmp, ignore_errors=True)
+    return {"bytes": round((rd + wr) / TRAFFIC_CALLS), "read_bytes": round(rd / TRAFFIC_CALLS),
+            "write_bytes": round(wr / TRAFFIC_CALLS),
+            "requests": {k: round(v / TRAFFIC_CALLS) for k, v in totals.items()},
+            "gspmm_kernel_dispatches_per_call": dispatches["read"] / TRAFFIC_CALLS,
+            "source": "this run: rocprofv3 --pmc {} and {} over {} calls of gspmm u_mul_e_sum on "
+                      "the same graph in a child process; bytes = 128 x (requests - 32B - 64B) + "
+                      "64 x 64B + 32 x 32B reads, 32 x (transactions - 64B) + 64 x 64B "
+                      "writes".format(" ".join(READ_COUNTERS), " ".join(WRITE_COUNTERS),
+                                      TRAFFIC_CALLS)}
 
 
 # ---------------------------------------------------------------- timing
@@ -340,7 +444,8 @@ def workload_gat(args):
                    "edge_feat_units_per_step": units, **gstats},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": args.traffic, "traffic_source": GSPMM_TRAFFIC_SOURCE,
+                     "traffic": (args.traffic_result or {}).get("bytes"),
+                     "traffic_detail": args.traffic_result,
                      "kernel": "gspmm u_mul_e_sum", "algorithmic_bytes": spmm_bytes,
                      "avg_ms": round(spmm_ms, 4)},
         "breakdown_ms": breakdown,
@@ -405,9 +510,11 @@ def time_gather_ceilings(g, N, E, H, args):
         (N, H * D) table by N random edge sources (gspmm's source-row reads);
       * rows_1KB_in_order: the same table by 0 .. N - 1, a streaming copy;
       * rows_1KB_streamed: the same table read once in order and hardly
-        written (segment_reduce sum over runs of 64 rows): a streaming read.
+        written (segment_reduce sum over runs of 64 rows): a streaming read;
+      * stream_read_1.28GB / _2.56GB: a bare one-pass read (mdgl_read_stream,
+        16 KB per workgroup), the read ceiling of this GPU.
     Each figure is GB/s of bytes moved per launch (4 index + gathered + written
-    per row; read + written for the streaming read)."""
+    per row; read + written for the streaming reads)."""
     import torch
 
     from mojodgl import _lib
@@ -453,6 +560,24 @@ def time_gather_ceilings(g, N, E, H, args):
     out["rows_1KB_streamed"] = dict(t, bytes=nbytes, GBps=round(nbytes / t["median_ms"] / 1e6, 1),
                                     table_MB=round(rows * 1024 / 1e6, 1))
     del table, runs, view
+    # the one-pass streaming read the bandwidth figures are judged against
+    # (mdgl_read_stream: 16 KB per workgroup, 16-byte nontemporal loads, one
+    # 16-byte word written per workgroup), at the size of C4's values and of
+    # the GAT node table
+    for name, nbytes in (("stream_read_1.28GB", 1_280_000_000),
+                         ("stream_read_2.56GB", 2_560_000_000)):
+        buf = torch.ones(nbytes // 4, device="cuda")
+        sink_bytes = int(L.mdgl_read_stream_sink_bytes(nbytes))
+        sink = torch.empty(sink_bytes // 4, device="cuda")
+
+        def read():
+            _lib.check(L.mdgl_read_stream(buf.data_ptr(), nbytes, sink.data_ptr(),
+                                          _lib.stream()), "read_stream")
+
+        t = cold(read)
+        moved = nbytes + sink_bytes
+        out[name] = dict(t, bytes=moved, GBps=round(moved / t["median_ms"] / 1e6, 1))
+        del buf, sink
     free_gpu()
     return out
 
@@ -614,6 +739,12 @@ def section_c1(args):
     g.edata["e"] = torch.from_numpy(ex).cuda()
     reds = ("sum", "mean", "max", "min")
 
+    def c1_bytes(red, es):
+        # indptr, (src, eid) per edge, the source and edge rows, the output
+        # rows, and the two int32 arg rows of max / min
+        return (4 * (N + 1) + 8 * E + es * E * D + es * E * D + es * N * D
+                + (8 * N * D if red in ("max", "min") else 0))
+
     def call(red):
         g.update_all(fn.u_mul_e("h", "e", "m"), getattr(fn, red)("m", "z"))
 
@@ -625,12 +756,10 @@ def section_c1(args):
     timer = OpTimer()
     ms = run_steps(step, args.steps, args.warmup, timer)
     units = E * D
-    base = 4 * (N + 1) + 8 * E + 4 * E * D + 4 * E * D + 4 * N * D
     cold = ColdTimer(args.reps, 3)
     ops_out = {}
     for red in reds:
-        nbytes = base + (8 * N * D if red in ("max", "min") else 0)
-        ent = hbm_entry(cold(lambda: call(red)), nbytes, units)
+        ent = hbm_entry(cold(lambda: call(red)), c1_bytes(red, 4), units)
         ent["warm_ms"] = round(timer.avg_ms("update_all_" + red), 4)
         ops_out["update_all_u_mul_e_" + red] = ent
     # the four calls captured once in a HIP graph and replayed: the launches
@@ -690,6 +819,30 @@ def section_c1(args):
                                        "the whole graph, the four update_all reductions "
                                        "kernel-only (gspmm, then +-inf -> 0 for max / min)",
                                        cores)
+    # float64, the reference's precision, on the same graph and values
+    h64, e64 = hx.astype(np.float64), ex.astype(np.float64)
+    g.ndata["h"] = torch.from_numpy(h64).cuda()
+    g.edata["e"] = torch.from_numpy(e64).cuda()
+    ops64 = {"update_all_u_mul_e_" + red: hbm_entry(cold(lambda: call(red)), c1_bytes(red, 8),
+                                                    units) for red in reds}
+    f64 = {"workload": "update_all u_mul_e + sum/mean/max/min, uniform graph, float64 (the "
+                       "reference's precision)",
+           "num_nodes": N, "num_edges": E, "feat": D, "ops": ops64}
+    if not args.no_cpu_baseline:
+        z64 = np.empty((N, D), dtype=np.float64)
+        zr64 = np.empty_like(z64)
+
+        def once64():
+            for red in range(4):
+                L.oracle_gspmm(_p(indptr), _p(indices), _p(eid), _p(h64), _p(e64), _p(z64), N,
+                               2, D, D, D, red, _p(deg), None, None, None, None, 1)
+                if red in (1, 2):
+                    L.oracle_replace_inf_with_zero(_p(z64), _p(zr64), z64.size, 1)
+
+        f64["cpu_baseline"] = cpu_rate(once64, 4 * units, args.cpu_seconds_extra,
+                                       "GEdge·feat/s", "the whole graph, the four update_all "
+                                       "reductions kernel-only, float64", cores)
+    out["f64"] = f64
     return out
 
 
@@ -787,19 +940,45 @@ def section_c3(args):
         "copy_u_max_arg": lambda: spmm._run(g, "copy_lhs", "max", h, None, want_arg=True,
                                             arg_dtype=torch.int32),
     }
-    b_mul = 4 * (N + 1) + 8 * E + 4 * E * F + 4 * E + 4 * N * F
-    b_mean = 4 * (N + 1) + 4 * E + 4 * E * F + 4 * N * F
-    b_max = b_mean + 4 * N * F
+    def c3_bytes(es):
+        # u_mul_e_sum, copy_u_mean, copy_u_max (+ int32 arg_u)
+        mean = 4 * (N + 1) + 4 * E + es * E * F + es * N * F
+        return (4 * (N + 1) + 8 * E + es * E * F + es * E + es * N * F, mean, mean + 4 * N * F)
+
     cold = ColdTimer(args.reps, 2)
     log("timing c3")
     ops_out = {name: hbm_entry(cold(fn_), b, E * F, cache_note=True)
-               for (name, fn_), b in zip(calls.items(), (b_mul, b_mean, b_max))}
+               for (name, fn_), b in zip(calls.items(), c3_bytes(4))}
+    # the cache-level ceiling of this access pattern: the same kernels over
+    # the same CSR (destination rows, degrees, slot order, edge weights) with
+    # every source folded into the first 1,024 nodes (a 2.4 MB table, which
+    # each XCD's 4 MB L2 holds) or into the first block's 4,600 nodes (11 MB,
+    # which the 256 MB MALL holds): the rate of the gathers when they hit
+    log("c3 cache-resident ceilings")
+    ceilings = {}
+    for label, fold in (("l2_resident_1024_rows", 1024), ("mall_resident_4600_rows", 4600)):
+        gc = dgl.graph((u % fold, v), num_nodes=N)
+        gc._device_csr("in")
+        ccalls = {
+            "u_mul_e_sum": lambda: ops.u_mul_e_sum(gc, h, w),
+            "copy_u_mean": lambda: ops.copy_u_mean(gc, h),
+            "copy_u_max_arg": lambda: spmm._run(gc, "copy_lhs", "max", h, None, want_arg=True,
+                                                arg_dtype=torch.int32),
+        }
+        ceilings[label] = {name: cold(fn_) for name, fn_ in ccalls.items()}
+        del gc, ccalls
+        free_gpu()
+    for name, ent in ops_out.items():
+        c = ceilings["l2_resident_1024_rows"][name]["median_ms"]
+        ent["ceiling_ms"] = c
+        ent["ceiling_frac"] = round(c / ent["median_ms"], 4)
     out = {"workload": "GCN aggregation on a 50-block community graph, float32",
            "num_nodes": N, "num_edges": E, "feat": F,
            "note": "95% of the edges stay inside 4,600-node blocks, so the L2 and the MALL serve "
                    "most source rows: rates above the HBM peak are cache-assisted "
-                   "(compulsory bytes 2.48 GB)",
-           "ops": ops_out}
+                   "(compulsory bytes 2.48 GB); ceiling_frac = the same op over the same CSR "
+                   "with its sources folded into an L2-resident table, divided by the op",
+           "ops": ops_out, "cache_ceilings": ceilings}
     if not args.no_cpu_baseline:
         oracle, L, cores = oracle_setup()
         S, nnz, ip, src, eid = csr_sample(g, args.cpu_fraction_c3)
@@ -826,7 +1005,41 @@ def section_c3(args):
             "the in-edges of the first {} destination rows ({} edges, {:.1%} of E) through "
             "u_mul_e_sum (restated kernel + broadcast extension: w is (E, 1)), copy_u_mean and "
             "copy_u_max with arg outputs, float32".format(S, nnz, nnz / E), cores)
-    del g, h, w, calls
+    # float64, the reference's precision, on the same graph
+    h64, w64 = h.double(), w.double()
+    calls64 = {
+        "u_mul_e_sum": lambda: ops.u_mul_e_sum(g, h64, w64),
+        "copy_u_mean": lambda: ops.copy_u_mean(g, h64),
+        "copy_u_max_arg": lambda: spmm._run(g, "copy_lhs", "max", h64, None, want_arg=True,
+                                            arg_dtype=torch.int32),
+    }
+    log("timing c3 in float64")
+    f64 = {"workload": "GCN aggregation on a 50-block community graph, float64 (the reference's "
+                       "precision)",
+           "num_nodes": N, "num_edges": E, "feat": F,
+           "ops": {name: hbm_entry(cold(fn_), b, E * F, cache_note=True)
+                   for (name, fn_), b in zip(calls64.items(), c3_bytes(8))}}
+    if not args.no_cpu_baseline:
+        hh64 = hh.astype(np.float64)
+        wh64 = wh.astype(np.float64)
+        z64 = np.empty((S, F), dtype=np.float64)
+        zr64 = np.empty_like(z64)
+
+        def once64():
+            L.oracle_gspmm(_p(ip), _p(src), _p(eid), _p(hh64), _p(wh64), _p(z64), S, 2, F, 1, F,
+                           0, _p(deg), _p(loff), _p(roff), None, None, 1)
+            L.oracle_gspmm(_p(ip), _p(src), _p(eid), _p(hh64), _p(hh64), _p(z64), S, 5, F, F, F,
+                           3, _p(deg), None, None, None, None, 1)
+            L.oracle_gspmm(_p(ip), _p(src), _p(eid), _p(hh64), _p(hh64), _p(z64), S, 5, F, F, F,
+                           1, _p(deg), None, None, _p(au), _p(ae), 1)
+            L.oracle_replace_inf_with_zero(_p(z64), _p(zr64), z64.size, 1)
+
+        f64["cpu_baseline"] = cpu_rate(
+            once64, 3 * nnz * F, args.cpu_seconds_extra, "GEdge·feat/s",
+            "the in-edges of the first {} destination rows ({} edges, {:.1%} of E) through the "
+            "three ops, float64".format(S, nnz, nnz / E), cores)
+    out["f64"] = f64
+    del g, h, w, h64, w64, calls, calls64
     free_gpu()
     return out
 
@@ -919,7 +1132,53 @@ def section_c4(args):
                                  "the first {} segments ({} rows) through segment_reduce sum, "
                                  "max (+ replace_inf) and segment_softmax, float32".format(ns, nr),
                                  cores)}
-    del g, h, val, seglen_d, lens, ibuf, fbuf, calls, helpers
+    del ibuf, fbuf, helpers
+    # float64, the reference's precision, on the same graph and segments
+    h64, val64 = h.double(), val.double()
+    calls64 = {
+        "u_dot_v": (lambda: ops.u_dot_v(g, h64, h64), 8 * E + 8 * E * F * 2 + 8 * E, E * F),
+        "segment_reduce_sum": (lambda: ops.segment_reduce(seglen_d, val64, "sum"),
+                               4 * (S + 1) + 8 * R * 16 + 8 * S * 16, R * 16),
+        "segment_reduce_max": (lambda: ops.segment_reduce(seglen_d, val64, "max"),
+                               4 * (S + 1) + 8 * R * 16 + 8 * S * 16, R * 16),
+        "segment_softmax": (lambda: ops.segment_softmax(seglen_d, val64),
+                            4 * (S + 1) + 8 * R * 16 * 2, R * 16),
+    }
+    log("timing c4 in float64")
+    f64 = {"workload": "u_dot_v link scoring + segment_reduce sum/max + segment_softmax, "
+                       "float64 (the reference's precision)",
+           "num_nodes": N, "num_edges": E, "segments": S, "rows": R,
+           "ops": {name: hbm_entry(cold(fn_), b, units)
+                   for name, (fn_, b, units) in calls64.items()}}
+    if not args.no_cpu_baseline:
+        hh64 = hh.astype(np.float64)
+        vh64 = vh.astype(np.float64)
+        score64 = np.empty((ne, 1), dtype=np.float64)
+        sred64 = np.empty((ns, 16), dtype=np.float64)
+        sres64 = np.empty_like(sred64)
+        ssm64 = np.zeros((nr, 16), dtype=np.float64)
+
+        def once_dot64():
+            Lo.oracle_gsddmm(_p(us), _p(vs), _p(hh64), _p(hh64), _p(score64), ne, 0, 1, 4, F, F,
+                             1, None, None, F, 1)
+
+        def once_seg64():
+            Lo.oracle_segment_reduce(_p(offs), _p(vh64), _p(sred64), ns, 16, 0, nr, 1)
+            Lo.oracle_segment_reduce(_p(offs), _p(vh64), _p(sred64), ns, 16, 1, nr, 1)
+            Lo.oracle_replace_inf_with_zero(_p(sred64), _p(sres64), sred64.size, 1)
+            Lo.oracle_segment_softmax(_p(offs), _p(vh64), _p(ssm64), ns, 16, nr, 1)
+
+        f64["cpu_baseline"] = {
+            "u_dot_v": cpu_rate(once_dot64, ne * F, args.cpu_seconds_extra, "GEdge·feat/s",
+                                "the first {} edges ({:.0%} of E), float64".format(ne, ne / E),
+                                cores),
+            "segments": cpu_rate(once_seg64, 3 * nr * 16, args.cpu_seconds_extra,
+                                 "G row·feat/s",
+                                 "the first {} segments ({} rows) through segment_reduce sum, "
+                                 "max (+ replace_inf) and segment_softmax, float64".format(ns, nr),
+                                 cores)}
+    out["f64"] = f64
+    del g, h, val, h64, val64, seglen_d, lens, calls, calls64
     free_gpu()
     return out
 
@@ -994,7 +1253,45 @@ def section_c5(args):
             "segment_mm": cpu_rate(once_s, 2.0 * ns * K * K, args.cpu_seconds_extra, "GFLOP/s",
                                    "{} rows in 64 segments of the same proportions, float32; "
                                    "serial, as the reference's kernel".format(ns), 1)}
-    del a, b, idx, w0
+    del w0
+    # float64, the reference's precision, on the float64 matrix cores
+    # (v_mfma_f64_16x16x4f64), same rows, blocks and groups
+    a64, b64 = a.double(), b.double()
+    del a, b
+    free_gpu()
+    log("timing c5 in float64")
+    f64 = {"workload": "RGCN relation transform: gather_mm + segment_mm, float64 (the "
+                       "reference's precision)",
+           "rows": n, "d1": K, "d2": K, "relations": R,
+           "ops": {"gather_mm": mfma_entry(cold(lambda: ops.gather_mm(a64, b64, idx_b=idx)),
+                                           flops, 8 * n * K * 2 + 8 * n + 8 * R * K * K,
+                                           MFMA_F64_PEAK_TFLOPS),
+                   "segment_mm": mfma_entry(cold(lambda: ops.segment_mm(a64, b64, seglen)),
+                                            flops, 8 * n * K * 2 + 8 * R * K * K + 8 * R,
+                                            MFMA_F64_PEAK_TFLOPS)},
+           "arithmetic": "float64 in and out on v_mfma_f64_16x16x4f64; frac is against the "
+                         "78.6 TFLOP/s float64 MFMA peak"}
+    if not args.no_cpu_baseline:
+        ah64 = ah.astype(np.float64)
+        bh64 = bh.astype(np.float64)
+        og64 = np.empty((ng, K), dtype=np.float64)
+        ahs64 = ahs.astype(np.float64)
+        os64 = np.zeros((ns, K), dtype=np.float64)
+
+        def once_g64():
+            L.oracle_gather_mm(_p(ah64), _p(bh64), _p(ih), _p(og64), ng, K, K, 1)
+
+        def once_s64():
+            L.oracle_segment_mm(_p(ahs64), _p(bh64), _p(os64), _p(sl), ns, K, R, K, 1)
+
+        f64["cpu_baseline"] = {
+            "gather_mm": cpu_rate(once_g64, 2.0 * ng * K * K, args.cpu_seconds_extra, "GFLOP/s",
+                                  "the first {} rows, float64".format(ng), cores),
+            "segment_mm": cpu_rate(once_s64, 2.0 * ns * K * K, args.cpu_seconds_extra, "GFLOP/s",
+                                   "{} rows in 64 segments of the same proportions, float64; "
+                                   "serial, as the reference's kernel".format(ns), 1)}
+    out["f64"] = f64
+    del a64, b64, idx
     free_gpu()
     return out
 
@@ -1063,6 +1360,7 @@ def workload_section(name):
 
 
 WORKLOADS = {"gat": workload_gat, "gat_train": workload_gat_train,
+             "gspmm_traffic": workload_gspmm_traffic,
              **{k: workload_section(k) for k in SECTIONS}}
 
 
@@ -1097,13 +1395,20 @@ def main():
     ap.add_argument("--cpu-seconds-extra", type=float, default=3.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="finish with a 1 GiB device-to-device copy (counter calibration)")
-    ap.add_argument("--traffic", type=float, default=GSPMM_TRAFFIC_BYTES,
-                    help="HBM bytes per gspmm launch measured by rocprofv3 (reported as is)")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the live rocprofv3 measurement of the headline gspmm's bytes")
+    ap.add_argument("--traffic-timeout", type=float, default=150.0,
+                    help="time limit of each rocprofv3 counter pass (seconds)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: mojodgl runs on a single MI355X and has no "
               "multi-GPU path (--gpus {} requested)".format(args.gpus), file=sys.stderr)
         sys.exit(2)
+    t_start = time.perf_counter()
+    args.traffic_result = None
+    if args.workload == "gat" and not args.no_traffic:
+        # child processes, before this one touches the GPU
+        args.traffic_result = measure_traffic(args)
     import torch
 
     if not torch.cuda.is_available():
@@ -1114,8 +1419,10 @@ def main():
         import mojodgl.heterograph as hg
 
         hg.CHUNK_LEN = args.chunk_len
-    t_start = time.perf_counter()
     res = WORKLOADS[args.workload](args)
+    if args.workload == "gspmm_traffic":
+        print(json.dumps(res), flush=True)
+        return
     if args.workload == "gat" and not args.headline_only:
         configs = {"c2_f64": res.pop("c2_f64")}
         for name, fn_ in SECTIONS.items():
@@ -1123,6 +1430,8 @@ def main():
             configs[name] = fn_(args)
         res["configs"] = {"c1": configs["c1"], "c2_f64": configs["c2_f64"],
                           "c3": configs["c3"], "c4": configs["c4"], "c5": configs["c5"]}
+        for name in ("c1", "c3", "c4", "c5"):
+            res["configs"][name + "_f64"] = configs[name].pop("f64")
     res["bench_wall_s"] = round(time.perf_counter() - t_start, 1)
     if args.calibrate_copy:
         # a plain device copy of 1 GiB, for scaling rocprofv3 byte counters

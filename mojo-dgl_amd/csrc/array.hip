@@ -405,6 +405,53 @@ hipError_t launch_segment_ids(const int32_t* offsets, int64_t num_seg, int64_t n
   return hipGetLastError();
 }
 
+// A streaming read: each workgroup reads its own 16 KB once (four 16-byte
+// nontemporal loads per lane, all issued before any is used) and writes one
+// 16-byte word of their XOR, so the launch moves the buffer once and
+// writes 1/1024 of it. The library's kernels are measured against its rate.
+constexpr int RS_PER = 4;
+constexpr int64_t RS_BYTES = (int64_t)BLOCK * RS_PER * 16;  // bytes per workgroup
+typedef unsigned int rs_u4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(BLOCK) void read_stream_kernel(const rs_u4* __restrict__ src,
+                                                            int64_t n16,
+                                                            rs_u4* __restrict__ sink) {
+  const int64_t base = (int64_t)blockIdx.x * BLOCK * RS_PER;
+  rs_u4 v[RS_PER];
+#pragma unroll
+  for (int j = 0; j < RS_PER; ++j) {
+    const int64_t i = base + j * BLOCK + threadIdx.x;
+    v[j] = i < n16 ? __builtin_nontemporal_load(src + i) : rs_u4{0, 0, 0, 0};
+  }
+  rs_u4 x = v[0];
+#pragma unroll
+  for (int j = 1; j < RS_PER; ++j) x ^= v[j];
+  for (int off = 32; off >= 1; off >>= 1) {
+    x.x ^= __shfl_xor(x.x, off);
+    x.y ^= __shfl_xor(x.y, off);
+    x.z ^= __shfl_xor(x.z, off);
+    x.w ^= __shfl_xor(x.w, off);
+  }
+  __shared__ rs_u4 part[WAVES_PER_BLOCK];
+  if ((threadIdx.x & (WAVE - 1)) == 0) part[threadIdx.x / WAVE] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int q = 1; q < WAVES_PER_BLOCK; ++q) x ^= part[q];
+    sink[blockIdx.x] = x;
+  }
+}
+
+int64_t read_stream_sink_bytes(int64_t bytes) { return (bytes + RS_BYTES - 1) / RS_BYTES * 16; }
+
+hipError_t launch_read_stream(const void* src, int64_t bytes, void* sink, hipStream_t s) {
+  const int64_t n16 = bytes / 16;
+  const int64_t blocks = (bytes + RS_BYTES - 1) / RS_BYTES;
+  if (blocks == 0) return hipSuccess;
+  hipLaunchKernelGGL(read_stream_kernel, dim3((unsigned)blocks), dim3(BLOCK), 0, s,
+                     static_cast<const rs_u4*>(src), n16, static_cast<rs_u4*>(sink));
+  return hipGetLastError();
+}
+
 hipError_t launch_cumsum_i64(const int64_t* src, int64_t* dst, int64_t n, hipStream_t s) {
   if (n <= 0) return hipSuccess;
   const int64_t tiles = (n + CS_TILE - 1) / CS_TILE;

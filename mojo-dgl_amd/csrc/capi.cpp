@@ -184,6 +184,19 @@ int mdgl_cumsum(const int64_t* src, int64_t* dst, int64_t n, void* stream) {
   return hip_status(launch_cumsum_i64(src, dst, n, (hipStream_t)stream), "cumsum");
 }
 
+int64_t mdgl_read_stream_sink_bytes(int64_t bytes) {
+  return bytes < 0 ? -1 : read_stream_sink_bytes(bytes);
+}
+
+int mdgl_read_stream(const void* src, int64_t bytes, void* sink, void* stream) {
+  if (bytes < 0 || bytes % 16) return fail(MDGL_EINVAL, "read_stream: bytes must be a multiple of 16");
+  if (bytes == 0) return MDGL_OK;
+  if (!src || !sink) return fail(MDGL_EINVAL, "read_stream: null buffer");
+  if (!aligned(src, 16) || !aligned(sink, 16))
+    return fail(MDGL_EINVAL, "read_stream: buffers must be 16-byte aligned");
+  return hip_status(launch_read_stream(src, bytes, sink, (hipStream_t)stream), "read_stream");
+}
+
 int64_t mdgl_build_csr_workspace_bytes(int64_t num_edges, int64_t num_rows) {
   if (num_edges < 0 || num_rows < 0) return -1;
   return csr_workspace_bytes(num_edges, num_rows);

@@ -240,6 +240,8 @@ hipError_t launch_build_csr(const int32_t* key, const int32_t* other, int64_t nu
                             int64_t num_rows, int32_t* indptr, int32_t* indices, int32_t* eid,
                             void* workspace, hipStream_t stream);
 hipError_t launch_cumsum_i64(const int64_t* src, int64_t* dst, int64_t n, hipStream_t s);
+int64_t read_stream_sink_bytes(int64_t bytes);
+hipError_t launch_read_stream(const void* src, int64_t bytes, void* sink, hipStream_t s);
 // The positional edge_softmax plan built on the GPU (softmax_plan.hip):
 // positions grouped by the endpoint of their edge, rows binned by degree,
 // chunks of the long rows, the packed edge lists and the SoftDyn figures.
