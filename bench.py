@@ -512,7 +512,8 @@ def time_gather_ceilings(g, N, E, H, args):
       * rows_1KB_streamed: the same table read once in order and hardly
         written (segment_reduce sum over runs of 64 rows): a streaming read;
       * stream_read_1.28GB / _2.56GB: a bare one-pass read (mdgl_read_stream,
-        16 KB per workgroup), the read ceiling of this GPU.
+        a persistent grid of 16-byte nontemporal loads), the read ceiling of
+        this GPU.
     Each figure is GB/s of bytes moved per launch (4 index + gathered + written
     per row; read + written for the streaming reads)."""
     import torch
@@ -561,9 +562,9 @@ def time_gather_ceilings(g, N, E, H, args):
                                     table_MB=round(rows * 1024 / 1e6, 1))
     del table, runs, view
     # the one-pass streaming read the bandwidth figures are judged against
-    # (mdgl_read_stream: 16 KB per workgroup, 16-byte nontemporal loads, one
-    # 16-byte word written per workgroup), at the size of C4's values and of
-    # the GAT node table
+    # (mdgl_read_stream: 2,048 workgroups striding with 16-byte nontemporal
+    # loads, 32 KB per workgroup and round, next to nothing written), at the
+    # size of C4's values and of the GAT node table
     for name, nbytes in (("stream_read_1.28GB", 1_280_000_000),
                          ("stream_read_2.56GB", 2_560_000_000)):
         buf = torch.ones(nbytes // 4, device="cuda")

@@ -284,11 +284,12 @@ int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int3
                        const int32_t* slot_of_edge, int64_t num_edges, void* workspace,
                        int64_t workspace_bytes, int dtype, void* stream);
 
-/* A streaming read of `bytes` (a multiple of 16) at `src`: every workgroup
- * reads its own 16 KB once with 16-byte nontemporal loads and writes one
- * 16-byte word to `sink` (mdgl_read_stream_sink_bytes(bytes)). No counterpart
- * in the reference: it is the measured ceiling of a one-pass read on this GPU,
- * the rate the library's bandwidth-bound kernels are judged against. */
+/* A streaming read of `bytes` (a multiple of 16) at `src`: a fixed grid of
+ * 2,048 workgroups strides over it with 16-byte nontemporal loads, 32 KB per
+ * workgroup and round; `sink` (mdgl_read_stream_sink_bytes(bytes), 16-byte
+ * aligned) receives at most one 16-byte word per wavefront. No counterpart
+ * in the reference: it is the measured ceiling of a one-pass read on this
+ * GPU, the rate the library's bandwidth-bound kernels are judged against. */
 int mdgl_read_stream(const void* src, int64_t bytes, void* sink, void* stream);
 int64_t mdgl_read_stream_sink_bytes(int64_t bytes);
 

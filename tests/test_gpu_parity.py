@@ -732,6 +732,31 @@ def test_wrapping_gpu_lengths_are_refused():
             call()
 
 
+def test_read_stream_reads_every_vector():
+    """mdgl_read_stream folds every 16-byte vector into its wavefront's XOR
+    and writes only a wavefront whose XOR is 0x9e3779b9 in its first word:
+    with one such vector planted in zeros, exactly its wavefront's slot is
+    written (vector i is read in round i // (2048 * 2048), by workgroup
+    (i // 2048) % 2048, lane i % 256), including a vector in the last,
+    partial round."""
+    from mojodgl import _lib
+
+    L = _lib.lib()
+    n16 = 2048 * 2048 * 2 + 1000                     # two full rounds and a partial one
+    for i in (0, 5 * 2048 + 3 * 256 + 70, 2048 * 2048 * 2 + 999):
+        buf = torch.zeros(n16 * 4, dtype=torch.int32, device="cuda")
+        buf[4 * i] = np.int32(np.uint32(0x9e3779b9).view(np.int32))
+        sink_bytes = int(L.mdgl_read_stream_sink_bytes(n16 * 16))
+        sink = torch.full((sink_bytes // 4,), 7, dtype=torch.int32, device="cuda")
+        _lib.check(L.mdgl_read_stream(buf.data_ptr(), n16 * 16, sink.data_ptr(), _lib.stream()),
+                   "read_stream")
+        got = sink.cpu().numpy().reshape(-1, 4)
+        slot = ((i % (2048 * 2048)) // 2048) * 4 + (i % 256) // 64
+        want = np.full_like(got, 7)
+        want[slot] = [np.uint32(0x9e3779b9).view(np.int32), 0, 0, 0]
+        np.testing.assert_array_equal(got, want, err_msg=str(i))
+
+
 # ------------------------------------------------------------------ array helpers
 @pytest.mark.parametrize("n", [1, 100, 4095, 4096, 4097, 12289, 1_000_003])
 def test_cumsum_clamp_replace_inf_through_the_abi(n):
