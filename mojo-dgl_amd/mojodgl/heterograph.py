@@ -50,6 +50,9 @@ _Code2Str = TargetCode.CODE2STR
 
 # rows of more in-edges than this are split into chunks of this many for gspmm
 CHUNK_LEN = 512
+# pull runs a builtin pass over every edge (no subgraph) when the pulled rows
+# hold at least 1 / PULL_FULL_PASS of the edges
+PULL_FULL_PASS = 8
 
 
 def chunk_plan(indptr: np.ndarray, chunk_len: int):
@@ -513,12 +516,25 @@ class DGLGraph(object):
         if int(v[0]) < 0 or int(v[-1]) >= self._num_nodes:
             raise DGLError("node ids must be in [0, {}), got [{}, {}]".format(
                 self._num_nodes, int(v[0]), int(v[-1])))
-        # the in-edges of `v`, selected on the GPU from the resident endpoints
-        # (edge-id order kept); the subgraph is built from them there
+        csr = self._device_csr("in")
+        ip = csr.host_indptr
+        pulled = int((ip[v + 1] - ip[v]).sum())  # in-edges of v, known on the host
+        if (isinstance(message_func, MessageFunction) and isinstance(reduce_func, ReduceFunction)
+                and apply_node_func is None and pulled * PULL_FULL_PASS >= self._E):
+            # a builtin output row depends on its own in-edges only, so a pass
+            # over every edge gives the subgraph's rows for v; taken when v's
+            # in-edges are a large share of the graph (no subgraph to build)
+            result = self._pass(message_func, reduce_func, None, write=False)
+            self._write_pulled(result, v)
+            return
+        # the in-edges of `v` in edge-id order, selected on the GPU: a stable
+        # grouping of the edges by whether their destination is pulled puts
+        # them last, `pulled` of them; the subgraph is built from them there
         du, dv = self._device_coo()
-        flag = torch.zeros(self._num_nodes, dtype=torch.bool, device=du.device)
-        flag[torch.from_numpy(v).to(du.device)] = True
-        sel = torch.nonzero(flag[dv.long()]).squeeze(1)
+        flag = torch.zeros(self._num_nodes, dtype=torch.int32, device=du.device)
+        flag[torch.from_numpy(v).to(du.device)] = 1
+        _, _, grouped = build_device_csr(flag[dv.long()], None, 2)
+        sel = grouped[self._E - pulled:].long()
         sub = DGLGraph(du[sel], dv[sel], num_nodes=self._num_nodes)
         for key, value in self._nstore.items():
             sub.ndata[key] = value
@@ -528,6 +544,11 @@ class DGLGraph(object):
             else:
                 sub.edata[key] = value[sel.cpu().numpy()]
         result = sub._pass(message_func, reduce_func, apply_node_func, write=False)
+        self._write_pulled(result, v)
+
+    def _write_pulled(self, result, v):
+        """Store each result feature with the rows outside `v` zeroed
+        (reference heterograph.py:344-347)."""
         for key, value in result.items():
             if isinstance(value, torch.Tensor):
                 rows = torch.zeros_like(value)

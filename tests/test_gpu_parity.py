@@ -1025,6 +1025,53 @@ def test_pull_and_readme_vector():
           np.float64, "pull")
 
 
+@pytest.mark.parametrize("msg,red", [("u_mul_e", "sum"), ("copy_u", "mean"), ("u_add_v", "max"),
+                                     ("copy_e", "min"), ("udf", "sum")])
+@pytest.mark.parametrize("on_gpu", [False, True])
+def test_pull_full_pass_and_subgraph_agree(msg, red, on_gpu, monkeypatch):
+    """pull runs a builtin pass over every edge when the pulled rows hold many
+    in-edges, and a subgraph of their in-edges (selected by the GPU grouping,
+    in edge-id order) otherwise: both give the reference's result (the pulled
+    rows of a full pass, zero elsewhere; max / min's +-inf -> 0), bit for bit
+    between the two, and a UDF message always takes the subgraph."""
+    n, e = 300, 5000
+    u, v = rand_graph(n, e, 29)
+    v[:400] = 7
+    rng = np.random.default_rng(30)
+    x, w = rng.normal(size=(n, 5)), rng.normal(size=(e, 5))
+    targets = np.array([3, 7, 8, 100, 299, 7])
+    if msg == "udf":
+        message = lambda edges: {"m": edges.src["x"] * edges.data["e"]}  # noqa: E731
+        ref_msg = ("mul", x, w)
+    elif msg == "u_add_v":
+        message = fn.u_add_v("x", "x", "m")
+        ref_msg = None
+    else:
+        message = getattr(fn, msg)(*{"u_mul_e": ("x", "e", "m"), "copy_u": ("x", "m"),
+                                     "copy_e": ("e", "m")}[msg])
+        ref_msg = {"u_mul_e": ("mul", x, w), "copy_u": ("copy_lhs", x, None),
+                   "copy_e": ("copy_rhs", None, w)}[msg]
+    got = {}
+    for full in (True, False):
+        monkeypatch.setattr(hg, "PULL_FULL_PASS", 10 ** 9 if full else 0)
+        g = dgl.graph((u, v), num_nodes=n)
+        g.ndata["x"] = torch.from_numpy(x).cuda() if on_gpu else x
+        g.edata["e"] = torch.from_numpy(w).cuda() if on_gpu else w
+        g.pull(targets, message, getattr(fn, red)("m", "h"))
+        h = g.ndata["h"]
+        got[full] = h.cpu().numpy() if isinstance(h, torch.Tensor) else np.asarray(h)
+    np.testing.assert_array_equal(got[True], got[False])
+    if ref_msg is None:
+        msgs = x[u] + x[v]
+        full_ref = oracle.gspmm(u, v, n, "copy_rhs", red, None, msgs)
+    else:
+        full_ref = oracle.gspmm(u, v, n, ref_msg[0], red, ref_msg[1], ref_msg[2])
+    full_ref = np.where(np.isinf(full_ref), 0.0, full_ref)
+    want = np.zeros_like(full_ref)
+    want[targets] = full_ref[targets]
+    close(got[False], want, np.abs(want) + 1e-12, np.float64, "pull {} {}".format(msg, red))
+
+
 def test_graph_from_gpu_ids_is_built_on_the_gpu():
     """GPU endpoint tensors: checked on the GPU, no host copy until a host query."""
     n, e = 700, 9000
