@@ -1345,6 +1345,51 @@ def workload_gat_train(args):
 SECTIONS = {"c1": section_c1, "c3": section_c3, "c4": section_c4, "c5": section_c5}
 
 
+def workload_c5_phases(args):
+    """segment_mm of the RGCN configuration in a loop, phase by phase, for a
+    power and clock sampler running beside it (amd-smi in another process):
+    the bf16-split kernel, the same call with every group forced onto the
+    float32 MFMA path (one b value out of the split's range), and the vendor
+    BLAS on one block. Each phase prints its wall-clock bounds."""
+    import torch
+
+    import mojodgl.ops as ops
+
+    n, K, R = 10_000_000, 128, 64
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    a = torch.randn(n, K, device="cuda", generator=gen)
+    b = torch.randn(R, K, K, device="cuda", generator=gen) * (1.0 / np.sqrt(K))
+    rng = np.random.default_rng(4)
+    seglen = rng.multinomial(n, rng.dirichlet(0.5 * np.ones(R)))
+    forced = b.clone()
+    forced[:, 0, 0] = 1e30
+    w0 = b[0].contiguous()
+    dst = torch.empty(n, K, device="cuda")
+    torch.backends.cuda.matmul.allow_tf32 = False
+    phases = []
+    for name, fn_ in (("segment_mm_bf16_split", lambda: ops.segment_mm(a, b, seglen)),
+                      ("segment_mm_float32_mfma", lambda: ops.segment_mm(a, forced, seglen)),
+                      ("torch_mm_one_block", lambda: torch.mm(a, w0, out=dst))):
+        fn_()
+        torch.cuda.synchronize()
+        t0 = time.time()
+        calls = 0
+        while time.time() - t0 < args.phase_seconds:
+            for _ in range(10):
+                fn_()
+            torch.cuda.synchronize()
+            calls += 10
+        t1 = time.time()
+        phases.append({"phase": name, "start": round(t0, 3), "end": round(t1, 3), "calls": calls,
+                       "ms_per_call": round((t1 - t0) * 1e3 / calls, 4)})
+        log("phase", name, round(t0, 3), round(t1, 3))
+        time.sleep(0.5)
+    return {"metric": "ms per call by phase", "value": phases[0]["ms_per_call"],
+            "unit": "ms", "ms_per_step": phases[0]["ms_per_call"], "dtype": "f32",
+            "config": {"workload": "RGCN segment_mm phases for a power sampler"},
+            "phases": phases}
+
+
 def workload_section(name):
     """One configuration alone, printed as its own line."""
 
@@ -1361,7 +1406,7 @@ def workload_section(name):
 
 
 WORKLOADS = {"gat": workload_gat, "gat_train": workload_gat_train,
-             "gspmm_traffic": workload_gspmm_traffic,
+             "gspmm_traffic": workload_gspmm_traffic, "c5_phases": workload_c5_phases,
              **{k: workload_section(k) for k in SECTIONS}}
 
 
@@ -1396,6 +1441,8 @@ def main():
     ap.add_argument("--cpu-seconds-extra", type=float, default=3.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="finish with a 1 GiB device-to-device copy (counter calibration)")
+    ap.add_argument("--phase-seconds", type=float, default=4.0,
+                    help="length of each phase of --workload c5_phases")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the live rocprofv3 measurement of the headline gspmm's bytes")
     ap.add_argument("--traffic-timeout", type=float, default=150.0,
