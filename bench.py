@@ -1349,8 +1349,9 @@ def workload_c5_phases(args):
     """segment_mm of the RGCN configuration in a loop, phase by phase, for a
     power and clock sampler running beside it (amd-smi in another process):
     the bf16-split kernel, the same call with every group forced onto the
-    float32 MFMA path (one b value out of the split's range), and the vendor
-    BLAS on one block. Each phase prints its wall-clock bounds."""
+    float32 MFMA path (one b value out of the split's range), the vendor BLAS
+    on one block, and segment_mm in float64. Each phase prints its wall-clock
+    bounds."""
     import torch
 
     import mojodgl.ops as ops
@@ -1367,9 +1368,11 @@ def workload_c5_phases(args):
     dst = torch.empty(n, K, device="cuda")
     torch.backends.cuda.matmul.allow_tf32 = False
     phases = []
+    a64, b64 = a.double(), b.double()
     for name, fn_ in (("segment_mm_bf16_split", lambda: ops.segment_mm(a, b, seglen)),
                       ("segment_mm_float32_mfma", lambda: ops.segment_mm(a, forced, seglen)),
-                      ("torch_mm_one_block", lambda: torch.mm(a, w0, out=dst))):
+                      ("torch_mm_one_block", lambda: torch.mm(a, w0, out=dst)),
+                      ("segment_mm_float64", lambda: ops.segment_mm(a64, b64, seglen))):
         fn_()
         torch.cuda.synchronize()
         t0 = time.time()
