@@ -566,6 +566,244 @@ __global__ __launch_bounds__(SB_THREADS, 1) void grouped_gemm_split_kernel(
   }
 }
 
+// ---------------------------------------------------------------- float64
+// float64 shapes with K a multiple of 16 up to 128 and a on a 16-byte
+// boundary (the host checks; others take grouped_gemm_kernel).
+//
+// Work mapping. As in the split kernel: one workgroup per CU (NW wavefronts)
+// holds the group's b block in LDS (128 columns x Kp, 132 doubles per row:
+// with 1,056-byte rows the reads below meet no bank conflict, where 1,040- or
+// 1,072-byte rows make every read wait twice as long, as measured), loaded
+// once per group it meets, and walks a contiguous range of tiles of
+// 16 * RB * NW rows in group order. A wavefront owns 16 * RB rows of a tile
+// and all 128 columns (RB x 8 blocks of v_mfma_f64_16x16x4f64), reads its
+// rows of a straight from global memory into registers (no LDS, no barrier
+// in the K loop), RS chunks of 16 ahead of the MFMAs that use them, wrapping
+// into the next tile's rows.
+//
+// The K axis goes in 16-wide chunks, four MFMA steps each. In chunk c, lane
+// (i, q) (i = lane % 16 the block row or column, q = lane / 16) supplies
+// k = 16c + 2q + (s & 1) + 8 (s >> 1) in step s: a[row i][16c + 2q .. +1]
+// and a[row i][16c + 8 + 2q .. +1], two 16-byte loads that cover 64
+// contiguous bytes of the row per instruction, and b[k][column i] from two
+// 16-byte LDS reads. The four steps of a chunk cover its 16 k exactly once.
+//
+// Arithmetic: each output is the sum over k of a * b, in float64, in the
+// MFMA units' order (the reference sums in k order: src/ported.mojo:786-790,
+// 1115-1119; the two agree to rounding).
+constexpr int F64_KMAX = 128;
+constexpr int F64_LD = F64_KMAX + 4;  // doubles per LDS row
+constexpr int F64_RB = 1, F64_NW = 8;  // the library's shape: 128-row tiles
+constexpr int F64_TM = 16 * F64_RB * F64_NW;
+constexpr int F64_SINK = GBN;  // doubles of the store sink in the workspace
+
+template <int NCH, int RB, int NW, bool GATHER>
+__global__ __launch_bounds__(64 * NW, 1) void grouped_gemm_f64_kernel(
+    GemmArgs<double> p, int64_t tiles_per_wg, const int32_t* __restrict__ tile_ptr,
+    const int32_t* __restrict__ group_off, double* __restrict__ sink) {
+  constexpr int TM = 16 * RB * NW;
+  constexpr int NT = 64 * NW;
+  constexpr int CB = GBN / 16;  // column blocks
+  __shared__ __align__(16) double Bs[GBN][F64_LD];
+  const int t = threadIdx.x;
+  const int lane = t & 63, w = t >> 6;
+  const int li = lane & 15, q = lane >> 4;
+  const int64_t total = tile_ptr[p.R];
+  const int64_t first = (int64_t)blockIdx.x * tiles_per_wg;
+  const int64_t last = first + tiles_per_wg < total ? first + tiles_per_wg : total;
+  if (first >= last) return;  // uniform per workgroup
+  const int64_t n0 = (int64_t)blockIdx.y * GBN;
+
+  // group metadata through scalar loads (uniform index, read-only arguments)
+  auto uget = [](const int32_t* __restrict__ arr, int64_t i) -> int64_t {
+    return arr[__builtin_amdgcn_readfirstlane((int)i)];
+  };
+  // the group of tile tl, from the group of an earlier tile
+  auto advance = [&](int64_t gg, int64_t tl) -> int64_t {
+    while (uget(tile_ptr, gg + 1) <= tl) ++gg;
+    return gg;
+  };
+  // The row of a behind row 16 (RB w + rb) + i of tile tl of group gg, and
+  // whether there is one (none past the group: that lane's loads then read
+  // row 0 and its stores go to the sink). gather_mm's rows come through the
+  // permutation, a vector load that is requested a whole tile before it is
+  // needed and not touched until then (its clamped index always valid), so
+  // waiting for it does not also wait for the loads and stores issued just
+  // before. Every global load and store in the tile loop is unconditional:
+  // the compiler counts only those it knows are issued, and a skippable
+  // store would make each tile's first wait cover the previous tile's
+  // stores.
+  auto row_of = [&](int64_t tl, int64_t gg, int rb, bool& ok) -> int32_t {
+    const int64_t m0 = uget(group_off, gg) + (tl - uget(tile_ptr, gg)) * TM;
+    const int64_t pos = m0 + 16 * (RB * w + rb) + li;
+    const int64_t end = uget(group_off, gg + 1);
+    ok = pos < end;
+    if constexpr (GATHER) return p.perm[ok ? pos : end - 1];
+    return (int32_t)pos;
+  };
+  auto base_of = [&](int32_t r, bool ok) -> const double* {
+    return p.a + (int64_t)(ok ? r : 0) * p.K;
+  };
+  // a[row][16c + 2q .. +1] and a[row][16c + 8 + 2q .. +1] (K = 16 NCH: no
+  // piece is past the row; a select of zeros past K would be placed right
+  // after the loads by the compiler and wait for them there)
+  auto load_chunk = [&](const double* bp, int c, double (&d)[4]) {
+    double x[2], y[2];
+    load_global_n<double, 2>(bp + 16 * c + 2 * q, x);
+    load_global_n<double, 2>(bp + 16 * c + 8 + 2 * q, y);
+    d[0] = x[0];
+    d[1] = x[1];
+    d[2] = y[0];
+    d[3] = y[1];
+  };
+
+  int64_t tile = first;
+  int64_t g = 0;
+  {
+    int64_t lo = 0, hi = p.R - 1;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi + 1) / 2;
+      if (uget(tile_ptr, mid) <= tile) lo = mid; else hi = mid - 1;
+    }
+    g = lo;
+  }
+  // rows of this tile (rid, rok) and of the next one (rid1, rok1, group g1;
+  // past the last tile, this tile's again)
+  int32_t rid[RB], rid1[RB];
+  bool rok[RB], rok1[RB];
+  int64_t g1 = g;
+  if (tile + 1 < last) g1 = advance(g, tile + 1);
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    rid[rb] = row_of(tile, g, rb, rok[rb]);
+    rid1[rb] = row_of(tile + 1 < last ? tile + 1 : tile, g1, rb, rok1[rb]);
+  }
+  // a values in a ring of RS chunks: chunk c lives in af[c % RS] and, once
+  // used, its slot takes the chunk RS later (this tile's or the next one's);
+  // a whole tile ahead for one row block per wavefront, half a tile for more
+  constexpr int RS = (RB > 1 && NCH % 2 == 0) ? NCH / 2 : NCH;
+  static_assert(NCH % RS == 0, "a tile's chunks fill the ring evenly");
+  double af[RS][RB][4];
+#pragma unroll
+  for (int c = 0; c < RS; ++c)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) load_chunk(base_of(rid[rb], rok[rb]), c, af[c][rb]);
+  // Wait for them here, once. Otherwise the wait before each tile's first
+  // MFMA is counted for the entry into the loop too (these loads only) and
+  // so also waits for most of the previous tile's output stores.
+  __builtin_amdgcn_s_waitcnt(0);
+
+  int64_t cur_g = -1;
+  auto run_tile = [&]() -> bool {
+    if (g != cur_g) {
+      __syncthreads();  // every wavefront is done with the previous block
+      const double* src = p.bt + g * p.N * p.Kp;
+      constexpr int CPR = NCH * 8;  // 16-byte pieces per LDS row
+      for (int c = t; c < GBN * CPR; c += NT) {
+        const int r = c / CPR, k = (c % CPR) * 2;
+        double v[2] = {0.0, 0.0};
+        if (n0 + r < p.N) load_global_n<double, 2>(src + (n0 + r) * p.Kp + k, v);
+        store_n<double, 2>(&Bs[r][k], v);
+      }
+      __syncthreads();
+      cur_g = g;
+    }
+    const bool has_next = tile + 1 < last;
+    const double* base[RB];
+    const double* base_n[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      base[rb] = base_of(rid[rb], rok[rb]);
+      base_n[rb] = base_of(rid1[rb], rok1[rb]);
+    }
+    // the rows of the tile after the next (past the last tile, the next one's)
+    int64_t g2 = g1;
+    int32_t rid2[RB];
+    bool rok2[RB];
+    const int64_t t2 = tile + 2 < last ? tile + 2 : tile + 1;
+    if (tile + 2 < last) g2 = advance(g1, t2);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) rid2[rb] = row_of(t2, g2, rb, rok2[rb]);
+
+    f64x4 acc[RB][CB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[rb][j][r] = 0.0;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      // four column blocks at a time: their b values, then the four steps
+      // over them (four or more independent accumulators between two MFMAs
+      // that share one)
+#pragma unroll
+      for (int jg = 0; jg < CB; jg += 4) {
+        double bv[4][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const double* bp = &Bs[16 * (jg + j) + li][16 * c + 2 * q];
+          double x[2], y[2];
+          load_n<double, 2>(bp, x);
+          load_n<double, 2>(bp + 8, y);
+          bv[j][0] = x[0];
+          bv[j][1] = x[1];
+          bv[j][2] = y[0];
+          bv[j][3] = y[1];
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+              acc[rb][jg + j] = __builtin_amdgcn_mfma_f64_16x16x4f64(
+                  af[c % RS][rb][s], bv[j][s], acc[rb][jg + j], 0, 0, 0);
+      }
+      // chunk c's values are used: request the chunk RS later (after the
+      // last tile, row 0's: loaded, never used), here and not later, where
+      // the scheduler would otherwise sink these loads
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        if (c + RS < NCH)
+          load_chunk(base[rb], c + RS, af[c % RS][rb]);
+        else
+          load_chunk(base_n[rb], c + RS - NCH, af[c % RS][rb]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // lane (i, q) holds column i of block rows q + 4r in acc[rb][j][r];
+    // rows past the group and columns past N go to the sink
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int32_t orow = __shfl(rok[rb] ? rid[rb] : -1, q + 4 * r);
+        double* o = p.out + (int64_t)(orow >= 0 ? orow : 0) * p.N + n0 + li;
+#pragma unroll
+        for (int j = 0; j < CB; ++j) {
+          double* d = orow >= 0 && n0 + 16 * j + li < p.N ? o + 16 * j : sink + 16 * j + li;
+          *d = acc[rb][j][r];
+        }
+      }
+    }
+    if (!has_next) return false;
+    ++tile;
+    g = g1;
+    g1 = g2;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      rid[rb] = rid1[rb];
+      rok[rb] = rok1[rb];
+      rid1[rb] = rid2[rb];
+      rok1[rb] = rok2[rb];
+    }
+    return true;
+  };
+  while (run_tile()) {
+  }
+}
+
 // ---------------------------------------------------------------- grouping
 // Exclusive prefixes of the group lengths and of their tile counts
 // ceil(len / tm), 1024 groups at a time by one workgroup (a scan in LDS per
@@ -792,12 +1030,13 @@ inline int split_slices(int64_t N, int64_t Kp) {
 }
 
 // Bytes of the b region: bt (float32 / float64 transposed) or, for float32,
-// the three bf16 planes (6 bytes per value) and their finiteness flags.
+// the three bf16 planes (6 bytes per value) and their finiteness flags; for
+// float64, then the float64 kernel's store sink.
 template <class T>
 int64_t b_region_bytes(int64_t K, int64_t N, int64_t R) {
   const int64_t v = R * N * gemm_kp<T>(K);
   if (sizeof(T) == 4) return ws_align(v * 6) + ws_align(R * SB_MAX_SLICES * 4);
-  return ws_align(v * (int64_t)sizeof(T));
+  return ws_align(v * (int64_t)sizeof(T)) + ws_align(F64_SINK * 8);
 }
 
 // Workspace of one grouped GEMM: the b region, then the grouping.
@@ -813,13 +1052,15 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather) {
   constexpr int EVH = 16 / sizeof(T);
   const bool split = sizeof(T) == 4 && Kp <= SB_KMAX && Kp == L.K &&
                         reinterpret_cast<uintptr_t>(L.a) % 16 == 0 && L.K % EVH == 0;
-  const int tm = split ? SB_TM : GBM;
+  const bool f64 = sizeof(T) == 8 && Kp <= F64_KMAX && Kp == L.K && aligned16(L.a);
+  const int tm = split ? SB_TM : (f64 ? F64_TM : GBM);
   char* w = static_cast<char*>(L.workspace);
   T* bt = reinterpret_cast<T*>(w);
   const int64_t vals = L.R * L.N * Kp;
   uint16_t* bt3 = reinterpret_cast<uint16_t*>(w);
   int32_t* bflags = reinterpret_cast<int32_t*>(w + ws_align(vals * 6));
   const int slices = split_slices(L.N, Kp);
+  double* sink = reinterpret_cast<double*>(w + ws_align(vals * 8));  // float64 only
   w += b_region_bytes<T>(L.K, L.N, L.R);
 
   if (split) {
@@ -876,6 +1117,34 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather) {
         default: hipLaunchKernelGGL((grouped_gemm_split_kernel<8>), grid, block, 0, L.stream, a, bt3,
                              bflags, slices, bsrc, L.trans_b, per, a.tile_ptr, a.group_off); break;
       }
+      return hipGetLastError();
+    }
+  }
+  if constexpr (sizeof(T) == 8) {
+    if (f64) {
+      // as for the split kernel: one workgroup per CU (its LDS block), each a
+      // contiguous range of tiles
+      const int64_t mt = (L.n + F64_TM - 1) / F64_TM + L.R;
+      int64_t wgs = 256 / nt;
+      if (wgs < 1) wgs = 1;
+      if (wgs > mt) wgs = mt;
+      const int64_t per = (mt + wgs - 1) / wgs;
+      const dim3 grid((unsigned)wgs, (unsigned)nt), block(64 * F64_NW);
+#define MDGL_F64_CASE(C)                                                                     \
+  case C:                                                                                    \
+    if (gather)                                                                              \
+      hipLaunchKernelGGL((grouped_gemm_f64_kernel<C, F64_RB, F64_NW, true>), grid, block, 0,  \
+                         L.stream, a, per, a.tile_ptr, a.group_off, sink);                   \
+    else                                                                                     \
+      hipLaunchKernelGGL((grouped_gemm_f64_kernel<C, F64_RB, F64_NW, false>), grid, block, 0, \
+                         L.stream, a, per, a.tile_ptr, a.group_off, sink);                   \
+    break;
+      switch (Kp / 16) {
+        MDGL_F64_CASE(1) MDGL_F64_CASE(2) MDGL_F64_CASE(3) MDGL_F64_CASE(4)
+        MDGL_F64_CASE(5) MDGL_F64_CASE(6) MDGL_F64_CASE(7) MDGL_F64_CASE(8)
+        default: return hipErrorInvalidValue;
+      }
+#undef MDGL_F64_CASE
       return hipGetLastError();
     }
   }

@@ -1340,6 +1340,90 @@ def test_grouped_mm_block_resident_shapes(d1, d2):
     np.testing.assert_array_equal(gm, want)
 
 
+@pytest.mark.parametrize("d1", [16, 48, 64, 112, 128])
+@pytest.mark.parametrize("d2", [1, 5, 128, 130, 256])
+def test_grouped_mm_float64_block_resident_shapes(d1, d2):
+    """The float64 kernel that keeps a b block in LDS (K a multiple of 16 up
+    to 128, rows of a 16-byte aligned): odd and even chunk counts, output
+    widths below, at and past one 128-column tile (columns past the width
+    and rows past a group go to the store sink), groups that are empty,
+    shorter than a 128-row tile or span many tiles; segment_mm and gather_mm
+    against the oracle, and gather_mm against segment_mm on the stably
+    sorted rows bit for bit."""
+    rng = np.random.default_rng(d1 * 1000 + d2 + 7)
+    r = 11
+    seglen = np.array([0, 1, 127, 128, 129, 255, 700, 0, 3, 2000, 257])
+    n = int(seglen.sum())
+    a = rng.normal(size=(n, d1))
+    b = rng.normal(size=(r, d1, d2)) / np.sqrt(d1)
+    idx = np.repeat(np.arange(r), seglen)
+    rng.shuffle(idx)
+    at, bt = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    out = torch.full((n + 1, d2), 7.0, dtype=torch.float64, device="cuda")
+    seg = ops.segment_mm(at, bt, seglen).cpu().numpy()
+    close(seg, oracle.segment_mm(a, b, seglen, np.float64),
+          oracle.segment_mm(np.abs(a), np.abs(b), seglen, np.float64), np.float64,
+          "segment_mm d1 {} d2 {}".format(d1, d2))
+    gm = ops.gather_mm(at, bt, idx_b=torch.from_numpy(idx).cuda()).cpu().numpy()
+    close(gm, oracle.gather_mm(a, b, idx, np.float64),
+          oracle.gather_mm(np.abs(a), np.abs(b), idx, np.float64), np.float64,
+          "gather_mm d1 {} d2 {}".format(d1, d2))
+    perm = np.argsort(idx, kind="stable")
+    want = np.empty_like(gm)
+    want[perm] = ops.segment_mm(a[perm], b, np.bincount(idx, minlength=r))
+    np.testing.assert_array_equal(gm, want)
+    # through the ABI into a buffer one row longer: the row past n is untouched
+    from mojodgl import _lib
+    L = _lib.lib()
+    code = _lib.dtype_code(np.float64)
+    ws_n = L.mdgl_segment_mm_workspace_bytes(n, d1, d2, r, code)
+    ws = torch.empty(max(ws_n, 1), dtype=torch.uint8, device="cuda")
+    sl = torch.from_numpy(seglen.astype(np.int64)).cuda()
+    assert L.mdgl_segment_mm(at.data_ptr(), bt.data_ptr(), out.data_ptr(), sl.data_ptr(), n, d1,
+                             r, d2, ws.data_ptr(), ws_n, code, _lib.stream()) == 0
+    o = out.cpu().numpy()
+    np.testing.assert_array_equal(o[:n], seg)
+    assert np.all(o[n] == 7.0)
+
+
+@pytest.mark.parametrize("case", ["inf_nan", "k_not_16", "unaligned"])
+def test_grouped_mm_float64_other_paths(case):
+    """float64 beside the block-resident kernel: inf and NaN propagate as in
+    IEEE arithmetic (the oracle on the same values), and shapes it does not
+    take (K not a multiple of 16, rows of a off a 16-byte boundary) go to the
+    general kernel with results within the tolerance rule."""
+    rng = np.random.default_rng(73)
+    r = 5
+    seglen = np.array([300, 0, 129, 1000, 77])
+    n = int(seglen.sum())
+    k = 24 if case == "k_not_16" else 64
+    a = rng.normal(size=(n, k))
+    b = rng.normal(size=(r, k, 40)) / np.sqrt(k)
+    if case == "inf_nan":
+        a[3, 5] = np.inf
+        a[10, 0] = -np.inf
+        a[20, 7] = np.nan
+        b[3, 9, 1] = np.inf
+    at = torch.from_numpy(a).cuda()
+    if case == "unaligned":
+        flat = torch.empty(n * k + 1, dtype=torch.float64, device="cuda")
+        at = flat[1:].view(n, k)
+        at.copy_(torch.from_numpy(a))
+    idx = np.repeat(np.arange(r), seglen)
+    seg = ops.segment_mm(at, torch.from_numpy(b).cuda(), seglen).cpu().numpy()
+    gat = ops.gather_mm(at, torch.from_numpy(b).cuda(),
+                        idx_b=torch.from_numpy(idx).cuda()).cpu().numpy()
+    with np.errstate(all="ignore"):
+        ref = oracle.segment_mm(a, b, seglen, np.float64)
+        bound = oracle.segment_mm(np.abs(a), np.abs(b), seglen, np.float64)
+    for got, what in ((seg, "segment_mm"), (gat, "gather_mm")):
+        fin = np.isfinite(ref)
+        assert np.array_equal(np.isnan(got), np.isnan(ref)), what
+        assert np.array_equal(got[np.isinf(ref)], ref[np.isinf(ref)]), what
+        close(got[fin], ref[fin], bound[fin], np.float64, what)
+    np.testing.assert_array_equal(seg, gat)
+
+
 def _grouped_both(a, b, seglen, idx):
     """segment_mm and gather_mm of the same rows on the GPU (numpy out)."""
     at, bt = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
