@@ -62,6 +62,10 @@ template <> struct Mfma<double> {
 };
 
 constexpr int GBM = 128, GBN = 128;
+// Workspace bytes where the block-resident kernels send the stores of rows
+// past a group and columns past N, so that every store is issued (see the
+// float64 kernel).
+constexpr int GEMM_SINK_BYTES = GBN * 8;
 
 template <class T>
 struct GemmArgs {
@@ -361,11 +365,12 @@ static __global__ __launch_bounds__(BLOCK) void split_b_kernel(const float* __re
   if (threadIdx.x == 0) flags[blockIdx.x] = bad;
 }
 
-template <int NCH>
+template <int NCH, bool GATHER, bool OUTV>
 __global__ __launch_bounds__(SB_THREADS, 1) void grouped_gemm_split_kernel(
     GemmArgs<float> p, const uint16_t* __restrict__ bt3, const int32_t* __restrict__ bflags,
     int slices, const float* __restrict__ b, int given_t, int64_t tiles_per_wg,
-    const int32_t* __restrict__ tile_ptr, const int32_t* __restrict__ group_off) {
+    const int32_t* __restrict__ tile_ptr, const int32_t* __restrict__ group_off,
+    float* __restrict__ sink) {
   typedef float f32x16 __attribute__((ext_vector_type(16)));
   __shared__ __align__(16) uint16_t Bs[3][GBN][SB_LD];
   const int t = threadIdx.x;
@@ -384,15 +389,25 @@ __global__ __launch_bounds__(SB_THREADS, 1) void grouped_gemm_split_kernel(
   auto uget = [](const int32_t* __restrict__ arr, int64_t i) -> int64_t {
     return arr[__builtin_amdgcn_readfirstlane((int)i)];
   };
-  // the row of a behind tile row 32w + lr (-1 past the group; its loads then
-  // read row 0, never stored)
-  auto row_of = [&](int64_t tl, int64_t gg) -> int32_t {
+  auto advance = [&](int64_t gg, int64_t tl) -> int64_t {
+    while (uget(tile_ptr, gg + 1) <= tl) ++gg;
+    return gg;
+  };
+  // The row of a behind tile row 32w + lr and whether there is one (rows
+  // past the group load row 0 and store to the sink); gather_mm's come
+  // through the permutation, requested a tile ahead. As in the float64
+  // kernel, the loads and stores of the tile loop are unconditional, so each
+  // wait covers only the loads it is for.
+  auto row_of = [&](int64_t tl, int64_t gg, bool& ok) -> int32_t {
     const int64_t m0 = uget(group_off, gg) + (tl - uget(tile_ptr, gg)) * SB_TM;
     const int64_t pos = m0 + w * 32 + lr;
-    return pos < uget(group_off, gg + 1) ? (p.perm ? p.perm[pos] : (int32_t)pos) : -1;
+    const int64_t end = uget(group_off, gg + 1);
+    ok = pos < end;
+    if constexpr (GATHER) return p.perm[ok ? pos : end - 1];
+    return (int32_t)pos;
   };
-  auto base_of = [&](int32_t r) -> const float* {
-    return p.a + (int64_t)(r >= 0 ? r : 0) * p.K + 8 * hf;
+  auto base_of = [&](int32_t r, bool ok) -> const float* {
+    return p.a + (int64_t)(ok ? r : 0) * p.K + 8 * hf;
   };
   // 8 consecutive floats (two 16-byte loads) from a row of a
   auto load_chunk = [&](const float* q, float (&d)[8]) {
@@ -421,14 +436,22 @@ __global__ __launch_bounds__(SB_THREADS, 1) void grouped_gemm_split_kernel(
     }
     g = lo;
   }
-  int32_t rid = row_of(tile, g);
-  const float* base = base_of(rid);
+  // rows of this tile and of the next one (group g1; past the last tile,
+  // this tile's)
+  int64_t g1 = g;
+  if (tile + 1 < last) g1 = advance(g, tile + 1);
+  bool rok, rok1;
+  int32_t rid = row_of(tile, g, rok);
+  int32_t rid1 = row_of(tile + 1 < last ? tile + 1 : tile, g1, rok1);
+  const float* base = base_of(rid, rok);
   // a values in a ring of RS chunks: chunk c lives in af[c % RS] and, once
   // used, its slot takes the chunk RS later (this tile's or the next one's)
   constexpr int RS = NCH >= 4 ? NCH / 2 : NCH;
   float af[RS][8];
 #pragma unroll
   for (int c = 0; c < RS; ++c) load_chunk(base + 16 * c, af[c]);
+  // waited for here, once: see the float64 kernel
+  __builtin_amdgcn_s_waitcnt(0);
 
   int64_t cur_g = -1;
   bool b_whole = false;  // the group's b block has a value that does not split
@@ -455,14 +478,13 @@ __global__ __launch_bounds__(SB_THREADS, 1) void grouped_gemm_split_kernel(
       cur_g = g;
     }
     const bool has_next = tile + 1 < last;
-    int64_t g_n = g;
-    int32_t rid_n = -1;
-    const float* base_n = base;
-    if (has_next) {
-      while (uget(tile_ptr, g_n + 1) <= tile + 1) ++g_n;
-      rid_n = row_of(tile + 1, g_n);
-      base_n = base_of(rid_n);
-    }
+    const float* base_n = base_of(rid1, rok1);
+    // the rows of the tile after the next (past the last tile, the next one's)
+    int64_t g2 = g1;
+    const int64_t t2 = tile + 2 < last ? tile + 2 : tile + 1;
+    if (tile + 2 < last) g2 = advance(g1, t2);
+    bool rok2;
+    const int32_t rid2 = row_of(t2, g2, rok2);
     f32x16 acc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -525,18 +547,22 @@ __global__ __launch_bounds__(SB_THREADS, 1) void grouped_gemm_split_kernel(
           }
         }
       }
-      // chunk c's values are used: request the chunk RS later
+      // chunk c's values are used: request the chunk RS later (after the
+      // last tile, row 0's: loaded, never used)
       if (c + RS < NCH)
         load_chunk(base + 16 * (c + RS), af[c % RS]);
-      else if (has_next)
+      else
         load_chunk(base_n + 16 * (c + RS - NCH), af[c % RS]);
+      __builtin_amdgcn_sched_barrier(0);
     }
     // lane (lr, hf) holds column lr of rows 8q + 4hf + r in acc[j][4q + r];
     // the quad transpose gives lane 4k4 + s4 row 8q + 4hf + s4 at columns
-    // 4k4 .. 4k4 + 3
+    // 4k4 .. 4k4 + 3. Rows past the group and columns past N go to the sink.
+    // (16-byte stores with OUTV, else element by element; one form per
+    // kernel: the compiler's wait counts are exact only with a single one)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int32_t orow = __shfl(rid, 8 * q + 4 * hf + s4);
+      const int32_t orow = __shfl(rok ? rid : -1, 8 * q + 4 * hf + s4);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float x[4];
@@ -544,21 +570,25 @@ __global__ __launch_bounds__(SB_THREADS, 1) void grouped_gemm_split_kernel(
         for (int v = 0; v < 4; ++v) x[v] = acc[j][4 * q + v];
         quad_transpose(x, s4);
         const int64_t n = n0 + 32 * j + 4 * k4;
-        if (orow < 0 || n >= p.N) continue;
-        float* o = p.out + (int64_t)orow * p.N + n;
-        if (p.out_vec && n + 4 <= p.N) {
-          store_n<float, 4>(o, x);
+        float* o = p.out + (int64_t)(orow >= 0 ? orow : 0) * p.N + n;
+        float* sk = sink + 32 * j + 4 * k4;
+        if constexpr (OUTV) {
+          // N is a multiple of 4: a piece is wholly inside or wholly past N
+          store_n<float, 4>(orow >= 0 && n < p.N ? o : sk, x);
         } else {
 #pragma unroll
-          for (int v = 0; v < 4; ++v)
-            if (n + v < p.N) o[v] = x[v];
+          for (int v = 0; v < 4; ++v) *(orow >= 0 && n + v < p.N ? o + v : sk + v) = x[v];
         }
       }
     }
     if (!has_next) return false;
     ++tile;
-    g = g_n;
-    rid = rid_n;
+    g = g1;
+    g1 = g2;
+    rid = rid1;
+    rok = rok1;
+    rid1 = rid2;
+    rok1 = rok2;
     base = base_n;
     return true;
   };
@@ -595,7 +625,6 @@ constexpr int F64_KMAX = 128;
 constexpr int F64_LD = F64_KMAX + 4;  // doubles per LDS row
 constexpr int F64_RB = 1, F64_NW = 8;  // the library's shape: 128-row tiles
 constexpr int F64_TM = 16 * F64_RB * F64_NW;
-constexpr int F64_SINK = GBN;  // doubles of the store sink in the workspace
 
 template <int NCH, int RB, int NW, bool GATHER>
 __global__ __launch_bounds__(64 * NW, 1) void grouped_gemm_f64_kernel(
@@ -1030,13 +1059,14 @@ inline int split_slices(int64_t N, int64_t Kp) {
 }
 
 // Bytes of the b region: bt (float32 / float64 transposed) or, for float32,
-// the three bf16 planes (6 bytes per value) and their finiteness flags; for
-// float64, then the float64 kernel's store sink.
+// the three bf16 planes (6 bytes per value) and their finiteness flags; then
+// the store sink of the block-resident kernels.
 template <class T>
 int64_t b_region_bytes(int64_t K, int64_t N, int64_t R) {
   const int64_t v = R * N * gemm_kp<T>(K);
-  if (sizeof(T) == 4) return ws_align(v * 6) + ws_align(R * SB_MAX_SLICES * 4);
-  return ws_align(v * (int64_t)sizeof(T)) + ws_align(F64_SINK * 8);
+  const int64_t sink = ws_align(GEMM_SINK_BYTES);
+  if (sizeof(T) == 4) return ws_align(v * 6) + ws_align(R * SB_MAX_SLICES * 4) + sink;
+  return ws_align(v * (int64_t)sizeof(T)) + sink;
 }
 
 // Workspace of one grouped GEMM: the b region, then the grouping.
@@ -1060,8 +1090,8 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather) {
   uint16_t* bt3 = reinterpret_cast<uint16_t*>(w);
   int32_t* bflags = reinterpret_cast<int32_t*>(w + ws_align(vals * 6));
   const int slices = split_slices(L.N, Kp);
-  double* sink = reinterpret_cast<double*>(w + ws_align(vals * 8));  // float64 only
   w += b_region_bytes<T>(L.K, L.N, L.R);
+  void* sink = w - ws_align(GEMM_SINK_BYTES);
 
   if (split) {
     hipLaunchKernelGGL(split_b_kernel, dim3((unsigned)(L.R * slices)), dim3(BLOCK), 0, L.stream,
@@ -1107,16 +1137,26 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather) {
       const int64_t per = (mt + wgs - 1) / wgs;
       const dim3 grid((unsigned)wgs, (unsigned)nt), block(SB_THREADS);
       const float* bsrc = static_cast<const float*>(L.b);
+      float* fsink = static_cast<float*>(sink);
+#define MDGL_SPLIT_LAUNCH(C, G, V)                                                              \
+  hipLaunchKernelGGL((grouped_gemm_split_kernel<C, G, V>), grid, block, 0, L.stream, a, bt3, \
+                     bflags, slices, bsrc, L.trans_b, per, a.tile_ptr, a.group_off, fsink)
+#define MDGL_SPLIT_CASE(C)                                       \
+  case C:                                                      \
+    if (gather) {                                              \
+      if (a.out_vec) MDGL_SPLIT_LAUNCH(C, true, true);         \
+      else MDGL_SPLIT_LAUNCH(C, true, false);                  \
+    } else {                                                   \
+      if (a.out_vec) MDGL_SPLIT_LAUNCH(C, false, true);        \
+      else MDGL_SPLIT_LAUNCH(C, false, false);                 \
+    }                                                          \
+    break;
       switch (Kp / 16) {
-        case 2: hipLaunchKernelGGL((grouped_gemm_split_kernel<2>), grid, block, 0, L.stream, a, bt3,
-                             bflags, slices, bsrc, L.trans_b, per, a.tile_ptr, a.group_off); break;
-        case 4: hipLaunchKernelGGL((grouped_gemm_split_kernel<4>), grid, block, 0, L.stream, a, bt3,
-                             bflags, slices, bsrc, L.trans_b, per, a.tile_ptr, a.group_off); break;
-        case 6: hipLaunchKernelGGL((grouped_gemm_split_kernel<6>), grid, block, 0, L.stream, a, bt3,
-                             bflags, slices, bsrc, L.trans_b, per, a.tile_ptr, a.group_off); break;
-        default: hipLaunchKernelGGL((grouped_gemm_split_kernel<8>), grid, block, 0, L.stream, a, bt3,
-                             bflags, slices, bsrc, L.trans_b, per, a.tile_ptr, a.group_off); break;
+        MDGL_SPLIT_CASE(2) MDGL_SPLIT_CASE(4) MDGL_SPLIT_CASE(6) MDGL_SPLIT_CASE(8)
+        default: return hipErrorInvalidValue;
       }
+#undef MDGL_SPLIT_CASE
+#undef MDGL_SPLIT_LAUNCH
       return hipGetLastError();
     }
   }
@@ -1134,10 +1174,10 @@ hipError_t launch_grouped(const GemmLaunch& L, bool gather) {
   case C:                                                                                    \
     if (gather)                                                                              \
       hipLaunchKernelGGL((grouped_gemm_f64_kernel<C, F64_RB, F64_NW, true>), grid, block, 0,  \
-                         L.stream, a, per, a.tile_ptr, a.group_off, sink);                   \
+                         L.stream, a, per, a.tile_ptr, a.group_off, static_cast<double*>(sink)); \
     else                                                                                     \
       hipLaunchKernelGGL((grouped_gemm_f64_kernel<C, F64_RB, F64_NW, false>), grid, block, 0, \
-                         L.stream, a, per, a.tile_ptr, a.group_off, sink);                   \
+                         L.stream, a, per, a.tile_ptr, a.group_off, static_cast<double*>(sink)); \
     break;
       switch (Kp / 16) {
         MDGL_F64_CASE(1) MDGL_F64_CASE(2) MDGL_F64_CASE(3) MDGL_F64_CASE(4)
