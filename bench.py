@@ -954,11 +954,14 @@ def section_c3(args):
     # the same CSR (destination rows, degrees, slot order, edge weights) with
     # every source folded into the first 1,024 nodes (a 2.4 MB table, which
     # each XCD's 4 MB L2 holds) or into the first block's 4,600 nodes (11 MB,
-    # which the 256 MB MALL holds): the rate of the gathers when they hit
+    # which the 256 MB MALL holds): the rate of the gathers when they hit.
+    # The folded graph keeps the original's lane layout (its locality, which
+    # picks the column slab width), so only where the sources sit changes.
     log("c3 cache-resident ceilings")
     ceilings = {}
     for label, fold in (("l2_resident_1024_rows", 1024), ("mall_resident_4600_rows", 4600)):
         gc = dgl.graph((u % fold, v), num_nodes=N)
+        gc._locality = g._source_locality()
         gc._device_csr("in")
         ccalls = {
             "u_mul_e_sum": lambda: ops.u_mul_e_sum(gc, h, w),

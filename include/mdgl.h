@@ -51,6 +51,13 @@ extern "C" {
  * elements, stride = dl rounded up to a multiple of 128 bytes (lhs itself
  * 128-byte aligned) */
 #define MDGL_LHS_LINE_ROWS 8
+/* mdgl_gspmm: rows wider than one 64-lane slab (256 float32 / 128 float64
+ * columns with 16-byte lanes) are cut into 32-lane slabs, two rows to a
+ * wavefront, when that makes at most 5 slabs -- for graphs whose sources lie
+ * near their destinations (mdgl_coo_locality), where a narrower slab of a
+ * block of neighbouring rows stays in cache. Results are the same bit for
+ * bit; only the lane layout changes. */
+#define MDGL_NARROW_SLABS 32
 /* mdgl_segment_reduce(_arg): the caller knows that no segment has more than
  * MDGL_SEGMENT_SPLIT_ROWS rows, so the pass that splits longer segments is
  * not launched (a longer segment is then still reduced whole, in row order) */
@@ -145,15 +152,25 @@ int mdgl_gspmm(const int32_t* indptr, const int32_t* indices, const int32_t* eid
                int64_t workspace_bytes, int flags, int dtype, void* stream);
 
 /* The lane width (values per lane: 1, 2 or 4 in float32, 1 or 2 in
- * float64) mdgl_gspmm picks for these operands, shapes, alignments and
- * flags, so a caller can tell how many rows share a wavefront (a row takes
- * ceil(dout / vec) lanes; 32 or fewer: several rows per wavefront) and how
- * many 64-lane column slabs a row is cut into. No counterpart in the
+ * float64) and, when `group` is not null, the lanes per row slab (a power
+ * of two up to 64) that mdgl_gspmm picks for these operands, shapes,
+ * alignments and flags, so a caller can tell how many rows share a
+ * wavefront (64 / group) and how many column slabs a row is cut into
+ * (ceil(ceil(dout / vec) / group)). No counterpart in the
  * reference (its kernel is a CPU loop, src/ported.mojo:352-423); it is the
  * planning query behind the host's scheduling choices for a gspmm call. */
 int mdgl_gspmm_lanes(int op, int64_t dl, int64_t dr, int64_t dout, int nd,
                      const int64_t* lhs_shape, const int64_t* rhs_shape, const void* lhs,
-                     const void* rhs, int flags, int dtype, int64_t* vec);
+                     const void* rhs, int flags, int dtype, int64_t* vec, int64_t* group);
+
+/* Locality of a graph for mdgl_gspmm's MDGL_NARROW_SLABS: partial[b]
+ * (device int64, MDGL_COO_LOCALITY_BLOCKS of them) receives workgroup b's
+ * count of the edges i (COO u, v on the GPU, int32) with |u[i] - v[i]| <
+ * window; their sum is the count over all edges. No counterpart in the
+ * reference (a scheduling statistic, computed once per graph). */
+#define MDGL_COO_LOCALITY_BLOCKS 1024
+int mdgl_coo_locality(const int32_t* u, const int32_t* v, int64_t num_edges, int64_t window,
+                      int64_t* partial, void* stream);
 
 /* Workspace mdgl_gspmm needs for `num_chunks` chunk partials. */
 int64_t mdgl_gspmm_workspace_bytes(int64_t num_chunks, int64_t dout, int reduce_op, int dtype);

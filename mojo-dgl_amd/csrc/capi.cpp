@@ -444,6 +444,26 @@ void choose_gspmm_lanes(GspmmParams& p, int op, int64_t dl, int64_t dr, int64_t 
   }
 }
 
+// Lanes per row slab: the power of two covering the row's vectors, at most
+// 64. With MDGL_NARROW_SLABS, rows wider than 64 vectors take 32-lane slabs
+// (two rows per wavefront) when that makes at most GSPMM_NARROW_MAX_SLABS of
+// them: each slab walks all of a row's edges again, and on a graph whose
+// sources lie near their destinations the 512-byte slabs of a block of
+// neighbouring rows stay in an XCD's 4 MB L2 where 1 KB slabs do not
+// (float32 602-column rows: 3 -> 5 walks, 10-14 % faster on a 50-block
+// community graph; float64 ones: 5 -> 10 walks, 1-4 % slower, so excluded).
+constexpr int GSPMM_NARROW_MAX_SLABS = 5;
+int gspmm_group(int64_t dout, int vec, int flags, bool dot) {
+  const int64_t nvec = (dout + vec - 1) / vec;
+  int gmax = WAVE;
+  if ((flags & MDGL_NARROW_SLABS) && !dot && nvec > WAVE &&
+      (nvec + WAVE / 2 - 1) / (WAVE / 2) <= GSPMM_NARROW_MAX_SLABS)
+    gmax = WAVE / 2;
+  int g = 1;
+  while (g < nvec && g < gmax) g <<= 1;
+  return g;
+}
+
 // The broadcast descriptor of a gspmm's operands (copy ops and nd = 0: the
 // identity); 0 or a failure status.
 int gspmm_bcast(int op, int64_t dl, int64_t dr, int64_t dout, int nd, const int64_t* lhs_shape,
@@ -560,6 +580,7 @@ int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* e
   }
   const int vw = vec_width(dtype);
   choose_gspmm_lanes(p, op, dl, dr, dout, lhs, rhs, es, dtype, dot_out != nullptr);
+  p.group = gspmm_group(dout, p.vec, flags, dot_out != nullptr);
   if (p.vec > 1 && dout % p.vec == 0 && aligned(dst, p.vec * es)) p.flags |= F_OUT_VEC;
   if (dot_out) {
     // the fused dot: mul / sum, 16-byte lanes, lhs rows contiguous, the edge
@@ -618,7 +639,7 @@ int mdgl_gspmm(const int32_t* indptr, const int32_t* indices, const int32_t* eid
 
 int mdgl_gspmm_lanes(int op, int64_t dl, int64_t dr, int64_t dout, int nd,
                      const int64_t* lhs_shape, const int64_t* rhs_shape, const void* lhs,
-                     const void* rhs, int flags, int dtype, int64_t* vec) {
+                     const void* rhs, int flags, int dtype, int64_t* vec, int64_t* group) {
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "gspmm_lanes: bad dtype %d", dtype);
   if (op < OP_ADD || op > OP_COPY_RHS || op == OP_DOT)
     return fail(MDGL_EINVAL, "gspmm_lanes: bad op %d", op);
@@ -634,7 +655,19 @@ int mdgl_gspmm_lanes(int op, int64_t dl, int64_t dr, int64_t dout, int nd,
   }
   choose_gspmm_lanes(p, op, dl, dr, dout, lhs, rhs, es, dtype, false);
   *vec = p.vec;
+  if (group) *group = gspmm_group(dout, p.vec, flags, false);
   return MDGL_OK;
+}
+
+static_assert(MDGL_COO_LOCALITY_BLOCKS == COO_LOCALITY_BLOCKS, "one count per workgroup");
+
+int mdgl_coo_locality(const int32_t* u, const int32_t* v, int64_t num_edges, int64_t window,
+                      int64_t* partial, void* stream) {
+  if (num_edges < 0 || window < 0) return fail(MDGL_EINVAL, "coo_locality: negative size");
+  if (!partial) return fail(MDGL_EINVAL, "coo_locality: null output");
+  if (num_edges > 0 && (!u || !v)) return fail(MDGL_EINVAL, "coo_locality: null endpoints");
+  return hip_status(launch_coo_locality(u, v, num_edges, window, partial, (hipStream_t)stream),
+                    "coo_locality");
 }
 
 int mdgl_gspmm_mul_sum_dot(const int32_t* indptr, const int32_t* indices, const int32_t* eid,

@@ -226,6 +226,31 @@ __global__ __launch_bounds__(BLOCK) void gather_i32_kernel(const int32_t* __rest
     out[i] = src[idx[i]];
 }
 
+// Each workgroup counts its grid-stride share of the edges whose endpoints
+// differ by less than `window` and writes the count to partial[blockIdx.x]
+// (no atomics: the caller adds the COO_LOCALITY_BLOCKS counts).
+__global__ __launch_bounds__(BLOCK) void coo_locality_kernel(const int32_t* __restrict__ u,
+                                                             const int32_t* __restrict__ v,
+                                                             int64_t n, int64_t window,
+                                                             int64_t* __restrict__ partial) {
+  __shared__ int64_t sums[WAVES_PER_BLOCK];
+  int64_t c = 0;
+  for (int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * BLOCK) {
+    const int64_t d = (int64_t)u[i] - (int64_t)v[i];
+    c += (d < window && -d < window) ? 1 : 0;
+  }
+  for (int off = WAVE / 2; off > 0; off >>= 1) c += __shfl_xor(c, off);
+  const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+  if (lane == 0) sums[w] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t t = 0;
+    for (int i = 0; i < WAVES_PER_BLOCK; ++i) t += sums[i];
+    partial[blockIdx.x] = t;
+  }
+}
+
 unsigned grid_of(int64_t n) {
   int64_t b = (n + BLOCK - 1) / BLOCK;
   if (b > 65536) b = 65536;
@@ -296,6 +321,13 @@ hipError_t launch_build_csr(const int32_t* key, const int32_t* other, int64_t nu
   if (num_edges && other)
     hipLaunchKernelGGL(gather_i32_kernel, dim3(grid_of(num_edges)), dim3(BLOCK), 0, stream,
                        other, eid, indices, num_edges);
+  return hipGetLastError();
+}
+
+hipError_t launch_coo_locality(const int32_t* u, const int32_t* v, int64_t n, int64_t window,
+                               int64_t* partial, hipStream_t s) {
+  hipLaunchKernelGGL(coo_locality_kernel, dim3(COO_LOCALITY_BLOCKS), dim3(BLOCK), 0, s, u, v, n,
+                     window, partial);
   return hipGetLastError();
 }
 

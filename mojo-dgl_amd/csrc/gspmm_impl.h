@@ -445,8 +445,7 @@ hipError_t launch_gspmm_op(const GspmmParams& p) {
   a.flags = p.flags;
   a.vec = VEC;
   const int64_t nvec = (p.dout + VEC - 1) / VEC;
-  int G = 1;
-  while (G < nvec && G < WAVE) G <<= 1;
+  const int G = p.group;  // chosen by the host (gspmm_group)
   a.G = G;
   a.S = (int)((nvec + G - 1) / G);
   a.num_chunks = p.num_chunks;

@@ -37,6 +37,7 @@ struct GspmmParams {
   int op, red;  // red in {SUM, MAX, MIN}; mean is F_MEAN
   int flags;
   int vec;      // elements per lane (1 or 16 / sizeof(T))
+  int group;    // lanes per row slab (a power of two, at most 64)
   int64_t num_chunks;
   const int32_t* chunk_row;
   const int32_t* chunk_start;
@@ -59,6 +60,12 @@ struct GspmmParams {
 
 template <class T, int RED>
 hipError_t launch_gspmm_red(const GspmmParams& p);
+
+// Per-block counts of the edges i with |u[i] - v[i]| < window, into
+// partial[0 .. COO_LOCALITY_BLOCKS) (csr.hip).
+constexpr int COO_LOCALITY_BLOCKS = 1024;
+hipError_t launch_coo_locality(const int32_t* u, const int32_t* v, int64_t n, int64_t window,
+                               int64_t* partial, hipStream_t s);
 
 // segment_reduce: out[s, k] = red over value rows offsets[s] .. offsets[s+1]
 // (segment_impl.h). red in {SUM, MAX, MIN}, mean is F_MEAN; arg (max / min,

@@ -53,6 +53,8 @@ FLOAT32, FLOAT64 = 0, 1
 REPLACE_INF = 1
 RHS_CSR_ORDER = 2
 LHS_LINE_ROWS = 8  # mdgl_gspmm: lhs rows copied to start on 128-byte lines
+NARROW_SLABS = 32  # mdgl_gspmm: 32-lane column slabs for wide rows (a local graph)
+COO_LOCALITY_BLOCKS = 1024  # counts written by mdgl_coo_locality
 SEGMENTS_SHORT = 4  # mdgl_segment_reduce: no segment longer than SEGMENT_SPLIT_ROWS
 SEGMENTS_SKIP_LONG = 8  # mdgl_segment_reduce: longer segments left for a LONG_ONLY call
 SEGMENTS_LONG_ONLY = 16  # mdgl_segment_reduce: only the segments longer than SEGMENT_SPLIT_ROWS
@@ -78,7 +80,8 @@ _SIGNATURES = {
     "mdgl_gspmm": ([_P, _P, _P, _P, _P, _P, _I64, _C, _I64, _I64, _I64, _C, _P, _C, _P, _P, _P,
                     _P, _P, _P, _I64, _I32, _P, _P, _I64, _P, _I64, _C, _C, _P], _C),
     "mdgl_gspmm_workspace_bytes": ([_I64, _I64, _C, _C], _I64),
-    "mdgl_gspmm_lanes": ([_C, _I64, _I64, _I64, _C, _P, _P, _P, _P, _C, _C, _P], _C),
+    "mdgl_gspmm_lanes": ([_C, _I64, _I64, _I64, _C, _P, _P, _P, _P, _C, _C, _P, _P], _C),
+    "mdgl_coo_locality": ([_P, _P, _I64, _I64, _P, _P], _C),
     "mdgl_edge_softmax_positional": ([_P, _I64, _P, _I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P,
                                       _P, _I64, _C, _P], _C),
     "mdgl_edge_softmax_positional_workspace_bytes": ([_I64, _I64, _I64, _P, _P, _C], _I64),

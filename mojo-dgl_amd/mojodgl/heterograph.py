@@ -53,6 +53,11 @@ CHUNK_LEN = 512
 # pull runs a builtin pass over every edge (no subgraph) when the pulled rows
 # hold at least 1 / PULL_FULL_PASS of the edges
 PULL_FULL_PASS = 8
+# a graph is local when at least LOCAL_FRACTION of its edges join nodes whose
+# ids differ by less than LOCAL_WINDOW (the rows whose 512-byte column slabs
+# fill an XCD's 4 MB L2); gspmm then cuts wide rows into narrower slabs
+LOCAL_WINDOW = 4096
+LOCAL_FRACTION = 0.5
 
 
 def chunk_plan(indptr: np.ndarray, chunk_len: int):
@@ -249,6 +254,29 @@ class DGLGraph(object):
         self._csr = {}
         self._draw = {}
         self._dcsr = {}
+        self._locality = None
+
+    def _source_locality(self):
+        """Fraction of the edges whose source id lies within LOCAL_WINDOW of
+        their destination id (once per graph, counted on the GPU by
+        mdgl_coo_locality): high on graphs whose node ids follow their
+        communities, where narrower gspmm column slabs of a block of
+        neighbouring rows stay in cache."""
+        if self._locality is None:
+            if self._E == 0:
+                self._locality = 0.0
+            else:
+                u, v = self._device_coo()
+                part = torch.empty(_lib.COO_LOCALITY_BLOCKS, dtype=torch.int64, device=u.device)
+                _lib.check(_lib.lib().mdgl_coo_locality(u.data_ptr(), v.data_ptr(), self._E,
+                                                        LOCAL_WINDOW, part.data_ptr(),
+                                                        _lib.stream()), "coo_locality")
+                self._locality = int(part.cpu().numpy().sum()) / self._E
+        return self._locality
+
+    def _local(self):
+        """Whether gspmm should cut wide rows into narrower column slabs."""
+        return self._source_locality() >= LOCAL_FRACTION
 
     @property
     def _u(self):

@@ -31,16 +31,16 @@ CSR_ORDER_MIN_EDGES = 1 << 20
 
 def _lanes(code, dl, dr, dout, nd, ls, rs, lhs, rhs, flags, dtype):
     """(packed, slabs) of the lane layout mdgl_gspmm picks for these operands
-    (mdgl_gspmm_lanes): whether several rows share a wavefront (a row's
-    lanes number 32 or fewer) and how many 64-lane column slabs a row is cut
+    and flags (mdgl_gspmm_lanes): whether several rows share a wavefront
+    (slabs of 32 lanes or fewer) and how many column slabs a row is cut
     into."""
-    vec = ctypes.c_int64()
+    vec, group = ctypes.c_int64(), ctypes.c_int64()
     _lib.check(_lib.lib().mdgl_gspmm_lanes(
         code, dl, dr, dout, nd, None if ls is None else ls.ctypes.data,
         None if rs is None else rs.ctypes.data, _lib.ptr(lhs), _lib.ptr(rhs), flags,
-        _lib.dtype_code(dtype), ctypes.byref(vec)), "gspmm_lanes")
+        _lib.dtype_code(dtype), ctypes.byref(vec), ctypes.byref(group)), "gspmm_lanes")
     lanes = -(-dout // vec.value)
-    return lanes <= 32, -(-lanes // 64)
+    return group.value <= 32, -(-lanes // group.value)
 
 
 def _line_rows(lhs, rows, dl, num_edges, dtype):
@@ -129,6 +129,10 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
                 lhs = lined
                 flags |= _lib.LHS_LINE_ROWS
         packed, slabs = _lanes(code, dl, dr, dout, nd, ls, rs, lhs, rhs, flags, dtype)
+        if slabs > 1 and g._local():
+            # wide rows on a graph whose sources lie near their destinations
+            flags |= _lib.NARROW_SLABS
+            packed, slabs = _lanes(code, dl, dr, dout, nd, ls, rs, lhs, rhs, flags, dtype)
         sched = csr.chunks
         if narrow_split and packed and narrow_split < sched.chunk_len:
             sched = csr.chunks_for(narrow_split)

@@ -47,8 +47,9 @@ def err(lib):
 
 
 def test_gspmm_lane_query(lib):
-    """mdgl_gspmm_lanes reports the lane width mdgl_gspmm launches with
-    (host pointers stand in: the query reads only their alignment)."""
+    """mdgl_gspmm_lanes reports the lane width and lanes per row slab
+    mdgl_gspmm launches with (host pointers stand in: the query reads only
+    their alignment)."""
     import numpy as np
     from mojodgl import _lib
 
@@ -56,15 +57,21 @@ def test_gspmm_lane_query(lib):
     base = (buf.ctypes.data + 255) // 256 * 256          # 256-byte aligned
     mul, cl = _lib.BINARY_OPS["mul"], _lib.OP_COPY_LHS
 
-    def vec(op, dl, dr, dout, lshape=None, rshape=None, lhs=base, rhs=base, flags=0, dt=0):
-        out = ctypes.c_int64(-1)
+    def lanes(op, dl, dr, dout, lshape=None, rshape=None, lhs=base, rhs=base, flags=0, dt=0):
+        out, grp = ctypes.c_int64(-1), ctypes.c_int64(-1)
         nd = 0 if lshape is None else len(lshape)
         ls = None if lshape is None else (ctypes.c_int64 * nd)(*lshape)
         rs = None if rshape is None else (ctypes.c_int64 * nd)(*rshape)
         rc = lib.mdgl_gspmm_lanes(op, dl, dr, dout, nd, ls, rs, lhs, rhs, flags, dt,
-                                  ctypes.byref(out))
+                                  ctypes.byref(out), ctypes.byref(grp))
         assert rc == 0, err(lib)
-        return out.value
+        rc = lib.mdgl_gspmm_lanes(op, dl, dr, dout, nd, ls, rs, lhs, rhs, flags, dt,
+                                  ctypes.byref(out), None)     # the group is optional
+        assert rc == 0, err(lib)
+        return out.value, grp.value
+
+    def vec(*args, **kw):
+        return lanes(*args, **kw)[0]
 
     assert vec(cl, 64, 64, 64) == 4                      # 16-byte float32 lanes
     assert vec(cl, 64, 64, 64, dt=1) == 2                # 16-byte float64 lanes
@@ -78,11 +85,21 @@ def test_gspmm_lane_query(lib):
     assert vec(mul, 48, 8, 48, (8, 6), (8, 1)) == 2
     # heads of 3 columns: one element per lane
     assert vec(mul, 12, 4, 12, (4, 3), (4, 1)) == 1
+    # lanes per slab: the power of two covering the row's lanes, at most 64;
+    # with NARROW_SLABS 32 for wider rows when that makes at most 5 slabs
+    line, narrow = _lib.LHS_LINE_ROWS, _lib.LHS_LINE_ROWS | _lib.NARROW_SLABS
+    assert lanes(cl, 64, 64, 64) == (4, 16)
+    assert lanes(cl, 602, 602, 602, flags=line) == (4, 64)             # 151 lanes, 3 slabs
+    assert lanes(cl, 602, 602, 602, flags=narrow) == (4, 32)           # 5 slabs
+    assert lanes(cl, 602, 602, 602, flags=narrow, dt=1) == (2, 64)     # 301 lanes: 10 would be
+    assert lanes(cl, 256, 256, 256, flags=_lib.NARROW_SLABS, dt=1) == (2, 32)   # 4 slabs
+    assert lanes(cl, 256, 256, 256, flags=_lib.NARROW_SLABS) == (4, 64)         # one slab
+    assert lanes(mul, 256, 8, 256, (8, 32), (8, 1), flags=_lib.NARROW_SLABS) == (4, 64)
     rc = lib.mdgl_gspmm_lanes(_lib.BINARY_OPS["dot"], 4, 4, 4, 0, None, None, base, base, 0, 0,
-                              ctypes.byref(ctypes.c_int64()))
+                              ctypes.byref(ctypes.c_int64()), None)
     assert rc == -1 and "op" in err(lib)
     rc = lib.mdgl_gspmm_lanes(cl, 64, 64, 64, 0, None, None, base + 16, base,
-                              _lib.LHS_LINE_ROWS, 0, ctypes.byref(ctypes.c_int64()))
+                              _lib.LHS_LINE_ROWS, 0, ctypes.byref(ctypes.c_int64()), None)
     assert rc == -1 and "128-byte" in err(lib)
 
 

@@ -239,6 +239,99 @@ def test_gspmm_line_aligned_rows(dtype, d):
         np.testing.assert_array_equal(got, want, err_msg="{} {} d={}".format(oop, red, d))
 
 
+def _block_graph(n, e, block, inside, seed):
+    """Edges mostly inside blocks of `block` consecutive node ids (a fraction
+    `inside`), the rest uniform: the community layout of a local graph."""
+    rng = np.random.default_rng(seed)
+    v = rng.integers(0, n, e)
+    local = rng.random(e) < inside
+    lo = (v // block) * block
+    u = np.where(local, lo + rng.integers(0, block, e), rng.integers(0, n, e))
+    return np.minimum(u, n - 1), v
+
+
+@pytest.mark.parametrize("dtype,d", [(np.float32, 602), (np.float32, 300), (np.float64, 256),
+                                     (np.float64, 602)])
+def test_gspmm_narrow_slabs_are_bit_identical(dtype, d, monkeypatch):
+    """On a local graph, gspmm cuts rows wider than one 64-lane slab into
+    32-lane slabs (MDGL_NARROW_SLABS, two rows per wavefront) when that makes
+    at most 5 slabs: values and args bit-identical to the 64-lane layout for
+    sum / mean / max / min with and without an edge weight, rows split into
+    chunks or not; against the oracle bit-exact for whole rows and max/min,
+    within the tolerance for split sums (chunk partials fold in chunk
+    order)."""
+    from mojodgl.ops import spmm
+
+    n, e = 3000, 120000
+    u, v = _block_graph(n, e, 300, 0.95, 40 + d)
+    rng = np.random.default_rng(41 + d)
+    x = rng.normal(size=(n, d)).astype(dtype)
+    w = rng.random((e, 1)).astype(dtype)
+    results = {}
+    for local in (True, False):
+        monkeypatch.setattr(hg, "LOCAL_FRACTION", 0.0 if local else 2.0)
+        g = dgl.graph((u, v), num_nodes=n)
+        assert g._local() is local
+        for chunk in (512, 16):
+            monkeypatch.setattr(hg, "CHUNK_LEN", chunk)
+            for oop, red, L, R in (("mul", "sum", x, w), ("copy_lhs", "mean", x, None),
+                                   ("copy_lhs", "max", x, None), ("mul", "min", x, w)):
+                got, (au, ae) = spmm._gspmm(g, oop, red, L, R)
+                results[(local, chunk, oop, red)] = (got, au, ae)
+    for key, (got, au, ae) in results.items():
+        local, chunk, oop, red = key
+        L, R = x, (w if oop == "mul" else None)
+        what = "{} {} local={} chunk={}".format(oop, red, local, chunk)
+        wide = results[(False, chunk, oop, red)]
+        for a_, b_ in zip((got, au, ae), wide):
+            if a_ is not None:
+                np.testing.assert_array_equal(a_, b_, err_msg=what + " against 64 lanes")
+        if red in ("max", "min"):
+            want, ru, re_ = oracle.gspmm(u, v, n, oop, red, L, R, dtype, with_arg=True)
+            np.testing.assert_array_equal(au, ru, err_msg=what)
+            np.testing.assert_array_equal(ae, re_, err_msg=what)
+            np.testing.assert_array_equal(got, want, err_msg=what)
+            continue
+        want = oracle.gspmm(u, v, n, oop, red, L, R, dtype)
+        if chunk == 512:
+            np.testing.assert_array_equal(got, want, err_msg=what)
+        else:
+            absx = np.abs(x)
+            bound = oracle.gspmm(u, v, n, oop, red, absx, R, dtype)
+            close(got, want, bound, dtype, what)
+
+
+def test_coo_locality_counts_and_graph_predicate():
+    """mdgl_coo_locality: the per-workgroup counts add up to the number of
+    edges with |u - v| < window (numpy), for windows 0, 1, 4096 and one past
+    every difference, and for no edges; a block graph is local, a uniform one
+    is not."""
+    from mojodgl import _lib
+
+    L = _lib.lib()
+    rng = np.random.default_rng(44)
+    n, e = 200000, 1_000_003
+    u = rng.integers(0, n, e).astype(np.int32)
+    v = np.where(rng.random(e) < 0.3, np.clip(u + rng.integers(-5000, 5000, e), 0, n - 1),
+                 rng.integers(0, n, e)).astype(np.int32)
+    ut, vt = torch.from_numpy(u).cuda(), torch.from_numpy(v).cuda()
+    part = torch.full((_lib.COO_LOCALITY_BLOCKS,), -7, dtype=torch.int64, device="cuda")
+    diff = np.abs(u.astype(np.int64) - v.astype(np.int64))
+    for window in (0, 1, 4096, n + 1):
+        assert L.mdgl_coo_locality(ut.data_ptr(), vt.data_ptr(), e, window, part.data_ptr(),
+                                   _lib.stream()) == 0
+        assert int(part.cpu().numpy().sum()) == int((diff < window).sum()), window
+    assert L.mdgl_coo_locality(None, None, 0, 4096, part.data_ptr(), _lib.stream()) == 0
+    assert np.all(part.cpu().numpy() == 0)
+    assert L.mdgl_coo_locality(None, None, 0, 4096, None, _lib.stream()) == _lib.EINVAL
+    bu, bv = _block_graph(100000, 500000, 4000, 0.95, 45)
+    assert dgl.graph((bu, bv), num_nodes=100000)._local()
+    ru, rv = rand_graph(100000, 500000, 46)
+    assert not dgl.graph((ru, rv), num_nodes=100000)._local()
+    none = np.zeros(0, dtype=np.int64)
+    assert dgl.graph((none, none), num_nodes=5)._source_locality() == 0.0
+
+
 def test_gspmm_power_law_hubs_against_oracle():
     """Degrees spanning 0 .. 5000 with the default split threshold."""
     rng = np.random.default_rng(7)
