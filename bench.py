@@ -256,6 +256,80 @@ def run_steps(step, steps, warmup, timer):
     return (t1 - t0) * 1e3 / steps
 
 
+class _CountingLib:
+    """Stands in for the loaded libmdgl handle and counts its mdgl_* calls."""
+
+    def __init__(self, real):
+        self._real = real
+        self.calls = {}
+
+    def __getattr__(self, name):
+        attr = getattr(self._real, name)
+        if not name.startswith("mdgl_"):
+            return attr
+
+        def counted(*a):
+            self.calls[name] = self.calls.get(name, 0) + 1
+            return attr(*a)
+        return counted
+
+
+def host_accounting(calls, reps):
+    """Host-side cost of each public call (the reference's profile_deep.py
+    counts ctypes calls and allocations per op; bench/analysis.md:84 its
+    glue time): the libmdgl entry points one call makes, by name; the device
+    allocations it asks torch's caching allocator for (requests and bytes;
+    the allocator serves them from its cache after the first call); the host
+    time until the call returns (its GPU work enqueued, not finished), median
+    of `reps`; and the time per call when `reps` calls run back to back (HIP
+    events), which the host time bounds for small ops. Each call runs once
+    first, so the graph's one-time set-up (CSR build, schedules) is not
+    counted."""
+    import torch
+
+    from mojodgl import _lib
+
+    out = {}
+    real = _lib.lib()
+    s = torch.cuda.Event(enable_timing=True)
+    t = torch.cuda.Event(enable_timing=True)
+    for name, fn_ in calls.items():
+        fn_()
+        torch.cuda.synchronize()
+        proxy = _CountingLib(real)
+        m0 = torch.cuda.memory_stats()
+        _lib._lib = proxy
+        try:
+            fn_()
+        finally:
+            _lib._lib = real
+        m1 = torch.cuda.memory_stats()
+        torch.cuda.synchronize()
+        host = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn_()
+            host.append(time.perf_counter() - t0)
+        torch.cuda.synchronize()
+        s.record()
+        for _ in range(reps):
+            fn_()
+        t.record()
+        torch.cuda.synchronize()
+        out[name] = {
+            "lib_calls": sum(proxy.calls.values()),
+            "entry_points": dict(sorted(proxy.calls.items())),
+            "device_allocations": int(m1.get("allocation.all.allocated", 0)
+                                      - m0.get("allocation.all.allocated", 0)),
+            "device_alloc_bytes": int(m1.get("allocated_bytes.all.allocated", 0)
+                                      - m0.get("allocated_bytes.all.allocated", 0)),
+            "host_us": round(float(np.median(host)) * 1e6, 1),
+            "back_to_back_us": round(s.elapsed_time(t) * 1e3 / reps, 1),
+        }
+    return out
+
+
 class ColdTimer:
     """Per-op GPU time: `warmup` untimed calls, then `reps` calls, each
     between two HIP events on torch's current stream (where libmdgl
@@ -452,6 +526,14 @@ def workload_gat(args):
         "kernels": kernels,
     }
     if not args.step_only:
+        log("host-side cost per call of the step's ops")
+        e0 = ops.u_add_v(g, el, er)
+        a0 = ops.edge_softmax(g, e0)
+        result["host_accounting"] = host_accounting({
+            "gsddmm_u_add_v": lambda: ops.u_add_v(g, el, er),
+            "edge_softmax": lambda: ops.edge_softmax(g, e0),
+            "gspmm_u_mul_e_sum": lambda: ops.u_mul_e_sum(g, h, a0)}, 5)
+        del e0, a0
         log("the step's ops alone with cold caches")
         result["cold_caches"] = time_gat_ops_cold(g, el, er, h, N, E, H, D, args)
         log("outside the step: graph build, edge_softmax over a subset, forward + backward")
@@ -794,6 +876,12 @@ def section_c1(args):
             f()
         torch.cuda.synchronize()
         extra[name] = round((time.perf_counter() - t0) * 1e3 / args.steps, 4)
+    acct = {"update_all_u_mul_e_" + red: (lambda r=red: call(r)) for red in reds}
+    acct["pull_u_mul_e_sum"] = lambda: g.pull(pull_nodes, fn.u_mul_e("h", "e", "m"),
+                                              fn.sum("m", "z"))
+    acct["update_all_sum_numpy_inputs"] = lambda: g2.update_all(fn.u_mul_e("h", "e", "m"),
+                                                                fn.sum("m", "z"))
+    accounting = host_accounting(acct, 200)
     out = {"workload": "update_all u_mul_e + sum/mean/max/min, uniform graph, float32",
            "num_nodes": N, "num_edges": E, "feat": D,
            "note": "cache-resident and launch-bound: 55-60 MB of algorithmic bytes per call",
@@ -801,7 +889,7 @@ def section_c1(args):
            "unit": "GEdge·feat/s", "ops": ops_out,
            "graph_replay": {"ms_per_step": round(gms, 4),
                             "value": round(4 * units / gms / 1e6, 2)},
-           "outside_step_ms": extra}
+           "outside_step_ms": extra, "host_accounting": accounting}
     if not args.no_cpu_baseline:
         oracle, L, cores = oracle_setup()
         indptr, indices, eid = oracle.csr(u, v, N, "dst")

@@ -29,11 +29,28 @@ __all__ = ["gspmm"]
 CSR_ORDER_MIN_EDGES = 1 << 20
 
 
+_LANES = {}
+
+
 def _lanes(code, dl, dr, dout, nd, ls, rs, lhs, rhs, flags, dtype):
     """(packed, slabs) of the lane layout mdgl_gspmm picks for these operands
     and flags (mdgl_gspmm_lanes): whether several rows share a wavefront
     (slabs of 32 lanes or fewer) and how many column slabs a row is cut
-    into."""
+    into. The answer depends only on the sizes, shapes, flags, dtype and the
+    operands' alignment (within 128 bytes), so it is kept per such key: the
+    query costs more host time than a small gspmm's kernel."""
+    key = (code, dl, dr, dout, nd, None if ls is None else tuple(ls),
+           None if rs is None else tuple(rs), _lib.ptr(lhs) % 128 if lhs is not None else -1,
+           _lib.ptr(rhs) % 128 if rhs is not None else -1, flags, np.dtype(dtype).str)
+    got = _LANES.get(key)
+    if got is None:
+        if len(_LANES) >= 4096:  # many distinct shapes: start over rather than grow
+            _LANES.clear()
+        got = _LANES[key] = _lanes_query(code, dl, dr, dout, nd, ls, rs, lhs, rhs, flags, dtype)
+    return got
+
+
+def _lanes_query(code, dl, dr, dout, nd, ls, rs, lhs, rhs, flags, dtype):
     vec, group = ctypes.c_int64(), ctypes.c_int64()
     _lib.check(_lib.lib().mdgl_gspmm_lanes(
         code, dl, dr, dout, nd, None if ls is None else ls.ctypes.data,

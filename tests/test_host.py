@@ -432,3 +432,22 @@ def test_bench_measures_one_gpu_only():
                          capture_output=True, text=True, timeout=120)
     assert out.returncode == 2
     assert "one GPU" in out.stderr
+
+
+def test_bench_host_accounting_counts_library_calls():
+    """bench.py's per-call accounting stands in for the library handle and
+    counts its mdgl_* calls by name, passing everything else through."""
+    import bench
+
+    class Fake:
+        other = 5
+
+        def mdgl_a(self, x):
+            return x + 1
+
+        def mdgl_b(self):
+            return "b"
+
+    c = bench._CountingLib(Fake())
+    assert c.mdgl_a(1) == 2 and c.mdgl_a(2) == 3 and c.mdgl_b() == "b" and c.other == 5
+    assert c.calls == {"mdgl_a": 2, "mdgl_b": 1}
