@@ -429,6 +429,18 @@ void choose_gspmm_lanes(GspmmParams& p, int op, int64_t dl, int64_t dr, int64_t 
           : (dtype == MDGL_FLOAT32 && dout % 2 == 0 ? 2 : 1);
   p.lmode = op == OP_COPY_RHS ? M_CONTIG : pick_mode(p.bc, true, dout, p.vec, dl, lhs, es, lined);
   p.rmode = op == OP_COPY_LHS ? M_CONTIG : pick_mode(p.bc, false, dout, p.vec, dr, rhs, es);
+  // float64 rows of 129-256 columns: 32-byte lanes (two 16-byte loads each)
+  // make one 64-lane slab, so the row's edges are walked once instead of twice
+  if (dtype == MDGL_FLOAT64 && !dot && p.vec == vw && dout > WAVE * vw && dout <= 2 * WAVE * vw &&
+      dout % (2 * vw) == 0 && p.lmode != M_GATHER && p.rmode != M_GATHER) {
+    const int lm = op == OP_COPY_RHS ? M_CONTIG : pick_mode(p.bc, true, dout, 2 * vw, dl, lhs, es, lined);
+    const int rm = op == OP_COPY_LHS ? M_CONTIG : pick_mode(p.bc, false, dout, 2 * vw, dr, rhs, es);
+    if (lm != M_GATHER && rm != M_GATHER) {
+      p.vec = 2 * vw;
+      p.lmode = lm;
+      p.rmode = rm;
+    }
+  }
   if (!dot && !lined && p.vec > 1 && (p.lmode == M_GATHER || p.rmode == M_GATHER)) {
     for (int nv = p.vec / 2; nv >= 1; nv /= 2) {
       if (nv > 1 && dout % nv != 0) continue;

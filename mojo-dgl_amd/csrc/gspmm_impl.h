@@ -519,6 +519,8 @@ hipError_t launch_gspmm_red(const GspmmParams& p) {
   if (p.vec == VecOf<T>::n) return launch_gspmm_vec<T, RED, VecOf<T>::n>(p);
   if constexpr (VecOf<T>::n == 4) {
     if (p.vec == 2) return launch_gspmm_vec<T, RED, 2>(p);  // 8-byte lanes (even widths)
+  } else {
+    if (p.vec == 4) return launch_gspmm_vec<T, RED, 4>(p);  // 32-byte float64 lanes
   }
   return launch_gspmm_vec<T, RED, 1>(p);
 }

@@ -92,7 +92,12 @@ def test_gspmm_lane_query(lib):
     assert lanes(cl, 602, 602, 602, flags=line) == (4, 64)             # 151 lanes, 3 slabs
     assert lanes(cl, 602, 602, 602, flags=narrow) == (4, 32)           # 5 slabs
     assert lanes(cl, 602, 602, 602, flags=narrow, dt=1) == (2, 64)     # 301 lanes: 10 would be
-    assert lanes(cl, 256, 256, 256, flags=_lib.NARROW_SLABS, dt=1) == (2, 32)   # 4 slabs
+    assert lanes(cl, 130, 130, 130, flags=_lib.NARROW_SLABS, dt=1) == (2, 32)   # 65 lanes: 3
+    # float64 rows of 129-256 columns (a multiple of 4): 32-byte lanes, one slab
+    assert lanes(cl, 256, 256, 256, dt=1) == (4, 64)
+    assert lanes(cl, 200, 200, 200, dt=1) == (4, 64)
+    assert lanes(cl, 258, 258, 258, dt=1) == (2, 64)                            # 2 slabs
+    assert lanes(mul, 256, 8, 256, (8, 32), (8, 1), dt=1) == (4, 64)            # GAT heads
     assert lanes(cl, 256, 256, 256, flags=_lib.NARROW_SLABS) == (4, 64)         # one slab
     assert lanes(mul, 256, 8, 256, (8, 32), (8, 1), flags=_lib.NARROW_SLABS) == (4, 64)
     rc = lib.mdgl_gspmm_lanes(_lib.BINARY_OPS["dot"], 4, 4, 4, 0, None, None, base, base, 0, 0,

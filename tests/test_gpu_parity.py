@@ -110,6 +110,45 @@ def test_gspmm_feature_widths(d):
                                       err_msg="{} d={}".format(name, d))
 
 
+@pytest.mark.parametrize("d,heads", [(132, None), (200, None), (256, None), (256, 8), (260, None)])
+def test_gspmm_float64_wide_lanes(d, heads, chunk_len):
+    """float64 rows of 129-256 columns (a multiple of 4) take 32-byte lanes, one
+    slab per row (260 columns keep 16-byte lanes and two slabs): values and
+    args bit-identical to the oracle in float64, whole rows and rows split
+    into chunks, a full edge operand and one per head splat over its columns
+    (the GAT layout), every reducer."""
+    from mojodgl.ops import spmm
+
+    n, e = 300, 6000
+    u, v = rand_graph(n, e, 50 + d)
+    rng = np.random.default_rng(51 + d)
+    g = dgl.graph((u, v), num_nodes=n)
+    if heads:
+        x = rng.normal(size=(n, heads, d // heads))
+        w = rng.random((e, heads, 1))
+    else:
+        x = rng.normal(size=(n, d))
+        w = rng.normal(size=(e, d))
+    for oop, red in (("mul", "sum"), ("mul", "mean"), ("add", "max"), ("div", "min"),
+                     ("copy_lhs", "max")):
+        R = None if oop == "copy_lhs" else w
+        got, (au, ae) = spmm._gspmm(g, oop, red, x, R)
+        what = "{} {} d={} heads={} chunk={}".format(oop, red, d, heads, chunk_len)
+        if red in ("max", "min"):
+            want, ru, re_ = oracle.gspmm(u, v, n, oop, red, x, R, np.float64, with_arg=True)
+            np.testing.assert_array_equal(au, ru, err_msg=what)
+            np.testing.assert_array_equal(ae, re_, err_msg=what)
+            np.testing.assert_array_equal(got, want, err_msg=what)
+        else:
+            want = oracle.gspmm(u, v, n, oop, red, x, R, np.float64)
+            if chunk_len is None:
+                np.testing.assert_array_equal(got, want, err_msg=what)
+            else:
+                bound = oracle.gspmm(u, v, n, oop, red, np.abs(x), None if R is None
+                                     else np.abs(R), np.float64)
+                close(got, want, bound, np.float64, what)
+
+
 @pytest.mark.parametrize("longest", [600, 640, 641])
 def test_gspmm_rows_just_over_a_chunk(longest):
     """With 512-slot chunks, rows of up to 640 slots stay whole when no row is
