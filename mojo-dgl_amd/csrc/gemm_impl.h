@@ -1218,7 +1218,7 @@ struct TnArgs {
   int a_vec, g_vec, tiles_n;
 };
 
-template <class T, int BK>
+template <class T, int BK, bool VECT, bool GATHER>
 __global__ __launch_bounds__(BLOCK) void grouped_tn_kernel(TnArgs<T> p) {
   using M = Mfma<T>;
   using acc_t = typename M::acc_t;
@@ -1248,26 +1248,45 @@ __global__ __launch_bounds__(BLOCK) void grouped_tn_kernel(TnArgs<T> p) {
   const int li = lane & 15, h = lane >> 4;
 
   T ra[PASSES][EV], rb[PASSES][EV];
-  auto load_stage = [&](int64_t k0) {
+  // gather_mm's rows of a stage come through the permutation: they are
+  // requested one stage ahead (an unconditional load of a clamped index; the
+  // row test is applied where they are used), so no stage waits for them
+  auto stage_rows = [&](int64_t k0, int32_t (&rid)[PASSES]) {
+#pragma unroll
+    for (int q = 0; q < PASSES; ++q) {
+      const int64_t pos = k0 + q * RPP + t / CPR;
+      if constexpr (GATHER) rid[q] = p.perm[pos < r_end ? pos : r_end - 1];
+      else rid[q] = 0;
+    }
+  };
+  // Each lane's 16-byte pieces of a stage (VECT: both operands' rows allow
+  // them): rows past the chunk and pieces past the width load row 0 /
+  // column 0 and are zeroed when the stage is written to LDS, at the end of
+  // the stage (a test right after a load would wait for the load there);
+  // otherwise element by element. The form is fixed at compile time: chosen
+  // at run time, the compiler merged both into element loads.
+  bool oka[PASSES], okb[PASSES];
+  auto load_stage = [&](int64_t k0, const int32_t (&rids)[PASSES]) {
 #pragma unroll
     for (int q = 0; q < PASSES; ++q) {
       const int r = q * RPP + t / CPR;
       const int col = (t % CPR) * EV;
       const int64_t pos = k0 + r;
       const bool ok = pos < r_end;
-      const int64_t rid = ok ? (p.perm ? (int64_t)p.perm[pos] : pos) : 0;
+      const int64_t rid = ok ? (GATHER ? (int64_t)rids[q] : pos) : 0;
       const int64_t ca = m0 + col, cb = n0 + col;
-      if (ok && p.a_vec && ca + EV <= p.D1) {
-        load_vec<T>(p.a + rid * p.D1 + ca, ra[q]);
+      if constexpr (VECT) {
+        oka[q] = ok && ca < p.D1;  // D1 and D2 are multiples of EV
+        okb[q] = ok && cb < p.D2;
+        load_vec<T>(p.a + rid * p.D1 + (ca < p.D1 ? ca : 0), ra[q]);
+        load_vec<T>(p.g + rid * p.D2 + (cb < p.D2 ? cb : 0), rb[q]);
       } else {
+        oka[q] = okb[q] = true;
 #pragma unroll
-        for (int v = 0; v < EV; ++v) ra[q][v] = (ok && ca + v < p.D1) ? p.a[rid * p.D1 + ca + v] : T(0);
-      }
-      if (ok && p.g_vec && cb + EV <= p.D2) {
-        load_vec<T>(p.g + rid * p.D2 + cb, rb[q]);
-      } else {
-#pragma unroll
-        for (int v = 0; v < EV; ++v) rb[q][v] = (ok && cb + v < p.D2) ? p.g[rid * p.D2 + cb + v] : T(0);
+        for (int v = 0; v < EV; ++v) {
+          ra[q][v] = (ok && ca + v < p.D1) ? p.a[rid * p.D1 + ca + v] : T(0);
+          rb[q][v] = (ok && cb + v < p.D2) ? p.g[rid * p.D2 + cb + v] : T(0);
+        }
       }
     }
   };
@@ -1276,8 +1295,14 @@ __global__ __launch_bounds__(BLOCK) void grouped_tn_kernel(TnArgs<T> p) {
     for (int q = 0; q < PASSES; ++q) {
       const int r = q * RPP + t / CPR;
       const int col = (t % CPR) * EV;
-      store_vec<T>(&As[buf][r][col], ra[q]);
-      store_vec<T>(&Bs[buf][r][col], rb[q]);
+      T xa[EV], xb[EV];
+#pragma unroll
+      for (int v = 0; v < EV; ++v) {
+        xa[v] = oka[q] ? ra[q][v] : T(0);
+        xb[v] = okb[q] ? rb[q][v] : T(0);
+      }
+      store_vec<T>(&As[buf][r][col], xa);
+      store_vec<T>(&Bs[buf][r][col], xb);
     }
   };
 
@@ -1290,12 +1315,18 @@ __global__ __launch_bounds__(BLOCK) void grouped_tn_kernel(TnArgs<T> p) {
       for (int r = 0; r < 4; ++r) acc[i][j][r] = T(0);
 
   const int64_t nstages = (r_end - r0 + BK - 1) / BK;  // a chunk holds at least one row
-  load_stage(r0);
+  int32_t rid_a[PASSES], rid_b[PASSES];
+  stage_rows(r0, rid_a);
+  load_stage(r0, rid_a);
   store_stage(0);
+  stage_rows(r0 + BK, rid_a);  // the next stage's rows
   __syncthreads();
   for (int64_t s = 0; s < nstages; ++s) {
     const int buf = s & 1;
-    if (s + 1 < nstages) load_stage(r0 + (s + 1) * BK);
+    if (s + 1 < nstages) load_stage(r0 + (s + 1) * BK, rid_a);
+    stage_rows(r0 + (s + 2) * BK, rid_b);
+#pragma unroll
+    for (int q = 0; q < PASSES; ++q) rid_a[q] = rid_b[q];
     __builtin_amdgcn_s_setprio(1);  // MFMA issue first (as in the forward kernel)
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 4) {
@@ -1418,10 +1449,18 @@ hipError_t launch_grouped_grad(const GemmGradLaunch& L, bool gather) {
   // rows gathered through the permutation wait longer: shallower stages,
   // half the LDS, twice the workgroups per CU to cover them
   const dim3 grid((unsigned)max_chunks, (unsigned)(tiles_m * a.tiles_n));
-  if (perm)
-    hipLaunchKernelGGL((grouped_tn_kernel<T, 16>), grid, dim3(BLOCK), 0, L.stream, a);
+  const bool vect = a.a_vec && a.g_vec;
+  if (perm && vect)
+    hipLaunchKernelGGL((grouped_tn_kernel<T, 16, true, true>), grid, dim3(BLOCK), 0, L.stream, a);
+  else if (perm)
+    hipLaunchKernelGGL((grouped_tn_kernel<T, 16, false, true>), grid, dim3(BLOCK), 0, L.stream,
+                       a);
+  else if (vect)
+    hipLaunchKernelGGL((grouped_tn_kernel<T, Mfma<T>::BK, true, false>), grid, dim3(BLOCK), 0,
+                       L.stream, a);
   else
-    hipLaunchKernelGGL((grouped_tn_kernel<T, Mfma<T>::BK>), grid, dim3(BLOCK), 0, L.stream, a);
+    hipLaunchKernelGGL((grouped_tn_kernel<T, Mfma<T>::BK, false, false>), grid, dim3(BLOCK), 0,
+                       L.stream, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t E = L.D1 * L.D2;
