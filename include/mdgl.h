@@ -80,6 +80,14 @@ const char* mdgl_last_error(void);
  * shaped for (256 on MI355X), always > 1. */
 int64_t mdgl_workers(void);
 
+/* No counterpart in the reference (it has no tracing). 1 when the library
+ * pushes a roctx range named after each entry point around every call that
+ * validates or launches (the environment held MDGL_ROCTX, not "0", when the
+ * library first looked, and the ROCm roctx library
+ * librocprofiler-sdk-roctx.so.1 was found), else 0. The ranges are host
+ * time per call; `rocprofv3 --marker-trace` records them. */
+int mdgl_trace_ranges(void);
+
 /* Replaces capi.mojo:54-56. Inclusive int64 prefix sum, dst[i] = src[0..i]. */
 int mdgl_cumsum(const int64_t* src, int64_t* dst, int64_t n, void* stream);
 

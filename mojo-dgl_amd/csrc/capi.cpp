@@ -4,8 +4,11 @@
 // feature shapes into the collapsed broadcast descriptor, chooses per
 // operand how a lane loads its columns (16-byte vector, one splatted scalar,
 // or a scalar gather), and dispatches to the kernel launchers.
+#include <dlfcn.h>
+
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -19,6 +22,55 @@ using namespace mdgl;
 namespace {
 
 thread_local std::string g_last_error;
+
+// roctx ranges around the entry points. With MDGL_ROCTX set (to anything but
+// "0") when the library first needs it, the ROCm 7 roctx library is opened and
+// every entry point that validates or launches pushes a range named after
+// itself for the length of the call (host time: validation, workspace layout
+// and launches; `rocprofv3 --marker-trace` lists them beside the kernels).
+// Otherwise, or when the roctx library is not found, a range costs one load
+// and one branch. Ranges are per thread and nest, as roctx's push/pop ranges
+// do.
+struct Roctx {
+  int (*push)(const char*) = nullptr;
+  int (*pop)() = nullptr;
+};
+
+const Roctx& roctx() {
+  static const Roctx r = [] {
+    Roctx t;
+    const char* on = std::getenv("MDGL_ROCTX");
+    if (!on || !*on || std::strcmp(on, "0") == 0) return t;
+    void* h = dlopen("librocprofiler-sdk-roctx.so.1", RTLD_NOW | RTLD_LOCAL);
+    if (!h) h = dlopen("/opt/rocm/lib/librocprofiler-sdk-roctx.so.1", RTLD_NOW | RTLD_LOCAL);
+    if (!h) return t;
+    auto push = reinterpret_cast<int (*)(const char*)>(dlsym(h, "roctxRangePushA"));
+    auto pop = reinterpret_cast<int (*)()>(dlsym(h, "roctxRangePop"));
+    if (push && pop) {
+      t.push = push;
+      t.pop = pop;
+    }
+    return t;
+  }();
+  return r;
+}
+
+class Range {
+ public:
+  explicit Range(const char* name) : pop_(roctx().pop) {
+    if (pop_) roctx().push(name);
+  }
+  ~Range() {
+    if (pop_) pop_();
+  }
+  Range(const Range&) = delete;
+  Range& operator=(const Range&) = delete;
+
+ private:
+  int (*pop_)();
+};
+
+#define MDGL_RANGE() const Range mdgl_range_(__func__)
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -156,6 +208,8 @@ const char* mdgl_last_error(void) { return g_last_error.c_str(); }
 
 int64_t mdgl_workers(void) { return 256; }
 
+int mdgl_trace_ranges(void) { return roctx().pop != nullptr; }
+
 int64_t mdgl_segment_offsets_workspace_bytes(int64_t num) {
   return num < 0 ? -1 : segment_offsets_workspace_bytes(num);
 }
@@ -163,6 +217,7 @@ int64_t mdgl_segment_offsets_workspace_bytes(int64_t num) {
 int mdgl_segment_offsets(const int64_t* seglen, int64_t num, int64_t chunk_len, int32_t* offsets,
                          int64_t* stats, void* workspace, int64_t workspace_bytes,
                          void* stream) {
+  MDGL_RANGE();
   if (num < 0) return fail(MDGL_EINVAL, "segment_offsets: negative count");
   if (num >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "segment_offsets: 2**31 or more segments");
   if (!offsets || !stats || (num > 0 && !seglen))
@@ -179,6 +234,7 @@ int mdgl_segment_offsets(const int64_t* seglen, int64_t num, int64_t chunk_len, 
 }
 
 int mdgl_cumsum(const int64_t* src, int64_t* dst, int64_t n, void* stream) {
+  MDGL_RANGE();
   if (n < 0) return fail(MDGL_EINVAL, "cumsum: n must be >= 0");
   if (n > 0 && (!src || !dst)) return fail(MDGL_EINVAL, "cumsum: null buffer");
   return hip_status(launch_cumsum_i64(src, dst, n, (hipStream_t)stream), "cumsum");
@@ -189,6 +245,7 @@ int64_t mdgl_read_stream_sink_bytes(int64_t bytes) {
 }
 
 int mdgl_read_stream(const void* src, int64_t bytes, void* sink, void* stream) {
+  MDGL_RANGE();
   if (bytes < 0 || bytes % 16) return fail(MDGL_EINVAL, "read_stream: bytes must be a multiple of 16");
   if (bytes == 0) return MDGL_OK;
   if (!src || !sink) return fail(MDGL_EINVAL, "read_stream: null buffer");
@@ -205,6 +262,7 @@ int64_t mdgl_build_csr_workspace_bytes(int64_t num_edges, int64_t num_rows) {
 int mdgl_build_csr(const int32_t* key, const int32_t* other, int64_t num_edges, int64_t num_rows,
                    int32_t* indptr, int32_t* indices, int32_t* eid, void* workspace,
                    int64_t workspace_bytes, void* stream) {
+  MDGL_RANGE();
   if (num_edges < 0 || num_rows < 0) return fail(MDGL_EINVAL, "build_csr: negative size");
   if (num_edges >= (int64_t(1) << 31) || num_rows >= (int64_t(1) << 31))
     return fail(MDGL_EINVAL, "build_csr: 2**31 or more edges or rows");
@@ -228,6 +286,7 @@ int mdgl_build_csr(const int32_t* key, const int32_t* other, int64_t num_edges, 
 int mdgl_edge_softmax_grad(const int32_t* row_of, const void* a, const void* grad,
                            const void* row_sum, void* dst, int64_t num_edges, int64_t d, int dtype,
                            void* stream) {
+  MDGL_RANGE();
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "edge_softmax_grad: bad dtype %d", dtype);
   if (num_edges < 0 || d < 0) return fail(MDGL_EINVAL, "edge_softmax_grad: negative size");
   if (num_edges >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "edge_softmax_grad: 2**31 or more edges");
@@ -242,6 +301,7 @@ int mdgl_edge_softmax_grad(const int32_t* row_of, const void* a, const void* gra
 int mdgl_gspmm_edge_grad(const int32_t* vids, const int32_t* indptr, const void* grad_out,
                          const int32_t* arg_e, void* dst, int64_t num_edges, int64_t d, int mean,
                          double alpha, int dtype, void* stream) {
+  MDGL_RANGE();
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "gspmm_edge_grad: bad dtype %d", dtype);
   if (num_edges < 0 || d < 0) return fail(MDGL_EINVAL, "gspmm_edge_grad: negative size");
   if (num_edges >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "gspmm_edge_grad: 2**31 or more edges");
@@ -255,6 +315,7 @@ int mdgl_gspmm_edge_grad(const int32_t* vids, const int32_t* indptr, const void*
 
 int mdgl_rows_by_degree(const int32_t* indptr, const void* src, void* dst, int64_t rows,
                         int64_t d, int dtype, void* stream) {
+  MDGL_RANGE();
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "rows_by_degree: bad dtype %d", dtype);
   if (rows < 0 || d < 0) return fail(MDGL_EINVAL, "rows_by_degree: negative size");
   if (rows == 0 || d == 0) return MDGL_OK;
@@ -265,6 +326,7 @@ int mdgl_rows_by_degree(const int32_t* indptr, const void* src, void* dst, int64
 
 int mdgl_gather_rows(const void* src, const int32_t* idx, void* dst, int64_t n, int64_t width,
                      int dtype, void* stream) {
+  MDGL_RANGE();
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "gather_rows: bad dtype %d", dtype);
   if (n < 0 || width < 0) return fail(MDGL_EINVAL, "gather_rows: negative size");
   if (n == 0 || width == 0) return MDGL_OK;
@@ -275,6 +337,7 @@ int mdgl_gather_rows(const void* src, const int32_t* idx, void* dst, int64_t n, 
 
 int mdgl_scatter_rows(const void* src, const int32_t* idx, void* dst, int64_t n, int64_t width,
                       int dtype, void* stream) {
+  MDGL_RANGE();
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "scatter_rows: bad dtype %d", dtype);
   if (n < 0 || width < 0) return fail(MDGL_EINVAL, "scatter_rows: negative size");
   if (n == 0 || width == 0) return MDGL_OK;
@@ -285,6 +348,7 @@ int mdgl_scatter_rows(const void* src, const int32_t* idx, void* dst, int64_t n,
 
 int mdgl_keep_where(const void* mask, const void* src, void* dst, int64_t n, int dtype,
                     void* stream) {
+  MDGL_RANGE();
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "keep_where: bad dtype %d", dtype);
   if (n < 0) return fail(MDGL_EINVAL, "keep_where: n must be >= 0");
   if (n > 0 && (!mask || !src || !dst)) return fail(MDGL_EINVAL, "keep_where: null buffer");
@@ -293,6 +357,7 @@ int mdgl_keep_where(const void* mask, const void* src, void* dst, int64_t n, int
 }
 
 int mdgl_scale(const void* src, void* dst, int64_t n, double alpha, int dtype, void* stream) {
+  MDGL_RANGE();
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "scale: bad dtype %d", dtype);
   if (n < 0) return fail(MDGL_EINVAL, "scale: n must be >= 0");
   if (n > 0 && (!src || !dst)) return fail(MDGL_EINVAL, "scale: null buffer");
@@ -300,6 +365,7 @@ int mdgl_scale(const void* src, void* dst, int64_t n, double alpha, int dtype, v
 }
 
 int mdgl_replace_inf_with_zero(const void* src, void* dst, int64_t n, int dtype, void* stream) {
+  MDGL_RANGE();
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "replace_inf_with_zero: bad dtype %d", dtype);
   if (n < 0) return fail(MDGL_EINVAL, "replace_inf_with_zero: n must be >= 0");
   if (n > 0 && (!src || !dst)) return fail(MDGL_EINVAL, "replace_inf_with_zero: null buffer");
@@ -309,6 +375,7 @@ int mdgl_replace_inf_with_zero(const void* src, void* dst, int64_t n, int dtype,
 
 int mdgl_clamp_i64(const int64_t* src, int64_t* dst, int64_t n, int64_t lo, int64_t hi,
                    void* stream) {
+  MDGL_RANGE();
   if (n < 0) return fail(MDGL_EINVAL, "clamp_i64: n must be >= 0");
   if (n > 0 && (!src || !dst)) return fail(MDGL_EINVAL, "clamp_i64: null buffer");
   return hip_status(launch_clamp_i64(src, dst, n, lo, hi, (hipStream_t)stream), "clamp_i64");
@@ -318,6 +385,7 @@ int mdgl_gsddmm(const int32_t* uids, const int32_t* vids, const void* lhs, const
                 void* dst, int64_t num_edges, int lhs_target, int rhs_target, int op, int64_t dl,
                 int64_t dr, int64_t dout, int nd, const int64_t* lhs_shape,
                 const int64_t* rhs_shape, int dtype, void* stream) {
+  MDGL_RANGE();
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "gsddmm: bad dtype %d", dtype);
   if (op < OP_ADD || op > OP_COPY_RHS) return fail(MDGL_EINVAL, "gsddmm: bad op %d", op);
   if (lhs_target < 0 || lhs_target > 2 || rhs_target < 0 || rhs_target > 2)
@@ -643,6 +711,7 @@ int mdgl_gspmm(const int32_t* indptr, const int32_t* indices, const int32_t* eid
                int64_t num_chunks, int32_t chunk_len, const int32_t* heavy_rows,
                const int32_t* heavy_ptr, int64_t num_heavy, void* workspace,
                int64_t workspace_bytes, int flags, int dtype, void* stream) {
+  MDGL_RANGE();
   return gspmm_common(indptr, indices, eid, lhs, rhs, dst, num_dst, op, dl, dr, dout, reduce_op,
                       deg, nd, lhs_shape, rhs_shape, arg_u, arg_e, chunk_row, chunk_start,
                       num_chunks, chunk_len, heavy_rows, heavy_ptr, num_heavy, workspace,
@@ -652,6 +721,7 @@ int mdgl_gspmm(const int32_t* indptr, const int32_t* indices, const int32_t* eid
 int mdgl_gspmm_lanes(int op, int64_t dl, int64_t dr, int64_t dout, int nd,
                      const int64_t* lhs_shape, const int64_t* rhs_shape, const void* lhs,
                      const void* rhs, int flags, int dtype, int64_t* vec, int64_t* group) {
+  MDGL_RANGE();
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "gspmm_lanes: bad dtype %d", dtype);
   if (op < OP_ADD || op > OP_COPY_RHS || op == OP_DOT)
     return fail(MDGL_EINVAL, "gspmm_lanes: bad op %d", op);
@@ -675,6 +745,7 @@ static_assert(MDGL_COO_LOCALITY_BLOCKS == COO_LOCALITY_BLOCKS, "one count per wo
 
 int mdgl_coo_locality(const int32_t* u, const int32_t* v, int64_t num_edges, int64_t window,
                       int64_t* partial, void* stream) {
+  MDGL_RANGE();
   if (num_edges < 0 || window < 0) return fail(MDGL_EINVAL, "coo_locality: negative size");
   if (!partial) return fail(MDGL_EINVAL, "coo_locality: null output");
   if (num_edges > 0 && (!u || !v)) return fail(MDGL_EINVAL, "coo_locality: null endpoints");
@@ -690,6 +761,7 @@ int mdgl_gspmm_mul_sum_dot(const int32_t* indptr, const int32_t* indices, const 
                            int64_t num_chunks, int32_t chunk_len, const int32_t* heavy_rows,
                            const int32_t* heavy_ptr, int64_t num_heavy, void* workspace,
                            int64_t workspace_bytes, int dtype, void* stream) {
+  MDGL_RANGE();
   if (num_dst > 0 && dout > 0 && !dot) return fail(MDGL_EINVAL, "gspmm dot: null dot output");
   return gspmm_common(indptr, indices, eid, lhs, rhs, dst, num_dst, OP_MUL, dl, dr, dout, RED_SUM,
                       nullptr, nd, lhs_shape, rhs_shape, nullptr, nullptr, chunk_row, chunk_start,
@@ -741,6 +813,7 @@ int segment_common(const char* what, const int32_t* offsets, const void* value, 
 
 int mdgl_segment_reduce(const int32_t* offsets, const void* value, void* dst, int64_t num_seg,
                         int64_t d, int reduce_op, int64_t n, int flags, int dtype, void* stream) {
+  MDGL_RANGE();
   return segment_common("segment_reduce", offsets, value, dst, nullptr, num_seg, d, reduce_op, n,
                         flags, dtype, stream);
 }
@@ -748,6 +821,7 @@ int mdgl_segment_reduce(const int32_t* offsets, const void* value, void* dst, in
 int mdgl_segment_reduce_arg(const int32_t* offsets, const void* value, void* dst, int32_t* arg,
                             int64_t num_seg, int64_t d, int reduce_op, int64_t n, int flags,
                             int dtype, void* stream) {
+  MDGL_RANGE();
   if (reduce_op != RED_MAX && reduce_op != RED_MIN)
     return fail(MDGL_EINVAL, "segment_reduce_arg: reduce_op must be max or min, got %d", reduce_op);
   if (num_seg > 0 && d > 0 && !arg) return fail(MDGL_EINVAL, "segment_reduce_arg: null buffer");
@@ -757,6 +831,7 @@ int mdgl_segment_reduce_arg(const int32_t* offsets, const void* value, void* dst
 
 int mdgl_segment_ids(const int32_t* offsets, int64_t num_seg, int64_t n, int32_t* dst,
                      void* stream) {
+  MDGL_RANGE();
   if (num_seg < 0 || n < 0) return fail(MDGL_EINVAL, "segment_ids: negative size");
   if (num_seg >= (int64_t(1) << 31) || n >= (int64_t(1) << 31))
     return fail(MDGL_EINVAL, "segment_ids: 2**31 or more segments or rows");
@@ -783,6 +858,7 @@ static void softmax_geom(int64_t d, int dtype, const void* logits, const void* o
 
 int mdgl_softmax_geometry(int64_t d, int dtype, const void* logits, const void* out,
                           int64_t* slots, int64_t* chunk_len) {
+  MDGL_RANGE();
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "softmax_geometry: bad dtype %d", dtype);
   if (d <= 0 || !slots || !chunk_len) return fail(MDGL_EINVAL, "softmax_geometry: bad arguments");
   int vec;
@@ -906,6 +982,7 @@ int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, v
                          const int32_t* chunk_row, const int32_t* chunk_start,
                          const int32_t* chunk_first, int64_t num_chunks, int64_t slots,
                          void* workspace, int64_t workspace_bytes, int dtype, void* stream) {
+  MDGL_RANGE();
   (void)scratch;
   if (n < 0) return fail(MDGL_EINVAL, "segment_softmax: negative size");
   if (n >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "segment_softmax: 2**31 or more rows");
@@ -918,6 +995,7 @@ int mdgl_segment_softmax(const int32_t* offsets, const void* value, void* dst, v
 
 int mdgl_segment_softmax_short(const int32_t* offsets, const void* value, void* dst,
                                int64_t num_seg, int64_t d, int64_t n, int dtype, void* stream) {
+  MDGL_RANGE();
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "segment_softmax_short: bad dtype %d", dtype);
   if (num_seg < 0 || d < 0 || n < 0) return fail(MDGL_EINVAL, "segment_softmax_short: negative size");
   if (num_seg >= (int64_t(1) << 31) || n >= (int64_t(1) << 31))
@@ -949,6 +1027,7 @@ int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int3
                        const int32_t* chunk_first, int64_t num_chunks, int64_t slots,
                        const int32_t* slot_of_edge, int64_t num_edges, void* workspace,
                        int64_t workspace_bytes, int dtype, void* stream) {
+  MDGL_RANGE();
   (void)indices;
   (void)scratch;
   if (num_nodes > 0 && d > 0 && !eid) return fail(MDGL_EINVAL, "edge_softmax: null eid");
@@ -1005,6 +1084,7 @@ int mdgl_edge_softmax_positional(const int32_t* ends, int64_t num_edges, const i
                                  int32_t* group_pos, int64_t* id_range, void* range_event,
                                  void* workspace, int64_t workspace_bytes, int dtype,
                                  void* stream) {
+  MDGL_RANGE();
   const char* what = "edge_softmax_positional";
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "%s: bad dtype %d", what, dtype);
   if (num_edges < 0 || num_sel < 0 || num_nodes < 0 || d < 0)
@@ -1200,6 +1280,7 @@ int mdgl_segment_mm_grad(const void* a, const void* b, const void* grad_out,
                          const int64_t* seglen_a, void* grad_a, void* grad_b, int64_t n,
                          int64_t d1, int64_t r, int64_t d2, void* workspace,
                          int64_t workspace_bytes, int dtype, void* stream) {
+  MDGL_RANGE();
   return grouped_grad_common(a, b, grad_out, grad_a, grad_b, nullptr, seglen_a, n, d1, d2, r,
                              workspace, workspace_bytes, dtype, stream, false);
 }
@@ -1208,6 +1289,7 @@ int mdgl_gather_mm_grad(const void* a, const void* b, const int64_t* idx_b, cons
                         void* grad_a, void* grad_b, int64_t n, int64_t d1, int64_t d2,
                         int64_t r, void* workspace, int64_t workspace_bytes, int dtype,
                         void* stream) {
+  MDGL_RANGE();
   return grouped_grad_common(a, b, grad_out, grad_a, grad_b, idx_b, nullptr, n, d1, d2, r,
                              workspace, workspace_bytes, dtype, stream, true);
 }
@@ -1215,6 +1297,7 @@ int mdgl_gather_mm_grad(const void* a, const void* b, const int64_t* idx_b, cons
 int mdgl_segment_mm(const void* a, const void* b, void* dst, const int64_t* seglen_a, int64_t n,
                     int64_t d1, int64_t r, int64_t d2, void* workspace, int64_t workspace_bytes,
                     int dtype, void* stream) {
+  MDGL_RANGE();
   return grouped_common(a, b, dst, nullptr, seglen_a, n, d1, d2, r, workspace, workspace_bytes,
                         dtype, stream, false);
 }
@@ -1222,6 +1305,7 @@ int mdgl_segment_mm(const void* a, const void* b, void* dst, const int64_t* segl
 int mdgl_gather_mm(const void* a, const void* b, const int64_t* idx_b, void* dst, int64_t n,
                    int64_t d1, int64_t d2, int64_t r, void* workspace, int64_t workspace_bytes,
                    int dtype, void* stream) {
+  MDGL_RANGE();
   return grouped_common(a, b, dst, idx_b, nullptr, n, d1, d2, r, workspace, workspace_bytes,
                         dtype, stream, true);
 }
@@ -1276,6 +1360,7 @@ extern "C" int mdgl_gspmm_noalloc(const int32_t* indptr, const int32_t* indices,
                                   int32_t chunk_len, const int32_t* heavy_rows,
                                   const int32_t* heavy_ptr, int64_t num_heavy, int flags,
                                   int dtype, void* stream) {
+  MDGL_RANGE();
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "gspmm_noalloc: bad dtype %d", dtype);
   if (num_chunks < 0 || dout < 0) return fail(MDGL_EINVAL, "gspmm_noalloc: negative size");
   if (!row_widths_fit(dout, dsize(dtype)) || num_chunks >= (int64_t(1) << 31))

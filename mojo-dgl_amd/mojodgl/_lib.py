@@ -70,6 +70,7 @@ _C = ctypes.c_int
 _SIGNATURES = {
     "mdgl_last_error": ([], ctypes.c_char_p),
     "mdgl_workers": ([], _I64),
+    "mdgl_trace_ranges": ([], _C),
     "mdgl_cumsum": ([_P, _P, _I64, _P], _C),
     "mdgl_segment_offsets": ([_P, _I64, _I64, _P, _P, _P, _I64, _P], _C),
     "mdgl_segment_offsets_workspace_bytes": ([_I64], _I64),
@@ -294,25 +295,22 @@ def ptr(t) -> int | None:
 
 
 # ------------------------------------------------------------------ values
-_TORCH_TO_NP = {torch.float32: np.float32, torch.float64: np.float64}
+_F32, _F64 = np.dtype(np.float32), np.dtype(np.float64)
+_TORCH_TO_NP = {torch.float32: _F32, torch.float64: _F64}
+_NP_TO_TORCH = {_F32: torch.float32, _F64: torch.float64}
 
 
 class Feat:
     """A validated feature operand: a float32/float64 numpy array or tensor."""
 
-    __slots__ = ("data", "is_torch", "device", "shape")
+    __slots__ = ("data", "is_torch", "device", "shape", "dtype")
 
     def __init__(self, data, is_torch, dev):
         self.data = data
         self.is_torch = is_torch
         self.device = dev
         self.shape = tuple(data.shape)
-
-    @property
-    def dtype(self):
-        if self.is_torch:
-            return np.dtype(_TORCH_TO_NP[self.data.dtype])
-        return self.data.dtype
+        self.dtype = _TORCH_TO_NP[data.dtype] if is_torch else data.dtype
 
     @property
     def ndim(self):
@@ -359,18 +357,27 @@ def feature(a) -> Feat:
 
 
 def common_dtype(*feats) -> np.dtype:
-    kinds = [f.dtype for f in feats if f is not None]
-    if kinds and all(k == np.float32 for k in kinds):
-        return np.dtype(np.float32)
-    return np.dtype(np.float64)
+    """float32 when every given operand is float32, else float64."""
+    seen = False
+    for f in feats:
+        if f is not None:
+            if f.dtype != _F32:
+                return _F64
+            seen = True
+    return _F32 if seen else _F64
 
 
 def dtype_code(dtype) -> int:
-    return FLOAT32 if np.dtype(dtype) == np.float32 else FLOAT64
+    if dtype is _F32:
+        return FLOAT32
+    return FLOAT32 if np.dtype(dtype) == _F32 else FLOAT64
 
 
 def torch_dtype(dtype) -> torch.dtype:
-    return torch.float32 if np.dtype(dtype) == np.float32 else torch.float64
+    t = _NP_TO_TORCH.get(dtype) if isinstance(dtype, np.dtype) else None
+    if t is not None:
+        return t
+    return torch.float32 if np.dtype(dtype) == _F32 else torch.float64
 
 
 def on_device(f: Feat, dtype) -> torch.Tensor:

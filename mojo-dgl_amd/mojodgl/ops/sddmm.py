@@ -87,9 +87,11 @@ def out_feat_shape(lshape, rshape, dot=False):
 _SHAPE_ARGS = {}
 
 
-def shape_args(lshape, rshape):
-    """(nd, lhs feature shape, rhs feature shape) host arrays for the C ABI
-    (kept per shape pair: the arrays are only read)."""
+def shape_ptrs(lshape, rshape):
+    """(nd, lhs feature shape, rhs feature shape, their addresses, key) for
+    the C ABI: int64 host arrays, kept per shape pair (they are only read),
+    their data pointers, which the caller passes while it holds the arrays,
+    and the pair of feature-shape tuples they hold."""
     key = (feat_shape(lshape), feat_shape(rshape))
     got = _SHAPE_ARGS.get(key)
     if got is None:
@@ -98,7 +100,7 @@ def shape_args(lshape, rshape):
         assert lf.size == rf.size
         lf.flags.writeable = False
         rf.flags.writeable = False
-        got = (int(lf.size), lf, rf)
+        got = (int(lf.size), lf, rf, lf.ctypes.data, rf.ctypes.data, key)
         if len(_SHAPE_ARGS) < 4096:
             _SHAPE_ARGS[key] = got
     return got
@@ -174,20 +176,22 @@ def gsddmm(g, op, lhs_data, rhs_data, lhs_target="u", rhs_target="v"):
     rt = R if R is not None else L
     dl, dr = width(lt.shape), width(rt.shape)
     if code in (OP_COPY_LHS, OP_COPY_RHS):
-        nd, ls, rs = 0, None, None
+        nd, lsp, rsp = 0, None, None
     else:
-        nd, ls, rs = shape_args(L.shape, R.shape)
+        # the arrays stay referenced (here and in the cache) through the call
+        nd, _lsa, _rsa, lsp, rsp, _ = shape_ptrs(L.shape, R.shape)
     lhs = _lib.on_device(L, dtype) if L is not None else None
     rhs = _lib.on_device(R, dtype) if R is not None else None
     uids, vids = g._device_coo()
-    out = torch.empty((num_edges, dout), dtype=_lib.torch_dtype(dtype), device=_lib.device())
+    # allocated in its final shape: the same row-major bytes as (E, dout)
+    out = torch.empty((num_edges,) + tuple(fshape), dtype=_lib.torch_dtype(dtype),
+                      device=_lib.device())
     rc = _lib.lib().mdgl_gsddmm(
         _lib.ptr(uids), _lib.ptr(vids), _lib.ptr(lhs), _lib.ptr(rhs), out.data_ptr(), num_edges,
-        TARGETS[lhs_target], TARGETS[rhs_target], code, dl, dr, dout, nd,
-        None if ls is None else ls.ctypes.data, None if rs is None else rs.ctypes.data,
+        TARGETS[lhs_target], TARGETS[rhs_target], code, dl, dr, dout, nd, lsp, rsp,
         _lib.dtype_code(dtype), _lib.stream())
     _lib.check(rc, "gsddmm")
-    return _lib.give_back(out.reshape((num_edges,) + tuple(fshape)), as_torch, dev)
+    return _lib.give_back(out, as_torch, dev)
 
 
 def _gen_sddmm_func(lhs_target, rhs_target, binary_op):

@@ -18,7 +18,7 @@ from .. import _lib
 from .._lib import BINARY_OPS, OP_COPY_LHS, OP_COPY_RHS, REDUCERS
 from . import _autograd
 from ..base import DGLError
-from .sddmm import _check_rows, feat_shape, out_feat_shape, reshape_lhs_rhs, shape_args, width
+from .sddmm import _check_rows, feat_shape, out_feat_shape, reshape_lhs_rhs, shape_ptrs, width
 
 __all__ = ["gspmm"]
 
@@ -29,32 +29,35 @@ __all__ = ["gspmm"]
 CSR_ORDER_MIN_EDGES = 1 << 20
 
 
+_OPS = frozenset(BINARY_OPS) | {"copy_lhs", "copy_rhs"}
+
 _LANES = {}
 
 
-def _lanes(code, dl, dr, dout, nd, ls, rs, lhs, rhs, flags, dtype):
+def _lanes(code, dl, dr, dout, sp, lhs, rhs, flags, dtype):
     """(packed, slabs) of the lane layout mdgl_gspmm picks for these operands
     and flags (mdgl_gspmm_lanes): whether several rows share a wavefront
     (slabs of 32 lanes or fewer) and how many column slabs a row is cut
-    into. The answer depends only on the sizes, shapes, flags, dtype and the
-    operands' alignment (within 128 bytes), so it is kept per such key: the
-    query costs more host time than a small gspmm's kernel."""
-    key = (code, dl, dr, dout, nd, None if ls is None else tuple(ls),
-           None if rs is None else tuple(rs), _lib.ptr(lhs) % 128 if lhs is not None else -1,
-           _lib.ptr(rhs) % 128 if rhs is not None else -1, flags, np.dtype(dtype).str)
+    into. `sp` is shape_ptrs' entry for the operands' feature shapes (None
+    for the copy ops). The answer depends only on the sizes, shapes, flags,
+    dtype and the operands' alignment (within 128 bytes), so it is kept per
+    such key: the query costs more host time than a small gspmm's kernel."""
+    key = (code, dl, dr, dout, None if sp is None else sp[5],
+           lhs.data_ptr() % 128 if lhs is not None else -1,
+           rhs.data_ptr() % 128 if rhs is not None else -1, flags, dtype.str)
     got = _LANES.get(key)
     if got is None:
         if len(_LANES) >= 4096:  # many distinct shapes: start over rather than grow
             _LANES.clear()
-        got = _LANES[key] = _lanes_query(code, dl, dr, dout, nd, ls, rs, lhs, rhs, flags, dtype)
+        got = _LANES[key] = _lanes_query(code, dl, dr, dout, sp, lhs, rhs, flags, dtype)
     return got
 
 
-def _lanes_query(code, dl, dr, dout, nd, ls, rs, lhs, rhs, flags, dtype):
+def _lanes_query(code, dl, dr, dout, sp, lhs, rhs, flags, dtype):
     vec, group = ctypes.c_int64(), ctypes.c_int64()
+    nd, lsp, rsp = (0, None, None) if sp is None else (sp[0], sp[3], sp[4])
     _lib.check(_lib.lib().mdgl_gspmm_lanes(
-        code, dl, dr, dout, nd, None if ls is None else ls.ctypes.data,
-        None if rs is None else rs.ctypes.data, _lib.ptr(lhs), _lib.ptr(rhs), flags,
+        code, dl, dr, dout, nd, lsp, rsp, _lib.ptr(lhs), _lib.ptr(rhs), flags,
         _lib.dtype_code(dtype), ctypes.byref(vec), ctypes.byref(group)), "gspmm_lanes")
     lanes = -(-dout // vec.value)
     return group.value <= 32, -(-lanes // group.value)
@@ -92,7 +95,7 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
     bit for bit (the backward passes' reductions use it)."""
     if reduce_op not in REDUCERS:
         raise DGLError("reduce_op {} not recognized".format(reduce_op))
-    if op not in list(BINARY_OPS) + ["copy_lhs", "copy_rhs"]:
+    if op not in _OPS:
         raise DGLError("op {} not recognized".format(op))
     if op == "dot":
         raise DGLError("dot is not a gspmm operator; use gsddmm")
@@ -121,21 +124,23 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
     dout = 1
     for s_ in fshape:
         dout *= int(s_)
+    # results allocated in their final shapes: the same row-major bytes as
+    # (num_dst, dout)
     shape = (num_dst,) + tuple(fshape)
     tdt = _lib.torch_dtype(dtype)
+    dcode = _lib.dtype_code(dtype)
     gdev = _lib.device()
-    out = torch.empty((num_dst, dout), dtype=tdt, device=gdev)
+    out = torch.empty(shape, dtype=tdt, device=gdev)
     arg = want_arg and reduce_op in ("max", "min")
-    arg_u = torch.empty((num_dst, dout), dtype=torch.int32, device=gdev) if arg else None
-    arg_e = torch.empty((num_dst, dout), dtype=torch.int32, device=gdev) if arg else None
+    arg_u = torch.empty(shape, dtype=torch.int32, device=gdev) if arg else None
+    arg_e = torch.empty(shape, dtype=torch.int32, device=gdev) if arg else None
     if num_dst and dout:
         lt = L if L is not None else R
         rt = R if R is not None else L
         dl, dr = width(lt.shape), width(rt.shape)
-        if code in (OP_COPY_LHS, OP_COPY_RHS):
-            nd, ls, rs = 0, None, None
-        else:
-            nd, ls, rs = shape_args(L.shape, R.shape)
+        # the shape arrays stay referenced (in `sp` and the cache) through the call
+        sp = None if code in (OP_COPY_LHS, OP_COPY_RHS) else shape_ptrs(L.shape, R.shape)
+        nd, lsp, rsp = (0, None, None) if sp is None else (sp[0], sp[3], sp[4])
         lhs = _lib.on_device(L, dtype) if L is not None else None
         rhs = _lib.on_device(R, dtype) if R is not None else None
         csr = g._device_csr(kind)
@@ -145,11 +150,11 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
             if lined is not None:
                 lhs = lined
                 flags |= _lib.LHS_LINE_ROWS
-        packed, slabs = _lanes(code, dl, dr, dout, nd, ls, rs, lhs, rhs, flags, dtype)
+        packed, slabs = _lanes(code, dl, dr, dout, sp, lhs, rhs, flags, dtype)
         if slabs > 1 and g._local():
             # wide rows on a graph whose sources lie near their destinations
             flags |= _lib.NARROW_SLABS
-            packed, slabs = _lanes(code, dl, dr, dout, nd, ls, rs, lhs, rhs, flags, dtype)
+            packed, slabs = _lanes(code, dl, dr, dout, sp, lhs, rhs, flags, dtype)
         sched = csr.chunks
         if narrow_split and packed and narrow_split < sched.chunk_len:
             sched = csr.chunks_for(narrow_split)
@@ -162,8 +167,8 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
             # packed rows, several to a wavefront, do better without it)
             perm = torch.empty(num_edges, dtype=tdt, device=gdev)
             _lib.check(_lib.lib().mdgl_gather_rows(rhs.data_ptr(), csr.eid.data_ptr(),
-                                                   perm.data_ptr(), num_edges, 1,
-                                                   _lib.dtype_code(dtype), _lib.stream()),
+                                                   perm.data_ptr(), num_edges, 1, dcode,
+                                                   _lib.stream()),
                        "gather_rows")
             rhs = perm
             flags |= _lib.RHS_CSR_ORDER
@@ -171,23 +176,20 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
         nbytes = 0
         if sched.num_chunks:
             nbytes = _lib.lib().mdgl_gspmm_workspace_bytes(sched.num_chunks, dout,
-                                                             REDUCERS[reduce_op],
-                                                             _lib.dtype_code(dtype))
+                                                             REDUCERS[reduce_op], dcode)
         if nbytes:
             ws = torch.empty(nbytes, dtype=torch.uint8, device=gdev)
         rc = _lib.lib().mdgl_gspmm(
             csr.indptr.data_ptr(), csr.indices.data_ptr(), csr.eid.data_ptr(), _lib.ptr(lhs),
             _lib.ptr(rhs), out.data_ptr(), num_dst, code, dl, dr, dout, REDUCERS[reduce_op], None,
-            nd, None if ls is None else ls.ctypes.data, None if rs is None else rs.ctypes.data,
-            _lib.ptr(arg_u), _lib.ptr(arg_e), _lib.ptr(sched.chunk_row),
+            nd, lsp, rsp, _lib.ptr(arg_u), _lib.ptr(arg_e), _lib.ptr(sched.chunk_row),
             _lib.ptr(sched.chunk_start), sched.num_chunks, sched.chunk_len,
             _lib.ptr(sched.heavy_rows), _lib.ptr(sched.heavy_ptr), sched.num_heavy, _lib.ptr(ws),
-            nbytes, flags, _lib.dtype_code(dtype), _lib.stream())
+            nbytes, flags, dcode, _lib.stream())
         _lib.check(rc, "gspmm")
-    out = out.reshape(shape)
     if arg:
-        arg_u = arg_u.reshape(shape).to(arg_dtype)
-        arg_e = arg_e.reshape(shape).to(arg_dtype)
+        arg_u = arg_u.to(arg_dtype)
+        arg_e = arg_e.to(arg_dtype)
     return out, arg_u, arg_e, as_torch, dev
 
 
@@ -205,7 +207,7 @@ def _mul_sum_dot(g, grad, y, x, kind="out"):
             and G.is_cuda and X.is_cuda and Y.is_cuda):
         return None
     dtype = np.float32 if G.dtype == torch.float32 else np.float64
-    nd, ls, rs = shape_args(G.shape, Y.shape)
+    nd, _lsa, _rsa, lsp, rsp, _ = shape_ptrs(G.shape, Y.shape)
     dout = width(G.shape)
     dr = width(Y.shape)
     num_rows = g.number_of_nodes()
@@ -223,7 +225,7 @@ def _mul_sum_dot(g, grad, y, x, kind="out"):
     rc = _lib.lib().mdgl_gspmm_mul_sum_dot(
         csr.indptr.data_ptr(), csr.indices.data_ptr(), csr.eid.data_ptr(), G.data_ptr(),
         Y.data_ptr(), X.data_ptr(), dx.data_ptr(), dot.data_ptr(), num_rows, dout, dr, dout, nd,
-        ls.ctypes.data, rs.ctypes.data, _lib.ptr(sched.chunk_row), _lib.ptr(sched.chunk_start),
+        lsp, rsp, _lib.ptr(sched.chunk_row), _lib.ptr(sched.chunk_start),
         sched.num_chunks, sched.chunk_len, _lib.ptr(sched.heavy_rows), _lib.ptr(sched.heavy_ptr),
         sched.num_heavy, _lib.ptr(ws), nbytes, _lib.dtype_code(dtype), _lib.stream())
     if rc == _lib.ENOTSUP:

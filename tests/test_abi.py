@@ -251,3 +251,29 @@ def test_workspace_sizes(lib):
         wide = grad(n, 2048, 2048, r, 0)
         assert wide - fwd(n, 2048, 2048, r, 0) < (1 << 28) + r * 2048 * 2048 * 4 + (1 << 27)
         assert grad(n, d1, d2, r, 1) > small
+
+
+@pytest.mark.parametrize("setting,expect", [(None, 0), ("0", 0), ("1", 1)])
+def test_trace_ranges_follow_the_environment(setting, expect):
+    """MDGL_ROCTX turns the per-entry-point roctx ranges on (the ROCm roctx
+    library ships in the image); calls that fail validation still return
+    their status with a range open around them."""
+    import subprocess
+    import sys
+
+    env = dict(os.environ)
+    env.pop("MDGL_ROCTX", None)
+    if setting is not None:
+        env["MDGL_ROCTX"] = setting
+    code = (
+        "import sys; sys.path.insert(0, %r)\n"
+        "from mojodgl import _lib\n"
+        "lib = _lib.lib()\n"
+        "print(lib.mdgl_trace_ranges(), lib.mdgl_cumsum(None, None, -1, None),"
+        " lib.mdgl_trace_ranges())\n" % os.path.join(ROOT, "mojo-dgl_amd"))
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                         timeout=120)
+    assert out.returncode == 0, out.stderr
+    on, status, again = out.stdout.split()
+    assert int(on) == int(again) == expect
+    assert int(status) == -1  # MDGL_EINVAL
