@@ -255,6 +255,7 @@ class DGLGraph(object):
         self._draw = {}
         self._dcsr = {}
         self._locality = None
+        self._launches = {}  # gspmm call shapes seen on this graph (ops/spmm.py)
 
     def _source_locality(self):
         """Fraction of the edges whose source id lies within LOCAL_WINDOW of
@@ -338,6 +339,12 @@ class DGLGraph(object):
             raw = (host, indptr, indices, eid)
             self._draw[kind] = raw
         return raw
+
+    def _current_csr(self, kind):
+        """The GPU CSR of `kind` if it is built and has the schedules for the
+        current CHUNK_LEN (what _device_csr would return), else None."""
+        cached = self._dcsr.get(kind)
+        return cached if cached is not None and cached.params == int(CHUNK_LEN) else None
 
     def _device_csr(self, kind):
         """The GPU CSR of `kind` with the schedules for the current CHUNK_LEN."""

@@ -63,6 +63,14 @@ def _lanes_query(code, dl, dr, dout, sp, lhs, rhs, flags, dtype):
     return group.value <= 32, -(-lanes // group.value)
 
 
+def _line_rows_pay(rows, dl, num_edges, dtype):
+    """Whether copying lhs to line-aligned rows can pay (_line_rows): rows
+    of 512 bytes or more whose size is no multiple of 128 bytes, gathered at
+    least 8 times each."""
+    row_bytes = dl * np.dtype(dtype).itemsize
+    return not (row_bytes % 128 == 0 or row_bytes < 512 or rows == 0 or num_edges < 8 * rows)
+
+
 def _line_rows(lhs, rows, dl, num_edges, dtype):
     """lhs copied to rows that each start on a 128-byte line (the layout of
     mdgl_gspmm's MDGL_LHS_LINE_ROWS), or None when that does not pay: rows of
@@ -70,10 +78,10 @@ def _line_rows(lhs, rows, dl, num_edges, dtype):
     slab of them touches one line more than it needs; the copy reads and
     writes the table once, worth it for rows of a slab or more that the
     edges gather at least 8 times each."""
+    if not _line_rows_pay(rows, dl, num_edges, dtype):
+        return None
     es = np.dtype(dtype).itemsize
     row_bytes = dl * es
-    if row_bytes % 128 == 0 or row_bytes < 512 or rows == 0 or num_edges < 8 * rows:
-        return None
     stride = -(-row_bytes // 128) * 128 // es
     free, _ = torch.cuda.mem_get_info(lhs.device)
     if rows * stride * es > free // 4:  # the copy must not crowd out the caller's memory
@@ -81,6 +89,82 @@ def _line_rows(lhs, rows, dl, num_edges, dtype):
     padded = torch.empty((rows, stride), dtype=lhs.dtype, device=lhs.device)
     padded[:, :dl].copy_(lhs.reshape(rows, dl))
     return padded
+
+
+_FLOATS = (torch.float32, torch.float64)
+# positions of the per-call values in mdgl_gspmm's argument list
+_A_LHS, _A_RHS, _A_OUT, _A_ARG_U, _A_ARG_E, _A_WS, _A_STREAM = 3, 4, 5, 16, 17, 25, 29
+_LAUNCHES_MAX = 256  # call shapes kept per graph
+
+
+class _Launch:
+    """A gspmm call shape seen before on a graph, replayed without the full
+    path's validation and choices: the argument list mdgl_gspmm got for
+    operands of these shapes, dtypes and alignments, the per-call values
+    (operand, result and workspace addresses, the stream) filled in at each
+    call. Taken only for GPU tensors that the full path would use in place
+    (contiguous, on the current GPU, one float dtype) and calls whose
+    choices depend on shapes alone (no line-row copy, no CSR-order edge
+    operand). It holds the CSR it was made for and is dropped when the graph
+    holds another one (a new chunk length)."""
+
+    __slots__ = ("csr", "args", "shape", "tdt", "gdev", "arg", "arg_dtype", "nbytes", "local",
+                 "dev", "sp")
+
+    def run(self, lhs, rhs):
+        gdev = self.gdev
+        out = torch.empty(self.shape, dtype=self.tdt, device=gdev)
+        args = list(self.args)
+        args[_A_LHS] = None if lhs is None else lhs.data_ptr()
+        args[_A_RHS] = None if rhs is None else rhs.data_ptr()
+        args[_A_OUT] = out.data_ptr()
+        arg_u = arg_e = None
+        if self.arg:
+            arg_u = torch.empty(self.shape, dtype=torch.int32, device=gdev)
+            arg_e = torch.empty(self.shape, dtype=torch.int32, device=gdev)
+            args[_A_ARG_U] = arg_u.data_ptr()
+            args[_A_ARG_E] = arg_e.data_ptr()
+        ws = None
+        if self.nbytes:
+            ws = torch.empty(self.nbytes, dtype=torch.uint8, device=gdev)
+            args[_A_WS] = ws.data_ptr()
+        args[_A_STREAM] = _lib.stream()
+        _lib.check(_lib.lib().mdgl_gspmm(*args), "gspmm")
+        if self.arg:
+            arg_u = arg_u.to(self.arg_dtype)
+            arg_e = arg_e.to(self.arg_dtype)
+        return out, arg_u, arg_e, True, self.dev
+
+
+def _operand_key(t):
+    """(shape, dtype, address mod 128, device index) of a contiguous float
+    GPU tensor, else None (without touching the GPU)."""
+    if not isinstance(t, torch.Tensor) or not t.is_cuda or t.dtype not in _FLOATS \
+            or not t.is_contiguous():
+        return None
+    return t.shape, t.dtype, t.data_ptr() % 128, t.get_device()
+
+
+def _launch_key(op, reduce_op, lhs, rhs, replace_inf, want_arg, arg_dtype, kind, narrow_split):
+    """Key of a call shape for _Launch, or None when the call must take the
+    full path (operands it would convert or copy: host arrays, another GPU,
+    non-contiguous tensors, two dtypes)."""
+    lk = rk = None
+    if op != "copy_rhs":
+        lk = _operand_key(lhs)
+        if lk is None:
+            return None
+    if op != "copy_lhs":
+        rk = _operand_key(rhs)
+        if rk is None:
+            return None
+    if lk is not None and rk is not None and lk[1] != rk[1]:
+        return None
+    dev = _lib.current_device()  # operands on the GPU: its state is up
+    if (lk is not None and lk[3] != dev) or (rk is not None and rk[3] != dev):
+        return None
+    return (kind, op, reduce_op, replace_inf, want_arg, arg_dtype, narrow_split, lk, rk, dev,
+            CSR_ORDER_MIN_EDGES, _lanes)
 
 
 def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False,
@@ -92,7 +176,17 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
     several rows share a wavefront, split rows longer than this (instead of
     the graph's chunk length) so a wavefront's rows have bounded lengths --
     their sums then fold in chunks, within the tolerance rule rather than
-    bit for bit (the backward passes' reductions use it)."""
+    bit for bit (the backward passes' reductions use it). A call shape seen
+    before on `g` replays its launch (_Launch)."""
+    key = _launch_key(op, reduce_op, lhs_data, rhs_data, replace_inf, want_arg, arg_dtype, kind,
+                      narrow_split)
+    if key is not None:
+        launch = g._launches.get(key)
+        if launch is not None and launch.csr is g._current_csr(kind) \
+                and (launch.local is None or g._local() is launch.local):
+            # the copy ops read one operand; the other is passed as null
+            return launch.run(None if op == "copy_rhs" else lhs_data,
+                              None if op == "copy_lhs" else rhs_data)
     if reduce_op not in REDUCERS:
         raise DGLError("reduce_op {} not recognized".format(reduce_op))
     if op not in _OPS:
@@ -145,13 +239,18 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
         rhs = _lib.on_device(R, dtype) if R is not None else None
         csr = g._device_csr(kind)
         flags = _lib.REPLACE_INF if replace_inf else 0
+        replay = key is not None
         if lhs is not None and code != OP_COPY_RHS:
+            replay = replay and not _line_rows_pay(lt.shape[0], dl, num_edges, dtype)
             lined = _line_rows(lhs, lt.shape[0], dl, num_edges, dtype)
             if lined is not None:
                 lhs = lined
                 flags |= _lib.LHS_LINE_ROWS
         packed, slabs = _lanes(code, dl, dr, dout, sp, lhs, rhs, flags, dtype)
-        if slabs > 1 and g._local():
+        local = None
+        if slabs > 1:
+            local = g._local()
+        if local:
             # wide rows on a graph whose sources lie near their destinations
             flags |= _lib.NARROW_SLABS
             packed, slabs = _lanes(code, dl, dr, dout, sp, lhs, rhs, flags, dtype)
@@ -172,6 +271,7 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
                        "gather_rows")
             rhs = perm
             flags |= _lib.RHS_CSR_ORDER
+            replay = False
         ws = None
         nbytes = 0
         if sched.num_chunks:
@@ -179,14 +279,25 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
                                                              REDUCERS[reduce_op], dcode)
         if nbytes:
             ws = torch.empty(nbytes, dtype=torch.uint8, device=gdev)
-        rc = _lib.lib().mdgl_gspmm(
+        args = [
             csr.indptr.data_ptr(), csr.indices.data_ptr(), csr.eid.data_ptr(), _lib.ptr(lhs),
             _lib.ptr(rhs), out.data_ptr(), num_dst, code, dl, dr, dout, REDUCERS[reduce_op], None,
             nd, lsp, rsp, _lib.ptr(arg_u), _lib.ptr(arg_e), _lib.ptr(sched.chunk_row),
             _lib.ptr(sched.chunk_start), sched.num_chunks, sched.chunk_len,
             _lib.ptr(sched.heavy_rows), _lib.ptr(sched.heavy_ptr), sched.num_heavy, _lib.ptr(ws),
-            nbytes, flags, dcode, _lib.stream())
-        _lib.check(rc, "gspmm")
+            nbytes, flags, dcode, _lib.stream()]
+        _lib.check(_lib.lib().mdgl_gspmm(*args), "gspmm")
+        if replay:
+            launch = _Launch()
+            launch.csr, launch.sp, launch.local = csr, sp, local
+            launch.shape, launch.tdt, launch.gdev, launch.dev = shape, tdt, gdev, dev
+            launch.arg, launch.arg_dtype, launch.nbytes = arg, arg_dtype, nbytes
+            for i in (_A_LHS, _A_RHS, _A_OUT, _A_ARG_U, _A_ARG_E, _A_WS, _A_STREAM):
+                args[i] = None
+            launch.args = tuple(args)
+            if len(g._launches) >= _LAUNCHES_MAX:
+                g._launches.clear()
+            g._launches[key] = launch
     if arg:
         arg_u = arg_u.to(arg_dtype)
         arg_e = arg_e.to(arg_dtype)

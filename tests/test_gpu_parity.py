@@ -433,6 +433,73 @@ def test_gspmm_zero_degree_and_empty_graph():
     assert ops.u_mul_e_sum(empty, np.zeros((0, 4)), np.zeros((0, 4))).shape == (0, 4)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_gspmm_replayed_launches_match_the_full_path(dtype, monkeypatch):
+    """A gspmm call shape seen before on a graph replays its launch: the
+    results of the replay equal those of the full path on a fresh graph, bit
+    for bit (values and args), for whole and split rows, packed and wide
+    rows, broadcast operands, both copy ops (with an operand they do not read
+    passed anyway), an operand one element off its allocation's start, and a
+    new chunk length (the replay is dropped with the CSR it was made for);
+    numpy operands and mixed dtypes always take the full path."""
+    from mojodgl.ops import spmm
+
+    n, e = 3000, 40000
+    rng = np.random.default_rng(70)
+    u = rng.integers(0, n, e)
+    v = np.minimum(rng.zipf(1.8, e) - 1, n - 1)  # hub rows, split at chunk length 16
+    dev = torch.device("cuda")
+    x64 = torch.randn(n, 64, dtype=dtype, device=dev)
+    x602 = torch.randn(n, 602, dtype=dtype, device=dev)
+    x512 = torch.randn(n, 512, dtype=dtype, device=dev)  # several column slabs
+    w512 = torch.rand(e, 512, dtype=dtype, device=dev)
+    xh = torch.randn(n, 4, 16, dtype=dtype, device=dev)
+    w64 = torch.rand(e, 64, dtype=dtype, device=dev)
+    w1 = torch.rand(e, 1, dtype=dtype, device=dev)
+    wh = torch.rand(e, 4, 1, dtype=dtype, device=dev)
+    base = torch.randn(n * 64 + 1, dtype=dtype, device=dev)
+    xoff = base[1:].view(n, 64)  # contiguous, one element into its allocation
+    cases = [("mul", "sum", x64, w64), ("add", "max", x64, w64), ("div", "min", x64, w64),
+             ("mul", "mean", x602, w1), ("mul", "sum", xh, wh), ("sub", "max", xh, wh),
+             ("copy_lhs", "sum", x64, w64), ("copy_rhs", "max", x64, w64),
+             ("copy_lhs", "min", x602, None), ("mul", "sum", xoff, w64),
+             ("copy_lhs", "sum", x512, None), ("add", "max", x512, w512)]
+
+    def run(g, op, red, L, R):
+        out, (au, ae) = spmm._gspmm(g, op, red, L, R)
+        return [t.cpu() if t is not None else None for t in (out, au, ae)]
+
+    def same(a, b, what):
+        for p, q in zip(a, b):
+            assert (p is None) == (q is None), what
+            if p is not None:
+                assert torch.equal(p, q), what
+
+    for chunk in (2 ** 30, 16):
+        monkeypatch.setattr(hg, "CHUNK_LEN", chunk)
+        g = dgl.graph((u, v), num_nodes=n)
+        for op, red, L, R in cases:
+            what = "{} {} {} chunk={}".format(op, red, tuple(L.shape), chunk)
+            first = run(g, op, red, L, R)
+            count = len(g._launches)
+            assert count >= 1, what
+            second = run(g, op, red, L, R)
+            assert len(g._launches) == count, what  # replayed, not recorded again
+            same(second, first, what + " replay")
+            same(second, run(dgl.graph((u, v), num_nodes=n), op, red, L, R), what + " fresh")
+    # the graph of the last round met another chunk length: its replays are dropped
+    monkeypatch.setattr(hg, "CHUNK_LEN", 2 ** 30)
+    for op, red, L, R in cases[:3]:
+        same(run(g, op, red, L, R), run(dgl.graph((u, v), num_nodes=n), op, red, L, R),
+             "{} {} after a new chunk length".format(op, red))
+    # operands the full path converts are never replayed
+    g = dgl.graph((u, v), num_nodes=n)
+    other = torch.float64 if dtype == torch.float32 else torch.float32
+    spmm._gspmm(g, "mul", "sum", x64.cpu().numpy(), w64.cpu().numpy())
+    spmm._gspmm(g, "mul", "sum", x64, w64.to(other))
+    assert len(g._launches) == 0
+
+
 # ------------------------------------------------------------------ gsddmm
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("lt,rt", list(itertools.permutations("uve", 2)))
