@@ -48,6 +48,8 @@ Only torch tensors take part (numpy operands have no autograd).
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import torch
 from torch.autograd.function import once_differentiable
@@ -151,7 +153,7 @@ def _reduce_to(t, shape):
     if pad[:keep] != full[:keep] or any(p != 1 for p in pad[keep:]):
         raise DGLError("backward of an operand broadcast along {} -> {} is not supported "
                        "(only trailing broadcast axes)".format(part, full))
-    inner = int(np.prod(full[keep:], dtype=np.int64))
+    inner = int(math.prod(full[keep:]))
     from .segment import segment_reduce
 
     flat = t.contiguous().reshape(-1, 1)
@@ -288,7 +290,7 @@ def _mul_grad(g, x, G, yshape):
         keep -= 1
     if keep < len(ypad) and tuple(ypad[:keep]) == tuple(full[:keep]) \
             and tuple(x.shape[1:]) == tuple(full):
-        inner = int(np.prod(full[keep:], dtype=np.int64))
+        inner = int(math.prod(full[keep:]))
         lead = tuple(full[:keep])
         xs = x.reshape((x.shape[0],) + lead + (inner,))
         gs = G.reshape((G.shape[0],) + lead + (inner,))
@@ -399,7 +401,7 @@ def _segment_ids(seg, n):
 
 
 def _flat(shape):
-    return 1 if len(shape) < 2 else int(np.prod(shape[1:], dtype=np.int64))
+    return 1 if len(shape) < 2 else int(math.prod(shape[1:]))
 
 
 class SegmentReduce(torch.autograd.Function):

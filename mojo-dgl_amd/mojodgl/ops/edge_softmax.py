@@ -12,6 +12,8 @@ float32/float64.
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import torch
 
@@ -80,7 +82,7 @@ def _edge_softmax(graph, logits, eids, norm_by, keep=None):
     if len(shape) == 1:
         d = 1
     elif len(shape) >= 2 and shape[-1] == 1:
-        d = int(np.prod(shape[1:], dtype=np.int64))
+        d = int(math.prod(shape[1:]))
     else:
         raise DGLError("logits must be (E,), (E, 1) or (E, *, 1); got shape {}".format(shape))
     if norm_by not in ("dst", "src"):

@@ -8,6 +8,7 @@ sddmm.py:50-68), and the result keeps the operands' float32/float64 dtype.
 
 from __future__ import annotations
 
+import math
 import sys
 from itertools import product
 
@@ -168,7 +169,7 @@ def gsddmm(g, op, lhs_data, rhs_data, lhs_target="u", rhs_target="v"):
     dtype = _lib.common_dtype(L, R)
     as_torch = _lib.wants_torch(L, R)
     dev = _lib.out_device(L, R)
-    dout = int(np.prod(fshape[:-1] if op == "dot" else fshape, dtype=np.int64))
+    dout = int(math.prod(fshape[:-1] if op == "dot" else fshape))
     if num_edges == 0 or dout == 0:
         empty = np.zeros((num_edges,) + tuple(fshape), dtype=dtype)
         return torch.from_numpy(empty).to(dev) if as_torch else empty

@@ -10,6 +10,8 @@ one small read back.
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import torch
 
@@ -131,7 +133,7 @@ class _Segments:
 
 
 def _flat_width(shape):
-    return 1 if len(shape) < 2 else int(np.prod(shape[1:], dtype=np.int64))
+    return 1 if len(shape) < 2 else int(math.prod(shape[1:]))
 
 
 def segment_reduce(seglen, value, reducer="sum"):
