@@ -159,6 +159,22 @@ int mdgl_gspmm(const int32_t* indptr, const int32_t* indices, const int32_t* eid
                const int32_t* heavy_ptr, int64_t num_heavy, void* workspace,
                int64_t workspace_bytes, int flags, int dtype, void* stream);
 
+/* mdgl_gspmm over the listed rows only: dst[rows[i]] for i < num_rows, each
+ * row whole (no heavy-row split: a row's messages fold in CSR order in one
+ * unit), the other rows of dst left as they are. Rows outside [0, num_dst)
+ * are skipped; a row listed twice is written twice with the same values.
+ * Replaces the subgraph the reference builds for `pull`
+ * (python/mojodgl/heterograph.py:318-347: the in-edges of the pulled nodes
+ * cut out and reduced by update_all, then every other row zeroed): the
+ * caller zero-fills dst and reduces the pulled rows of the graph's own CSR.
+ * Same operands, flags and outputs as mdgl_gspmm. */
+int mdgl_gspmm_rows(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
+                    const void* lhs, const void* rhs, void* dst, int64_t num_dst, int op,
+                    int64_t dl, int64_t dr, int64_t dout, int reduce_op, const int32_t* deg,
+                    int nd, const int64_t* lhs_shape, const int64_t* rhs_shape, int32_t* arg_u,
+                    int32_t* arg_e, const int32_t* rows, int64_t num_rows, int flags, int dtype,
+                    void* stream);
+
 /* The lane width (values per lane: 1, 2 or 4 in float32, 1 or 2 in
  * float64) and, when `group` is not null, the lanes per row slab (a power
  * of two up to 64) that mdgl_gspmm picks for these operands, shapes,

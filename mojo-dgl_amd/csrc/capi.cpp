@@ -579,7 +579,8 @@ int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* e
                  int64_t num_chunks, int32_t chunk_len, const int32_t* heavy_rows,
                  const int32_t* heavy_ptr, int64_t num_heavy, void* workspace,
                  int64_t workspace_bytes, int flags, int dtype, void* stream,
-                 const void* rowop = nullptr, void* dot_out = nullptr) {
+                 const void* rowop = nullptr, void* dot_out = nullptr,
+                 const int32_t* rows = nullptr, int64_t num_listed = -1) {
   if (!dtype_ok(dtype)) return fail(MDGL_EINVAL, "gspmm: bad dtype %d", dtype);
   if (op < OP_ADD || op > OP_COPY_RHS || op == OP_DOT)
     return fail(MDGL_EINVAL, "gspmm: bad op %d (dot is a gsddmm operator)", op);
@@ -596,6 +597,10 @@ int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* e
     return fail(MDGL_EINVAL, "gspmm: incomplete heavy-row schedule");
   if (num_chunks == 0 && num_heavy != 0)
     return fail(MDGL_EINVAL, "gspmm: heavy rows without chunks");
+  const bool listed = num_listed >= 0;  // mdgl_gspmm_rows
+  if (listed && num_listed >= (int64_t(1) << 31))
+    return fail(MDGL_EINVAL, "gspmm_rows: 2**31 or more rows listed");
+  if (listed && num_listed > 0 && !rows) return fail(MDGL_EINVAL, "gspmm_rows: null rows");
   GspmmParams p{};
   p.indptr = indptr;
   p.indices = indices;
@@ -618,7 +623,12 @@ int gspmm_common(const int32_t* indptr, const int32_t* indices, const int32_t* e
   p.arg_e = arg ? arg_e : nullptr;
   p.stream = (hipStream_t)stream;
   if (int rc = gspmm_bcast(op, dl, dr, dout, nd, lhs_shape, rhs_shape, &p.bc)) return rc;
-  if (num_dst == 0 || dout == 0) return MDGL_OK;
+  if (num_dst == 0 || dout == 0 || num_listed == 0) return MDGL_OK;
+  if (listed) {
+    p.rows = rows;
+    p.row_limit = num_dst;
+    p.num_rows = num_listed;
+  }
   if (!indptr || !dst) return fail(MDGL_EINVAL, "gspmm: null indptr or output");
   if (op != OP_COPY_LHS && !eid) return fail(MDGL_EINVAL, "gspmm: null eid");
   if (op != OP_COPY_RHS && !indices) return fail(MDGL_EINVAL, "gspmm: null indices");
@@ -716,6 +726,21 @@ int mdgl_gspmm(const int32_t* indptr, const int32_t* indices, const int32_t* eid
                       deg, nd, lhs_shape, rhs_shape, arg_u, arg_e, chunk_row, chunk_start,
                       num_chunks, chunk_len, heavy_rows, heavy_ptr, num_heavy, workspace,
                       workspace_bytes, flags, dtype, stream);
+}
+
+int mdgl_gspmm_rows(const int32_t* indptr, const int32_t* indices, const int32_t* eid,
+                    const void* lhs, const void* rhs, void* dst, int64_t num_dst, int op,
+                    int64_t dl, int64_t dr, int64_t dout, int reduce_op, const int32_t* deg,
+                    int nd, const int64_t* lhs_shape, const int64_t* rhs_shape, int32_t* arg_u,
+                    int32_t* arg_e, const int32_t* rows, int64_t num_rows, int flags, int dtype,
+                    void* stream) {
+  MDGL_RANGE();
+  if (num_rows < 0) return fail(MDGL_EINVAL, "gspmm_rows: negative row count");
+  // every listed row whole, in one unit (no heavy-row schedule)
+  return gspmm_common(indptr, indices, eid, lhs, rhs, dst, num_dst, op, dl, dr, dout, reduce_op,
+                      deg, nd, lhs_shape, rhs_shape, arg_u, arg_e, nullptr, nullptr, 0, 0,
+                      nullptr, nullptr, 0, nullptr, 0, flags, dtype, stream, nullptr, nullptr,
+                      rows, num_rows);
 }
 
 int mdgl_gspmm_lanes(int op, int64_t dl, int64_t dr, int64_t dout, int nd,

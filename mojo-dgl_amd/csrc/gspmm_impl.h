@@ -66,6 +66,8 @@ struct GspmmArgs {
   const T* rowop;  // dot output (see GspmmParams), else null
   T* dot_out;
   int dot_lanes;
+  const int32_t* rows;  // listed rows (see GspmmParams), else null
+  int64_t row_limit;
 };
 
 template <class T, int VEC, int M>
@@ -127,9 +129,15 @@ __device__ __forceinline__ void gspmm_body(const GspmmArgs<T>& a, bool chunk, in
       stop = (end - start > a.chunk_len) ? start + a.chunk_len : end;
     } else {
       row = unit;
-      start = a.indptr[row];
-      stop = a.indptr[row + 1];
-      if (stop - start > a.chunk_len) ok = false;  // heavy: done by chunks + combine
+      if (a.rows) {
+        row = a.rows[unit];
+        if (row < 0 || row >= a.row_limit) ok = false;  // not a row of the graph: skipped
+      }
+      if (ok) {
+        start = a.indptr[row];
+        stop = a.indptr[row + 1];
+        if (stop - start > a.chunk_len) ok = false;  // heavy: done by chunks + combine
+      }
     }
   }
 
@@ -466,6 +474,8 @@ hipError_t launch_gspmm_op(const GspmmParams& p) {
   a.rowop = static_cast<const T*>(p.rowop);
   a.dot_out = static_cast<T*>(p.dot_out);
   a.dot_lanes = p.dot_lanes;
+  a.rows = p.rows;
+  a.row_limit = p.row_limit;
   if (a.num_blocks > 0) {
     const bool copy_l = OP == OP_COPY_LHS, copy_r = OP == OP_COPY_RHS;
     const int lm = copy_r ? a.rmode : a.lmode;

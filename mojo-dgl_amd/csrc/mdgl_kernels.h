@@ -55,6 +55,10 @@ struct GspmmParams {
   const void* rowop;
   void* dot_out;
   int dot_lanes;
+  // optional: the rows to reduce (num_rows of them, each in [0, row_limit));
+  // null: rows 0 .. num_rows - 1
+  const int32_t* rows;
+  int64_t row_limit;
   hipStream_t stream;
 };
 

@@ -80,6 +80,8 @@ _SIGNATURES = {
                     _C),
     "mdgl_gspmm": ([_P, _P, _P, _P, _P, _P, _I64, _C, _I64, _I64, _I64, _C, _P, _C, _P, _P, _P,
                     _P, _P, _P, _I64, _I32, _P, _P, _I64, _P, _I64, _C, _C, _P], _C),
+    "mdgl_gspmm_rows": ([_P, _P, _P, _P, _P, _P, _I64, _C, _I64, _I64, _I64, _C, _P, _C, _P,
+                         _P, _P, _P, _P, _I64, _C, _C, _P], _C),
     "mdgl_gspmm_workspace_bytes": ([_I64, _I64, _C, _C], _I64),
     "mdgl_gspmm_lanes": ([_C, _I64, _I64, _I64, _C, _P, _P, _P, _P, _C, _C, _P, _P], _C),
     "mdgl_coo_locality": ([_P, _P, _I64, _I64, _P, _P], _C),

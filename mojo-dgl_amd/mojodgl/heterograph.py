@@ -50,8 +50,12 @@ _Code2Str = TargetCode.CODE2STR
 
 # rows of more in-edges than this are split into chunks of this many for gspmm
 CHUNK_LEN = 512
-# pull runs a builtin pass over every edge (no subgraph) when the pulled rows
-# hold at least 1 / PULL_FULL_PASS of the edges
+# pull reduces the pulled rows of the graph's own CSR (mdgl_gspmm_rows, each
+# row whole) for a builtin u_op_e / copy message with a builtin reducer when
+# no pulled row has more in-edges than this; otherwise it runs a builtin pass
+# over every edge (no subgraph) when the pulled rows hold at least
+# 1 / PULL_FULL_PASS of the edges, else a subgraph of their in-edges
+PULL_ROWS_MAX_DEGREE = 4096
 PULL_FULL_PASS = 8
 # a graph is local when at least LOCAL_FRACTION of its edges join nodes whose
 # ids differ by less than LOCAL_WINDOW (the rows whose 512-byte column slabs
@@ -553,9 +557,24 @@ class DGLGraph(object):
                 self._num_nodes, int(v[0]), int(v[-1])))
         csr = self._device_csr("in")
         ip = csr.host_indptr
-        pulled = int((ip[v + 1] - ip[v]).sum())  # in-edges of v, known on the host
-        if (isinstance(message_func, MessageFunction) and isinstance(reduce_func, ReduceFunction)
-                and apply_node_func is None and pulled * PULL_FULL_PASS >= self._E):
+        degs = ip[v + 1] - ip[v]  # in-edges of v, known on the host
+        pulled = int(degs.sum())
+        builtin = (isinstance(message_func, MessageFunction)
+                   and isinstance(reduce_func, ReduceFunction) and apply_node_func is None)
+        fused = self._fusable(message_func) if builtin else None
+        if fused is not None and int(degs.max()) <= PULL_ROWS_MAX_DEGREE:
+            op, lhs_field, rhs_field = fused
+            lhs = self.ndata[lhs_field] if lhs_field is not None else None
+            rhs = self.edata[rhs_field] if rhs_field is not None else None
+            if not _autograd.needs_grad(lhs, rhs):
+                # the pulled rows of the graph's CSR, every other row zero
+                red = reduce_func.name
+                out, _, _, as_torch, dev = _spmm._run(
+                    self, op, red, lhs, rhs, replace_inf=red in ("max", "min"),
+                    rows=_lib.i32_device(v))
+                self.ndata[reduce_func.out_field] = _lib.give_back(out, as_torch, dev)
+                return
+        if builtin and pulled * PULL_FULL_PASS >= self._E:
             # a builtin output row depends on its own in-edges only, so a pass
             # over every edge gives the subgraph's rows for v; taken when v's
             # in-edges are a large share of the graph (no subgraph to build)

@@ -168,7 +168,7 @@ def _launch_key(op, reduce_op, lhs, rhs, replace_inf, want_arg, arg_dtype, kind,
 
 
 def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False,
-         arg_dtype=torch.int64, kind="in", narrow_split=None):
+         arg_dtype=torch.int64, kind="in", narrow_split=None, rows=None):
     """Validate, launch, and return device tensors (out, arg_u, arg_e) plus
     the caller-container info. `kind` "out" reduces over the out-CSR instead
     (the reversed graph: rows are sources, the node operand is read at the
@@ -176,10 +176,12 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
     several rows share a wavefront, split rows longer than this (instead of
     the graph's chunk length) so a wavefront's rows have bounded lengths --
     their sums then fold in chunks, within the tolerance rule rather than
-    bit for bit (the backward passes' reductions use it). A call shape seen
+    bit for bit (the backward passes' reductions use it). `rows` (an int32
+    GPU tensor of distinct node ids): reduce those rows only, each whole
+    (mdgl_gspmm_rows), the other rows of the result zero. A call shape seen
     before on `g` replays its launch (_Launch)."""
-    key = _launch_key(op, reduce_op, lhs_data, rhs_data, replace_inf, want_arg, arg_dtype, kind,
-                      narrow_split)
+    key = None if rows is not None else _launch_key(
+        op, reduce_op, lhs_data, rhs_data, replace_inf, want_arg, arg_dtype, kind, narrow_split)
     if key is not None:
         launch = g._launches.get(key)
         if launch is not None and launch.csr is g._current_csr(kind) \
@@ -224,10 +226,15 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
     tdt = _lib.torch_dtype(dtype)
     dcode = _lib.dtype_code(dtype)
     gdev = _lib.device()
-    out = torch.empty(shape, dtype=tdt, device=gdev)
     arg = want_arg and reduce_op in ("max", "min")
-    arg_u = torch.empty(shape, dtype=torch.int32, device=gdev) if arg else None
-    arg_e = torch.empty(shape, dtype=torch.int32, device=gdev) if arg else None
+    if rows is None:
+        out = torch.empty(shape, dtype=tdt, device=gdev)
+        arg_u = torch.empty(shape, dtype=torch.int32, device=gdev) if arg else None
+        arg_e = torch.empty(shape, dtype=torch.int32, device=gdev) if arg else None
+    else:  # the rows that are not listed stay zero (no message: arg -1)
+        out = torch.zeros(shape, dtype=tdt, device=gdev)
+        arg_u = torch.full(shape, -1, dtype=torch.int32, device=gdev) if arg else None
+        arg_e = torch.full(shape, -1, dtype=torch.int32, device=gdev) if arg else None
     if num_dst and dout:
         lt = L if L is not None else R
         rt = R if R is not None else L
@@ -240,6 +247,10 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
         csr = g._device_csr(kind)
         flags = _lib.REPLACE_INF if replace_inf else 0
         replay = key is not None
+        if rows is not None:
+            # the layout choices below pay over whole graphs, not a few rows
+            return _run_rows(csr, rows, code, reduce_op, lhs, rhs, out, arg_u, arg_e, dl, dr,
+                             dout, nd, lsp, rsp, flags, dcode, arg, arg_dtype, as_torch, dev)
         if lhs is not None and code != OP_COPY_RHS:
             replay = replay and not _line_rows_pay(lt.shape[0], dl, num_edges, dtype)
             lined = _line_rows(lhs, lt.shape[0], dl, num_edges, dtype)
@@ -298,6 +309,21 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
             if len(g._launches) >= _LAUNCHES_MAX:
                 g._launches.clear()
             g._launches[key] = launch
+    if arg:
+        arg_u = arg_u.to(arg_dtype)
+        arg_e = arg_e.to(arg_dtype)
+    return out, arg_u, arg_e, as_torch, dev
+
+
+def _run_rows(csr, rows, code, reduce_op, lhs, rhs, out, arg_u, arg_e, dl, dr, dout, nd, lsp,
+              rsp, flags, dcode, arg, arg_dtype, as_torch, dev):
+    """The listed rows of a gspmm over `csr` (mdgl_gspmm_rows), into the
+    zero-filled results."""
+    _lib.check(_lib.lib().mdgl_gspmm_rows(
+        csr.indptr.data_ptr(), csr.indices.data_ptr(), csr.eid.data_ptr(), _lib.ptr(lhs),
+        _lib.ptr(rhs), out.data_ptr(), out.shape[0], code, dl, dr, dout, REDUCERS[reduce_op],
+        None, nd, lsp, rsp, _lib.ptr(arg_u), _lib.ptr(arg_e), rows.data_ptr(), rows.shape[0],
+        flags, dcode, _lib.stream()), "gspmm_rows")
     if arg:
         arg_u = arg_u.to(arg_dtype)
         arg_e = arg_e.to(arg_dtype)

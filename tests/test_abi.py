@@ -156,6 +156,16 @@ def test_invalid_arguments_are_rejected_without_launching(lib):
     # too many b blocks for the GPU bucketing
     rc = lib.mdgl_gather_mm(1, 1, 1, 1, 100, 4, 4, 100000, 1, 1 << 40, 0, None)
     assert rc == -3
+    # a row list: its count must not be negative, and a non-empty one needs its rows
+    rc = lib.mdgl_gspmm_rows(1, 1, 1, 1, 1, 1, 10, 2, 4, 4, 4, 0, None, 0, None, None, None,
+                             None, None, -1, 0, 0, None)
+    assert rc == -1 and "negative" in err(lib)
+    rc = lib.mdgl_gspmm_rows(1, 1, 1, 1, 1, 1, 10, 2, 4, 4, 4, 0, None, 0, None, None, None,
+                             None, None, 3, 0, 0, None)
+    assert rc == -1 and "null rows" in err(lib)
+    rc = lib.mdgl_gspmm_rows(1, 1, 1, 1, 1, 1, 10, 2, 4, 4, 4, 7, None, 0, None, None, None,
+                             None, 1, 3, 0, 0, None)
+    assert rc == -1 and "reduce_op" in err(lib)
 
 
 def test_empty_problems_are_no_ops(lib):
@@ -163,6 +173,9 @@ def test_empty_problems_are_no_ops(lib):
                           None, None, None, None, None, 0, 0, None, None, 0, None, 0, 0, 0,
                           None) == 0
     assert lib.mdgl_segment_mm(None, None, None, None, 0, 4, 2, 3, None, 0, 0, None) == 0
+    # no rows listed: nothing to do, whatever the buffers
+    assert lib.mdgl_gspmm_rows(None, None, None, None, None, None, 10, 2, 4, 4, 4, 0, None, 0,
+                               None, None, None, None, None, 0, 0, 0, None) == 0
     assert lib.mdgl_cumsum(None, None, 0, None) == 0
     assert lib.mdgl_segment_softmax_short(None, None, None, 0, 4, 0, 0, None) == 0
 

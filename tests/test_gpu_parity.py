@@ -1228,11 +1228,13 @@ def test_pull_and_readme_vector():
                                      ("copy_e", "min"), ("udf", "sum")])
 @pytest.mark.parametrize("on_gpu", [False, True])
 def test_pull_full_pass_and_subgraph_agree(msg, red, on_gpu, monkeypatch):
-    """pull runs a builtin pass over every edge when the pulled rows hold many
-    in-edges, and a subgraph of their in-edges (selected by the GPU grouping,
-    in edge-id order) otherwise: both give the reference's result (the pulled
-    rows of a full pass, zero elsewhere; max / min's +-inf -> 0), bit for bit
-    between the two, and a UDF message always takes the subgraph."""
+    """pull reduces the pulled rows of the graph's own CSR (mdgl_gspmm_rows)
+    for a builtin u_op_e / copy message, and otherwise runs a builtin pass
+    over every edge when the pulled rows hold many in-edges, or a subgraph of
+    their in-edges (selected by the GPU grouping, in edge-id order): all give
+    the reference's result (the pulled rows of a full pass, zero elsewhere;
+    max / min's +-inf -> 0), bit for bit between them, and a UDF message or
+    u_add_v always takes the full pass or the subgraph."""
     n, e = 300, 5000
     u, v = rand_graph(n, e, 29)
     v[:400] = 7
@@ -1251,15 +1253,19 @@ def test_pull_full_pass_and_subgraph_agree(msg, red, on_gpu, monkeypatch):
         ref_msg = {"u_mul_e": ("mul", x, w), "copy_u": ("copy_lhs", x, None),
                    "copy_e": ("copy_rhs", None, w)}[msg]
     got = {}
-    for full in (True, False):
-        monkeypatch.setattr(hg, "PULL_FULL_PASS", 10 ** 9 if full else 0)
+    for mode, full, rows_max in (("full", 10 ** 9, -1), ("subgraph", 0, -1),
+                                 ("rows", 0, hg.PULL_ROWS_MAX_DEGREE)):
+        monkeypatch.setattr(hg, "PULL_FULL_PASS", full)
+        monkeypatch.setattr(hg, "PULL_ROWS_MAX_DEGREE", rows_max)
         g = dgl.graph((u, v), num_nodes=n)
         g.ndata["x"] = torch.from_numpy(x).cuda() if on_gpu else x
         g.edata["e"] = torch.from_numpy(w).cuda() if on_gpu else w
         g.pull(targets, message, getattr(fn, red)("m", "h"))
         h = g.ndata["h"]
-        got[full] = h.cpu().numpy() if isinstance(h, torch.Tensor) else np.asarray(h)
-    np.testing.assert_array_equal(got[True], got[False])
+        got[mode] = h.cpu().numpy() if isinstance(h, torch.Tensor) else np.asarray(h)
+    np.testing.assert_array_equal(got["full"], got["subgraph"])
+    np.testing.assert_array_equal(got["rows"], got["subgraph"])
+    got[False] = got["subgraph"]
     if ref_msg is None:
         msgs = x[u] + x[v]
         full_ref = oracle.gspmm(u, v, n, "copy_rhs", red, None, msgs)
@@ -1269,6 +1275,58 @@ def test_pull_full_pass_and_subgraph_agree(msg, red, on_gpu, monkeypatch):
     want = np.zeros_like(full_ref)
     want[targets] = full_ref[targets]
     close(got[False], want, np.abs(want) + 1e-12, np.float64, "pull {} {}".format(msg, red))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_gspmm_rows_reduces_the_listed_rows_whole(dtype):
+    """mdgl_gspmm_rows through the C ABI: the listed rows of the graph's CSR,
+    each whole (a row four times the chunk length folds in CSR order, bit for
+    bit with the oracle for sum / mean / max / min and their args), every
+    other row of the output untouched, ids outside the graph skipped and a
+    row listed twice written with the same values; pull on such rows goes
+    the same way and matches update_all's rows that are not split."""
+    from mojodgl import _lib
+
+    n, e = 400, 30000
+    u, v = rand_graph(n, e, 61)
+    v[:2048] = 5  # a row of more than CHUNK_LEN in-edges: split by update_all, whole here
+    rng = np.random.default_rng(62)
+    x = rng.normal(size=(n, 12)).astype(dtype)
+    w = rng.normal(size=(e, 12)).astype(dtype)
+    g = dgl.graph((u, v), num_nodes=n)
+    csr = g._device_csr("in")
+    tdt = torch.float32 if dtype == np.float32 else torch.float64
+    xt, wt = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
+    listed = np.array([5, 0, 399, 5, -1, 400, 123, 77], dtype=np.int32)  # 5 twice; two outside
+    rows_t = torch.from_numpy(listed).cuda()
+    keep = np.unique(listed[(listed >= 0) & (listed < n)])
+    for red in ("sum", "mean", "max", "min"):
+        out = torch.full((n, 12), 7.0, dtype=tdt, device="cuda")
+        au = torch.full((n, 12), -9, dtype=torch.int32, device="cuda")
+        ae = torch.full((n, 12), -9, dtype=torch.int32, device="cuda")
+        rc = _lib.lib().mdgl_gspmm_rows(
+            csr.indptr.data_ptr(), csr.indices.data_ptr(), csr.eid.data_ptr(), xt.data_ptr(),
+            wt.data_ptr(), out.data_ptr(), n, _lib.BINARY_OPS["mul"], 12, 12, 12,
+            _lib.REDUCERS[red], None, 0, None, None, au.data_ptr(), ae.data_ptr(),
+            rows_t.data_ptr(), len(listed), 0, _lib.dtype_code(dtype), _lib.stream())
+        _lib.check(rc, "gspmm_rows")
+        got, gu, ge = out.cpu().numpy(), au.cpu().numpy(), ae.cpu().numpy()
+        others = np.setdiff1d(np.arange(n), keep)
+        assert np.all(got[others] == 7.0) and np.all(gu[others] == -9) and np.all(ge[others] == -9)
+        if red in ("max", "min"):
+            want, ru, re_ = oracle.gspmm(u, v, n, "mul", red, x, w, dtype, with_arg=True)
+            np.testing.assert_array_equal(gu[keep], ru[keep], err_msg=red)
+            np.testing.assert_array_equal(ge[keep], re_[keep], err_msg=red)
+        else:
+            want = oracle.gspmm(u, v, n, "mul", red, x, w, dtype)
+        np.testing.assert_array_equal(got[keep], want[keep], err_msg=red)
+    # pull takes the same path: the long row whole, others zero
+    g.ndata["x"] = xt
+    g.edata["e"] = wt
+    g.pull(keep, fn.u_mul_e("x", "e", "m"), fn.sum("m", "h"))
+    want = np.zeros((n, 12), dtype=dtype)
+    want[keep] = oracle.gspmm(u, v, n, "mul", "sum", x, w, dtype)[keep]
+    np.testing.assert_array_equal(g.ndata["h"].cpu().numpy(), want)
 
 
 def test_graph_from_gpu_ids_is_built_on_the_gpu():
