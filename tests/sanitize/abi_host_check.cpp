@@ -96,6 +96,16 @@ static void gspmm_arguments() {
   EXPECT(mdgl_gspmm(dummy, dummy, dummy, dummy, dummy, dummy, 5, 2, 8, 8, 8, 0, nullptr, 0,
                     nullptr, nullptr, nullptr, nullptr, dummy, dummy, 3, 4, dummy, dummy, 1,
                     nullptr, 0, 0, MDGL_FLOAT32, nullptr) == MDGL_EWORKSPACE);
+  // the row-list form: a negative count, or a non-empty list without its rows
+  EXPECT(mdgl_gspmm_rows(dummy, dummy, dummy, dummy, dummy, dummy, 5, 2, 8, 8, 8, 0, nullptr, 0,
+                         nullptr, nullptr, nullptr, nullptr, nullptr, -1, 0, MDGL_FLOAT32,
+                         nullptr) == MDGL_EINVAL);
+  EXPECT(mdgl_gspmm_rows(dummy, dummy, dummy, dummy, dummy, dummy, 5, 2, 8, 8, 8, 0, nullptr, 0,
+                         nullptr, nullptr, nullptr, nullptr, nullptr, 3, 0, MDGL_FLOAT32,
+                         nullptr) == MDGL_EINVAL);
+  EXPECT(mdgl_gspmm_rows(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 5, 2, 8, 8, 8, 0,
+                         nullptr, 0, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0,
+                         MDGL_FLOAT32, nullptr) == MDGL_OK);
   // the no-allocation form refuses partials beyond its scratch before anything else
   EXPECT(mdgl_gspmm_noalloc(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 10, 2, 4096,
                             4096, 4096, 0, nullptr, 0, nullptr, nullptr, nullptr, nullptr,
@@ -134,6 +144,7 @@ static void sizes_and_geometry() {
 
 static void other_entry_points() {
   EXPECT(mdgl_workers() > 1);
+  EXPECT(mdgl_trace_ranges() == 0 || mdgl_trace_ranges() == 1);
   EXPECT(mdgl_segment_reduce(nullptr, nullptr, nullptr, 0, 4, 0, 0, 0, MDGL_FLOAT32, nullptr) ==
          MDGL_OK);
   EXPECT(mdgl_segment_reduce(nullptr, nullptr, nullptr, 3, 4, 7, 0, 0, MDGL_FLOAT32, nullptr) ==

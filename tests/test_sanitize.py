@@ -38,10 +38,13 @@ def _clean(stderr):
     return "AddressSanitizer" not in stderr and "runtime error" not in stderr
 
 
-def test_abi_host_code_under_sanitizers():
+@pytest.mark.parametrize("roctx", ["0", "1"])
+def test_abi_host_code_under_sanitizers(roctx):
+    """The host checks with the roctx ranges off and on (the roctx library
+    opened at run time and a range pushed and popped around every call)."""
     exe = _make("_build/abi_host_check")
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0",
-               UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1")
+               UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1", MDGL_ROCTX=roctx)
     proc = subprocess.run([exe], capture_output=True, text=True, timeout=300, env=env)
     assert proc.returncode == 0 and _clean(proc.stderr), proc.stdout + proc.stderr
     assert "abi host checks passed" in proc.stdout
