@@ -355,6 +355,8 @@ class DGLGraph(object):
         params = int(CHUNK_LEN)
         cached = self._dcsr.get(kind)
         if cached is None or cached.params != params:
+            if cached is not None:
+                self._launches.clear()  # replays of the old schedules (they hold its CSR)
             cached = _DeviceCSR(self._device_raw(kind), params)
             self._dcsr[kind] = cached
         return cached

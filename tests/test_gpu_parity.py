@@ -487,11 +487,13 @@ def test_gspmm_replayed_launches_match_the_full_path(dtype, monkeypatch):
             assert len(g._launches) == count, what  # replayed, not recorded again
             same(second, first, what + " replay")
             same(second, run(dgl.graph((u, v), num_nodes=n), op, red, L, R), what + " fresh")
-    # the graph of the last round met another chunk length: its replays are dropped
+    # the graph of the last round met another chunk length: its replays are
+    # dropped with the CSR they were made for
     monkeypatch.setattr(hg, "CHUNK_LEN", 2 ** 30)
-    for op, red, L, R in cases[:3]:
+    for i, (op, red, L, R) in enumerate(cases[:3]):
         same(run(g, op, red, L, R), run(dgl.graph((u, v), num_nodes=n), op, red, L, R),
              "{} {} after a new chunk length".format(op, red))
+        assert len(g._launches) == i + 1
     # operands the full path converts are never replayed
     g = dgl.graph((u, v), num_nodes=n)
     other = torch.float64 if dtype == torch.float32 else torch.float32
