@@ -377,15 +377,15 @@ def _subset_softmax_grad(grouping, a, grad_out):
     dx[i] = a[i] * (G[i] - s[endpoint i]) with s the per-group sums of G * a
     (folded in the group's order of appearance); rows past k are zero."""
     L = a.shape[0]
-    a2 = a.reshape(L, -1)
-    d = a2.shape[1]
+    d = math.prod(a.shape[1:])
+    a2 = a.reshape(L, d)
     dx = torch.zeros_like(a2)
     endpoint = grouping.get("endpoint")
     if endpoint is None or endpoint.numel() == 0 or d == 0:
         return dx.reshape(a.shape)
     k = endpoint.numel()
     indptr = grouping["indptr"]
-    gk = grad_out.contiguous().reshape(L, -1)[:k]
+    gk = grad_out.contiguous().reshape(L, d)[:k]
     _group_softmax_grad(a2[:k], gk, endpoint, indptr, indptr.numel() - 1,
                         order=grouping["eid"], out=dx[:k])
     return dx.reshape(a.shape)
@@ -487,9 +487,11 @@ class EdgeSoftmax(torch.autograd.Function):
         if ctx.grouping is not None:
             dx = _subset_softmax_grad(ctx.grouping, a, grad_out)
             return None, _back(dx, ctx.like), None, None
-        E = a.shape[0]
-        a2 = a.reshape(E, -1)
-        G = grad_out.contiguous().reshape(E, -1)
+        E, d = a.shape[0], math.prod(a.shape[1:])
+        if E == 0 or d == 0:  # no logits: the gradient is as empty as they are
+            return None, _back(torch.zeros_like(a), ctx.like), None, None
+        a2 = a.reshape(E, d)
+        G = grad_out.contiguous().reshape(E, d)
         p = _gsddmm(g, "mul", G, a2, "e", "e")
         row = "v" if norm_by == "dst" else "u"
         s = _node_reduce(g, p, row).contiguous()

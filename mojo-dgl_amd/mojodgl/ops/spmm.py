@@ -297,6 +297,9 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
             _lib.ptr(sched.chunk_start), sched.num_chunks, sched.chunk_len,
             _lib.ptr(sched.heavy_rows), _lib.ptr(sched.heavy_ptr), sched.num_heavy, _lib.ptr(ws),
             nbytes, flags, dcode, _lib.stream()]
+        if num_edges == 0:
+            _edge_buffers_non_null(args, (1, 2, 4))
+            replay = False
         _lib.check(_lib.lib().mdgl_gspmm(*args), "gspmm")
         if replay:
             launch = _Launch()
@@ -315,15 +318,26 @@ def _run(g, op, reduce_op, lhs_data, rhs_data, replace_inf=False, want_arg=False
     return out, arg_u, arg_e, as_torch, dev
 
 
+def _edge_buffers_non_null(args, positions):
+    """On a graph without edges no row has a slot, so the kernels read no
+    edge data; the ABI still takes the edge buffers (empty GPU tensors, whose
+    address is 0) as non-null pointers: the CSR's indptr stands in."""
+    for i in positions:
+        if not args[i]:
+            args[i] = args[0]
+
+
 def _run_rows(csr, rows, code, reduce_op, lhs, rhs, out, arg_u, arg_e, dl, dr, dout, nd, lsp,
               rsp, flags, dcode, arg, arg_dtype, as_torch, dev):
     """The listed rows of a gspmm over `csr` (mdgl_gspmm_rows), into the
     zero-filled results."""
-    _lib.check(_lib.lib().mdgl_gspmm_rows(
-        csr.indptr.data_ptr(), csr.indices.data_ptr(), csr.eid.data_ptr(), _lib.ptr(lhs),
-        _lib.ptr(rhs), out.data_ptr(), out.shape[0], code, dl, dr, dout, REDUCERS[reduce_op],
-        None, nd, lsp, rsp, _lib.ptr(arg_u), _lib.ptr(arg_e), rows.data_ptr(), rows.shape[0],
-        flags, dcode, _lib.stream()), "gspmm_rows")
+    args = [csr.indptr.data_ptr(), csr.indices.data_ptr(), csr.eid.data_ptr(), _lib.ptr(lhs),
+            _lib.ptr(rhs), out.data_ptr(), out.shape[0], code, dl, dr, dout,
+            REDUCERS[reduce_op], None, nd, lsp, rsp, _lib.ptr(arg_u), _lib.ptr(arg_e),
+            rows.data_ptr(), rows.shape[0], flags, dcode, _lib.stream()]
+    if csr.eid.shape[0] == 0:
+        _edge_buffers_non_null(args, (1, 2, 4))
+    _lib.check(_lib.lib().mdgl_gspmm_rows(*args), "gspmm_rows")
     if arg:
         arg_u = arg_u.to(arg_dtype)
         arg_e = arg_e.to(arg_dtype)
@@ -351,6 +365,8 @@ def _mul_sum_dot(g, grad, y, x, kind="out"):
     E = g.number_of_edges()
     if X.shape != G.shape or Y.shape[0] != E or G.shape[0] != num_rows or dr == 0:
         return None
+    if E == 0:  # no messages: both gradients are zero
+        return torch.zeros_like(x), torch.zeros_like(y)
     csr = g._device_csr(kind)
     sched = csr.chunks
     gdev = _lib.device()

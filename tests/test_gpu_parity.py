@@ -434,6 +434,59 @@ def test_gspmm_zero_degree_and_empty_graph():
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_graph_with_nodes_and_no_edges(dtype):
+    """A graph of nodes without edges (empty GPU edge buffers, whose address
+    is 0): gspmm gives every row the reduce identity (args -1), twice in a
+    row (the second call a replay), update_all and pull give zeros for every
+    builtin, gsddmm and edge_softmax give empty results, and the gradients
+    through them are zero or empty."""
+    from mojodgl.ops import spmm
+
+    n = 37
+    empty = np.zeros(0, dtype=np.int64)
+    g = dgl.graph((empty, empty), num_nodes=n)
+    dev = torch.device("cuda")
+    x = torch.randn(n, 8, 4, dtype=dtype, device=dev)
+    w = torch.randn(0, 8, 1, dtype=dtype, device=dev)
+    ident = {"sum": 0.0, "mean": 0.0, "max": -np.inf, "min": np.inf}
+    for _ in range(2):
+        for op, L, R in (("mul", x, w), ("add", x, w), ("copy_lhs", x, None),
+                         ("copy_rhs", None, w)):
+            for red in ("sum", "mean", "max", "min"):
+                out, (au, ae) = spmm._gspmm(g, op, red, L, R)
+                assert out.shape == (n, 8, 4 if op != "copy_rhs" else 1)
+                assert torch.all(out == ident[red]), (op, red)
+                if au is not None:
+                    assert torch.all(au == -1) and torch.all(ae == -1)
+    g.ndata["x"] = x
+    g.edata["w"] = w
+    for msg in (fn.u_mul_e("x", "w", "m"), fn.copy_u("x", "m"), fn.copy_e("w", "m"),
+                fn.u_add_v("x", "x", "m")):
+        for red in ("sum", "mean", "max", "min"):
+            g.update_all(msg, getattr(fn, red)("m", "h"))
+            assert torch.all(g.ndata["h"] == 0)
+            g.pull(np.array([0, 5, 36]), msg, getattr(fn, red)("m", "p"))
+            assert torch.all(g.ndata["p"] == 0)
+    g.update_all(lambda edges: {"m": edges.src["x"] * 2}, fn.sum("m", "h"))
+    assert torch.all(g.ndata["h"] == 0)
+    assert ops.u_add_v(g, x, x).shape == (0, 8, 4)
+    assert ops.edge_softmax(g, w).shape == (0, 8, 1)
+    # gradients: zero for the node operand, empty for the edge operand
+    xr = x.clone().requires_grad_()
+    el = torch.randn(n, 8, 1, dtype=dtype, device=dev, requires_grad=True)
+    a = ops.edge_softmax(g, torch.nn.functional.leaky_relu(ops.u_add_v(g, el, el), 0.2))
+    wr = a.detach().clone().requires_grad_()
+    out = ops.u_mul_e_sum(g, xr, wr) + ops.u_mul_e_sum(g, xr, a)
+    out.backward(torch.ones_like(out))
+    assert torch.all(xr.grad == 0) and wr.grad.shape == (0, 8, 1)
+    assert el.grad is None or torch.all(el.grad == 0)
+    for red in ("max", "min", "mean"):
+        xm = x.clone().requires_grad_()
+        ops.gspmm(g, "copy_lhs", red, xm, None).sum().backward()
+        assert torch.all(xm.grad == 0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 def test_gspmm_replayed_launches_match_the_full_path(dtype, monkeypatch):
     """A gspmm call shape seen before on a graph replays its launch: the
     results of the replay equal those of the full path on a fresh graph, bit
