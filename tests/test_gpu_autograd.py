@@ -12,6 +12,8 @@ formed in a different order); the float32 GAT chain to rtol 1e-4 / atol 1e-5
 of the float64 chain.
 """
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -214,7 +216,7 @@ def test_gsddmm_copy_and_broadcast_backward():
 # ------------------------------------------------------------------ edge_softmax
 def ref_edge_softmax(u, v, n, logits, norm_by):
     key = torch.from_numpy(v if norm_by == "dst" else u).to(DEV)
-    flat = logits.reshape(logits.shape[0], -1)
+    flat = logits.reshape(logits.shape[0], math.prod(logits.shape[1:]))
     idx = key[:, None].expand_as(flat)
     mx = torch.full((n, flat.shape[1]), -float("inf"), dtype=flat.dtype, device=DEV)
     mx = mx.scatter_reduce(0, idx, flat, "amax", include_self=True)
@@ -292,7 +294,7 @@ def ref_segment_ids(seglen):
 
 def ref_segment_reduce(seglen, value, reducer):
     ids = ref_segment_ids(seglen)
-    flat = value.reshape(value.shape[0], -1)
+    flat = value.reshape(value.shape[0], math.prod(value.shape[1:]))
     S, d = len(seglen), flat.shape[1]
     if reducer in ("sum", "mean"):
         out = torch.zeros((S, d), dtype=flat.dtype, device=DEV).index_add(0, ids, flat)
@@ -310,7 +312,7 @@ def ref_segment_reduce(seglen, value, reducer):
 
 def ref_segment_softmax(seglen, value):
     ids = ref_segment_ids(seglen)
-    flat = value.reshape(value.shape[0], -1)
+    flat = value.reshape(value.shape[0], math.prod(value.shape[1:]))
     S = len(seglen)
     mx = torch.full((S, flat.shape[1]), -float("inf"), dtype=flat.dtype, device=DEV)
     mx = mx.scatter_reduce(0, ids[:, None].expand_as(flat), flat, "amax", include_self=True)
@@ -680,3 +682,100 @@ def test_update_all_gradient_is_zero_where_inf_became_zero(red):
                                 for f in range(e) if v[f] == v[e])
             want = float(xd[u[e], k]) if first else 0.0
             assert float(gy[e, k]) == want, (e, k)
+
+
+# ------------------------------------------------------------------ randomized gradients
+_RANDOM_XY = [((3, 4), (3, 4)), ((3, 4), (3, 1)), ((8, 32), (8, 1)), ((4, 16), (4, 1)),
+              ((64,), (1,)), ((5,), (5,)), ((2, 6), (2, 1)), ((3, 130), (3, 1)), ((300,), (300,)),
+              ((1,), (1,))]
+
+
+def _random_graph(rng, distinct_with_loops):
+    """Random edges (some graphs with a hub or with no edges at all); for
+    max / min, distinct non-loop edges plus a loop on every node, so no row
+    is empty and no two messages of a row tie."""
+    n = int(rng.integers(1, 500))
+    e = int(rng.integers(0, 5000)) if rng.random() > 0.05 else 0
+    u, v = rng.integers(0, n, e), rng.integers(0, n, e)
+    if e and rng.random() < 0.4:
+        v[: int(rng.integers(1, e + 1))] = rng.integers(0, n)
+    if distinct_with_loops:
+        pairs = np.unique(np.stack([u, v], 1), axis=0) if e else np.zeros((0, 2), np.int64)
+        pairs = pairs[pairs[:, 0] != pairs[:, 1]]
+        u = np.concatenate([pairs[:, 0], np.arange(n)])
+        v = np.concatenate([pairs[:, 1], np.arange(n)])
+        p = rng.permutation(u.size)
+        u, v = u[p], v[p]
+    return n, u.astype(np.int64), v.astype(np.int64)
+
+
+def _random_leaf(shape, rng, positive=False):
+    t = torch.from_numpy(rng.standard_normal(shape)).to(DEV)
+    return (t.abs() + 0.5 if positive else t).requires_grad_(True)
+
+
+def _check_pair(out, ref, inputs, seed, tag, fwd_atol=1e-12):
+    torch.testing.assert_close(out, ref, rtol=1e-11, atol=fwd_atol,
+                               msg=lambda m: "{} forward: {}".format(tag, m))
+    for a, b in zip(grads(out, inputs, seed), grads(ref, inputs, seed)):
+        torch.testing.assert_close(a, b, rtol=1e-9, atol=1e-11,
+                                   msg=lambda m: "{} gradient: {}".format(tag, m))
+
+
+def _random_gradient_case(seed):
+    rng = np.random.default_rng(77000 + seed)
+    op = ["copy_lhs", "copy_rhs", "add", "sub", "mul", "div"][rng.integers(6)]
+    red = ["sum", "mean", "max", "min"][rng.integers(4)]
+    n, u, v = _random_graph(rng, red in ("max", "min"))
+    E = u.size
+    g = dgl.graph((u, v), num_nodes=n)
+    xs, ys = _RANDOM_XY[rng.integers(len(_RANDOM_XY))]
+    ys = xs if op == "copy_rhs" else ys
+    tag = "seed {} n {} E {} {} {} {} {}".format(seed, n, E, op, red, xs, ys)
+    x = _random_leaf((n,) + xs, rng) if op != "copy_rhs" else None
+    y = _random_leaf((E,) + ys, rng, positive=(op == "div")) if op != "copy_lhs" else None
+    _check_pair(ops.gspmm(g, op, red, x, y), ref_spmm(u, v, n, op, red, x, y), [x, y], seed,
+                tag)
+
+    tx, ty = ["u", "v", "e"][rng.integers(3)], ["u", "v", "e"][rng.integers(3)]
+    sop = ["add", "sub", "mul", "div", "dot"][rng.integers(5)]
+    xs2, ys2 = _RANDOM_XY[rng.integers(len(_RANDOM_XY))]
+    ys2 = xs2 if sop == "dot" else ys2
+    x2 = _random_leaf(((E if tx == "e" else n),) + xs2, rng)
+    y2 = _random_leaf(((E if ty == "e" else n),) + ys2, rng, positive=(sop == "div"))
+    _check_pair(ops.gsddmm(g, sop, x2, y2, lhs_target=tx, rhs_target=ty),
+                ref_sddmm(u, v, sop, x2, y2, tx, ty), [x2, y2], seed + 1,
+                "{} | gsddmm {} {} {} {} {}".format(tag, sop, tx, ty, xs2, ys2))
+
+    heads = [(), (1,), (4, 1), (8, 1), (2, 3, 1)][rng.integers(5)]
+    norm_by = ["dst", "src"][rng.integers(2)]
+    scale = float(rng.choice([1.0, 3.0, 30.0]))  # 30: exp(x - max) underflows in places
+    lg = (torch.from_numpy(rng.standard_normal((E,) + heads)).to(DEV) * scale).requires_grad_(True)
+    _check_pair(ops.edge_softmax(g, lg, norm_by=norm_by), ref_edge_softmax(u, v, n, lg, norm_by),
+                [lg], seed + 2, "{} | edge_softmax {} {}".format(tag, heads, norm_by),
+                fwd_atol=1e-13)
+
+    S = int(rng.integers(0, 300))
+    seglen = rng.poisson(float(rng.choice([0.5, 3, 20, 700])), S)
+    d = [(3, 2), (), (5,), (17,)][rng.integers(4)]
+    vals = _random_leaf((int(seglen.sum()),) + d, rng)
+    sred = ["sum", "mean", "max", "min"][rng.integers(4)]
+    sl = torch.from_numpy(seglen).to(DEV) if rng.random() < 0.5 else seglen
+    stag = "{} | segment {} S {} {}".format(tag, sred, S, d)
+    out = ops.segment_reduce(sl, vals, sred)
+    _check_pair(out, ref_segment_reduce(seglen, vals, sred).reshape(out.shape), [vals], seed + 3,
+                stag)
+    _check_pair(ops.segment_softmax(sl, vals), ref_segment_softmax(seglen, vals), [vals],
+                seed + 4, stag + " softmax", fwd_atol=1e-13)
+
+
+@pytest.mark.parametrize("block", range(4))
+def test_random_gradient_cases(block):
+    """Fixed-seed random cases through every differentiable op, float64,
+    against torch's autograd over the restatements above: graphs with hubs,
+    empty rows or no edges, every message op and reducer, broadcast edge
+    operands (the fused u_mul_e pass among them), all target pairs of
+    gsddmm, softmax heads and underflowing logits, empty and long
+    segments with lengths on the host or the GPU."""
+    for seed in range(block * 50, (block + 1) * 50):
+        _random_gradient_case(seed)
