@@ -556,7 +556,8 @@ def workload_gat(args):
 def time_gat_ops_cold(g, el, er, h, N, E, H, D, args):
     """The step's three libmdgl ops one at a time, each after a 512 MB write
     that evicts the L2 and the MALL (median and best of --reps, HIP events),
-    with the same algorithmic bytes as the step's figures."""
+    with the same algorithmic bytes as the step's figures; and copy_u_sum
+    over the same graph and node table, outside the step."""
     import torch
 
     import mojodgl.ops as ops
@@ -573,6 +574,11 @@ def time_gat_ops_cold(g, el, er, h, N, E, H, D, args):
          4 * (N + 1) + 8 * E + 4 * E * H * D + 4 * E * H + 4 * N * H * D, E * H * D),
     )
     out = {name: hbm_entry(cold(fn), nbytes, units) for name, fn, nbytes, units in ops_}
+    # not in the step: the same gspmm without the edge operand (the source
+    # rows, their ids and the output only), beside the read_rows ceilings
+    out["gspmm_copy_u_sum_not_in_step"] = hbm_entry(
+        cold(lambda: ops.copy_u_sum(g, h)), 4 * (N + 1) + 4 * E + 4 * E * H * D + 4 * N * H * D,
+        E * H * D)
     del e, a
     return out
 
@@ -595,7 +601,12 @@ def time_gather_ceilings(g, N, E, H, args):
         written (segment_reduce sum over runs of 64 rows): a streaming read;
       * stream_read_1.28GB / _2.56GB: a bare one-pass read (mdgl_read_stream,
         a persistent grid of 16-byte nontemporal loads), the read ceiling of
-        this GPU.
+        this GPU;
+      * read_rows_1KB_by_csr_source: the 1 KB rows of an (N, H * D) table
+        read by the in-CSR's sources in slot order and not written
+        (mdgl_read_rows): gspmm's source-row reads with nothing else;
+      * read_rows_1KB_by_csr_source_out_written: the same reads beside a
+        write of N 1 KB rows (gspmm's output volume).
     Each figure is GB/s of bytes moved per launch (4 index + gathered + written
     per row; read + written for the streaming reads)."""
     import torch
@@ -643,6 +654,24 @@ def time_gather_ceilings(g, N, E, H, args):
     out["rows_1KB_streamed"] = dict(t, bytes=nbytes, GBps=round(nbytes / t["median_ms"] / 1e6, 1),
                                     table_MB=round(rows * 1024 / 1e6, 1))
     del table, runs, view
+    # gspmm's source-row reads alone, then beside its output's write volume
+    indices = g._device_csr("in").indices
+    assert indices.numel() == E
+    table = torch.randn(N, 256, device="cuda", generator=gen)
+    dst = torch.empty(N, 256, device="cuda")
+    sink = torch.empty(int(L.mdgl_read_rows_sink_bytes(E)) // 4, device="cuda")
+    for name, dst_rows in (("read_rows_1KB_by_csr_source", 0),
+                           ("read_rows_1KB_by_csr_source_out_written", N)):
+        def read_rows():
+            _lib.check(L.mdgl_read_rows(table.data_ptr(), N, 1024, indices.data_ptr(), E,
+                                        dst.data_ptr(), dst_rows, sink.data_ptr(),
+                                        _lib.stream()), "read_rows")
+
+        t = cold(read_rows)
+        nbytes = E * (4 + 1024) + dst_rows * 1024
+        out[name] = dict(t, bytes=nbytes, GBps=round(nbytes / t["median_ms"] / 1e6, 1),
+                         table_MB=round(N * 1024 / 1e6, 1))
+    del table, dst, sink
     # the one-pass streaming read the bandwidth figures are judged against
     # (mdgl_read_stream: 2,048 workgroups striding with 16-byte nontemporal
     # loads, 32 KB per workgroup and round, next to nothing written), at the

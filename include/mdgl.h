@@ -334,6 +334,21 @@ int mdgl_edge_softmax_(const int32_t* indptr, const int32_t* indices, const int3
 int mdgl_read_stream(const void* src, int64_t bytes, void* sink, void* stream);
 int64_t mdgl_read_stream_sink_bytes(int64_t bytes);
 
+/* A bare read of rows by an index list: for i < n, the row idx[i] of `src`
+ * (src_rows rows of row_bytes bytes, a multiple of 16 in [16, 1024]; indices
+ * outside [0, src_rows) are skipped), a wavefront per 64 indices reading 16
+ * bytes per lane, 8 rows in flight. Wavefront w writes the XOR of the 16-byte
+ * vectors it read to sink[w] (mdgl_read_rows_sink_bytes(n) bytes, 16-byte
+ * aligned); with dst_rows > 0 it also writes, to each of the rows
+ * [w * dst_rows / W, (w + 1) * dst_rows / W) of `dst` (W = the wavefront
+ * count, rows of row_bytes), the XOR of each vector position over its rows.
+ * No counterpart in the reference: the ceiling of gspmm's source-row reads
+ * (the in-CSR's sources as the index list), alone and beside its output's
+ * write volume. */
+int mdgl_read_rows(const void* src, int64_t src_rows, int64_t row_bytes, const int32_t* idx,
+                   int64_t n, void* dst, int64_t dst_rows, void* sink, void* stream);
+int64_t mdgl_read_rows_sink_bytes(int64_t n);
+
 /* edge_softmax over a subset of edge ids, the whole call on the GPU with no
  * host read. Replaces the positional branch of the reference's host code
  * (python/mojodgl/ops/edge_softmax.py:119-158, the per-call Python grouping

@@ -453,6 +453,68 @@ hipError_t launch_read_stream(const void* src, int64_t bytes, void* sink, hipStr
   return hipGetLastError();
 }
 
+// A bare read of rows by an index list, the node-row access of gspmm with
+// nothing else: a wavefront per 64 indices (loaded at once, broadcast by
+// v_readlane), lane l reading the l-th 16-byte vector of each row, RR_U rows
+// in flight, folded by XOR. Indices outside [0, src_rows) are skipped. Each
+// wavefront writes its XOR (16 bytes) to sink[w]; with dst_rows > 0 it also
+// writes its lanes' XORs as the rows [w * dst_rows / W, (w + 1) * dst_rows / W)
+// of dst (W wavefronts, nontemporal stores): the same reads beside a write
+// volume, such as gspmm's output rows.
+constexpr int RR_U = 8;
+
+__global__ __launch_bounds__(BLOCK) void read_rows_kernel(
+    const rs_u4* __restrict__ src, int64_t src_rows, int vecs, const int32_t* __restrict__ idx,
+    int64_t n, rs_u4* __restrict__ dst, int64_t dst_rows, rs_u4* __restrict__ sink,
+    int64_t nblocks) {
+  const int64_t b = xcd_remap(blockIdx.x, nblocks);
+  const int64_t w = b * WAVES_PER_BLOCK + threadIdx.x / WAVE;
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int64_t base = w * WAVE;
+  if (base >= n) return;
+  const int cnt = n - base < WAVE ? (int)(n - base) : WAVE;
+  const int my = lane < cnt ? idx[base + lane] : -1;
+  const bool mine = lane < vecs;
+  rs_u4 x{0, 0, 0, 0};
+  for (int j = 0; j < cnt; j += RR_U) {
+    rs_u4 v[RR_U];
+#pragma unroll
+    for (int u = 0; u < RR_U; ++u) {
+      const int s = __builtin_amdgcn_readlane(my, j + u < cnt ? j + u : cnt - 1);
+      const bool ok = j + u < cnt && s >= 0 && s < src_rows && mine;
+      v[u] = ok ? src[(int64_t)s * vecs + lane] : rs_u4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < RR_U; ++u) x ^= v[u];
+  }
+  if (dst_rows > 0 && mine) {
+    const int64_t waves = (n + WAVE - 1) / WAVE;
+    const int64_t lo = w * dst_rows / waves, hi = (w + 1) * dst_rows / waves;
+    for (int64_t r = lo; r < hi; ++r) __builtin_nontemporal_store(x, dst + r * vecs + lane);
+  }
+  for (int off = 32; off >= 1; off >>= 1) {
+    x.x ^= __shfl_xor(x.x, off);
+    x.y ^= __shfl_xor(x.y, off);
+    x.z ^= __shfl_xor(x.z, off);
+    x.w ^= __shfl_xor(x.w, off);
+  }
+  if (lane == 0) sink[w] = x;
+}
+
+int64_t read_rows_sink_bytes(int64_t n) { return (n + WAVE - 1) / WAVE * 16; }
+
+hipError_t launch_read_rows(const void* src, int64_t src_rows, int64_t row_bytes,
+                            const int32_t* idx, int64_t n, void* dst, int64_t dst_rows, void* sink,
+                            hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  const int64_t waves = (n + WAVE - 1) / WAVE;
+  const int64_t blocks = (waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
+  hipLaunchKernelGGL(read_rows_kernel, dim3((unsigned)blocks), dim3(BLOCK), 0, s,
+                     static_cast<const rs_u4*>(src), src_rows, (int)(row_bytes / 16), idx, n,
+                     static_cast<rs_u4*>(dst), dst_rows, static_cast<rs_u4*>(sink), blocks);
+  return hipGetLastError();
+}
+
 hipError_t launch_cumsum_i64(const int64_t* src, int64_t* dst, int64_t n, hipStream_t s) {
   if (n <= 0) return hipSuccess;
   const int64_t tiles = (n + CS_TILE - 1) / CS_TILE;

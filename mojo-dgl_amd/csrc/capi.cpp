@@ -244,6 +244,25 @@ int64_t mdgl_read_stream_sink_bytes(int64_t bytes) {
   return bytes < 0 ? -1 : read_stream_sink_bytes(bytes);
 }
 
+int64_t mdgl_read_rows_sink_bytes(int64_t n) { return n < 0 ? -1 : read_rows_sink_bytes(n); }
+
+int mdgl_read_rows(const void* src, int64_t src_rows, int64_t row_bytes, const int32_t* idx,
+                   int64_t n, void* dst, int64_t dst_rows, void* sink, void* stream) {
+  MDGL_RANGE();
+  if (row_bytes < 16 || row_bytes > 1024 || row_bytes % 16)
+    return fail(MDGL_EINVAL, "read_rows: row_bytes must be a multiple of 16 in [16, 1024]");
+  if (src_rows < 0 || n < 0 || dst_rows < 0) return fail(MDGL_EINVAL, "read_rows: negative size");
+  if (n >= (int64_t(1) << 31)) return fail(MDGL_EINVAL, "read_rows: 2**31 or more indices");
+  if (n == 0) return MDGL_OK;
+  if (!src || !idx || !sink || (dst_rows > 0 && !dst))
+    return fail(MDGL_EINVAL, "read_rows: null buffer");
+  if (!aligned(src, 16) || !aligned(sink, 16) || (dst_rows > 0 && !aligned(dst, 16)))
+    return fail(MDGL_EINVAL, "read_rows: buffers must be 16-byte aligned");
+  return hip_status(launch_read_rows(src, src_rows, row_bytes, idx, n, dst, dst_rows, sink,
+                                     (hipStream_t)stream),
+                    "read_rows");
+}
+
 int mdgl_read_stream(const void* src, int64_t bytes, void* sink, void* stream) {
   MDGL_RANGE();
   if (bytes < 0 || bytes % 16) return fail(MDGL_EINVAL, "read_stream: bytes must be a multiple of 16");

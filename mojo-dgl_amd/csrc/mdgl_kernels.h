@@ -253,6 +253,10 @@ hipError_t launch_build_csr(const int32_t* key, const int32_t* other, int64_t nu
 hipError_t launch_cumsum_i64(const int64_t* src, int64_t* dst, int64_t n, hipStream_t s);
 int64_t read_stream_sink_bytes(int64_t bytes);
 hipError_t launch_read_stream(const void* src, int64_t bytes, void* sink, hipStream_t s);
+int64_t read_rows_sink_bytes(int64_t n);
+hipError_t launch_read_rows(const void* src, int64_t src_rows, int64_t row_bytes,
+                            const int32_t* idx, int64_t n, void* dst, int64_t dst_rows, void* sink,
+                            hipStream_t s);
 // The positional edge_softmax plan built on the GPU (softmax_plan.hip):
 // positions grouped by the endpoint of their edge, rows binned by degree,
 // chunks of the long rows, the packed edge lists and the SoftDyn figures.

@@ -90,6 +90,8 @@ _SIGNATURES = {
     "mdgl_edge_softmax_positional_workspace_bytes": ([_I64, _I64, _I64, _P, _P, _C], _I64),
     "mdgl_read_stream": ([_P, _I64, _P, _P], _C),
     "mdgl_read_stream_sink_bytes": ([_I64], _I64),
+    "mdgl_read_rows": ([_P, _I64, _I64, _P, _I64, _P, _I64, _P, _P], _C),
+    "mdgl_read_rows_sink_bytes": ([_I64], _I64),
     "mdgl_gspmm_noalloc": ([_P, _P, _P, _P, _P, _P, _I64, _C, _I64, _I64, _I64, _C, _P, _C, _P, _P,
                             _P, _P, _P, _P, _I64, _I32, _P, _P, _I64, _C, _C, _P], _C),
     "mdgl_gspmm_mul_sum_dot": ([_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _C, _P,

@@ -1011,6 +1011,46 @@ def test_read_stream_reads_every_vector():
         np.testing.assert_array_equal(got, want, err_msg=str(i))
 
 
+@pytest.mark.parametrize("row_bytes,n,dst_rows", [(1024, 64 * 50 + 17, 0), (1024, 1000, 2500),
+                                                   (48, 130, 7), (16, 64, 0)])
+def test_read_rows_folds_the_listed_rows(row_bytes, n, dst_rows):
+    """mdgl_read_rows: wavefront w (indices [64 w, 64 w + 64)) writes to
+    sink[w] the XOR of every 16-byte vector of its rows, skipping indices
+    outside the table (negative or past its rows); with dst_rows it writes
+    each vector position's XOR over its rows to its share of dst's rows."""
+    from mojodgl import _lib
+
+    L = _lib.lib()
+    rng = np.random.default_rng(row_bytes + n)
+    rows, vecs = 300, row_bytes // 16
+    table = rng.integers(-2 ** 31, 2 ** 31, (rows, vecs, 4), dtype=np.int64).astype(np.int32)
+    idx = rng.integers(-3, rows + 3, n).astype(np.int32)
+    src = torch.from_numpy(table).cuda()
+    idt = torch.from_numpy(idx).cuda()
+    waves = -(-n // 64)
+    assert int(L.mdgl_read_rows_sink_bytes(n)) == waves * 16
+    sink = torch.zeros(waves * 4, dtype=torch.int32, device="cuda")
+    dst = torch.full((max(dst_rows, 1), vecs, 4), 7, dtype=torch.int32, device="cuda")
+    _lib.check(L.mdgl_read_rows(src.data_ptr(), rows, row_bytes, idt.data_ptr(), n,
+                                dst.data_ptr(), dst_rows, sink.data_ptr(), _lib.stream()),
+               "read_rows")
+    want_sink = np.zeros((waves, 4), dtype=np.int32)
+    want_dst = np.full((max(dst_rows, 1), vecs, 4), 7, dtype=np.int32)
+    for w in range(waves):
+        sel = idx[w * 64:(w + 1) * 64]
+        sel = sel[(sel >= 0) & (sel < rows)]
+        per_pos = np.bitwise_xor.reduce(table[sel], axis=0) if sel.size else \
+            np.zeros((vecs, 4), np.int32)
+        want_sink[w] = np.bitwise_xor.reduce(per_pos, axis=0)
+        for r in range(w * dst_rows // waves, (w + 1) * dst_rows // waves):
+            want_dst[r] = per_pos
+    np.testing.assert_array_equal(sink.cpu().numpy().reshape(waves, 4), want_sink)
+    np.testing.assert_array_equal(dst.cpu().numpy(), want_dst)
+    with pytest.raises(dgl.DGLError, match="row_bytes"):
+        _lib.check(L.mdgl_read_rows(src.data_ptr(), rows, 24, idt.data_ptr(), n, None, 0,
+                                    sink.data_ptr(), _lib.stream()), "read_rows")
+
+
 # ------------------------------------------------------------------ array helpers
 @pytest.mark.parametrize("n", [1, 100, 4095, 4096, 4097, 12289, 1_000_003])
 def test_cumsum_clamp_replace_inf_through_the_abi(n):
