@@ -1626,6 +1626,33 @@ def test_edge_softmax_power_law_and_mask_through_the_abi():
             np.testing.assert_array_equal(got, first)
 
 
+@pytest.mark.parametrize("dtype,heads", [(np.float32, 8), (np.float32, 16), (np.float32, 24),
+                                         (np.float64, 4), (np.float64, 8)])
+def test_edge_softmax_row_pass_write_and_table_pass_agree(dtype, heads, monkeypatch):
+    """edge_softmax(ALL) writes rows of whole 64-byte pieces from its row
+    pass and other rows through the (max, sum) table and an edge-parallel
+    pass: on a power-law graph (hub rows split into chunks, packed rows)
+    both forms, forced in turn, give the same bits, within the tolerance
+    of the oracle."""
+    es = importlib.import_module("mojodgl.ops.edge_softmax")  # the module, not the function
+
+    rng = np.random.default_rng(heads)
+    n = 3000
+    deg = np.minimum(rng.zipf(1.8, n), 5000)
+    v = rng.permutation(np.repeat(np.arange(n), deg))
+    u = rng.integers(0, n, v.size)
+    logits = (rng.normal(size=(v.size, heads, 1)) * 3).astype(dtype)
+    g = dgl.graph((u, v), num_nodes=n)
+    lt = torch.from_numpy(logits).cuda()
+    got = {}
+    for name, row_bytes in (("row pass", 1), ("table pass", 1 << 30)):
+        monkeypatch.setattr(es, "TWO_PASS_ROW_BYTES", row_bytes)
+        got[name] = ops.edge_softmax(g, lt).cpu().numpy()
+    np.testing.assert_array_equal(got["row pass"], got["table pass"])
+    ref = oracle.edge_softmax(u, v, n, logits, dtype=np.float64)
+    close(got["row pass"], ref, ref, dtype, "edge_softmax {} heads".format(heads))
+
+
 def test_results_are_deterministic_run_to_run():
     """No atomics anywhere: every op gives the same bits on a second run
     (power-law rows split into chunks, packed softmax rows, grouped GEMM)."""
