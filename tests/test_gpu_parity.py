@@ -1684,6 +1684,67 @@ def test_results_are_deterministic_run_to_run():
         assert torch.equal(x, y)
 
 
+def test_ops_follow_the_callers_stream():
+    """Every op launches on torch's current stream and orders its own side
+    copies after it: on a second stream (default priority), with the inputs
+    made there by kernels still running when the ops are queued (a chain of
+    large products in front of them), the results equal the default
+    stream's bit for bit -- the GAT layer, segment ops with GPU lengths,
+    edge_softmax over GPU eids, gather_mm and a backward pass."""
+    rng = np.random.default_rng(93)
+    n = 4000
+    z = np.minimum(rng.zipf(2.1, n), 2000)
+    deg = rng.multinomial(90000, z / z.sum())
+    v = rng.permutation(np.repeat(np.arange(n), deg))
+    u = rng.integers(0, n, v.size)
+    E = v.size
+    g = dgl.graph((torch.from_numpy(u).cuda(), torch.from_numpy(v).cuda()), num_nodes=n)
+    seglen_h = rng.poisson(9, 1500)
+    eids_h = rng.integers(0, E, E // 3)
+
+    def inputs(busy):
+        # the inputs come out of the stream's own queue, behind `busy`
+        gen = torch.Generator(device="cuda").manual_seed(94)
+        base = torch.randn(6_000_000, device="cuda", generator=gen)
+        if busy:
+            m = torch.randn(2048, 2048, device="cuda", generator=gen)
+            for _ in range(12):
+                m = torch.tanh(m @ m)
+            base = base + m.sum() * 0
+        h = base[:n * 64].reshape(n, 4, 16).clone()
+        el = base[n * 64:n * 68].reshape(n, 4, 1).clone()
+        x = base[:E * 4].reshape(E, 4, 1).clone()
+        seglen = torch.from_numpy(seglen_h).cuda()
+        val = base[:int(seglen_h.sum()) * 8].reshape(-1, 8).clone()
+        a = base[:20000 * 64].reshape(20000, 64).clone()
+        b = base[:8 * 64 * 64].reshape(8, 64, 64).clone()
+        idx = torch.from_numpy(rng_idx).cuda()
+        return h, el, x, seglen, val, a, b, idx
+
+    rng_idx = rng.integers(0, 8, 20000)
+
+    def run(busy):
+        h, el, x, seglen, val, a, b, idx = inputs(busy)
+        e = ops.u_add_v(g, el, el)
+        att = ops.edge_softmax(g, e)
+        hr = h.clone().requires_grad_()
+        z = ops.u_mul_e_sum(g, hr, att)
+        z.backward(torch.ones_like(z))
+        return [e, att, z.detach(), hr.grad, ops.copy_u_max(g, h),
+                ops.edge_softmax(g, x, eids=torch.from_numpy(eids_h).cuda()),
+                ops.segment_reduce(seglen, val, "max"), ops.segment_softmax(seglen, val),
+                ops.gather_mm(a, b, idx_b=idx)]
+
+    want = [t.clone() for t in run(False)]
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        got = run(True)
+    side.synchronize()
+    for i, (x, y) in enumerate(zip(want, got)):
+        assert torch.equal(x, y), i
+
+
 @pytest.mark.parametrize("d1", [32, 64, 96, 128])
 @pytest.mark.parametrize("d2", [1, 5, 128, 130, 256])
 def test_grouped_mm_block_resident_shapes(d1, d2):
