@@ -1745,6 +1745,71 @@ def test_ops_follow_the_callers_stream():
         assert torch.equal(x, y), i
 
 
+def test_ops_from_several_threads_share_a_graph():
+    """Four Python threads, each on its own stream, run the GAT layer, a
+    pull, segment ops with GPU lengths and gather_mm over one graph whose
+    device CSR, softmax plan and launch cache they build on first use
+    concurrently; every result equals the one computed alone on a separate
+    graph of the same edges (the library keeps its error text per thread and
+    has no other mutable state but the no-alloc scratch)."""
+    import threading
+
+    rng = np.random.default_rng(95)
+    n = 3000
+    z = np.minimum(rng.zipf(2.1, n), 1500)
+    deg = rng.multinomial(60000, z / z.sum())
+    v = rng.permutation(np.repeat(np.arange(n), deg))
+    u = rng.integers(0, n, v.size)
+    gen = torch.Generator(device="cuda").manual_seed(96)
+    h = torch.randn(n, 4, 16, device="cuda", generator=gen)
+    el = torch.randn(n, 4, 1, device="cuda", generator=gen)
+    seglen = torch.from_numpy(rng.poisson(6, 1000)).cuda()
+    val = torch.randn(int(seglen.sum()), 8, device="cuda", generator=gen)
+    a = torch.randn(10000, 64, device="cuda", generator=gen)
+    b = torch.randn(8, 64, 64, device="cuda", generator=gen)
+    idx = torch.randint(0, 8, (10000,), device="cuda", generator=gen)
+    pulled = np.arange(0, n, 3)
+
+    def run(g, tag):
+        # features under names of the thread's own
+        e = ops.u_add_v(g, el, el)
+        att = ops.edge_softmax(g, e)
+        g.ndata["h" + tag] = h
+        g.edata["a" + tag] = att
+        g.pull(pulled, fn.u_mul_e("h" + tag, "a" + tag, "m"), fn.sum("m", "p" + tag))
+        return [e, att, ops.u_mul_e_sum(g, h, att), g.ndata["p" + tag], ops.copy_u_max(g, h),
+                ops.segment_reduce(seglen, val, "sum"), ops.segment_softmax(seglen, val),
+                ops.gather_mm(a, b, idx_b=idx)]
+
+    want = [t.clone() for t in run(dgl.graph((u, v), num_nodes=n), "")]
+    torch.cuda.synchronize()
+    shared = dgl.graph((u, v), num_nodes=n)
+    results, errors = {}, []
+
+    def worker(k):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                outs = [run(shared, str(k)) for _ in range(3)]
+                outs = [[t.clone() for t in o] for o in outs]
+            s.synchronize()
+            results[k] = outs
+        except Exception as exc:  # reported below, in the test's thread
+            errors.append(repr(exc))
+
+    threads = [threading.Thread(target=worker, args=(k,)) for k in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not errors, errors
+    assert sorted(results) == [0, 1, 2, 3]
+    for k, outs in results.items():
+        for rep, got in enumerate(outs):
+            for i, (x, y) in enumerate(zip(want, got)):
+                assert torch.equal(x, y), (k, rep, i)
+
+
 @pytest.mark.parametrize("d1", [32, 64, 96, 128])
 @pytest.mark.parametrize("d2", [1, 5, 128, 130, 256])
 def test_grouped_mm_block_resident_shapes(d1, d2):
