@@ -242,6 +242,11 @@ class OpTimer:
 
 
 def run_steps(step, steps, warmup, timer):
+    """ms per step over `steps` timed steps (after `warmup`), bracketed by
+    synchronizations; then the same number of steps again with HIP events
+    around each op for `timer`'s per-op figures (kept out of the step's
+    clock: a launch-bound step would otherwise carry the events' host
+    cost)."""
     import torch
 
     for _ in range(warmup):
@@ -249,9 +254,12 @@ def run_steps(step, steps, warmup, timer):
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        step(timer)
+        step(None)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    for _ in range(steps):
+        step(timer)
+    torch.cuda.synchronize()
     timer.collect()
     return (t1 - t0) * 1e3 / steps
 
