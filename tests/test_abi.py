@@ -166,6 +166,18 @@ def test_invalid_arguments_are_rejected_without_launching(lib):
     rc = lib.mdgl_gspmm_rows(1, 1, 1, 1, 1, 1, 10, 2, 4, 4, 4, 7, None, 0, None, None, None,
                              None, 1, 3, 0, 0, None)
     assert rc == -1 and "reduce_op" in err(lib)
+    # the row-read ceiling: row sizes, counts, buffers and their alignment
+    for row_bytes in (0, 8, 24, 1040):
+        assert lib.mdgl_read_rows(16, 10, row_bytes, 16, 64, None, 0, 16, None) == -1
+        assert "row_bytes" in err(lib)
+    assert lib.mdgl_read_rows(16, 10, 64, 16, -1, None, 0, 16, None) == -1
+    assert lib.mdgl_read_rows(16, 10, 64, 16, 1 << 31, None, 0, 16, None) == -1
+    assert lib.mdgl_read_rows(16, 10, 64, None, 64, None, 0, 16, None) == -1
+    assert "null" in err(lib)
+    assert lib.mdgl_read_rows(16, 10, 64, 16, 64, None, 5, 16, None) == -1  # rows, no dst
+    assert lib.mdgl_read_rows(8, 10, 64, 16, 64, None, 0, 16, None) == -1
+    assert "aligned" in err(lib)
+    assert lib.mdgl_read_rows_sink_bytes(65) == 32 and lib.mdgl_read_rows_sink_bytes(-1) == -1
 
 
 def test_empty_problems_are_no_ops(lib):
@@ -178,6 +190,7 @@ def test_empty_problems_are_no_ops(lib):
                                None, None, None, None, None, 0, 0, 0, None) == 0
     assert lib.mdgl_cumsum(None, None, 0, None) == 0
     assert lib.mdgl_segment_softmax_short(None, None, None, 0, 4, 0, 0, None) == 0
+    assert lib.mdgl_read_rows(None, 0, 64, None, 0, None, 0, None, None) == 0
 
 
 def test_build_csr_arguments(lib):
