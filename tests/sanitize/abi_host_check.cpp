@@ -162,6 +162,12 @@ static void other_entry_points() {
   EXPECT(mdgl_replace_inf_with_zero(nullptr, nullptr, 5, MDGL_FLOAT64, nullptr) == MDGL_EINVAL);
   EXPECT(mdgl_scatter_rows(nullptr, nullptr, nullptr, 0, 8, MDGL_FLOAT32, nullptr) == MDGL_OK);
   EXPECT(mdgl_gather_rows(nullptr, nullptr, nullptr, 4, 8, MDGL_FLOAT32, nullptr) == MDGL_EINVAL);
+  EXPECT(mdgl_read_rows(nullptr, 0, 64, nullptr, 0, nullptr, 0, nullptr, nullptr) == MDGL_OK);
+  EXPECT(mdgl_read_rows(nullptr, 10, 24, nullptr, 64, nullptr, 0, nullptr, nullptr) ==
+         MDGL_EINVAL);
+  EXPECT(mdgl_read_rows(nullptr, 10, 64, nullptr, 64, nullptr, 0, nullptr, nullptr) ==
+         MDGL_EINVAL);
+  EXPECT(mdgl_read_rows_sink_bytes(64) == 16 && mdgl_read_rows_sink_bytes(-1) == -1);
 }
 
 int main() {
