@@ -444,6 +444,16 @@ def i64_device(a) -> torch.Tensor:
     return torch.from_numpy(i64(a)).to(device())
 
 
+def settle() -> None:
+    """Wait until the work queued so far on the current stream has run. A
+    graph's lazily built device structures (endpoints, CSR schedules,
+    softmax plans) are cached only after this, so a call on another stream
+    or thread that finds them cached reads them complete. Once per
+    structure; these builds therefore belong before a HIP graph capture (the
+    CSR build reads its row pointers back anyway)."""
+    torch.cuda.current_stream().synchronize()
+
+
 def i32_device(a: np.ndarray) -> torch.Tensor:
     """An int64 host index array as an int32 GPU tensor (values checked < 2**31)."""
     if a.size and (int(a.max()) >= 2 ** 31 or int(a.min()) < -2 ** 31):

@@ -111,6 +111,7 @@ class _Chunks:
         self.chunk_start = _lib.i32_device(start)
         self.heavy_rows = _lib.i32_device(heavy)
         self.heavy_ptr = _lib.i32_device(ptr)
+        _lib.settle()  # cached by its CSR, possibly read from another stream
 
 
 def build_device_csr(key: torch.Tensor, other, num_rows: int):
@@ -162,6 +163,7 @@ class _DeviceCSR:
             pos = torch.empty(E, dtype=torch.int32, device=self.eid.device)
             pos[self.eid.to(torch.int64)] = torch.arange(E, dtype=torch.int32,
                                                          device=self.eid.device)
+            _lib.settle()
             self._slot_of_eid = pos
         return self._slot_of_eid
 
@@ -170,8 +172,10 @@ class _DeviceCSR:
         lane layout (cached)."""
         key = (int(slots), int(chunk_len))
         if key not in self._softmax:
-            self._softmax[key] = SoftmaxPlan.from_device(self.indptr, slots, chunk_len,
-                                                         ordered=True, eid=self.eid)
+            plan = SoftmaxPlan.from_device(self.indptr, slots, chunk_len, ordered=True,
+                                           eid=self.eid)
+            _lib.settle()
+            self._softmax[key] = plan
         return self._softmax[key]
 
 
@@ -233,6 +237,7 @@ class DGLGraph(object):
             dev = _lib.device()
             self._dcoo = (u.to(device=dev, dtype=torch.int32).contiguous(),
                           v.to(device=dev, dtype=torch.int32).contiguous())
+            _lib.settle()
         else:
             u = i64(u)
             v = i64(v)
@@ -365,7 +370,9 @@ class DGLGraph(object):
         """int32 GPU copies of the edge endpoints, in edge-id order."""
         self._check_int32()
         if self._dcoo is None:
-            self._dcoo = (_lib.i32_device(self._u), _lib.i32_device(self._v))
+            coo = (_lib.i32_device(self._u), _lib.i32_device(self._v))
+            _lib.settle()
+            self._dcoo = coo
         return self._dcoo
 
     # -------------------------------------------------------------- queries
